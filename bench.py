@@ -1,0 +1,290 @@
+#!/usr/bin/env python3
+"""Attention-stage benchmark of the OpenAttention sparse decode step on one MI355X.
+
+Workload (the metric's configuration): B=32 sequences of N=32768
+keys, Llama-3.1-8B attention shapes (32 query / 8 KV heads, d=128, bf16 K/V), 1% read
+(C=64 clusters, E=216 expanded tokens, sink 3 + local 3 + top-9), synthetic Gaussian-mixture
+keys (256 centres per KV head).  One "step" is one pass of the decode stage of one layer over
+the whole batch: index update -> QGS scan -> top-k -> ErrorGate -> water-filling -> top-q ->
+residual proxies + fused softmax.  `--layers` replicas of the layer state (> 2 GB of working
+set in total) are visited round-robin so the 256 MB Infinity Cache cannot serve repeats.  The
+timed loop replays a hipGraph of one step of every replica, as the deployed path does
+(graph_runner.py:639-655); n advances by one token per step.
+
+Reported (one JSON line): us per layer-step (value), tokens/s (B / t_layer), the roofline of
+the dominant kernel (algorithmic bytes per launch / its average duration from HIP events),
+the stage-level algorithmic bandwidth, the per-stage breakdown, the dense bf16 decode
+comparator (this library's split-K kernel and torch SDPA, the faster is the denominator) and
+the CPU restatement timed on one sequence of the same workload (cpu_baseline, scaled to B).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+import types
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HQ, HKV, D, G = 32, 8, 128, 4
+PEAK_HBM_GBPS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--rho", type=float, default=0.01)
+    p.add_argument("--batch", type=int, default=32)
+    p.add_argument("--ctx", type=int, default=32768)
+    p.add_argument("--layers", type=int, default=4, help="rotating layer replicas")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-dense", action="store_true")
+    p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a hipGraph")
+    p.add_argument("--cpu-reps", type=int, default=3)
+    return p.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): the sparse decode "
+              "stage needs no collective and this build measures one GPU's share", flush=True)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from openattention_amd import _build, lib, synth
+    if not os.path.exists(_build.lib_path()):
+        _build.build()
+    lib.load()
+    from openattention_amd import ops
+    from openattention_amd.method import C as CTX, OursHIP
+    from openattention_amd.prefill import build_row
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    B, N, L = a.batch, a.ctx, a.layers
+    n_steps = a.warmup + a.steps
+    Lmax = N + n_steps + 1
+    T0 = N - 1
+    static = synth.static_metric(L)
+    m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=L, static=static)
+    Ks, Vs, Qs = [], [], []
+    t0 = time.time()
+    for l in range(L):
+        K, V, q, qq, _ = synth.make_layer(3, B, N + n_steps, Lmax, 256, dev, layer=l)
+        for b in range(B):
+            build_row(m.st[l], b, K[b], V[b], qq[b], T0, static["M"][l], static["inv_freq"], 1.0, l, G)
+        Ks.append(K)
+        Vs.append(V)
+        Qs.append(q)
+        del qq
+        torch.cuda.synchronize()
+        log(f"[bench] layer {l} built ({time.time() - t0:.1f}s)")
+    CTX.K, CTX.V = Ks, Vs
+    n_arr = torch.arange(N, N + n_steps, device=dev, dtype=torch.int32)
+    n_buf = torch.empty(1, device=dev, dtype=torch.int32)
+    CTX.n_dev = n_buf
+    CTX.n0_dev = torch.tensor([T0], device=dev, dtype=torch.int32)
+    counts = {m.bud.counts(n) for n in range(N, N + n_steps)}
+    assert len(counts) == 1, "sink/local/top-k must stay constant over the timed window"
+    ns, nl, k_top = counts.pop()
+
+    def step_all(i, marks=None):
+        n_buf.copy_(n_arr[i:i + 1])
+        for l in range(L):
+            m.decode(l, Qs[l], N + i, marks=marks if l == 0 else None)
+
+    # ---- warm-up (eager), then capture one step of every layer in a hipGraph
+    for i in range(a.warmup):
+        step_all(i)
+    torch.cuda.synchronize()
+    graph = None
+    if not a.no_graph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for l in range(L):
+                m.decode(l, Qs[l], N + a.warmup)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for l in range(L):
+                m.decode(l, Qs[l], N + a.warmup)
+        torch.cuda.synchronize()
+
+    # ---- timed region: K steps, each one layer-step per replica
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.time()
+    e0.record()
+    for i in range(a.warmup, n_steps):
+        if graph is not None:
+            n_buf.copy_(n_arr[i:i + 1])
+            graph.replay()
+        else:
+            step_all(i)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.time() - w0
+    gpu_ms = e0.elapsed_time(e1)
+    layer_steps = a.steps * L
+    us_layer = gpu_ms * 1e3 / layer_steps
+    log(f"[bench] timed {layer_steps} layer-steps: {us_layer:.1f} us/layer-step (wall {wall * 1e3 / layer_steps:.1f} us)")
+
+    # ---- per-stage breakdown (eager, events between stages on the launch stream)
+    per = {}
+    for rep in range(3):
+        marks = []
+        i = a.warmup + (rep % a.steps)
+        n_buf.copy_(n_arr[i:i + 1])
+        for l in range(L):
+            mk = []
+            m.decode(l, Qs[l], N + i, marks=mk)
+            marks.append(mk)
+        torch.cuda.synchronize()
+        for mk in marks:
+            for (n0, e_a), (n1, e_b) in zip(mk[:-1], mk[1:]):
+                per.setdefault(n1, []).append(e_a.elapsed_time(e_b) * 1e3)
+    stage_us = {k: statistics.median(v) for k, v in per.items()}
+    log("[bench] stages (us): " + ", ".join(f"{k} {v:.1f}" for k, v in stage_us.items()))
+
+    # ---- algorithmic bytes (SURVEY 8d formula) per kernel and for the stage
+    R, Cn, E = B * HQ, m.Cn, m.E
+    NSX = ns + nl + k_top
+    n_mid = N + a.warmup
+    alg = {
+        "qgs_scan": B * HKV * n_mid * 32,
+        "errorgate": R * Cn * (2 * D * 4 + 4),
+        "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * 2 * D * 4,
+    }
+    stage_alg = B * HKV * n_mid * 32 + R * (NSX + E) * 2 * D * 2 + R * Cn * (3 * D * 4 + 4)
+    dom = max(stage_us, key=lambda k: stage_us[k])
+    dom_bytes = alg.get(dom)
+    roof_kernel = dom if dom_bytes is not None else "qgs_scan"
+    dom_bytes = alg[roof_kernel]
+    achieved = dom_bytes / (stage_us[roof_kernel] * 1e-6) / 1e9
+    roofline = {"kernel": roof_kernel, "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+                "traffic": None, "bytes_per_launch": dom_bytes,
+                "avg_launch_us": round(stage_us[roof_kernel], 2)}
+    stage_gbps = stage_alg / (us_layer * 1e-6) / 1e9
+
+    # ---- dense comparator on the same tensors (layer 0)
+    dense = {}
+    if not a.no_dense:
+        K0, V0 = Ks[0].view(-1, Lmax, D), Vs[0].view(-1, Lmax, D)
+        q0 = Qs[0].reshape(-1, D).contiguous()
+        n_dense = torch.tensor([N], device=dev, dtype=torch.int32)
+        ws = torch.empty(R * 64 * (D + 2), device=dev)
+        outd = torch.empty_like(q0)
+
+        def run_ours():
+            ops.dense_decode(q0, K0, V0, n_dense, out=outd, nsplit=64, ws=ws)
+
+        kd, vd = Ks[0][:, :, :N], Vs[0][:, :, :N]
+
+        def run_sdpa():
+            return torch.nn.functional.scaled_dot_product_attention(Qs[0], kd, vd, enable_gqa=True,
+                                                                    scale=D ** -0.5)
+
+        for name, fn in (("ours_splitk", run_ours), ("torch_sdpa", run_sdpa)):
+            try:
+                for _ in range(3):
+                    fn()
+                torch.cuda.synchronize()
+                ts = []
+                for _ in range(10):
+                    x0, x1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    x0.record()
+                    fn()
+                    x1.record()
+                    torch.cuda.synchronize()
+                    ts.append(x0.elapsed_time(x1) * 1e3)
+                dense[name] = round(statistics.median(ts), 1)
+            except Exception as ex:  # noqa: BLE001
+                dense[name] = f"failed: {type(ex).__name__}: {ex}"[:200]
+        log(f"[bench] dense (us): {dense}")
+    dense_best = min([v for v in dense.values() if isinstance(v, float)], default=None)
+
+    # ---- CPU restatement on a bounded sample: sequence b=0 of layer 0
+    cpu = None
+    if not a.no_cpu_baseline:
+        from oracle import oracle as O
+        st = m.st[0]
+        n_cpu = N + n_steps  # every generated token has joined the index; decode one more step
+        rows = slice(0, HQ)
+        kvr = slice(0, HKV)
+
+        def np16(t):
+            return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+        sub = {f: getattr(st, f)[kvr if f in ("codes", "U", "scale") else rows].detach().cpu().numpy().copy()
+               for f in ("codes", "U", "scale", "colmean", "cent", "asg", "nb", "Sk", "Sk2", "Sv",
+                         "reclist", "reccnt")}
+        sub["W"] = np16(st.W[rows])
+        sub["K"] = np16(Ks[0][0])
+        sub["V"] = np16(Vs[0][0])
+        qn = np16(Qs[0][0].reshape(-1, D))
+        sc = np.float32(D ** -0.5)
+        ns2, nl2, k2 = m.bud.counts(N)
+        times = []
+        for rep in range(a.cpu_reps + 1):
+            work = {k: v.copy() for k, v in sub.items()}
+            c0 = time.perf_counter()
+            O.decode_step(work, qn, N, ns2, nl2, k2, E, G, sc, np.float32(float(sc) ** 2),
+                          update_index=False)
+            dt = time.perf_counter() - c0
+            if rep > 0:
+                times.append(dt)
+        t_seq = statistics.median(times)
+        cpu = {"value": round(t_seq * B * 1e6, 1), "unit": "us/layer-step (B=%d, scaled from one sequence)" % B,
+               "cores": 1, "kind": "port",
+               "sample": f"1 of {B} sequences (32 query-head rows), layer 0, N={N}, decode stage without the "
+                         f"index update; median of {a.cpu_reps} runs, x{B}"}
+        log(f"[bench] cpu: {t_seq * 1e3:.1f} ms per sequence -> {cpu['value']:.0f} us per B={B} layer-step")
+        del n_cpu
+
+    rec = {
+        "metric": "attn-stage us/layer at B=32, 32K ctx, 1% read; achieved HBM GB/s vs peak",
+        "value": round(us_layer, 2),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(us_layer / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 K/V + int8 codes, fp32 accumulate",
+        "data": "synthetic (seeded Gaussian-mixture keys, 256 centres/KV head; N(0,1) values)",
+        "config": {"workload": f"config3 sparse decode stage, one layer-step: B={B}, N={N}, rho={a.rho}, "
+                               f"C={Cn}, E={E}, sink/local/top-k {ns}/{nl}/{k_top}",
+                   "B": B, "N": N, "rho": a.rho, "C": Cn, "E": E, "layers_rotated": L,
+                   "mode": "eager" if graph is None else "hipgraph"},
+        "tokens_per_s": round(B / (us_layer * 1e-6), 1),
+        "stage_alg_bytes": stage_alg,
+        "stage_alg_GBps": round(stage_gbps, 1),
+        "stage_frac_of_peak": round(stage_gbps / PEAK_HBM_GBPS, 4),
+        "stages_us": {k: round(v, 2) for k, v in stage_us.items()},
+        "roofline": roofline,
+        "dense_us": dense,
+        "speedup_vs_dense": round(dense_best / us_layer, 2) if dense_best else None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

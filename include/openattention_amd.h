@@ -1,0 +1,175 @@
+/*
+ * openattention_amd -- C ABI of the gfx950 kernels of OpenAttention's sparse decode path.
+ *
+ * Conventions for every entry point:
+ *   - plain device pointers, element strides (not bytes) and sizes; no torch types.
+ *   - `stream` is a hipStream_t passed as void*; every launch goes on it, nothing synchronises,
+ *     nothing allocates and nothing is read back on the host, so a caller may capture a whole
+ *     decode step in a hipGraph.
+ *   - the current length n (and n0, the prefix length at build time) are read from device
+ *     memory (`n_dev`, `n0_dev`: one int32 each), as the reference's graph-safe kernels do.
+ *   - return 0 on success, -22 (OA_EINVAL) when a shape/stride/size check fails, otherwise
+ *     the hipError_t of the launch.  oa_error_string() gives the text.
+ *   - head_dim is 128, the QGS rank 32, the QGC rank 16 and the GQA group 4 (Llama-3.1-8B);
+ *     other values are rejected.
+ *   - rows R = B * HQ query-head rows; kv_rows = B * HKV; row r reads KV row r / (R / kv_rows).
+ *
+ * Reference interfaces (paths relative to the hyunwoo137/OpenAttention checkout) each function
+ * replaces are cited per declaration.  The reference binds these stages from Python; the
+ * ctypes binding of this library is openattention_amd/lib.py.
+ */
+#ifndef OPENATTENTION_AMD_H
+#define OPENATTENTION_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OA_EINVAL (-22)
+
+/* ABI version of this header (1). */
+int oa_abi_version(void);
+
+/* Text for a status returned by any entry point. */
+const char* oa_error_string(int status);
+
+/*
+ * OpenAttention.flash: one online softmax per query-head row over the selected tokens (sel),
+ * the expanded tokens (exp_idx) and the cluster proxies (kbar, vbar, log_n).
+ * Replaces ours_flash (inference/methods_eager.py:161-172; kernel :91-158) when
+ * proxy_per_kv == 0 and decode_expand_attention (triton_expand_decode.py:139-165; kernel
+ * :31-136) when proxy_per_kv == 1 (kbar/vbar rows indexed by KV head).
+ *   q (rows, 128) bf16; k, v (kv_rows, Lmax, 128) bf16; sel (rows, n_sel), exp_idx
+ *   (rows, n_exp) int32 with -1 padding; kbar, vbar (rows or kv_rows, n_bins, 128) bf16 or
+ *   fp32 (kbar_is_f32); log_n (rows, n_bins) fp32 natural log, -inf = no proxy;
+ *   out (rows, 128) bf16.  A row with nothing valid returns 0.
+ *   n_split > 1 splits each row's list over n_split workgroups (the reference's split-K
+ *   variant for few rows, inference/ours_graph.py:214-262 + graph_runner.py:299-312); the
+ *   caller passes workspaces ws_m, ws_l (rows*n_split fp32) and ws_acc (rows*n_split*128).
+ */
+int oa_flash_decode(const void* q, long q_stride, const void* k, const void* v, long kv_stride_b,
+                    long kv_stride_s, const int32_t* sel, long sel_stride, int n_sel,
+                    const int32_t* exp_idx, long exp_stride, int n_exp, const void* kbar,
+                    const void* vbar, long kbar_stride_b, long kbar_stride_n, int kbar_is_f32,
+                    int proxy_per_kv, const float* log_n, long log_n_stride, int n_bins, void* out,
+                    long out_stride, int rows, int kv_rows, int head_dim, float sm_scale,
+                    int n_split, float* ws_m, float* ws_l, float* ws_acc, void* stream);
+
+/*
+ * Index update of the token at position n-1: its int8 QGS code (KV-head rows), its nearest
+ * QGC centroid, the cluster's pooled sums (n, sum k, sum k^2, sum v) and the cluster's list
+ * of generated tokens (capacity rmax; the count keeps growing past it, marking overflow).
+ * Replaces _k_index_update_d2 (inference/ours_graph.py:43-90).
+ *   codes (kv_rows, codes_lmax, 32) int8; U (kv_rows, 128, 32), scale (kv_rows, 32) fp32;
+ *   W (rows, 128, 16) bf16; colmean (rows, 16), cent (rows, C, 16) fp32; asg (rows,
+ *   asg_stride) int32; nb (rows, C), Sk, Sk2, Sv (rows, C, 128) fp32; reclist (rows, C, rmax),
+ *   reccnt (rows, C) int32.
+ */
+int oa_index_update(const void* K, const void* V, long kv_stride_b, long kv_stride_s, int rows,
+                    int kv_rows, int head_dim, int8_t* codes, int codes_lmax, int rank_q,
+                    const float* U, const float* scale, const void* W, const float* colmean,
+                    int rank_c, const float* cent, int C, int32_t* asg, long asg_stride, float* nb,
+                    float* Sk, float* Sk2, float* Sv, int32_t* reclist, int32_t* reccnt, int rmax,
+                    const int* n_dev, void* stream);
+
+/*
+ * QGS query projection zq = (q U) * scale and its exact fixed-point form (exponent fexp per
+ * row, four int8 limbs of round(zq * 2^fexp) per KV-head block).  Replaces the torch
+ * projection of inference/ours_graph.py:298 (StaticTopKMasker._scores,
+ * static_top_k.py:203-213).
+ *   limbs (kv_rows, 16, 32) int8; fexp (rows) int32; zq_out (rows, 32) fp32 or NULL.
+ */
+int oa_qgs_prep(const void* q, long q_stride, const float* U, const float* scale, int rows,
+                int kv_rows, int head_dim, int rank, int8_t* limbs, int* fexp, float* zq_out,
+                void* stream);
+
+/*
+ * QGS scan: exact score of every position for the 4 query heads of each KV head, on the
+ * int8 matrix cores; sink (< ns), local (>= n - nl) and unwritten positions are -inf; plus
+ * the maximum of every 64-token tile.  Replaces _k_qgs_scan_tm
+ * (inference/graph_runner.py:100-120).
+ *   S (rows, s_stride >= ceil(Lmax/64)*64) fp32; TM (rows, tm_stride >= ceil(Lmax/64)) fp32.
+ */
+int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
+                const int* fexp, float* S, long s_stride, float* TM, long tm_stride,
+                const int* n_dev, int ns, int nl, void* stream);
+
+/*
+ * Exact top-k per row (ties to the lower position) among the k tiles with the largest
+ * maxima; sel = [0..ns) ++ [n-nl..n) ++ top; the selected scores in S are set to -inf.
+ * Replaces _k_select (inference/graph_runner.py:123-159).
+ */
+int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int rows,
+                   int ntiles, int32_t* sel, long sel_stride, const int* n_dev, int ns, int nl,
+                   int k_top, void* stream);
+
+/*
+ * ErrorGate: wl1 score and tail count of every cluster (pooled sums minus the selected
+ * tokens).  Replaces _k_errorgate (inference/ours_fused.py:122-154).
+ *   score, n_t (rows, C) fp32.
+ */
+int oa_errorgate(const void* q, long q_stride, const void* K, long k_stride_b, long k_stride_s,
+                 int rows, int kv_rows, int head_dim, const int32_t* asg, long asg_stride,
+                 const int32_t* sel, long sel_stride, int n_sel, const float* Sk, const float* Sk2,
+                 const float* nb, int C, float sm_scale, float* score, float* n_t, void* stream);
+
+/*
+ * Hierarchical water-filling of the exact-read budget E over the clusters (fp64 bisection of
+ * UTAMultiBinAttention._hier_quota_impl, multibin.py:1385-1422).  Replaces _k_waterfill
+ * (inference/ours_fused.py:157-216).   quota (rows, C) fp32 (integer valued, sums to
+ * min(E, sum of live tail counts)).
+ */
+int oa_waterfill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,
+                 void* stream);
+
+/*
+ * Within-cluster top-q by QGS score over CSR members + generated tokens; exp_idx segments
+ * grouped by cluster, -1 past the total.  Replaces _k_topq_d2 (inference/ours_graph.py:138-166).
+ *   mem (rows, mem_stride) int32 CSR; cstart, clen (rows, C) int32; exp_idx (rows, E) int32.
+ */
+int oa_topq(const float* S, long s_stride, const int32_t* mem, long mem_stride,
+            const int32_t* cstart, const int32_t* clen, const int32_t* reclist,
+            const int32_t* reccnt, int rmax, const int32_t* asg, long asg_stride,
+            const float* quota, int rows, int C, int32_t* exp_idx, int E, const int* n_dev,
+            const int* n0_dev, void* stream);
+
+/*
+ * Residual proxies: kbar', vbar' (bf16, rows x C x 128) and ln n' (fp32, -inf = none) of the
+ * tokens still unread.  Replaces _k_resid_scatter + _k_resid_norm
+ * (inference/ours_fused.py:366-407).
+ */
+int oa_residual(const void* K, const void* V, long kv_stride_b, long kv_stride_s, int rows,
+                int kv_rows, int head_dim, const int32_t* asg, long asg_stride,
+                const int32_t* sel, long sel_stride, int n_sel, const int32_t* exp_idx, int E,
+                const float* quota, const float* n_t, const float* Sk, const float* Sv, int C,
+                void* kbar_r, void* vbar_r, float* log_n, void* stream);
+
+/*
+ * Residual proxies fused with OpenAttention.flash: every K/V row read once, proxies kept in
+ * registers (fp32).  Replaces the residual + ours_flash pair of the deployed step
+ * (inference/ours_graph.py:324-344).   out (rows, 128) bf16.
+ */
+int oa_residual_flash(const void* q, long q_stride, const void* K, const void* V,
+                      long kv_stride_b, long kv_stride_s, int rows, int kv_rows, int head_dim,
+                      const int32_t* asg, long asg_stride, const int32_t* sel, long sel_stride,
+                      int n_sel, const int32_t* exp_idx, int E, const float* quota,
+                      const float* n_t, const float* Sk, const float* Sv, int C, float sm_scale,
+                      void* out, long out_stride, void* stream);
+
+/*
+ * Dense bf16 decode attention over positions [0, n) (the comparator), split-K over nsplit key
+ * chunks + combine; workspaces ws_m, ws_l (rows*nsplit) and ws_acc (rows*nsplit*128) fp32.
+ * Replaces _k_dense_split + _k_dense_combine (inference/graph_runner.py:259-312).
+ */
+int oa_dense_decode(const void* q, long q_stride, const void* K, const void* V, long kv_stride_b,
+                    long kv_stride_s, int rows, int kv_rows, int head_dim, int Lmax,
+                    const int* n_dev, float sm_scale, int nsplit, float* ws_m, float* ws_l,
+                    float* ws_acc, void* out, long out_stride, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPENATTENTION_AMD_H */

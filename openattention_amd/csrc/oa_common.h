@@ -1,0 +1,92 @@
+// Shared device helpers for the OpenAttention sparse-decode kernels (gfx950, wave64).
+//
+// Conventions used by every kernel in this library:
+//   * head_dim D is 128 (Llama-3.1-8B shapes); the host entry points reject anything else.
+//   * one wavefront is 64 lanes; a "lane group" is 16 consecutive lanes.
+//   * all reductions that feed a discrete decision (top-k, quota, argmax) use a fixed
+//     butterfly order (xor 32,16,8,4,2,1 over the 64 lanes), so every lane ends with the
+//     same bits and the CPU restatement can replay the exact order.
+//   * the library is compiled with -ffp-contract=off: a fused multiply-add only happens
+//     where the source calls fmaf()/fma() explicitly.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "openattention_amd.h"
+
+#define OA_D 128
+#define OA_WAVE 64
+
+namespace oa {
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// round-to-nearest-even fp32 -> bf16 (NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// unpack 8 bf16 (one 16-byte load) into floats
+__device__ __forceinline__ void unpack8(const uint4 w, float* x) {
+  x[0] = __uint_as_float(w.x << 16); x[1] = __uint_as_float(w.x & 0xffff0000u);
+  x[2] = __uint_as_float(w.y << 16); x[3] = __uint_as_float(w.y & 0xffff0000u);
+  x[4] = __uint_as_float(w.z << 16); x[5] = __uint_as_float(w.z & 0xffff0000u);
+  x[6] = __uint_as_float(w.w << 16); x[7] = __uint_as_float(w.w & 0xffff0000u);
+}
+
+// ---- butterfly reductions over the full wave (every lane gets the result) -------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+// reductions inside a 16-lane group
+__device__ __forceinline__ float group16_sum(float v) {
+  v = v + __shfl_xor(v, 8, 64);
+  v = v + __shfl_xor(v, 4, 64);
+  v = v + __shfl_xor(v, 2, 64);
+  v = v + __shfl_xor(v, 1, 64);
+  return v;
+}
+
+// Canonical 128-term fp32 dot product used wherever the result feeds a discrete decision:
+// lane l holds elements l and l+64; p_l = fma(a[l+64], b[l+64], a[l]*b[l]); then the wave
+// butterfly.  Every lane returns the same value.
+__device__ __forceinline__ float dot128_canon(float a_lo, float b_lo, float a_hi, float b_hi) {
+  float p = fmaf(a_hi, b_hi, a_lo * b_lo);
+  return wave_sum(p);
+}
+
+// order-preserving uint32 image of a float (larger float -> larger key, -inf lowest)
+__device__ __forceinline__ uint32_t float_key(float s) {
+  uint32_t b = __float_as_uint(s);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+}  // namespace oa
+
+// host-side launch status helper: the last launch error as an int
+#define OA_LAUNCH_STATUS() ((int)hipGetLastError())

@@ -1,0 +1,218 @@
+// ErrorGate (wl1 cluster score) and hierarchical water-filling of the exact-read budget E.
+//
+// ErrorGate follows the accuracy-path estimator: tail statistics of every QGC cluster are the
+// cached pooled sums minus the selected tokens (methods_eager.py:612-627, ours_fused.py:122-154),
+// moments as UTAMultiBinAttention._moments_from_key_stats (multibin.py:605-644) with
+// s2 = 0 for clusters of fewer than two tail tokens (multibin.py:734-738), and the wl1 score
+// zbar + log n + s2/2 + log max(erf(sqrt(s2)/sqrt2), 1e-30) (multibin.py:2370-2389).
+//
+// Water-filling is UTAMultiBinAttention._hier_quota_impl (multibin.py:1385-1422): fp64,
+// w_b = exp(s_b - max s), 64 bisection steps on log(lambda) for sum_b min(n_b, lambda w_b) = E,
+// q_b = floor(min(n_b, lambda w_b)) (q = n when the tail is smaller than E), leftover tokens one
+// each to the highest-score live clusters with room, in score order (ties to the lower
+// cluster id).  Sums that feed comparisons use a fixed order (lane-strided partials, then the
+// wave butterfly) and the elementary functions come from oa_detmath.h, so the integer quotas
+// are reproducible bit for bit on the CPU.
+#include "oa_common.h"
+#include "oa_detmath.h"
+
+namespace {
+
+constexpr int kGateThreads = 256;
+constexpr int kMaxSel = 64;
+constexpr int kMaxC = 256;
+
+struct GateArgs {
+  const uint16_t* q; long q_stride;
+  const uint16_t* K; long k_sb; long k_ss; int G;
+  const int32_t* asg; long asg_stride;
+  const int32_t* sel; long sel_stride; int n_sel;
+  const float* Sk; const float* Sk2; long st_stride_r;   // (R, C, D): row stride in floats
+  const float* nb; long nb_stride;
+  float* score; float* n_t; long out_stride;
+  int C; float sc; float sc2;
+};
+
+__global__ void __launch_bounds__(kGateThreads) errorgate_kernel(GateArgs a) {
+  __shared__ float s_k[kMaxSel][OA_D];
+  __shared__ int s_cid[kMaxSel];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int kvr = row / a.G;
+  for (int i = tid; i < a.n_sel; i += kGateThreads) {
+    int tok = a.sel[(long)row * a.sel_stride + i];
+    s_cid[i] = (tok >= 0) ? a.asg[(long)row * a.asg_stride + tok] : -1;
+  }
+  for (int e = tid; e < a.n_sel * OA_D; e += kGateThreads) {
+    int i = e / OA_D, d = e % OA_D;
+    int tok = a.sel[(long)row * a.sel_stride + i];
+    s_k[i][d] = (tok >= 0) ? oa::bf16_to_f32(a.K[(long)kvr * a.k_sb + (long)tok * a.k_ss + d]) : 0.f;
+  }
+  __syncthreads();
+  const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
+  const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
+  const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
+  for (int c = wave; c < a.C; c += kGateThreads / 64) {
+    const long base = (long)row * a.st_stride_r + (long)c * OA_D;
+    float sk_lo = a.Sk[base + lane], sk_hi = a.Sk[base + lane + 64];
+    float s2_lo = a.Sk2[base + lane], s2_hi = a.Sk2[base + lane + 64];
+    float nt = a.nb[(long)row * a.nb_stride + c];
+    for (int i = 0; i < a.n_sel; ++i) {
+      if (s_cid[i] == c) {
+        const float k_lo = s_k[i][lane], k_hi = s_k[i][lane + 64];
+        sk_lo = sk_lo - k_lo;
+        sk_hi = sk_hi - k_hi;
+        s2_lo = s2_lo - k_lo * k_lo;
+        s2_hi = s2_hi - k_hi * k_hi;
+        nt = nt - 1.0f;
+      }
+    }
+    const float den = fmaxf(nt, 1.0f);
+    const float kb_lo = sk_lo / den, kb_hi = sk_hi / den;
+    const float ks_lo = s2_lo / den, ks_hi = s2_hi / den;
+    const float v_lo = fmaxf(ks_lo - kb_lo * kb_lo, 0.f);
+    const float v_hi = fmaxf(ks_hi - kb_hi * kb_hi, 0.f);
+    const float zbar = a.sc * oa::dot128_canon(q_lo, kb_lo, q_hi, kb_hi);
+    float s2 = a.sc2 * oa::dot128_canon(qq_lo, v_lo, qq_hi, v_hi);
+    if (!(nt >= 2.0f)) s2 = 0.f;
+    const float s2c = fmaxf(s2, 0.f);
+    const float sig = sqrtf(s2c);
+    const float er = oa::det_erff(sig * 0.70710677f);
+    const float log_d = 0.5f * s2c + oa::det_logf(fmaxf(er, 1e-30f));
+    const float score = (zbar + oa::det_logf(fmaxf(nt, 1.0f))) + log_d;
+    if (lane == 0) {
+      a.score[(long)row * a.out_stride + c] = score;
+      a.n_t[(long)row * a.out_stride + c] = nt;
+    }
+  }
+}
+
+// one wave per row; cluster c lives in lane c % 64, slot c / 64
+__device__ __forceinline__ double canon_sum(const double* x, int C, int lane) {
+  double p = 0.0;
+  bool first = true;
+  for (int j = 0; j < 4; ++j) {
+    int c = lane + 64 * j;
+    if (c < C) {
+      p = first ? x[j] : p + x[j];
+      first = false;
+    }
+  }
+  return oa::wave_sum(p);
+}
+
+__global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__ score,
+                                                       const float* __restrict__ n_t, long in_stride,
+                                                       float* __restrict__ quota, long q_stride, int C,
+                                                       double budget) {
+  __shared__ double s_key[kMaxC];
+  __shared__ int s_room[kMaxC];
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
+  double sv[4], w[4], cap[4], qv[4];
+  bool ok[4];
+  double smax = NEG;
+  for (int j = 0; j < 4; ++j) {
+    int c = lane + 64 * j;
+    sv[j] = NEG; w[j] = 0.0; cap[j] = 0.0; ok[j] = false;
+    if (c < C) {
+      float nt = n_t[(long)row * in_stride + c];
+      ok[j] = nt > 1.0f;
+      if (ok[j]) {
+        sv[j] = (double)score[(long)row * in_stride + c];
+        cap[j] = (double)nt;
+      }
+      smax = fmax(smax, sv[j]);
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) smax = fmax(smax, __shfl_xor(smax, m, 64));
+  if (!(smax > NEG && smax < -NEG)) smax = 0.0;
+  double rmax = 0.0;
+  for (int j = 0; j < 4; ++j) {
+    if (ok[j]) w[j] = oa::det_exp(sv[j] - smax);
+    double ratio = (w[j] > 0.0) ? cap[j] / fmax(w[j], 1e-300) : 0.0;
+    if (lane + 64 * j < C) rmax = fmax(rmax, ratio);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) rmax = fmax(rmax, __shfl_xor(rmax, m, 64));
+  const double tot = canon_sum(cap, C, lane);
+  double lo = -3.0 * 2.302585092994046;
+  double hi = oa::det_log(fmax(rmax, 1e-3)) + 1.0;
+  for (int it = 0; it < 64; ++it) {
+    const double mid = 0.5 * (lo + hi);
+    const double em = oa::det_exp(mid);
+    double part[4];
+    for (int j = 0; j < 4; ++j) part[j] = fmin(cap[j], em * w[j]);
+    const double f = canon_sum(part, C, lane);
+    if (f > budget) hi = mid; else lo = mid;
+  }
+  const double el = oa::det_exp(lo);
+  for (int j = 0; j < 4; ++j) {
+    qv[j] = floor(fmin(cap[j], el * w[j]));
+    if (tot <= budget) qv[j] = cap[j];
+  }
+  const double qsum = canon_sum(qv, C, lane);
+  double rem = fmin(tot, budget) - qsum;
+  rem = rint(rem > 0.0 ? rem : 0.0);
+  // order: live clusters by score descending (dead clusters as -inf), ties to the lower id
+  for (int j = 0; j < 4; ++j) {
+    int c = lane + 64 * j;
+    if (c < C) {
+      s_key[c] = ok[j] ? sv[j] : NEG;
+      s_room[c] = qv[j] < cap[j] ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  for (int j = 0; j < 4; ++j) {
+    int c = lane + 64 * j;
+    if (c >= C) continue;
+    double add = 0.0;
+    if (s_room[c]) {
+      int rank = 0;
+      const double kc = s_key[c];
+      for (int c2 = 0; c2 < C; ++c2) {
+        if (!s_room[c2]) continue;
+        const double k2 = s_key[c2];
+        if (k2 > kc || (k2 == kc && c2 < c)) ++rank;
+      }
+      if ((double)rank < rem) add = 1.0;
+    }
+    quota[(long)row * q_stride + c] = (float)(qv[j] + add);
+  }
+}
+
+}  // namespace
+
+extern "C" int oa_errorgate(const void* q, long q_stride, const void* K, long k_stride_b,
+                            long k_stride_s, int rows, int kv_rows, int head_dim,
+                            const int32_t* asg, long asg_stride, const int32_t* sel, long sel_stride,
+                            int n_sel, const float* Sk, const float* Sk2, const float* nb, int C,
+                            float sm_scale, float* score, float* n_t, void* stream) {
+  if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || n_sel < 0 || n_sel > kMaxSel ||
+      C <= 0)
+    return OA_EINVAL;
+  GateArgs a;
+  a.q = (const uint16_t*)q; a.q_stride = q_stride;
+  a.K = (const uint16_t*)K; a.k_sb = k_stride_b; a.k_ss = k_stride_s; a.G = rows / kv_rows;
+  a.asg = asg; a.asg_stride = asg_stride;
+  a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
+  a.Sk = Sk; a.Sk2 = Sk2; a.st_stride_r = (long)C * OA_D;
+  a.nb = nb; a.nb_stride = C;
+  a.score = score; a.n_t = n_t; a.out_stride = C;
+  a.C = C; a.sc = sm_scale;
+  a.sc2 = (float)((double)sm_scale * (double)sm_scale);
+  hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads), 0, (hipStream_t)stream, a);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_waterfill(const float* score, const float* n_t, int rows, int C, int budget,
+                            float* quota, void* stream) {
+  if (rows <= 0 || C <= 0 || C > kMaxC || budget < 0) return OA_EINVAL;
+  hipLaunchKernelGGL(waterfill_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, score, n_t,
+                     (long)C, quota, (long)C, C, (double)budget);
+  return OA_LAUNCH_STATUS();
+}

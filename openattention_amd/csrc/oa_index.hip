@@ -1,0 +1,116 @@
+// Index update of the token written at position n-1 (device-side n).
+//
+// Reference: _k_index_update_d2 (inference/ours_graph.py:43-90) and the eager step 1 of
+// Ours.decode (methods_eager.py:586-601); accuracy-path counterparts StaticTopKMasker._extend
+// (static_top_k.py:166-183) and UTAMultiBinAttention._profile_extend (multibin.py:2062-2096).
+//   code_r  = clamp(rint((k . U[:, r]) / scale_r), -127, 127)        (KV-head row only)
+//   zp_j    = bf16(k . W[:, j]) - colmean_j                            (per query-head row)
+//   cluster = argmax_c (zp . cent_c - 0.5 |cent_c|^2), ties to the lower id
+//   n_c += 1; Sk_c += k; Sk2_c += k*k; Sv_c += v; append n-1 to the cluster's generated list
+// Dot products use the canonical order of oa_common.h; zp . cent and |cent|^2 are sequential
+// fma chains over j = 0..15 -- the CPU restatement replays both.
+#include "oa_common.h"
+
+namespace {
+
+constexpr int RQ = 32;
+constexpr int RC = 16;
+
+struct IdxArgs {
+  const uint16_t* K; const uint16_t* V; long kv_sb; long kv_ss;
+  int8_t* codes; int Lmax_codes;
+  const float* U; const float* scale;
+  const uint16_t* W; const float* colmean; const float* cent;
+  int32_t* asg; long asg_stride;
+  float* nb; float* Sk; float* Sk2; float* Sv;
+  int32_t* reclist; int32_t* reccnt; int rmax;
+  const int* n_dev; int C; int G;
+};
+
+__global__ void __launch_bounds__(64) index_update_kernel(IdxArgs a) {
+  const int r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int kvr = r / a.G;
+  const int pos = *a.n_dev - 1;
+  const uint16_t* kp = a.K + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
+  const uint16_t* vp = a.V + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
+  const float k_lo = oa::bf16_to_f32(kp[lane]), k_hi = oa::bf16_to_f32(kp[lane + 64]);
+  const float v_lo = oa::bf16_to_f32(vp[lane]), v_hi = oa::bf16_to_f32(vp[lane + 64]);
+  if (r % a.G == 0) {
+    const float* Ub = a.U + (long)kvr * OA_D * RQ;
+    for (int j = 0; j < RQ; ++j) {
+      const float zc = oa::dot128_canon(k_lo, Ub[lane * RQ + j], k_hi, Ub[(lane + 64) * RQ + j]);
+      float code = rintf(zc / a.scale[(long)kvr * RQ + j]);
+      code = fminf(fmaxf(code, -127.f), 127.f);
+      if (lane == j) a.codes[((long)kvr * a.Lmax_codes + pos) * RQ + j] = (int8_t)(int)code;
+    }
+  }
+  const uint16_t* Wb = a.W + (long)r * OA_D * RC;
+  float zp[RC];
+#pragma unroll
+  for (int j = 0; j < RC; ++j) {
+    const float d = oa::dot128_canon(k_lo, oa::bf16_to_f32(Wb[lane * RC + j]), k_hi,
+                                     oa::bf16_to_f32(Wb[(lane + 64) * RC + j]));
+    zp[j] = oa::bf16_round(d) - a.colmean[(long)r * RC + j];
+  }
+  float best = -INFINITY;
+  int bidx = 0x7fffffff;
+  const float* cb = a.cent + (long)r * a.C * RC;
+  for (int c = lane; c < a.C; c += 64) {
+    const float* cc = cb + (long)c * RC;
+    float sim = zp[0] * cc[0];
+    float h = cc[0] * cc[0];
+#pragma unroll
+    for (int j = 1; j < RC; ++j) {
+      sim = fmaf(zp[j], cc[j], sim);
+      h = fmaf(cc[j], cc[j], h);
+    }
+    const float dist = sim - 0.5f * h;
+    if (dist > best || bidx == 0x7fffffff) { best = dist; bidx = c; }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ob = __shfl_xor(best, m, 64);
+    const int oi = __shfl_xor(bidx, m, 64);
+    if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
+  }
+  const int c = bidx;
+  const long sb = ((long)r * a.C + c) * OA_D;
+  a.Sk[sb + lane] += k_lo;
+  a.Sk[sb + lane + 64] += k_hi;
+  a.Sk2[sb + lane] += k_lo * k_lo;
+  a.Sk2[sb + lane + 64] += k_hi * k_hi;
+  a.Sv[sb + lane] += v_lo;
+  a.Sv[sb + lane + 64] += v_hi;
+  if (lane == 0) {
+    a.asg[(long)r * a.asg_stride + pos] = c;
+    a.nb[(long)r * a.C + c] += 1.0f;
+    const long rc = (long)r * a.C + c;
+    const int cnt = a.reccnt[rc];
+    if (cnt < a.rmax) a.reclist[rc * a.rmax + cnt] = pos;
+    a.reccnt[rc] = cnt + 1;
+  }
+}
+
+}  // namespace
+
+extern "C" int oa_index_update(const void* K, const void* V, long kv_stride_b, long kv_stride_s,
+                               int rows, int kv_rows, int head_dim, int8_t* codes, int codes_lmax,
+                               int rank_q, const float* U, const float* scale, const void* W,
+                               const float* colmean, int rank_c, const float* cent, int C,
+                               int32_t* asg, long asg_stride, float* nb, float* Sk, float* Sk2,
+                               float* Sv, int32_t* reclist, int32_t* reccnt, int rmax,
+                               const int* n_dev, void* stream) {
+  if (head_dim != OA_D || rank_q != RQ || rank_c != RC || kv_rows <= 0 || rows % kv_rows != 0 ||
+      C <= 0 || rmax < 0)
+    return OA_EINVAL;
+  IdxArgs a;
+  a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.kv_sb = kv_stride_b; a.kv_ss = kv_stride_s;
+  a.codes = codes; a.Lmax_codes = codes_lmax; a.U = U; a.scale = scale;
+  a.W = (const uint16_t*)W; a.colmean = colmean; a.cent = cent;
+  a.asg = asg; a.asg_stride = asg_stride; a.nb = nb; a.Sk = Sk; a.Sk2 = Sk2; a.Sv = Sv;
+  a.reclist = reclist; a.reccnt = reccnt; a.rmax = rmax; a.n_dev = n_dev; a.C = C;
+  a.G = rows / kv_rows;
+  hipLaunchKernelGGL(index_update_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, a);
+  return OA_LAUNCH_STATUS();
+}

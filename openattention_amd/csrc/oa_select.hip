@@ -1,0 +1,244 @@
+// QGS selection on gfx950: query projection, int8 code scan, exact top-k.
+//
+// Reference semantics: StaticTopKMasker._scores (static_top_k.py:197-218: zq = (q U) * scale,
+// score_i = zq . code_i), add_mask (static_top_k.py:221-262: top-k over positions not already
+// taken by the sink/local maskers), deployed scan/select kernels graph_runner.py:100-159.
+//
+// Exactness.  The reference's fp32 matmul has no defined summation order, so this library
+// fixes one that any implementation can reproduce bit for bit:
+//   F_row   = 30 - e, where max_r |zq_r| = m * 2^e with m in [0.5, 1)
+//   Z_r     = rint(zq_r * 2^F_row)              (|Z_r| < 2^30, an int32)
+//   S_i     = sum_r Z_r * code_{i,r}            (exact integer, |S_i| < 2^43)
+//   score_i = fp32(S_i * 2^-F_row)              (one rounding)
+// The integer sum is order independent, so it is evaluated on the int8 matrix cores:
+// Z_r is split into four signed 8-bit limbs and one v_mfma_i32_16x16x32_i8 multiplies the
+// 16 limb rows (4 query heads x 4 limbs) of a KV head with the 32-byte codes of 16 tokens.
+// Each output lane then holds the four limb partials of one (token, head) and recombines
+// them exactly in fp64 (all values are integers below 2^53).
+// Top-k ties break to the lower position (graph_runner.py:127-151 rule).
+#include "oa_common.h"
+
+typedef int oa_v4i __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int RQ = 32;   // QGS rank (bytes of code per token)
+constexpr int GQ = 4;    // query heads per KV head (limb rows = GQ * 4 = 16)
+
+// ------------------------------------------------------------------------------------------
+// prep: one wave per query-head row.  zq = (q . U[:, r]) * scale_r (canonical dot order),
+// then the fixed-point exponent and the four int8 limbs of Z_r.
+__global__ void __launch_bounds__(64) qgs_prep_kernel(const uint16_t* __restrict__ q, long q_stride,
+                                                      const float* __restrict__ U,      // (BH, D, RQ)
+                                                      const float* __restrict__ scale,  // (BH, RQ)
+                                                      int G, int8_t* __restrict__ limbs, // (BH, 16, RQ)
+                                                      int* __restrict__ fexp, float* __restrict__ zq_out) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int kvr = row / G;
+  const int g = row % G;
+  const float q_lo = oa::bf16_to_f32(q[(long)row * q_stride + lane]);
+  const float q_hi = oa::bf16_to_f32(q[(long)row * q_stride + lane + 64]);
+  const float* Ub = U + (long)kvr * OA_D * RQ;
+  float myz = 0.f;
+  for (int j = 0; j < RQ; ++j) {
+    float d = oa::dot128_canon(q_lo, Ub[lane * RQ + j], q_hi, Ub[(lane + 64) * RQ + j]);
+    float z = d * scale[(long)kvr * RQ + j];
+    if (lane == j) myz = z;
+  }
+  float a = (lane < RQ) ? fabsf(myz) : 0.f;
+  float emax = oa::wave_max(a);
+  int F = 0;
+  int Z = 0;
+  if (emax > 0.f && emax < INFINITY) {
+    int ex;
+    (void)frexpf(emax, &ex);
+    F = 30 - ex;
+    if (lane < RQ) Z = (int)rint(ldexp((double)myz, F));
+  }
+  if (lane < RQ) {
+    int l0 = (int)(int8_t)(Z & 0xff);
+    int z1 = (Z - l0) >> 8;
+    int l1 = (int)(int8_t)(z1 & 0xff);
+    int z2 = (z1 - l1) >> 8;
+    int l2 = (int)(int8_t)(z2 & 0xff);
+    int l3 = (z2 - l2) >> 8;
+    int8_t* Lb = limbs + (long)kvr * 16 * RQ;
+    Lb[(g * 4 + 0) * RQ + lane] = (int8_t)l0;
+    Lb[(g * 4 + 1) * RQ + lane] = (int8_t)l1;
+    Lb[(g * 4 + 2) * RQ + lane] = (int8_t)l2;
+    Lb[(g * 4 + 3) * RQ + lane] = (int8_t)l3;
+    if (zq_out) zq_out[(long)row * RQ + lane] = myz;
+  }
+  if (lane == 0) fexp[row] = F;
+}
+
+// ------------------------------------------------------------------------------------------
+// scan: grid (token chunks of kTokWG, BH).  4 waves; each wave streams 64-token tiles, four
+// MFMA blocks of 16 tokens per tile.  Writes the fp32 score of every position (sink/local and
+// positions >= n as -inf) and the maximum of every 64-token tile per query-head row.
+constexpr int kScanThreads = 256;
+constexpr int kTokWG = 1024;
+
+__global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
+    const int8_t* __restrict__ codes, int Lmax, const int8_t* __restrict__ limbs,
+    const int* __restrict__ fexp, float* __restrict__ S, long s_stride, float* __restrict__ TM,
+    long tm_stride, const int* __restrict__ n_dev, int ns, int nl) {
+  const int kvr = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int kg = lane >> 4;        // k-group for the operands; head g for the output
+  const int nn = lane & 15;        // token inside a 16-token block; limb row for A
+  const int n = *n_dev;
+  const int dead_hi = n - nl;      // positions >= dead_hi are local or not yet written
+
+  const long a_op = *reinterpret_cast<const long*>(limbs + (long)kvr * 16 * RQ + nn * RQ + kg * 8);
+  const int row = kvr * GQ + kg;
+  const double inv = ldexp(1.0, -fexp[row]);
+  float* Srow = S + (long)row * s_stride;
+  float* TMrow = TM + (long)row * tm_stride;
+  const int8_t* cb = codes + (long)kvr * Lmax * RQ;
+
+  const int tile_begin = blockIdx.x * (kTokWG / 64) + wave * (kTokWG / 256);
+  const int ntile_total = (Lmax + 63) / 64;
+  for (int tt = 0; tt < kTokWG / 256; ++tt) {
+    const int tile = tile_begin + tt;
+    if (tile >= ntile_total) break;
+    long b_op[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int tok = tile * 64 + b * 16 + nn;
+      b_op[b] = (tok < Lmax) ? *reinterpret_cast<const long*>(cb + (long)tok * RQ + kg * 8) : 0L;
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      oa_v4i zero = {0, 0, 0, 0};
+      oa_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_op, b_op[b], zero, 0, 0, 0);
+      double s = (double)acc[3];
+      s = fma(s, 256.0, (double)acc[2]);
+      s = fma(s, 256.0, (double)acc[1]);
+      s = fma(s, 256.0, (double)acc[0]);
+      float sc = (float)(s * inv);
+      const int tok = tile * 64 + b * 16 + nn;
+      if (tok < ns || tok >= dead_hi) sc = -INFINITY;
+      Srow[tok] = sc;
+      tmax = fmaxf(tmax, sc);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 8, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 4, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
+    if (nn == 0) TMrow[tile] = tmax;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// select: one wave per query-head row.  The k tiles with the largest maxima (ties to the
+// lower tile) hold every top-k token, the lowest-position tied ones included; the row top-k
+// is taken among their scores (ties to the lower position).  Then
+// sel = [0..ns) ++ [n-nl..n) ++ top, and the selected tokens' scores are set to -inf so the
+// within-cluster top-q ranks them last.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    unsigned long long o = __shfl_xor(v, m, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+constexpr int kMaxTilesLds = 4096;   // Lmax <= 262144
+constexpr int kMaxTop = 64;
+
+__global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, long s_stride,
+                                                         const float* __restrict__ TM, long tm_stride,
+                                                         int ntiles, int32_t* __restrict__ sel,
+                                                         long sel_stride, const int* __restrict__ n_dev,
+                                                         int ns, int nl, int k_top) {
+  __shared__ float s_tm[kMaxTilesLds];
+  __shared__ int s_tile[kMaxTop];
+  __shared__ float s_sc[kMaxTop * 64];
+  __shared__ int s_top[kMaxTop];
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int n = *n_dev;
+  float* Srow = S + (long)row * s_stride;
+  for (int t = lane; t < ntiles; t += 64) s_tm[t] = TM[(long)row * tm_stride + t];
+  __syncthreads();
+  // k best tiles
+  for (int i = 0; i < k_top; ++i) {
+    unsigned long long best = 0ull;
+    for (int t = lane; t < ntiles; t += 64) {
+      float v = s_tm[t];
+      if (v != v) continue;  // NaN marks a tile already taken
+      unsigned long long key = ((unsigned long long)oa::float_key(v) << 32) | (0xffffffffu - (unsigned)t);
+      best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    const int t = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
+    if (lane == 0) s_tile[i] = t;
+    __syncthreads();
+    if (lane == 0) s_tm[t] = __uint_as_float(0x7fc00000u);
+    __syncthreads();
+  }
+  for (int i = 0; i < k_top; ++i) s_sc[i * 64 + lane] = Srow[(long)s_tile[i] * 64 + lane];
+  __syncthreads();
+  // row top-k among the candidate tiles
+  for (int i = 0; i < k_top; ++i) {
+    unsigned long long best = 0ull;
+    for (int j = 0; j < k_top; ++j) {
+      float v = s_sc[j * 64 + lane];
+      if (v != v) continue;
+      const unsigned pos = (unsigned)(s_tile[j] * 64 + lane);
+      unsigned long long key = ((unsigned long long)oa::float_key(v) << 32) | (0xffffffffu - pos);
+      best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    const int pos = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
+    if (lane == 0) s_top[i] = pos;
+    for (int j = 0; j < k_top; ++j)
+      if (s_tile[j] * 64 + lane == pos) s_sc[j * 64 + lane] = __uint_as_float(0x7fc00000u);
+    __syncthreads();
+  }
+  int32_t* sr = sel + (long)row * sel_stride;
+  if (lane < ns) sr[lane] = lane;
+  if (lane < nl) sr[ns + lane] = n - nl + lane;
+  for (int i = lane; i < k_top; i += 64) sr[ns + nl + i] = s_top[i];
+  __syncthreads();
+  for (int i = lane; i < k_top; i += 64) Srow[s_top[i]] = -INFINITY;
+}
+
+}  // namespace
+
+extern "C" int oa_qgs_prep(const void* q, long q_stride, const float* U, const float* scale,
+                           int rows, int kv_rows, int head_dim, int rank, int8_t* limbs, int* fexp,
+                           float* zq_out, void* stream) {
+  if (head_dim != OA_D || rank != RQ || kv_rows <= 0 || rows != kv_rows * GQ) return OA_EINVAL;
+  hipLaunchKernelGGL(qgs_prep_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream,
+                     (const uint16_t*)q, q_stride, U, scale, GQ, limbs, fexp, zq_out);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
+                           const int* fexp, float* S, long s_stride, float* TM, long tm_stride,
+                           const int* n_dev, int ns, int nl, void* stream) {
+  if (rank != RQ || kv_rows <= 0 || Lmax <= 0) return OA_EINVAL;
+  const int ntile = (Lmax + 63) / 64;
+  if (s_stride < (long)ntile * 64 || tm_stride < ntile || ns < 0 || nl < 0) return OA_EINVAL;
+  dim3 grid((Lmax + kTokWG - 1) / kTokWG, kv_rows);
+  hipLaunchKernelGGL(qgs_scan_kernel, grid, dim3(kScanThreads), 0, (hipStream_t)stream, codes, Lmax,
+                     limbs, fexp, S, s_stride, TM, tm_stride, n_dev, ns, nl);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int rows,
+                              int ntiles, int32_t* sel, long sel_stride, const int* n_dev, int ns,
+                              int nl, int k_top, void* stream) {
+  if (rows <= 0 || ntiles <= 0 || ntiles > kMaxTilesLds || k_top < 0 || k_top > kMaxTop ||
+      k_top > ntiles || ns < 0 || nl < 0 || ns > 64 || nl > 64 || sel_stride < ns + nl + k_top)
+    return OA_EINVAL;
+  hipLaunchKernelGGL(topk_select_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, S, s_stride,
+                     TM, tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
+  return OA_LAUNCH_STATUS();
+}

@@ -1,0 +1,176 @@
+"""Method surface of the deployed decode step, backed by the gfx950 kernels.
+
+Mirrors inference/methods_eager.py:176-265 (Ctx, attn_hook, Method) and the deployed method
+OursG3/OursG2 (inference/ours_fastbuild.py:143-304, inference/ours_graph.py:265-347):
+  OursHIP(a, B, Lmax, dev).build(l, b, q, T)   prefill index build of layer l, batch row b
+  OursHIP(...).decode(l, q, n) -> (B, HQ, 1, D)  one decode step of layer l; the new K,V is
+                                                already at position n-1; n is also in C.n_dev
+Every buffer of the step is preallocated (per layer for the index, shared for the step's
+work buffers), nothing is read back on the host, and n / n0 are read on the device, so one
+decode step can be captured in a hipGraph (torch.cuda.CUDAGraph) and replayed.  The host
+only computes (ns, nl, k_top) from n, which the reference also keys its graphs by
+(eval_accuracy.py:64-66).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as TF
+
+from openattention_amd import ops
+from openattention_amd.budget import CTX_LEN, budget
+from openattention_amd.prefill import LayerState, build_row
+
+HQ, HKV, D, NL = 32, 8, 128, 32
+G = HQ // HKV
+SC = D ** -0.5
+RMAX = 256
+SCAN_TILE = 64
+
+
+class Ctx:
+    """Run state shared by the attention hook and the method (methods_eager.py:176-189)."""
+    phase = "prefill"
+    brow = 0
+    n = 0
+    K = None            # per layer (B, HKV, Lmax, D)
+    V = None
+    qlen = []           # question-chunk length per batch row
+    method = None
+    n_dev = None        # int32 (1,) device scalar: current length
+    n0_dev = None       # int32 (1,) device scalar: prefix length at the build
+    kv_idx = None       # int64 (1,) device index of the write position (n-1)
+
+
+C = Ctx()
+
+
+def attn_hook(module, query, key, value, attention_mask, dropout=0.0, scaling=None, is_causal=None, **kw):
+    """Attention-function hook with device-side positions (graph_runner.py:469-482)."""
+    l = module.layer_idx
+    T = query.shape[2]
+    if C.phase == "prefill":
+        b = C.brow
+        C.K[l][b:b + 1, :, :T] = key
+        C.V[l][b:b + 1, :, :T] = value
+        out = TF.scaled_dot_product_attention(query.float(), key.float(), value.float(), is_causal=True,
+                                              enable_gqa=True, scale=SC).to(query.dtype)
+        C.method.build(l, b, query, T)
+        return out.transpose(1, 2).contiguous(), None
+    C.K[l].index_copy_(2, C.kv_idx, key)
+    C.V[l].index_copy_(2, C.kv_idx, value)
+    out = C.method.decode(l, query, C.n)
+    return out.transpose(1, 2).contiguous(), None
+
+
+class Method:
+    name = "base"
+
+    def __init__(self, a, B, Lmax, dev):
+        self.a, self.B, self.Lmax, self.dev = a, B, Lmax, dev
+        self.R = B * HQ
+
+    def build(self, l, b, q, T):
+        pass
+
+
+class OursHIP(Method):
+    """The deployed OpenAttention decode step (QGS scan + top-k, ErrorGate, water-filling,
+    within-cluster top-q, residual proxies, fused softmax) on the gfx950 kernels."""
+    name = "ours_hip"
+
+    def __init__(self, a, B, Lmax, dev, n_layers: int = NL, static: dict | None = None,
+                 ctx_len: int = CTX_LEN, rule: str = "multibin", fused: bool = True):
+        super().__init__(a, B, Lmax, dev)
+        self.bud = budget(a.rho, ctx_len=ctx_len, rule=rule)
+        self.Cn, self.E = self.bud.C, self.bud.E
+        self.n_layers = n_layers
+        self.fused = fused
+        self.static = static
+        self.st = [LayerState(B, HKV, G, Lmax, self.Cn, RMAX, dev) for _ in range(n_layers)]
+        R, BH = self.R, B * HKV
+        self.ntiles = -(-Lmax // SCAN_TILE)
+        self.SW = self.ntiles * SCAN_TILE
+        f32 = dict(device=dev, dtype=torch.float32)
+        i32 = dict(device=dev, dtype=torch.int32)
+        self.limbs = torch.zeros(BH, 16, 32, device=dev, dtype=torch.int8)
+        self.fexp = torch.zeros(R, **i32)
+        self.S = torch.empty(R, self.SW, **f32)
+        self.TM = torch.empty(R, self.ntiles, **f32)
+        self.score = torch.empty(R, self.Cn, **f32)
+        self.n_t = torch.empty(R, self.Cn, **f32)
+        self.quota = torch.empty(R, self.Cn, **f32)
+        self.exp_idx = torch.empty(R, max(self.E, 1), **i32)
+        self.out = torch.empty(R, D, device=dev, dtype=torch.bfloat16)
+        self._sel = {}
+        if not fused:
+            self.kbar_r = torch.empty(R, self.Cn, D, device=dev, dtype=torch.bfloat16)
+            self.vbar_r = torch.empty(R, self.Cn, D, device=dev, dtype=torch.bfloat16)
+            self.log_n = torch.empty(R, self.Cn, **f32)
+
+    # ---------------------------------------------------------------- prefill
+    def build(self, l, b, q, T):
+        """Index build of layer l, batch row b after K,V of the prefix are in C.K[l][b, :, :T].
+        q: (1, HQ, Tq, D) prefill queries; the last C.qlen[b] rows are the question chunk."""
+        if self.static is None:
+            raise RuntimeError("OursHIP needs the static query metric (dict with M, inv_freq, "
+                               "attention_scaling)")
+        Qn = C.qlen[b]
+        qrows = q[0, :, q.shape[2] - Qn:, :]
+        build_row(self.st[l], b, C.K[l][b], C.V[l][b], qrows, T, self.static["M"][l],
+                  self.static["inv_freq"], float(self.static.get("attention_scaling", 1.0)), l, G)
+
+    # ---------------------------------------------------------------- decode
+    def sel_buffer(self, NS: int) -> torch.Tensor:
+        if NS not in self._sel:
+            self._sel[NS] = torch.empty(self.R, NS, device=self.dev, dtype=torch.int32)
+        return self._sel[NS]
+
+    def decode(self, l, q, n, marks: list | None = None):
+        """One decode step of layer l.  `marks`, when given, receives (stage, event) pairs
+        recorded on the current stream after each stage (per-stage timing)."""
+        st = self.st[l]
+
+        def mark(name):
+            if marks is not None:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record()
+                marks.append((name, ev))
+
+        K = C.K[l].view(-1, self.Lmax, D)
+        V = C.V[l].view(-1, self.Lmax, D)
+        qr = q.reshape(self.R, D)
+        if not qr.is_contiguous():
+            qr = qr.contiguous()
+        ns, nl, k_top = self.bud.counts(n)
+        if n - ns - nl < k_top:
+            raise ValueError(f"n={n} too small for sink {ns} + local {nl} + top-k {k_top}")
+        NS = ns + nl + k_top
+        sel = self.sel_buffer(NS)
+        mark("start")
+        ops.index_update(K, V, st, C.n_dev, RMAX)
+        mark("index_update")
+        ops.qgs_prep(qr, st.U, st.scale, self.limbs, self.fexp)
+        mark("qgs_prep")
+        ops.qgs_scan(st.codes, self.limbs, self.fexp, self.S, self.TM, C.n_dev, ns, nl)
+        mark("qgs_scan")
+        ops.topk_select(self.S, self.TM, sel, C.n_dev, ns, nl, k_top)
+        mark("topk_select")
+        ops.errorgate(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, SC)
+        mark("errorgate")
+        ops.waterfill(self.score, self.n_t, self.quota, self.E)
+        mark("waterfill")
+        ops.topq(self.S, st, self.quota, self.exp_idx, C.n_dev, C.n0_dev, RMAX)
+        mark("topq")
+        if self.fused:
+            ops.residual_flash(qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk,
+                               st.Sv, self.out, SC)
+            mark("residual_flash")
+        else:
+            ops.residual(K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk, st.Sv,
+                         self.kbar_r, self.vbar_r, self.log_n)
+            mark("residual")
+            ops.flash_decode(qr, K, V, sel, self.exp_idx, self.kbar_r, self.vbar_r, self.log_n,
+                             proxy_per_kv=False, sm_scale=SC, out=self.out)
+            mark("flash")
+        self.last_sel = sel
+        return self.out.view(self.B, HQ, 1, D)

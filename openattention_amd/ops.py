@@ -1,0 +1,244 @@
+"""torch-tensor front end of the gfx950 kernels.
+
+Operator surface kept from the reference:
+  ours_flash(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, nb=None)      methods_eager.py:161-172
+  decode_expand_attention(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n,
+                          sm_scale=None, block_n=64, block_b=64, num_warps=4)
+                                                                        triton_expand_decode.py:139-165
+plus one function per decode stage (index_update, qgs_prep, qgs_scan, topk_select, errorgate,
+waterfill, topq, residual, residual_flash, dense_decode), each a thin checked call of the C ABI
+(include/openattention_amd.h) on torch's current HIP stream.  Shape, dtype, device, alignment
+and stride checks happen here; the kernels trust them.  There is no CPU path: tensors must live
+on a HIP device and the kernel library must be built.
+"""
+from __future__ import annotations
+
+import torch
+
+from openattention_amd import lib
+
+HEAD_DIM = 128
+RANK_Q = 32
+RANK_C = 16
+GROUP = 4
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _dev(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError("openattention_amd kernels need tensors on a HIP device "
+                               f"(got {t.device}); there is no CPU fallback")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _rows_contig(t: torch.Tensor, name: str, align_elems: int = 1) -> None:
+    _need(t.stride(-1) == 1, f"{name}: last dimension must be contiguous")
+    for s in t.stride()[:-1]:
+        _need(s % align_elems == 0, f"{name}: strides must be multiples of {align_elems} elements")
+    _need(t.data_ptr() % (2 * align_elems if t.dtype == torch.bfloat16 else 4 * align_elems) == 0,
+          f"{name}: base pointer misaligned")
+
+
+def _contig(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    _need(t.dtype == dtype, f"{name}: expected {dtype}, got {t.dtype}")
+    _need(t.is_contiguous(), f"{name}: must be contiguous")
+
+
+# ================================================================== OpenAttention.flash
+def flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, *, proxy_per_kv: bool,
+                 sm_scale: float, n_bins: int | None = None, n_split: int | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Shared body of ours_flash / decode_expand_attention."""
+    dev = _dev(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n)
+    R, D = q.shape
+    _need(D == HEAD_DIM, f"head_dim must be {HEAD_DIM}")
+    _need(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
+          "q, k, v must be bfloat16")
+    _need(k.dim() == 3 and k.shape == v.shape and k.stride() == v.stride() and k.shape[2] == D,
+          "k, v must be (B*HKV, Lmax, D) with identical strides")
+    BH = k.shape[0]
+    _need(R % BH == 0, "rows of q must be a multiple of the KV rows of k")
+    _rows_contig(q, "q", 8)
+    _rows_contig(k, "k", 8)
+    _rows_contig(v, "v", 8)
+    _need(sel_idx.dtype == torch.int32 and exp_idx.dtype == torch.int32, "indices must be int32")
+    _need(sel_idx.shape[0] == R and exp_idx.shape[0] == R, "index rows must match q")
+    _need(sel_idx.stride(-1) == 1 and exp_idx.stride(-1) == 1, "index rows must be contiguous")
+    NB = kbar.shape[1] if n_bins is None else int(n_bins)
+    _need(0 <= NB <= kbar.shape[1], "nb out of range")
+    _need(kbar.shape == vbar.shape and kbar.stride() == vbar.stride() and kbar.dtype == vbar.dtype,
+          "kbar and vbar must match")
+    _need(kbar.dtype in (torch.bfloat16, torch.float32), "kbar/vbar must be bf16 or fp32")
+    _need(kbar.shape[0] == (BH if proxy_per_kv else R) and kbar.shape[2] == D, "kbar shape")
+    _rows_contig(kbar, "kbar", 8 if kbar.dtype == torch.bfloat16 else 4)
+    _need(log_n.dtype == torch.float32 and log_n.shape[0] == R and log_n.stride(-1) == 1,
+          "log_n must be fp32 (R, C)")
+    if out is None:
+        out = torch.empty_like(q)
+    T = sel_idx.shape[1] + exp_idx.shape[1] + NB
+    if n_split is None:
+        # few rows cannot fill the GPU: split each row's list (reference: ours_graph.py:276)
+        n_split = 1 if R >= 512 else max(2, min(16, (4096 // max(R, 1)), -(-T // 32)))
+    n_split = max(1, int(n_split))
+    ws = None
+    if n_split > 1:
+        ws = torch.empty(R * n_split * (HEAD_DIM + 2), device=dev, dtype=torch.float32)
+        ws_m = ws[: R * n_split]
+        ws_l = ws[R * n_split: 2 * R * n_split]
+        ws_acc = ws[2 * R * n_split:]
+    lib.call("oa_flash_decode",
+             _ptr(q), q.stride(0), _ptr(k), _ptr(v), k.stride(0), k.stride(1),
+             _ptr(sel_idx), sel_idx.stride(0), sel_idx.shape[1],
+             _ptr(exp_idx), exp_idx.stride(0), exp_idx.shape[1],
+             _ptr(kbar), _ptr(vbar), kbar.stride(0), kbar.stride(1),
+             1 if kbar.dtype == torch.float32 else 0, 1 if proxy_per_kv else 0,
+             _ptr(log_n), log_n.stride(0), NB, _ptr(out), out.stride(0),
+             R, BH, D, float(sm_scale), n_split,
+             _ptr(ws_m) if ws is not None else None, _ptr(ws_l) if ws is not None else None,
+             _ptr(ws_acc) if ws is not None else None, _stream(dev))
+    return out
+
+
+def ours_flash(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, nb=None):
+    """q:(R,D) k,v:(B*HKV,Lmax,D) sel:(R,Ns) exp:(R,Ne) int32 (-1 = pad); kbar,vbar:(R,C,D);
+    log_n:(R,C) natural log, -inf = no proxy.  nb overrides the proxy count (0 = P3 off).
+    Same contract as inference/methods_eager.py:161-172; sm_scale = D**-0.5."""
+    return flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, proxy_per_kv=False,
+                        sm_scale=HEAD_DIM ** -0.5, n_bins=nb)
+
+
+def decode_expand_attention(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, sm_scale=None,
+                            block_n=64, block_b=64, num_warps=4):
+    """q:(BQ,D) k,v:(BH,K,D) sel_idx:(BQ,N_SEL) exp_idx:(BQ,N_EXP) kbar,vbar:(BH,NB,D)
+    log_n:(BQ,NB) -> (BQ,D).  Same contract as triton_expand_decode.py:139-165; the Triton
+    tuning arguments (block_n, block_b, num_warps) are accepted and ignored."""
+    D = q.shape[1]
+    scale = D ** -0.5 if sm_scale is None else float(sm_scale)
+    return flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, proxy_per_kv=True,
+                        sm_scale=scale)
+
+
+# ================================================================== decode-stage kernels
+def index_update(K, V, st, n_dev: torch.Tensor, rmax: int) -> None:
+    """The token at n-1 joins the index (ours_graph.py:43-90).  st: LayerState-like object
+    with codes, U, scale, W, colmean, cent, asg, nb, Sk, Sk2, Sv, reclist, reccnt (one layer,
+    all batch rows, flattened to rows)."""
+    dev = _dev(K, V, n_dev)
+    BH, Lmax, D = K.shape
+    R = st.nb.shape[0]
+    C = st.nb.shape[1]
+    lib.call("oa_index_update", _ptr(K), _ptr(V), K.stride(0), K.stride(1), R, BH, D,
+             _ptr(st.codes), st.codes.shape[1], RANK_Q, _ptr(st.U), _ptr(st.scale), _ptr(st.W),
+             _ptr(st.colmean), RANK_C, _ptr(st.cent), C, _ptr(st.asg), st.asg.stride(0),
+             _ptr(st.nb), _ptr(st.Sk), _ptr(st.Sk2), _ptr(st.Sv), _ptr(st.reclist),
+             _ptr(st.reccnt), rmax, _ptr(n_dev), _stream(dev))
+
+
+def qgs_prep(q, U, scale, limbs, fexp, zq_out=None) -> None:
+    dev = _dev(q, U, scale, limbs, fexp)
+    R = q.shape[0]
+    BH = U.shape[0]
+    _rows_contig(q, "q")
+    lib.call("oa_qgs_prep", _ptr(q), q.stride(0), _ptr(U), _ptr(scale), R, BH, q.shape[1], RANK_Q,
+             _ptr(limbs), _ptr(fexp), _ptr(zq_out), _stream(dev))
+
+
+def qgs_scan(codes, limbs, fexp, S, TM, n_dev, ns: int, nl: int) -> None:
+    dev = _dev(codes, limbs, fexp, S, TM, n_dev)
+    BH, Lmax, rq = codes.shape
+    lib.call("oa_qgs_scan", _ptr(codes), BH, Lmax, rq, _ptr(limbs), _ptr(fexp), _ptr(S), S.stride(0),
+             _ptr(TM), TM.stride(0), _ptr(n_dev), ns, nl, _stream(dev))
+
+
+def topk_select(S, TM, sel, n_dev, ns: int, nl: int, k_top: int) -> None:
+    dev = _dev(S, TM, sel, n_dev)
+    R = S.shape[0]
+    lib.call("oa_topk_select", _ptr(S), S.stride(0), _ptr(TM), TM.stride(0), R, TM.shape[1],
+             _ptr(sel), sel.stride(0), _ptr(n_dev), ns, nl, k_top, _stream(dev))
+
+
+def errorgate(q, K, asg, sel, Sk, Sk2, nb, score, n_t, sm_scale: float) -> None:
+    dev = _dev(q, K, asg, sel, Sk, Sk2, nb, score, n_t)
+    R, C = nb.shape
+    BH = K.shape[0]
+    lib.call("oa_errorgate", _ptr(q), q.stride(0), _ptr(K), K.stride(0), K.stride(1), R, BH,
+             q.shape[1], _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1],
+             _ptr(Sk), _ptr(Sk2), _ptr(nb), C, float(sm_scale), _ptr(score), _ptr(n_t), _stream(dev))
+
+
+def waterfill(score, n_t, quota, E: int) -> None:
+    dev = _dev(score, n_t, quota)
+    R, C = score.shape
+    lib.call("oa_waterfill", _ptr(score), _ptr(n_t), R, C, int(E), _ptr(quota), _stream(dev))
+
+
+def topq(S, st, quota, exp_idx, n_dev, n0_dev, rmax: int) -> None:
+    dev = _dev(S, quota, exp_idx, n_dev, n0_dev)
+    R, C = quota.shape
+    lib.call("oa_topq", _ptr(S), S.stride(0), _ptr(st.mem), st.mem.stride(0), _ptr(st.cstart),
+             _ptr(st.clen), _ptr(st.reclist), _ptr(st.reccnt), rmax, _ptr(st.asg), st.asg.stride(0),
+             _ptr(quota), R, C, _ptr(exp_idx), exp_idx.shape[1], _ptr(n_dev), _ptr(n0_dev),
+             _stream(dev))
+
+
+def residual(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n) -> None:
+    dev = _dev(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n)
+    R, C = quota.shape
+    BH = K.shape[0]
+    lib.call("oa_residual", _ptr(K), _ptr(V), K.stride(0), K.stride(1), R, BH, K.shape[2],
+             _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1], _ptr(exp_idx),
+             exp_idx.shape[1], _ptr(quota), _ptr(n_t), _ptr(Sk), _ptr(Sv), C, _ptr(kbar_r),
+             _ptr(vbar_r), _ptr(log_n), _stream(dev))
+
+
+def residual_flash(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out, sm_scale: float) -> None:
+    dev = _dev(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out)
+    R, C = quota.shape
+    BH = K.shape[0]
+    lib.call("oa_residual_flash", _ptr(q), q.stride(0), _ptr(K), _ptr(V), K.stride(0), K.stride(1),
+             R, BH, K.shape[2], _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1],
+             _ptr(exp_idx), exp_idx.shape[1], _ptr(quota), _ptr(n_t), _ptr(Sk), _ptr(Sv), C,
+             float(sm_scale), _ptr(out), out.stride(0), _stream(dev))
+
+
+def dense_decode(q, K, V, n_dev, out=None, sm_scale: float | None = None, nsplit: int | None = None,
+                 ws: torch.Tensor | None = None) -> torch.Tensor:
+    """Dense decode attention over [0, n) (graph_runner.py:259-312 comparator)."""
+    dev = _dev(q, K, V, n_dev)
+    R, D = q.shape
+    BH, Lmax, _ = K.shape
+    _rows_contig(q, "q", 8)
+    _rows_contig(K, "K", 8)
+    if nsplit is None:
+        nsplit = max(4, min(256, 2048 // BH))
+    if out is None:
+        out = torch.empty_like(q)
+    need = R * nsplit * (HEAD_DIM + 2)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, device=dev, dtype=torch.float32)
+    scale = D ** -0.5 if sm_scale is None else sm_scale
+    lib.call("oa_dense_decode", _ptr(q), q.stride(0), _ptr(K), _ptr(V), K.stride(0), K.stride(1), R,
+             BH, D, Lmax, _ptr(n_dev), float(scale), nsplit, _ptr(ws[: R * nsplit]),
+             _ptr(ws[R * nsplit: 2 * R * nsplit]), _ptr(ws[2 * R * nsplit: need]), _ptr(out),
+             out.stride(0), _stream(dev))
+    return out

@@ -1,0 +1,223 @@
+"""Per-request index build at prefill (QGS codes, QGC clusters, cluster sums, CSR lists).
+
+Follows the deployed build (inference/methods_eager.py:505-555, inference/ours_fastbuild.py:
+199-304) with the accuracy-path choices where the two differ (k-means seed 1234 + 31(l+1) of
+multibin.py:1894):
+  a10  M_st rotated to the decode position T by the closed-form window average over w = 32
+       positions (StaticTopKMasker._rot_avg, static_top_k.py:103-131); M_q from P <= 64
+       question rows, each rotated to T (static_top_k.py:185-194); M = 1/2 nt(M_st) + 1/2
+       nt(M_q), nt = trace normalisation; U = top-32 eigenvectors of the group-mean M per KV
+       head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.
+  a11  zc = k U (fp32); scale = max(max_t |zc| / 127, 1e-12) per (KV head, coordinate),
+       fixed at the build; codes = clamp(round(zc / scale), -127, 127) int8
+       (static_top_k.py:174-181).
+  a12  zP = bf16(k W) - colmean; 4 Lloyd iterations with the bf16 distance
+       bf16(bf16(zP_bf16 . c_bf16) - bf16(|c|^2 / 2)), argmax with ties to the lower cluster,
+       centroid = mean (an empty cluster keeps its initial point) (methods_eager.py:526-547).
+  a13  CSR member lists = stable argsort of the assignment; n_b, sum k, sum k^2, sum v per
+       cluster in fp32 (ours_fastbuild.py:293-301).
+The torch operations here run on whichever device the tensors live on.  torch.linalg.eigh and
+the fp32 scatter sums are not bitwise reproducible across devices/libraries, so the decode
+stage's parity tests inject one built state into both the GPU kernels and the CPU restatement.
+"""
+from __future__ import annotations
+
+import torch
+
+D = 128
+RQ, RC = 32, 16
+WIN = 32
+P_ROWS = 64
+ITERS = 4
+
+
+def rope_cs(inv_freq: torch.Tensor, scaling: float, positions: torch.Tensor):
+    """static_top_k.py:91-95"""
+    freqs = positions.float().unsqueeze(-1) * inv_freq.unsqueeze(0)
+    emb = torch.cat([freqs, freqs], -1)
+    return emb.cos() * scaling, emb.sin() * scaling
+
+
+def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """static_top_k.py:97-100"""
+    h = x.shape[-1] // 2
+    return x * cos + torch.cat([-x[..., h:], x[..., :h]], -1) * sin
+
+
+def rot_coefs(inv_freq: torch.Tensor, scaling: float, p: int, w: int):
+    """fp64 window-average coefficients of R_t M R_t^T, t in [p, p+w) (static_top_k.py:108-126)."""
+    dev = inv_freq.device
+    th = torch.cat([inv_freq, inv_freq]).double()
+    a = th.unsqueeze(1)
+    b = th.unsqueeze(0)
+
+    def mean_exp(alpha):
+        if w <= 64:
+            t = torch.arange(p, p + w, device=dev, dtype=torch.float64)
+            ph = alpha.unsqueeze(-1) * t
+            return torch.complex(ph.cos().mean(-1), ph.sin().mean(-1))
+        z = torch.polar(torch.ones_like(alpha), alpha)
+        den = 1 - z
+        small = den.abs() < 1e-9
+        s = torch.where(small, torch.full_like(z, float(w)),
+                        (1 - z ** w) / torch.where(small, torch.ones_like(den), den))
+        return s * torch.polar(torch.ones_like(alpha), alpha * p) / w
+
+    Em = mean_exp(a - b)
+    Ep = mean_exp(a + b)
+    cc = 0.5 * (Em.real + Ep.real)
+    ss = 0.5 * (Em.real - Ep.real)
+    cs = 0.5 * (Ep.imag - Em.imag)
+    sc = 0.5 * (Ep.imag + Em.imag)
+    return [x.float() * (scaling * scaling) for x in (cc, ss, cs, sc)]
+
+
+def j_matrix(dim: int, dev) -> torch.Tensor:
+    h = dim // 2
+    J = torch.zeros(dim, dim, device=dev)
+    J[:h, h:] = -torch.eye(h, device=dev)
+    J[h:, :h] = torch.eye(h, device=dev)
+    return J
+
+
+def rot_avg(M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, p: int, w: int = WIN):
+    """mean_{t in [p, p+w)} R_t M R_t^T, closed form (static_top_k.py:103-131)."""
+    cc, ss, cs, sc = rot_coefs(inv_freq, scaling, p, w)
+    J = j_matrix(M_pre.shape[-1], M_pre.device)
+    M = M_pre.float()
+    return cc * M + cs * (M @ J.T) + sc * (J @ M) + ss * (J @ M @ J.T)
+
+
+def question_moment(qrows: torch.Tensor, inv_freq: torch.Tensor, scaling: float) -> torch.Tensor:
+    """M_q from P <= 64 of the question rows (HQ, Qn, D), row i rotated by Qn - i positions
+    (static_top_k.py:185-194)."""
+    Qn = qrows.shape[1]
+    P = min(P_ROWS, max(Qn - 2, 1))
+    pi = torch.linspace(0, max(Qn - 3, 0), P, device=qrows.device).long().unique()
+    qsel = qrows.index_select(1, pi).float()
+    cos, sin = rope_cs(inv_freq, scaling, (Qn - pi).to(qrows.device))
+    qrot = rope_apply(qsel, cos, sin)
+    return torch.matmul(qrot.transpose(-1, -2), qrot) / qrot.shape[1]
+
+
+def trace_norm(x: torch.Tensor) -> torch.Tensor:
+    return x / torch.diagonal(x, dim1=-2, dim2=-1).sum(-1).clamp(min=1e-12)[..., None, None]
+
+
+def query_metric(M_pre: torch.Tensor, qrows: torch.Tensor, T: int, inv_freq, scaling) -> torch.Tensor:
+    """M = 1/2 nt(M_st rotated to T) + 1/2 nt(M_q)  (methods_eager.py:511-518)."""
+    Mst = rot_avg(M_pre, inv_freq, scaling, T, WIN)
+    Mq = question_moment(qrows, inv_freq, scaling)
+    return 0.5 * trace_norm(Mst) + 0.5 * trace_norm(Mq)
+
+
+def kmeans_seed(layer: int) -> int:
+    """multibin.py:1894 (accuracy path); the deployed build uses 31 * (layer + 1)."""
+    return 1234 + 31 * (layer + 1)
+
+
+@torch.no_grad()
+def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int,
+              M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, layer: int,
+              G: int = 4) -> None:
+    """Build batch row b of one layer's index into `st` (a LayerState).
+
+    K, V: (HKV, >=T, D) bf16 of this batch row; qrows: (HQ, Qn, D) question rows.
+    """
+    dev = K.device
+    HKV = K.shape[0]
+    HQ = HKV * G
+    C = st.C
+    k = K[:, :T]
+    v = V[:, :T]
+    M = query_metric(M_pre.to(dev), qrows, T, inv_freq.to(dev), scaling)           # (HQ, D, D)
+    # QGS (a11): one U per KV head
+    _, Ukv = torch.linalg.eigh(M.view(HKV, G, D, D).mean(1))
+    U = Ukv[..., -RQ:].contiguous()
+    zc = torch.matmul(k.float(), U)
+    scale = (zc.abs().amax(1, keepdim=True) / 127.0).clamp(min=1e-12)
+    r0 = b * HKV
+    st.codes[r0:r0 + HKV, :T] = (zc / scale).round().clamp(-127, 127).to(torch.int8)
+    st.U[r0:r0 + HKV] = U
+    st.scale[r0:r0 + HKV] = scale[:, 0]
+    # QGC projection (a10/a12)
+    ev, Uq = torch.linalg.eigh(M)
+    W = (Uq[..., -RC:] * ev[..., -RC:].clamp(min=0).sqrt().unsqueeze(-2)).to(torch.bfloat16)
+    krep = k.repeat_interleave(G, 0).contiguous()
+    zP = torch.matmul(krep, W.contiguous()).float()                                  # bf16 matmul
+    colmean = zP.mean(1, keepdim=True)
+    zP = zP - colmean
+    g = torch.Generator(device="cpu").manual_seed(kmeans_seed(layer))
+    init = torch.randperm(T, generator=g)[:C].to(dev)
+    cent = zP.index_select(1, init).clone()
+    zb = zP.to(torch.bfloat16)
+    asg = torch.empty(HQ, T, device=dev, dtype=torch.long)
+    ones = torch.ones(HQ, T, device=dev)
+    for _ in range(ITERS):
+        half = (0.5 * (cent * cent).sum(-1)).to(torch.bfloat16).unsqueeze(1)
+        cb = cent.to(torch.bfloat16).transpose(1, 2).contiguous()
+        for h0 in range(0, HQ, 8):
+            asg[h0:h0 + 8] = (torch.matmul(zb[h0:h0 + 8], cb[h0:h0 + 8]) - half[h0:h0 + 8]).argmax(-1)
+        acc = torch.zeros(HQ, C, RC, device=dev).scatter_add_(1, asg.unsqueeze(-1).expand(-1, -1, RC), zP)
+        cnt = torch.zeros(HQ, C, device=dev).scatter_add_(1, asg, ones)
+        cent = torch.where(cnt.unsqueeze(-1) > 0, acc / cnt.clamp(min=1).unsqueeze(-1),
+                           zP.index_select(1, init))
+    q0 = b * HQ
+    st.asg[q0:q0 + HQ, :T] = asg.to(torch.int32)
+    st.W[q0:q0 + HQ] = W
+    st.colmean[q0:q0 + HQ] = colmean[:, 0]
+    st.cent[q0:q0 + HQ] = cent
+    # cluster sums (a13) and CSR member lists
+    idx = asg.unsqueeze(-1).expand(-1, -1, D)
+    kf = krep.float()
+    vf = v.repeat_interleave(G, 0).float()
+    nb = torch.zeros(HQ, C, device=dev).scatter_add_(1, asg, ones)
+    st.nb[q0:q0 + HQ] = nb
+    st.Sk[q0:q0 + HQ] = torch.zeros(HQ, C, D, device=dev).scatter_add_(1, idx, kf)
+    st.Sk2[q0:q0 + HQ] = torch.zeros(HQ, C, D, device=dev).scatter_add_(1, idx, kf * kf)
+    st.Sv[q0:q0 + HQ] = torch.zeros(HQ, C, D, device=dev).scatter_add_(1, idx, vf)
+    st.mem[q0:q0 + HQ, :T] = torch.argsort(asg, dim=-1, stable=True).to(torch.int32)
+    cntc = nb.round().to(torch.int32)
+    st.cstart[q0:q0 + HQ] = (cntc.cumsum(-1) - cntc).to(torch.int32)
+    st.clen[q0:q0 + HQ] = cntc
+    st.reccnt[q0:q0 + HQ] = 0
+
+
+class LayerState:
+    """One layer's decode index for all B batch rows (rows flattened: KV rows b*HKV + h,
+    query-head rows b*HQ + h)."""
+
+    FIELDS = ("codes", "U", "scale", "W", "colmean", "cent", "asg", "nb", "Sk", "Sk2", "Sv",
+              "mem", "cstart", "clen", "reclist", "reccnt")
+
+    def __init__(self, B: int, HKV: int, G: int, Lmax: int, C: int, rmax: int, dev):
+        BH, R = B * HKV, B * HKV * G
+        self.B, self.HKV, self.G, self.Lmax, self.C, self.rmax = B, HKV, G, Lmax, C, rmax
+        z = lambda *s, dt=torch.float32: torch.zeros(*s, device=dev, dtype=dt)  # noqa: E731
+        self.codes = z(BH, Lmax, RQ, dt=torch.int8)
+        self.U = z(BH, D, RQ)
+        self.scale = z(BH, RQ)
+        self.W = z(R, D, RC, dt=torch.bfloat16)
+        self.colmean = z(R, RC)
+        self.cent = z(R, C, RC)
+        self.asg = z(R, Lmax, dt=torch.int32)
+        self.nb = z(R, C)
+        self.Sk = z(R, C, D)
+        self.Sk2 = z(R, C, D)
+        self.Sv = z(R, C, D)
+        self.mem = z(R, Lmax, dt=torch.int32)
+        self.cstart = z(R, C, dt=torch.int32)
+        self.clen = z(R, C, dt=torch.int32)
+        self.reclist = z(R, C, max(rmax, 1), dt=torch.int32)
+        self.reccnt = z(R, C, dt=torch.int32)
+
+    def to_numpy(self) -> dict:
+        return {f: getattr(self, f).detach().cpu().contiguous().numpy().copy()
+                if getattr(self, f).dtype != torch.bfloat16 else
+                getattr(self, f).detach().cpu().contiguous().view(torch.int16).numpy().view("uint16").copy()
+                for f in self.FIELDS}
+
+    def clone(self) -> "LayerState":
+        new = LayerState.__new__(LayerState)
+        new.__dict__.update({k: (v.clone() if torch.is_tensor(v) else v) for k, v in self.__dict__.items()})
+        return new

@@ -1,0 +1,222 @@
+"""numpy front end of the CPU restatement (oracle/oa_oracle.c) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, as the
+checker.  Each wrapper names the reference lines the C function restates.
+
+Pinning (what fixes each function independently of the GPU code) is done in
+tests/test_oracle_pins.py: brute-force integer/Fraction scores, fp64 closed forms, an exact
+rational water-filling solver, libm comparisons of the deterministic elementary functions,
+sorted-selection brute force for top-k / top-q, and invariants.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+D, RQ, RC = 128, 32, 16
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        from oracle import build as _b
+        if not os.path.exists(_b.LIB) or os.path.getmtime(_b.LIB) < os.path.getmtime(_b.SRC):
+            _b.build()
+        lib = ct.CDLL(_b.LIB)
+        lib.oa_det_exp.restype = ct.c_double
+        lib.oa_det_exp.argtypes = [ct.c_double]
+        lib.oa_det_log.restype = ct.c_double
+        lib.oa_det_log.argtypes = [ct.c_double]
+        lib.oa_det_logf.restype = ct.c_float
+        lib.oa_det_logf.argtypes = [ct.c_float]
+        lib.oa_det_erff.restype = ct.c_float
+        lib.oa_det_erff.argtypes = [ct.c_float]
+        _LIB = lib
+    return _LIB
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ct.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ------------------------------------------------------------------ elementary functions
+def det_exp(x: float) -> float:
+    return _lib().oa_det_exp(float(x))
+
+
+def det_log(x: float) -> float:
+    return _lib().oa_det_log(float(x))
+
+
+def det_logf(x: float) -> float:
+    return _lib().oa_det_logf(float(x))
+
+
+def det_erff(x: float) -> float:
+    return _lib().oa_det_erff(float(x))
+
+
+# ------------------------------------------------------------------ decode-stage functions
+def qgs_prep(q_bf16: np.ndarray, U: np.ndarray, scale: np.ndarray, G: int):
+    """static_top_k.py:203-213 -> (zq (R,32) f32, fexp (R,) i32, Z (R,32) i32)"""
+    q = _c(q_bf16, np.uint16)
+    R = q.shape[0]
+    U = _c(U, np.float32)
+    scale = _c(scale, np.float32)
+    zq = np.zeros((R, RQ), np.float32)
+    fexp = np.zeros(R, np.int32)
+    Z = np.zeros((R, RQ), np.int32)
+    _lib().oa_ref_qgs_prep(_p(q), _p(U), _p(scale), ct.c_int(R), ct.c_int(G), _p(zq), _p(fexp), _p(Z))
+    return zq, fexp, Z
+
+
+def qgs_scores(codes: np.ndarray, Z: np.ndarray, fexp: np.ndarray, G: int, n: int, ns: int, nl: int,
+               ncols: int | None = None) -> np.ndarray:
+    """static_top_k.py:197-218 + sink/local masking -> S (R, ncols) f32"""
+    codes = _c(codes, np.int8)
+    BH, Lmax, _ = codes.shape
+    Z = _c(Z, np.int32)
+    fexp = _c(fexp, np.int32)
+    R = Z.shape[0]
+    ncols = Lmax if ncols is None else ncols
+    S = np.zeros((R, ncols), np.float32)
+    _lib().oa_ref_qgs_scores(_p(codes), ct.c_int(Lmax), _p(Z), _p(fexp), ct.c_int(R), ct.c_int(G),
+                             ct.c_int(n), ct.c_int(ns), ct.c_int(nl), ct.c_int(ncols), _p(S))
+    return S
+
+
+def topk_select(S: np.ndarray, n: int, ns: int, nl: int, k: int) -> np.ndarray:
+    """basic_fixed.py:48-67,354-363 + fixed/base.py:74-85 -> sel (R, ns+nl+k) i32"""
+    S = _c(S, np.float32)
+    R, ncols = S.shape
+    sel = np.zeros((R, ns + nl + k), np.int32)
+    _lib().oa_ref_topk_select(_p(S), ct.c_int(ncols), ct.c_int(R), ct.c_int(n), ct.c_int(ns),
+                              ct.c_int(nl), ct.c_int(k), _p(sel))
+    return sel
+
+
+def errorgate(q_bf16, K_bf16, asg, sel, Sk, Sk2, nb, G: int, sc: float, sc2: float):
+    """multibin.py:605-644, 734-738, 2370-2389; methods_eager.py:612-627 -> (score, n_t) (R,C) f32"""
+    q = _c(q_bf16, np.uint16)
+    K = _c(K_bf16, np.uint16)
+    asg = _c(asg, np.int32)
+    sel = _c(sel, np.int32)
+    Sk, Sk2, nb = _c(Sk, np.float32), _c(Sk2, np.float32), _c(nb, np.float32)
+    R, C = nb.shape
+    Lmax = K.shape[1]
+    score = np.zeros((R, C), np.float32)
+    n_t = np.zeros((R, C), np.float32)
+    _lib().oa_ref_errorgate(_p(q), _p(K), ct.c_int(Lmax), _p(asg), _p(sel), ct.c_int(sel.shape[1]),
+                            _p(Sk), _p(Sk2), _p(nb), ct.c_int(R), ct.c_int(G), ct.c_int(C),
+                            ct.c_float(sc), ct.c_float(sc2), _p(score), _p(n_t))
+    return score, n_t
+
+
+def waterfill(score, n_t, E: int) -> np.ndarray:
+    """multibin.py:1385-1422 (+ order 2471-2472) -> quota (R,C) f32"""
+    score, n_t = _c(score, np.float32), _c(n_t, np.float32)
+    R, C = score.shape
+    quota = np.zeros((R, C), np.float32)
+    _lib().oa_ref_waterfill(_p(score), _p(n_t), ct.c_int(R), ct.c_int(C), ct.c_double(float(E)),
+                            _p(quota))
+    return quota
+
+
+def topq(S, asg, sel, quota, n: int, E: int) -> np.ndarray:
+    """multibin.py:2522-2558 with lower-position ties -> exp_idx (R,E) i32"""
+    S = _c(S, np.float32)
+    asg = _c(asg, np.int32)
+    sel = _c(sel, np.int32)
+    quota = _c(quota, np.float32)
+    R, C = quota.shape
+    exp_idx = np.zeros((R, E), np.int32)
+    _lib().oa_ref_topq(_p(S), ct.c_int(S.shape[1]), _p(asg), ct.c_int(asg.shape[1]), _p(sel),
+                       ct.c_int(sel.shape[1]), _p(quota), ct.c_int(R), ct.c_int(C), ct.c_int(n),
+                       ct.c_int(E), _p(exp_idx))
+    return exp_idx
+
+
+def residual(K_bf16, V_bf16, asg, sel, exp_idx, quota, n_t, Sk, Sv, G: int):
+    """multibin.py:2598-2642 (residual_stats='full') -> (kbar_r, vbar_r (R,C,D), log_n (R,C)) f64"""
+    K, V = _c(K_bf16, np.uint16), _c(V_bf16, np.uint16)
+    asg, sel, exp_idx = _c(asg, np.int32), _c(sel, np.int32), _c(exp_idx, np.int32)
+    quota, n_t = _c(quota, np.float32), _c(n_t, np.float32)
+    Sk, Sv = _c(Sk, np.float32), _c(Sv, np.float32)
+    R, C = quota.shape
+    kb = np.zeros((R, C, D), np.float64)
+    vb = np.zeros((R, C, D), np.float64)
+    ln = np.zeros((R, C), np.float64)
+    _lib().oa_ref_residual(_p(K), _p(V), ct.c_int(K.shape[1]), _p(asg), _p(sel), ct.c_int(sel.shape[1]),
+                           _p(exp_idx), ct.c_int(exp_idx.shape[1]), _p(quota), _p(n_t), _p(Sk), _p(Sv),
+                           ct.c_int(R), ct.c_int(G), ct.c_int(C), _p(kb), _p(vb), _p(ln))
+    return kb, vb, ln
+
+
+def flash(q_bf16, K_bf16, V_bf16, sel, exp_idx, kbar, vbar, log_n, G: int, sm: float,
+          proxy_per_kv: bool = False) -> np.ndarray:
+    """multibin.py:2727-2747, methods_eager.py:708-720 (fp64) -> out (R,D) f64"""
+    q, K, V = _c(q_bf16, np.uint16), _c(K_bf16, np.uint16), _c(V_bf16, np.uint16)
+    sel, exp_idx = _c(sel, np.int32), _c(exp_idx, np.int32)
+    kbar, vbar, log_n = _c(kbar, np.float64), _c(vbar, np.float64), _c(log_n, np.float64)
+    R = q.shape[0]
+    out = np.zeros((R, D), np.float64)
+    _lib().oa_ref_flash(_p(q), _p(K), _p(V), ct.c_int(K.shape[1]), _p(sel), ct.c_int(sel.shape[1]),
+                        _p(exp_idx), ct.c_int(exp_idx.shape[1]), _p(kbar), _p(vbar), _p(log_n),
+                        ct.c_int(log_n.shape[1]), ct.c_int(1 if proxy_per_kv else 0), ct.c_int(R),
+                        ct.c_int(G), ct.c_double(sm), _p(out))
+    return out
+
+
+def dense(q_bf16, K_bf16, V_bf16, n: int, G: int, sm: float) -> np.ndarray:
+    q, K, V = _c(q_bf16, np.uint16), _c(K_bf16, np.uint16), _c(V_bf16, np.uint16)
+    R = q.shape[0]
+    out = np.zeros((R, D), np.float64)
+    _lib().oa_ref_dense(_p(q), _p(K), _p(V), ct.c_int(K.shape[1]), ct.c_int(n), ct.c_int(R), ct.c_int(G),
+                        ct.c_double(sm), _p(out))
+    return out
+
+
+def index_update(st: dict, pos: int, G: int, rmax: int) -> None:
+    """ours_graph.py:43-90; mutates st['codes','asg','nb','Sk','Sk2','Sv','reclist','reccnt']"""
+    names = ("codes", "asg", "nb", "Sk", "Sk2", "Sv", "reclist", "reccnt")
+    for k in names:
+        assert st[k].flags["C_CONTIGUOUS"]
+    K, V = _c(st["K"], np.uint16), _c(st["V"], np.uint16)
+    R, C = st["nb"].shape
+    _lib().oa_ref_index_update(_p(K), _p(V), ct.c_int(K.shape[1]), ct.c_int(pos), ct.c_int(R), ct.c_int(G),
+                               ct.c_int(C), _p(st["codes"]), _p(_c(st["U"], np.float32)),
+                               _p(_c(st["scale"], np.float32)), _p(_c(st["W"], np.uint16)),
+                               _p(_c(st["colmean"], np.float32)), _p(_c(st["cent"], np.float32)),
+                               _p(st["asg"]), _p(st["nb"]), _p(st["Sk"]), _p(st["Sk2"]), _p(st["Sv"]),
+                               _p(st["reclist"]), _p(st["reccnt"]), ct.c_int(rmax))
+
+
+# ------------------------------------------------------------------ composition
+def decode_step(st: dict, q_bf16: np.ndarray, n: int, ns: int, nl: int, k: int, E: int, G: int,
+                sm: float, sm2: float, rmax: int = 256, update_index: bool = True) -> dict:
+    """The deployed decode step of one layer (ours_graph.py:290-347) with multibin decision
+    semantics: index update of position n-1, QGS scores, top-k, ErrorGate, water-filling,
+    within-cluster top-q, residual proxies, merge softmax.  Mutates the index state in st when
+    update_index is set.  Returns every intermediate."""
+    if update_index:
+        index_update(st, n - 1, G, rmax)
+    zq, fexp, Z = qgs_prep(q_bf16, st["U"], st["scale"], G)
+    S = qgs_scores(st["codes"], Z, fexp, G, n, ns, nl)
+    sel = topk_select(S, n, ns, nl, k)
+    score, n_t = errorgate(q_bf16, st["K"], st["asg"], sel, st["Sk"], st["Sk2"], st["nb"], G, sm, sm2)
+    quota = waterfill(score, n_t, E)
+    exp_idx = topq(S, st["asg"], sel, quota, n, E)
+    kb, vb, ln = residual(st["K"], st["V"], st["asg"], sel, exp_idx, quota, n_t, st["Sk"], st["Sv"], G)
+    out = flash(q_bf16, st["K"], st["V"], sel, exp_idx, kb, vb, ln, G, sm)
+    return dict(zq=zq, fexp=fexp, Z=Z, S=S, sel=sel, score=score, n_t=n_t, quota=quota,
+                exp_idx=exp_idx, kbar_r=kb, vbar_r=vb, log_n=ln, out=out)

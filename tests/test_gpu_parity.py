@@ -1,0 +1,338 @@
+"""GPU parity of every decode-stage kernel against the CPU restatement (oracle/) on the same
+seeded inputs.  Decision outputs (codes, cluster ids, QGS scores, top-k, ErrorGate scores, tail
+counts, quotas, expanded sets) must be bit-exact; floating outputs must be within the tolerance
+BASELINE.json states for bf16 (2e-2 relative per row; observed errors are printed).
+"""
+import math
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from openattention_amd import ops
+from openattention_amd.budget import budget
+from openattention_amd.method import RMAX, C as CTX, OursHIP
+from openattention_amd.prefill import LayerState
+from tests.helpers import (D, G, HKV, HQ, SC, SC2, bf16_np, bf16_to_f32, build_layer, f32_to_bf16,
+                           np_bf16, state_np)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF16_TOL = 2e-2
+
+
+def rel_rows(got: np.ndarray, ref: np.ndarray) -> np.ndarray:
+    den = np.maximum(np.linalg.norm(ref, axis=-1), 1e-30)
+    return np.linalg.norm(got - ref, axis=-1) / den
+
+
+def _i32(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.int32)).to(DEV)
+
+
+def _f32(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(DEV)
+
+
+# ------------------------------------------------------------------ OpenAttention.flash
+@pytest.mark.parametrize("proxy_per_kv,kb_dtype,n_split", [(False, torch.bfloat16, 1),
+                                                            (False, torch.bfloat16, 4),
+                                                            (True, torch.float32, 1),
+                                                            (True, torch.bfloat16, 3)])
+def test_flash_vs_oracle(proxy_per_kv, kb_dtype, n_split):
+    """methods_eager.selftest shapes (methods_eager.py:693-728): B=2, Lmax=4096, C=64, Ns=14,
+    Ne=216 with 7 -1 pads, 5 proxies per row at -inf."""
+    print(f"[case] flash proxy_per_kv={proxy_per_kv} kb={kb_dtype} split={n_split}", flush=True)
+    g = torch.Generator().manual_seed(0)
+    B, Lmax, Cn, Ns, Ne = 2, 4096, 64, 14, 216
+    R, BH = B * HQ, B * HKV
+    k = torch.randn(BH, Lmax, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(BH, Lmax, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(R, D, generator=g).to(torch.bfloat16)
+    perm = torch.stack([torch.randperm(Lmax, generator=g) for _ in range(R)])
+    sel, ex = perm[:, :Ns].int(), perm[:, Ns:Ns + Ne].int().clone()
+    ex[:, -7:] = -1
+    PR = BH if proxy_per_kv else R
+    kb = torch.randn(PR, Cn, D, generator=g).to(kb_dtype)
+    vb = torch.randn(PR, Cn, D, generator=g).to(kb_dtype)
+    ln = torch.rand(R, Cn, generator=g) * 5
+    ln[:, :5] = -math.inf
+    sel[3, :] = -1           # rows with fewer valid entries
+    ex[3, :] = -1
+    ln[3, :] = -math.inf     # row 3: nothing valid -> 0
+    args = [t.to(DEV) for t in (q, k, v, sel, ex, kb, vb, ln)]
+    out = ops.flash_decode(*args, proxy_per_kv=proxy_per_kv, sm_scale=SC, n_split=n_split)
+    torch.cuda.synchronize()
+    got = bf16_to_f32(bf16_np(out))
+    ref = O.flash(bf16_np(q), bf16_np(k), bf16_np(v), sel.numpy(), ex.numpy(), kb.double().numpy(),
+                  vb.double().numpy(), ln.double().numpy(), HQ // HKV, SC, proxy_per_kv=proxy_per_kv)
+    assert np.all(got[3] == 0)
+    keep = np.arange(R) != 3
+    rel = rel_rows(got[keep], ref[keep])
+    print(f"  flash rel err median {np.median(rel):.2e} max {rel.max():.2e}")
+    assert rel.max() < BF16_TOL
+
+
+def test_ours_flash_nb_zero_is_plain_sparse_softmax():
+    print("[case] ours_flash nb=0", flush=True)
+    from openattention_amd import ours_flash
+    g = torch.Generator().manual_seed(1)
+    R, BH, Lmax = 64, 16, 1024
+    k = torch.randn(BH, Lmax, D, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(BH, Lmax, D, generator=g).to(torch.bfloat16).to(DEV)
+    q = torch.randn(R, D, generator=g).to(torch.bfloat16).to(DEV)
+    sel = torch.randint(0, Lmax, (R, 40), generator=g).int().to(DEV)
+    ex = torch.full((R, 8), -1, dtype=torch.int32).to(DEV)
+    kb = torch.randn(R, 4, D, generator=g).to(torch.bfloat16).to(DEV)
+    ln = torch.zeros(R, 4).to(DEV)
+    o1 = ours_flash(q, k, v, sel, ex, kb, kb, ln, nb=0).float().cpu().numpy()
+    ref = O.flash(bf16_np(q), bf16_np(k), bf16_np(v), sel.cpu().numpy(), ex.cpu().numpy(),
+                  np.zeros((R, 1, D)), np.zeros((R, 1, D)), np.full((R, 1), -np.inf), 4, SC)
+    assert rel_rows(o1, ref).max() < BF16_TOL
+
+
+# ------------------------------------------------------------------ state-based stages
+@pytest.fixture(scope="module")
+def lay32k():
+    """Config-2 shape: B=1, N=32768, 256-centre mixture, 1% deployed split (C=64, E=216)."""
+    print("[case] build B=1 N=32768 C=64", flush=True)
+    return build_layer(cfg=2, B=1, N=32768, Lmax=32768 + 64, C=64, n_centers=256, dev=DEV)
+
+
+@pytest.fixture(scope="module")
+def lay4k():
+    """Config-1 shape: B=2, N=4096, 64-centre mixture, 1% split scaled to N (C=8, E=27)."""
+    print("[case] build B=2 N=4096 C=8", flush=True)
+    return build_layer(cfg=1, B=2, N=4096, Lmax=4096 + 64, C=8, n_centers=64, dev=DEV)
+
+
+def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
+    """Run every stage kernel once; returns the intermediates (numpy)."""
+    st = lay.st
+    R = lay.B * HQ
+    K = lay.K.reshape(-1, lay.Lmax, D)
+    V = lay.V.reshape(-1, lay.Lmax, D)
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    n0_dev = torch.tensor([lay.T], device=DEV, dtype=torch.int32)
+    ntiles = -(-lay.Lmax // 64)
+    S = torch.empty(R, ntiles * 64, device=DEV)
+    TM = torch.empty(R, ntiles, device=DEV)
+    limbs = torch.zeros(lay.B * HKV, 16, 32, device=DEV, dtype=torch.int8)
+    fexp = torch.zeros(R, device=DEV, dtype=torch.int32)
+    zq = torch.zeros(R, 32, device=DEV)
+    sel = torch.empty(R, ns + nl + k, device=DEV, dtype=torch.int32)
+    score = torch.empty(R, lay.C, device=DEV)
+    n_t = torch.empty(R, lay.C, device=DEV)
+    quota = torch.empty(R, lay.C, device=DEV)
+    exp_idx = torch.empty(R, max(E, 1), device=DEV, dtype=torch.int32)
+    out = torch.empty(R, D, device=DEV, dtype=torch.bfloat16)
+    kbr = torch.empty(R, lay.C, D, device=DEV, dtype=torch.bfloat16)
+    vbr = torch.empty_like(kbr)
+    lnr = torch.empty(R, lay.C, device=DEV)
+    qr = q.reshape(R, D).contiguous()
+    r = {}
+    ops.index_update(K, V, st, n_dev, rmax)
+    torch.cuda.synchronize()
+    r["state"] = st.to_numpy()
+    ops.qgs_prep(qr, st.U, st.scale, limbs, fexp, zq)
+    ops.qgs_scan(st.codes, limbs, fexp, S, TM, n_dev, ns, nl)
+    torch.cuda.synchronize()
+    r.update(zq=zq.cpu().numpy(), fexp=fexp.cpu().numpy(), limbs=limbs.cpu().numpy(),
+             S=S.cpu().numpy().copy(), TM=TM.cpu().numpy())
+    ops.topk_select(S, TM, sel, n_dev, ns, nl, k)
+    ops.errorgate(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score, n_t, SC)
+    ops.waterfill(score, n_t, quota, E)
+    ops.topq(S, st, quota, exp_idx, n_dev, n0_dev, rmax)
+    ops.residual(K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, kbr, vbr, lnr)
+    ops.residual_flash(qr, K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, out, SC)
+    torch.cuda.synchronize()
+    r.update(S_after=S.cpu().numpy(), sel=sel.cpu().numpy(), score=score.cpu().numpy(),
+             n_t=n_t.cpu().numpy(), quota=quota.cpu().numpy(), exp_idx=exp_idx.cpu().numpy()[:, :E],
+             kbar_r=bf16_to_f32(bf16_np(kbr)), vbar_r=bf16_to_f32(bf16_np(vbr)), log_n=lnr.cpu().numpy(),
+             out=bf16_to_f32(bf16_np(out)))
+    return r
+
+
+def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
+    b = budget(rho, ctx_len=lay.N if lay.N < 32768 else 32768, rule=rule)
+    n = lay.N if n is None else n
+    ns, nl, k = b.counts(n)
+    E = b.E
+    assert b.C == lay.C
+    q = lay.q if step_q is None else step_q
+    pre = state_np(lay)
+    print(f"[case] stages {tag} B={lay.B} n={n} C={lay.C} E={E} ns={ns} nl={nl} k={k}", flush=True)
+    g = _stages_gpu(lay, q, n, ns, nl, k, E)
+    ref = O.decode_step(pre, bf16_np(q.reshape(-1, D)), n, ns, nl, k, E, G, np.float32(SC),
+                        np.float32(SC2), rmax=RMAX)
+    for f in ("codes", "asg", "nb", "Sk", "Sk2", "Sv", "reclist", "reccnt"):
+        assert np.array_equal(g["state"][f], pre[f]), f"index update: {f} differs"
+    assert np.array_equal(g["zq"], ref["zq"])
+    assert np.array_equal(g["fexp"], ref["fexp"])
+    # limbs reconstruct Z exactly
+    L = g["limbs"].astype(np.int64).reshape(lay.B * HKV, G, 4, 32)
+    Zg = (L[:, :, 0] + 256 * L[:, :, 1] + 65536 * L[:, :, 2] + 16777216 * L[:, :, 3]).reshape(-1, 32)
+    assert np.array_equal(Zg, ref["Z"])
+    S = g["S"][:, :n]
+    assert np.array_equal(S, ref["S"][:, :n]), "QGS scores differ"
+    ntile_n = -(-n // 64)
+    tm_ref = np.full((S.shape[0], ntile_n), -np.inf, np.float32)
+    Sp = np.full((S.shape[0], ntile_n * 64), -np.inf, np.float32)
+    Sp[:, :n] = S
+    tm_ref = Sp.reshape(S.shape[0], ntile_n, 64).max(-1)
+    assert np.array_equal(g["TM"][:, :ntile_n], tm_ref)
+    assert np.array_equal(g["sel"], ref["sel"]), "top-k selection differs"
+    assert np.all(np.take_along_axis(g["S_after"], g["sel"].astype(np.int64), 1) == -np.inf)
+    assert np.array_equal(g["n_t"], ref["n_t"])
+    assert np.array_equal(g["score"], ref["score"]), "ErrorGate scores differ"
+    assert np.array_equal(g["quota"], ref["quota"]), "quotas differ"
+    assert np.array_equal(g["exp_idx"], ref["exp_idx"]), "expanded sets differ"
+    live = np.isfinite(ref["log_n"])
+    assert np.array_equal(np.isfinite(g["log_n"]), live)
+    assert np.allclose(g["log_n"][live], ref["log_n"][live], rtol=1e-6)
+    kb_ref = ref["kbar_r"][live]
+    err_k = np.abs(g["kbar_r"][live] - kb_ref) / (np.abs(kb_ref) + 1e-2)
+    assert err_k.max() < BF16_TOL, err_k.max()
+    rel = rel_rows(g["out"], ref["out"])
+    print(f"  out rel err median {np.median(rel):.2e} max {rel.max():.2e}; "
+          f"exact reads/row {(g['exp_idx'] >= 0).sum(1).mean():.1f} + {g['sel'].shape[1]}")
+    assert rel.max() < BF16_TOL
+    return g, ref
+
+
+def test_stages_config2_shape(lay32k):
+    _compare_step(lay32k, 0.01, "multibin", tag="cfg2")
+
+
+def test_stages_config1_shape_both_rules(lay4k):
+    _compare_step(lay4k, 0.01, "multibin", tag="cfg1-multibin")
+
+
+def test_decode_steps_track_oracle(lay4k):
+    """Several decode steps through OursHIP.decode: the index state, the selection and the
+    output follow the CPU restatement step after step (the generated-token lists matter)."""
+    print("[case] OursHIP multi-step", flush=True)
+    a = types.SimpleNamespace(rho=0.01)
+    lay = lay4k
+    m = OursHIP(a, lay.B, lay.Lmax, DEV, n_layers=1, static=lay.static, ctx_len=lay.N, rule="deployed")
+    m.st[0] = lay.st.clone()
+    CTX.K, CTX.V = [lay.K], [lay.V]
+    CTX.n0_dev = torch.tensor([lay.T], device=DEV, dtype=torch.int32)
+    st_np = state_np(lay)
+    g = torch.Generator().manual_seed(5)
+    n = lay.N
+    for step in range(6):
+        # write a fresh token at n-1 (keys near the existing mixture) and decode
+        kn = (lay.K[:, :, :64].float().mean(2) + 0.3 * torch.randn(lay.B, HKV, D, generator=g).to(DEV))
+        vn = torch.randn(lay.B, HKV, D, generator=g).to(DEV)
+        lay.K[:, :, n - 1] = kn.to(torch.bfloat16)
+        lay.V[:, :, n - 1] = vn.to(torch.bfloat16)
+        st_np["K"] = bf16_np(lay.K.reshape(-1, lay.Lmax, D))
+        st_np["V"] = bf16_np(lay.V.reshape(-1, lay.Lmax, D))
+        CTX.n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+        q = (lay.q.float() + 0.05 * torch.randn(lay.q.shape, generator=g).to(DEV)).to(torch.bfloat16)
+        out = m.decode(0, q, n)
+        torch.cuda.synchronize()
+        ns, nl, k = m.bud.counts(n)
+        ref = O.decode_step(st_np, bf16_np(q.reshape(-1, D)), n, ns, nl, k, m.E, G, np.float32(SC),
+                            np.float32(SC2), rmax=RMAX)
+        assert np.array_equal(m.last_sel.cpu().numpy(), ref["sel"]), f"step {step}: sel"
+        assert np.array_equal(m.quota.cpu().numpy(), ref["quota"]), f"step {step}: quota"
+        assert np.array_equal(m.exp_idx.cpu().numpy()[:, :m.E], ref["exp_idx"]), f"step {step}: exp"
+        rel = rel_rows(bf16_to_f32(bf16_np(out.reshape(-1, D))), ref["out"])
+        assert rel.max() < BF16_TOL, (step, rel.max())
+        for f in ("asg", "nb", "Sk", "reccnt", "reclist", "codes"):
+            assert np.array_equal(getattr(m.st[0], f).cpu().numpy(), st_np[f]), f"step {step}: {f}"
+        n += 1
+
+
+def test_topq_generated_list_overflow_fallback(lay4k):
+    """A cluster whose generated-token list overflowed (count > rmax) is served by scanning
+    [n0, n) for its tokens (ours_graph.py:284-287): same expanded set as the oracle."""
+    print("[case] topq overflow", flush=True)
+    lay = lay4k
+    st = lay.st.clone()
+    small = LayerState(lay.B, HKV, G, lay.Lmax, lay.C, 1, DEV)
+    for f in LayerState.FIELDS:
+        if f not in ("reclist", "reccnt"):
+            getattr(small, f).copy_(getattr(st, f))
+    lay2 = types.SimpleNamespace(**{**lay.__dict__, "st": small})
+    n = lay.N
+    pre = state_np(lay2)
+    # the query of every head points at key 100; three generated copies of that key land in
+    # its cluster, whose list (capacity 1) overflows, and that cluster takes most of the quota
+    q = lay.K[:, :, 100].repeat_interleave(G, 1).unsqueeze(2).contiguous()
+    for step in range(3):
+        b = budget(0.01, ctx_len=lay.N)
+        ns, nl, k = b.counts(n)
+        lay.K[:, :, n - 1] = lay.K[:, :, 100]
+        pre["K"] = bf16_np(lay.K.reshape(-1, lay.Lmax, D))
+        gres = _stages_gpu(lay2, q, n, ns, nl, k, b.E, rmax=1)
+        ref = O.decode_step(pre, bf16_np(q.reshape(-1, D)), n, ns, nl, k, b.E, G, np.float32(SC),
+                            np.float32(SC2), rmax=1)
+        assert np.array_equal(gres["exp_idx"], ref["exp_idx"])
+        n += 1
+    cnt = small.reccnt.cpu().numpy()
+    quota = gres["quota"]
+    assert int(cnt.max()) > 1
+    assert np.any((cnt > 1) & (quota > 0)), "no overflowed cluster was expanded"
+
+
+def test_dense_decode_vs_oracle(lay4k):
+    print("[case] dense", flush=True)
+    lay = lay4k
+    K = lay.K.reshape(-1, lay.Lmax, D)
+    V = lay.V.reshape(-1, lay.Lmax, D)
+    n = lay.N - 10
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    qr = lay.q.reshape(-1, D).contiguous()
+    out = ops.dense_decode(qr, K, V, n_dev)
+    torch.cuda.synchronize()
+    ref = O.dense(bf16_np(qr), bf16_np(K), bf16_np(V), n, G, SC)
+    rel = rel_rows(bf16_to_f32(bf16_np(out)), ref)
+    print(f"  dense rel err max {rel.max():.2e}")
+    assert rel.max() < BF16_TOL
+
+
+def test_decode_step_graph_replay(lay4k):
+    """One decode step captured in a hipGraph replays to the eager result, several times, with
+    eager work and synchronisations in between."""
+    print("[case] graph replay", flush=True)
+    a = types.SimpleNamespace(rho=0.01)
+    lay = lay4k
+    m = OursHIP(a, lay.B, lay.Lmax, DEV, n_layers=1, static=lay.static, ctx_len=lay.N)
+    CTX.K, CTX.V = [lay.K], [lay.V]
+    n = lay.N
+    CTX.n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    CTX.n0_dev = torch.tensor([lay.T], device=DEV, dtype=torch.int32)
+    base = lay.st.clone()
+    q = lay.q.clone()
+
+    def reset():
+        for f in LayerState.FIELDS:
+            getattr(m.st[0], f).copy_(getattr(base, f))
+
+    reset()
+    eager = m.decode(0, q, n).clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        reset()
+        m.decode(0, q, n)        # warm-up on the side stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    reset()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        out = m.decode(0, q, n)
+    for rep in range(3):
+        reset()
+        torch.cuda.synchronize()
+        _ = torch.randn(1000, device=DEV).sum()   # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from eager"

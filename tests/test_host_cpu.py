@@ -1,0 +1,141 @@
+"""Host-side logic on the CPU: budget accounting, the prefill build (metric, codes, clusters,
+sums, CSR) and the composed restatement of the decode step."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from openattention_amd import prefill, synth
+from openattention_amd.budget import DEPLOYED, budget
+from tests.helpers import D, G, HKV, HQ, SC, SC2, bf16_np, bf16_to_f32, build_layer, state_np
+
+
+# ------------------------------------------------------------------ budget
+def test_budget_counts_match_reference_accounting():
+    # run_openattention.sh:27-31 split, methods_eager.py:605-607 counts at n = 32768
+    assert budget(0.01).counts(32768) == (3, 3, 9)
+    assert budget(0.03).counts(32768) == (3, 3, 9)
+    assert budget(0.05).counts(32768) == (3, 3, 8)
+    assert budget(0.10).counts(32768) == (3, 3, 9)
+    assert {r: (budget(r).C, budget(r).E) for r in DEPLOYED} == DEPLOYED
+    # config 1 (N=4096, C and E scaled with the accounting context): the multibin masker sizes
+    # int(1e-4 * n) are 0 there, the deployed floor is 1
+    b = budget(0.01, ctx_len=4096)
+    assert (b.C, b.E) == (8, 27)
+    assert b.counts(4096) == (0, 0, 1)
+    assert budget(0.01, ctx_len=4096, rule="deployed").counts(4096) == (1, 1, 1)
+    # realised read at 32K and 1% (reference accounting): (6 + 9 + 216 + 96) / 32768
+    assert abs(budget(0.01).realised_read(32768) - 327 / 32768) < 1e-12
+    with pytest.raises(ValueError):
+        budget(0.02)
+
+
+# ------------------------------------------------------------------ metric (a10)
+def test_rot_avg_closed_form_vs_explicit_rotations():
+    """static_top_k.py:103-131 closed form == mean_t R_t M R_t^T with the explicit rotation
+    matrix of multibin.py:1606-1615."""
+    g = torch.Generator().manual_seed(0)
+    A = torch.randn(3, D, D, generator=g)
+    M = A @ A.transpose(-1, -2) / D
+    inv = synth.llama31_inv_freq()
+    p, w = 5000, 32
+    closed = prefill.rot_avg(M, inv, 1.0, p, w)
+    J = prefill.j_matrix(D, "cpu")
+    acc = torch.zeros_like(M, dtype=torch.float64)
+    for t in range(p, p + w):
+        cos, sin = prefill.rope_cs(inv.double(), 1.0, torch.tensor([t], dtype=torch.float64))
+        Rt = torch.diag(cos[0]) + torch.diag(sin[0]) @ J.double()
+        acc += Rt @ M.double() @ Rt.T
+    explicit = (acc / w).float()
+    assert torch.allclose(closed, explicit, atol=2e-5, rtol=1e-4)
+    # the rotation of a row vector by RoPE equals rope_apply
+    x = torch.randn(4, D, generator=g)
+    cos, sin = prefill.rope_cs(inv, 1.0, torch.tensor([37]))
+    Rt = torch.diag(cos[0]) + torch.diag(sin[0]) @ J
+    assert torch.allclose(prefill.rope_apply(x, cos, sin), x @ Rt.T, atol=1e-5)
+
+
+# ------------------------------------------------------------------ build (a11-a13)
+@pytest.fixture(scope="module")
+def lay():
+    return build_layer(cfg=1, B=1, N=4096, Lmax=4096 + 16, C=8, n_centers=64, dev="cpu")
+
+
+def test_build_invariants(lay):
+    st, T = lay.st, lay.T
+    codes = st.codes[:, :T].to(torch.int32)
+    assert int(codes.abs().max()) == 127                       # scale = max|zc| / 127
+    # codes reproduce k U / scale up to rounding
+    k = lay.K[0, :, :T].float()
+    zc = torch.matmul(k, st.U[:HKV])
+    assert torch.all((zc / st.scale[:HKV, None, :] - codes).abs() <= 0.5 + 1e-3)
+    # U orthonormal columns, W = eigvecs * sqrt(eigvals) (rank 16)
+    assert torch.allclose(st.U[0].T @ st.U[0], torch.eye(32), atol=1e-4)
+    # every token assigned, counts and sums consistent, CSR grouped and position-ordered
+    asg = st.asg[:, :T].long()
+    assert int(asg.min()) >= 0 and int(asg.max()) < lay.C
+    assert torch.all(st.nb.sum(1) == T)
+    for r in (0, 5, 31):
+        kv = r // G
+        kr = lay.K[0, kv, :T].float()
+        ref = torch.zeros(lay.C, D).index_add_(0, asg[r], kr)
+        assert torch.allclose(st.Sk[r], ref, atol=1e-3, rtol=1e-4)
+        mem = st.mem[r, :T].long()
+        assert torch.equal(torch.sort(mem).values, torch.arange(T))
+        for c in range(lay.C):
+            s, l = int(st.cstart[r, c]), int(st.clen[r, c])
+            seg = mem[s:s + l]
+            assert torch.all(asg[r, seg] == c)
+            assert torch.all(seg[1:] > seg[:-1])
+
+
+def test_kmeans_assignment_is_nearest_under_bf16_rule(lay):
+    """After the last Lloyd step every point sits at its nearest centroid of the previous
+    centroids; re-running one assignment with the final centroids moves few points (Lloyd
+    has converged in 4 iterations on the mixture)."""
+    st, T = lay.st, lay.T
+    k = lay.K[0, :, :T]
+    krep = k.repeat_interleave(G, 0)
+    zP = torch.matmul(krep, st.W[:HQ]).float() - st.colmean[:HQ, None, :]
+    half = (0.5 * (st.cent[:HQ] ** 2).sum(-1)).to(torch.bfloat16).unsqueeze(1)
+    a = (torch.matmul(zP.to(torch.bfloat16), st.cent[:HQ].to(torch.bfloat16).transpose(1, 2)) - half).argmax(-1)
+    moved = (a != st.asg[:HQ, :T].long()).float().mean().item()
+    assert moved < 0.05, moved
+
+
+# ------------------------------------------------------------------ composed decode step
+def test_oracle_decode_step_invariants_and_accuracy(lay):
+    n = lay.N
+    b = budget(0.01, ctx_len=lay.N)
+    assert b.C == lay.C
+    ns, nl, k = b.counts(n)
+    st = state_np(lay)
+    q = bf16_np(lay.q.reshape(-1, D))
+    r = O.decode_step(st, q, n, ns, nl, k, b.E, G, np.float32(SC), np.float32(SC2))
+    R = HQ
+    assert r["sel"].shape == (R, ns + nl + k)
+    assert np.array_equal(r["quota"].sum(1), np.minimum(b.E, np.where(r["n_t"] > 1, r["n_t"], 0).sum(1)))
+    for row in range(R):
+        ex = r["exp_idx"][row]
+        ex = ex[ex >= 0]
+        assert len(set(ex.tolist())) == len(ex)
+        assert not (set(ex.tolist()) & set(r["sel"][row].tolist()))
+        assert np.all(ex < n)
+        # each expanded token belongs to the cluster of its segment
+        base = 0
+        for c in range(lay.C):
+            qc = int(r["quota"][row, c])
+            assert np.all(st["asg"][row, r["exp_idx"][row, base:base + qc]] == c)
+            base += qc
+
+    # the estimator converges to dense attention as the exact-read budget grows, and equals it
+    # once every tail token is read (each query here attends ~64 near-tied keys of its mixture
+    # component, which the 1% budget cannot cover, so no accuracy bound is asserted at 1%)
+    dense = O.dense(q, st["K"], st["V"], n, G, SC)
+    for E, bound in ((500, 1e-2), (5000, 1e-6)):
+        st2 = state_np(lay)
+        r2 = O.decode_step(st2, q, n, ns, nl, k, E, G, np.float32(SC), np.float32(SC2))
+        rel = np.linalg.norm(r2["out"] - dense, axis=1) / np.linalg.norm(dense, axis=1)
+        assert rel.max() < bound, (E, rel.max())

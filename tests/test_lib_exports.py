@@ -1,0 +1,52 @@
+"""The kernel library loads without a GPU and exports every entry point the public header
+declares; the ctypes binding covers exactly that list; bad arguments are rejected before any
+launch."""
+import os
+import re
+import subprocess
+
+from openattention_amd import _build, lib
+
+HDR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                   "openattention_amd.h")
+
+
+def declared():
+    text = open(HDR).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(oa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    path = _build.lib_path()
+    assert os.path.exists(path), "run __graft_entry__.build() first"
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (oa_[a-z0-9_]+)", out))
+    names = declared()
+    assert names, "no declarations parsed"
+    missing = [n for n in names if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_binding_matches_header():
+    assert sorted(lib.SIGNATURES) == declared()
+
+
+def test_library_loads_and_reports():
+    L = lib.load()
+    assert L.oa_abi_version() == 1
+    assert b"invalid argument" in L.oa_error_string(-22)
+    for name in lib.SIGNATURES:
+        assert getattr(L, name) is not None
+
+
+def test_argument_checks_reject_before_launch():
+    """Shape checks fire on the host side of the C ABI (no device is touched)."""
+    L = lib.load()
+    # head_dim 64 is rejected by every entry point that takes it
+    st = L.oa_flash_decode(None, 0, None, None, 0, 0, None, 0, 1, None, 0, 1, None, None, 0, 0, 0, 0,
+                           None, 0, 0, None, 0, 32, 8, 64, 0.1, 1, None, None, None, None)
+    assert st == -22
+    assert L.oa_waterfill(None, None, 4, 300, 10, None, None) == -22          # C > 256
+    assert L.oa_topk_select(None, 0, None, 0, 4, 10, None, 5, None, 0, 0, 20, None) == -22   # k > tiles
+    assert L.oa_qgs_prep(None, 0, None, None, 32, 8, 128, 16, None, None, None, None) == -22  # rank 16

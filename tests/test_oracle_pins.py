@@ -1,0 +1,352 @@
+"""Pins of the CPU restatement (oracle/) against what fixes each function independently:
+libm, exact integer/rational arithmetic, fp64 closed forms, brute-force sorting and the
+reference's own torch formulation of the water-filling (methods_eager.py:558-581), restated
+here in fp64.  A plausible mistake in the oracle (a dropped term, a wrong sign, a swapped
+tie rule, an off-by-one in the sink/local window) fails at least one of these.
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import SC, SC2, bf16_to_f32, f32_to_bf16
+
+RNG = np.random.default_rng(1234)
+
+
+# ------------------------------------------------------------------ elementary functions
+def _ulp_err(got, ref):
+    return abs(got - ref) / math.ulp(ref) if ref != 0 else abs(got)
+
+
+@pytest.mark.parametrize("x", list(np.linspace(-700, 700, 257)) + [-1e-9, 0.0, 1e-12, 0.5, 1.0,
+                                                                  -745.0, 709.7])
+def test_det_exp_vs_libm(x):
+    assert _ulp_err(O.det_exp(x), math.exp(x)) <= 2.0
+
+
+def test_det_exp_specials():
+    assert O.det_exp(-1000.0) == 0.0
+    assert math.isinf(O.det_exp(1000.0))
+    assert math.isnan(O.det_exp(float("nan")))
+    assert O.det_exp(0.0) == 1.0
+
+
+@pytest.mark.parametrize("x", list(np.exp(np.linspace(-300, 300, 301))) + [1.0, 2.0, 0.5, 1e-300,
+                                                                          123456.789, 1e-3])
+def test_det_log_vs_libm(x):
+    ref = math.log(x)
+    assert abs(O.det_log(x) - ref) <= 2.0 * math.ulp(ref if ref != 0 else 1e-300) + 1e-300
+
+
+def test_det_log_specials():
+    assert O.det_log(1.0) == 0.0
+    assert O.det_log(0.0) == -math.inf
+    assert math.isnan(O.det_log(-1.0))
+
+
+def test_det_erff_vs_libm():
+    xs = np.concatenate([np.linspace(0, 4.5, 3001), -np.linspace(0, 4.5, 301),
+                         np.float32(RNG.uniform(0, 3, 2000))]).astype(np.float32)
+    for x in xs:
+        ref = math.erf(float(x))
+        got = O.det_erff(float(x))
+        assert abs(got - np.float32(ref)) <= np.spacing(np.float32(abs(ref)) if ref != 0 else np.float32(1e-38)), (x, got, ref)
+
+
+def test_det_logf_vs_libm():
+    xs = np.float32(np.concatenate([np.arange(1, 5000), RNG.uniform(1e-30, 1, 500)]))
+    for x in xs:
+        ref = np.float32(math.log(float(x)))
+        got = np.float32(O.det_logf(float(x)))
+        assert abs(got - ref) <= np.spacing(abs(ref) if ref != 0 else np.float32(1e-38))
+
+
+# ------------------------------------------------------------------ QGS scores
+def _rand_state(R=8, BH=2, N=300):
+    q = f32_to_bf16(RNG.normal(size=(R, 128)).astype(np.float32))
+    U = RNG.normal(size=(BH, 128, 32)).astype(np.float32) / 8
+    scale = np.abs(RNG.normal(size=(BH, 32))).astype(np.float32) * 0.05 + 1e-3
+    codes = RNG.integers(-127, 128, size=(BH, N, 32)).astype(np.int8)
+    return q, U, scale, codes
+
+
+def test_qgs_prep_exact_fixed_point():
+    q, U, scale, _ = _rand_state()
+    zq, fexp, Z = O.qgs_prep(q, U, scale, 4)
+    qf = bf16_to_f32(q).astype(np.float64)
+    for r in range(q.shape[0]):
+        ref = (qf[r] @ U[r // 4].astype(np.float64)) * scale[r // 4]
+        assert np.allclose(zq[r], ref, rtol=2e-5, atol=1e-6)
+        m, e = math.frexp(float(np.max(np.abs(zq[r]))))
+        assert fexp[r] == 30 - e
+        for j in range(32):
+            assert Z[r, j] == int(round(math.ldexp(float(zq[r, j]), int(fexp[r])))), (r, j)
+        assert np.max(np.abs(Z[r])) < 2 ** 30
+
+
+def test_qgs_scores_exact_rounding_and_mask():
+    q, U, scale, codes = _rand_state(N=200)
+    zq, fexp, Z = O.qgs_prep(q, U, scale, 4)
+    n, ns, nl = 190, 3, 2
+    S = O.qgs_scores(codes, Z, fexp, 4, n, ns, nl, ncols=256)
+    for r in range(q.shape[0]):
+        for i in list(range(0, 10)) + list(range(180, 256)) + list(RNG.integers(0, 256, 20)):
+            if i < ns or i >= n - nl:
+                assert S[r, i] == -np.inf
+                continue
+            exact = sum(int(Z[r, j]) * int(codes[r // 4, i, j]) for j in range(32))
+            ref = np.float32(float(Fraction(exact, 2 ** int(fexp[r]))))
+            assert S[r, i] == ref
+            # and the fixed point is an honest approximation of the fp64 product zq . code
+            f64 = float(zq[r].astype(np.float64) @ codes[r // 4, i].astype(np.float64))
+            assert abs(S[r, i] - f64) <= 1e-6 * max(1.0, float(np.abs(zq[r]).sum()) * 127)
+
+
+# ------------------------------------------------------------------ top-k
+def test_topk_brute_force_and_ties():
+    R, ncols, n = 6, 300, 297
+    S = RNG.normal(size=(R, ncols)).astype(np.float32)
+    S[:, 40:60] = 2.5                      # a block of ties
+    S[0, :] = 1.0                          # an all-tied row
+    ns, nl, k = 2, 3, 9
+    S[:, :ns] = -np.inf
+    S[:, n - nl:] = -np.inf
+    sel = O.topk_select(S, n, ns, nl, k)
+    for r in range(R):
+        assert list(sel[r, :ns]) == list(range(ns))
+        assert list(sel[r, ns:ns + nl]) == list(range(n - nl, n))
+        cand = list(range(ns, n - nl))
+        order = sorted(cand, key=lambda i: (-S[r, i], i))
+        assert list(sel[r, ns + nl:]) == order[:k]
+
+
+# ------------------------------------------------------------------ ErrorGate
+def _gate_ref_fp64(q, K, asg, sel, Sk, Sk2, nb, G):
+    R, C = nb.shape
+    score = np.zeros((R, C))
+    n_t = np.zeros((R, C))
+    qf = bf16_to_f32(q).astype(np.float64)
+    Kf = bf16_to_f32(K).astype(np.float64)
+    for r in range(R):
+        for c in range(C):
+            sk = Sk[r, c].astype(np.float64).copy()
+            s2 = Sk2[r, c].astype(np.float64).copy()
+            nt = float(nb[r, c])
+            for t in sel[r]:
+                if asg[r, t] == c:
+                    sk -= Kf[r // G, t]
+                    s2 -= Kf[r // G, t] ** 2
+                    nt -= 1
+            den = max(nt, 1.0)
+            kb = sk / den
+            var = np.maximum(s2 / den - kb * kb, 0)
+            zbar = SC * (qf[r] @ kb)
+            sv = SC * SC * ((qf[r] ** 2) @ var) if nt >= 2 else 0.0
+            sig = math.sqrt(max(sv, 0.0))
+            score[r, c] = zbar + math.log(den) + 0.5 * sv + math.log(max(math.erf(sig / math.sqrt(2)), 1e-30))
+            n_t[r, c] = nt
+    return score, n_t
+
+
+def test_errorgate_vs_fp64_closed_form():
+    R, BH, L, C, G = 8, 2, 400, 12, 4
+    q = f32_to_bf16(RNG.normal(size=(R, 128)).astype(np.float32))
+    K = f32_to_bf16(RNG.normal(size=(BH, L, 128)).astype(np.float32))
+    asg = RNG.integers(0, C, size=(R, L)).astype(np.int32)
+    Kf = bf16_to_f32(K)
+    nb = np.zeros((R, C), np.float32)
+    Sk = np.zeros((R, C, 128), np.float32)
+    Sk2 = np.zeros((R, C, 128), np.float32)
+    for r in range(R):
+        for t in range(L):
+            c = asg[r, t]
+            nb[r, c] += 1
+            Sk[r, c] += Kf[r // G, t]
+            Sk2[r, c] += Kf[r // G, t] ** 2
+    sel = np.stack([RNG.choice(L, 11, replace=False) for _ in range(R)]).astype(np.int32)
+    score, n_t = O.errorgate(q, K, asg, sel, Sk, Sk2, nb, G, np.float32(SC), np.float32(SC2))
+    ref_s, ref_n = _gate_ref_fp64(q, K, asg, sel, Sk, Sk2, nb, G)
+    assert np.array_equal(n_t, ref_n.astype(np.float32))
+    assert np.allclose(score, ref_s, rtol=2e-4, atol=2e-3)
+
+
+# ------------------------------------------------------------------ water-filling
+def _hier_quota_methods_eager_fp64(score, cap, live, E):
+    """methods_eager.py:558-581 (Ours.hier_quota) restated in numpy fp64: exact solve by
+    sorting cap/w, lambda from the crossing index, floors, leftover by score order."""
+    R, C = score.shape
+    out = np.zeros((R, C))
+    for r in range(R):
+        s = np.where(live[r], score[r].astype(np.float64), -np.inf)
+        w = np.where(live[r], np.exp(s - s.max()), 0.0)
+        cp = np.where(live[r], cap[r].astype(np.float64), 0.0)
+        tot = cp.sum()
+        ratio = np.where(w > 0, cp / np.maximum(w, 1e-30), np.inf)
+        o = np.argsort(ratio, kind="stable")
+        r_s, c_s, w_s = ratio[o], cp[o], w[o]
+        c_ex = np.cumsum(c_s) - c_s
+        w_suf = np.cumsum(w_s[::-1])[::-1]
+        f_at = np.where(w_suf > 0, c_ex + r_s * w_suf, np.inf)
+        j = int(np.argmax(f_at >= E))
+        lam = (E - c_ex[j]) / max(w_suf[j], 1e-30)
+        qb = np.minimum(cp, np.floor(lam * w))
+        if tot <= E:
+            qb = cp.copy()
+        rem = max(min(tot, E) - qb.sum(), 0)
+        order = sorted(range(C), key=lambda c: (-s[c], c))
+        k = 0
+        for c in order:
+            if qb[c] < cp[c] and k < rem:
+                qb[c] += 1
+                k += 1
+        out[r] = qb
+    return out
+
+
+@pytest.mark.parametrize("C,E", [(8, 40), (64, 216), (192, 679), (256, 2877), (64, 100000)])
+def test_waterfill_invariants_and_exact_solve(C, E):
+    R = 20
+    score = (RNG.normal(size=(R, C)) * 3).astype(np.float32)
+    n_t = RNG.integers(0, 900, size=(R, C)).astype(np.float32)
+    n_t[:, :3] = 1.0                     # dead clusters (n <= 1)
+    quota = O.waterfill(score, n_t, E)
+    live = n_t > 1
+    cap = np.where(live, n_t, 0)
+    assert np.all(quota == np.floor(quota)) and np.all(quota >= 0)
+    assert np.all(quota <= cap)
+    assert np.all(quota[~live] == 0)
+    assert np.array_equal(quota.sum(1), np.minimum(cap.sum(1), E))
+    ref = _hier_quota_methods_eager_fp64(score, n_t, live, float(E))
+    diff = quota != ref
+    # the bisection and the exact solve may differ only where lambda*w sits on an integer
+    assert diff.sum() <= 2 * R * 0.01 * C + 2, diff.sum()
+
+
+def test_waterfill_hand_example():
+    """Two live clusters of equal score, caps 10 and 4, E = 9: lambda w = 4.5 each, the small one
+    saturates at 4, the other takes 5.  A third cluster has n = 1 (dead)."""
+    score = np.array([[0.0, 0.0, 5.0]], np.float32)
+    n_t = np.array([[10.0, 4.0, 1.0]], np.float32)
+    q = O.waterfill(score, n_t, 9)
+    assert list(q[0]) == [5.0, 4.0, 0.0]
+    # scores e and 0: w = (1, 1/e); E = 3, caps large: lambda (1 + 1/e) = 3 -> q = floor(2.19),
+    # floor(0.81) = (2, 0), leftover 1 to the higher score -> (3, 0)
+    q = O.waterfill(np.array([[1.0, 0.0]], np.float32), np.array([[50.0, 50.0]], np.float32), 3)
+    assert list(q[0]) == [3.0, 0.0]
+    # tail smaller than the budget: every live member is read
+    q = O.waterfill(np.array([[1.0, 2.0]], np.float32), np.array([[3.0, 2.0]], np.float32), 100)
+    assert list(q[0]) == [3.0, 2.0]
+
+
+# ------------------------------------------------------------------ top-q
+def test_topq_brute_force():
+    R, L, C, n, E = 4, 500, 10, 480, 60
+    S = RNG.normal(size=(R, L)).astype(np.float32)
+    S[:, 100:140] = 0.25                  # ties
+    asg = RNG.integers(0, C, size=(R, L)).astype(np.int32)
+    sel = np.stack([RNG.choice(n, 9, replace=False) for _ in range(R)]).astype(np.int32)
+    quota = np.zeros((R, C), np.float32)
+    for r in range(R):
+        counts = np.bincount(np.delete(asg[r, :n], sel[r]), minlength=C)
+        left = E
+        for c in RNG.permutation(C):
+            qc = int(min(counts[c], RNG.integers(0, 12), left))
+            quota[r, c] = qc
+            left -= qc
+    S2 = S.copy()
+    for r in range(R):
+        S2[r, sel[r]] = -np.inf
+    ex = O.topq(S2, asg, sel, quota, n, E)
+    for r in range(R):
+        base = 0
+        for c in range(C):
+            qc = int(quota[r, c])
+            seg = ex[r, base:base + qc]
+            mem = [i for i in range(n) if asg[r, i] == c and i not in set(sel[r].tolist())]
+            want = sorted(mem, key=lambda i: (-S[r, i], i))[:qc]
+            assert sorted(seg.tolist()) == sorted(want), (r, c)
+            base += qc
+        assert np.all(ex[r, base:] == -1)
+
+
+# ------------------------------------------------------------------ residual + merge
+def test_flash_closed_form_and_invariants():
+    R, BH, L, NS, NE, NB = 8, 2, 300, 7, 20, 5
+    q = f32_to_bf16(RNG.normal(size=(R, 128)).astype(np.float32))
+    K = f32_to_bf16(RNG.normal(size=(BH, L, 128)).astype(np.float32))
+    V = f32_to_bf16(RNG.normal(size=(BH, L, 128)).astype(np.float32))
+    perm = np.stack([RNG.permutation(L) for _ in range(R)])
+    sel = perm[:, :NS].astype(np.int32)
+    ex = perm[:, NS:NS + NE].astype(np.int32)
+    ex[:, -4:] = -1
+    kb = RNG.normal(size=(R, NB, 128))
+    vb = RNG.normal(size=(R, NB, 128))
+    ln = RNG.uniform(0, 5, size=(R, NB))
+    ln[:, 0] = -np.inf
+    out = O.flash(q, K, V, sel, ex, kb, vb, ln, 4, SC)
+    qf, Kf, Vf = bf16_to_f32(q).astype(np.float64), bf16_to_f32(K).astype(np.float64), bf16_to_f32(V).astype(np.float64)
+    for r in range(R):
+        toks = [t for t in list(sel[r]) + list(ex[r]) if t >= 0]
+        z = [SC * (qf[r] @ Kf[r // 4, t]) for t in toks] + [SC * (qf[r] @ kb[r, b]) + ln[r, b] for b in range(NB)]
+        vs = [Vf[r // 4, t] for t in toks] + [vb[r, b] for b in range(NB)]
+        z = np.array(z)
+        p = np.exp(z - z.max())
+        ref = (p[:, None] * np.array(vs)).sum(0) / p.sum()
+        assert np.allclose(out[r], ref, rtol=1e-12, atol=1e-12)
+    # every token exact and no proxy == dense attention
+    full = np.tile(np.arange(L, dtype=np.int32), (R, 1))
+    none = np.full((R, 1), -1, np.int32)
+    o1 = O.flash(q, K, V, full, none, kb[:, :1] * 0, vb[:, :1] * 0, np.full((R, 1), -np.inf), 4, SC)
+    o2 = O.dense(q, K, V, L, 4, SC)
+    assert np.allclose(o1, o2, rtol=1e-12, atol=1e-12)
+    # a proxy that stands for one token (n = 1, ln n = 0) is that token
+    t = 17
+    one = np.full((R, 1), t, np.int32)
+    kt = np.stack([Kf[r // 4, t] for r in range(R)])[:, None]
+    vt = np.stack([Vf[r // 4, t] for r in range(R)])[:, None]
+    o3 = O.flash(q, K, V, sel, none, kt, vt, np.zeros((R, 1)), 4, SC)
+    o4 = O.flash(q, K, V, np.concatenate([sel, one], 1), none, kt, vt, np.full((R, 1), -np.inf), 4, SC)
+    assert np.allclose(o3, o4, rtol=1e-12, atol=1e-12)
+
+
+def test_residual_closed_form():
+    R, BH, L, C, G = 4, 1, 200, 6, 4
+    K = f32_to_bf16(RNG.normal(size=(BH, L, 128)).astype(np.float32))
+    V = f32_to_bf16(RNG.normal(size=(BH, L, 128)).astype(np.float32))
+    asg = RNG.integers(0, C, size=(R, L)).astype(np.int32)
+    Kf, Vf = bf16_to_f32(K).astype(np.float64), bf16_to_f32(V).astype(np.float64)
+    nb = np.zeros((R, C), np.float32)
+    Sk = np.zeros((R, C, 128), np.float32)
+    Sv = np.zeros((R, C, 128), np.float32)
+    for r in range(R):
+        for t in range(L):
+            nb[r, asg[r, t]] += 1
+            Sk[r, asg[r, t]] += Kf[0, t]
+            Sv[r, asg[r, t]] += Vf[0, t]
+    sel = np.stack([RNG.choice(L, 5, replace=False) for _ in range(R)]).astype(np.int32)
+    ex = np.full((R, 12), -1, np.int32)
+    quota = np.zeros((R, C), np.float32)
+    n_t = nb.copy()
+    for r in range(R):
+        for t in sel[r]:
+            n_t[r, asg[r, t]] -= 1
+        rest = [t for t in range(L) if t not in set(sel[r].tolist())]
+        pick = RNG.choice(rest, 8, replace=False)
+        pick = sorted(pick, key=lambda t: asg[r, t])
+        ex[r, :8] = pick
+        for t in pick:
+            quota[r, asg[r, t]] += 1
+    kb, vb, ln = O.residual(K, V, asg, sel, ex, quota, n_t, Sk, Sv, G)
+    for r in range(R):
+        read = set(sel[r].tolist()) | set(int(t) for t in ex[r] if t >= 0)
+        for c in range(C):
+            rest = [t for t in range(L) if asg[r, t] == c and t not in read]
+            if rest:
+                assert np.allclose(kb[r, c], Kf[0, rest].mean(0), atol=2e-5)
+                assert np.allclose(vb[r, c], Vf[0, rest].mean(0), atol=2e-5)
+                assert abs(ln[r, c] - math.log(len(rest))) < 1e-12
+            else:
+                assert ln[r, c] == -np.inf
