@@ -108,12 +108,15 @@ int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int
 /*
  * ErrorGate: wl1 score and tail count of every cluster (pooled sums minus the selected
  * tokens).  Replaces _k_errorgate (inference/ours_fused.py:122-154).
+ *   sm_scale_sq is the fp32 value of the squared scale as the estimator forms it (the square
+ *   taken in double, then rounded: multibin.py:643), which can differ from fp32(s)^2 by 1 ulp.
  *   score, n_t (rows, C) fp32.
  */
 int oa_errorgate(const void* q, long q_stride, const void* K, long k_stride_b, long k_stride_s,
                  int rows, int kv_rows, int head_dim, const int32_t* asg, long asg_stride,
                  const int32_t* sel, long sel_stride, int n_sel, const float* Sk, const float* Sk2,
-                 const float* nb, int C, float sm_scale, float* score, float* n_t, void* stream);
+                 const float* nb, int C, float sm_scale, float sm_scale_sq, float* score,
+                 float* n_t, void* stream);
 
 /*
  * Hierarchical water-filling of the exact-read budget E over the clusters (fp64 bisection of
@@ -123,6 +126,16 @@ int oa_errorgate(const void* q, long q_stride, const void* K, long k_stride_b, l
  */
 int oa_waterfill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,
                  void* stream);
+
+/*
+ * ErrorGate and water-filling fused in one launch per row (scores kept on chip; score and n_t
+ * are also written out).  Same results as oa_errorgate followed by oa_waterfill.
+ */
+int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, long k_stride_s,
+                 int rows, int kv_rows, int head_dim, const int32_t* asg, long asg_stride,
+                 const int32_t* sel, long sel_stride, int n_sel, const float* Sk, const float* Sk2,
+                 const float* nb, int C, float sm_scale, float sm_scale_sq, int budget,
+                 float* score, float* n_t, float* quota, void* stream);
 
 /*
  * Within-cluster top-q by QGS score over CSR members + generated tokens; exp_idx segments

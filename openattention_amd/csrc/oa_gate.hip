@@ -33,60 +33,92 @@ struct GateArgs {
   int C; float sc; float sc2;
 };
 
-__global__ void __launch_bounds__(kGateThreads) errorgate_kernel(GateArgs a) {
+// score of one cluster from its pooled sums (lane holds dims lane and lane+64)
+__device__ __forceinline__ void gate_cluster(const GateArgs& a, int c, float sk_lo, float sk_hi,
+                                             float s2_lo, float s2_hi, float nt, float q_lo,
+                                             float q_hi, float qq_lo, float qq_hi, const int* s_cid,
+                                             float (*s_k)[OA_D], int lane, float* score_out,
+                                             float* nt_out) {
+  for (int i = 0; i < a.n_sel; ++i) {
+    if (s_cid[i] == c) {
+      const float k_lo = s_k[i][lane], k_hi = s_k[i][lane + 64];
+      sk_lo = sk_lo - k_lo;
+      sk_hi = sk_hi - k_hi;
+      s2_lo = s2_lo - k_lo * k_lo;
+      s2_hi = s2_hi - k_hi * k_hi;
+      nt = nt - 1.0f;
+    }
+  }
+  const float den = fmaxf(nt, 1.0f);
+  const float kb_lo = sk_lo / den, kb_hi = sk_hi / den;
+  const float ks_lo = s2_lo / den, ks_hi = s2_hi / den;
+  const float v_lo = fmaxf(ks_lo - kb_lo * kb_lo, 0.f);
+  const float v_hi = fmaxf(ks_hi - kb_hi * kb_hi, 0.f);
+  const float zbar = a.sc * oa::dot128_canon(q_lo, kb_lo, q_hi, kb_hi);
+  float s2 = a.sc2 * oa::dot128_canon(qq_lo, v_lo, qq_hi, v_hi);
+  if (!(nt >= 2.0f)) s2 = 0.f;
+  const float s2c = fmaxf(s2, 0.f);
+  const float sig = sqrtf(s2c);
+  const float er = oa::det_erff(sig * 0.70710677f);
+  const float log_d = 0.5f * s2c + oa::det_logf(fmaxf(er, 1e-30f));
+  *score_out = (zbar + oa::det_logf(fmaxf(nt, 1.0f))) + log_d;
+  *nt_out = nt;
+}
+
+// ErrorGate of one row by a 256-thread workgroup; results to (score, n_t) rows (global or LDS)
+__device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* score_row,
+                                         float* nt_row) {
   __shared__ float s_k[kMaxSel][OA_D];
   __shared__ int s_cid[kMaxSel];
-  const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int kvr = row / a.G;
   for (int i = tid; i < a.n_sel; i += kGateThreads) {
-    int tok = a.sel[(long)row * a.sel_stride + i];
+    const int tok = a.sel[(long)row * a.sel_stride + i];
     s_cid[i] = (tok >= 0) ? a.asg[(long)row * a.asg_stride + tok] : -1;
   }
   for (int e = tid; e < a.n_sel * OA_D; e += kGateThreads) {
-    int i = e / OA_D, d = e % OA_D;
-    int tok = a.sel[(long)row * a.sel_stride + i];
+    const int i = e / OA_D, d = e % OA_D;
+    const int tok = a.sel[(long)row * a.sel_stride + i];
     s_k[i][d] = (tok >= 0) ? oa::bf16_to_f32(a.K[(long)kvr * a.k_sb + (long)tok * a.k_ss + d]) : 0.f;
   }
   __syncthreads();
   const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
   const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
   const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
-  for (int c = wave; c < a.C; c += kGateThreads / 64) {
-    const long base = (long)row * a.st_stride_r + (long)c * OA_D;
-    float sk_lo = a.Sk[base + lane], sk_hi = a.Sk[base + lane + 64];
-    float s2_lo = a.Sk2[base + lane], s2_hi = a.Sk2[base + lane + 64];
-    float nt = a.nb[(long)row * a.nb_stride + c];
-    for (int i = 0; i < a.n_sel; ++i) {
-      if (s_cid[i] == c) {
-        const float k_lo = s_k[i][lane], k_hi = s_k[i][lane + 64];
-        sk_lo = sk_lo - k_lo;
-        sk_hi = sk_hi - k_hi;
-        s2_lo = s2_lo - k_lo * k_lo;
-        s2_hi = s2_hi - k_hi * k_hi;
-        nt = nt - 1.0f;
+  constexpr int kBatch = 8;
+  constexpr int kWaves = kGateThreads / 64;
+  for (int c0 = wave; c0 < a.C; c0 += kWaves * kBatch) {
+    float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {          // the batch's statistics, all loads in flight
+      const int c = c0 + kWaves * i;
+      const long base = (long)row * a.st_stride_r + (long)(c < a.C ? c : 0) * OA_D;
+      sk[i][0] = a.Sk[base + lane];
+      sk[i][1] = a.Sk[base + lane + 64];
+      s2[i][0] = a.Sk2[base + lane];
+      s2[i][1] = a.Sk2[base + lane + 64];
+      nbv[i] = a.nb[(long)row * a.nb_stride + (c < a.C ? c : 0)];
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int c = c0 + kWaves * i;
+      if (c >= a.C) break;
+      float sc, nt;
+      gate_cluster(a, c, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
+                   s_cid, s_k, lane, &sc, &nt);
+      if (lane == 0) {
+        score_row[c] = sc;
+        nt_row[c] = nt;
       }
     }
-    const float den = fmaxf(nt, 1.0f);
-    const float kb_lo = sk_lo / den, kb_hi = sk_hi / den;
-    const float ks_lo = s2_lo / den, ks_hi = s2_hi / den;
-    const float v_lo = fmaxf(ks_lo - kb_lo * kb_lo, 0.f);
-    const float v_hi = fmaxf(ks_hi - kb_hi * kb_hi, 0.f);
-    const float zbar = a.sc * oa::dot128_canon(q_lo, kb_lo, q_hi, kb_hi);
-    float s2 = a.sc2 * oa::dot128_canon(qq_lo, v_lo, qq_hi, v_hi);
-    if (!(nt >= 2.0f)) s2 = 0.f;
-    const float s2c = fmaxf(s2, 0.f);
-    const float sig = sqrtf(s2c);
-    const float er = oa::det_erff(sig * 0.70710677f);
-    const float log_d = 0.5f * s2c + oa::det_logf(fmaxf(er, 1e-30f));
-    const float score = (zbar + oa::det_logf(fmaxf(nt, 1.0f))) + log_d;
-    if (lane == 0) {
-      a.score[(long)row * a.out_stride + c] = score;
-      a.n_t[(long)row * a.out_stride + c] = nt;
-    }
   }
+}
+
+__global__ void __launch_bounds__(kGateThreads) errorgate_kernel(GateArgs a) {
+  const int row = blockIdx.x;
+  gate_row(a, row, a.score + (long)row * a.out_stride, a.n_t + (long)row * a.out_stride);
 }
 
 // one wave per row; cluster c lives in lane c % 64, slot c / 64
@@ -103,14 +135,10 @@ __device__ __forceinline__ double canon_sum(const double* x, int C, int lane) {
   return oa::wave_sum(p);
 }
 
-__global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__ score,
-                                                       const float* __restrict__ n_t, long in_stride,
-                                                       float* __restrict__ quota, long q_stride, int C,
-                                                       double budget) {
-  __shared__ double s_key[kMaxC];
-  __shared__ int s_room[kMaxC];
-  const int row = blockIdx.x;
-  const int lane = threadIdx.x;
+// water-filling of one row by one wave (lane = threadIdx.x % 64); score/n_t rows may be in LDS
+__device__ __forceinline__ void waterfill_row(const float* score_row, const float* nt_row,
+                                              float* quota_row, int C, double budget, int lane,
+                                              double* s_key, int* s_room) {
   const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
   double sv[4], w[4], cap[4], qv[4];
   bool ok[4];
@@ -119,10 +147,10 @@ __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__
     int c = lane + 64 * j;
     sv[j] = NEG; w[j] = 0.0; cap[j] = 0.0; ok[j] = false;
     if (c < C) {
-      float nt = n_t[(long)row * in_stride + c];
+      float nt = nt_row[c];
       ok[j] = nt > 1.0f;
       if (ok[j]) {
-        sv[j] = (double)score[(long)row * in_stride + c];
+        sv[j] = (double)score_row[c];
         cap[j] = (double)nt;
       }
       smax = fmax(smax, sv[j]);
@@ -166,7 +194,8 @@ __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__
       s_room[c] = qv[j] < cap[j] ? 1 : 0;
     }
   }
-  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
   for (int j = 0; j < 4; ++j) {
     int c = lane + 64 * j;
     if (c >= C) continue;
@@ -181,8 +210,39 @@ __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__
       }
       if ((double)rank < rem) add = 1.0;
     }
-    quota[(long)row * q_stride + c] = (float)(qv[j] + add);
+    quota_row[c] = (float)(qv[j] + add);
   }
+}
+
+
+__global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__ score,
+                                                       const float* __restrict__ n_t, long in_stride,
+                                                       float* __restrict__ quota, long q_stride, int C,
+                                                       double budget) {
+  __shared__ double s_key[kMaxC];
+  __shared__ int s_room[kMaxC];
+  const int row = blockIdx.x;
+  waterfill_row(score + (long)row * in_stride, n_t + (long)row * in_stride,
+                quota + (long)row * q_stride, C, budget, threadIdx.x, s_key, s_room);
+}
+
+// ErrorGate and water-filling of one row in one workgroup: the scores stay in LDS and
+// wave 0 solves the quotas
+__global__ void __launch_bounds__(kGateThreads) gate_fill_kernel(GateArgs a, float* quota,
+                                                                 double budget) {
+  __shared__ float s_score[kMaxC], s_nt[kMaxC];
+  __shared__ double s_key[kMaxC];
+  __shared__ int s_room[kMaxC];
+  const int row = blockIdx.x;
+  gate_row(a, row, s_score, s_nt);
+  __syncthreads();
+  for (int c = threadIdx.x; c < a.C; c += kGateThreads) {
+    a.score[(long)row * a.out_stride + c] = s_score[c];
+    a.n_t[(long)row * a.out_stride + c] = s_nt[c];
+  }
+  if (threadIdx.x < 64)
+    waterfill_row(s_score, s_nt, quota + (long)row * a.out_stride, a.C, budget, threadIdx.x, s_key,
+                  s_room);
 }
 
 }  // namespace
@@ -191,7 +251,8 @@ extern "C" int oa_errorgate(const void* q, long q_stride, const void* K, long k_
                             long k_stride_s, int rows, int kv_rows, int head_dim,
                             const int32_t* asg, long asg_stride, const int32_t* sel, long sel_stride,
                             int n_sel, const float* Sk, const float* Sk2, const float* nb, int C,
-                            float sm_scale, float* score, float* n_t, void* stream) {
+                            float sm_scale, float sm_scale_sq, float* score, float* n_t,
+                            void* stream) {
   if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || n_sel < 0 || n_sel > kMaxSel ||
       C <= 0)
     return OA_EINVAL;
@@ -204,8 +265,31 @@ extern "C" int oa_errorgate(const void* q, long q_stride, const void* K, long k_
   a.nb = nb; a.nb_stride = C;
   a.score = score; a.n_t = n_t; a.out_stride = C;
   a.C = C; a.sc = sm_scale;
-  a.sc2 = (float)((double)sm_scale * (double)sm_scale);
+  a.sc2 = sm_scale_sq;
   hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads), 0, (hipStream_t)stream, a);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b,
+                            long k_stride_s, int rows, int kv_rows, int head_dim,
+                            const int32_t* asg, long asg_stride, const int32_t* sel, long sel_stride,
+                            int n_sel, const float* Sk, const float* Sk2, const float* nb, int C,
+                            float sm_scale, float sm_scale_sq, int budget, float* score, float* n_t,
+                            float* quota, void* stream) {
+  if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || n_sel < 0 || n_sel > kMaxSel ||
+      C <= 0 || C > kMaxC || budget < 0)
+    return OA_EINVAL;
+  GateArgs a;
+  a.q = (const uint16_t*)q; a.q_stride = q_stride;
+  a.K = (const uint16_t*)K; a.k_sb = k_stride_b; a.k_ss = k_stride_s; a.G = rows / kv_rows;
+  a.asg = asg; a.asg_stride = asg_stride;
+  a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
+  a.Sk = Sk; a.Sk2 = Sk2; a.st_stride_r = (long)C * OA_D;
+  a.nb = nb; a.nb_stride = C;
+  a.score = score; a.n_t = n_t; a.out_stride = C;
+  a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
+  hipLaunchKernelGGL(gate_fill_kernel, dim3(rows), dim3(kGateThreads), 0, (hipStream_t)stream, a,
+                     quota, (double)budget);
   return OA_LAUNCH_STATUS();
 }
 

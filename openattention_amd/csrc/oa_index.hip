@@ -38,26 +38,47 @@ __global__ void __launch_bounds__(64) index_update_kernel(IdxArgs a) {
   const float v_lo = oa::bf16_to_f32(vp[lane]), v_hi = oa::bf16_to_f32(vp[lane + 64]);
   if (r % a.G == 0) {
     const float* Ub = a.U + (long)kvr * OA_D * RQ;
+    float ul[RQ], uh[RQ];
+#pragma unroll
+    for (int j = 0; j < RQ; j += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(Ub + lane * RQ + j);
+      const float4 y = *reinterpret_cast<const float4*>(Ub + (lane + 64) * RQ + j);
+      ul[j] = x.x; ul[j + 1] = x.y; ul[j + 2] = x.z; ul[j + 3] = x.w;
+      uh[j] = y.x; uh[j + 1] = y.y; uh[j + 2] = y.z; uh[j + 3] = y.w;
+    }
+    int8_t mycode = 0;
+#pragma unroll
     for (int j = 0; j < RQ; ++j) {
-      const float zc = oa::dot128_canon(k_lo, Ub[lane * RQ + j], k_hi, Ub[(lane + 64) * RQ + j]);
+      const float zc = oa::dot128_canon(k_lo, ul[j], k_hi, uh[j]);
       float code = rintf(zc / a.scale[(long)kvr * RQ + j]);
       code = fminf(fmaxf(code, -127.f), 127.f);
-      if (lane == j) a.codes[((long)kvr * a.Lmax_codes + pos) * RQ + j] = (int8_t)(int)code;
+      if (lane == j) mycode = (int8_t)(int)code;
     }
+    if (lane < RQ) a.codes[((long)kvr * a.Lmax_codes + pos) * RQ + lane] = mycode;
   }
+  // lane l holds rows l and l+64 of W (16 bf16 each, 32 contiguous bytes)
   const uint16_t* Wb = a.W + (long)r * OA_D * RC;
+  float wl[RC], wh[RC];
+  oa::unpack8(*reinterpret_cast<const uint4*>(Wb + lane * RC), wl);
+  oa::unpack8(*reinterpret_cast<const uint4*>(Wb + lane * RC + 8), wl + 8);
+  oa::unpack8(*reinterpret_cast<const uint4*>(Wb + (lane + 64) * RC), wh);
+  oa::unpack8(*reinterpret_cast<const uint4*>(Wb + (lane + 64) * RC + 8), wh + 8);
   float zp[RC];
 #pragma unroll
   for (int j = 0; j < RC; ++j) {
-    const float d = oa::dot128_canon(k_lo, oa::bf16_to_f32(Wb[lane * RC + j]), k_hi,
-                                     oa::bf16_to_f32(Wb[(lane + 64) * RC + j]));
+    const float d = oa::dot128_canon(k_lo, wl[j], k_hi, wh[j]);
     zp[j] = oa::bf16_round(d) - a.colmean[(long)r * RC + j];
   }
   float best = -INFINITY;
   int bidx = 0x7fffffff;
   const float* cb = a.cent + (long)r * a.C * RC;
   for (int c = lane; c < a.C; c += 64) {
-    const float* cc = cb + (long)c * RC;
+    float cc[RC];
+#pragma unroll
+    for (int j = 0; j < RC; j += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(cb + (long)c * RC + j);
+      cc[j] = x.x; cc[j + 1] = x.y; cc[j + 2] = x.z; cc[j + 3] = x.w;
+    }
     float sim = zp[0] * cc[0];
     float h = cc[0] * cc[0];
 #pragma unroll

@@ -9,14 +9,15 @@
 // Softmax merge (multibin.py:2727-2747): one softmax over {selected} U {expanded} U {proxies},
 // proxy logit s q.kbar'_c + ln n'_c.
 //
-// gfx950 decomposition: one 256-thread workgroup per query-head row.  Each of its four waves
-// owns clusters c = w, w+4, ...: it walks the cluster's own contiguous segment of exp_idx
-// (written grouped by cluster by the top-q kernel) plus the cluster's selected tokens,
-// accumulating the residual sums in registers while folding the same K,V rows into the
-// wave's online softmax, then folds the cluster's proxy.  Every K/V row is read once, the
-// sums are owned by one wave (no atomics, run-to-run deterministic), and the proxies never
-// leave registers.  A lane holds dims (2l, 2l+1), so a row is one 4-byte load per lane.
-// Wave 0 also folds the selected tokens.  The four wave states are merged at the end.
+// gfx950 decomposition: one 256-thread workgroup per query-head row, 16 lane groups of 16
+// lanes; a lane holds 8 of the 128 dims, so a K or V row is one 16-byte load per lane.  Lane
+// group g owns clusters g, g+16, ...: it walks the cluster's selected tokens and its own
+// contiguous segment of exp_idx (the top-q kernel writes segments grouped by cluster), four
+// tokens in flight, accumulating the residual sums in registers while folding the same K,V
+// rows into the group's online softmax, then folds the cluster's proxy.  Every K/V row and
+// every statistics row is read once, the sums are owned by one lane group (no atomics,
+// run-to-run deterministic) and the proxies never leave registers.  The 16 group softmax
+// states are merged in a fixed order at the end.
 //
 // oa_residual writes kbar', vbar' (bf16) and ln n' instead of the softmax (the operator
 // surface of the reference's residual kernels), for use with oa_flash_decode.
@@ -25,9 +26,10 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+constexpr int kGroups = kThreads / 16;
 constexpr int kMaxC = 256;
 constexpr int kMaxSel = 64;
+constexpr int kMaxE = 4096;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct ResArgs {
@@ -44,153 +46,178 @@ struct ResArgs {
 };
 
 struct Soft {
-  float m, l, a0, a1;
-  __device__ __forceinline__ void init() { m = -INFINITY; l = 0.f; a0 = 0.f; a1 = 0.f; }
-  __device__ __forceinline__ void add(float z, float v0, float v1) {
+  float m, l, a[8];
+  __device__ __forceinline__ void init() {
+    m = -INFINITY; l = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = 0.f;
+  }
+  __device__ __forceinline__ void add(float z, const float* v) {
     const float mn = fmaxf(m, z);
     const float al = exp2f(m - mn);
     const float p = exp2f(z - mn);
-    a0 = fmaf(p, v0, a0 * al);
-    a1 = fmaf(p, v1, a1 * al);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = fmaf(p, v[i], a[i] * al);
     l = fmaf(l, al, p);
     m = mn;
   }
 };
 
-__device__ __forceinline__ float2 ld_bf16x2(const uint16_t* p) {
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-  return make_float2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+__device__ __forceinline__ float dot8(const float* a, const float* b) {
+  float p = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p = fmaf(a[i], b[i], p);
+  return p;
 }
 
 template <bool FUSED>
 __global__ void __launch_bounds__(kThreads) residual_kernel(ResArgs a) {
   __shared__ int s_base[kMaxC + 1];
   __shared__ int s_q[kMaxC];
+  __shared__ int s_stok[kMaxSel];
   __shared__ int s_scid[kMaxSel];
-  __shared__ float s_m[kWaves], s_l[kWaves];
-  __shared__ float s_acc[kWaves][OA_D];
+  __shared__ int s_exp[kMaxE];
+  __shared__ float s_m[kGroups], s_l[kGroups];
+  __shared__ float s_acc[kGroups][OA_D];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
+  const int grp = tid >> 4;
+  const int sub = tid & 15;
+  const int d0 = sub * 8;
   const int kvr = row / a.G;
-  const int d0 = 2 * lane;
   const uint16_t* Kb = a.K + (long)kvr * a.kv_sb + d0;
   const uint16_t* Vb = a.V + (long)kvr * a.kv_sb + d0;
 
-  if (tid == 0) {
-    int acc = 0;
-    for (int c = 0; c < a.C; ++c) {
-      const int qc = (int)a.quota[(long)row * a.C + c];
-      s_q[c] = qc;
-      s_base[c] = acc;
-      acc += qc;
+  if (tid < 64) {
+    // quotas -> segment bases: lane l owns clusters 4l..4l+3, exclusive scan over lanes
+    int v[4], loc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid * 4 + i;
+      v[i] = c < a.C ? (int)a.quota[(long)row * a.C + c] : 0;
+      loc += v[i];
     }
-    s_base[a.C] = acc;
+    int incl = loc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += t;
+    }
+    int run = incl - loc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid * 4 + i;
+      if (c < a.C) { s_q[c] = v[i]; s_base[c] = run; }
+      run += v[i];
+    }
+    if (tid == 63) s_base[a.C] = incl;
   }
   for (int i = tid; i < a.n_sel; i += kThreads) {
     const int tok = a.sel[(long)row * a.sel_stride + i];
+    s_stok[i] = tok;
     s_scid[i] = tok >= 0 ? a.asg[(long)row * a.asg_stride + tok] : -1;
   }
+  for (int j = tid; j < a.E; j += kThreads) s_exp[j] = a.exq[(long)row * a.E + j];
   __syncthreads();
 
-  const float2 qv = ld_bf16x2(a.q + (long)row * a.q_stride + d0);
+  float qv[8];
+  oa::unpack8(*reinterpret_cast<const uint4*>(a.q + (long)row * a.q_stride + d0), qv);
   const float zs = a.sm_scale * kLog2e;
   Soft sm;
   sm.init();
-  if (FUSED && wave == 0) {
-    for (int i = 0; i < a.n_sel; ++i) {
-      const int tok = a.sel[(long)row * a.sel_stride + i];
-      if (tok < 0) continue;
-      const float2 k = ld_bf16x2(Kb + (long)tok * a.kv_ss);
-      const float2 v = ld_bf16x2(Vb + (long)tok * a.kv_ss);
-      const float z = oa::wave_sum(fmaf(qv.y, k.y, qv.x * k.x)) * zs;
-      sm.add(z, v.x, v.y);
-    }
-  }
-  const int32_t* erow = a.exq + (long)row * a.E;
-  for (int c = wave; c < a.C; c += kWaves) {
-    float dk0 = 0.f, dk1 = 0.f, dv0 = 0.f, dv1 = 0.f;
+  for (int c = grp; c < a.C; c += kGroups) {
+    float dk[8], dv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { dk[i] = 0.f; dv[i] = 0.f; }
+    // the selected tokens of this cluster (each selected token lies in exactly one cluster, so
+    // the softmax sees it exactly once)
     for (int i = 0; i < a.n_sel; ++i) {
       if (s_scid[i] != c) continue;
-      const int tok = a.sel[(long)row * a.sel_stride + i];
-      const float2 k = ld_bf16x2(Kb + (long)tok * a.kv_ss);
-      const float2 v = ld_bf16x2(Vb + (long)tok * a.kv_ss);
-      dk0 += k.x; dk1 += k.y; dv0 += v.x; dv1 += v.y;
+      const long off = (long)s_stok[i] * a.kv_ss;
+      float kx[8], vx[8];
+      oa::unpack8(*reinterpret_cast<const uint4*>(Kb + off), kx);
+      oa::unpack8(*reinterpret_cast<const uint4*>(Vb + off), vx);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { dk[e] += kx[e]; dv[e] += vx[e]; }
+      if (FUSED) sm.add(oa::group16_sum(dot8(qv, kx)) * zs, vx);
     }
+    // the cluster's segment of expanded tokens, four in flight
+    const int qc = s_q[c];
     const int b0 = s_base[c];
-    const int b1 = min(s_base[c] + s_q[c], a.E);
-    int j = b0;
-    for (; j + 4 <= b1; j += 4) {
-      int t[4];
-      float2 k[4], v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) t[u] = erow[j + u];
+    const int b1 = min(b0 + qc, a.E);
+    for (int j = b0; j < b1; j += 4) {
+      uint4 kw[4], vw[4];
+      int tk[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const long off = (long)(t[u] >= 0 ? t[u] : 0) * a.kv_ss;
-        k[u] = ld_bf16x2(Kb + off);
-        v[u] = ld_bf16x2(Vb + off);
+        tk[u] = (j + u < b1) ? s_exp[j + u] : -1;
+        const long off = (long)(tk[u] >= 0 ? tk[u] : 0) * a.kv_ss;
+        kw[u] = *reinterpret_cast<const uint4*>(Kb + off);
+        vw[u] = *reinterpret_cast<const uint4*>(Vb + off);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (t[u] < 0) continue;
-        dk0 += k[u].x; dk1 += k[u].y; dv0 += v[u].x; dv1 += v[u].y;
-        if (FUSED) {
-          const float z = oa::wave_sum(fmaf(qv.y, k[u].y, qv.x * k[u].x)) * zs;
-          sm.add(z, v[u].x, v[u].y);
-        }
+        if (tk[u] < 0) continue;
+        float kx[8], vx[8];
+        oa::unpack8(kw[u], kx);
+        oa::unpack8(vw[u], vx);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { dk[e] += kx[e]; dv[e] += vx[e]; }
+        if (FUSED) sm.add(oa::group16_sum(dot8(qv, kx)) * zs, vx);
       }
     }
-    for (; j < b1; ++j) {
-      const int tok = erow[j];
-      if (tok < 0) continue;
-      const float2 k = ld_bf16x2(Kb + (long)tok * a.kv_ss);
-      const float2 v = ld_bf16x2(Vb + (long)tok * a.kv_ss);
-      dk0 += k.x; dk1 += k.y; dv0 += v.x; dv1 += v.y;
-      if (FUSED) {
-        const float z = oa::wave_sum(fmaf(qv.y, k.y, qv.x * k.x)) * zs;
-        sm.add(z, v.x, v.y);
-      }
-    }
+    // the proxy of the members still unread
     const long sb = ((long)row * a.C + c) * OA_D + d0;
-    const float2 sk = *reinterpret_cast<const float2*>(a.Sk + sb);
-    const float2 sv = *reinterpret_cast<const float2*>(a.Sv + sb);
-    const float nr = a.n_t[(long)row * a.C + c] - (float)s_q[c];
+    const float4 k0 = *reinterpret_cast<const float4*>(a.Sk + sb);
+    const float4 k1 = *reinterpret_cast<const float4*>(a.Sk + sb + 4);
+    const float4 v0 = *reinterpret_cast<const float4*>(a.Sv + sb);
+    const float4 v1 = *reinterpret_cast<const float4*>(a.Sv + sb + 4);
+    const float sk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const float svv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    const float nr = a.n_t[(long)row * a.C + c] - (float)qc;
     const float den = fmaxf(nr, 1.0f);
-    const float kb0 = (sk.x - dk0) / den, kb1 = (sk.y - dk1) / den;
-    const float vb0 = (sv.x - dv0) / den, vb1 = (sv.y - dv1) / den;
+    float kb[8], vb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kb[e] = (sk[e] - dk[e]) / den;
+      vb[e] = (svv[e] - dv[e]) / den;
+    }
     const bool live = nr > 0.5f;
     const float ln = live ? logf(den) : -INFINITY;
     if (FUSED) {
-      if (live) {
-        const float z = (oa::wave_sum(fmaf(qv.y, kb1, qv.x * kb0)) * a.sm_scale + ln) * kLog2e;
-        sm.add(z, vb0, vb1);
-      }
+      const float dot = oa::group16_sum(dot8(qv, kb));
+      if (live) sm.add((dot * a.sm_scale + ln) * kLog2e, vb);
     } else {
       const long ob = ((long)row * a.C + c) * OA_D + d0;
-      const uint32_t kw = (uint32_t)oa::f32_to_bf16(kb0) | ((uint32_t)oa::f32_to_bf16(kb1) << 16);
-      const uint32_t vw = (uint32_t)oa::f32_to_bf16(vb0) | ((uint32_t)oa::f32_to_bf16(vb1) << 16);
-      *reinterpret_cast<uint32_t*>(a.kbar_r + ob) = kw;
-      *reinterpret_cast<uint32_t*>(a.vbar_r + ob) = vw;
-      if (lane == 0) a.logn[(long)row * a.C + c] = ln;
+      uint4 kw, vw;
+      kw.x = (uint32_t)oa::f32_to_bf16(kb[0]) | ((uint32_t)oa::f32_to_bf16(kb[1]) << 16);
+      kw.y = (uint32_t)oa::f32_to_bf16(kb[2]) | ((uint32_t)oa::f32_to_bf16(kb[3]) << 16);
+      kw.z = (uint32_t)oa::f32_to_bf16(kb[4]) | ((uint32_t)oa::f32_to_bf16(kb[5]) << 16);
+      kw.w = (uint32_t)oa::f32_to_bf16(kb[6]) | ((uint32_t)oa::f32_to_bf16(kb[7]) << 16);
+      vw.x = (uint32_t)oa::f32_to_bf16(vb[0]) | ((uint32_t)oa::f32_to_bf16(vb[1]) << 16);
+      vw.y = (uint32_t)oa::f32_to_bf16(vb[2]) | ((uint32_t)oa::f32_to_bf16(vb[3]) << 16);
+      vw.z = (uint32_t)oa::f32_to_bf16(vb[4]) | ((uint32_t)oa::f32_to_bf16(vb[5]) << 16);
+      vw.w = (uint32_t)oa::f32_to_bf16(vb[6]) | ((uint32_t)oa::f32_to_bf16(vb[7]) << 16);
+      *reinterpret_cast<uint4*>(a.kbar_r + ob) = kw;
+      *reinterpret_cast<uint4*>(a.vbar_r + ob) = vw;
+      if (sub == 0) a.logn[(long)row * a.C + c] = ln;
     }
   }
   if (!FUSED) return;
-  if (lane == 0) { s_m[wave] = sm.m; s_l[wave] = sm.l; }
-  s_acc[wave][d0] = sm.a0;
-  s_acc[wave][d0 + 1] = sm.a1;
+  if (sub == 0) { s_m[grp] = sm.m; s_l[grp] = sm.l; }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s_acc[grp][d0 + i] = sm.a[i];
   __syncthreads();
   if (tid < OA_D) {
     float M = -INFINITY;
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w]);
+    for (int g = 0; g < kGroups; ++g) M = fmaxf(M, s_m[g]);
     float L = 0.f, A = 0.f;
     if (M > -INFINITY) {
-      for (int w = 0; w < kWaves; ++w) {
-        if (s_m[w] > -INFINITY) {
-          const float wt = exp2f(s_m[w] - M);
-          L = fmaf(s_l[w], wt, L);
-          A = fmaf(s_acc[w][tid], wt, A);
+      for (int g = 0; g < kGroups; ++g) {
+        if (s_m[g] > -INFINITY) {
+          const float wt = exp2f(s_m[g] - M);
+          L = fmaf(s_l[g], wt, L);
+          A = fmaf(s_acc[g][tid], wt, A);
         }
       }
     }
@@ -206,7 +233,7 @@ int launch(bool fused, const void* q, long q_stride, const void* K, const void* 
            float sm_scale, void* out, long out_stride, void* kbar_r, void* vbar_r, float* logn,
            void* stream) {
   if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || C <= 0 || C > kMaxC ||
-      n_sel < 0 || n_sel > kMaxSel || E < 0 || (kv_ss % 2) != 0)
+      n_sel < 0 || n_sel > kMaxSel || E < 0 || E > kMaxE || (kv_ss % 8) != 0 || (kv_sb % 8) != 0)
     return OA_EINVAL;
   ResArgs a;
   a.q = (const uint16_t*)q; a.q_stride = q_stride;
@@ -234,7 +261,7 @@ extern "C" int oa_residual_flash(const void* q, long q_stride, const void* K, co
                                  const int32_t* exp_idx, int E, const float* quota,
                                  const float* n_t, const float* Sk, const float* Sv, int C,
                                  float sm_scale, void* out, long out_stride, void* stream) {
-  if (!out) return OA_EINVAL;
+  if (!out || (q_stride % 8) != 0) return OA_EINVAL;
   return launch(true, q, q_stride, K, V, kv_stride_b, kv_stride_s, rows, kv_rows, head_dim, asg,
                 asg_stride, sel, sel_stride, n_sel, exp_idx, E, quota, n_t, Sk, Sv, C, sm_scale,
                 out, out_stride, nullptr, nullptr, nullptr, stream);
@@ -247,7 +274,7 @@ extern "C" int oa_residual(const void* K, const void* V, long kv_stride_b, long 
                            const float* Sk, const float* Sv, int C, void* kbar_r, void* vbar_r,
                            float* log_n, void* stream) {
   if (!kbar_r || !vbar_r || !log_n) return OA_EINVAL;
-  // the query is not read by the residual-only variant; pass K so the pointer is valid
+  // the residual-only variant reads no query; K stands in so the pointer is valid
   return launch(false, K, 0, K, V, kv_stride_b, kv_stride_s, rows, kv_rows, head_dim, asg,
                 asg_stride, sel, sel_stride, n_sel, exp_idx, E, quota, n_t, Sk, Sv, C, 0.f,
                 nullptr, 0, kbar_r, vbar_r, log_n, stream);

@@ -40,10 +40,20 @@ __global__ void __launch_bounds__(64) qgs_prep_kernel(const uint16_t* __restrict
   const float q_lo = oa::bf16_to_f32(q[(long)row * q_stride + lane]);
   const float q_hi = oa::bf16_to_f32(q[(long)row * q_stride + lane + 64]);
   const float* Ub = U + (long)kvr * OA_D * RQ;
+  // lane l holds rows l and l+64 of U (32 contiguous floats each)
+  float ul[RQ], uh[RQ];
+#pragma unroll
+  for (int j = 0; j < RQ; j += 4) {
+    const float4 a = *reinterpret_cast<const float4*>(Ub + lane * RQ + j);
+    const float4 b = *reinterpret_cast<const float4*>(Ub + (lane + 64) * RQ + j);
+    ul[j] = a.x; ul[j + 1] = a.y; ul[j + 2] = a.z; ul[j + 3] = a.w;
+    uh[j] = b.x; uh[j + 1] = b.y; uh[j + 2] = b.z; uh[j + 3] = b.w;
+  }
   float myz = 0.f;
+#pragma unroll
   for (int j = 0; j < RQ; ++j) {
-    float d = oa::dot128_canon(q_lo, Ub[lane * RQ + j], q_hi, Ub[(lane + 64) * RQ + j]);
-    float z = d * scale[(long)kvr * RQ + j];
+    const float d = oa::dot128_canon(q_lo, ul[j], q_hi, uh[j]);
+    const float z = d * scale[(long)kvr * RQ + j];
     if (lane == j) myz = z;
   }
   float a = (lane < RQ) ? fabsf(myz) : 0.f;
@@ -151,6 +161,10 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 constexpr int kMaxTilesLds = 4096;   // Lmax <= 262144
 constexpr int kMaxTop = 64;
 
+__device__ __forceinline__ unsigned long long tile_key(float v, int t) {
+  return ((unsigned long long)oa::float_key(v) << 32) | (0xffffffffu - (unsigned)t);
+}
+
 __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, long s_stride,
                                                          const float* __restrict__ TM, long tm_stride,
                                                          int ntiles, int32_t* __restrict__ sel,
@@ -164,48 +178,61 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
   const int lane = threadIdx.x;
   const int n = *n_dev;
   float* Srow = S + (long)row * s_stride;
-  for (int t = lane; t < ntiles; t += 64) s_tm[t] = TM[(long)row * tm_stride + t];
+  const float NaN = __uint_as_float(0x7fc00000u);
+  // lane l owns tiles l, l+64, ...; it caches the best key among its untaken tiles
+  unsigned long long mine = 0ull;
+  for (int t = lane; t < ntiles; t += 64) {
+    const float v = TM[(long)row * tm_stride + t];
+    s_tm[t] = v;
+    const unsigned long long kk = tile_key(v, t);
+    mine = kk > mine ? kk : mine;
+  }
   __syncthreads();
-  // k best tiles
   for (int i = 0; i < k_top; ++i) {
-    unsigned long long best = 0ull;
-    for (int t = lane; t < ntiles; t += 64) {
-      float v = s_tm[t];
-      if (v != v) continue;  // NaN marks a tile already taken
-      unsigned long long key = ((unsigned long long)oa::float_key(v) << 32) | (0xffffffffu - (unsigned)t);
-      best = key > best ? key : best;
-    }
-    best = wave_max_u64(best);
+    const unsigned long long best = wave_max_u64(mine);
     const int t = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
     if (lane == 0) s_tile[i] = t;
-    __syncthreads();
-    if (lane == 0) s_tm[t] = __uint_as_float(0x7fc00000u);
-    __syncthreads();
-  }
-  for (int i = 0; i < k_top; ++i) s_sc[i * 64 + lane] = Srow[(long)s_tile[i] * 64 + lane];
-  __syncthreads();
-  // row top-k among the candidate tiles
-  for (int i = 0; i < k_top; ++i) {
-    unsigned long long best = 0ull;
-    for (int j = 0; j < k_top; ++j) {
-      float v = s_sc[j * 64 + lane];
-      if (v != v) continue;
-      const unsigned pos = (unsigned)(s_tile[j] * 64 + lane);
-      unsigned long long key = ((unsigned long long)oa::float_key(v) << 32) | (0xffffffffu - pos);
-      best = key > best ? key : best;
+    if (best == mine) {            // the owner lane: mark taken and rescan its tiles
+      s_tm[t] = NaN;
+      mine = 0ull;
+      for (int u = lane; u < ntiles; u += 64) {
+        const float v = s_tm[u];
+        if (v != v) continue;
+        const unsigned long long kk = tile_key(v, u);
+        mine = kk > mine ? kk : mine;
+      }
     }
-    best = wave_max_u64(best);
+  }
+  __syncthreads();
+  // candidates: lane l holds column l of the k chosen tiles
+  mine = 0ull;
+  for (int j = 0; j < k_top; ++j) {
+    const float v = Srow[(long)s_tile[j] * 64 + lane];
+    s_sc[j * 64 + lane] = v;
+    const unsigned long long kk = tile_key(v, s_tile[j] * 64 + lane);
+    mine = kk > mine ? kk : mine;
+  }
+  for (int i = 0; i < k_top; ++i) {
+    const unsigned long long best = wave_max_u64(mine);
     const int pos = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
     if (lane == 0) s_top[i] = pos;
-    for (int j = 0; j < k_top; ++j)
-      if (s_tile[j] * 64 + lane == pos) s_sc[j * 64 + lane] = __uint_as_float(0x7fc00000u);
-    __syncthreads();
+    if (best == mine) {
+      mine = 0ull;
+      for (int j = 0; j < k_top; ++j) {
+        const int pj = s_tile[j] * 64 + lane;
+        if (pj == pos) s_sc[j * 64 + lane] = NaN;
+        const float v = s_sc[j * 64 + lane];
+        if (v != v) continue;
+        const unsigned long long kk = tile_key(v, pj);
+        mine = kk > mine ? kk : mine;
+      }
+    }
   }
+  __syncthreads();
   int32_t* sr = sel + (long)row * sel_stride;
   if (lane < ns) sr[lane] = lane;
   if (lane < nl) sr[ns + lane] = n - nl + lane;
   for (int i = lane; i < k_top; i += 64) sr[ns + nl + i] = s_top[i];
-  __syncthreads();
   for (int i = lane; i < k_top; i += 64) Srow[s_top[i]] = -INFINITY;
 }
 

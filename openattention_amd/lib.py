@@ -30,7 +30,8 @@ SIGNATURES = {
     "oa_qgs_prep": [P, L, P, P, I, I, I, I, P, P, P, P],
     "oa_qgs_scan": [P, I, I, I, P, P, P, L, P, L, P, I, I, P],
     "oa_topk_select": [P, L, P, L, I, I, P, L, P, I, I, I, P],
-    "oa_errorgate": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, P, P, P],
+    "oa_errorgate": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, P, P, P],
+    "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P],
     "oa_waterfill": [P, P, I, I, I, P, P],
     "oa_topq": [P, L, P, L, P, P, P, P, I, P, L, P, I, I, P, I, P, P, P],
     "oa_residual": [P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, P, P, P, P],

@@ -155,10 +155,9 @@ class OursHIP(Method):
         mark("qgs_scan")
         ops.topk_select(self.S, self.TM, sel, C.n_dev, ns, nl, k_top)
         mark("topk_select")
-        ops.errorgate(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, SC)
-        mark("errorgate")
-        ops.waterfill(self.score, self.n_t, self.quota, self.E)
-        mark("waterfill")
+        ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota,
+                      SC, self.E)
+        mark("gate_fill")
         ops.topq(self.S, st, self.quota, self.exp_idx, C.n_dev, C.n0_dev, RMAX)
         mark("topq")
         if self.fused:

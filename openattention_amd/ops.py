@@ -178,12 +178,26 @@ def topk_select(S, TM, sel, n_dev, ns: int, nl: int, k_top: int) -> None:
 
 
 def errorgate(q, K, asg, sel, Sk, Sk2, nb, score, n_t, sm_scale: float) -> None:
+    """wl1 cluster scores; sm_scale is the Python (double) scale, whose square is formed in
+    double and rounded once, as the estimator does (multibin.py:643)."""
     dev = _dev(q, K, asg, sel, Sk, Sk2, nb, score, n_t)
     R, C = nb.shape
     BH = K.shape[0]
     lib.call("oa_errorgate", _ptr(q), q.stride(0), _ptr(K), K.stride(0), K.stride(1), R, BH,
              q.shape[1], _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1],
-             _ptr(Sk), _ptr(Sk2), _ptr(nb), C, float(sm_scale), _ptr(score), _ptr(n_t), _stream(dev))
+             _ptr(Sk), _ptr(Sk2), _ptr(nb), C, float(sm_scale), float(sm_scale) * float(sm_scale),
+             _ptr(score), _ptr(n_t), _stream(dev))
+
+
+def gate_fill(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota, sm_scale: float, E: int) -> None:
+    """ErrorGate + water-filling in one launch (same results as errorgate then waterfill)."""
+    dev = _dev(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota)
+    R, C = nb.shape
+    BH = K.shape[0]
+    lib.call("oa_gate_fill", _ptr(q), q.stride(0), _ptr(K), K.stride(0), K.stride(1), R, BH,
+             q.shape[1], _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1],
+             _ptr(Sk), _ptr(Sk2), _ptr(nb), C, float(sm_scale), float(sm_scale) * float(sm_scale),
+             int(E), _ptr(score), _ptr(n_t), _ptr(quota), _stream(dev))
 
 
 def waterfill(score, n_t, quota, E: int) -> None:

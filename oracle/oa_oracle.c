@@ -97,7 +97,8 @@ static double canon_sum_c(const double* x, int C) {
 /* ------------------------------------------------------------------ deterministic libm
  * Same published algorithms, constants and term counts as the device header:
  * exp  Cody-Waite (fdlibm ln2 split) + Taylor to r^13; log  2 atanh((m-1)/(m+1)) series to
- * f^23; erf  80-term Maclaurin series for |x| < 4, +-1 beyond. */
+ * f^23; erf  (2/sqrt(pi)) x sum_n (-1)^n x^(2n) / (n!(2n+1)), 72 terms in Horner form for
+ * |x| < 4 (coefficients rounded to double), +-1 beyond. */
 double oa_det_exp(double x) {
   if (x != x) return x;
   if (x > 709.782712893384) return INFINITY;
@@ -136,18 +137,42 @@ double oa_det_log(double x) {
 
 float oa_det_logf(float x) { return (float)oa_det_log((double)x); }
 
+static const double kErfC[72] = {
+    0x1.0000000000000p+0, -0x1.5555555555555p-2, 0x1.999999999999ap-4,
+    -0x1.8618618618618p-6, 0x1.2f684bda12f68p-8, -0x1.8d3018d3018d3p-11,
+    0x1.c01c01c01c01cp-14, -0x1.bbd779334ef0bp-17, 0x1.87a00187a0018p-20,
+    -0x1.3777c55568ccdp-23, 0x1.c2e3054870b38p-27, -0x1.2b67310aa9f3ap-30,
+    0x1.6f448e13e85e1p-34, -0x1.a289ee7e40f74p-38, 0x1.bd577e658d020p-42,
+    -0x1.bc6250fb14231p-46, 0x1.a173a167fba4dp-50, -0x1.7271cbe5863ecp-54,
+    0x1.377c2110f2083p-58, -0x1.f1b4073b34a68p-63, 0x1.7abd72258fb6ep-67,
+    -0x1.13246abce1bddp-71, 0x1.7e6b81382cd42p-76, -0x1.fd6bebd65107ap-81,
+    0x1.45c0a838efe59p-85, -0x1.909c9de3a31c5p-90, 0x1.da7460554e5dbp-95,
+    -0x1.0eef30fa10d2cp-99, 0x1.2ac65385f79acp-104, -0x1.3e81bb5701ac5p-109,
+    0x1.4899fcdef0a8dp-114, -0x1.486eea20c2656p-119, 0x1.3e53defc4e233p-124,
+    -0x1.2b778acc3dedfp-129, 0x1.11ae81077a49ep-134, -0x1.e6597092ccbf0p-140,
+    0x1.a47767f2a3c32p-145, -0x1.61f30bc3acd1ap-150, 0x1.22521d98f98a9p-155,
+    -0x1.d05cc9e3507c9p-161, 0x1.6a513f56f8a2fp-166, -0x1.13f85fc9e143ep-171,
+    0x1.9aa19d4d16643p-177, -0x1.2a8fa59ffec31p-182, 0x1.a8830736a5123p-188,
+    -0x1.273d8edcec957p-193, 0x1.91ef82b367a95p-199, -0x1.0be5a4cd94283p-204,
+    0x1.5dd4c9219115ap-210, -0x1.bfb10e0f68c50p-216, 0x1.18d952ef00889p-221,
+    -0x1.59982b2e94840p-227, 0x1.a13ec00b39f6fp-233, -0x1.ee6cefaa5a158p-239,
+    0x1.1f9dec94da5f8p-244, -0x1.48a6b3820b441p-250, 0x1.70f41ac13e2a1p-256,
+    -0x1.970f1cb2ad53fp-262, 0x1.b97d90d3e603bp-268, -0x1.d6db2a7c68dcbp-274,
+    0x1.edf1e6e4658a9p-280, -0x1.fdcf88bbf71dbp-286, 0x1.02eb04e5f82f5p-291,
+    -0x1.02e2bc1b5790ep-297, 0x1.fdbe706576d5dp-304, -0x1.ee3d33862f55bp-310,
+    0x1.d80e20102c46ep-316, -0x1.bc3cf47bca3afp-322, 0x1.9c00b17fe33c8p-328,
+    -0x1.78a61f51a767fp-334, 0x1.537ae8ecb0688p-340, -0x1.2dbafa5779b80p-346,
+};
+
 float oa_det_erff(float xf) {
   const double x = (double)xf;
   if (x != x) return xf;
   const double ax = x < 0.0 ? -x : x;
   if (ax >= 4.0) return x < 0.0 ? -1.0f : 1.0f;
-  const double mx2 = -(ax * ax);
-  double t = ax, sum = ax;
-  for (int n = 1; n <= 80; ++n) {
-    t = (t * mx2) / (double)n;
-    sum = sum + t / (double)(2 * n + 1);
-  }
-  const float rf = (float)(sum * 0x1.20dd750429b6dp+0);
+  const double x2 = ax * ax;
+  double s = kErfC[71];
+  for (int n = 70; n >= 0; --n) s = fma(s, x2, kErfC[n]);
+  const float rf = (float)((ax * s) * 0x1.20dd750429b6dp+0);
   return x < 0.0 ? -rf : rf;
 }
 
@@ -353,9 +378,8 @@ void oa_ref_waterfill(const float* score, const float* n_t, int R, int C, double
  * Per-token rank within its bin by the selector score, trunc_keep = rank < quota
  * (multibin.py:2522-2558); ties to the lower position (ours_graph.py:93-135).  Members are
  * derived from asg over [0, n) minus the selected tokens -- independent of the device's CSR
- * and generated-token lists.  Segment layout: cluster c at [base_c, base_c + q_c), members
- * above the threshold key first, then the tied ones, each group in position order.  Slots
- * past sum q are -1. */
+ * and generated-token lists.  Segment layout: cluster c at [base_c, base_c + q_c), its chosen
+ * members in position order.  Slots past sum q are -1. */
 void oa_ref_topq(const float* S, int ncols, const int32_t* asg, int Lmax, const int32_t* sel, int n_sel,
                  const float* quota, int R, int C, int n, int E, int32_t* exp_idx) {
   uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)(n > 0 ? n : 1));
@@ -380,28 +404,15 @@ void oa_ref_topq(const float* S, int ncols, const int32_t* asg, int Lmax, const 
       }
       qsort(keys, (size_t)m, sizeof(uint64_t), cmp_desc_key);
       const int take = qc < m ? qc : m;
-      if (take <= 0) {
-        base += qc;
-        continue;
+      /* the chosen members, listed in position order */
+      for (int j = 0; j < take; ++j) tmp[j] = (int32_t)(0xffffffffu - (uint32_t)(keys[j] & 0xffffffffu));
+      for (int a = 1; a < take; ++a) {
+        int32_t x = tmp[a];
+        int b = a - 1;
+        while (b >= 0 && tmp[b] > x) { tmp[b + 1] = tmp[b]; --b; }
+        tmp[b + 1] = x;
       }
-      const uint32_t T = (uint32_t)(keys[take - 1] >> 32);
-      int o = 0;
-      for (int pass = 0; pass < 2; ++pass) {
-        int k2 = 0;
-        for (int j = 0; j < take; ++j) {
-          const uint32_t kk = (uint32_t)(keys[j] >> 32);
-          if ((pass == 0 && kk > T) || (pass == 1 && kk == T))
-            tmp[k2++] = (int32_t)(0xffffffffu - (uint32_t)(keys[j] & 0xffffffffu));
-        }
-        /* position order inside each group */
-        for (int a = 1; a < k2; ++a) {
-          int32_t x = tmp[a];
-          int b = a - 1;
-          while (b >= 0 && tmp[b] > x) { tmp[b + 1] = tmp[b]; --b; }
-          tmp[b + 1] = x;
-        }
-        for (int j = 0; j < k2 && base + o < E; ++j) out[base + o++] = tmp[j];
-      }
+      for (int j = 0; j < take && base + j < E; ++j) out[base + j] = tmp[j];
       base += qc;
     }
   }

@@ -144,12 +144,15 @@ def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
     ops.topk_select(S, TM, sel, n_dev, ns, nl, k)
     ops.errorgate(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score, n_t, SC)
     ops.waterfill(score, n_t, quota, E)
+    score2, n_t2, quota2 = torch.empty_like(score), torch.empty_like(n_t), torch.empty_like(quota)
+    ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score2, n_t2, quota2, SC, E)
     ops.topq(S, st, quota, exp_idx, n_dev, n0_dev, rmax)
     ops.residual(K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, kbr, vbr, lnr)
     ops.residual_flash(qr, K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, out, SC)
     torch.cuda.synchronize()
     r.update(S_after=S.cpu().numpy(), sel=sel.cpu().numpy(), score=score.cpu().numpy(),
              n_t=n_t.cpu().numpy(), quota=quota.cpu().numpy(), exp_idx=exp_idx.cpu().numpy()[:, :E],
+             fused=(score2.cpu().numpy(), n_t2.cpu().numpy(), quota2.cpu().numpy()),
              kbar_r=bf16_to_f32(bf16_np(kbr)), vbar_r=bf16_to_f32(bf16_np(vbr)), log_n=lnr.cpu().numpy(),
              out=bf16_to_f32(bf16_np(out)))
     return r
@@ -188,6 +191,8 @@ def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
     assert np.array_equal(g["n_t"], ref["n_t"])
     assert np.array_equal(g["score"], ref["score"]), "ErrorGate scores differ"
     assert np.array_equal(g["quota"], ref["quota"]), "quotas differ"
+    for got, want in zip(g["fused"], (g["score"], g["n_t"], g["quota"])):
+        assert np.array_equal(got, want), "fused gate+fill differs from the separate kernels"
     assert np.array_equal(g["exp_idx"], ref["exp_idx"]), "expanded sets differ"
     live = np.isfinite(ref["log_n"])
     assert np.array_equal(np.isfinite(g["log_n"]), live)
