@@ -64,15 +64,15 @@ int oa_flash_decode(const void* q, long q_stride, const void* k, const void* v, 
  * Replaces _k_index_update_d2 (inference/ours_graph.py:43-90).
  *   codes (kv_rows, codes_lmax, 32) int8; U (kv_rows, 128, 32), scale (kv_rows, 32) fp32;
  *   W (rows, 128, 16) bf16; colmean (rows, 16), cent (rows, C, 16) fp32; asg (rows,
- *   asg_stride) int32; nb (rows, C), Sk, Sk2, Sv (rows, C, 128) fp32; reclist (rows, C, rmax),
- *   reccnt (rows, C) int32.
+ *   asg_stride) int32 and its byte copy asg8 (rows, asg8_stride) uint8 (C <= 256); nb (rows, C),
+ *   Sk, Sk2, Sv (rows, C, 128) fp32; reclist (rows, C, rmax), reccnt (rows, C) int32.
  */
 int oa_index_update(const void* K, const void* V, long kv_stride_b, long kv_stride_s, int rows,
                     int kv_rows, int head_dim, int8_t* codes, int codes_lmax, int rank_q,
                     const float* U, const float* scale, const void* W, const float* colmean,
-                    int rank_c, const float* cent, int C, int32_t* asg, long asg_stride, float* nb,
-                    float* Sk, float* Sk2, float* Sv, int32_t* reclist, int32_t* reccnt, int rmax,
-                    const int* n_dev, void* stream);
+                    int rank_c, const float* cent, int C, int32_t* asg, long asg_stride,
+                    uint8_t* asg8, long asg8_stride, float* nb, float* Sk, float* Sk2, float* Sv,
+                    int32_t* reclist, int32_t* reccnt, int rmax, const int* n_dev, void* stream);
 
 /*
  * QGS query projection zq = (q U) * scale and its exact fixed-point form (exponent fexp per
@@ -138,15 +138,18 @@ int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, l
                  float* score, float* n_t, float* quota, void* stream);
 
 /*
- * Within-cluster top-q by QGS score over CSR members + generated tokens; exp_idx segments
- * grouped by cluster, -1 past the total.  Replaces _k_topq_d2 (inference/ours_graph.py:138-166).
- *   mem (rows, mem_stride) int32 CSR; cstart, clen (rows, C) int32; exp_idx (rows, E) int32.
+ * Within-cluster top-q: the q_c best tail members of every cluster by QGS score (ties to the
+ * lower position), written to exp_idx in segments grouped by cluster (position order inside a
+ * segment), -1 past the total.  Replaces _k_topq_d2 (inference/ours_graph.py:138-166): instead
+ * of gathering member scores through the CSR lists, each row is streamed once in chunks of 8192
+ * positions (scores S, from oa_topk_select, and the byte cluster ids asg8), and the chunks'
+ * candidates are merged.
+ *   quota (rows, C) fp32; exp_idx (rows, E) int32; cand: caller workspace of cand_elems >=
+ *   rows * ceil(Lmax/8192) * E 64-bit entries.  E <= 4096, C <= 256.
  */
-int oa_topq(const float* S, long s_stride, const int32_t* mem, long mem_stride,
-            const int32_t* cstart, const int32_t* clen, const int32_t* reclist,
-            const int32_t* reccnt, int rmax, const int32_t* asg, long asg_stride,
-            const float* quota, int rows, int C, int32_t* exp_idx, int E, const int* n_dev,
-            const int* n0_dev, void* stream);
+int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
+            const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
+            const int* n_dev, uint64_t* cand, long cand_elems, void* stream);
 
 /*
  * Residual proxies: kbar', vbar' (bf16, rows x C x 128) and ln n' (fp32, -inf = none) of the

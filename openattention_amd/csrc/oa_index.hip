@@ -6,7 +6,8 @@
 //   code_r  = clamp(rint((k . U[:, r]) / scale_r), -127, 127)        (KV-head row only)
 //   zp_j    = bf16(k . W[:, j]) - colmean_j                            (per query-head row)
 //   cluster = argmax_c (zp . cent_c - 0.5 |cent_c|^2), ties to the lower id
-//   n_c += 1; Sk_c += k; Sk2_c += k*k; Sv_c += v; append n-1 to the cluster's generated list
+//   n_c += 1; Sk_c += k; Sk2_c += k*k; Sv_c += v; append n-1 to the cluster's generated list;
+//   the cluster id is stored as int32 (asg) and as uint8 (asg8, the byte stream top-q reads)
 // Dot products use the canonical order of oa_common.h; zp . cent and |cent|^2 are sequential
 // fma chains over j = 0..15 -- the CPU restatement replays both.
 #include "oa_common.h"
@@ -22,6 +23,7 @@ struct IdxArgs {
   const float* U; const float* scale;
   const uint16_t* W; const float* colmean; const float* cent;
   int32_t* asg; long asg_stride;
+  uint8_t* asg8; long asg8_stride;
   float* nb; float* Sk; float* Sk2; float* Sv;
   int32_t* reclist; int32_t* reccnt; int rmax;
   const int* n_dev; int C; int G;
@@ -105,6 +107,7 @@ __global__ void __launch_bounds__(64) index_update_kernel(IdxArgs a) {
   a.Sv[sb + lane + 64] += v_hi;
   if (lane == 0) {
     a.asg[(long)r * a.asg_stride + pos] = c;
+    a.asg8[(long)r * a.asg8_stride + pos] = (uint8_t)c;
     a.nb[(long)r * a.C + c] += 1.0f;
     const long rc = (long)r * a.C + c;
     const int cnt = a.reccnt[rc];
@@ -119,17 +122,18 @@ extern "C" int oa_index_update(const void* K, const void* V, long kv_stride_b, l
                                int rows, int kv_rows, int head_dim, int8_t* codes, int codes_lmax,
                                int rank_q, const float* U, const float* scale, const void* W,
                                const float* colmean, int rank_c, const float* cent, int C,
-                               int32_t* asg, long asg_stride, float* nb, float* Sk, float* Sk2,
+                               int32_t* asg, long asg_stride, uint8_t* asg8, long asg8_stride,
+                               float* nb, float* Sk, float* Sk2,
                                float* Sv, int32_t* reclist, int32_t* reccnt, int rmax,
                                const int* n_dev, void* stream) {
   if (head_dim != OA_D || rank_q != RQ || rank_c != RC || kv_rows <= 0 || rows % kv_rows != 0 ||
-      C <= 0 || rmax < 0)
+      C <= 0 || C > 256 || rmax < 0 || !asg8)
     return OA_EINVAL;
   IdxArgs a;
   a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.kv_sb = kv_stride_b; a.kv_ss = kv_stride_s;
   a.codes = codes; a.Lmax_codes = codes_lmax; a.U = U; a.scale = scale;
   a.W = (const uint16_t*)W; a.colmean = colmean; a.cent = cent;
-  a.asg = asg; a.asg_stride = asg_stride; a.nb = nb; a.Sk = Sk; a.Sk2 = Sk2; a.Sv = Sv;
+  a.asg = asg; a.asg_stride = asg_stride; a.asg8 = asg8; a.asg8_stride = asg8_stride; a.nb = nb; a.Sk = Sk; a.Sk2 = Sk2; a.Sv = Sv;
   a.reclist = reclist; a.reccnt = reccnt; a.rmax = rmax; a.n_dev = n_dev; a.C = C;
   a.G = rows / kv_rows;
   hipLaunchKernelGGL(index_update_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, a);

@@ -25,15 +25,15 @@ SIGNATURES = {
     "oa_error_string": [I],
     "oa_flash_decode": [P, L, P, P, L, L, P, L, I, P, L, I, P, P, L, L, I, I, P, L, I, P, L,
                         I, I, I, F, I, P, P, P, P],
-    "oa_index_update": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, P, P, P, P, P,
-                        I, P, P],
+    "oa_index_update": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
+                        P, I, P, P],
     "oa_qgs_prep": [P, L, P, P, I, I, I, I, P, P, P, P],
     "oa_qgs_scan": [P, I, I, I, P, P, P, L, P, L, P, I, I, P],
     "oa_topk_select": [P, L, P, L, I, I, P, L, P, I, I, I, P],
     "oa_errorgate": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, P, P, P],
     "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P],
     "oa_waterfill": [P, P, I, I, I, P, P],
-    "oa_topq": [P, L, P, L, P, P, P, P, I, P, L, P, I, I, P, I, P, P, P],
+    "oa_topq": [P, L, P, L, P, I, I, I, P, I, P, P, L, P],
     "oa_residual": [P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, P, P, P, P],
     "oa_residual_flash": [P, L, P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, F, P, L,
                           P],

@@ -150,7 +150,7 @@ def index_update(K, V, st, n_dev: torch.Tensor, rmax: int) -> None:
     lib.call("oa_index_update", _ptr(K), _ptr(V), K.stride(0), K.stride(1), R, BH, D,
              _ptr(st.codes), st.codes.shape[1], RANK_Q, _ptr(st.U), _ptr(st.scale), _ptr(st.W),
              _ptr(st.colmean), RANK_C, _ptr(st.cent), C, _ptr(st.asg), st.asg.stride(0),
-             _ptr(st.nb), _ptr(st.Sk), _ptr(st.Sk2), _ptr(st.Sv), _ptr(st.reclist),
+             _ptr(st.asg8), st.asg8.stride(0), _ptr(st.nb), _ptr(st.Sk), _ptr(st.Sk2), _ptr(st.Sv), _ptr(st.reclist),
              _ptr(st.reccnt), rmax, _ptr(n_dev), _stream(dev))
 
 
@@ -206,13 +206,25 @@ def waterfill(score, n_t, quota, E: int) -> None:
     lib.call("oa_waterfill", _ptr(score), _ptr(n_t), R, C, int(E), _ptr(quota), _stream(dev))
 
 
-def topq(S, st, quota, exp_idx, n_dev, n0_dev, rmax: int) -> None:
-    dev = _dev(S, quota, exp_idx, n_dev, n0_dev)
+TOPQ_CHUNK = 8192
+
+
+def topq_workspace(rows: int, Lmax: int, E: int, dev) -> torch.Tensor:
+    """Candidate workspace of oa_topq: rows * ceil(Lmax/8192) * E 64-bit entries."""
+    return torch.empty(rows * (-(-Lmax // TOPQ_CHUNK)) * max(E, 1), device=dev, dtype=torch.int64)
+
+
+def topq(S, asg8, quota, exp_idx, n_dev, cand: torch.Tensor | None = None) -> torch.Tensor:
+    """Within-cluster top-q (exp_idx segments grouped by cluster, position order inside)."""
+    dev = _dev(S, asg8, quota, exp_idx, n_dev)
     R, C = quota.shape
-    lib.call("oa_topq", _ptr(S), S.stride(0), _ptr(st.mem), st.mem.stride(0), _ptr(st.cstart),
-             _ptr(st.clen), _ptr(st.reclist), _ptr(st.reccnt), rmax, _ptr(st.asg), st.asg.stride(0),
-             _ptr(quota), R, C, _ptr(exp_idx), exp_idx.shape[1], _ptr(n_dev), _ptr(n0_dev),
-             _stream(dev))
+    Lmax = asg8.shape[1]
+    E = exp_idx.shape[1]
+    if cand is None:
+        cand = topq_workspace(R, Lmax, E, dev)
+    lib.call("oa_topq", _ptr(S), S.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R, C, Lmax,
+             _ptr(exp_idx), E, _ptr(n_dev), _ptr(cand), cand.numel(), _stream(dev))
+    return cand
 
 
 def residual(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n) -> None:

@@ -164,6 +164,7 @@ def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor,
                            zP.index_select(1, init))
     q0 = b * HQ
     st.asg[q0:q0 + HQ, :T] = asg.to(torch.int32)
+    st.asg8[q0:q0 + HQ, :T] = asg.to(torch.uint8)
     st.W[q0:q0 + HQ] = W
     st.colmean[q0:q0 + HQ] = colmean[:, 0]
     st.cent[q0:q0 + HQ] = cent
@@ -187,11 +188,13 @@ class LayerState:
     """One layer's decode index for all B batch rows (rows flattened: KV rows b*HKV + h,
     query-head rows b*HQ + h)."""
 
-    FIELDS = ("codes", "U", "scale", "W", "colmean", "cent", "asg", "nb", "Sk", "Sk2", "Sv",
+    FIELDS = ("codes", "U", "scale", "W", "colmean", "cent", "asg", "asg8", "nb", "Sk", "Sk2", "Sv",
               "mem", "cstart", "clen", "reclist", "reccnt")
 
     def __init__(self, B: int, HKV: int, G: int, Lmax: int, C: int, rmax: int, dev):
         BH, R = B * HKV, B * HKV * G
+        if C > 256:
+            raise ValueError("at most 256 clusters (cluster ids are also kept as bytes)")
         self.B, self.HKV, self.G, self.Lmax, self.C, self.rmax = B, HKV, G, Lmax, C, rmax
         z = lambda *s, dt=torch.float32: torch.zeros(*s, device=dev, dtype=dt)  # noqa: E731
         self.codes = z(BH, Lmax, RQ, dt=torch.int8)
@@ -201,6 +204,7 @@ class LayerState:
         self.colmean = z(R, RC)
         self.cent = z(R, C, RC)
         self.asg = z(R, Lmax, dt=torch.int32)
+        self.asg8 = z(R, Lmax, dt=torch.uint8)
         self.nb = z(R, C)
         self.Sk = z(R, C, D)
         self.Sk2 = z(R, C, D)

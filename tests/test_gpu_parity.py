@@ -146,7 +146,7 @@ def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
     ops.waterfill(score, n_t, quota, E)
     score2, n_t2, quota2 = torch.empty_like(score), torch.empty_like(n_t), torch.empty_like(quota)
     ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score2, n_t2, quota2, SC, E)
-    ops.topq(S, st, quota, exp_idx, n_dev, n0_dev, rmax)
+    ops.topq(S, st.asg8, quota, exp_idx, n_dev)
     ops.residual(K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, kbr, vbr, lnr)
     ops.residual_flash(qr, K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, out, SC)
     torch.cuda.synchronize()
@@ -172,6 +172,7 @@ def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
                         np.float32(SC2), rmax=RMAX)
     for f in ("codes", "asg", "nb", "Sk", "Sk2", "Sv", "reclist", "reccnt"):
         assert np.array_equal(g["state"][f], pre[f]), f"index update: {f} differs"
+    assert np.array_equal(g["state"]["asg8"][:, :n], pre["asg"][:, :n].astype(np.uint8))
     assert np.array_equal(g["zq"], ref["zq"])
     assert np.array_equal(g["fexp"], ref["fexp"])
     # limbs reconstruct Z exactly
@@ -250,12 +251,14 @@ def test_decode_steps_track_oracle(lay4k):
         assert rel.max() < BF16_TOL, (step, rel.max())
         for f in ("asg", "nb", "Sk", "reccnt", "reclist", "codes"):
             assert np.array_equal(getattr(m.st[0], f).cpu().numpy(), st_np[f]), f"step {step}: {f}"
+        assert np.array_equal(m.st[0].asg8.cpu().numpy()[:, :n], st_np["asg"][:, :n].astype(np.uint8))
         n += 1
 
 
 def test_topq_generated_list_overflow_fallback(lay4k):
-    """A cluster whose generated-token list overflowed (count > rmax) is served by scanning
-    [n0, n) for its tokens (ours_graph.py:284-287): same expanded set as the oracle."""
+    """Generated tokens that overflow their cluster's list (count > rmax; ours_graph.py:284-287)
+    are still expanded like any member: top-q streams every position [0, n) with its cluster
+    id, so the expanded set matches the oracle, which derives members from asg alone."""
     print("[case] topq overflow", flush=True)
     lay = lay4k
     st = lay.st.clone()
