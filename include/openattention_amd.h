@@ -140,16 +140,16 @@ int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, l
 /*
  * Within-cluster top-q: the q_c best tail members of every cluster by QGS score (ties to the
  * lower position), written to exp_idx in segments grouped by cluster (position order inside a
- * segment), -1 past the total.  Replaces _k_topq_d2 (inference/ours_graph.py:138-166): instead
- * of gathering member scores through the CSR lists, each row is streamed once in chunks of 8192
- * positions (scores S, from oa_topk_select, and the byte cluster ids asg8), and the chunks'
- * candidates are merged.
- *   quota (rows, C) fp32; exp_idx (rows, E) int32; cand: caller workspace of cand_elems >=
- *   rows * ceil(Lmax/8192) * E 64-bit entries.  E <= 4096, C <= 256.
+ * segment, -1 past the chosen members), -1 past the quota total; a segment straddling E keeps
+ * its best E - base members.  Replaces _k_topq_d2 (inference/ours_graph.py:138-166): instead
+ * of gathering member scores through the CSR lists, one workgroup streams each row once
+ * (scores S from oa_topk_select, byte cluster ids asg8) and selects by per-cluster histogram
+ * thresholds.
+ *   quota (rows, C) fp32; exp_idx (rows, E) int32.  E <= 4096, C <= 256, Lmax <= 2^24.
  */
 int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
             const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
-            const int* n_dev, uint64_t* cand, long cand_elems, void* stream);
+            const int* n_dev, void* stream);
 
 /*
  * Residual proxies: kbar', vbar' (bf16, rows x C x 128) and ln n' (fp32, -inf = none) of the

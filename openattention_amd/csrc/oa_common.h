@@ -63,6 +63,48 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
   return v;
 }
+// ---- order-independent reductions on the DPP network (no LDS round trips) ------------------
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror fold each 16-lane row;
+// row_bcast15 (rows 1, 3) and row_bcast31 (rows 2, 3) fold the rows into lane 63, which is then
+// read into a scalar: every lane returns the wave's maximum.  Lanes a DPP step does not write
+// keep their own value (old = src), so max() leaves them unchanged.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ unsigned dpp_u32(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWMASK, 0xf, false);
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ unsigned long long dpp_max_u64_step(unsigned long long v) {
+  const unsigned lo = dpp_u32<CTRL, ROWMASK>((unsigned)v);
+  const unsigned hi = dpp_u32<CTRL, ROWMASK>((unsigned)(v >> 32));
+  const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+  return o > v ? o : v;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  v = dpp_max_u64_step<0xB1, 0xf>(v);    // quad_perm [1,0,3,2]
+  v = dpp_max_u64_step<0x4E, 0xf>(v);    // quad_perm [2,3,0,1]
+  v = dpp_max_u64_step<0x141, 0xf>(v);   // row_half_mirror
+  v = dpp_max_u64_step<0x140, 0xf>(v);   // row_mirror
+  v = dpp_max_u64_step<0x142, 0xa>(v);   // row_bcast15
+  v = dpp_max_u64_step<0x143, 0xc>(v);   // row_bcast31
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, 63);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), 63);
+  return ((unsigned long long)hi << 32) | lo;
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ unsigned dpp_max_u32_step(unsigned v) {
+  const unsigned o = dpp_u32<CTRL, ROWMASK>(v);
+  return o > v ? o : v;
+}
+__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
+  v = dpp_max_u32_step<0xB1, 0xf>(v);
+  v = dpp_max_u32_step<0x4E, 0xf>(v);
+  v = dpp_max_u32_step<0x141, 0xf>(v);
+  v = dpp_max_u32_step<0x140, 0xf>(v);
+  v = dpp_max_u32_step<0x142, 0xa>(v);
+  v = dpp_max_u32_step<0x143, 0xc>(v);
+  return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // reductions inside a 16-lane group
 __device__ __forceinline__ float group16_sum(float v) {
   v = v + __shfl_xor(v, 8, 64);

@@ -8,201 +8,180 @@
 // Selected, sink, local and unwritten positions carry a -inf score and never qualify.
 //
 // exp_idx row layout: cluster c owns slots [base_c, base_c + q_c), base_c = sum_{c'<c} q_c';
-// a segment lists its chosen members in position order; slots past sum q are -1.
+// a segment lists its chosen members in position order and is -1 past them; slots past sum q
+// are -1.  Only E slots exist: a segment straddling E keeps its best E - base_c members.
 //
-// gfx950 decomposition.  About 40 of 64 clusters carry a quota and their members cover most
-// of a row, so the row is streamed once instead of gathering member scores:
-//   topq_chunk: grid (chunks of 8192 positions, rows).  A workgroup copies its chunk's scores
-//     and 8-bit cluster ids into LDS with coalesced loads, then finds, for every cluster at
-//     once, the exact top-min(q_c, members) of the chunk by an MSB-first radix select over the
-//     unique 48-bit key (order-preserving score key, then the complement of the position inside
-//     the chunk): 12 passes of 4-bit digits with per-cluster LDS histograms and per-cluster
-//     digit searches.  Candidates go to the caller's workspace as 64-bit keys
-//     (score key << 32 | ~position), q_c slots per cluster per chunk.
-//   topq_merge: one workgroup per row; each wave takes clusters round-robin and extracts the
-//     q_c best candidate keys over the chunks with wave butterflies, then writes the winners in
-//     position order.
+// gfx950 decomposition: one 1024-thread workgroup per row.  About 40 of 64 clusters carry a
+// quota and their members cover most of the row, so the row is streamed (scores S and byte
+// cluster ids asg8, coalesced) into registers -- 1024 * PPT positions at a time, PPT per
+// thread -- and every selection step works on those registers and on LDS:
+//   P1  per-cluster min and max score key (LDS atomics; lanes of one 64-position batch rarely
+//       share a cluster, so they rarely collide);
+//   P2  per-cluster histogram of NB linear bins between that min and max (monotone binning:
+//       a higher score never lands in a lower bin);
+//   P3  one wave per cluster: t = min(q_c, members, E - base_c), the bin b* holding the t-th
+//       best member, `above` = members in higher bins, `need` = t - above from bin b*;
+//   P4  members above b* are chosen; members of bin b* are staged in LDS as unique 64-bit keys
+//       (score key << 32 | ~position) when some must be dropped;
+//   P5  one wave per staged cluster picks the `need` best staged keys (repeated wave maxima for
+//       small `need`, an MSB-first bitwise search on ballot counts otherwise); a cluster whose
+//       bin b* does not fit in LDS is resolved by the same bitwise search run block-wide over
+//       the row, streamed again;
+//   P6  the chosen (cluster << 24 | position) words, sum t <= E of them, are bitonic-sorted in
+//       LDS, which orders them by cluster and then position, and every slot of the exp_idx
+//       row is written once (-1 where a segment is short).
+// Rows longer than 1024 * PPT positions are processed in segments that are re-read from
+// global memory (L2 / Infinity Cache) in each pass.  Rows are read in groups of four
+// positions, so both row strides are multiples of 4 and hold round_up(Lmax, 4) entries.
+#include <algorithm>
+
 #include "oa_common.h"
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxC = 256;
 constexpr int kMaxE = 4096;
-constexpr int kChunk = 8192;
-constexpr int kDigits = 16;     // 4-bit radix digits
-constexpr int kPasses = 12;     // 48-bit keys
-constexpr int KREG = 16;        // candidate slots per lane in the merge
+constexpr int kMaxPos = 1 << 24;               // positions are packed into 24 bits in P6
+constexpr int kExtractMax = 40;                // need above this: bitwise threshold search
+constexpr int kBCapMax = 8192;                 // staged boundary keys (u64)
 constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
+constexpr int kLdsLimit = 160 * 1024;
 
-// dynamic LDS layout of the chunk kernel
-struct ChunkLds {
-  uint32_t key[kChunk];
-  uint8_t cid[kChunk];
+enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3 };
+
+struct TopqArgs {
+  const float* S; long s_stride;
+  const uint8_t* asg8; long a_stride;
+  const float* quota; int C; int E; const int* n_dev;
+  int32_t* exp_idx;
+  int nb;          // bins per cluster (power of two, >= 64)
+  int nb_shift;    // log2(nb)
+  int bcap;        // staged boundary capacity (u64 keys)
+  int cpow;        // power of two >= E for the P6 sort
 };
 
-__global__ void __launch_bounds__(kThreads) topq_chunk_kernel(
-    const float* __restrict__ S, long s_stride, const uint8_t* __restrict__ asg8, long a_stride,
-    const float* __restrict__ quota, int C, int E, const int* __restrict__ n_dev,
-    unsigned long long* __restrict__ cand, int nchunks) {
+__device__ __forceinline__ float unkey(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ int bin_of(uint32_t key, float fmin, float scale, int nb) {
+  const float x = (unkey(key) - fmin) * scale;
+  return min((int)x, nb - 1);
+}
+
+__device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
+  return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (unsigned)pos);
+}
+
+// append one chosen (cluster << 24 | position) word per taking lane, one LDS atomic per wave
+__device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t* cst, int* ctot,
+                                              int lane) {
+  const unsigned long long bal = __ballot(take);
+  if (bal == 0ull) return;
+  const int leader = __ffsll((long long)bal) - 1;
+  int off = 0;
+  if (lane == leader) off = atomicAdd(ctot, __popcll(bal));
+  off = __shfl(off, leader, 64);
+  if (take) cst[off + __popcll(bal & ((1ull << lane) - 1ull))] = word;
+}
+
+// P5 on one staged cluster: the `need` largest of cnt unique keys, held KR per lane
+template <int KR>
+__device__ void select_staged(const unsigned long long* src, int cnt, int need, int c,
+                              uint32_t* cst, int* ctot, int lane) {
+  unsigned long long x[KR];
+#pragma unroll
+  for (int j = 0; j < KR; ++j) x[j] = src[min(j * 64 + lane, cnt - 1)];
+#pragma unroll
+  for (int j = 0; j < KR; ++j) x[j] = j * 64 + lane < cnt ? x[j] : 0ull;
+  unsigned long long T = 0ull;
+  if (need <= kExtractMax) {
+    unsigned taken = 0u;
+    for (int k = 0; k < need; ++k) {
+      unsigned long long best = 0ull;
+#pragma unroll
+      for (int j = 0; j < KR; ++j)
+        if (!((taken >> j) & 1u) && x[j] > best) best = x[j];
+      best = oa::wave_max_u64(best);
+#pragma unroll
+      for (int j = 0; j < KR; ++j)
+        if (x[j] == best) taken |= 1u << j;
+      T = best;
+    }
+  } else {
+    for (int bit = 63; bit >= 0; --bit) {
+      const unsigned long long cnd = T | (1ull << bit);
+      int k = 0;
+#pragma unroll
+      for (int j = 0; j < KR; ++j) k += __popcll(__ballot(x[j] >= cnd));
+      if (k >= need) T = cnd;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KR; ++j) {
+    const bool take = x[j] != 0ull && x[j] >= T;
+    const uint32_t pos = 0xffffffffu - (uint32_t)(x[j] & 0xffffffffull);
+    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctot, lane);
+  }
+}
+
+// the same from LDS in a loop, for more than 1024 staged keys
+__device__ void select_staged_loop(const unsigned long long* src, int cnt, int need, int c,
+                                   uint32_t* cst, int* ctot, int lane) {
+  unsigned long long T = 0ull;
+  for (int bit = 63; bit >= 0; --bit) {
+    const unsigned long long cnd = T | (1ull << bit);
+    int k = 0;
+    for (int b0 = 0; b0 < cnt; b0 += 64) {
+      const int j = b0 + lane;
+      k += __popcll(__ballot(j < cnt && src[min(j, cnt - 1)] >= cnd));
+    }
+    if (k >= need) T = cnd;
+  }
+  for (int b0 = 0; b0 < cnt; b0 += 64) {
+    const int j = b0 + lane;
+    const unsigned long long x = src[min(j, cnt - 1)];
+    const bool take = j < cnt && x >= T;
+    const uint32_t pos = 0xffffffffu - (uint32_t)(x & 0xffffffffull);
+    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctot, lane);
+  }
+}
+
+template <int PPT>
+__global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
-  ChunkLds& L = *reinterpret_cast<ChunkLds*>(dyn);
-  // per-cluster arrays after the chunk copy: hist (C x 16), pref, krem, q, base, fill, staging
-  int* s_hist = reinterpret_cast<int*>(reinterpret_cast<char*>(dyn) + sizeof(ChunkLds));
-  unsigned long long* s_pref = reinterpret_cast<unsigned long long*>(s_hist + C * kDigits);
-  int* s_krem = reinterpret_cast<int*>(s_pref + C);
-  int* s_q = s_krem + C;
-  int* s_base = s_q + C;
-  int* s_fill = s_base + C + 1;
-  unsigned long long* s_stage = reinterpret_cast<unsigned long long*>(
-      (reinterpret_cast<uintptr_t>(s_fill + C) + 7) & ~static_cast<uintptr_t>(7));
-  const int chunk = blockIdx.x;
-  const int row = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int n = *n_dev;
-  const int p0 = chunk * kChunk;
-  const int len = max(0, min(kChunk, n - p0));
-  unsigned long long* out = cand + ((long)row * nchunks + chunk) * E;
-  if (tid < 64) {
-    int v[4], loc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid * 4 + i;
-      v[i] = c < C ? (int)quota[(long)row * C + c] : 0;
-      loc += v[i];
-    }
-    int incl = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (tid >= off) incl += t;
-    }
-    int run = incl - loc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid * 4 + i;
-      if (c < C) { s_q[c] = v[i]; s_base[c] = run; }
-      run += v[i];
-    }
-    if (tid == 63) s_base[C] = incl;
-  }
-  for (int i = tid; i < len; i += kThreads) {
-    L.key[i] = oa::float_key(S[(long)row * s_stride + p0 + i]);
-    L.cid[i] = asg8[(long)row * a_stride + p0 + i];
-  }
-  for (int e = tid; e < C * kDigits; e += kThreads) s_hist[e] = 0;
-  for (int c = tid; c < C; c += kThreads) { s_pref[c] = 0ull; s_fill[c] = 0; }
-  __syncthreads();
-  const int total = min(s_base[C], E);
-  for (int j = tid; j < total; j += kThreads) s_stage[j] = 0ull;
-  // qualifying members per cluster -> target count min(q, members)
-  for (int i = tid; i < len; i += kThreads) {
-    const int c = L.cid[i];
-    if (c < C && s_q[c] > 0 && L.key[i] > kNegInfKey) atomicAdd(&s_hist[c * kDigits], 1);
-  }
-  __syncthreads();
-  for (int c = tid; c < C; c += kThreads) {
-    s_krem[c] = min(s_q[c], s_hist[c * kDigits]);
-    s_hist[c * kDigits] = 0;
-  }
-  __syncthreads();
-  // radix select of the s_krem[c]-th largest 48-bit key of every cluster at once
-  for (int pass = 0; pass < kPasses; ++pass) {
-    const int shift = 44 - 4 * pass;
-    for (int i = tid; i < len; i += kThreads) {
-      const int c = L.cid[i];
-      if (c >= C || s_krem[c] <= 0 || L.key[i] <= kNegInfKey) continue;
-      const unsigned long long k48 = ((unsigned long long)L.key[i] << 16) | (0xffffu - (unsigned)i);
-      if ((k48 >> (shift + 4)) == (s_pref[c] >> (shift + 4)))
-        atomicAdd(&s_hist[c * kDigits + (int)((k48 >> shift) & 15u)], 1);
-    }
-    __syncthreads();
-    for (int c = tid; c < C; c += kThreads) {
-      const int k = s_krem[c];
-      if (k > 0) {
-        int cum = 0, digit = 0, nk = k;
-        for (int d = kDigits - 1; d >= 0; --d) {
-          const int h = s_hist[c * kDigits + d];
-          if (cum + h >= k) { digit = d; nk = k - cum; break; }
-          cum += h;
-        }
-        s_pref[c] |= ((unsigned long long)digit) << shift;
-        s_krem[c] = nk;
-      }
-      for (int d = 0; d < kDigits; ++d) s_hist[c * kDigits + d] = 0;
-    }
-    __syncthreads();
-  }
-  // every qualifying key >= the cluster's threshold is a candidate (keys are unique)
-  for (int i = tid; i < len; i += kThreads) {
-    const int c = L.cid[i];
-    if (c >= C || s_q[c] <= 0 || L.key[i] <= kNegInfKey) continue;
-    const unsigned long long k48 = ((unsigned long long)L.key[i] << 16) | (0xffffu - (unsigned)i);
-    if (k48 >= s_pref[c]) {
-      const int slot = atomicAdd(&s_fill[c], 1);
-      if (slot < s_q[c] && s_base[c] + slot < total)
-        s_stage[s_base[c] + slot] =
-            ((unsigned long long)L.key[i] << 32) | (0xffffffffu - (unsigned)(p0 + i));
-    }
-  }
-  __syncthreads();
-  // each cluster's candidates in position order (descending complement), then written out
-  for (int c = tid; c < C; c += kThreads) {
-    const int b = s_base[c];
-    const int m = min(min(s_fill[c], s_q[c]), total - b);
-    for (int a = 1; a < m; ++a) {
-      const unsigned long long x = s_stage[b + a];
-      const unsigned xp = 0xffffffffu - (unsigned)(x & 0xffffffffull);
-      int j = a - 1;
-      while (j >= 0 && (0xffffffffu - (unsigned)(s_stage[b + j] & 0xffffffffull)) > xp) {
-        s_stage[b + j + 1] = s_stage[b + j];
-        --j;
-      }
-      s_stage[b + j + 1] = x;
-    }
-  }
-  __syncthreads();
-  for (int j = tid; j < total; j += kThreads) out[j] = s_stage[j];
-}
-
-size_t chunk_lds_bytes(int C, int E) {
-  return sizeof(ChunkLds) + sizeof(int) * C * kDigits + sizeof(unsigned long long) * C +
-         sizeof(int) * (4 * C + 2) + 8 + sizeof(unsigned long long) * (size_t)E;
-}
-
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const unsigned long long o = __shfl_xor(v, m, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-__device__ __forceinline__ int lanes_below(bool flag, int lane, int* total) {
-  const unsigned long long b = __ballot(flag);
-  *total = __popcll(b);
-  return __popcll(b & ((1ull << lane) - 1ull));
-}
-
-// Candidate slot idx (0 <= idx < nchunks*q) of cluster c: chunk idx / q, entry idx % q.  Over
-// idx the non-empty candidates appear in ascending position order.
-__global__ void __launch_bounds__(kThreads) topq_merge_kernel(
-    const unsigned long long* __restrict__ cand, int nchunks, const float* __restrict__ quota,
-    int C, int E, int32_t* __restrict__ exp_idx) {
-  __shared__ int s_q[kMaxC];
+  __shared__ int s_w[kMaxC];              // min(q_c, E - base_c), clamped at 0
   __shared__ int s_base[kMaxC + 1];
+  __shared__ uint32_t s_kmin[kMaxC], s_kmax[kMaxC];
+  __shared__ float s_fmin[kMaxC], s_scale[kMaxC];
+  __shared__ int s_t[kMaxC], s_bstar[kMaxC], s_above[kMaxC], s_bcnt[kMaxC];
+  __shared__ int s_mode[kMaxC], s_boff[kMaxC], s_bcur[kMaxC];
+  __shared__ int s_tpre[kMaxC + 1];
+  __shared__ int s_fbl[kMaxC];
+  __shared__ int s_bused, s_nfb, s_ctot, s_fbcnt[3];
+  unsigned long long* s_bst = dyn;                                    // bcap
+  uint32_t* s_cst = reinterpret_cast<uint32_t*>(dyn + a.bcap);        // cpow
+  int* s_hist = reinterpret_cast<int*>(s_cst + a.cpow);               // C * nb
+
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
+  const int C = a.C, E = a.E, NB = a.nb;
+  const int n = *a.n_dev;
+  const float* srow = a.S + (long)row * a.s_stride;
+  const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
+  int32_t* erow = a.exp_idx + (long)row * E;
+
+  // ---- P0: quota prefix, per-cluster state, histogram clear
   if (wave == 0) {
     int v[4], loc = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = lane * 4 + i;
-      v[i] = c < C ? (int)quota[(long)row * C + c] : 0;
+      v[i] = c < C ? (int)a.quota[(long)row * C + c] : 0;
       loc += v[i];
     }
     int incl = loc;
@@ -214,98 +193,306 @@ __global__ void __launch_bounds__(kThreads) topq_merge_kernel(
     int run = incl - loc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = lane * 4 + i;
-      if (c < C) { s_q[c] = v[i]; s_base[c] = run; }
+      const int c = lane * 4 + i;     // 0..255
+      s_base[c] = run;
+      s_w[c] = c < C ? max(0, min(v[i], E - run)) : 0;
       run += v[i];
     }
-    if (lane == 63) s_base[C] = incl;
+    if (lane == 63) s_base[kMaxC] = incl;
+  }
+  for (int c = tid; c < kMaxC; c += kThreads) {
+    s_kmin[c] = 0xffffffffu; s_kmax[c] = 0u; s_t[c] = 0; s_mode[c] = kModeNone; s_bcur[c] = 0;
+  }
+  for (int i = tid; i < C * NB; i += kThreads) s_hist[i] = 0;
+  if (tid == 0) { s_bused = 0; s_nfb = 0; s_ctot = 0; s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0; }
+  __syncthreads();
+
+  // register i of a thread holds position sg*SEG + (i/4)*4096 + 4*tid + i%4: each group of four
+  // consecutive positions arrives as one float4 of scores and one u32 of cluster ids
+  constexpr int SEG = kThreads * PPT;
+  constexpr int NG = PPT / 4;
+  static_assert(PPT % 4 == 0, "PPT must be a multiple of 4");
+  const int nseg = n > 0 ? (n + SEG - 1) / SEG : 0;
+  uint32_t kk[PPT];              // score key of a qualifying member, else 0
+  uint32_t cp[NG];               // cluster ids, 4 per register
+  auto pos_of = [&](int sg, int i) -> int { return sg * SEG + (i >> 2) * 4096 + 4 * tid + (i & 3); };
+
+  // stream segment sg of the row into registers (clamped loads: all of them in flight); rows
+  // are read up to the multiple of 4 that follows n - 1
+  auto load = [&](int sg) {
+    const int last4 = (n - 1) & ~3;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int p = min(sg * SEG + g * 4096 + 4 * tid, last4);
+      const float4 v = *reinterpret_cast<const float4*>(srow + p);
+      cp[g] = *reinterpret_cast<const uint32_t*>(arow + p);
+      kk[4 * g] = __float_as_uint(v.x);
+      kk[4 * g + 1] = __float_as_uint(v.y);
+      kk[4 * g + 2] = __float_as_uint(v.z);
+      kk[4 * g + 3] = __float_as_uint(v.w);
+    }
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
+      const int c = (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu);
+      const bool q = pos_of(sg, i) < n && key > kNegInfKey && s_w[c] > 0;
+      kk[i] = q ? key : 0u;
+    }
+  };
+  auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+
+  // ---- P1: per-cluster key range
+  for (int sg = 0; sg < nseg; ++sg) {
+    load(sg);
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      if (kk[i]) {
+        const int c = cid(i);
+        atomicMin(&s_kmin[c], kk[i]);
+        atomicMax(&s_kmax[c], kk[i]);
+      }
+    }
   }
   __syncthreads();
-  const int total = s_base[C];
-  int32_t* erow = exp_idx + (long)row * E;
-  for (int j = total + tid; j < E; j += kThreads) erow[j] = -1;
-  const unsigned long long* crow = cand + (long)row * nchunks * E;
-  for (int c = wave; c < C; c += kWaves) {
-    const int q = s_q[c];
-    if (q <= 0) continue;
-    const int base = s_base[c];
-    const int limit = min(q, E - base);
-    if (limit <= 0) continue;
-    const int M = nchunks * q;
-    // threshold T = the limit-th largest candidate key (keys are unique, 0 = empty slot)
-    unsigned long long T = 0ull;
-    if (M <= 64 * KREG) {
-      unsigned long long key[KREG];
-#pragma unroll
-      for (int j = 0; j < KREG; ++j) {
-        const int idx = j * 64 + lane;
-        key[j] = idx < M ? crow[(long)(idx / q) * E + base + idx % q] : 0ull;
-      }
-      unsigned taken = 0u;
-      for (int t = 0; t < limit; ++t) {
-        unsigned long long best = 0ull;
-#pragma unroll
-        for (int j = 0; j < KREG; ++j)
-          if (!((taken >> j) & 1u) && key[j] > best) best = key[j];
-        best = wave_max_u64(best);
-        if (best == 0ull) break;
-        T = best;
-#pragma unroll
-        for (int j = 0; j < KREG; ++j)
-          if (key[j] == best) taken |= 1u << j;
-      }
-    } else {
-      unsigned long long prev = ~0ull;
-      for (int t = 0; t < limit; ++t) {
-        unsigned long long best = 0ull;
-        for (int idx = lane; idx < M; idx += 64) {
-          const unsigned long long kk = crow[(long)(idx / q) * E + base + idx % q];
-          if (kk < prev && kk > best) best = kk;
-        }
-        best = wave_max_u64(best);
-        if (best == 0ull) break;
-        T = best;
-        prev = best;
-      }
+  for (int c = tid; c < C; c += kThreads) {
+    float scale = 0.f, fmin = 0.f;
+    if (s_kmax[c] >= s_kmin[c]) {
+      fmin = unkey(s_kmin[c]);
+      const float d = unkey(s_kmax[c]) - fmin;
+      scale = d > 0.f ? (float)NB / d : 0.f;
+      if (!(scale <= 3.0e38f)) scale = 0.f;      // d subnormal: one bin, resolved by P5
     }
-    if (T == 0ull) continue;
-    // emit the candidates >= T in slot order = position order
-    int run = 0;
-    for (int b0 = 0; b0 < M; b0 += 64) {
-      const int idx = b0 + lane;
-      const unsigned long long kk = idx < M ? crow[(long)(idx / q) * E + base + idx % q] : 0ull;
-      const bool take = kk != 0ull && kk >= T;
-      int tot;
-      const int below = lanes_below(take, lane, &tot);
-      if (take && run + below < limit)
-        erow[base + run + below] = (int)(0xffffffffu - (unsigned)(kk & 0xffffffffull));
-      run += tot;
+    s_fmin[c] = fmin;
+    s_scale[c] = scale;
+  }
+  __syncthreads();
+
+  // ---- P2: histogram
+  for (int sg = 0; sg < nseg; ++sg) {
+    if (nseg > 1) load(sg);
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      if (kk[i]) {
+        const int c = cid(i);
+        atomicAdd(&s_hist[(c << a.nb_shift) + bin_of(kk[i], s_fmin[c], s_scale[c], NB)], 1);
+      }
     }
   }
+  __syncthreads();
+
+  // ---- P3: threshold bin per cluster (one wave per cluster)
+  const int npl = NB >> 6;       // bins per lane
+  for (int c = wave; c < C; c += kWaves) {
+    const int w = s_w[c];
+    if (w <= 0) continue;
+    const int* h = s_hist + (c << a.nb_shift) + lane * npl;
+    int ls = 0;
+    for (int j = 0; j < npl; ++j) ls += h[j];
+    int sfx = ls;                // members in lanes >= this one
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int x = __shfl_down(sfx, off, 64);
+      if (lane + off < 64) sfx += x;
+    }
+    const int m = __shfl(sfx, 0, 64);
+    const int t = min(w, m);
+    if (t <= 0) continue;
+    const unsigned long long bal = __ballot(sfx >= t);
+    const int L = 63 - __clzll((long long)bal);
+    if (lane == L) {
+      int acc = sfx - ls;
+      int bs = lane * npl, bc = 0;
+      for (int j = npl - 1; j >= 0; --j) {
+        if (acc + h[j] >= t) { bs = lane * npl + j; bc = h[j]; break; }
+        acc += h[j];
+      }
+      const int need = t - acc;
+      s_t[c] = t;
+      s_bstar[c] = bs;
+      s_above[c] = acc;
+      s_bcnt[c] = bc;
+      int mode = kModeAll;
+      if (need < bc) {
+        const int off = atomicAdd(&s_bused, bc);
+        if (off + bc <= a.bcap) {
+          mode = kModeStaged;
+          s_boff[c] = off;
+        } else {
+          mode = kModeBlock;
+          s_fbl[atomicAdd(&s_nfb, 1)] = c;
+        }
+      }
+      s_mode[c] = mode;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {               // prefix of t over clusters: first chosen word of each cluster
+    int v[4], loc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = s_t[lane * 4 + i]; loc += v[i]; }
+    int incl = loc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    int run = incl - loc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { s_tpre[lane * 4 + i] = run; run += v[i]; }
+    if (lane == 63) s_tpre[kMaxC] = incl;
+  }
+
+  // ---- P4: chosen members above b*, staged members of b*
+  for (int sg = 0; sg < nseg; ++sg) {
+    if (nseg > 1) load(sg);
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      bool take = false, stage = false;
+      int c = 0;
+      if (kk[i]) {
+        c = cid(i);
+        const int mode = s_mode[c];
+        const int b = bin_of(kk[i], s_fmin[c], s_scale[c], NB);
+        const int bs = s_bstar[c];
+        take = b > bs || (b == bs && mode == kModeAll);
+        stage = b == bs && mode == kModeStaged;
+      }
+      const int p = pos_of(sg, i);
+      append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst, &s_ctot, lane);
+      if (stage) s_bst[s_boff[c] + atomicAdd(&s_bcur[c], 1)] = key64(kk[i], p);
+    }
+  }
+  __syncthreads();
+
+  // ---- P5: resolve bin b* of the staged clusters, one wave per cluster
+  for (int c = wave; c < C; c += kWaves) {
+    if (s_mode[c] != kModeStaged) continue;
+    const int cnt = s_bcnt[c];
+    const int need = s_t[c] - s_above[c];
+    const unsigned long long* src = s_bst + s_boff[c];
+    if (cnt <= 64) select_staged<1>(src, cnt, need, c, s_cst, &s_ctot, lane);
+    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, s_cst, &s_ctot, lane);
+    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, s_cst, &s_ctot, lane);
+    else select_staged_loop(src, cnt, need, c, s_cst, &s_ctot, lane);
+  }
+  // clusters whose bin b* did not fit in LDS: block-wide bitwise search, re-streaming the row
+  // (rare; keeps the row's registers dead during P5)
+  const int nfb = s_nfb;         // final since the P3 barrier
+  for (int f = 0; f < nfb; ++f) {
+    const int c = s_fbl[f];
+    const int bs = s_bstar[c];
+    const int need = s_t[c] - s_above[c];
+    const float fmin = s_fmin[c], scale = s_scale[c];
+    unsigned long long T = 0ull;
+    for (int bit = 63, it = 0; bit >= 0; --bit, ++it) {
+      const unsigned long long cnd = T | (1ull << bit);
+      int k = 0;
+      for (int sg = 0; sg < nseg; ++sg) {
+        load(sg);
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+          const int p = pos_of(sg, i);
+          const bool in = kk[i] && cid(i) == c && bin_of(kk[i], fmin, scale, NB) == bs &&
+                          key64(kk[i], p) >= cnd;
+          k += __popcll(__ballot(in));
+        }
+      }
+      // three counters in rotation: the one cleared here is next added to two barriers later
+      if (lane == 0 && k) atomicAdd(&s_fbcnt[it % 3], k);
+      __syncthreads();
+      if (s_fbcnt[it % 3] >= need) T = cnd;
+      if (tid == 0) s_fbcnt[(it + 2) % 3] = 0;
+    }
+    for (int sg = 0; sg < nseg; ++sg) {
+      load(sg);
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int p = pos_of(sg, i);
+        const bool take = kk[i] && cid(i) == c && bin_of(kk[i], fmin, scale, NB) == bs &&
+                          key64(kk[i], p) >= T;
+        append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst, &s_ctot, lane);
+      }
+    }
+    __syncthreads();
+    if (tid == 0) { s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0; }
+    __syncthreads();
+  }
+  __syncthreads();
+
+  // ---- P6: order the chosen words by (cluster, position) and write the row
+  const int total = s_ctot;      // == sum_c t_c
+  int P = 1;
+  while (P < total) P <<= 1;
+  for (int i = total + tid; i < P; i += kThreads) s_cst[i] = 0xffffffffu;
+  __syncthreads();
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < P; i += kThreads) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint32_t x = s_cst[i], y = s_cst[ixj];
+          const bool up = (i & k) == 0;
+          if ((x > y) == up) { s_cst[i] = y; s_cst[ixj] = x; }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int sl = tid; sl < E; sl += kThreads) {
+    // cluster owning slot sl: the last c with base_c <= sl (bases are non-decreasing)
+    int lo = 0, hi = C - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_base[mid] <= sl) lo = mid; else hi = mid - 1;
+    }
+    const int r = sl - s_base[lo];
+    int v = -1;
+    if (sl < s_base[C] && r < s_t[lo]) v = (int)(s_cst[s_tpre[lo] + r] & 0xffffffu);
+    erow[sl] = v;
+  }
+}
+
+template <int PPT>
+int launch_row(const TopqArgs& a, int rows, size_t lds, hipStream_t s) {
+  const hipError_t e = hipFuncSetAttribute((const void*)topq_row_kernel<PPT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(topq_row_kernel<PPT>, dim3(rows), dim3(kThreads), lds, s, a);
+  return OA_LAUNCH_STATUS();
 }
 
 }  // namespace
 
 extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
                        const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
-                       const int* n_dev, uint64_t* cand, long cand_elems, void* stream) {
-  if (rows <= 0 || C <= 0 || C > kMaxC || E < 0 || E > kMaxE || Lmax <= 0) return OA_EINVAL;
-  const int nchunks = (Lmax + kChunk - 1) / kChunk;
-  if (!cand || cand_elems < (long)rows * nchunks * (E > 0 ? E : 1)) return OA_EINVAL;
+                       const int* n_dev, void* stream) {
+  const long lmax4 = ((long)Lmax + 3) & ~3L;
+  if (rows <= 0 || C <= 0 || C > kMaxC || E < 0 || E > kMaxE || Lmax <= 0 || Lmax > kMaxPos ||
+      !S || !asg8 || !quota || !n_dev || (E > 0 && !exp_idx) || s_stride % 4 || asg8_stride % 4 ||
+      s_stride < lmax4 || asg8_stride < lmax4 || (reinterpret_cast<uintptr_t>(S) & 15) ||
+      (reinterpret_cast<uintptr_t>(asg8) & 3))
+    return OA_EINVAL;
+  if (E == 0) return 0;
+  TopqArgs a;
+  a.S = S; a.s_stride = s_stride; a.asg8 = asg8; a.a_stride = asg8_stride; a.quota = quota;
+  a.C = C; a.E = E; a.n_dev = n_dev; a.exp_idx = exp_idx;
+  // bins per cluster: a power of two in [64, 256] with C * nb <= 16384
+  int nb = 256;
+  while (nb > 64 && C * nb > 16384) nb >>= 1;
+  a.nb = nb;
+  a.nb_shift = 0;
+  while ((1 << a.nb_shift) < nb) ++a.nb_shift;
+  a.cpow = 1;
+  while (a.cpow < E) a.cpow <<= 1;
+  const size_t static_lds = sizeof(int) * (16 * kMaxC + 8);
+  const size_t fixed = sizeof(uint32_t) * a.cpow + sizeof(int) * (size_t)C * nb;
+  const long room = (long)kLdsLimit - (long)static_lds - (long)fixed;
+  a.bcap = (int)std::min<long>(kBCapMax, room / 8);
+  if (a.bcap < 64) return OA_EINVAL;
+  const size_t lds = sizeof(unsigned long long) * a.bcap + fixed;
   hipStream_t s = (hipStream_t)stream;
-  if (E > 0) {
-    const size_t lds = chunk_lds_bytes(C, E);
-    if (lds > 65536) {
-      const hipError_t e = hipFuncSetAttribute((const void*)topq_chunk_kernel,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return (int)e;
-    }
-    hipLaunchKernelGGL(topq_chunk_kernel, dim3(nchunks, rows), dim3(kThreads), lds, s, S, s_stride,
-                       asg8, asg8_stride, quota, C, E, n_dev, (unsigned long long*)cand, nchunks);
-    const int st = OA_LAUNCH_STATUS();
-    if (st) return st;
-  }
-  hipLaunchKernelGGL(topq_merge_kernel, dim3(rows), dim3(kThreads), 0, s,
-                     (const unsigned long long*)cand, nchunks, quota, C, E, exp_idx);
-  return OA_LAUNCH_STATUS();
+  if (Lmax <= kThreads * 8) return launch_row<8>(a, rows, lds, s);
+  if (Lmax <= kThreads * 16) return launch_row<16>(a, rows, lds, s);
+  if (Lmax <= kThreads * 36) return launch_row<36>(a, rows, lds, s);
+  return launch_row<44>(a, rows, lds, s);
 }

@@ -100,7 +100,6 @@ class OursHIP(Method):
         self.n_t = torch.empty(R, self.Cn, **f32)
         self.quota = torch.empty(R, self.Cn, **f32)
         self.exp_idx = torch.empty(R, max(self.E, 1), **i32)
-        self.cand = ops.topq_workspace(R, Lmax, self.E, dev)
         self.out = torch.empty(R, D, device=dev, dtype=torch.bfloat16)
         self._sel = {}
         if not fused:
@@ -159,7 +158,7 @@ class OursHIP(Method):
         ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota,
                       SC, self.E)
         mark("gate_fill")
-        ops.topq(self.S, st.asg8, self.quota, self.exp_idx, C.n_dev, self.cand)
+        ops.topq(self.S, st.asg8, self.quota, self.exp_idx, C.n_dev)
         mark("topq")
         if self.fused:
             ops.residual_flash(qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk,

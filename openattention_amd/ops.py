@@ -206,25 +206,14 @@ def waterfill(score, n_t, quota, E: int) -> None:
     lib.call("oa_waterfill", _ptr(score), _ptr(n_t), R, C, int(E), _ptr(quota), _stream(dev))
 
 
-TOPQ_CHUNK = 8192
-
-
-def topq_workspace(rows: int, Lmax: int, E: int, dev) -> torch.Tensor:
-    """Candidate workspace of oa_topq: rows * ceil(Lmax/8192) * E 64-bit entries."""
-    return torch.empty(rows * (-(-Lmax // TOPQ_CHUNK)) * max(E, 1), device=dev, dtype=torch.int64)
-
-
-def topq(S, asg8, quota, exp_idx, n_dev, cand: torch.Tensor | None = None) -> torch.Tensor:
+def topq(S, asg8, quota, exp_idx, n_dev) -> None:
     """Within-cluster top-q (exp_idx segments grouped by cluster, position order inside)."""
     dev = _dev(S, asg8, quota, exp_idx, n_dev)
     R, C = quota.shape
     Lmax = asg8.shape[1]
     E = exp_idx.shape[1]
-    if cand is None:
-        cand = topq_workspace(R, Lmax, E, dev)
     lib.call("oa_topq", _ptr(S), S.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R, C, Lmax,
-             _ptr(exp_idx), E, _ptr(n_dev), _ptr(cand), cand.numel(), _stream(dev))
-    return cand
+             _ptr(exp_idx), E, _ptr(n_dev), _stream(dev))
 
 
 def residual(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n) -> None:

@@ -204,7 +204,8 @@ class LayerState:
         self.colmean = z(R, RC)
         self.cent = z(R, C, RC)
         self.asg = z(R, Lmax, dt=torch.int32)
-        self.asg8 = z(R, Lmax, dt=torch.uint8)
+        # byte ids are streamed four at a time: rows padded to a multiple of 64 entries
+        self.asg8 = z(R, -(-Lmax // 64) * 64, dt=torch.uint8)
         self.nb = z(R, C)
         self.Sk = z(R, C, D)
         self.Sk2 = z(R, C, D)

@@ -403,7 +403,10 @@ void oa_ref_topq(const float* S, int ncols, const int32_t* asg, int Lmax, const 
         keys[m++] = ((uint64_t)fkey(S[(long)r * ncols + i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
       }
       qsort(keys, (size_t)m, sizeof(uint64_t), cmp_desc_key);
-      const int take = qc < m ? qc : m;
+      /* the row holds E slots: a segment that would run past E keeps its best E - base members
+       * (the reference never overflows, as its water-filling keeps sum q <= E) */
+      int take = qc < m ? qc : m;
+      if (take > E - base) take = E - base > 0 ? E - base : 0;
       /* the chosen members, listed in position order */
       for (int j = 0; j < take; ++j) tmp[j] = (int32_t)(0xffffffffu - (uint32_t)(keys[j] & 0xffffffffu));
       for (int a = 1; a < take; ++a) {
@@ -412,7 +415,7 @@ void oa_ref_topq(const float* S, int ncols, const int32_t* asg, int Lmax, const 
         while (b >= 0 && tmp[b] > x) { tmp[b + 1] = tmp[b]; --b; }
         tmp[b + 1] = x;
       }
-      for (int j = 0; j < take && base + j < E; ++j) out[base + j] = tmp[j];
+      for (int j = 0; j < take; ++j) out[base + j] = tmp[j];
       base += qc;
     }
   }

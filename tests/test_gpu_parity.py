@@ -288,6 +288,39 @@ def test_topq_generated_list_overflow_fallback(lay4k):
     assert np.any((cnt > 1) & (quota > 0)), "no overflowed cluster was expanded"
 
 
+@pytest.mark.parametrize("n,C,E,seed", [(20000, 16, 300, 1), (8192, 4, 64, 2), (777, 8, 4096, 3)])
+def test_topq_adversarial_quotas(n, C, E, seed):
+    """Top-q on synthetic rows built to hit every branch: scores on a coarse grid (many ties,
+    broken by position), one cluster holding ~60% of the row (more than 1024 members per
+    8192-position chunk), quotas above the member count, quota sums above E (a segment cut at
+    E), a partial last chunk, and an output buffer holding stale values."""
+    print(f"[case] topq adversarial n={n} C={C} E={E}", flush=True)
+    rng = np.random.default_rng(seed)
+    R, Lmax = 6, -(-(n + 300) // 64) * 64     # row strides: multiples of 4 (oa_topq reads 4 at a time)
+    S = np.round(rng.standard_normal((R, Lmax)) * 4) / 4
+    S = S.astype(np.float32) + np.float32(0.0)     # no -0.0, as for exact integer scores
+    p = np.full(C, 0.4 / (C - 1))
+    p[0] = 0.6
+    asg = rng.choice(C, size=(R, Lmax), p=p).astype(np.int32)
+    asg[:, n:] = 0
+    ns = 16
+    sel = np.stack([rng.choice(n, ns, replace=False) for _ in range(R)]).astype(np.int32)
+    for r in range(R):
+        S[r, sel[r]] = -np.inf
+    quota = rng.integers(0, 2 * max(E // C, 1) + 3, size=(R, C)).astype(np.float32)
+    quota[0, 0] = min(E, 900)          # deep cluster-0 quota: streaming extraction
+    quota[1] = 0.0                     # a row with no quota at all
+    quota[2, C - 1] = 10 * n           # quota far above membership, past E
+    ref = O.topq(S, asg, sel, quota, n, E)
+    exp_idx = torch.full((R, E), 12345, device=DEV, dtype=torch.int32)
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    asg8 = torch.from_numpy(asg.astype(np.uint8)).to(DEV)
+    ops.topq(_f32(S), asg8, _f32(quota), exp_idx, n_dev)
+    torch.cuda.synchronize()
+    got = exp_idx.cpu().numpy()
+    assert np.array_equal(got, ref), f"rows differ: {np.nonzero((got != ref).any(1))[0]}"
+
+
 def test_dense_decode_vs_oracle(lay4k):
     print("[case] dense", flush=True)
     lay = lay4k

@@ -272,6 +272,33 @@ def test_topq_brute_force():
         assert np.all(ex[r, base:] == -1)
 
 
+def test_topq_overfull_quotas_brute_force():
+    """Quotas above the member count leave -1 in the rest of the segment; a quota sum above E
+    cuts the straddling segment to its best-scoring E - base members (in position order)."""
+    R, L, C, n, E = 3, 400, 6, 390, 50
+    S = np.round(RNG.normal(size=(R, L)) * 2).astype(np.float32) / 2    # many ties
+    S += np.float32(0.0)          # no -0.0: exact integer scores are never negative zero
+    asg = RNG.integers(0, C, size=(R, L)).astype(np.int32)
+    sel = np.stack([RNG.choice(n, 5, replace=False) for _ in range(R)]).astype(np.int32)
+    quota = RNG.integers(0, 25, size=(R, C)).astype(np.float32)
+    quota[:, 1] = 500.0                                   # far above any membership
+    S2 = S.copy()
+    for r in range(R):
+        S2[r, sel[r]] = -np.inf
+    ex = O.topq(S2, asg, sel, quota, n, E)
+    for r in range(R):
+        want_row = np.full(E, -1, np.int64)
+        base = 0
+        for c in range(C):
+            qc = int(quota[r, c])
+            mem = [i for i in range(n) if asg[r, i] == c and i not in set(sel[r].tolist())]
+            best = sorted(mem, key=lambda i: (-S[r, i], i))[:max(0, min(qc, E - base))]
+            for j, t in enumerate(sorted(best)):
+                want_row[base + j] = t
+            base += qc
+        assert np.array_equal(ex[r], want_row), r
+
+
 # ------------------------------------------------------------------ residual + merge
 def test_flash_closed_form_and_invariants():
     R, BH, L, NS, NE, NB = 8, 2, 300, 7, 20, 5
