@@ -4,7 +4,7 @@
 //   * head_dim D is 128 (Llama-3.1-8B shapes); the host entry points reject anything else.
 //   * one wavefront is 64 lanes; a "lane group" is 16 consecutive lanes.
 //   * all reductions that feed a discrete decision (top-k, quota, argmax) use a fixed
-//     butterfly order (xor 32,16,8,4,2,1 over the 64 lanes), so every lane ends with the
+//     butterfly order (xor 1,2,4,8,16,32 over the 64 lanes), so every lane ends with the
 //     same bits and the CPU restatement can replay the exact order.
 //   * the library is compiled with -ffp-contract=off: a fused multiply-add only happens
 //     where the source calls fmaf()/fma() explicitly.
@@ -43,26 +43,92 @@ __device__ __forceinline__ void unpack8(const uint4 w, float* x) {
 }
 
 // ---- butterfly reductions over the full wave (every lane gets the result) -------------------
+// Canonical order: the xor butterfly with m = 1, 2, 4, 8, 16, 32 (lane l adds the value of lane
+// l ^ m at each level).  Each level maps onto a cross-lane primitive that delivers exactly the
+// partner's value: quad_perm [1,0,3,2] (m=1) and [2,3,0,1] (m=2); row_half_mirror (m=4) and
+// row_mirror (m=8), whose sources lie in the partner's quad / 8-lane group, which is uniform by
+// then; v_permlane16_swap / v_permlane32_swap (m=16, 32), whose two results are the lane's own
+// value and its partner's.  Addition is commutative, so every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf,
+                                                    0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp((int)b, (int)b, CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp((int)(b >> 32), (int)(b >> 32), CTRL, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ float swap16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ double swap16_sum(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const auto lo = __builtin_amdgcn_permlane16_swap((unsigned)b, (unsigned)b, false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap((unsigned)(b >> 32), (unsigned)(b >> 32), false, false);
+  const double x = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0]));
+  const double y = __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+  return x + y;
+}
+__device__ __forceinline__ double swap32_sum(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const auto lo = __builtin_amdgcn_permlane32_swap((unsigned)b, (unsigned)b, false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap((unsigned)(b >> 32), (unsigned)(b >> 32), false, false);
+  const double x = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0]));
+  const double y = __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+  return x + y;
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-  return v;
+  v = v + dpp_f32<0xB1>(v);     // m = 1
+  v = v + dpp_f32<0x4E>(v);     // m = 2
+  v = v + dpp_f32<0x141>(v);    // m = 4
+  v = v + dpp_f32<0x140>(v);    // m = 8
+  v = swap16_sum(v);            // m = 16
+  return swap32_sum(v);         // m = 32
 }
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-  return v;
+  v = v + dpp_f64<0xB1>(v);
+  v = v + dpp_f64<0x4E>(v);
+  v = v + dpp_f64<0x141>(v);
+  v = v + dpp_f64<0x140>(v);
+  v = swap16_sum(v);
+  return swap32_sum(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
+  v += __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(v, v, 0x140, 0xf, 0xf, false);
+  const auto r16 = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  v = (int)(r16[0] + r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return (int)(r32[0] + r32[1]);
 }
+// sum inside each aligned 16-lane group (a DPP row), order m = 1, 2, 4, 8
+__device__ __forceinline__ float group16_sum(float v) {
+  v = v + dpp_f32<0xB1>(v);
+  v = v + dpp_f32<0x4E>(v);
+  v = v + dpp_f32<0x141>(v);
+  return v + dpp_f32<0x140>(v);
+}
+
 // ---- order-independent reductions on the DPP network (no LDS round trips) ------------------
 // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror fold each 16-lane row;
 // row_bcast15 (rows 1, 3) and row_bcast31 (rows 2, 3) fold the rows into lane 63, which is then
@@ -105,18 +171,10 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
   return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// reductions inside a 16-lane group
-__device__ __forceinline__ float group16_sum(float v) {
-  v = v + __shfl_xor(v, 8, 64);
-  v = v + __shfl_xor(v, 4, 64);
-  v = v + __shfl_xor(v, 2, 64);
-  v = v + __shfl_xor(v, 1, 64);
-  return v;
-}
 
 // Canonical 128-term fp32 dot product used wherever the result feeds a discrete decision:
 // lane l holds elements l and l+64; p_l = fma(a[l+64], b[l+64], a[l]*b[l]); then the wave
-// butterfly.  Every lane returns the same value.
+// butterfly (m = 1, 2, ..., 32).  Every lane returns the same value.
 __device__ __forceinline__ float dot128_canon(float a_lo, float b_lo, float a_hi, float b_hi) {
   float p = fmaf(a_hi, b_hi, a_lo * b_lo);
   return wave_sum(p);

@@ -18,7 +18,8 @@
 
 namespace {
 
-constexpr int kGateThreads = 256;
+constexpr int kGateThreads = 512;
+constexpr int kGateWaves = kGateThreads / 64;
 constexpr int kMaxSel = 64;
 constexpr int kMaxC = 256;
 
@@ -33,15 +34,16 @@ struct GateArgs {
   int C; float sc; float sc2;
 };
 
-// score of one cluster from its pooled sums (lane holds dims lane and lane+64)
-__device__ __forceinline__ void gate_cluster(const GateArgs& a, int c, float sk_lo, float sk_hi,
-                                             float s2_lo, float s2_hi, float nt, float q_lo,
-                                             float q_hi, float qq_lo, float qq_hi, const int* s_cid,
-                                             float (*s_k)[OA_D], int lane, float* score_out,
-                                             float* nt_out) {
+// the two wave-wide parts of one cluster's score (lane holds dims lane and lane+64): the tail
+// sums minus the selected tokens, then zbar = sc q.kbar and the raw sc2 (q*q).var
+__device__ __forceinline__ void gate_dots(const GateArgs& a, int c, float sk_lo, float sk_hi,
+                                          float s2_lo, float s2_hi, float nt, float q_lo,
+                                          float q_hi, float qq_lo, float qq_hi, const int* s_cid,
+                                          const float* s_k, int lane, float* zbar_out,
+                                          float* s2_out, float* nt_out) {
   for (int i = 0; i < a.n_sel; ++i) {
     if (s_cid[i] == c) {
-      const float k_lo = s_k[i][lane], k_hi = s_k[i][lane + 64];
+      const float k_lo = s_k[i * OA_D + lane], k_hi = s_k[i * OA_D + lane + 64];
       sk_lo = sk_lo - k_lo;
       sk_hi = sk_hi - k_hi;
       s2_lo = s2_lo - k_lo * k_lo;
@@ -54,22 +56,28 @@ __device__ __forceinline__ void gate_cluster(const GateArgs& a, int c, float sk_
   const float ks_lo = s2_lo / den, ks_hi = s2_hi / den;
   const float v_lo = fmaxf(ks_lo - kb_lo * kb_lo, 0.f);
   const float v_hi = fmaxf(ks_hi - kb_hi * kb_hi, 0.f);
-  const float zbar = a.sc * oa::dot128_canon(q_lo, kb_lo, q_hi, kb_hi);
-  float s2 = a.sc2 * oa::dot128_canon(qq_lo, v_lo, qq_hi, v_hi);
+  *zbar_out = a.sc * oa::dot128_canon(q_lo, kb_lo, q_hi, kb_hi);
+  *s2_out = a.sc2 * oa::dot128_canon(qq_lo, v_lo, qq_hi, v_hi);
+  *nt_out = nt;
+}
+
+// the scalar tail of one cluster's wl1 score
+__device__ __forceinline__ float gate_score(float zbar, float s2, float nt) {
   if (!(nt >= 2.0f)) s2 = 0.f;
   const float s2c = fmaxf(s2, 0.f);
   const float sig = sqrtf(s2c);
   const float er = oa::det_erff(sig * 0.70710677f);
   const float log_d = 0.5f * s2c + oa::det_logf(fmaxf(er, 1e-30f));
-  *score_out = (zbar + oa::det_logf(fmaxf(nt, 1.0f))) + log_d;
-  *nt_out = nt;
+  return (zbar + oa::det_logf(fmaxf(nt, 1.0f))) + log_d;
 }
 
-// ErrorGate of one row by a 256-thread workgroup; results to (score, n_t) rows (global or LDS)
-__device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* score_row,
-                                         float* nt_row) {
-  __shared__ float s_k[kMaxSel][OA_D];
+// ErrorGate of one row by a 512-thread workgroup into LDS rows (score, n_t).  The wave-wide dot
+// products run eight clusters per wave with all loads in flight; the scalar tails (erf, logs)
+// then run one cluster per thread.  Dynamic LDS: n_sel * 128 floats of selected keys.
+__device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_score, float* s_nt) {
+  extern __shared__ float s_k[];
   __shared__ int s_cid[kMaxSel];
+  __shared__ float s_zbar[kMaxC], s_s2[kMaxC];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -78,47 +86,64 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* scor
     const int tok = a.sel[(long)row * a.sel_stride + i];
     s_cid[i] = (tok >= 0) ? a.asg[(long)row * a.asg_stride + tok] : -1;
   }
-  for (int e = tid; e < a.n_sel * OA_D; e += kGateThreads) {
-    const int i = e / OA_D, d = e % OA_D;
+  for (int e = tid; e < a.n_sel * (OA_D / 8); e += kGateThreads) {
+    const int i = e / (OA_D / 8), d8 = (e % (OA_D / 8)) * 8;
     const int tok = a.sel[(long)row * a.sel_stride + i];
-    s_k[i][d] = (tok >= 0) ? oa::bf16_to_f32(a.K[(long)kvr * a.k_sb + (long)tok * a.k_ss + d]) : 0.f;
+    float x[8];
+    if (tok >= 0) {
+      oa::unpack8(*reinterpret_cast<const uint4*>(a.K + (long)kvr * a.k_sb + (long)tok * a.k_ss + d8), x);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_k[i * OA_D + d8 + j] = x[j];
   }
   __syncthreads();
   const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
   const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
   const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
   constexpr int kBatch = 8;
-  constexpr int kWaves = kGateThreads / 64;
-  for (int c0 = wave; c0 < a.C; c0 += kWaves * kBatch) {
+  for (int c0 = wave; c0 < a.C; c0 += kGateWaves * kBatch) {
     float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {          // the batch's statistics, all loads in flight
-      const int c = c0 + kWaves * i;
-      const long base = (long)row * a.st_stride_r + (long)(c < a.C ? c : 0) * OA_D;
+      const int c = min(c0 + kGateWaves * i, a.C - 1);
+      const long base = (long)row * a.st_stride_r + (long)c * OA_D;
       sk[i][0] = a.Sk[base + lane];
       sk[i][1] = a.Sk[base + lane + 64];
       s2[i][0] = a.Sk2[base + lane];
       s2[i][1] = a.Sk2[base + lane + 64];
-      nbv[i] = a.nb[(long)row * a.nb_stride + (c < a.C ? c : 0)];
+      nbv[i] = a.nb[(long)row * a.nb_stride + c];
     }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      const int c = c0 + kWaves * i;
-      if (c >= a.C) break;
-      float sc, nt;
-      gate_cluster(a, c, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
-                   s_cid, s_k, lane, &sc, &nt);
-      if (lane == 0) {
-        score_row[c] = sc;
-        nt_row[c] = nt;
+      const int c = c0 + kGateWaves * i;
+      if (c < a.C) {
+        float zb, sv, nt;
+        gate_dots(a, c, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
+                  s_cid, s_k, lane, &zb, &sv, &nt);
+        if (lane == 0) {
+          s_zbar[c] = zb;
+          s_s2[c] = sv;
+          s_nt[c] = nt;
+        }
       }
     }
   }
+  __syncthreads();
+  for (int c = tid; c < a.C; c += kGateThreads) s_score[c] = gate_score(s_zbar[c], s_s2[c], s_nt[c]);
+  __syncthreads();
 }
 
 __global__ void __launch_bounds__(kGateThreads) errorgate_kernel(GateArgs a) {
+  __shared__ float s_score[kMaxC], s_nt[kMaxC];
   const int row = blockIdx.x;
-  gate_row(a, row, a.score + (long)row * a.out_stride, a.n_t + (long)row * a.out_stride);
+  gate_row(a, row, s_score, s_nt);
+  for (int c = threadIdx.x; c < a.C; c += kGateThreads) {
+    a.score[(long)row * a.out_stride + c] = s_score[c];
+    a.n_t[(long)row * a.out_stride + c] = s_nt[c];
+  }
 }
 
 // one wave per row; cluster c lives in lane c % 64, slot c / 64
@@ -133,6 +158,22 @@ __device__ __forceinline__ double canon_sum(const double* x, int C, int lane) {
     }
   }
   return oa::wave_sum(p);
+}
+
+__device__ __forceinline__ double wave_max_f64(double v) {
+#pragma unroll
+  for (int m = 1; m <= 32; m <<= 1) v = fmax(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// f(mid) = sum_b min(cap_b, exp(mid) w_b) in the canonical order
+__device__ __forceinline__ double fill_at(double mid, const double* cap, const double* w, int C,
+                                          int lane) {
+  const double em = oa::det_exp(mid);
+  double part[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) part[j] = fmin(cap[j], em * w[j]);
+  return canon_sum(part, C, lane);
 }
 
 // water-filling of one row by one wave (lane = threadIdx.x % 64); score/n_t rows may be in LDS
@@ -156,8 +197,7 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
       smax = fmax(smax, sv[j]);
     }
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) smax = fmax(smax, __shfl_xor(smax, m, 64));
+  smax = wave_max_f64(smax);
   if (!(smax > NEG && smax < -NEG)) smax = 0.0;
   double rmax = 0.0;
   for (int j = 0; j < 4; ++j) {
@@ -165,18 +205,27 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
     double ratio = (w[j] > 0.0) ? cap[j] / fmax(w[j], 1e-300) : 0.0;
     if (lane + 64 * j < C) rmax = fmax(rmax, ratio);
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) rmax = fmax(rmax, __shfl_xor(rmax, m, 64));
+  rmax = wave_max_f64(rmax);
   const double tot = canon_sum(cap, C, lane);
   double lo = -3.0 * 2.302585092994046;
   double hi = oa::det_log(fmax(rmax, 1e-3)) + 1.0;
-  for (int it = 0; it < 64; ++it) {
+  // 64 bisection steps, two per iteration: the step after mid probes 0.5*(lo+mid) or
+  // 0.5*(mid+hi), both evaluated beside mid, so the sequence of (lo, hi) is that of 64 single
+  // steps
+  for (int it = 0; it < 32; ++it) {
     const double mid = 0.5 * (lo + hi);
-    const double em = oa::det_exp(mid);
-    double part[4];
-    for (int j = 0; j < 4; ++j) part[j] = fmin(cap[j], em * w[j]);
-    const double f = canon_sum(part, C, lane);
-    if (f > budget) hi = mid; else lo = mid;
+    const double m_lo = 0.5 * (lo + mid);
+    const double m_hi = 0.5 * (mid + hi);
+    const double f = fill_at(mid, cap, w, C, lane);
+    const double f_lo = fill_at(m_lo, cap, w, C, lane);
+    const double f_hi = fill_at(m_hi, cap, w, C, lane);
+    if (f > budget) {
+      hi = mid;
+      if (f_lo > budget) hi = m_lo; else lo = m_lo;
+    } else {
+      lo = mid;
+      if (f_hi > budget) hi = m_hi; else lo = m_hi;
+    }
   }
   const double el = oa::det_exp(lo);
   for (int j = 0; j < 4; ++j) {
@@ -235,7 +284,6 @@ __global__ void __launch_bounds__(kGateThreads) gate_fill_kernel(GateArgs a, flo
   __shared__ int s_room[kMaxC];
   const int row = blockIdx.x;
   gate_row(a, row, s_score, s_nt);
-  __syncthreads();
   for (int c = threadIdx.x; c < a.C; c += kGateThreads) {
     a.score[(long)row * a.out_stride + c] = s_score[c];
     a.n_t[(long)row * a.out_stride + c] = s_nt[c];
@@ -254,7 +302,8 @@ extern "C" int oa_errorgate(const void* q, long q_stride, const void* K, long k_
                             float sm_scale, float sm_scale_sq, float* score, float* n_t,
                             void* stream) {
   if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || n_sel < 0 || n_sel > kMaxSel ||
-      C <= 0)
+      C <= 0 || C > kMaxC || k_stride_b % 8 || k_stride_s % 8 ||
+      (reinterpret_cast<uintptr_t>(K) & 15))
     return OA_EINVAL;
   GateArgs a;
   a.q = (const uint16_t*)q; a.q_stride = q_stride;
@@ -266,7 +315,8 @@ extern "C" int oa_errorgate(const void* q, long q_stride, const void* K, long k_
   a.score = score; a.n_t = n_t; a.out_stride = C;
   a.C = C; a.sc = sm_scale;
   a.sc2 = sm_scale_sq;
-  hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads),
+                     sizeof(float) * (size_t)n_sel * OA_D, (hipStream_t)stream, a);
   return OA_LAUNCH_STATUS();
 }
 
@@ -277,7 +327,8 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
                             float sm_scale, float sm_scale_sq, int budget, float* score, float* n_t,
                             float* quota, void* stream) {
   if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || n_sel < 0 || n_sel > kMaxSel ||
-      C <= 0 || C > kMaxC || budget < 0)
+      C <= 0 || C > kMaxC || budget < 0 || k_stride_b % 8 || k_stride_s % 8 ||
+      (reinterpret_cast<uintptr_t>(K) & 15))
     return OA_EINVAL;
   GateArgs a;
   a.q = (const uint16_t*)q; a.q_stride = q_stride;
@@ -288,8 +339,9 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
   a.nb = nb; a.nb_stride = C;
   a.score = score; a.n_t = n_t; a.out_stride = C;
   a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
-  hipLaunchKernelGGL(gate_fill_kernel, dim3(rows), dim3(kGateThreads), 0, (hipStream_t)stream, a,
-                     quota, (double)budget);
+  hipLaunchKernelGGL(gate_fill_kernel, dim3(rows), dim3(kGateThreads),
+                     sizeof(float) * (size_t)n_sel * OA_D, (hipStream_t)stream, a, quota,
+                     (double)budget);
   return OA_LAUNCH_STATUS();
 }
 

@@ -54,22 +54,22 @@ static uint32_t fkey(float s) {
 }
 
 /* fixed-order 128-term dot product: p_l = fma(a[l+64], b[l+64], a[l]*b[l]), then the xor
- * butterfly over 64 partials (m = 32, 16, ..., 1).  Same order as the device helper. */
+ * butterfly over 64 partials (m = 1, 2, ..., 32).  Same order as the device helper. */
 static float dot128_canon(const float* a, const float* b) {
   float p[64], t[64];
   for (int l = 0; l < 64; ++l) p[l] = fmaf(a[l + 64], b[l + 64], a[l] * b[l]);
-  for (int m = 32; m >= 1; m >>= 1) {
+  for (int m = 1; m <= 32; m <<= 1) {
     for (int l = 0; l < 64; ++l) t[l] = p[l] + p[l ^ m];
     memcpy(p, t, sizeof p);
   }
   return p[0];
 }
 
-/* butterfly sum of 64 double partials */
+/* butterfly sum of 64 double partials (m = 1, 2, ..., 32) */
 static double bfly64(const double* x) {
   double p[64], t[64];
   memcpy(p, x, sizeof p);
-  for (int m = 32; m >= 1; m >>= 1) {
+  for (int m = 1; m <= 32; m <<= 1) {
     for (int l = 0; l < 64; ++l) t[l] = p[l] + p[l ^ m];
     memcpy(p, t, sizeof p);
   }
