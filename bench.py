@@ -47,11 +47,46 @@ def parse():
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a hipGraph")
     p.add_argument("--cpu-reps", type=int, default=3)
+    p.add_argument("--pmc-calibration", action="store_true",
+                   help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
     return p.parse_args()
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+# kernel function names of the stage labels (as rocprofv3 prints them)
+KERNELS = {"index_update": "index_update_kernel", "qgs_prep": "qgs_prep_kernel",
+           "qgs_scan": "qgs_scan_kernel", "topk_select": "topk_select_kernel",
+           "gate_fill": "gate_fill_kernel", "topq": "topq_row_kernel",
+           "residual_flash": "residual_kernel"}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+
+
+def traffic_bytes(stage: str):
+    """HBM bytes per launch of a stage kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration factor), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        k = t["kernels"][KERNELS[stage]]
+        return int(round(k["fetch_kib"] * 1024 / t["fetch_factor"] + k["write_kib"] * 1024 / t["write_factor"]))
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None
+
+
+def pmc_calibration():
+    """A plain device copy of known size (1 GiB read, 1 GiB written) for scaling the
+    FETCH_SIZE / WRITE_SIZE counters: run under rocprofv3 --pmc."""
+    import torch
+    src = torch.empty(1 << 28, device="cuda:0", dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": src.numel() * 4,
+                      "bytes_written": dst.numel() * 4, "launches": 5}), flush=True)
 
 
 def main():
@@ -60,6 +95,9 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): the sparse decode "
               "stage needs no collective and this build measures one GPU's share", flush=True)
         sys.exit(2)
+    if a.pmc_calibration:
+        pmc_calibration()
+        return
     import numpy as np
     import torch
 
@@ -160,24 +198,30 @@ def main():
     stage_us = {k: statistics.median(v) for k, v in per.items()}
     log("[bench] stages (us): " + ", ".join(f"{k} {v:.1f}" for k, v in stage_us.items()))
 
-    # ---- algorithmic bytes (SURVEY 8d formula) per kernel and for the stage
+    # ---- algorithmic bytes per launch of every stage kernel, and of the stage as a whole
+    # (stage: int8 codes + bf16 K,V of the exact set + fp32 Sk, Sk2, Sv and n, each read once)
     R, Cn, E = B * HQ, m.Cn, m.E
     NSX = ns + nl + k_top
     n_mid = N + a.warmup
     alg = {
-        "qgs_scan": B * HKV * n_mid * 32,
-        "errorgate": R * Cn * (2 * D * 4 + 4),
-        "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * 2 * D * 4,
+        # K, V row at n-1 per KV row; U (128x32 f32) per KV row; W (128x16 bf16), cent, colmean
+        # per query row; read-modify-write of Sk, Sk2, Sv rows and n of one cluster
+        "index_update": B * HKV * (2 * D * 2 + D * 32 * 4 + 32) + R * (D * 16 * 2 + Cn * 16 * 4 + 64
+                                                                      + 2 * (3 * D * 4 + 4)),
+        "qgs_prep": R * D * 2 + B * HKV * (D * 32 * 4 + 32 * 4) + B * HKV * 16 * 32,
+        "qgs_scan": B * HKV * n_mid * 32,                      # int8 codes
+        "topk_select": R * (-(-n_mid // 64)) * 4 + R * NSX * 4,  # tile maxima, sel out
+        "gate_fill": R * Cn * (2 * D * 4 + 4) + R * NSX * D * 2,  # Sk, Sk2, n; K of sel
+        "topq": R * n_mid * (4 + 1) + R * E * 4,               # fp32 scores + byte ids; exp out
+        "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * 2 * D * 4,  # K,V exact set; Sk, Sv
     }
     stage_alg = B * HKV * n_mid * 32 + R * (NSX + E) * 2 * D * 2 + R * Cn * (3 * D * 4 + 4)
-    dom = max(stage_us, key=lambda k: stage_us[k])
-    dom_bytes = alg.get(dom)
-    roof_kernel = dom if dom_bytes is not None else "qgs_scan"
+    roof_kernel = max(stage_us, key=lambda k: stage_us[k])
     dom_bytes = alg[roof_kernel]
     achieved = dom_bytes / (stage_us[roof_kernel] * 1e-6) / 1e9
     roofline = {"kernel": roof_kernel, "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
-                "traffic": None, "bytes_per_launch": dom_bytes,
+                "traffic": traffic_bytes(roof_kernel), "bytes_per_launch": dom_bytes,
                 "avg_launch_us": round(stage_us[roof_kernel], 2)}
     stage_gbps = stage_alg / (us_layer * 1e-6) / 1e9
 

@@ -299,6 +299,76 @@ def test_topq_overfull_quotas_brute_force():
         assert np.array_equal(ex[r], want_row), r
 
 
+# ------------------------------------------------------------------ index update
+def test_index_update_closed_form():
+    """ours_graph.py:43-90 / multibin.py:2062-2096: code = clamp(rint(k.U_r / scale_r), +-127)
+    on the KV row, cluster = argmax_c (bf16(k.W) - colmean).c - |c|^2/2 per query row, then
+    n, Sk, Sk2, Sv += (1, k, k*k, v) in fp32 and the position joins the cluster's list.
+    Checked in fp64; codes within 1e-4 of a rounding boundary and rows whose best two
+    distances are within 1e-3 are skipped (the restatement's fp32 order decides those)."""
+    rng = np.random.default_rng(77)
+    BH, G, C, L, pos, rmax = 3, 4, 12, 40, 17, 3
+    R = BH * G
+    K = f32_to_bf16(rng.normal(size=(BH, L, 128)).astype(np.float32))
+    V = f32_to_bf16(rng.normal(size=(BH, L, 128)).astype(np.float32))
+    U = rng.normal(size=(BH, 128, 32)).astype(np.float32) / 8
+    scale = rng.uniform(0.02, 0.2, size=(BH, 32)).astype(np.float32)
+    W = f32_to_bf16((rng.normal(size=(R, 128, 16)) / 8).astype(np.float32))
+    colmean = rng.normal(size=(R, 16)).astype(np.float32) * 0.1
+    cent = rng.normal(size=(R, C, 16)).astype(np.float32)
+    st = {"K": K, "V": V, "U": U, "scale": scale, "W": W, "colmean": colmean, "cent": cent,
+          "codes": np.zeros((BH, L, 32), np.int8), "asg": np.full((R, L), -5, np.int32),
+          "nb": rng.integers(0, 9, size=(R, C)).astype(np.float32),
+          "Sk": rng.normal(size=(R, C, 128)).astype(np.float32),
+          "Sk2": rng.uniform(0, 3, size=(R, C, 128)).astype(np.float32),
+          "Sv": rng.normal(size=(R, C, 128)).astype(np.float32),
+          "reclist": np.full((R, C, rmax), -7, np.int32),
+          "reccnt": rng.integers(0, rmax + 2, size=(R, C)).astype(np.int32)}
+    pre = {k: v.copy() for k, v in st.items()}
+    O.index_update(st, pos, G, rmax)
+    kf = bf16_to_f32(K).astype(np.float64)
+    vf = bf16_to_f32(V).astype(np.float64)
+    checked_codes = 0
+    for b in range(BH):
+        z = (kf[b, pos] @ U[b].astype(np.float64)) / scale[b].astype(np.float64)
+        want = np.clip(np.rint(z), -127, 127)
+        ok = np.abs(np.abs(z - np.floor(z)) - 0.5) > 1e-4
+        assert np.array_equal(st["codes"][b, pos][ok], want[ok].astype(np.int8))
+        checked_codes += ok.sum()
+        others = np.delete(np.arange(L), pos)
+        assert not st["codes"][b, others].any()
+    assert checked_codes > 0.9 * BH * 32
+    checked_rows = 0
+    for r in range(R):
+        kvr = r // G
+        zp = bf16_to_f32(f32_to_bf16((kf[kvr, pos] @ bf16_to_f32(W[r]).astype(np.float64)).astype(np.float32)))
+        zp = zp.astype(np.float64) - colmean[r]
+        cc = cent[r].astype(np.float64)
+        dist = cc @ zp - 0.5 * (cc * cc).sum(1)
+        order = np.argsort(-dist)
+        c = int(st["asg"][r, pos])
+        if dist[order[0]] - dist[order[1]] > 1e-3:
+            assert c == order[0], (r, c, order[:2])
+            checked_rows += 1
+        # the chosen cluster's statistics and list; every other cluster untouched
+        assert st["nb"][r, c] == pre["nb"][r, c] + 1
+        assert np.array_equal(st["Sk"][r, c], pre["Sk"][r, c] + bf16_to_f32(K[kvr, pos]))
+        kk = bf16_to_f32(K[kvr, pos])
+        assert np.array_equal(st["Sk2"][r, c], pre["Sk2"][r, c] + kk * kk)
+        assert np.array_equal(st["Sv"][r, c], pre["Sv"][r, c] + bf16_to_f32(V[kvr, pos]))
+        cnt = pre["reccnt"][r, c]
+        assert st["reccnt"][r, c] == cnt + 1
+        if cnt < rmax:
+            assert st["reclist"][r, c, cnt] == pos
+        mask = np.ones(C, bool)
+        mask[c] = False
+        for f in ("nb", "Sk", "Sk2", "Sv", "reccnt", "reclist"):
+            assert np.array_equal(st[f][r][mask], pre[f][r][mask]), f
+        assert np.array_equal(np.delete(st["asg"][r], pos), np.delete(pre["asg"][r], pos))
+    assert checked_rows >= R - 1
+    del vf
+
+
 # ------------------------------------------------------------------ residual + merge
 def test_flash_closed_form_and_invariants():
     R, BH, L, NS, NE, NB = 8, 2, 300, 7, 20, 5
