@@ -145,7 +145,7 @@ int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, l
  * of gathering member scores through the CSR lists, one workgroup streams each row once
  * (scores S from oa_topk_select, byte cluster ids asg8) and selects by per-cluster histogram
  * thresholds.
- *   quota (rows, C) fp32; exp_idx (rows, E) int32.  E <= 4096, C <= 256, Lmax <= 2^24.
+ *   quota (rows, C) fp32; exp_idx (rows, E) int32.  E <= 4096, C <= 256, Lmax < 2^24.
  */
 int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
             const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,

@@ -182,8 +182,9 @@ __device__ __forceinline__ float dot128_canon(float a_lo, float b_lo, float a_hi
 
 // order-preserving uint32 image of a float (larger float -> larger key, -inf lowest)
 __device__ __forceinline__ uint32_t float_key(float s) {
-  uint32_t b = __float_as_uint(s);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  const uint32_t b = __float_as_uint(s);
+  // negative: flip every bit; non-negative: set the sign bit
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
 }
 
 }  // namespace oa

@@ -9,15 +9,22 @@
 // Softmax merge (multibin.py:2727-2747): one softmax over {selected} U {expanded} U {proxies},
 // proxy logit s q.kbar'_c + ln n'_c.
 //
-// gfx950 decomposition: one 256-thread workgroup per query-head row, 16 lane groups of 16
-// lanes; a lane holds 8 of the 128 dims, so a K or V row is one 16-byte load per lane.  Lane
-// group g owns clusters g, g+16, ...: it walks the cluster's selected tokens and its own
-// contiguous segment of exp_idx (the top-q kernel writes segments grouped by cluster), four
-// tokens in flight, accumulating the residual sums in registers while folding the same K,V
-// rows into the group's online softmax, then folds the cluster's proxy.  Every K/V row and
-// every statistics row is read once, the sums are owned by one lane group (no atomics,
-// run-to-run deterministic) and the proxies never leave registers.  The 16 group softmax
-// states are merged in a fixed order at the end.
+// Fused kernel (oa_residual_flash), gfx950 decomposition.  The proxy logit needs only
+//   q.kbar'_c = (q.Sk_c - sum_{read i in c} q.k_i) / max(n'_c, 1),
+// scalars the softmax computes anyway, and the merged numerator regroups as
+//   sum_i (p_i - w_c(i) / den_c(i)) v_i + sum_c (w_c / den_c) Sv_c
+// (w_c the proxy weight, den_c = max(n'_c, 1)), so no per-cluster vector sums are formed.
+// One 512-thread workgroup per query-head row, 32 lane groups of 16 lanes (8 dims per lane):
+//   pass 1  every read token's q.k and every cluster's q.Sk as independent units, spread
+//           round-robin over the lane groups, eight loads in flight per group; the first
+//           batch of pass-2 rows is issued before the scalar phase and lands during it;
+//   scalars one thread per cluster sums its read tokens' dots in list order (selected tokens,
+//           then its exp_idx segment), forms the proxy logit; block max and weights;
+//   pass 2  every read token's V row and every cluster's Sv row scaled by its coefficient,
+//           accumulated per lane group and reduced over the groups in a fixed order.
+// Every K/V and statistics row is read once; all sums have a fixed order (deterministic).
+// exp_idx must list each cluster's tokens inside that cluster's quota segment (an expanded
+// token's cluster is the owner of its slot), which is the layout oa_topq writes.
 //
 // oa_residual writes kbar', vbar' (bf16) and ln n' instead of the softmax (the operator
 // surface of the reference's residual kernels), for use with oa_flash_decode.
@@ -226,6 +233,290 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(ResArgs a) {
   }
 }
 
+constexpr int kRFThreads = 512;
+constexpr int kRFGroups = kRFThreads / 16;
+constexpr int kRFWaves = kRFThreads / 64;
+constexpr int kBatch = 8;
+
+// fixed-order sum / max over the workgroup (thread partials -> wave butterfly -> waves in order)
+__device__ __forceinline__ float block_sum(float v, float* s_red, int tid) {
+  v = oa::wave_sum(v);
+  __syncthreads();
+  if ((tid & 63) == 0) s_red[tid >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRFWaves; ++w) t += s_red[w];
+  return t;
+}
+__device__ __forceinline__ float block_max(float v, float* s_red, int tid) {
+  v = oa::wave_max(v);
+  __syncthreads();
+  if ((tid & 63) == 0) s_red[tid >> 6] = v;
+  __syncthreads();
+  float t = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kRFWaves; ++w) t = fmaxf(t, s_red[w]);
+  return t;
+}
+
+__global__ void __launch_bounds__(kRFThreads) resflash_kernel(ResArgs a) {
+  extern __shared__ int dyn_rf[];
+  __shared__ int s_base[kMaxC + 1];
+  __shared__ int s_q[kMaxC];
+  __shared__ float s_nt[kMaxC];
+  __shared__ float s_qsk[kMaxC], s_l2[kMaxC], s_cw[kMaxC];
+  __shared__ float s_red[kRFWaves];
+  __shared__ float s_acc[kRFGroups][OA_D];
+  const int NI = a.n_sel + a.E;
+  int* s_tok = dyn_rf;                                        // NI
+  int* s_cid = s_tok + NI;                                    // NI
+  float* s_z = reinterpret_cast<float*>(s_cid + NI);          // NI: q.k, later the coefficient
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int grp = tid >> 4;
+  const int sub = tid & 15;
+  const int d0 = sub * 8;
+  const int C = a.C;
+  const int kvr = row / a.G;
+  const uint16_t* Kb = a.K + (long)kvr * a.kv_sb + d0;
+  const uint16_t* Vb = a.V + (long)kvr * a.kv_sb + d0;
+
+  // ---- phase 0: read lists, quota segments and tail counts (one round of loads: every
+  // thread issues its first quota, tail-count and list loads before using any of them)
+  int qv4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qv4[i] = (int)a.quota[(long)row * C + min((tid & 63) * 4 + i, C - 1)];
+  const float ntv = a.n_t[(long)row * C + min(tid, C - 1)];
+  int tok0 = -1;
+  if (NI > 0) {
+    const int i = min(tid, NI - 1);
+    tok0 = i < a.n_sel ? a.sel[(long)row * a.sel_stride + i] : a.exq[(long)row * a.E + (i - a.n_sel)];
+  }
+  if (tid < 64) {
+    int loc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qv4[i] = tid * 4 + i < C ? qv4[i] : 0;
+      loc += qv4[i];
+    }
+    int incl = loc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += t;
+    }
+    int run = incl - loc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid * 4 + i;
+      if (c < C) { s_q[c] = qv4[i]; s_base[c] = run; }
+      run += qv4[i];
+    }
+  }
+  if (tid < C) s_nt[tid] = ntv;
+  for (int c = tid + kRFThreads; c < C; c += kRFThreads) s_nt[c] = a.n_t[(long)row * C + c];
+  if (tid < NI) s_tok[tid] = tok0;
+  for (int i = tid + kRFThreads; i < NI; i += kRFThreads) {
+    const int tok = i < a.n_sel ? a.sel[(long)row * a.sel_stride + i]
+                                : a.exq[(long)row * a.E + (i - a.n_sel)];
+    s_tok[i] = tok;
+  }
+  float qv[8];
+  oa::unpack8(*reinterpret_cast<const uint4*>(a.q + (long)row * a.q_stride + d0), qv);
+  __syncthreads();
+
+  // ---- pass 1: q.k of every read token, q.Sk of every cluster; cluster ids of the read
+  // tokens (expanded tokens: the owner of their quota segment; selected tokens: asg).  The
+  // first batch of every stream is issued before any of them is used.
+  auto load_k = [&](int u0, uint4* w) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int u = min(u0 + j * kRFGroups, NI - 1);
+      const int tok = max(s_tok[u], 0);
+      w[j] = *reinterpret_cast<const uint4*>(Kb + (long)tok * a.kv_ss);
+    }
+  };
+  auto load_stat = [&](const float* base, int c0, float4 (*x)[2]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = min(c0 + j * kRFGroups, C - 1);
+      const float* p = base + ((long)row * C + c) * OA_D + d0;
+      x[j][0] = *reinterpret_cast<const float4*>(p);
+      x[j][1] = *reinterpret_cast<const float4*>(p + 4);
+    }
+  };
+  auto dots_k = [&](int u0, const uint4* w) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int u = u0 + j * kRFGroups;
+      float kx[8];
+      oa::unpack8(w[j], kx);
+      const float z = oa::group16_sum(dot8(qv, kx));
+      if (u < NI && sub == 0) s_z[u] = z;
+    }
+  };
+  auto dots_sk = [&](int c0, float4 (*x)[2]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = c0 + j * kRFGroups;
+      const float sk[8] = {x[j][0].x, x[j][0].y, x[j][0].z, x[j][0].w,
+                           x[j][1].x, x[j][1].y, x[j][1].z, x[j][1].w};
+      const float z = oa::group16_sum(dot8(qv, sk));
+      if (c < C && sub == 0) s_qsk[c] = z;
+    }
+  };
+  float4 skx[4][2];
+  uint4 kw[kBatch];
+  load_stat(a.Sk, grp, skx);
+  if (NI > 0) load_k(grp, kw);
+  int scid = -1;
+  const int stok = a.n_sel > 0 ? s_tok[min(tid, a.n_sel - 1)] : -1;
+  if (a.n_sel > 0) {
+    const int c = a.asg[(long)row * a.asg_stride + max(stok, 0)];
+    scid = stok >= 0 ? c : -1;
+  }
+  for (int i = tid; i < NI; i += kRFThreads) {
+    if (i < a.n_sel) continue;
+    int c = -1;
+    if (s_tok[i] >= 0) {
+      const int j = i - a.n_sel;
+      int lo = 0, hi = C - 1;                    // last cluster with base <= j
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_base[mid] <= j) lo = mid; else hi = mid - 1;
+      }
+      c = lo;
+    }
+    s_cid[i] = c;
+  }
+  if (tid < a.n_sel) s_cid[tid] = scid;
+  if (NI > 0) dots_k(grp, kw);
+  for (int u0 = grp + kRFGroups * kBatch; u0 < NI; u0 += kRFGroups * kBatch) {
+    load_k(u0, kw);
+    dots_k(u0, kw);
+  }
+  dots_sk(grp, skx);
+  for (int c0 = grp + kRFGroups * 4; c0 < C; c0 += kRFGroups * 4) {
+    load_stat(a.Sk, c0, skx);
+    dots_sk(c0, skx);
+  }
+  // first batch of pass 2, in flight through the scalar phase
+  uint4 vpre[kBatch];
+  float4 spre[4][2];
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) {
+    const int u = min(grp + j * kRFGroups, max(NI - 1, 0));
+    const int tok = NI > 0 ? max(s_tok[u], 0) : 0;
+    vpre[j] = *reinterpret_cast<const uint4*>(Vb + (long)tok * a.kv_ss);
+  }
+  load_stat(a.Sv, grp, spre);
+  __syncthreads();
+
+  // ---- scalars: proxy logits (log2 units), block max, weights, coefficients
+  const float zs = a.sm_scale * kLog2e;
+  for (int c = tid; c < C; c += kRFThreads) {
+    float Z = 0.f;
+    for (int i = 0; i < a.n_sel; ++i)
+      if (s_cid[i] == c) Z += s_z[i];
+    const int b1 = min(s_base[c] + s_q[c], a.E);
+    for (int j = s_base[c]; j < b1; ++j) {
+      const int i = a.n_sel + j;
+      if (s_cid[i] == c) Z += s_z[i];
+    }
+    const float nr = s_nt[c] - (float)s_q[c];
+    const float den = fmaxf(nr, 1.0f);
+    const bool live = nr > 0.5f;
+    s_l2[c] = live ? (((s_qsk[c] - Z) / den) * a.sm_scale + logf(den)) * kLog2e : -INFINITY;
+    s_cw[c] = den;
+  }
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int i = tid; i < NI; i += kRFThreads)
+    if (s_cid[i] >= 0) mx = fmaxf(mx, s_z[i] * zs);
+  for (int c = tid; c < C; c += kRFThreads) mx = fmaxf(mx, s_l2[c]);
+  const float M = block_max(mx, s_red, tid);
+  float lsum = 0.f;
+  for (int c = tid; c < C; c += kRFThreads) {
+    const float wc = M > -INFINITY && s_l2[c] > -INFINITY ? exp2f(s_l2[c] - M) : 0.f;
+    lsum += wc;
+    s_cw[c] = wc / s_cw[c];                 // w_c / den_c (0 for a dead proxy)
+  }
+  __syncthreads();
+  for (int i = tid; i < NI; i += kRFThreads) {
+    const int c = s_cid[i];
+    float coef = 0.f;
+    if (c >= 0) {
+      const float p = exp2f(s_z[i] * zs - M);
+      lsum += p;
+      coef = p - s_cw[c];
+    }
+    s_z[i] = coef;
+  }
+  const float L = block_sum(lsum, s_red, tid);   // its barriers also publish s_z
+
+  // ---- pass 2: coefficient-weighted V rows and Sv rows
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int u0 = grp; u0 < NI; u0 += kRFGroups * kBatch) {
+    uint4 w[kBatch];
+    if (u0 == grp) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) w[j] = vpre[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int u = min(u0 + j * kRFGroups, NI - 1);
+        const int tok = max(s_tok[u], 0);
+        w[j] = *reinterpret_cast<const uint4*>(Vb + (long)tok * a.kv_ss);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int u = u0 + j * kRFGroups;
+      const float cf = u < NI ? s_z[u] : 0.f;
+      float vx[8];
+      oa::unpack8(w[j], vx);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(cf, vx[e], acc[e]);
+    }
+  }
+  for (int c0 = grp; c0 < C; c0 += kRFGroups * 4) {
+    float4 x[4][2];
+    if (c0 == grp) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { x[j][0] = spre[j][0]; x[j][1] = spre[j][1]; }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = min(c0 + j * kRFGroups, C - 1);
+        const float* p = a.Sv + ((long)row * C + c) * OA_D + d0;
+        x[j][0] = *reinterpret_cast<const float4*>(p);
+        x[j][1] = *reinterpret_cast<const float4*>(p + 4);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = c0 + j * kRFGroups;
+      const float cf = c < C ? s_cw[c] : 0.f;
+      const float sv[8] = {x[j][0].x, x[j][0].y, x[j][0].z, x[j][0].w,
+                           x[j][1].x, x[j][1].y, x[j][1].z, x[j][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(cf, sv[e], acc[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_acc[grp][d0 + e] = acc[e];
+  __syncthreads();
+  if (tid < OA_D) {
+    float A = 0.f;
+    for (int g = 0; g < kRFGroups; ++g) A += s_acc[g][tid];
+    const float o = L > 0.f ? A / L : 0.f;
+    a.out[(long)row * a.out_stride + tid] = oa::f32_to_bf16(o);
+  }
+}
+
 int launch(bool fused, const void* q, long q_stride, const void* K, const void* V, long kv_sb,
            long kv_ss, int rows, int kv_rows, int head_dim, const int32_t* asg, long asg_stride,
            const int32_t* sel, long sel_stride, int n_sel, const int32_t* exp_idx, int E,
@@ -245,9 +536,15 @@ int launch(bool fused, const void* q, long q_stride, const void* K, const void* 
   a.C = C; a.sm_scale = sm_scale;
   a.out = (uint16_t*)out; a.out_stride = out_stride;
   a.kbar_r = (uint16_t*)kbar_r; a.vbar_r = (uint16_t*)vbar_r; a.logn = logn;
-  if (fused)
-    hipLaunchKernelGGL(residual_kernel<true>, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, a);
-  else
+  if (fused) {
+    const size_t lds = sizeof(int) * 3 * (size_t)(n_sel + E);
+    if (lds > 65536) {
+      const hipError_t e = hipFuncSetAttribute((const void*)resflash_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return (int)e;
+    }
+    hipLaunchKernelGGL(resflash_kernel, dim3(rows), dim3(kRFThreads), lds, (hipStream_t)stream, a);
+  } else
     hipLaunchKernelGGL(residual_kernel<false>, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, a);
   return OA_LAUNCH_STATUS();
 }

@@ -149,15 +149,6 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
 // is taken among their scores (ties to the lower position).  Then
 // sel = [0..ns) ++ [n-nl..n) ++ top, and the selected tokens' scores are set to -inf so the
 // within-cluster top-q ranks them last.
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    unsigned long long o = __shfl_xor(v, m, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 constexpr int kMaxTilesLds = 4096;   // Lmax <= 262144
 constexpr int kMaxTop = 64;
 
@@ -179,17 +170,27 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
   const int n = *n_dev;
   float* Srow = S + (long)row * s_stride;
   const float NaN = __uint_as_float(0x7fc00000u);
-  // lane l owns tiles l, l+64, ...; it caches the best key among its untaken tiles
+  // lane l owns tiles l, l+64, ...; it caches the best key among its untaken tiles.  Loads go
+  // out 16 per lane at a time (clamped addresses), so a row's tile maxima arrive in one or two
+  // rounds.
   unsigned long long mine = 0ull;
-  for (int t = lane; t < ntiles; t += 64) {
-    const float v = TM[(long)row * tm_stride + t];
-    s_tm[t] = v;
-    const unsigned long long kk = tile_key(v, t);
-    mine = kk > mine ? kk : mine;
+  for (int t0 = 0; t0 < ntiles; t0 += 64 * 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = TM[(long)row * tm_stride + min(t0 + j * 64 + lane, ntiles - 1)];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int t = t0 + j * 64 + lane;
+      if (t < ntiles) {
+        s_tm[t] = v[j];
+        const unsigned long long kk = tile_key(v[j], t);
+        mine = kk > mine ? kk : mine;
+      }
+    }
   }
   __syncthreads();
   for (int i = 0; i < k_top; ++i) {
-    const unsigned long long best = wave_max_u64(mine);
+    const unsigned long long best = oa::wave_max_u64(mine);
     const int t = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
     if (lane == 0) s_tile[i] = t;
     if (best == mine) {            // the owner lane: mark taken and rescan its tiles
@@ -204,16 +205,23 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
     }
   }
   __syncthreads();
-  // candidates: lane l holds column l of the k chosen tiles
+  // candidates: lane l holds column l of the k chosen tiles (loads 16 tiles at a time)
   mine = 0ull;
-  for (int j = 0; j < k_top; ++j) {
-    const float v = Srow[(long)s_tile[j] * 64 + lane];
-    s_sc[j * 64 + lane] = v;
-    const unsigned long long kk = tile_key(v, s_tile[j] * 64 + lane);
-    mine = kk > mine ? kk : mine;
+  for (int j0 = 0; j0 < k_top; j0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = Srow[(long)s_tile[min(j0 + j, k_top - 1)] * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (j0 + j < k_top) {
+        s_sc[(j0 + j) * 64 + lane] = v[j];
+        const unsigned long long kk = tile_key(v[j], s_tile[j0 + j] * 64 + lane);
+        mine = kk > mine ? kk : mine;
+      }
+    }
   }
   for (int i = 0; i < k_top; ++i) {
-    const unsigned long long best = wave_max_u64(mine);
+    const unsigned long long best = oa::wave_max_u64(mine);
     const int pos = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
     if (lane == 0) s_top[i] = pos;
     if (best == mine) {
@@ -234,6 +242,85 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
   if (lane < nl) sr[ns + lane] = n - nl + lane;
   for (int i = lane; i < k_top; i += 64) sr[ns + nl + i] = s_top[i];
   for (int i = lane; i < k_top; i += 64) Srow[s_top[i]] = -INFINITY;
+}
+
+// Register variant for rows of at most 64*TPL tiles and k_top <= 16: lane l keeps the keys of
+// tiles l, l+64, ... and later of column l of the k chosen tiles in registers; every extraction
+// step is one wave maximum (DPP) and an in-register update by the owning lane.
+template <int TPL>
+__global__ void __launch_bounds__(64) topk_select_reg_kernel(float* __restrict__ S, long s_stride,
+                                                             const float* __restrict__ TM,
+                                                             long tm_stride, int ntiles,
+                                                             int32_t* __restrict__ sel,
+                                                             long sel_stride,
+                                                             const int* __restrict__ n_dev, int ns,
+                                                             int nl, int k_top) {
+  constexpr int KR = 16;
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int n = *n_dev;
+  float* Srow = S + (long)row * s_stride;
+  unsigned long long tk[TPL];
+  float tv[TPL];
+#pragma unroll
+  for (int j = 0; j < TPL; ++j) tv[j] = TM[(long)row * tm_stride + min(j * 64 + lane, ntiles - 1)];
+  unsigned long long mine = 0ull;
+#pragma unroll
+  for (int j = 0; j < TPL; ++j) {
+    const int t = j * 64 + lane;
+    tk[j] = t < ntiles ? tile_key(tv[j], t) : 0ull;
+    mine = tk[j] > mine ? tk[j] : mine;
+  }
+  int my_tile = 0;               // lane i < k_top: the i-th chosen tile
+  for (int i = 0; i < k_top; ++i) {
+    const unsigned long long best = oa::wave_max_u64(mine);
+    const int t = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
+    if (lane == i) my_tile = t;
+    if (best == mine) {          // the owner lane drops the tile and refreshes its maximum
+      mine = 0ull;
+#pragma unroll
+      for (int j = 0; j < TPL; ++j) {
+        tk[j] = tk[j] == best ? 0ull : tk[j];
+        mine = tk[j] > mine ? tk[j] : mine;
+      }
+    }
+  }
+  // candidates: lane l holds column l of the k chosen tiles
+  unsigned long long ck[KR];
+  float cv[KR];
+#pragma unroll
+  for (int j = 0; j < KR; ++j) {
+    const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+    cv[j] = Srow[(long)tj * 64 + lane];
+  }
+  mine = 0ull;
+#pragma unroll
+  for (int j = 0; j < KR; ++j) {
+    const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+    ck[j] = j < k_top ? tile_key(cv[j], tj * 64 + lane) : 0ull;
+    mine = ck[j] > mine ? ck[j] : mine;
+  }
+  int my_pos = 0;                // lane i < k_top: the i-th selected position
+  for (int i = 0; i < k_top; ++i) {
+    const unsigned long long best = oa::wave_max_u64(mine);
+    const int pos = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
+    if (lane == i) my_pos = pos;
+    if (best == mine) {
+      mine = 0ull;
+#pragma unroll
+      for (int j = 0; j < KR; ++j) {
+        ck[j] = ck[j] == best ? 0ull : ck[j];
+        mine = ck[j] > mine ? ck[j] : mine;
+      }
+    }
+  }
+  int32_t* sr = sel + (long)row * sel_stride;
+  if (lane < ns) sr[lane] = lane;
+  if (lane < nl) sr[ns + lane] = n - nl + lane;
+  if (lane < k_top) {
+    sr[ns + nl + lane] = my_pos;
+    Srow[my_pos] = -INFINITY;
+  }
 }
 
 }  // namespace
@@ -265,7 +352,15 @@ extern "C" int oa_topk_select(float* S, long s_stride, const float* TM, long tm_
   if (rows <= 0 || ntiles <= 0 || ntiles > kMaxTilesLds || k_top < 0 || k_top > kMaxTop ||
       k_top > ntiles || ns < 0 || nl < 0 || ns > 64 || nl > 64 || sel_stride < ns + nl + k_top)
     return OA_EINVAL;
-  hipLaunchKernelGGL(topk_select_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, S, s_stride,
-                     TM, tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
+  hipStream_t st = (hipStream_t)stream;
+  if (k_top <= 16 && ntiles <= 64 * 16)
+    hipLaunchKernelGGL(topk_select_reg_kernel<16>, dim3(rows), dim3(64), 0, st, S, s_stride, TM,
+                       tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
+  else if (k_top <= 16 && ntiles <= 64 * 32)
+    hipLaunchKernelGGL(topk_select_reg_kernel<32>, dim3(rows), dim3(64), 0, st, S, s_stride, TM,
+                       tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
+  else
+    hipLaunchKernelGGL(topk_select_kernel, dim3(rows), dim3(64), 0, st, S, s_stride, TM, tm_stride,
+                       ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
   return OA_LAUNCH_STATUS();
 }

@@ -14,22 +14,28 @@
 // gfx950 decomposition: one 1024-thread workgroup per row.  About 40 of 64 clusters carry a
 // quota and their members cover most of the row, so the row is streamed (scores S and byte
 // cluster ids asg8, coalesced) into registers -- 1024 * PPT positions at a time, PPT per
-// thread -- and every selection step works on those registers and on LDS:
-//   P1  per-cluster min and max score key (LDS atomics; lanes of one 64-position batch rarely
-//       share a cluster, so they rarely collide);
-//   P2  per-cluster histogram of NB linear bins between that min and max (monotone binning:
-//       a higher score never lands in a lower bin);
-//   P3  one wave per cluster: t = min(q_c, members, E - base_c), the bin b* holding the t-th
-//       best member, `above` = members in higher bins, `need` = t - above from bin b*;
-//   P4  members above b* are chosen; members of bin b* are staged in LDS as unique 64-bit keys
-//       (score key << 32 | ~position) when some must be dropped;
+// thread -- and every selection step works on those registers and on LDS.  Scores are
+// compared through their order-preserving 32-bit key; its top 2*LB bits (LB = 8, 7 or 6 for
+// C <= 64, 128, 256) form the "prefix" of a member:
+//   L1  per-cluster histogram of the top LB key bits (LDS atomics; lanes of one 64-position
+//       batch rarely share a cluster, so they rarely collide);
+//   T1  one thread per cluster: t = min(q_c, members, E - base_c) and the level-1 bin holding
+//       the t-th best member (scan from the top bin; histogram rows padded against bank
+//       conflicts);
+//   L2  for clusters whose level-1 bin must be split: histogram of the next LB key bits of
+//       that bin's members only;
+//   T2  the prefix P_c holding the t-th best member, `above` = members with a larger prefix,
+//       `need` = t - above of the members with prefix P_c;
+//   P4  members with a larger prefix are chosen; members with prefix P_c are staged in LDS as
+//       unique 64-bit keys (score key << 32 | ~position) when some must be dropped;
 //   P5  one wave per staged cluster picks the `need` best staged keys (repeated wave maxima for
 //       small `need`, an MSB-first bitwise search on ballot counts otherwise); a cluster whose
-//       bin b* does not fit in LDS is resolved by the same bitwise search run block-wide over
-//       the row, streamed again;
-//   P6  the chosen (cluster << 24 | position) words, sum t <= E of them, are bitonic-sorted in
-//       LDS, which orders them by cluster and then position, and every slot of the exp_idx
-//       row is written once (-1 where a segment is short).
+//       prefix bin does not fit in LDS is resolved by the same bitwise search run block-wide
+//       over the row, streamed again;
+//   P6  every chosen (cluster << 24 | position) word gets its rank among its cluster's chosen
+//       words by position (counting, or a bitonic sort when more than 1024 were chosen), lands
+//       in an LDS copy of the exp_idx row, and the row is written out once (-1 where a
+//       segment is short).
 // Rows longer than 1024 * PPT positions are processed in segments that are re-read from
 // global memory (L2 / Infinity Cache) in each pass.  Rows are read in groups of four
 // positions, so both row strides are multiples of 4 and hold round_up(Lmax, 4) entries.
@@ -43,9 +49,10 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxC = 256;
 constexpr int kMaxE = 4096;
-constexpr int kMaxPos = 1 << 24;               // positions are packed into 24 bits in P6
+constexpr int kMaxPos = 1 << 24;               // positions (< 2^24 - 1) are packed into 24 bits in P6
 constexpr int kExtractMax = 40;                // need above this: bitwise threshold search
 constexpr int kBCapMax = 8192;                 // staged boundary keys (u64)
+constexpr int kRankMax = 1024;                 // above this many chosen words: bitonic sort
 constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
 constexpr int kLdsLimit = 160 * 1024;
 
@@ -56,20 +63,10 @@ struct TopqArgs {
   const uint8_t* asg8; long a_stride;
   const float* quota; int C; int E; const int* n_dev;
   int32_t* exp_idx;
-  int nb;          // bins per cluster (power of two, >= 64)
-  int nb_shift;    // log2(nb)
+  int lb;          // bits per histogram level (8, 7 or 6)
   int bcap;        // staged boundary capacity (u64 keys)
   int cpow;        // power of two >= E for the P6 sort
 };
-
-__device__ __forceinline__ float unkey(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
-__device__ __forceinline__ int bin_of(uint32_t key, float fmin, float scale, int nb) {
-  const float x = (unkey(key) - fmin) * scale;
-  return min((int)x, nb - 1);
-}
 
 __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
   return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (unsigned)pos);
@@ -154,34 +151,41 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
   __shared__ int s_w[kMaxC];              // min(q_c, E - base_c), clamped at 0
   __shared__ int s_base[kMaxC + 1];
-  __shared__ uint32_t s_kmin[kMaxC], s_kmax[kMaxC];
-  __shared__ float s_fmin[kMaxC], s_scale[kMaxC];
-  __shared__ int s_t[kMaxC], s_bstar[kMaxC], s_above[kMaxC], s_bcnt[kMaxC];
+  __shared__ int s_t[kMaxC], s_above[kMaxC], s_bcnt[kMaxC];
+  __shared__ int s_b1[kMaxC];             // level-1 bin to split at level 2, or -1
+  __shared__ int s_thr[kMaxC];            // final prefix threshold P_c
+  __shared__ int s_pm[kMaxC];             // (P_c << 2) | mode, one lookup per position
   __shared__ int s_mode[kMaxC], s_boff[kMaxC], s_bcur[kMaxC];
   __shared__ int s_tpre[kMaxC + 1];
   __shared__ int s_fbl[kMaxC];
   __shared__ int s_bused, s_nfb, s_ctot, s_fbcnt[3];
+  const int NB = 1 << a.lb;
+  const int HS = NB + 4;                  // padded histogram row (16-byte aligned)
   unsigned long long* s_bst = dyn;                                    // bcap
   uint32_t* s_cst = reinterpret_cast<uint32_t*>(dyn + a.bcap);        // cpow
-  int* s_hist = reinterpret_cast<int*>(s_cst + a.cpow);               // C * nb
+  int* s_out = reinterpret_cast<int*>(s_cst + a.cpow);                // cpow (E used)
+  int* s_hist = s_out + a.cpow;                                       // C * HS + 64 trash
 
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int C = a.C, E = a.E, NB = a.nb;
+  const int C = a.C, E = a.E;
+  const int sh1 = 32 - a.lb, sh2 = 32 - 2 * a.lb;
+  const int trash = C * HS + lane;        // per-lane histogram slot for non-members
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
   const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
   int32_t* erow = a.exp_idx + (long)row * E;
 
-  // ---- P0: quota prefix, per-cluster state, histogram clear
+  // ---- P0: quota prefix, per-cluster state, histogram and output clear
   if (wave == 0) {
     int v[4], loc = 0;
 #pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (int)a.quota[(long)row * C + min(lane * 4 + i, C - 1)];
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = lane * 4 + i;
-      v[i] = c < C ? (int)a.quota[(long)row * C + c] : 0;
+      v[i] = lane * 4 + i < C ? v[i] : 0;
       loc += v[i];
     }
     int incl = loc;
@@ -201,9 +205,11 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (lane == 63) s_base[kMaxC] = incl;
   }
   for (int c = tid; c < kMaxC; c += kThreads) {
-    s_kmin[c] = 0xffffffffu; s_kmax[c] = 0u; s_t[c] = 0; s_mode[c] = kModeNone; s_bcur[c] = 0;
+    s_t[c] = 0; s_mode[c] = kModeNone; s_bcur[c] = 0; s_b1[c] = -1; s_thr[c] = 0;
   }
-  for (int i = tid; i < C * NB; i += kThreads) s_hist[i] = 0;
+  for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
+  for (int i = tid; i < a.cpow / 4 + 1; i += kThreads)
+    if (4 * i < E) reinterpret_cast<int4*>(s_out)[i] = make_int4(-1, -1, -1, -1);
   if (tid == 0) { s_bused = 0; s_nfb = 0; s_ctot = 0; s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0; }
   __syncthreads();
 
@@ -234,87 +240,126 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
-      const int c = (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu);
-      const bool q = pos_of(sg, i) < n && key > kNegInfKey && s_w[c] > 0;
+      const bool q = pos_of(sg, i) < n && key > kNegInfKey;
       kk[i] = q ? key : 0u;
     }
   };
   auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
 
-  // ---- P1: per-cluster key range
+  // ---- L1: histogram of the top LB key bits per cluster
   for (int sg = 0; sg < nseg; ++sg) {
     load(sg);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      if (kk[i]) {
-        const int c = cid(i);
-        atomicMin(&s_kmin[c], kk[i]);
-        atomicMax(&s_kmax[c], kk[i]);
+      // branchless: a non-member counts into this lane's own trash slot
+      const int at = kk[i] ? (int)__umul24(cid(i), HS) + (int)(kk[i] >> sh1) : trash;
+      atomicAdd(&s_hist[at], 1);
+    }
+  }
+  __syncthreads();
+
+  // ---- T1: level-1 bin of the t-th best member.  16 threads per cluster (one DPP row), each
+  // holding NB/16 consecutive bins: a suffix scan over the 16 partial counts finds the thread
+  // whose bins hold the t-th best member, which finishes in registers.
+  for (int cb = 0; cb < C; cb += kThreads / 16) {
+    const int c = cb + (tid >> 4);
+    const int j = tid & 15;
+    int x[16];
+    int ls = 0;
+    const int bpt = NB >> 4;
+    const int w = c < C ? s_w[c] : 0;
+    const int* h = s_hist + min(c, C - 1) * HS + j * bpt;
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      x[b] = b < bpt ? h[min(b, bpt - 1)] : 0;
+      ls += x[b];
+    }
+    int sfx = ls;                // members in this thread's bins and above
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const int y = __shfl_down(sfx, off, 16);
+      if (j + off < 16) sfx += y;
+    }
+    const int m = __shfl(sfx, 0, 16);
+    if (c < C && w > 0) {
+      const int t = min(w, m);
+      if (t < w || m == 0) {     // at most w members: all of them (every prefix >= 0)
+        if (j == 0) {
+          s_t[c] = t;
+          if (t > 0) { s_mode[c] = kModeAll; s_above[c] = 0; s_bcnt[c] = t; s_thr[c] = 0; }
+        }
+      } else if (sfx >= t && sfx - ls < t) {
+        int acc = sfx - ls, b1 = j * bpt, cnt = 0;
+#pragma unroll
+        for (int b = 15; b >= 0; --b) {
+          if (b < bpt && cnt == 0 && acc + x[b] >= t) { b1 = j * bpt + b; cnt = x[b]; }
+          else if (b < bpt && cnt == 0) acc += x[b];
+        }
+        s_t[c] = t;
+        s_above[c] = acc;
+        if (t - acc == cnt) {    // the whole level-1 bin completes t: no split
+          s_bcnt[c] = cnt; s_mode[c] = kModeAll; s_thr[c] = b1 << a.lb;
+        } else {                 // split this bin at level 2
+          s_b1[c] = b1;
+        }
       }
     }
   }
   __syncthreads();
-  for (int c = tid; c < C; c += kThreads) {
-    float scale = 0.f, fmin = 0.f;
-    if (s_kmax[c] >= s_kmin[c]) {
-      fmin = unkey(s_kmin[c]);
-      const float d = unkey(s_kmax[c]) - fmin;
-      scale = d > 0.f ? (float)NB / d : 0.f;
-      if (!(scale <= 3.0e38f)) scale = 0.f;      // d subnormal: one bin, resolved by P5
-    }
-    s_fmin[c] = fmin;
-    s_scale[c] = scale;
-  }
+  for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
   __syncthreads();
 
-  // ---- P2: histogram
+  // ---- L2: next LB key bits of the members of each split level-1 bin
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      if (kk[i]) {
-        const int c = cid(i);
-        atomicAdd(&s_hist[(c << a.nb_shift) + bin_of(kk[i], s_fmin[c], s_scale[c], NB)], 1);
-      }
+      const int c = cid(i);
+      const bool in = kk[i] && (int)(kk[i] >> sh1) == s_b1[c];
+      const int at = in ? (int)__umul24(c, HS) + (int)((kk[i] >> sh2) & (NB - 1)) : trash;
+      atomicAdd(&s_hist[at], 1);
     }
   }
   __syncthreads();
 
-  // ---- P3: threshold bin per cluster (one wave per cluster)
-  const int npl = NB >> 6;       // bins per lane
-  for (int c = wave; c < C; c += kWaves) {
-    const int w = s_w[c];
-    if (w <= 0) continue;
-    const int* h = s_hist + (c << a.nb_shift) + lane * npl;
+  // ---- T2: prefix P_c of the t-th best member of each split cluster, staging plan (same
+  // 16-threads-per-cluster scan over the level-2 histogram)
+  for (int cb = 0; cb < C; cb += kThreads / 16) {
+    const int c = cb + (tid >> 4);
+    const int j = tid & 15;
+    const int b1 = c < C ? s_b1[c] : -1;
+    if (b1 < 0) continue;        // uniform over the cluster's 16 threads
+    int x[16];
     int ls = 0;
-    for (int j = 0; j < npl; ++j) ls += h[j];
-    int sfx = ls;                // members in lanes >= this one
+    const int bpt = NB >> 4;
+    const int* h = s_hist + c * HS + j * bpt;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int x = __shfl_down(sfx, off, 64);
-      if (lane + off < 64) sfx += x;
+    for (int b = 0; b < 16; ++b) {
+      x[b] = b < bpt ? h[min(b, bpt - 1)] : 0;
+      ls += x[b];
     }
-    const int m = __shfl(sfx, 0, 64);
-    const int t = min(w, m);
-    if (t <= 0) continue;
-    const unsigned long long bal = __ballot(sfx >= t);
-    const int L = 63 - __clzll((long long)bal);
-    if (lane == L) {
-      int acc = sfx - ls;
-      int bs = lane * npl, bc = 0;
-      for (int j = npl - 1; j >= 0; --j) {
-        if (acc + h[j] >= t) { bs = lane * npl + j; bc = h[j]; break; }
-        acc += h[j];
+    int sfx = ls;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const int y = __shfl_down(sfx, off, 16);
+      if (j + off < 16) sfx += y;
+    }
+    const int t2 = s_t[c] - s_above[c];          // rank of the t-th member inside bin b1
+    if (sfx >= t2 && sfx - ls < t2) {
+      int acc = sfx - ls, b2 = j * bpt, cnt = 0;
+#pragma unroll
+      for (int b = 15; b >= 0; --b) {
+        if (b < bpt && cnt == 0 && acc + x[b] >= t2) { b2 = j * bpt + b; cnt = x[b]; }
+        else if (b < bpt && cnt == 0) acc += x[b];
       }
-      const int need = t - acc;
-      s_t[c] = t;
-      s_bstar[c] = bs;
-      s_above[c] = acc;
-      s_bcnt[c] = bc;
+      const int need = t2 - acc;
+      s_above[c] = s_above[c] + acc;
+      s_bcnt[c] = cnt;
+      s_thr[c] = (b1 << a.lb) | b2;
       int mode = kModeAll;
-      if (need < bc) {
-        const int off = atomicAdd(&s_bused, bc);
-        if (off + bc <= a.bcap) {
+      if (need < cnt) {
+        const int off = atomicAdd(&s_bused, cnt);
+        if (off + cnt <= a.bcap) {
           mode = kModeStaged;
           s_boff[c] = off;
         } else {
@@ -342,7 +387,10 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (lane == 63) s_tpre[kMaxC] = incl;
   }
 
-  // ---- P4: chosen members above b*, staged members of b*
+  for (int c = tid; c < kMaxC; c += kThreads) s_pm[c] = (s_thr[c] << 2) | s_mode[c];
+  __syncthreads();
+
+  // ---- P4: chosen members above P_c, staged members at P_c
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
 #pragma unroll
@@ -351,12 +399,14 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       int c = 0;
       if (kk[i]) {
         c = cid(i);
-        const int mode = s_mode[c];
-        const int b = bin_of(kk[i], s_fmin[c], s_scale[c], NB);
-        const int bs = s_bstar[c];
-        take = b > bs || (b == bs && mode == kModeAll);
-        stage = b == bs && mode == kModeStaged;
+        const int pm = s_pm[c];
+        const int mode = pm & 3;
+        const int pf = (int)(kk[i] >> sh2);
+        const int P = pm >> 2;
+        take = mode != kModeNone && (pf > P || (pf == P && mode == kModeAll));
+        stage = pf == P && mode == kModeStaged;
       }
+      if (__ballot(take || stage) == 0ull) continue;      // the common case: nothing here
       const int p = pos_of(sg, i);
       append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst, &s_ctot, lane);
       if (stage) s_bst[s_boff[c] + atomicAdd(&s_bcur[c], 1)] = key64(kk[i], p);
@@ -364,7 +414,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   }
   __syncthreads();
 
-  // ---- P5: resolve bin b* of the staged clusters, one wave per cluster
+  // ---- P5: resolve prefix P_c of the staged clusters, one wave per cluster
   for (int c = wave; c < C; c += kWaves) {
     if (s_mode[c] != kModeStaged) continue;
     const int cnt = s_bcnt[c];
@@ -375,14 +425,13 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, s_cst, &s_ctot, lane);
     else select_staged_loop(src, cnt, need, c, s_cst, &s_ctot, lane);
   }
-  // clusters whose bin b* did not fit in LDS: block-wide bitwise search, re-streaming the row
-  // (rare; keeps the row's registers dead during P5)
-  const int nfb = s_nfb;         // final since the P3 barrier
+  // clusters whose prefix bin did not fit in LDS: block-wide bitwise search, re-streaming the
+  // row (rare; keeps the row's registers dead during P5)
+  const int nfb = s_nfb;         // final since the T2 barrier
   for (int f = 0; f < nfb; ++f) {
     const int c = s_fbl[f];
-    const int bs = s_bstar[c];
+    const int P = s_thr[c];
     const int need = s_t[c] - s_above[c];
-    const float fmin = s_fmin[c], scale = s_scale[c];
     unsigned long long T = 0ull;
     for (int bit = 63, it = 0; bit >= 0; --bit, ++it) {
       const unsigned long long cnd = T | (1ull << bit);
@@ -392,7 +441,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
           const int p = pos_of(sg, i);
-          const bool in = kk[i] && cid(i) == c && bin_of(kk[i], fmin, scale, NB) == bs &&
+          const bool in = kk[i] && cid(i) == c && (int)(kk[i] >> sh2) == P &&
                           key64(kk[i], p) >= cnd;
           k += __popcll(__ballot(in));
         }
@@ -408,7 +457,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
         const int p = pos_of(sg, i);
-        const bool take = kk[i] && cid(i) == c && bin_of(kk[i], fmin, scale, NB) == bs &&
+        const bool take = kk[i] && cid(i) == c && (int)(kk[i] >> sh2) == P &&
                           key64(kk[i], p) >= T;
         append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst, &s_ctot, lane);
       }
@@ -419,37 +468,54 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   }
   __syncthreads();
 
-  // ---- P6: order the chosen words by (cluster, position) and write the row
+  // ---- P6: each chosen word's rank inside its cluster (by position), into the LDS row copy
   const int total = s_ctot;      // == sum_c t_c
-  int P = 1;
-  while (P < total) P <<= 1;
-  for (int i = total + tid; i < P; i += kThreads) s_cst[i] = 0xffffffffu;
-  __syncthreads();
-  for (int k = 2; k <= P; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < P; i += kThreads) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint32_t x = s_cst[i], y = s_cst[ixj];
-          const bool up = (i & k) == 0;
-          if ((x > y) == up) { s_cst[i] = y; s_cst[ixj] = x; }
+  if (total <= kRankMax && 2 * a.bcap >= a.cpow) {
+    // group the words by cluster (segment tpre_c .. tpre_c + t_c of the staging area, free
+    // after P5), then rank each word among its own cluster's words only
+    uint32_t* s_grp = reinterpret_cast<uint32_t*>(s_bst);
+    for (int c = tid; c < C; c += kThreads) s_bcur[c] = 0;
+    __syncthreads();
+    for (int j = tid; j < total; j += kThreads) {
+      const uint32_t w = s_cst[j];
+      const int c = (int)(w >> 24);
+      s_grp[s_tpre[c] + atomicAdd(&s_bcur[c], 1)] = w;
+    }
+    __syncthreads();
+    for (int j = tid; j < total; j += kThreads) {
+      const uint32_t w = s_grp[j];
+      const int c = (int)(w >> 24);
+      const int b = s_tpre[c], t = s_t[c];
+      int rank = 0;
+      for (int k = b; k < b + t; ++k) rank += s_grp[k] < w ? 1 : 0;
+      s_out[s_base[c] + rank] = (int)(w & 0xffffffu);
+    }
+  } else {
+    int P = 1;
+    while (P < total) P <<= 1;
+    for (int i = total + tid; i < P; i += kThreads) s_cst[i] = 0xffffffffu;
+    __syncthreads();
+    for (int k = 2; k <= P; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < P; i += kThreads) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const uint32_t x = s_cst[i], y = s_cst[ixj];
+            const bool up = (i & k) == 0;
+            if ((x > y) == up) { s_cst[i] = y; s_cst[ixj] = x; }
+          }
         }
+        __syncthreads();
       }
-      __syncthreads();
+    }
+    for (int j = tid; j < total; j += kThreads) {
+      const uint32_t w = s_cst[j];
+      const int c = (int)(w >> 24);
+      s_out[s_base[c] + (j - s_tpre[c])] = (int)(w & 0xffffffu);
     }
   }
-  for (int sl = tid; sl < E; sl += kThreads) {
-    // cluster owning slot sl: the last c with base_c <= sl (bases are non-decreasing)
-    int lo = 0, hi = C - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_base[mid] <= sl) lo = mid; else hi = mid - 1;
-    }
-    const int r = sl - s_base[lo];
-    int v = -1;
-    if (sl < s_base[C] && r < s_t[lo]) v = (int)(s_cst[s_tpre[lo] + r] & 0xffffffu);
-    erow[sl] = v;
-  }
+  __syncthreads();
+  for (int sl = tid; sl < E; sl += kThreads) erow[sl] = s_out[sl];
 }
 
 template <int PPT>
@@ -467,7 +533,7 @@ extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long 
                        const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
                        const int* n_dev, void* stream) {
   const long lmax4 = ((long)Lmax + 3) & ~3L;
-  if (rows <= 0 || C <= 0 || C > kMaxC || E < 0 || E > kMaxE || Lmax <= 0 || Lmax > kMaxPos ||
+  if (rows <= 0 || C <= 0 || C > kMaxC || E < 0 || E > kMaxE || Lmax <= 0 || Lmax >= kMaxPos ||
       !S || !asg8 || !quota || !n_dev || (E > 0 && !exp_idx) || s_stride % 4 || asg8_stride % 4 ||
       s_stride < lmax4 || asg8_stride < lmax4 || (reinterpret_cast<uintptr_t>(S) & 15) ||
       (reinterpret_cast<uintptr_t>(asg8) & 3))
@@ -476,18 +542,14 @@ extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long 
   TopqArgs a;
   a.S = S; a.s_stride = s_stride; a.asg8 = asg8; a.a_stride = asg8_stride; a.quota = quota;
   a.C = C; a.E = E; a.n_dev = n_dev; a.exp_idx = exp_idx;
-  // bins per cluster: a power of two in [64, 256] with C * nb <= 16384
-  int nb = 256;
-  while (nb > 64 && C * nb > 16384) nb >>= 1;
-  a.nb = nb;
-  a.nb_shift = 0;
-  while ((1 << a.nb_shift) < nb) ++a.nb_shift;
-  a.cpow = 1;
+  // bits per histogram level: 8, 7 or 6, so that C * (2^lb + 4) ints stay near 64 KiB
+  a.lb = C <= 64 ? 8 : (C <= 128 ? 7 : 6);
+  a.cpow = 4;                   // >= 4: the LDS rows are cleared and scanned 4 words at a time
   while (a.cpow < E) a.cpow <<= 1;
   const size_t static_lds = sizeof(int) * (16 * kMaxC + 8);
-  const size_t fixed = sizeof(uint32_t) * a.cpow + sizeof(int) * (size_t)C * nb;
+  const size_t fixed = sizeof(uint32_t) * 2 * a.cpow + sizeof(int) * ((size_t)C * ((1 << a.lb) + 4) + 64);
   const long room = (long)kLdsLimit - (long)static_lds - (long)fixed;
-  a.bcap = (int)std::min<long>(kBCapMax, room / 8);
+  a.bcap = (int)std::min<long>(kBCapMax, room / 8) & ~3;   // keeps the LDS arrays 16-byte aligned
   if (a.bcap < 64) return OA_EINVAL;
   const size_t lds = sizeof(unsigned long long) * a.bcap + fixed;
   hipStream_t s = (hipStream_t)stream;
