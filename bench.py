@@ -59,7 +59,7 @@ def log(*a):
 # kernel function names of the stage labels (as rocprofv3 prints them)
 KERNELS = {"index_update": "index_update_kernel", "qgs_prep": "qgs_prep_kernel",
            "qgs_scan": "qgs_scan_kernel", "topk_select": "topk_select_kernel",
-           "gate_fill": "gate_fill_kernel", "topq": "topq_row_kernel",
+           "gate_fill": "errorgate_kernel", "topq": "topq_row_kernel",
            "residual_flash": "residual_kernel"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
 

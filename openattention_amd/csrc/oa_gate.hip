@@ -36,13 +36,16 @@ struct GateArgs {
 
 // the two wave-wide parts of one cluster's score (lane holds dims lane and lane+64): the tail
 // sums minus the selected tokens, then zbar = sc q.kbar and the raw sc2 (q*q).var
-__device__ __forceinline__ void gate_dots(const GateArgs& a, int c, float sk_lo, float sk_hi,
+__device__ __forceinline__ void gate_dots(const GateArgs& a, float sk_lo, float sk_hi,
                                           float s2_lo, float s2_hi, float nt, float q_lo,
-                                          float q_hi, float qq_lo, float qq_hi, const int* s_cid,
-                                          const float* s_k, int lane, float* zbar_out,
-                                          float* s2_out, float* nt_out) {
-  for (int i = 0; i < a.n_sel; ++i) {
-    if (s_cid[i] == c) {
+                                          float q_hi, float qq_lo, float qq_hi,
+                                          unsigned long long selmask, const float* s_k, int lane,
+                                          float* zbar_out, float* s2_out, float* nt_out) {
+  // the cluster's selected tokens, in selection order (bit i = selected token i)
+  while (selmask) {
+    const int i = __ffsll((long long)selmask) - 1;
+    selmask &= selmask - 1ull;
+    {
       const float k_lo = s_k[i * OA_D + lane], k_hi = s_k[i * OA_D + lane + 64];
       sk_lo = sk_lo - k_lo;
       sk_hi = sk_hi - k_hi;
@@ -76,15 +79,18 @@ __device__ __forceinline__ float gate_score(float zbar, float s2, float nt) {
 // then run one cluster per thread.  Dynamic LDS: n_sel * 128 floats of selected keys.
 __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_score, float* s_nt) {
   extern __shared__ float s_k[];
-  __shared__ int s_cid[kMaxSel];
+  __shared__ unsigned long long s_selmask[kMaxC];
   __shared__ float s_zbar[kMaxC], s_s2[kMaxC];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int kvr = row / a.G;
+  // ---- selected keys into LDS; per cluster, the mask of its selected tokens
+  for (int c = tid; c < a.C; c += kGateThreads) s_selmask[c] = 0ull;
+  __syncthreads();
   for (int i = tid; i < a.n_sel; i += kGateThreads) {
     const int tok = a.sel[(long)row * a.sel_stride + i];
-    s_cid[i] = (tok >= 0) ? a.asg[(long)row * a.asg_stride + tok] : -1;
+    if (tok >= 0) atomicOr(&s_selmask[a.asg[(long)row * a.asg_stride + tok]], 1ull << i);
   }
   for (int e = tid; e < a.n_sel * (OA_D / 8); e += kGateThreads) {
     const int i = e / (OA_D / 8), d8 = (e % (OA_D / 8)) * 8;
@@ -103,6 +109,7 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
   const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
   const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
   const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
+  // ---- tail statistics and the two dot products, eight clusters per wave
   constexpr int kBatch = 8;
   for (int c0 = wave; c0 < a.C; c0 += kGateWaves * kBatch) {
     float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
@@ -121,8 +128,8 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
       const int c = c0 + kGateWaves * i;
       if (c < a.C) {
         float zb, sv, nt;
-        gate_dots(a, c, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
-                  s_cid, s_k, lane, &zb, &sv, &nt);
+        gate_dots(a, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
+                  s_selmask[c], s_k, lane, &zb, &sv, &nt);
         if (lane == 0) {
           s_zbar[c] = zb;
           s_s2[c] = sv;
@@ -132,6 +139,7 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
     }
   }
   __syncthreads();
+  // ---- scalar tails, one cluster per thread
   for (int c = tid; c < a.C; c += kGateThreads) s_score[c] = gate_score(s_zbar[c], s_s2[c], s_nt[c]);
   __syncthreads();
 }
@@ -176,71 +184,65 @@ __device__ __forceinline__ double fill_at(double mid, const double* cap, const d
   return canon_sum(part, C, lane);
 }
 
-// water-filling of one row by one wave (lane = threadIdx.x % 64); score/n_t rows may be in LDS
-__device__ __forceinline__ void waterfill_row(const float* score_row, const float* nt_row,
-                                              float* quota_row, int C, double budget, int lane,
-                                              double* s_key, int* s_room) {
-  const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
-  double sv[4], w[4], cap[4], qv[4];
+// Water-filling, split so that the one-wave kernel and the workgroup-wide variant run the same
+// arithmetic.  Cluster c lives in lane c % 64, slot c / 64 of a wave.
+struct FillState {
+  double sv[4], w[4], cap[4];
   bool ok[4];
+  double lo, hi, tot;
+};
+
+// live clusters, weights w_b = exp(s_b - max s), total tail, and the bracket of log(lambda)
+__device__ __forceinline__ void fill_prologue(const float* score_row, const float* nt_row, int C,
+                                              int lane, FillState& f) {
+  const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
   double smax = NEG;
   for (int j = 0; j < 4; ++j) {
     int c = lane + 64 * j;
-    sv[j] = NEG; w[j] = 0.0; cap[j] = 0.0; ok[j] = false;
+    f.sv[j] = NEG; f.w[j] = 0.0; f.cap[j] = 0.0; f.ok[j] = false;
     if (c < C) {
       float nt = nt_row[c];
-      ok[j] = nt > 1.0f;
-      if (ok[j]) {
-        sv[j] = (double)score_row[c];
-        cap[j] = (double)nt;
+      f.ok[j] = nt > 1.0f;
+      if (f.ok[j]) {
+        f.sv[j] = (double)score_row[c];
+        f.cap[j] = (double)nt;
       }
-      smax = fmax(smax, sv[j]);
+      smax = fmax(smax, f.sv[j]);
     }
   }
   smax = wave_max_f64(smax);
   if (!(smax > NEG && smax < -NEG)) smax = 0.0;
   double rmax = 0.0;
   for (int j = 0; j < 4; ++j) {
-    if (ok[j]) w[j] = oa::det_exp(sv[j] - smax);
-    double ratio = (w[j] > 0.0) ? cap[j] / fmax(w[j], 1e-300) : 0.0;
+    if (f.ok[j]) f.w[j] = oa::det_exp(f.sv[j] - smax);
+    double ratio = (f.w[j] > 0.0) ? f.cap[j] / fmax(f.w[j], 1e-300) : 0.0;
     if (lane + 64 * j < C) rmax = fmax(rmax, ratio);
   }
   rmax = wave_max_f64(rmax);
-  const double tot = canon_sum(cap, C, lane);
-  double lo = -3.0 * 2.302585092994046;
-  double hi = oa::det_log(fmax(rmax, 1e-3)) + 1.0;
-  // 64 bisection steps, two per iteration: the step after mid probes 0.5*(lo+mid) or
-  // 0.5*(mid+hi), both evaluated beside mid, so the sequence of (lo, hi) is that of 64 single
-  // steps
-  for (int it = 0; it < 32; ++it) {
-    const double mid = 0.5 * (lo + hi);
-    const double m_lo = 0.5 * (lo + mid);
-    const double m_hi = 0.5 * (mid + hi);
-    const double f = fill_at(mid, cap, w, C, lane);
-    const double f_lo = fill_at(m_lo, cap, w, C, lane);
-    const double f_hi = fill_at(m_hi, cap, w, C, lane);
-    if (f > budget) {
-      hi = mid;
-      if (f_lo > budget) hi = m_lo; else lo = m_lo;
-    } else {
-      lo = mid;
-      if (f_hi > budget) hi = m_hi; else lo = m_hi;
-    }
-  }
-  const double el = oa::det_exp(lo);
+  f.tot = canon_sum(f.cap, C, lane);
+  f.lo = -3.0 * 2.302585092994046;
+  f.hi = oa::det_log(fmax(rmax, 1e-3)) + 1.0;
+}
+
+// quotas floor(min(n_b, lambda w_b)) at the final lo, leftover tokens one each to the live
+// clusters with room in score order (dead clusters as -inf), ties to the lower id
+__device__ __forceinline__ void fill_epilogue(const FillState& f, int C, double budget, int lane,
+                                              float* quota_row, double* s_key, int* s_room) {
+  const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
+  double qv[4];
+  const double el = oa::det_exp(f.lo);
   for (int j = 0; j < 4; ++j) {
-    qv[j] = floor(fmin(cap[j], el * w[j]));
-    if (tot <= budget) qv[j] = cap[j];
+    qv[j] = floor(fmin(f.cap[j], el * f.w[j]));
+    if (f.tot <= budget) qv[j] = f.cap[j];
   }
   const double qsum = canon_sum(qv, C, lane);
-  double rem = fmin(tot, budget) - qsum;
+  double rem = fmin(f.tot, budget) - qsum;
   rem = rint(rem > 0.0 ? rem : 0.0);
-  // order: live clusters by score descending (dead clusters as -inf), ties to the lower id
   for (int j = 0; j < 4; ++j) {
     int c = lane + 64 * j;
     if (c < C) {
-      s_key[c] = ok[j] ? sv[j] : NEG;
-      s_room[c] = qv[j] < cap[j] ? 1 : 0;
+      s_key[c] = f.ok[j] ? f.sv[j] : NEG;
+      s_room[c] = qv[j] < f.cap[j] ? 1 : 0;
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -252,10 +254,10 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
     if (s_room[c]) {
       int rank = 0;
       const double kc = s_key[c];
+#pragma unroll 8
       for (int c2 = 0; c2 < C; ++c2) {
-        if (!s_room[c2]) continue;
         const double k2 = s_key[c2];
-        if (k2 > kc || (k2 == kc && c2 < c)) ++rank;
+        rank += (s_room[c2] && (k2 > kc || (k2 == kc && c2 < c))) ? 1 : 0;
       }
       if ((double)rank < rem) add = 1.0;
     }
@@ -263,7 +265,39 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
   }
 }
 
+// water-filling of one row by one wave (lane = threadIdx.x % 64); score/n_t rows may be in LDS
+__device__ __forceinline__ void waterfill_row(const float* score_row, const float* nt_row,
+                                              float* quota_row, int C, double budget, int lane,
+                                              double* s_key, int* s_room) {
+  // ---- live clusters, weights and the bracket of log(lambda)
+  FillState f;
+  fill_prologue(score_row, nt_row, C, lane, f);
+  // ---- 64 bisection steps, two per iteration: the step after mid probes 0.5*(lo+mid) or
+  // 0.5*(mid+hi), both evaluated beside mid, so the sequence of (lo, hi) is that of 64 single
+  // steps
+  double lo = f.lo, hi = f.hi;
+  for (int it = 0; it < 32; ++it) {
+    const double mid = 0.5 * (lo + hi);
+    const double m_lo = 0.5 * (lo + mid);
+    const double m_hi = 0.5 * (mid + hi);
+    const double fm = fill_at(mid, f.cap, f.w, C, lane);
+    const double f_lo = fill_at(m_lo, f.cap, f.w, C, lane);
+    const double f_hi = fill_at(m_hi, f.cap, f.w, C, lane);
+    if (fm > budget) {
+      hi = mid;
+      if (f_lo > budget) hi = m_lo; else lo = m_lo;
+    } else {
+      lo = mid;
+      if (f_hi > budget) hi = m_hi; else lo = m_hi;
+    }
+  }
+  f.lo = lo;
+  f.hi = hi;
+  // ---- quotas, leftover tokens by score order
+  fill_epilogue(f, C, budget, lane, quota_row, s_key, s_room);
+}
 
+// one row per wave: the fill is a serial chain, so rows (not lanes) carry the parallelism
 __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__ score,
                                                        const float* __restrict__ n_t, long in_stride,
                                                        float* __restrict__ quota, long q_stride, int C,
@@ -273,24 +307,6 @@ __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__
   const int row = blockIdx.x;
   waterfill_row(score + (long)row * in_stride, n_t + (long)row * in_stride,
                 quota + (long)row * q_stride, C, budget, threadIdx.x, s_key, s_room);
-}
-
-// ErrorGate and water-filling of one row in one workgroup: the scores stay in LDS and
-// wave 0 solves the quotas
-__global__ void __launch_bounds__(kGateThreads) gate_fill_kernel(GateArgs a, float* quota,
-                                                                 double budget) {
-  __shared__ float s_score[kMaxC], s_nt[kMaxC];
-  __shared__ double s_key[kMaxC];
-  __shared__ int s_room[kMaxC];
-  const int row = blockIdx.x;
-  gate_row(a, row, s_score, s_nt);
-  for (int c = threadIdx.x; c < a.C; c += kGateThreads) {
-    a.score[(long)row * a.out_stride + c] = s_score[c];
-    a.n_t[(long)row * a.out_stride + c] = s_nt[c];
-  }
-  if (threadIdx.x < 64)
-    waterfill_row(s_score, s_nt, quota + (long)row * a.out_stride, a.C, budget, threadIdx.x, s_key,
-                  s_room);
 }
 
 }  // namespace
@@ -339,9 +355,14 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
   a.nb = nb; a.nb_stride = C;
   a.score = score; a.n_t = n_t; a.out_stride = C;
   a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
-  hipLaunchKernelGGL(gate_fill_kernel, dim3(rows), dim3(kGateThreads),
-                     sizeof(float) * (size_t)n_sel * OA_D, (hipStream_t)stream, a, quota,
-                     (double)budget);
+  // the gate is wide and short, the fill one serial chain per row: as two launches every row of
+  // each is resident at once instead of the fill holding the gate's workgroup slots
+  hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads),
+                     sizeof(float) * (size_t)n_sel * OA_D, (hipStream_t)stream, a);
+  const int st = OA_LAUNCH_STATUS();
+  if (st) return st;
+  hipLaunchKernelGGL(waterfill_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, score, n_t,
+                     (long)C, quota, (long)C, C, (double)budget);
   return OA_LAUNCH_STATUS();
 }
 
