@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a hipGraph")
     p.add_argument("--cpu-reps", type=int, default=3)
+    p.add_argument("--groups", type=int, default=2,
+                   help="split the batch into this many sequence groups on their own streams")
     p.add_argument("--pmc-calibration", action="store_true",
                    help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
     return p.parse_args()
@@ -57,7 +59,7 @@ def log(*a):
 
 
 # kernel function names of the stage labels (as rocprofv3 prints them)
-KERNELS = {"index_update": "index_update_kernel", "qgs_prep": "qgs_prep_kernel",
+KERNELS = {"index_prep": "index_prep_kernel",
            "qgs_scan": "qgs_scan_kernel", "topk_select": "topk_select_kernel",
            "gate_fill": "errorgate_kernel", "topq": "topq_row_kernel",
            "residual_flash": "residual_kernel"}
@@ -116,7 +118,7 @@ def main():
     Lmax = N + n_steps + 1
     T0 = N - 1
     static = synth.static_metric(L)
-    m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=L, static=static)
+    m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=L, static=static, groups=a.groups)
     Ks, Vs, Qs = [], [], []
     t0 = time.time()
     for l in range(L):
@@ -206,9 +208,12 @@ def main():
     alg = {
         # K, V row at n-1 per KV row; U (128x32 f32) per KV row; W (128x16 bf16), cent, colmean
         # per query row; read-modify-write of Sk, Sk2, Sv rows and n of one cluster
-        "index_update": B * HKV * (2 * D * 2 + D * 32 * 4 + 32) + R * (D * 16 * 2 + Cn * 16 * 4 + 64
-                                                                      + 2 * (3 * D * 4 + 4)),
-        "qgs_prep": R * D * 2 + B * HKV * (D * 32 * 4 + 32 * 4) + B * HKV * 16 * 32,
+        # index update: K, V row at n-1 and U (128x32 f32) per KV row; W, cent, colmean and a
+        # read-modify-write of one cluster's Sk, Sk2, Sv and n per query row.  Query
+        # projection: q per query row, U and scale per KV row, the limbs out.
+        "index_prep": B * HKV * (2 * D * 2 + D * 32 * 4 + 32) + R * (D * 16 * 2 + Cn * 16 * 4 + 64
+                                                                    + 2 * (3 * D * 4 + 4))
+        + R * D * 2 + B * HKV * (D * 32 * 4 + 32 * 4) + B * HKV * 16 * 32,
         "qgs_scan": B * HKV * n_mid * 32,                      # int8 codes
         "topk_select": R * (-(-n_mid // 64)) * 4 + R * NSX * 4,  # tile maxima, sel out
         "gate_fill": R * Cn * (2 * D * 4 + 4) + R * NSX * D * 2,  # Sk, Sk2, n; K of sel
@@ -316,7 +321,7 @@ def main():
         "config": {"workload": f"config3 sparse decode stage, one layer-step: B={B}, N={N}, rho={a.rho}, "
                                f"C={Cn}, E={E}, sink/local/top-k {ns}/{nl}/{k_top}",
                    "B": B, "N": N, "rho": a.rho, "C": Cn, "E": E, "layers_rotated": L,
-                   "mode": "eager" if graph is None else "hipgraph"},
+                   "mode": "eager" if graph is None else "hipgraph", "sequence_groups": a.groups},
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "stage_alg_bytes": stage_alg,
         "stage_alg_GBps": round(stage_gbps, 1),

@@ -86,6 +86,20 @@ int oa_qgs_prep(const void* q, long q_stride, const float* U, const float* scale
                 void* stream);
 
 /*
+ * oa_index_update and oa_qgs_prep in one launch (the two touch disjoint data; per query-head
+ * row one wave does each).  Replaces the pair _k_index_update_d2 + the zq projection at the
+ * start of the deployed step (inference/ours_graph.py:290-298).  Arguments: those of
+ * oa_index_update followed by q, q_stride, limbs, fexp of oa_qgs_prep; rows = 4 * kv_rows.
+ */
+int oa_index_prep(const void* K, const void* V, long kv_stride_b, long kv_stride_s, int rows,
+                  int kv_rows, int head_dim, int8_t* codes, int codes_lmax, int rank_q,
+                  const float* U, const float* scale, const void* W, const float* colmean,
+                  int rank_c, const float* cent, int C, int32_t* asg, long asg_stride,
+                  uint8_t* asg8, long asg8_stride, float* nb, float* Sk, float* Sk2, float* Sv,
+                  int32_t* reclist, int32_t* reccnt, int rmax, const int* n_dev, const void* q,
+                  long q_stride, int8_t* limbs, int* fexp, void* stream);
+
+/*
  * QGS scan: exact score of every position for the 4 query heads of each KV head, on the
  * int8 matrix cores; sink (< ns), local (>= n - nl) and unwritten positions are -inf; plus
  * the maximum of every 64-token tile.  Replaces _k_qgs_scan_tm

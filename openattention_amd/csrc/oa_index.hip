@@ -11,6 +11,7 @@
 // Dot products use the canonical order of oa_common.h; zp . cent and |cent|^2 are sequential
 // fma chains over j = 0..15 -- the CPU restatement replays both.
 #include "oa_common.h"
+#include "oa_prep.h"
 
 namespace {
 
@@ -29,9 +30,7 @@ struct IdxArgs {
   const int* n_dev; int C; int G;
 };
 
-__global__ void __launch_bounds__(64) index_update_kernel(IdxArgs a) {
-  const int r = blockIdx.x;
-  const int lane = threadIdx.x;
+__device__ __forceinline__ void index_update_row(const IdxArgs& a, int r, int lane) {
   const int kvr = r / a.G;
   const int pos = *a.n_dev - 1;
   const uint16_t* kp = a.K + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
@@ -116,6 +115,24 @@ __global__ void __launch_bounds__(64) index_update_kernel(IdxArgs a) {
   }
 }
 
+__global__ void __launch_bounds__(64) index_update_kernel(IdxArgs a) {
+  index_update_row(a, blockIdx.x, threadIdx.x);
+}
+
+struct PrepArgs {
+  const uint16_t* q; long q_stride; int8_t* limbs; int* fexp;
+};
+
+// one query-head row per 128-thread workgroup: wave 0 adds the token at n-1 to the index,
+// wave 1 projects the row's query (the two touch disjoint data)
+__global__ void __launch_bounds__(128) index_prep_kernel(IdxArgs a, PrepArgs p) {
+  if (threadIdx.x < 64)
+    index_update_row(a, blockIdx.x, threadIdx.x);
+  else
+    oa::qgs_prep_row(p.q, p.q_stride, a.U, a.scale, a.G, p.limbs, p.fexp, nullptr, blockIdx.x,
+                     threadIdx.x - 64);
+}
+
 }  // namespace
 
 extern "C" int oa_index_update(const void* K, const void* V, long kv_stride_b, long kv_stride_s,
@@ -137,5 +154,30 @@ extern "C" int oa_index_update(const void* K, const void* V, long kv_stride_b, l
   a.reclist = reclist; a.reccnt = reccnt; a.rmax = rmax; a.n_dev = n_dev; a.C = C;
   a.G = rows / kv_rows;
   hipLaunchKernelGGL(index_update_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, a);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_index_prep(const void* K, const void* V, long kv_stride_b, long kv_stride_s,
+                             int rows, int kv_rows, int head_dim, int8_t* codes, int codes_lmax,
+                             int rank_q, const float* U, const float* scale, const void* W,
+                             const float* colmean, int rank_c, const float* cent, int C,
+                             int32_t* asg, long asg_stride, uint8_t* asg8, long asg8_stride,
+                             float* nb, float* Sk, float* Sk2, float* Sv, int32_t* reclist,
+                             int32_t* reccnt, int rmax, const int* n_dev, const void* q,
+                             long q_stride, int8_t* limbs, int* fexp, void* stream) {
+  if (head_dim != OA_D || rank_q != RQ || rank_c != RC || kv_rows <= 0 || rows % kv_rows != 0 ||
+      rows / kv_rows != 4 || C <= 0 || C > 256 || rmax < 0 || !asg8 || !q || !limbs || !fexp)
+    return OA_EINVAL;
+  IdxArgs a;
+  a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.kv_sb = kv_stride_b; a.kv_ss = kv_stride_s;
+  a.codes = codes; a.Lmax_codes = codes_lmax; a.U = U; a.scale = scale;
+  a.W = (const uint16_t*)W; a.colmean = colmean; a.cent = cent;
+  a.asg = asg; a.asg_stride = asg_stride; a.asg8 = asg8; a.asg8_stride = asg8_stride; a.nb = nb;
+  a.Sk = Sk; a.Sk2 = Sk2; a.Sv = Sv;
+  a.reclist = reclist; a.reccnt = reccnt; a.rmax = rmax; a.n_dev = n_dev; a.C = C;
+  a.G = rows / kv_rows;
+  PrepArgs p;
+  p.q = (const uint16_t*)q; p.q_stride = q_stride; p.limbs = limbs; p.fexp = fexp;
+  hipLaunchKernelGGL(index_prep_kernel, dim3(rows), dim3(128), 0, (hipStream_t)stream, a, p);
   return OA_LAUNCH_STATUS();
 }

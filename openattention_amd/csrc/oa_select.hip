@@ -17,6 +17,7 @@
 // them exactly in fp64 (all values are integers below 2^53).
 // Top-k ties break to the lower position (graph_runner.py:127-151 rule).
 #include "oa_common.h"
+#include "oa_prep.h"
 
 typedef int oa_v4i __attribute__((ext_vector_type(4)));
 
@@ -26,61 +27,14 @@ constexpr int RQ = 32;   // QGS rank (bytes of code per token)
 constexpr int GQ = 4;    // query heads per KV head (limb rows = GQ * 4 = 16)
 
 // ------------------------------------------------------------------------------------------
-// prep: one wave per query-head row.  zq = (q . U[:, r]) * scale_r (canonical dot order),
-// then the fixed-point exponent and the four int8 limbs of Z_r.
+// prep: one wave per query-head row (body in oa_prep.h, shared with the fused index+prep kernel)
 __global__ void __launch_bounds__(64) qgs_prep_kernel(const uint16_t* __restrict__ q, long q_stride,
-                                                      const float* __restrict__ U,      // (BH, D, RQ)
-                                                      const float* __restrict__ scale,  // (BH, RQ)
-                                                      int G, int8_t* __restrict__ limbs, // (BH, 16, RQ)
-                                                      int* __restrict__ fexp, float* __restrict__ zq_out) {
-  const int row = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int kvr = row / G;
-  const int g = row % G;
-  const float q_lo = oa::bf16_to_f32(q[(long)row * q_stride + lane]);
-  const float q_hi = oa::bf16_to_f32(q[(long)row * q_stride + lane + 64]);
-  const float* Ub = U + (long)kvr * OA_D * RQ;
-  // lane l holds rows l and l+64 of U (32 contiguous floats each)
-  float ul[RQ], uh[RQ];
-#pragma unroll
-  for (int j = 0; j < RQ; j += 4) {
-    const float4 a = *reinterpret_cast<const float4*>(Ub + lane * RQ + j);
-    const float4 b = *reinterpret_cast<const float4*>(Ub + (lane + 64) * RQ + j);
-    ul[j] = a.x; ul[j + 1] = a.y; ul[j + 2] = a.z; ul[j + 3] = a.w;
-    uh[j] = b.x; uh[j + 1] = b.y; uh[j + 2] = b.z; uh[j + 3] = b.w;
-  }
-  float myz = 0.f;
-#pragma unroll
-  for (int j = 0; j < RQ; ++j) {
-    const float d = oa::dot128_canon(q_lo, ul[j], q_hi, uh[j]);
-    const float z = d * scale[(long)kvr * RQ + j];
-    if (lane == j) myz = z;
-  }
-  float a = (lane < RQ) ? fabsf(myz) : 0.f;
-  float emax = oa::wave_max(a);
-  int F = 0;
-  int Z = 0;
-  if (emax > 0.f && emax < INFINITY) {
-    int ex;
-    (void)frexpf(emax, &ex);
-    F = 30 - ex;
-    if (lane < RQ) Z = (int)rint(ldexp((double)myz, F));
-  }
-  if (lane < RQ) {
-    int l0 = (int)(int8_t)(Z & 0xff);
-    int z1 = (Z - l0) >> 8;
-    int l1 = (int)(int8_t)(z1 & 0xff);
-    int z2 = (z1 - l1) >> 8;
-    int l2 = (int)(int8_t)(z2 & 0xff);
-    int l3 = (z2 - l2) >> 8;
-    int8_t* Lb = limbs + (long)kvr * 16 * RQ;
-    Lb[(g * 4 + 0) * RQ + lane] = (int8_t)l0;
-    Lb[(g * 4 + 1) * RQ + lane] = (int8_t)l1;
-    Lb[(g * 4 + 2) * RQ + lane] = (int8_t)l2;
-    Lb[(g * 4 + 3) * RQ + lane] = (int8_t)l3;
-    if (zq_out) zq_out[(long)row * RQ + lane] = myz;
-  }
-  if (lane == 0) fexp[row] = F;
+                                                      const float* __restrict__ U,
+                                                      const float* __restrict__ scale, int G,
+                                                      int8_t* __restrict__ limbs,
+                                                      int* __restrict__ fexp,
+                                                      float* __restrict__ zq_out) {
+  oa::qgs_prep_row(q, q_stride, U, scale, G, limbs, fexp, zq_out, blockIdx.x, threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -28,6 +28,8 @@ SIGNATURES = {
     "oa_index_update": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
                         P, I, P, P],
     "oa_qgs_prep": [P, L, P, P, I, I, I, I, P, P, P, P],
+    "oa_index_prep": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
+                      P, I, P, P, L, P, P, P],
     "oa_qgs_scan": [P, I, I, I, P, P, P, L, P, L, P, I, I, P],
     "oa_topk_select": [P, L, P, L, I, I, P, L, P, I, I, I, P],
     "oa_errorgate": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, P, P, P],

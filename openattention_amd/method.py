@@ -13,6 +13,8 @@ only computes (ns, nl, k_top) from n, which the reference also keys its graphs b
 """
 from __future__ import annotations
 
+import types
+
 import torch
 import torch.nn.functional as TF
 
@@ -79,8 +81,16 @@ class OursHIP(Method):
     name = "ours_hip"
 
     def __init__(self, a, B, Lmax, dev, n_layers: int = NL, static: dict | None = None,
-                 ctx_len: int = CTX_LEN, rule: str = "multibin", fused: bool = True):
+                 ctx_len: int = CTX_LEN, rule: str = "multibin", fused: bool = True,
+                 groups: int = 1):
         super().__init__(a, B, Lmax, dev)
+        if groups < 1 or B % groups:
+            raise ValueError(f"groups={groups} must divide B={B}")
+        # the batch is split into `groups` sets of whole sequences whose stage chains run on
+        # their own streams (rows are independent): one group's latency-bound stages overlap
+        # another group's bandwidth-bound scan
+        self.groups = groups
+        self.streams = [torch.cuda.Stream(device=dev) for _ in range(groups)] if groups > 1 else []
         self.bud = budget(a.rho, ctx_len=ctx_len, rule=rule)
         self.Cn, self.E = self.bud.C, self.bud.E
         self.n_layers = n_layers
@@ -146,11 +156,21 @@ class OursHIP(Method):
             raise ValueError(f"n={n} too small for sink {ns} + local {nl} + top-k {k_top}")
         NS = ns + nl + k_top
         sel = self.sel_buffer(NS)
+        if self.groups > 1 and marks is None:
+            main = torch.cuda.current_stream()
+            per = self.B // self.groups
+            for g, s in enumerate(self.streams):
+                s.wait_stream(main)
+                with torch.cuda.stream(s):
+                    self._chain(st, K, V, qr, sel, slice(g * per * HQ, (g + 1) * per * HQ),
+                                slice(g * per * HKV, (g + 1) * per * HKV), ns, nl, k_top)
+            for s in self.streams:
+                main.wait_stream(s)
+            self.last_sel = sel
+            return self.out.view(self.B, HQ, 1, D)
         mark("start")
-        ops.index_update(K, V, st, C.n_dev, RMAX)
-        mark("index_update")
-        ops.qgs_prep(qr, st.U, st.scale, self.limbs, self.fexp)
-        mark("qgs_prep")
+        ops.index_prep(K, V, st, C.n_dev, RMAX, qr, self.limbs, self.fexp)
+        mark("index_prep")
         ops.qgs_scan(st.codes, self.limbs, self.fexp, self.S, self.TM, C.n_dev, ns, nl)
         mark("qgs_scan")
         ops.topk_select(self.S, self.TM, sel, C.n_dev, ns, nl, k_top)
@@ -173,3 +193,25 @@ class OursHIP(Method):
             mark("flash")
         self.last_sel = sel
         return self.out.view(self.B, HQ, 1, D)
+
+    def _chain(self, st, K, V, qr, sel, rs: slice, ks: slice, ns: int, nl: int, k_top: int):
+        """The decode stages on query-head rows `rs` and their KV rows `ks` (whole sequences)."""
+        sub = types.SimpleNamespace(
+            codes=st.codes[ks], U=st.U[ks], scale=st.scale[ks], W=st.W[rs], colmean=st.colmean[rs],
+            cent=st.cent[rs], asg=st.asg[rs], asg8=st.asg8[rs], nb=st.nb[rs], Sk=st.Sk[rs],
+            Sk2=st.Sk2[rs], Sv=st.Sv[rs], reclist=st.reclist[rs], reccnt=st.reccnt[rs])
+        Kg, Vg, qg, selg = K[ks], V[ks], qr[rs], sel[rs]
+        ops.index_prep(Kg, Vg, sub, C.n_dev, RMAX, qg, self.limbs[ks], self.fexp[rs])
+        ops.qgs_scan(sub.codes, self.limbs[ks], self.fexp[rs], self.S[rs], self.TM[rs], C.n_dev, ns, nl)
+        ops.topk_select(self.S[rs], self.TM[rs], selg, C.n_dev, ns, nl, k_top)
+        ops.gate_fill(qg, Kg, sub.asg, selg, sub.Sk, sub.Sk2, sub.nb, self.score[rs], self.n_t[rs],
+                      self.quota[rs], SC, self.E)
+        ops.topq(self.S[rs], sub.asg8, self.quota[rs], self.exp_idx[rs], C.n_dev)
+        if self.fused:
+            ops.residual_flash(qg, Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs],
+                               self.n_t[rs], sub.Sk, sub.Sv, self.out[rs], SC)
+        else:
+            ops.residual(Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs], self.n_t[rs],
+                         sub.Sk, sub.Sv, self.kbar_r[rs], self.vbar_r[rs], self.log_n[rs])
+            ops.flash_decode(qg, Kg, Vg, selg, self.exp_idx[rs], self.kbar_r[rs], self.vbar_r[rs],
+                             self.log_n[rs], proxy_per_kv=False, sm_scale=SC, out=self.out[rs])

@@ -154,6 +154,21 @@ def index_update(K, V, st, n_dev: torch.Tensor, rmax: int) -> None:
              _ptr(st.reccnt), rmax, _ptr(n_dev), _stream(dev))
 
 
+def index_prep(K, V, st, n_dev: torch.Tensor, rmax: int, q, limbs, fexp) -> None:
+    """index_update and qgs_prep in one launch (same results as the two calls)."""
+    dev = _dev(K, V, n_dev, q, limbs, fexp)
+    BH, Lmax, D = K.shape
+    R = st.nb.shape[0]
+    C = st.nb.shape[1]
+    _rows_contig(q, "q")
+    lib.call("oa_index_prep", _ptr(K), _ptr(V), K.stride(0), K.stride(1), R, BH, D,
+             _ptr(st.codes), st.codes.shape[1], RANK_Q, _ptr(st.U), _ptr(st.scale), _ptr(st.W),
+             _ptr(st.colmean), RANK_C, _ptr(st.cent), C, _ptr(st.asg), st.asg.stride(0),
+             _ptr(st.asg8), st.asg8.stride(0), _ptr(st.nb), _ptr(st.Sk), _ptr(st.Sk2), _ptr(st.Sv),
+             _ptr(st.reclist), _ptr(st.reccnt), rmax, _ptr(n_dev), _ptr(q), q.stride(0),
+             _ptr(limbs), _ptr(fexp), _stream(dev))
+
+
 def qgs_prep(q, U, scale, limbs, fexp, zq_out=None) -> None:
     dev = _dev(q, U, scale, limbs, fexp)
     R = q.shape[0]

@@ -321,6 +321,53 @@ def test_topq_adversarial_quotas(n, C, E, seed):
     assert np.array_equal(got, ref), f"rows differ: {np.nonzero((got != ref).any(1))[0]}"
 
 
+def test_decode_sequence_groups_match_single_chain(lay4k):
+    """Running the stage chain per sequence group on separate streams gives the same bits as
+    one chain over the whole batch (captured in a graph and replayed, and eagerly)."""
+    print("[case] sequence groups", flush=True)
+    a = types.SimpleNamespace(rho=0.01)
+    lay = lay4k
+    outs = []
+    for groups in (1, 2):
+        m = OursHIP(a, lay.B, lay.Lmax, DEV, n_layers=1, static=lay.static, ctx_len=lay.N, groups=groups)
+        for f in LayerState.FIELDS:
+            getattr(m.st[0], f).copy_(getattr(lay.st, f))
+        CTX.K, CTX.V = [lay.K], [lay.V]
+        CTX.n_dev = torch.tensor([lay.N], device=DEV, dtype=torch.int32)
+        CTX.n0_dev = torch.tensor([lay.T], device=DEV, dtype=torch.int32)
+        o = m.decode(0, lay.q.clone(), lay.N).clone()
+        torch.cuda.synchronize()
+        outs.append((o, m.exp_idx.clone(), m.quota.clone(), m.st[0].asg.clone()))
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
+
+
+def test_index_prep_matches_separate_calls(lay4k):
+    """oa_index_prep equals oa_index_update followed by oa_qgs_prep, bit for bit."""
+    print("[case] index+prep fused", flush=True)
+    lay = lay4k
+    K = lay.K.reshape(-1, lay.Lmax, D)
+    V = lay.V.reshape(-1, lay.Lmax, D)
+    n_dev = torch.tensor([lay.N], device=DEV, dtype=torch.int32)
+    qr = lay.q.reshape(-1, D).contiguous()
+    res = []
+    for fused in (False, True):
+        st = lay.st.clone()
+        limbs = torch.zeros(lay.B * HKV, 16, 32, device=DEV, dtype=torch.int8)
+        fexp = torch.zeros(lay.B * HQ, device=DEV, dtype=torch.int32)
+        if fused:
+            ops.index_prep(K, V, st, n_dev, RMAX, qr, limbs, fexp)
+        else:
+            ops.index_update(K, V, st, n_dev, RMAX)
+            ops.qgs_prep(qr, st.U, st.scale, limbs, fexp)
+        torch.cuda.synchronize()
+        res.append((st.to_numpy(), limbs.cpu().numpy(), fexp.cpu().numpy()))
+    for f in LayerState.FIELDS:
+        assert np.array_equal(res[0][0][f], res[1][0][f]), f
+    assert np.array_equal(res[0][1], res[1][1])
+    assert np.array_equal(res[0][2], res[1][2])
+
+
 def test_dense_decode_vs_oracle(lay4k):
     print("[case] dense", flush=True)
     lay = lay4k
