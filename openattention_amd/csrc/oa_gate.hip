@@ -154,11 +154,13 @@ __global__ void __launch_bounds__(kGateThreads) errorgate_kernel(GateArgs a) {
   }
 }
 
-// one wave per row; cluster c lives in lane c % 64, slot c / 64
+// one wave per row; cluster c lives in lane c % 64, slot c / 64 (NS slots per lane)
+template <int NS>
 __device__ __forceinline__ double canon_sum(const double* x, int C, int lane) {
   double p = 0.0;
   bool first = true;
-  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
     int c = lane + 64 * j;
     if (c < C) {
       p = first ? x[j] : p + x[j];
@@ -174,30 +176,39 @@ __device__ __forceinline__ double wave_max_f64(double v) {
   return v;
 }
 
-// f(mid) = sum_b min(cap_b, exp(mid) w_b) in the canonical order
-__device__ __forceinline__ double fill_at(double mid, const double* cap, const double* w, int C,
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)b, l);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// f = sum_b min(cap_b, em w_b) in the canonical order, em = exp(mid)
+template <int NS>
+__device__ __forceinline__ double fill_em(double em, const double* cap, const double* w, int C,
                                           int lane) {
-  const double em = oa::det_exp(mid);
-  double part[4];
+  double part[NS];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) part[j] = fmin(cap[j], em * w[j]);
-  return canon_sum(part, C, lane);
+  for (int j = 0; j < NS; ++j) part[j] = fmin(cap[j], em * w[j]);
+  return canon_sum<NS>(part, C, lane);
 }
 
 // Water-filling, split so that the one-wave kernel and the workgroup-wide variant run the same
 // arithmetic.  Cluster c lives in lane c % 64, slot c / 64 of a wave.
+template <int NS>
 struct FillState {
-  double sv[4], w[4], cap[4];
-  bool ok[4];
+  double sv[NS], w[NS], cap[NS];
+  bool ok[NS];
   double lo, hi, tot;
 };
 
 // live clusters, weights w_b = exp(s_b - max s), total tail, and the bracket of log(lambda)
+template <int NS>
 __device__ __forceinline__ void fill_prologue(const float* score_row, const float* nt_row, int C,
-                                              int lane, FillState& f) {
+                                              int lane, FillState<NS>& f) {
   const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
   double smax = NEG;
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NS; ++j) {
     int c = lane + 64 * j;
     f.sv[j] = NEG; f.w[j] = 0.0; f.cap[j] = 0.0; f.ok[j] = false;
     if (c < C) {
@@ -213,51 +224,56 @@ __device__ __forceinline__ void fill_prologue(const float* score_row, const floa
   smax = wave_max_f64(smax);
   if (!(smax > NEG && smax < -NEG)) smax = 0.0;
   double rmax = 0.0;
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NS; ++j) {
     if (f.ok[j]) f.w[j] = oa::det_exp(f.sv[j] - smax);
     double ratio = (f.w[j] > 0.0) ? f.cap[j] / fmax(f.w[j], 1e-300) : 0.0;
     if (lane + 64 * j < C) rmax = fmax(rmax, ratio);
   }
   rmax = wave_max_f64(rmax);
-  f.tot = canon_sum(f.cap, C, lane);
+  f.tot = canon_sum<NS>(f.cap, C, lane);
   f.lo = -3.0 * 2.302585092994046;
   f.hi = oa::det_log(fmax(rmax, 1e-3)) + 1.0;
 }
 
 // quotas floor(min(n_b, lambda w_b)) at the final lo, leftover tokens one each to the live
 // clusters with room in score order (dead clusters as -inf), ties to the lower id
-__device__ __forceinline__ void fill_epilogue(const FillState& f, int C, double budget, int lane,
-                                              float* quota_row, double* s_key, int* s_room) {
+template <int NS>
+__device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, double budget, int lane,
+                                              float* quota_row, double* s_key) {
   const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
-  double qv[4];
+  double qv[NS];
   const double el = oa::det_exp(f.lo);
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NS; ++j) {
     qv[j] = floor(fmin(f.cap[j], el * f.w[j]));
     if (f.tot <= budget) qv[j] = f.cap[j];
   }
-  const double qsum = canon_sum(qv, C, lane);
+  const double qsum = canon_sum<NS>(qv, C, lane);
   double rem = fmin(f.tot, budget) - qsum;
   rem = rint(rem > 0.0 ? rem : 0.0);
-  for (int j = 0; j < 4; ++j) {
+  // rank keys: live scores are floats (widened exactly), so the order-preserving 32-bit key of
+  // the float orders them; dead clusters take key 0 (below every live key, like -inf);
+  // clusters without room take no rank (0xffffffff marks them)
+  for (int j = 0; j < NS; ++j) {
     int c = lane + 64 * j;
     if (c < C) {
-      s_key[c] = f.ok[j] ? f.sv[j] : NEG;
-      s_room[c] = qv[j] < f.cap[j] ? 1 : 0;
+      const unsigned kf = f.ok[j] ? oa::float_key((float)f.sv[j]) : 0u;
+      s_key[c] = __longlong_as_double((long long)(qv[j] < f.cap[j] ? kf : 0xffffffffu));
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  for (int j = 0; j < 4; ++j) {
+  const unsigned* s_k32 = reinterpret_cast<const unsigned*>(s_key);   // low words
+  for (int j = 0; j < NS; ++j) {
     int c = lane + 64 * j;
     if (c >= C) continue;
     double add = 0.0;
-    if (s_room[c]) {
+    const unsigned kc = s_k32[2 * c];
+    if (kc != 0xffffffffu) {
       int rank = 0;
-      const double kc = s_key[c];
 #pragma unroll 8
       for (int c2 = 0; c2 < C; ++c2) {
-        const double k2 = s_key[c2];
-        rank += (s_room[c2] && (k2 > kc || (k2 == kc && c2 < c))) ? 1 : 0;
+        const unsigned k2 = s_k32[2 * c2];
+        rank += (k2 != 0xffffffffu && (k2 > kc || (k2 == kc && c2 < c))) ? 1 : 0;
       }
       if ((double)rank < rem) add = 1.0;
     }
@@ -266,12 +282,13 @@ __device__ __forceinline__ void fill_epilogue(const FillState& f, int C, double 
 }
 
 // water-filling of one row by one wave (lane = threadIdx.x % 64); score/n_t rows may be in LDS
+template <int NS>
 __device__ __forceinline__ void waterfill_row(const float* score_row, const float* nt_row,
                                               float* quota_row, int C, double budget, int lane,
-                                              double* s_key, int* s_room) {
+                                              double* s_key) {
   // ---- live clusters, weights and the bracket of log(lambda)
-  FillState f;
-  fill_prologue(score_row, nt_row, C, lane, f);
+  FillState<NS> f;
+  fill_prologue<NS>(score_row, nt_row, C, lane, f);
   // ---- 64 bisection steps, two per iteration: the step after mid probes 0.5*(lo+mid) or
   // 0.5*(mid+hi), both evaluated beside mid, so the sequence of (lo, hi) is that of 64 single
   // steps
@@ -280,9 +297,12 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
     const double mid = 0.5 * (lo + hi);
     const double m_lo = 0.5 * (lo + mid);
     const double m_hi = 0.5 * (mid + hi);
-    const double fm = fill_at(mid, f.cap, f.w, C, lane);
-    const double f_lo = fill_at(m_lo, f.cap, f.w, C, lane);
-    const double f_hi = fill_at(m_hi, f.cap, f.w, C, lane);
+    // the three exponentials in lanes 0, 1, 2 of one det_exp pass (the value is uniform, so
+    // the other lanes would repeat it), then broadcast
+    const double e = oa::det_exp(lane == 0 ? mid : (lane == 1 ? m_lo : m_hi));
+    const double fm = fill_em<NS>(readlane_f64(e, 0), f.cap, f.w, C, lane);
+    const double f_lo = fill_em<NS>(readlane_f64(e, 1), f.cap, f.w, C, lane);
+    const double f_hi = fill_em<NS>(readlane_f64(e, 2), f.cap, f.w, C, lane);
     if (fm > budget) {
       hi = mid;
       if (f_lo > budget) hi = m_lo; else lo = m_lo;
@@ -294,19 +314,34 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
   f.lo = lo;
   f.hi = hi;
   // ---- quotas, leftover tokens by score order
-  fill_epilogue(f, C, budget, lane, quota_row, s_key, s_room);
+  fill_epilogue<NS>(f, C, budget, lane, quota_row, s_key);
 }
 
 // one row per wave: the fill is a serial chain, so rows (not lanes) carry the parallelism
+template <int NS>
 __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__ score,
                                                        const float* __restrict__ n_t, long in_stride,
                                                        float* __restrict__ quota, long q_stride, int C,
                                                        double budget) {
   __shared__ double s_key[kMaxC];
-  __shared__ int s_room[kMaxC];
   const int row = blockIdx.x;
-  waterfill_row(score + (long)row * in_stride, n_t + (long)row * in_stride,
-                quota + (long)row * q_stride, C, budget, threadIdx.x, s_key, s_room);
+  waterfill_row<NS>(score + (long)row * in_stride, n_t + (long)row * in_stride,
+                    quota + (long)row * q_stride, C, budget, threadIdx.x, s_key);
+}
+
+int launch_fill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,
+                hipStream_t s) {
+  const int ns = (C + 63) / 64;
+  if (ns == 1)
+    hipLaunchKernelGGL(waterfill_kernel<1>, dim3(rows), dim3(64), 0, s, score, n_t, (long)C, quota,
+                       (long)C, C, (double)budget);
+  else if (ns == 2)
+    hipLaunchKernelGGL(waterfill_kernel<2>, dim3(rows), dim3(64), 0, s, score, n_t, (long)C, quota,
+                       (long)C, C, (double)budget);
+  else
+    hipLaunchKernelGGL(waterfill_kernel<4>, dim3(rows), dim3(64), 0, s, score, n_t, (long)C, quota,
+                       (long)C, C, (double)budget);
+  return OA_LAUNCH_STATUS();
 }
 
 }  // namespace
@@ -361,15 +396,11 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
                      sizeof(float) * (size_t)n_sel * OA_D, (hipStream_t)stream, a);
   const int st = OA_LAUNCH_STATUS();
   if (st) return st;
-  hipLaunchKernelGGL(waterfill_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, score, n_t,
-                     (long)C, quota, (long)C, C, (double)budget);
-  return OA_LAUNCH_STATUS();
+  return launch_fill(score, n_t, rows, C, budget, quota, (hipStream_t)stream);
 }
 
 extern "C" int oa_waterfill(const float* score, const float* n_t, int rows, int C, int budget,
                             float* quota, void* stream) {
   if (rows <= 0 || C <= 0 || C > kMaxC || budget < 0) return OA_EINVAL;
-  hipLaunchKernelGGL(waterfill_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, score, n_t,
-                     (long)C, quota, (long)C, C, (double)budget);
-  return OA_LAUNCH_STATUS();
+  return launch_fill(score, n_t, rows, C, budget, quota, (hipStream_t)stream);
 }
