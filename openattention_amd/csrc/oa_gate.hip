@@ -144,7 +144,8 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
   __syncthreads();
 }
 
-__global__ void __launch_bounds__(kGateThreads) errorgate_kernel(GateArgs a) {
+// 8 waves per SIMD (<= 64 VGPRs): every row of a B=32 batch is resident at once
+__global__ void __launch_bounds__(kGateThreads, 8) errorgate_kernel(GateArgs a) {
   __shared__ float s_score[kMaxC], s_nt[kMaxC];
   const int row = blockIdx.x;
   gate_row(a, row, s_score, s_nt);

@@ -16,8 +16,7 @@
 // (w_c the proxy weight, den_c = max(n'_c, 1)), so no per-cluster vector sums are formed.
 // One 512-thread workgroup per query-head row, 32 lane groups of 16 lanes (8 dims per lane):
 //   pass 1  every read token's q.k and every cluster's q.Sk as independent units, spread
-//           round-robin over the lane groups, eight loads in flight per group; the first
-//           batch of pass-2 rows is issued before the scalar phase and lands during it;
+//           round-robin over the lane groups, eight loads in flight per group;
 //   scalars one thread per cluster sums its read tokens' dots in list order (selected tokens,
 //           then its exp_idx segment), forms the proxy logit; block max and weights;
 //   pass 2  every read token's V row and every cluster's Sv row scaled by its coefficient,
@@ -236,7 +235,7 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(ResArgs a) {
 constexpr int kRFThreads = 512;
 constexpr int kRFGroups = kRFThreads / 16;
 constexpr int kRFWaves = kRFThreads / 64;
-constexpr int kBatch = 8;
+constexpr int kBatch = 4;
 
 // fixed-order sum / max over the workgroup (thread partials -> wave butterfly -> waves in order)
 __device__ __forceinline__ float block_sum(float v, float* s_red, int tid) {
@@ -260,7 +259,8 @@ __device__ __forceinline__ float block_max(float v, float* s_red, int tid) {
   return t;
 }
 
-__global__ void __launch_bounds__(kRFThreads) resflash_kernel(ResArgs a) {
+// 8 waves per SIMD (<= 64 VGPRs): every row of a B=32 batch is resident at once
+__global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
   extern __shared__ int dyn_rf[];
   __shared__ int s_base[kMaxC + 1];
   __shared__ int s_q[kMaxC];
@@ -401,16 +401,6 @@ __global__ void __launch_bounds__(kRFThreads) resflash_kernel(ResArgs a) {
     load_stat(a.Sk, c0, skx);
     dots_sk(c0, skx);
   }
-  // first batch of pass 2, in flight through the scalar phase
-  uint4 vpre[kBatch];
-  float4 spre[4][2];
-#pragma unroll
-  for (int j = 0; j < kBatch; ++j) {
-    const int u = min(grp + j * kRFGroups, max(NI - 1, 0));
-    const int tok = NI > 0 ? max(s_tok[u], 0) : 0;
-    vpre[j] = *reinterpret_cast<const uint4*>(Vb + (long)tok * a.kv_ss);
-  }
-  load_stat(a.Sv, grp, spre);
   __syncthreads();
 
   // ---- scalars: proxy logits (log2 units), block max, weights, coefficients
@@ -461,16 +451,11 @@ __global__ void __launch_bounds__(kRFThreads) resflash_kernel(ResArgs a) {
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   for (int u0 = grp; u0 < NI; u0 += kRFGroups * kBatch) {
     uint4 w[kBatch];
-    if (u0 == grp) {
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) w[j] = vpre[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int u = min(u0 + j * kRFGroups, NI - 1);
-        const int tok = max(s_tok[u], 0);
-        w[j] = *reinterpret_cast<const uint4*>(Vb + (long)tok * a.kv_ss);
-      }
+    for (int j = 0; j < kBatch; ++j) {
+      const int u = min(u0 + j * kRFGroups, NI - 1);
+      const int tok = max(s_tok[u], 0);
+      w[j] = *reinterpret_cast<const uint4*>(Vb + (long)tok * a.kv_ss);
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
@@ -484,18 +469,7 @@ __global__ void __launch_bounds__(kRFThreads) resflash_kernel(ResArgs a) {
   }
   for (int c0 = grp; c0 < C; c0 += kRFGroups * 4) {
     float4 x[4][2];
-    if (c0 == grp) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { x[j][0] = spre[j][0]; x[j][1] = spre[j][1]; }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = min(c0 + j * kRFGroups, C - 1);
-        const float* p = a.Sv + ((long)row * C + c) * OA_D + d0;
-        x[j][0] = *reinterpret_cast<const float4*>(p);
-        x[j][1] = *reinterpret_cast<const float4*>(p + 4);
-      }
-    }
+    load_stat(a.Sv, c0, x);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = c0 + j * kRFGroups;

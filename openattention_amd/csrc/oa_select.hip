@@ -198,10 +198,10 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
   for (int i = lane; i < k_top; i += 64) Srow[s_top[i]] = -INFINITY;
 }
 
-// Register variant for rows of at most 64*TPL tiles and k_top <= 16: lane l keeps the keys of
+// Register variant for rows of at most 64*TPL tiles and k_top <= KR: lane l keeps the keys of
 // tiles l, l+64, ... and later of column l of the k chosen tiles in registers; every extraction
 // step is one wave maximum (DPP) and an in-register update by the owning lane.
-template <int TPL>
+template <int TPL, int KR>
 __global__ void __launch_bounds__(64) topk_select_reg_kernel(float* __restrict__ S, long s_stride,
                                                              const float* __restrict__ TM,
                                                              long tm_stride, int ntiles,
@@ -209,7 +209,6 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(float* __restrict__
                                                              long sel_stride,
                                                              const int* __restrict__ n_dev, int ns,
                                                              int nl, int k_top) {
-  constexpr int KR = 16;
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
   const int n = *n_dev;
@@ -307,14 +306,17 @@ extern "C" int oa_topk_select(float* S, long s_stride, const float* TM, long tm_
       k_top > ntiles || ns < 0 || nl < 0 || ns > 64 || nl > 64 || sel_stride < ns + nl + k_top)
     return OA_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-  if (k_top <= 16 && ntiles <= 64 * 16)
-    hipLaunchKernelGGL(topk_select_reg_kernel<16>, dim3(rows), dim3(64), 0, st, S, s_stride, TM,
-                       tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
-  else if (k_top <= 16 && ntiles <= 64 * 32)
-    hipLaunchKernelGGL(topk_select_reg_kernel<32>, dim3(rows), dim3(64), 0, st, S, s_stride, TM,
-                       tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
+  // register variants sized to the row: TPL tiles per lane, KR candidate columns
+#define OA_TOPK_REG(T, KK)                                                                     \
+  hipLaunchKernelGGL((topk_select_reg_kernel<T, KK>), dim3(rows), dim3(64), 0, st, S, s_stride,  \
+                     TM, tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top)
+  const int tpl = (ntiles + 63) / 64;
+  if (k_top <= 9 && tpl <= 9) OA_TOPK_REG(9, 9);
+  else if (k_top <= 16 && tpl <= 16) OA_TOPK_REG(16, 16);
+  else if (k_top <= 16 && tpl <= 32) OA_TOPK_REG(32, 16);
   else
     hipLaunchKernelGGL(topk_select_kernel, dim3(rows), dim3(64), 0, st, S, s_stride, TM, tm_stride,
                        ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
+#undef OA_TOPK_REG
   return OA_LAUNCH_STATUS();
 }
