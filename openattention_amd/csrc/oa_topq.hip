@@ -17,25 +17,30 @@
 // thread -- and every selection step works on those registers and on LDS.  Scores are
 // compared through their order-preserving 32-bit key; its top 2*LB bits (LB = 8, 7 or 6 for
 // C <= 64, 128, 256) form the "prefix" of a member:
-//   L1  per-cluster histogram of the top LB key bits (LDS atomics; lanes of one 64-position
-//       batch rarely share a cluster, so they rarely collide);
-//   T1  one thread per cluster: t = min(q_c, members, E - base_c) and the level-1 bin holding
-//       the t-th best member (scan from the top bin; histogram rows padded against bank
-//       conflicts);
-//   L2  for clusters whose level-1 bin must be split: histogram of the next LB key bits of
-//       that bin's members only;
+//   L1  per-cluster histogram of the top LB key bits (LDS atomics).  Histogram rows carry one
+//       pad word after every NB/16 bins, so the 16 threads that scan a row read 16 banks;
+//   T1  16 threads per cluster: t = min(q_c, members, E - base_c) and the level-1 bin b1 holding
+//       the t-th best member.  Members of bins above b1 are chosen; when bin b1 must be split
+//       the cluster goes to level 2;
+//   L2  for clusters being split: histogram of the next LB key bits of bin b1's members.  The
+//       same pass gathers every member at or above its cluster's level-1 bound (b1 and above:
+//       a few thousand of the row's members) into an LDS list -- per-thread hit masks, one
+//       scan per wave and one LDS atomic per wave, no per-member atomics;
 //   T2  the prefix P_c holding the t-th best member, `above` = members with a larger prefix,
 //       `need` = t - above of the members with prefix P_c;
-//   P4  members with a larger prefix are chosen; members with prefix P_c are staged in LDS as
-//       unique 64-bit keys (score key << 32 | ~position) when some must be dropped;
+//   F   one pass over the gathered list: members above P_c are chosen (written straight into
+//       their cluster's segment of the chosen-word list), members at P_c are staged as unique
+//       64-bit keys (score key << 32 | ~position) when some of them must be dropped.  When the
+//       level-1 set does not fit in LDS the gathering runs as its own pass after T2, with the
+//       final bounds;
 //   P5  one wave per staged cluster picks the `need` best staged keys (repeated wave maxima for
 //       small `need`, an MSB-first bitwise search on ballot counts otherwise); a cluster whose
 //       prefix bin does not fit in LDS is resolved by the same bitwise search run block-wide
 //       over the row, streamed again;
-//   P6  every chosen (cluster << 24 | position) word gets its rank among its cluster's chosen
-//       words by position (counting, or a bitonic sort when more than 1024 were chosen), lands
-//       in an LDS copy of the exp_idx row, and the row is written out once (-1 where a
-//       segment is short).
+//   P6  every chosen (cluster << 24 | position) word gets its rank among its cluster's words by
+//       position (counting, or a bitonic sort when more than 1024 were chosen), lands in an
+//       LDS copy of the exp_idx row, and the row is written out once (-1 where a segment is
+//       short).
 // Rows longer than 1024 * PPT positions are processed in segments that are re-read from
 // global memory (L2 / Infinity Cache) in each pass.  Rows are read in groups of four
 // positions, so both row strides are multiples of 4 and hold round_up(Lmax, 4) entries.
@@ -49,11 +54,12 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxC = 256;
 constexpr int kMaxE = 4096;
-constexpr int kMaxPos = 1 << 24;               // positions (< 2^24 - 1) are packed into 24 bits in P6
+constexpr int kMaxPos = 1 << 24;               // positions (< 2^24 - 1) are packed into 24 bits
 constexpr int kExtractMax = 40;                // need above this: bitwise threshold search
-constexpr int kBCapMax = 8192;                 // staged boundary keys (u64)
+constexpr int kUCapMax = 16384;                // gathered members (u64)
 constexpr int kRankMax = 1024;                 // above this many chosen words: bitonic sort
 constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
+constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster with no quota
 constexpr int kLdsLimit = 160 * 1024;
 
 enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3 };
@@ -64,8 +70,10 @@ struct TopqArgs {
   const float* quota; int C; int E; const int* n_dev;
   int32_t* exp_idx;
   int lb;          // bits per histogram level (8, 7 or 6)
-  int bcap;        // staged boundary capacity (u64 keys)
-  int cpow;        // power of two >= E for the P6 sort
+  int ucap;        // gathered-member list capacity (entries; 64 per-lane trash slots follow)
+  int hwords;      // ints of the area holding the histogram, then the staged keys, then the row
+  int gcap;        // staged-key capacity (u64 entries)
+  int cpow;        // power of two >= E: chosen-word list and the P6 sort
 };
 
 __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
@@ -73,13 +81,13 @@ __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
 }
 
 // append one chosen (cluster << 24 | position) word per taking lane, one LDS atomic per wave
-__device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t* cst, int* ctot,
+__device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t* cst, int* ctr,
                                               int lane) {
   const unsigned long long bal = __ballot(take);
   if (bal == 0ull) return;
   const int leader = __ffsll((long long)bal) - 1;
   int off = 0;
-  if (lane == leader) off = atomicAdd(ctot, __popcll(bal));
+  if (lane == leader) off = atomicAdd(ctr, __popcll(bal));
   off = __shfl(off, leader, 64);
   if (take) cst[off + __popcll(bal & ((1ull << lane) - 1ull))] = word;
 }
@@ -87,7 +95,7 @@ __device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t
 // P5 on one staged cluster: the `need` largest of cnt unique keys, held KR per lane
 template <int KR>
 __device__ void select_staged(const unsigned long long* src, int cnt, int need, int c,
-                              uint32_t* cst, int* ctot, int lane) {
+                              uint32_t* cst, int* ctr, int lane) {
   unsigned long long x[KR];
 #pragma unroll
   for (int j = 0; j < KR; ++j) x[j] = src[min(j * 64 + lane, cnt - 1)];
@@ -120,13 +128,13 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
   for (int j = 0; j < KR; ++j) {
     const bool take = x[j] != 0ull && x[j] >= T;
     const uint32_t pos = 0xffffffffu - (uint32_t)(x[j] & 0xffffffffull);
-    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctot, lane);
+    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctr, lane);
   }
 }
 
 // the same from LDS in a loop, for more than 1024 staged keys
 __device__ void select_staged_loop(const unsigned long long* src, int cnt, int need, int c,
-                                   uint32_t* cst, int* ctot, int lane) {
+                                   uint32_t* cst, int* ctr, int lane) {
   unsigned long long T = 0ull;
   for (int bit = 63; bit >= 0; --bit) {
     const unsigned long long cnd = T | (1ull << bit);
@@ -142,7 +150,42 @@ __device__ void select_staged_loop(const unsigned long long* src, int cnt, int n
     const unsigned long long x = src[min(j, cnt - 1)];
     const bool take = j < cnt && x >= T;
     const uint32_t pos = 0xffffffffu - (uint32_t)(x & 0xffffffffull);
-    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctot, lane);
+    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctr, lane);
+  }
+}
+
+// 16 threads (one DPP row) scan one padded histogram row of NB bins from the top: thread j holds
+// bins [j*bpt, (j+1)*bpt) in x[], ls = their sum, sfx = members in its bins and all bins above
+struct RowScan {
+  int x[16];
+  int ls, sfx;
+};
+__device__ __forceinline__ void scan_row(const int* row, int j, int bpt, RowScan& r) {
+  const int* h = row + j * (bpt + 1);
+  r.ls = 0;
+#pragma unroll
+  for (int b = 0; b < 16; ++b) {
+    r.x[b] = b < bpt ? h[min(b, bpt - 1)] : 0;
+    r.ls += r.x[b];
+  }
+  r.sfx = r.ls;
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
+    const int y = __shfl_down(r.sfx, off, 16);
+    if (j + off < 16) r.sfx += y;
+  }
+}
+// on the thread whose bins hold the t-th best member (sfx >= t > sfx - ls): the bin (local
+// index), the members above it, and the members in it
+__device__ __forceinline__ void find_bin(const RowScan& r, int bpt, int t, int& bin, int& acc,
+                                         int& cnt) {
+  acc = r.sfx - r.ls;
+  bin = 0;
+  cnt = 0;
+#pragma unroll
+  for (int b = 15; b >= 0; --b) {
+    if (b < bpt && cnt == 0 && acc + r.x[b] >= t) { bin = b; cnt = r.x[b]; }
+    else if (b < bpt && cnt == 0) acc += r.x[b];
   }
 }
 
@@ -150,21 +193,29 @@ template <int PPT>
 __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
   __shared__ int s_w[kMaxC];              // min(q_c, E - base_c), clamped at 0
-  __shared__ int s_base[kMaxC + 1];
-  __shared__ int s_t[kMaxC], s_above[kMaxC], s_bcnt[kMaxC];
-  __shared__ int s_b1[kMaxC];             // level-1 bin to split at level 2, or -1
-  __shared__ int s_thr[kMaxC];            // final prefix threshold P_c
-  __shared__ int s_pm[kMaxC];             // (P_c << 2) | mode, one lookup per position
-  __shared__ int s_mode[kMaxC], s_boff[kMaxC], s_bcur[kMaxC];
-  __shared__ int s_tpre[kMaxC + 1];
+  __shared__ int s_base[kMaxC + 1];       // first exp_idx slot of each cluster
+  __shared__ int s_t[kMaxC];              // members chosen
+  __shared__ int s_above[kMaxC];          // members with a prefix above the boundary prefix
+  __shared__ int s_bcnt[kMaxC];           // members in the boundary prefix bin
+  __shared__ int s_b1[kMaxC];             // level-1 bin split at level 2, or -1
+  __shared__ int s_thr[kMaxC];            // final boundary prefix P_c (2*LB bits)
+  __shared__ unsigned s_lo[kMaxC];        // members whose prefix is >= s_lo[c] are gathered
+  __shared__ int s_mode[kMaxC];
+  __shared__ int s_goff[kMaxC], s_gcur[kMaxC];   // staged keys: segment start, fill count
+  __shared__ int s_ccur[kMaxC];           // chosen words written per cluster
+  __shared__ int s_tpre[kMaxC + 1];       // chosen-word segment start per cluster
   __shared__ int s_fbl[kMaxC];
-  __shared__ int s_bused, s_nfb, s_ctot, s_fbcnt[3];
+  __shared__ int s_gused, s_nfb, s_nsplit, s_hits1, s_ucnt, s_fbcnt[3];
   const int NB = 1 << a.lb;
-  const int HS = NB + 4;                  // padded histogram row (16-byte aligned)
-  unsigned long long* s_bst = dyn;                                    // bcap
-  uint32_t* s_cst = reinterpret_cast<uint32_t*>(dyn + a.bcap);        // cpow
-  int* s_out = reinterpret_cast<int*>(s_cst + a.cpow);                // cpow (E used)
-  int* s_hist = s_out + a.cpow;                                       // C * HS + 64 trash
+  const int HS = NB + 16;                 // histogram row: a pad word after every NB/16 bins
+  const int sb = a.lb - 4;                // bin b sits at word b + (b >> sb) of its row
+  const int bpt = NB >> 4;                // bins per scanning thread
+  uint32_t* s_uw = reinterpret_cast<uint32_t*>(dyn);                         // ucap + 64
+  uint32_t* s_uk = s_uw + a.ucap + 64;                                        // ucap + 64
+  int* s_hist = reinterpret_cast<int*>(dyn + a.ucap + 64);                    // hwords
+  unsigned long long* s_g = reinterpret_cast<unsigned long long*>(s_hist);    // after T2
+  int* s_out = s_hist;                                                        // after P5
+  uint32_t* s_cst = reinterpret_cast<uint32_t*>(s_hist + a.hwords);           // cpow
 
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -172,13 +223,14 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   const int lane = tid & 63;
   const int C = a.C, E = a.E;
   const int sh1 = 32 - a.lb, sh2 = 32 - 2 * a.lb;
+  const int sh1p = sh1 + sb, sh2p = sh2 + sb;   // shifts giving a bin's pad-word count
   const int trash = C * HS + lane;        // per-lane histogram slot for non-members
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
   const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
   int32_t* erow = a.exp_idx + (long)row * E;
 
-  // ---- P0: quota prefix, per-cluster state, histogram and output clear
+  // ---- P0: quota prefix, per-cluster state, histogram clear
   if (wave == 0) {
     int v[4], loc = 0;
 #pragma unroll
@@ -205,18 +257,21 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (lane == 63) s_base[kMaxC] = incl;
   }
   for (int c = tid; c < kMaxC; c += kThreads) {
-    s_t[c] = 0; s_mode[c] = kModeNone; s_bcur[c] = 0; s_b1[c] = -1; s_thr[c] = 0;
+    s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_b1[c] = -1; s_thr[c] = 0; s_lo[c] = kNoGather;
+    s_mode[c] = kModeNone; s_goff[c] = 0; s_gcur[c] = 0; s_ccur[c] = 0;
   }
   for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
-  for (int i = tid; i < a.cpow / 4 + 1; i += kThreads)
-    if (4 * i < E) reinterpret_cast<int4*>(s_out)[i] = make_int4(-1, -1, -1, -1);
-  if (tid == 0) { s_bused = 0; s_nfb = 0; s_ctot = 0; s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0; }
+  if (tid == 0) {
+    s_gused = 0; s_nfb = 0; s_nsplit = 0; s_hits1 = 0; s_ucnt = 0;
+    s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0;
+  }
   __syncthreads();
 
   // register i of a thread holds position sg*SEG + (i/4)*4096 + 4*tid + i%4: each group of four
   // consecutive positions arrives as one float4 of scores and one u32 of cluster ids
   constexpr int SEG = kThreads * PPT;
   constexpr int NG = PPT / 4;
+  constexpr int CH = 12;         // positions whose per-cluster lookups are issued together
   static_assert(PPT % 4 == 0, "PPT must be a multiple of 4");
   const int nseg = n > 0 ? (n + SEG - 1) / SEG : 0;
   uint32_t kk[PPT];              // score key of a qualifying member, else 0
@@ -237,141 +292,170 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       kk[4 * g + 2] = __float_as_uint(v.z);
       kk[4 * g + 3] = __float_as_uint(v.w);
     }
+    const int lim = n - sg * SEG - 4 * tid;   // register i is in the row iff (i/4)*4096 + i%4 < lim
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
-      const bool q = pos_of(sg, i) < n && key > kNegInfKey;
+      const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
       kk[i] = q ? key : 0u;
     }
   };
   auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+
+  // append the members flagged in hb (bit i = register i) to the gathered list: an exclusive
+  // scan of the per-thread counts inside the wave, one LDS atomic per wave for its base.  Every
+  // register is written: a member to the next list slot, anything else to the lane's trash slot
+  // (the histograms bound the list size, so the slots never run past ucap)
+  auto gather = [&](int sg, unsigned long long hb) {
+    const int cnt = __popcll(hb);
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const int tot = __shfl(incl, 63, 64);
+    int wbase = 0;
+    if (lane == 0 && tot > 0) wbase = atomicAdd(&s_ucnt, tot);
+    wbase = __shfl(wbase, 0, 64);
+    const int tr = a.ucap + lane;
+    int d = wbase + incl - cnt - tr;           // next list slot, relative to the trash slot
+    const int pbase = sg * SEG + 4 * tid;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int hit = (int)((hb >> i) & 1ull);
+      const int dst = tr + __mul24(hit, d);
+      s_uw[dst] = ((uint32_t)cid(i) << 24) | (uint32_t)(pbase + (i >> 2) * 4096 + (i & 3));
+      s_uk[dst] = kk[i];
+      d += hit;
+    }
+  };
+
+  // T2 on the level-2 histogram: prefix P_c of the t-th best member of each split cluster and
+  // the staging plan for its boundary bin
+  auto t2 = [&]() {
+    for (int cb = 0; cb < C; cb += kThreads / 16) {
+      const int c = cb + (tid >> 4);
+      const int j = tid & 15;
+      const int b1 = c < C ? s_b1[c] : -1;
+      if (b1 < 0) continue;      // uniform over the cluster's 16 threads
+      RowScan r;
+      scan_row(s_hist + c * HS, j, bpt, r);
+      const int t2 = s_t[c] - s_above[c];        // rank of the t-th member inside bin b1
+      if (r.sfx >= t2 && r.sfx - r.ls < t2) {
+        int b, acc, cnt;
+        find_bin(r, bpt, t2, b, acc, cnt);
+        const int need = t2 - acc;
+        const int P = (b1 << a.lb) | (j * bpt + b);
+        s_above[c] = s_above[c] + acc;
+        s_bcnt[c] = cnt;
+        s_thr[c] = P;
+        int mode = kModeAll;
+        unsigned lo = (unsigned)P;
+        if (need < cnt) {
+          const int off = atomicAdd(&s_gused, cnt);
+          if (off + cnt <= a.gcap) {
+            mode = kModeStaged;
+            s_goff[c] = off;
+          } else {               // boundary bin too large for LDS: resolved block-wide in P5
+            mode = kModeBlock;
+            lo = (unsigned)P + 1u;
+            s_fbl[atomicAdd(&s_nfb, 1)] = c;
+          }
+        }
+        s_mode[c] = mode;
+        s_lo[c] = lo;
+      }
+    }
+  };
+  auto clear_hist = [&]() {
+    for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
+  };
 
   // ---- L1: histogram of the top LB key bits per cluster
   for (int sg = 0; sg < nseg; ++sg) {
     load(sg);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      // branchless: a non-member counts into this lane's own trash slot
-      const int at = kk[i] ? (int)__umul24(cid(i), HS) + (int)(kk[i] >> sh1) : trash;
-      atomicAdd(&s_hist[at], 1);
+      const uint32_t k = kk[i];
+      int slot = (int)__umul24(cid(i), HS) + (int)(k >> sh1) + (int)(k >> sh1p);
+      asm volatile("" : "+v"(slot));   // computed in every lane: a select, not a branch
+      atomicAdd(&s_hist[k ? slot : trash], 1);
     }
   }
   __syncthreads();
 
-  // ---- T1: level-1 bin of the t-th best member.  16 threads per cluster (one DPP row), each
-  // holding NB/16 consecutive bins: a suffix scan over the 16 partial counts finds the thread
-  // whose bins hold the t-th best member, which finishes in registers.
+  // ---- T1: level-1 bin of the t-th best member, 16 threads per cluster
   for (int cb = 0; cb < C; cb += kThreads / 16) {
     const int c = cb + (tid >> 4);
     const int j = tid & 15;
-    int x[16];
-    int ls = 0;
-    const int bpt = NB >> 4;
     const int w = c < C ? s_w[c] : 0;
-    const int* h = s_hist + min(c, C - 1) * HS + j * bpt;
-#pragma unroll
-    for (int b = 0; b < 16; ++b) {
-      x[b] = b < bpt ? h[min(b, bpt - 1)] : 0;
-      ls += x[b];
-    }
-    int sfx = ls;                // members in this thread's bins and above
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-      const int y = __shfl_down(sfx, off, 16);
-      if (j + off < 16) sfx += y;
-    }
-    const int m = __shfl(sfx, 0, 16);
+    RowScan r;
+    scan_row(s_hist + min(c, C - 1) * HS, j, bpt, r);
+    const int m = __shfl(r.sfx, 0, 16);
     if (c < C && w > 0) {
       const int t = min(w, m);
-      if (t < w || m == 0) {     // at most w members: all of them (every prefix >= 0)
+      if (t > 0 && t == m) {     // every member is chosen
         if (j == 0) {
-          s_t[c] = t;
-          if (t > 0) { s_mode[c] = kModeAll; s_above[c] = 0; s_bcnt[c] = t; s_thr[c] = 0; }
+          s_t[c] = t; s_mode[c] = kModeAll; s_thr[c] = 0; s_lo[c] = 1u;
+          atomicAdd(&s_hits1, t);
         }
-      } else if (sfx >= t && sfx - ls < t) {
-        int acc = sfx - ls, b1 = j * bpt, cnt = 0;
-#pragma unroll
-        for (int b = 15; b >= 0; --b) {
-          if (b < bpt && cnt == 0 && acc + x[b] >= t) { b1 = j * bpt + b; cnt = x[b]; }
-          else if (b < bpt && cnt == 0) acc += x[b];
-        }
+      } else if (t > 0 && r.sfx >= t && r.sfx - r.ls < t) {
+        int b, acc, cnt;
+        find_bin(r, bpt, t, b, acc, cnt);
+        const int b1 = j * bpt + b;
         s_t[c] = t;
         s_above[c] = acc;
+        s_bcnt[c] = cnt;
+        // members have a prefix >= 8, so a bound of 1 gathers all of them and no non-member
+        s_lo[c] = max((unsigned)b1 << a.lb, 1u);
         if (t - acc == cnt) {    // the whole level-1 bin completes t: no split
-          s_bcnt[c] = cnt; s_mode[c] = kModeAll; s_thr[c] = b1 << a.lb;
-        } else {                 // split this bin at level 2
-          s_b1[c] = b1;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
-  __syncthreads();
-
-  // ---- L2: next LB key bits of the members of each split level-1 bin
-  for (int sg = 0; sg < nseg; ++sg) {
-    if (nseg > 1) load(sg);
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int c = cid(i);
-      const bool in = kk[i] && (int)(kk[i] >> sh1) == s_b1[c];
-      const int at = in ? (int)__umul24(c, HS) + (int)((kk[i] >> sh2) & (NB - 1)) : trash;
-      atomicAdd(&s_hist[at], 1);
-    }
-  }
-  __syncthreads();
-
-  // ---- T2: prefix P_c of the t-th best member of each split cluster, staging plan (same
-  // 16-threads-per-cluster scan over the level-2 histogram)
-  for (int cb = 0; cb < C; cb += kThreads / 16) {
-    const int c = cb + (tid >> 4);
-    const int j = tid & 15;
-    const int b1 = c < C ? s_b1[c] : -1;
-    if (b1 < 0) continue;        // uniform over the cluster's 16 threads
-    int x[16];
-    int ls = 0;
-    const int bpt = NB >> 4;
-    const int* h = s_hist + c * HS + j * bpt;
-#pragma unroll
-    for (int b = 0; b < 16; ++b) {
-      x[b] = b < bpt ? h[min(b, bpt - 1)] : 0;
-      ls += x[b];
-    }
-    int sfx = ls;
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-      const int y = __shfl_down(sfx, off, 16);
-      if (j + off < 16) sfx += y;
-    }
-    const int t2 = s_t[c] - s_above[c];          // rank of the t-th member inside bin b1
-    if (sfx >= t2 && sfx - ls < t2) {
-      int acc = sfx - ls, b2 = j * bpt, cnt = 0;
-#pragma unroll
-      for (int b = 15; b >= 0; --b) {
-        if (b < bpt && cnt == 0 && acc + x[b] >= t2) { b2 = j * bpt + b; cnt = x[b]; }
-        else if (b < bpt && cnt == 0) acc += x[b];
-      }
-      const int need = t2 - acc;
-      s_above[c] = s_above[c] + acc;
-      s_bcnt[c] = cnt;
-      s_thr[c] = (b1 << a.lb) | b2;
-      int mode = kModeAll;
-      if (need < cnt) {
-        const int off = atomicAdd(&s_bused, cnt);
-        if (off + cnt <= a.bcap) {
-          mode = kModeStaged;
-          s_boff[c] = off;
+          s_mode[c] = kModeAll; s_thr[c] = b1 << a.lb;
         } else {
-          mode = kModeBlock;
-          s_fbl[atomicAdd(&s_nfb, 1)] = c;
+          s_b1[c] = b1;
+          atomicAdd(&s_nsplit, 1);
         }
+        atomicAdd(&s_hits1, acc + cnt);
       }
-      s_mode[c] = mode;
     }
   }
   __syncthreads();
-  if (wave == 0) {               // prefix of t over clusters: first chosen word of each cluster
+  const bool split = s_nsplit > 0;
+  const bool fits = s_hits1 <= a.ucap;   // block-uniform: the level-1 set fits in the list
+
+  if (split && !fits) {
+    // ---- L2 (registers): next LB key bits of the members of each split level-1 bin, over the
+    // whole row; the gathering then runs with the final bounds
+    clear_hist();
+    __syncthreads();
+    for (int sg = 0; sg < nseg; ++sg) {
+      if (nseg > 1) load(sg);
+#pragma unroll
+      for (int i0 = 0; i0 < PPT; i0 += CH) {
+        int b1v[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+          if (i0 + j < PPT) b1v[j] = s_b1[cid(i0 + j)];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          if (i0 + j < PPT) {
+            const int i = i0 + j;
+            const uint32_t k = kk[i];
+            const bool in = k && (int)(k >> sh1) == b1v[j];
+            int slot = (int)__umul24(cid(i), HS) + (int)((k >> sh2) & (NB - 1)) +
+                       (int)((k >> sh2p) & 15u);
+            asm volatile("" : "+v"(slot));
+            atomicAdd(&s_hist[in ? slot : trash], 1);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    t2();
+    __syncthreads();
+  }
+
+  if (wave == 0) {               // prefix of t over clusters: chosen-word segment of each cluster
     int v[4], loc = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[i] = s_t[lane * 4 + i]; loc += v[i]; }
@@ -387,30 +471,56 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (lane == 63) s_tpre[kMaxC] = incl;
   }
 
-  for (int c = tid; c < kMaxC; c += kThreads) s_pm[c] = (s_thr[c] << 2) | s_mode[c];
-  __syncthreads();
-
-  // ---- P4: chosen members above P_c, staged members at P_c
+  // ---- G: gather every member whose prefix reaches its cluster's bound (the level-1 bound, or
+  // the final one when the level-2 histogram came from the registers)
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
+    unsigned long long hb = 0ull;
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      bool take = false, stage = false;
-      int c = 0;
-      if (kk[i]) {
-        c = cid(i);
-        const int pm = s_pm[c];
-        const int mode = pm & 3;
-        const int pf = (int)(kk[i] >> sh2);
-        const int P = pm >> 2;
-        take = mode != kModeNone && (pf > P || (pf == P && mode == kModeAll));
-        stage = pf == P && mode == kModeStaged;
-      }
-      if (__ballot(take || stage) == 0ull) continue;      // the common case: nothing here
-      const int p = pos_of(sg, i);
-      append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst, &s_ctot, lane);
-      if (stage) s_bst[s_boff[c] + atomicAdd(&s_bcur[c], 1)] = key64(kk[i], p);
+    for (int i0 = 0; i0 < PPT; i0 += CH) {
+      unsigned lov[CH];
+#pragma unroll
+      for (int j = 0; j < CH; ++j)
+        if (i0 + j < PPT) lov[j] = s_lo[cid(i0 + j)];
+#pragma unroll
+      for (int j = 0; j < CH; ++j)
+        if (i0 + j < PPT && (kk[i0 + j] >> sh2) >= lov[j]) hb |= 1ull << (i0 + j);
     }
+    gather(sg, hb);
+  }
+  __syncthreads();
+  const int ucnt = min(s_ucnt, a.ucap);
+
+  if (split && fits) {
+    // ---- L2 (list): the gathered set holds every member of each split bin
+    clear_hist();
+    __syncthreads();
+    for (int j = tid; j < ucnt; j += kThreads) {
+      const int c = (int)(s_uw[j] >> 24);
+      const uint32_t k = s_uk[j];
+      if ((int)(k >> sh1) == s_b1[c]) {
+        const uint32_t b2 = (k >> sh2) & (NB - 1);
+        atomicAdd(&s_hist[c * HS + (int)b2 + (int)(b2 >> sb)], 1);
+      }
+    }
+    __syncthreads();
+    t2();
+    __syncthreads();
+  }
+
+  // ---- F: gathered members above P_c are chosen, members at P_c of a staged cluster staged
+  for (int j = tid; j < ucnt; j += kThreads) {
+    const uint32_t e = s_uw[j];
+    const uint32_t key = s_uk[j];
+    const int c = (int)(e >> 24);
+    const int pos = (int)(e & 0xffffffu);
+    const int pf = (int)(key >> sh2);
+    const int P = s_thr[c];
+    const int mode = s_mode[c];
+    if (pf > P || (pf == P && mode == kModeAll))
+      s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos;
+    else if (pf == P && mode == kModeStaged)
+      s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(key, pos);
   }
   __syncthreads();
 
@@ -419,11 +529,12 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (s_mode[c] != kModeStaged) continue;
     const int cnt = s_bcnt[c];
     const int need = s_t[c] - s_above[c];
-    const unsigned long long* src = s_bst + s_boff[c];
-    if (cnt <= 64) select_staged<1>(src, cnt, need, c, s_cst, &s_ctot, lane);
-    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, s_cst, &s_ctot, lane);
-    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, s_cst, &s_ctot, lane);
-    else select_staged_loop(src, cnt, need, c, s_cst, &s_ctot, lane);
+    const unsigned long long* src = s_g + s_goff[c];
+    uint32_t* dst = s_cst + s_tpre[c];
+    if (cnt <= 64) select_staged<1>(src, cnt, need, c, dst, &s_ccur[c], lane);
+    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, dst, &s_ccur[c], lane);
+    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, dst, &s_ccur[c], lane);
+    else select_staged_loop(src, cnt, need, c, dst, &s_ccur[c], lane);
   }
   // clusters whose prefix bin did not fit in LDS: block-wide bitwise search, re-streaming the
   // row (rare; keeps the row's registers dead during P5)
@@ -459,7 +570,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         const int p = pos_of(sg, i);
         const bool take = kk[i] && cid(i) == c && (int)(kk[i] >> sh2) == P &&
                           key64(kk[i], p) >= T;
-        append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst, &s_ctot, lane);
+        append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst + s_tpre[c], &s_ccur[c], lane);
       }
     }
     __syncthreads();
@@ -467,27 +578,18 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     __syncthreads();
   }
   __syncthreads();
+  for (int sl = tid; sl < E; sl += kThreads) s_out[sl] = -1;   // the staged keys are dead
+  __syncthreads();
 
   // ---- P6: each chosen word's rank inside its cluster (by position), into the LDS row copy
-  const int total = s_ctot;      // == sum_c t_c
-  if (total <= kRankMax && 2 * a.bcap >= a.cpow) {
-    // group the words by cluster (segment tpre_c .. tpre_c + t_c of the staging area, free
-    // after P5), then rank each word among its own cluster's words only
-    uint32_t* s_grp = reinterpret_cast<uint32_t*>(s_bst);
-    for (int c = tid; c < C; c += kThreads) s_bcur[c] = 0;
-    __syncthreads();
+  const int total = s_tpre[kMaxC];   // == sum_c t_c; every cluster's segment is full
+  if (total <= kRankMax) {
     for (int j = tid; j < total; j += kThreads) {
       const uint32_t w = s_cst[j];
       const int c = (int)(w >> 24);
-      s_grp[s_tpre[c] + atomicAdd(&s_bcur[c], 1)] = w;
-    }
-    __syncthreads();
-    for (int j = tid; j < total; j += kThreads) {
-      const uint32_t w = s_grp[j];
-      const int c = (int)(w >> 24);
       const int b = s_tpre[c], t = s_t[c];
       int rank = 0;
-      for (int k = b; k < b + t; ++k) rank += s_grp[k] < w ? 1 : 0;
+      for (int k = b; k < b + t; ++k) rank += s_cst[k] < w ? 1 : 0;
       s_out[s_base[c] + rank] = (int)(w & 0xffffffu);
     }
   } else {
@@ -542,16 +644,20 @@ extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long 
   TopqArgs a;
   a.S = S; a.s_stride = s_stride; a.asg8 = asg8; a.a_stride = asg8_stride; a.quota = quota;
   a.C = C; a.E = E; a.n_dev = n_dev; a.exp_idx = exp_idx;
-  // bits per histogram level: 8, 7 or 6, so that C * (2^lb + 4) ints stay near 64 KiB
+  // bits per histogram level: 8, 7 or 6, so that C * (2^lb + 16) ints stay near 64 KiB
   a.lb = C <= 64 ? 8 : (C <= 128 ? 7 : 6);
   a.cpow = 4;                   // >= 4: the LDS rows are cleared and scanned 4 words at a time
   while (a.cpow < E) a.cpow <<= 1;
-  const size_t static_lds = sizeof(int) * (16 * kMaxC + 8);
-  const size_t fixed = sizeof(uint32_t) * 2 * a.cpow + sizeof(int) * ((size_t)C * ((1 << a.lb) + 4) + 64);
-  const long room = (long)kLdsLimit - (long)static_lds - (long)fixed;
-  a.bcap = (int)std::min<long>(kBCapMax, room / 8) & ~3;   // keeps the LDS arrays 16-byte aligned
-  if (a.bcap < 64) return OA_EINVAL;
-  const size_t lds = sizeof(unsigned long long) * a.bcap + fixed;
+  // dynamic LDS: gathered list (ucap + 64 trash entries: a word array and a key array) |
+  // histogram -> staged keys -> output row (hwords ints) | chosen words (cpow u32)
+  const long hist = (long)C * ((1 << a.lb) + 16) + 64;
+  a.hwords = (int)((std::max<long>(hist, a.cpow) + 3) & ~3L);
+  const long static_lds = (long)sizeof(int) * (16 * kMaxC + 8);
+  const long room = (long)kLdsLimit - static_lds - 4L * a.hwords - 4L * a.cpow - 8L * 64;
+  a.ucap = (int)std::min<long>(kUCapMax, room / 8) & ~3;   // keeps the histogram 16-byte aligned
+  a.gcap = std::min(a.hwords / 2, a.ucap - E);             // the final gathering fits in ucap
+  if (a.gcap < 64) return OA_EINVAL;
+  const size_t lds = 8 * (size_t)(a.ucap + 64) + 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
   hipStream_t s = (hipStream_t)stream;
   if (Lmax <= kThreads * 8) return launch_row<8>(a, rows, lds, s);
   if (Lmax <= kThreads * 16) return launch_row<16>(a, rows, lds, s);

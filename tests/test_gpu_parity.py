@@ -321,6 +321,36 @@ def test_topq_adversarial_quotas(n, C, E, seed):
     assert np.array_equal(got, ref), f"rows differ: {np.nonzero((got != ref).any(1))[0]}"
 
 
+@pytest.mark.parametrize("n,C,E,seed", [(30000, 2, 300, 4), (60000, 4, 512, 5)])
+def test_topq_level1_set_exceeds_list(n, C, E, seed):
+    """Top-q when a row's level-1 boundary bins hold more members than the LDS gathering list:
+    every score sits in [1, 2) on a grid of eight values, so each cluster's level-1 bin holds all
+    of its members and each level-2 bin thousands (the register level-2 pass, the gathering with
+    final bounds, and the block-wide search for boundary bins too large to stage).  n = 60000 is
+    past one register segment (streamed twice per pass)."""
+    print(f"[case] topq level-1 overflow n={n} C={C} E={E}", flush=True)
+    rng = np.random.default_rng(seed)
+    R, Lmax = 3, -(-(n + 300) // 64) * 64
+    S = (1.0 + rng.integers(0, 8, size=(R, Lmax)) / 8.0).astype(np.float32)
+    asg = rng.integers(0, C, size=(R, Lmax)).astype(np.int32)
+    asg[:, n:] = 0
+    sel = np.stack([rng.choice(n, 16, replace=False) for _ in range(R)]).astype(np.int32)
+    for r in range(R):
+        S[r, sel[r]] = -np.inf
+    quota = np.zeros((R, C), np.float32)
+    quota[0] = E // C                  # every cluster split inside its level-1 bin
+    quota[1, 0] = 7                    # one small quota
+    quota[2] = rng.integers(1, E // C, size=C)
+    ref = O.topq(S, asg, sel, quota, n, E)
+    exp_idx = torch.full((R, E), 12345, device=DEV, dtype=torch.int32)
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    asg8 = torch.from_numpy(asg.astype(np.uint8)).to(DEV)
+    ops.topq(_f32(S), asg8, _f32(quota), exp_idx, n_dev)
+    torch.cuda.synchronize()
+    got = exp_idx.cpu().numpy()
+    assert np.array_equal(got, ref), f"rows differ: {np.nonzero((got != ref).any(1))[0]}"
+
+
 def test_decode_sequence_groups_match_single_chain(lay4k):
     """Running the stage chain per sequence group on separate streams gives the same bits as
     one chain over the whole batch (captured in a graph and replayed, and eagerly)."""
