@@ -58,6 +58,7 @@ constexpr int kMaxPos = 1 << 24;               // positions (< 2^24 - 1) are pac
 constexpr int kExtractMax = 40;                // need above this: bitwise threshold search
 constexpr int kUCapMax = 16384;                // gathered members (u64)
 constexpr int kRankMax = 1024;                 // above this many chosen words: bitonic sort
+constexpr int kUPT = 8;                        // gathered entries per thread handled together
 constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
 constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster with no quota
 constexpr int kLdsLimit = 160 * 1024;
@@ -80,6 +81,14 @@ __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
   return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (unsigned)pos);
 }
 
+// Staged keys of one cluster share their top 2*LB bits (the prefix P) and, since positions are
+// below 2^24, bits 24..31 of the inverted position: a bitwise threshold search starts from those
+// bits (key64_floor) and decides only the others, from bit 63 - 2*LB down, skipping 31..24.
+__device__ __forceinline__ unsigned long long key64_floor(int P, int lb2) {
+  return ((unsigned long long)(unsigned)P << (64 - lb2)) | 0xff000000ull;
+}
+__device__ __forceinline__ int next_free_bit(int bit) { return bit == 32 ? 23 : bit - 1; }
+
 // append one chosen (cluster << 24 | position) word per taking lane, one LDS atomic per wave
 __device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t* cst, int* ctr,
                                               int lane) {
@@ -94,8 +103,8 @@ __device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t
 
 // P5 on one staged cluster: the `need` largest of cnt unique keys, held KR per lane
 template <int KR>
-__device__ void select_staged(const unsigned long long* src, int cnt, int need, int c,
-                              uint32_t* cst, int* ctr, int lane) {
+__device__ void select_staged(const unsigned long long* src, int cnt, int need, int c, int P,
+                              int lb2, uint32_t* cst, int* ctr, int lane) {
   unsigned long long x[KR];
 #pragma unroll
   for (int j = 0; j < KR; ++j) x[j] = src[min(j * 64 + lane, cnt - 1)];
@@ -116,7 +125,8 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
       T = best;
     }
   } else {
-    for (int bit = 63; bit >= 0; --bit) {
+    T = key64_floor(P, lb2);
+    for (int bit = 63 - lb2; bit >= 0; bit = next_free_bit(bit)) {
       const unsigned long long cnd = T | (1ull << bit);
       int k = 0;
 #pragma unroll
@@ -133,10 +143,10 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
 }
 
 // the same from LDS in a loop, for more than 1024 staged keys
-__device__ void select_staged_loop(const unsigned long long* src, int cnt, int need, int c,
-                                   uint32_t* cst, int* ctr, int lane) {
-  unsigned long long T = 0ull;
-  for (int bit = 63; bit >= 0; --bit) {
+__device__ void select_staged_loop(const unsigned long long* src, int cnt, int need, int c, int P,
+                                   int lb2, uint32_t* cst, int* ctr, int lane) {
+  unsigned long long T = key64_floor(P, lb2);
+  for (int bit = 63 - lb2; bit >= 0; bit = next_free_bit(bit)) {
     const unsigned long long cnd = T | (1ull << bit);
     int k = 0;
     for (int b0 = 0; b0 < cnt; b0 += 64) {
@@ -154,42 +164,46 @@ __device__ void select_staged_loop(const unsigned long long* src, int cnt, int n
   }
 }
 
-// 16 threads (one DPP row) scan one padded histogram row of NB bins from the top: thread j holds
-// bins [j*bpt, (j+1)*bpt) in x[], ls = their sum, sfx = members in its bins and all bins above
+// 16 threads (one DPP row) scan one padded histogram row of NB = 16 * BPT bins from the top:
+// thread j holds bins [j*BPT, (j+1)*BPT) in x[], ls = their sum, sfx = members in its bins and
+// all bins above (a suffix scan on row_shl DPP moves: lanes past the row's end read 0)
+template <int BPT>
 struct RowScan {
-  int x[16];
+  int x[BPT];
   int ls, sfx;
 };
-__device__ __forceinline__ void scan_row(const int* row, int j, int bpt, RowScan& r) {
-  const int* h = row + j * (bpt + 1);
+template <int BPT>
+__device__ __forceinline__ void scan_row(const int* row, int j, RowScan<BPT>& r) {
+  const int* h = row + j * (BPT + 1);
   r.ls = 0;
 #pragma unroll
-  for (int b = 0; b < 16; ++b) {
-    r.x[b] = b < bpt ? h[min(b, bpt - 1)] : 0;
+  for (int b = 0; b < BPT; ++b) {
+    r.x[b] = h[b];
     r.ls += r.x[b];
   }
-  r.sfx = r.ls;
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) {
-    const int y = __shfl_down(r.sfx, off, 16);
-    if (j + off < 16) r.sfx += y;
-  }
+  int v = r.ls;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x101, 0xf, 0xf, false);   // row_shl:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x102, 0xf, 0xf, false);   // row_shl:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0xf, false);   // row_shl:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0xf, false);   // row_shl:8
+  r.sfx = v;
 }
 // on the thread whose bins hold the t-th best member (sfx >= t > sfx - ls): the bin (local
 // index), the members above it, and the members in it
-__device__ __forceinline__ void find_bin(const RowScan& r, int bpt, int t, int& bin, int& acc,
+template <int BPT>
+__device__ __forceinline__ void find_bin(const RowScan<BPT>& r, int t, int& bin, int& acc,
                                          int& cnt) {
   acc = r.sfx - r.ls;
   bin = 0;
   cnt = 0;
 #pragma unroll
-  for (int b = 15; b >= 0; --b) {
-    if (b < bpt && cnt == 0 && acc + r.x[b] >= t) { bin = b; cnt = r.x[b]; }
-    else if (b < bpt && cnt == 0) acc += r.x[b];
+  for (int b = BPT - 1; b >= 0; --b) {
+    if (cnt == 0 && acc + r.x[b] >= t) { bin = b; cnt = r.x[b]; }
+    else if (cnt == 0) acc += r.x[b];
   }
 }
 
-template <int PPT>
+template <int PPT, int LB>
 __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
   __shared__ int s_w[kMaxC];              // min(q_c, E - base_c), clamped at 0
@@ -206,10 +220,10 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   __shared__ int s_tpre[kMaxC + 1];       // chosen-word segment start per cluster
   __shared__ int s_fbl[kMaxC];
   __shared__ int s_gused, s_nfb, s_nsplit, s_hits1, s_ucnt, s_fbcnt[3];
-  const int NB = 1 << a.lb;
-  const int HS = NB + 16;                 // histogram row: a pad word after every NB/16 bins
-  const int sb = a.lb - 4;                // bin b sits at word b + (b >> sb) of its row
-  const int bpt = NB >> 4;                // bins per scanning thread
+  constexpr int NB = 1 << LB;
+  constexpr int HS = NB + 16;             // histogram row: a pad word after every NB/16 bins
+  constexpr int sb = LB - 4;              // bin b sits at word b + (b >> sb) of its row
+  constexpr int bpt = NB >> 4;            // bins per scanning thread
   uint32_t* s_uw = reinterpret_cast<uint32_t*>(dyn);                         // ucap + 64
   uint32_t* s_uk = s_uw + a.ucap + 64;                                        // ucap + 64
   int* s_hist = reinterpret_cast<int*>(dyn + a.ucap + 64);                    // hwords
@@ -222,8 +236,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int C = a.C, E = a.E;
-  const int sh1 = 32 - a.lb, sh2 = 32 - 2 * a.lb;
-  const int sh1p = sh1 + sb, sh2p = sh2 + sb;   // shifts giving a bin's pad-word count
+  constexpr int sh1 = 32 - LB, sh2 = 32 - 2 * LB;
+  constexpr int sh1p = sh1 + sb, sh2p = sh2 + sb;   // shifts giving a bin's pad-word count
   const int trash = C * HS + lane;        // per-lane histogram slot for non-members
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
@@ -321,13 +335,15 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     const int tr = a.ucap + lane;
     int d = wbase + incl - cnt - tr;           // next list slot, relative to the trash slot
     const int pbase = sg * SEG + 4 * tid;
+    const uint32_t hlo = (uint32_t)hb, hhi = (uint32_t)(hb >> 32);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int hit = (int)((hb >> i) & 1ull);
-      const int dst = tr + __mul24(hit, d);
+      // 0 or -1: bit i of hb, sign-extended
+      const int m = __builtin_amdgcn_sbfe((int)(i < 32 ? hlo : hhi), i & 31, 1);
+      const int dst = tr + (d & m);
       s_uw[dst] = ((uint32_t)cid(i) << 24) | (uint32_t)(pbase + (i >> 2) * 4096 + (i & 3));
       s_uk[dst] = kk[i];
-      d += hit;
+      d -= m;
     }
   };
 
@@ -339,14 +355,14 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       const int j = tid & 15;
       const int b1 = c < C ? s_b1[c] : -1;
       if (b1 < 0) continue;      // uniform over the cluster's 16 threads
-      RowScan r;
-      scan_row(s_hist + c * HS, j, bpt, r);
+      RowScan<bpt> r;
+      scan_row(s_hist + c * HS, j, r);
       const int t2 = s_t[c] - s_above[c];        // rank of the t-th member inside bin b1
       if (r.sfx >= t2 && r.sfx - r.ls < t2) {
         int b, acc, cnt;
-        find_bin(r, bpt, t2, b, acc, cnt);
+        find_bin(r, t2, b, acc, cnt);
         const int need = t2 - acc;
-        const int P = (b1 << a.lb) | (j * bpt + b);
+        const int P = (b1 << LB) | (j * bpt + b);
         s_above[c] = s_above[c] + acc;
         s_bcnt[c] = cnt;
         s_thr[c] = P;
@@ -390,8 +406,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     const int c = cb + (tid >> 4);
     const int j = tid & 15;
     const int w = c < C ? s_w[c] : 0;
-    RowScan r;
-    scan_row(s_hist + min(c, C - 1) * HS, j, bpt, r);
+    RowScan<bpt> r;
+    scan_row(s_hist + min(c, C - 1) * HS, j, r);
     const int m = __shfl(r.sfx, 0, 16);
     if (c < C && w > 0) {
       const int t = min(w, m);
@@ -402,15 +418,15 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         }
       } else if (t > 0 && r.sfx >= t && r.sfx - r.ls < t) {
         int b, acc, cnt;
-        find_bin(r, bpt, t, b, acc, cnt);
+        find_bin(r, t, b, acc, cnt);
         const int b1 = j * bpt + b;
         s_t[c] = t;
         s_above[c] = acc;
         s_bcnt[c] = cnt;
         // members have a prefix >= 8, so a bound of 1 gathers all of them and no non-member
-        s_lo[c] = max((unsigned)b1 << a.lb, 1u);
+        s_lo[c] = max((unsigned)b1 << LB, 1u);
         if (t - acc == cnt) {    // the whole level-1 bin completes t: no split
-          s_mode[c] = kModeAll; s_thr[c] = b1 << a.lb;
+          s_mode[c] = kModeAll; s_thr[c] = b1 << LB;
         } else {
           s_b1[c] = b1;
           atomicAdd(&s_nsplit, 1);
@@ -495,12 +511,20 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     // ---- L2 (list): the gathered set holds every member of each split bin
     clear_hist();
     __syncthreads();
-    for (int j = tid; j < ucnt; j += kThreads) {
-      const int c = (int)(s_uw[j] >> 24);
-      const uint32_t k = s_uk[j];
-      if ((int)(k >> sh1) == s_b1[c]) {
-        const uint32_t b2 = (k >> sh2) & (NB - 1);
-        atomicAdd(&s_hist[c * HS + (int)b2 + (int)(b2 >> sb)], 1);
+    for (int j0 = 0; j0 < ucnt; j0 += kThreads * kUPT) {
+      int c[kUPT];
+      uint32_t k[kUPT];
+#pragma unroll
+      for (int u = 0; u < kUPT; ++u) {
+        const int j = min(j0 + u * kThreads + tid, ucnt - 1);
+        c[u] = (int)(s_uw[j] >> 24);
+        k[u] = s_uk[j];
+      }
+#pragma unroll
+      for (int u = 0; u < kUPT; ++u) {
+        const bool in = j0 + u * kThreads + tid < ucnt && (int)(k[u] >> sh1) == s_b1[c[u]];
+        const uint32_t b2 = (k[u] >> sh2) & (NB - 1);
+        atomicAdd(&s_hist[in ? c[u] * HS + (int)b2 + (int)(b2 >> sb) : trash], 1);
       }
     }
     __syncthreads();
@@ -509,18 +533,30 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   }
 
   // ---- F: gathered members above P_c are chosen, members at P_c of a staged cluster staged
-  for (int j = tid; j < ucnt; j += kThreads) {
-    const uint32_t e = s_uw[j];
-    const uint32_t key = s_uk[j];
-    const int c = (int)(e >> 24);
-    const int pos = (int)(e & 0xffffffu);
-    const int pf = (int)(key >> sh2);
-    const int P = s_thr[c];
-    const int mode = s_mode[c];
-    if (pf > P || (pf == P && mode == kModeAll))
-      s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos;
-    else if (pf == P && mode == kModeStaged)
-      s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(key, pos);
+  for (int j0 = 0; j0 < ucnt; j0 += kThreads * kUPT) {
+    uint32_t e[kUPT], key[kUPT];
+    int P[kUPT], mode[kUPT];
+#pragma unroll
+    for (int u = 0; u < kUPT; ++u) {
+      const int j = min(j0 + u * kThreads + tid, ucnt - 1);
+      e[u] = s_uw[j];
+      key[u] = s_uk[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kUPT; ++u) {
+      const int c = (int)(e[u] >> 24);
+      P[u] = s_thr[c];
+      mode[u] = j0 + u * kThreads + tid < ucnt ? s_mode[c] : kModeNone;
+    }
+#pragma unroll
+    for (int u = 0; u < kUPT; ++u) {
+      const int c = (int)(e[u] >> 24);
+      const int pf = (int)(key[u] >> sh2);
+      if (mode[u] != kModeNone && (pf > P[u] || (pf == P[u] && mode[u] == kModeAll)))
+        s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = e[u];
+      else if (pf == P[u] && mode[u] == kModeStaged)
+        s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(key[u], (int)(e[u] & 0xffffffu));
+    }
   }
   __syncthreads();
 
@@ -531,10 +567,11 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     const int need = s_t[c] - s_above[c];
     const unsigned long long* src = s_g + s_goff[c];
     uint32_t* dst = s_cst + s_tpre[c];
-    if (cnt <= 64) select_staged<1>(src, cnt, need, c, dst, &s_ccur[c], lane);
-    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, dst, &s_ccur[c], lane);
-    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, dst, &s_ccur[c], lane);
-    else select_staged_loop(src, cnt, need, c, dst, &s_ccur[c], lane);
+    const int P = s_thr[c];
+    if (cnt <= 64) select_staged<1>(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
+    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
+    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
+    else select_staged_loop(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
   }
   // clusters whose prefix bin did not fit in LDS: block-wide bitwise search, re-streaming the
   // row (rare; keeps the row's registers dead during P5)
@@ -543,8 +580,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     const int c = s_fbl[f];
     const int P = s_thr[c];
     const int need = s_t[c] - s_above[c];
-    unsigned long long T = 0ull;
-    for (int bit = 63, it = 0; bit >= 0; --bit, ++it) {
+    unsigned long long T = key64_floor(P, 2 * LB);
+    for (int bit = 63 - 2 * LB, it = 0; bit >= 0; bit = next_free_bit(bit), ++it) {
       const unsigned long long cnd = T | (1ull << bit);
       int k = 0;
       for (int sg = 0; sg < nseg; ++sg) {
@@ -588,8 +625,15 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       const uint32_t w = s_cst[j];
       const int c = (int)(w >> 24);
       const int b = s_tpre[c], t = s_t[c];
-      int rank = 0;
-      for (int k = b; k < b + t; ++k) rank += s_cst[k] < w ? 1 : 0;
+      int rank = 0, k = b;
+      for (; k + 8 <= b + t; k += 8) {
+        uint32_t y[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) y[u] = s_cst[k + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rank += y[u] < w ? 1 : 0;
+      }
+      for (; k < b + t; ++k) rank += s_cst[k] < w ? 1 : 0;
       s_out[s_base[c] + rank] = (int)(w & 0xffffffu);
     }
   } else {
@@ -620,13 +664,21 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   for (int sl = tid; sl < E; sl += kThreads) erow[sl] = s_out[sl];
 }
 
-template <int PPT>
+template <int PPT, int LB>
 int launch_row(const TopqArgs& a, int rows, size_t lds, hipStream_t s) {
-  const hipError_t e = hipFuncSetAttribute((const void*)topq_row_kernel<PPT>,
+  const hipError_t e = hipFuncSetAttribute((const void*)topq_row_kernel<PPT, LB>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(topq_row_kernel<PPT>, dim3(rows), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((topq_row_kernel<PPT, LB>), dim3(rows), dim3(kThreads), lds, s, a);
   return OA_LAUNCH_STATUS();
+}
+
+template <int LB>
+int launch_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStream_t s) {
+  if (Lmax <= kThreads * 8) return launch_row<8, LB>(a, rows, lds, s);
+  if (Lmax <= kThreads * 16) return launch_row<16, LB>(a, rows, lds, s);
+  if (Lmax <= kThreads * 36) return launch_row<36, LB>(a, rows, lds, s);
+  return launch_row<44, LB>(a, rows, lds, s);
 }
 
 }  // namespace
@@ -659,8 +711,7 @@ extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long 
   if (a.gcap < 64) return OA_EINVAL;
   const size_t lds = 8 * (size_t)(a.ucap + 64) + 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
   hipStream_t s = (hipStream_t)stream;
-  if (Lmax <= kThreads * 8) return launch_row<8>(a, rows, lds, s);
-  if (Lmax <= kThreads * 16) return launch_row<16>(a, rows, lds, s);
-  if (Lmax <= kThreads * 36) return launch_row<36>(a, rows, lds, s);
-  return launch_row<44>(a, rows, lds, s);
+  if (a.lb == 8) return launch_lb<8>(a, rows, Lmax, lds, s);
+  if (a.lb == 7) return launch_lb<7>(a, rows, Lmax, lds, s);
+  return launch_lb<6>(a, rows, Lmax, lds, s);
 }

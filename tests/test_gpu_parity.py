@@ -288,12 +288,14 @@ def test_topq_generated_list_overflow_fallback(lay4k):
     assert np.any((cnt > 1) & (quota > 0)), "no overflowed cluster was expanded"
 
 
-@pytest.mark.parametrize("n,C,E,seed", [(20000, 16, 300, 1), (8192, 4, 64, 2), (777, 8, 4096, 3)])
+@pytest.mark.parametrize("n,C,E,seed", [(20000, 16, 300, 1), (8192, 4, 64, 2), (777, 8, 4096, 3),
+                                           (20000, 100, 600, 6), (12000, 200, 1000, 7)])
 def test_topq_adversarial_quotas(n, C, E, seed):
     """Top-q on synthetic rows built to hit every branch: scores on a coarse grid (many ties,
     broken by position), one cluster holding ~60% of the row (more than 1024 members per
     8192-position chunk), quotas above the member count, quota sums above E (a segment cut at
-    E), a partial last chunk, and an output buffer holding stale values."""
+    E), a partial last chunk, and an output buffer holding stale values.  C = 100 and 200 run
+    the 7- and 6-bit histogram levels."""
     print(f"[case] topq adversarial n={n} C={C} E={E}", flush=True)
     rng = np.random.default_rng(seed)
     R, Lmax = 6, -(-(n + 300) // 64) * 64     # row strides: multiples of 4 (oa_topq reads 4 at a time)
