@@ -59,10 +59,11 @@ def log(*a):
 
 
 # kernel function names of the stage labels (as rocprofv3 prints them)
-KERNELS = {"index_prep": "index_prep_kernel",
-           "qgs_scan": "qgs_scan_kernel", "topk_select": "topk_select_kernel",
-           "gate_fill": "errorgate_kernel", "topq": "topq_row_kernel",
-           "residual_flash": "residual_kernel"}
+# (a stage may launch more than one kernel: its traffic is the sum)
+KERNELS = {"index_prep": ["index_prep_kernel"],
+           "qgs_scan": ["qgs_scan_kernel"], "topk_select": ["topk_select_reg_kernel"],
+           "gate_fill": ["errorgate_kernel", "waterfill_kernel"], "topq": ["topq_row_kernel"],
+           "residual_flash": ["resflash_kernel"]}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
 
 
@@ -72,8 +73,11 @@ def traffic_bytes(stage: str):
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
-        k = t["kernels"][KERNELS[stage]]
-        return int(round(k["fetch_kib"] * 1024 / t["fetch_factor"] + k["write_kib"] * 1024 / t["write_factor"]))
+        tot = 0.0
+        for name in KERNELS[stage]:
+            k = t["kernels"][name]
+            tot += k["fetch_kib"] * 1024 / t["fetch_factor"] + k["write_kib"] * 1024 / t["write_factor"]
+        return int(round(tot))
     except (OSError, KeyError, ValueError, ZeroDivisionError):
         return None
 
