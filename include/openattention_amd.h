@@ -198,6 +198,61 @@ int oa_dense_decode(const void* q, long q_stride, const void* K, const void* V, 
                     const int* n_dev, float sm_scale, int nsplit, float* ws_m, float* ws_l,
                     float* ws_acc, void* out, long out_stride, void* stream);
 
+/* ---- prefill index build (one request: kv_rows KV-head rows, rows = G * kv_rows query rows) */
+
+/*
+ * QGS codes of tokens [0, T): zc = k U (fp32 fma chain over d), scale = max(max_t |zc| / 127,
+ * 1e-12) per (KV row, coordinate), codes = clamp(rint(zc / scale), -127, 127).  K: kv_rows
+ * rows of (T, 128) bf16 at k_stride_h / k_stride_t; U (kv_rows, 128, 32) fp32; codes
+ * (kv_rows, codes_stride_h / 32, 32) int8; scale (kv_rows, 32); amax_ws (kv_rows * 32) uint32
+ * scratch.  Replaces the code step of inference/ours_fastbuild.py:256-261 and
+ * methods_eager.py:519-525 (StaticTopKMasker._extend, static_top_k.py:174-181).
+ */
+int oa_qgs_codes(const void* K, long k_stride_h, long k_stride_t, int kv_rows, int T,
+                 const float* U, int8_t* codes, long codes_stride_h, float* scale,
+                 uint32_t* amax_ws, void* stream);
+
+/*
+ * QGC projection zP = bf16(k W) - colmean on the bf16 matrix cores; colmean = mean over the T
+ * tokens of bf16(k W) (fp64 tile sums in a fixed order).  W (rows, 128, 16) bf16 (per query
+ * row); zP (rows, zp_stride) fp32 with zp_stride >= 16 T; colmean (rows, 16); tile_ws
+ * (rows * ceil(T/64) * 16) fp64 scratch; zraw_out (rows, zp_stride) bf16 bits of k W, or NULL.
+ * Replaces the projection of inference/ours_fastbuild.py:264-275 and methods_eager.py:526-531.
+ */
+int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, int rows, int G, int T,
+                   const void* W, float* zP, long zp_stride, float* colmean, double* tile_ws,
+                   uint16_t* zraw_out, void* stream);
+
+/*
+ * k-means assignment: asg_t = argmax_c bf16(bf16(bf16(zP_t) . bf16(c)) - bf16(|c|^2 / 2)), ties
+ * to the lower cluster, written as int32 and uint8.  cent (rows, C, 16) fp32.  Replaces
+ * _k_km_assign (inference/ours_fastbuild.py:52-82) and methods_eager.py:536-540.
+ */
+int oa_kmeans_assign(const float* zP, long zp_stride, int rows, int T, const float* cent, int C,
+                     int32_t* asg, long asg_stride, uint8_t* asg8, long asg8_stride, void* stream);
+
+/*
+ * k-means update: centroid = mean of the members' zP rows (fp64 sum in position order, one
+ * rounding), or zP[init_idx[c]] for an empty cluster; cnt_out (rows, C) member counts or NULL.
+ * Replaces _k_km_update (inference/ours_fastbuild.py:85-108) and methods_eager.py:541-547.
+ */
+int oa_kmeans_update(const float* zP, long zp_stride, int rows, int T, const uint8_t* asg8,
+                     long asg8_stride, int C, const int32_t* init_idx, float* cent, float* cnt_out,
+                     void* stream);
+
+/*
+ * Cluster statistics and CSR member lists: nb = member count, Sk = sum k, Sk2 = sum k*k,
+ * Sv = sum v (fp64 sums in position order, one rounding); mem = members by cluster, in position
+ * order (the stable argsort of the assignment), cstart / clen per cluster.  K, V: kv_rows rows
+ * of (T, 128) bf16; nb (rows, C); Sk, Sk2, Sv (rows, C, 128); mem (rows, mem_stride).
+ * Replaces _k_cluster_sums and the CSR build of inference/ours_fastbuild.py:111-139, 293-301
+ * (methods_eager.py:548-555).
+ */
+int oa_cluster_build(const void* K, const void* V, long kv_stride_h, long kv_stride_t, int rows,
+                     int G, int T, const uint8_t* asg8, long asg8_stride, int C, float* nb,
+                     float* Sk, float* Sk2, float* Sv, int32_t* mem, long mem_stride,
+                     int32_t* cstart, int32_t* clen, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

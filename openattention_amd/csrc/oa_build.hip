@@ -1,0 +1,549 @@
+// Prefill index build on gfx950: QGS codes, QGC projection, k-means (assign / update), and the
+// cluster statistics with their CSR member lists.  One request (batch row) at a time: kv_rows
+// KV-head rows and rows = G * kv_rows query-head rows; query row r reads KV row r / G.
+//
+// Reference: the fast build of inference/ours_fastbuild.py:236-304 and the eager build of
+// inference/methods_eager.py:505-555, with the accuracy-path semantics where they differ:
+//   codes    zc = k U (fp32), scale = max(max_t |zc| / 127, 1e-12) per (KV head, coordinate),
+//            codes = clamp(rint(zc / scale), -127, 127)  (static_top_k.py:174-181)
+//   project  zP = bf16(k W) - colmean, colmean = mean_t bf16(k W)  (methods_eager.py:526-531,
+//            ours_fastbuild.py:264-275)
+//   assign   a_t = argmax_c bf16(bf16(bf16(zP_t) . bf16(c)) - bf16(|c|^2 / 2)), ties to the lower
+//            cluster  (ours_fastbuild.py:52-82, methods_eager.py:536-540)
+//   update   c = mean of the members, an empty cluster keeps its initial point
+//            (ours_fastbuild.py:85-108, methods_eager.py:541-547)
+//   sums     n_c, Sk_c = sum k, Sk2_c = sum k*k, Sv_c = sum v over the members; member lists =
+//            stable argsort of the assignment  (ours_fastbuild.py:111-139, 293-301)
+//
+// Orders.  The reference leaves every summation order to its libraries.  This build fixes one
+// wherever a CPU restatement has to match it bit for bit:
+//   codes    zc_r = fma chain over d = 0..127 in fp32 (z = fma(k_d, U_dr, z), from z = 0);
+//   colmean  per 64-token tile an fp64 sum in a fixed lane order, the tiles summed in order,
+//            then one rounding of sum / T to fp32;
+//   update   per cluster an fp64 sum of the members in position order, one rounding of
+//            sum / count to fp32;
+//   sums     per cluster fp64 sums of k, k*k and v over the members in position order, one
+//            rounding to fp32.
+// The two matrix products of the QGC step (k W and zP . c) run on the bf16 matrix cores with
+// fp32 accumulation, as the reference's bf16 matmuls do; their fp32 partial rounding is the
+// hardware's, so the CPU restatement matches them up to an agreement rate (ties of the bf16
+// result), not bit for bit.
+#include <algorithm>
+
+#include "oa_common.h"
+
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short short4v;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float float4v;
+
+constexpr int kD = 128;
+constexpr int kRQ = 32;       // QGS rank
+constexpr int kRC = 16;       // QGC rank
+constexpr int kMaxC = 256;
+
+__device__ __forceinline__ __bf16 bits_bf16(uint16_t h) { return __builtin_bit_cast(__bf16, h); }
+
+// ---------------------------------------------------------------------------------- codes
+// zc of one token (one lane) against U in LDS (U[d][r], 128 x 32 floats): fma chain over d
+__device__ __forceinline__ void token_zc(const uint16_t* krow, const float* sU, float z[kRQ]) {
+#pragma unroll
+  for (int r = 0; r < kRQ; ++r) z[r] = 0.f;
+  for (int d0 = 0; d0 < kD; d0 += 8) {
+    const uint4 w = *reinterpret_cast<const uint4*>(krow + d0);
+    float kv[8];
+    oa::unpack8(w, kv);
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) {
+      const float4* u4 = reinterpret_cast<const float4*>(sU + (d0 + dd) * kRQ);
+#pragma unroll
+      for (int r4 = 0; r4 < kRQ / 4; ++r4) {
+        const float4 u = u4[r4];
+        z[4 * r4] = fmaf(kv[dd], u.x, z[4 * r4]);
+        z[4 * r4 + 1] = fmaf(kv[dd], u.y, z[4 * r4 + 1]);
+        z[4 * r4 + 2] = fmaf(kv[dd], u.z, z[4 * r4 + 2]);
+        z[4 * r4 + 3] = fmaf(kv[dd], u.w, z[4 * r4 + 3]);
+      }
+    }
+  }
+}
+
+constexpr int kCodeThreads = 256;
+
+__global__ void __launch_bounds__(64) clear_u32_kernel(uint32_t* p, int n) {
+  for (int i = threadIdx.x + blockIdx.x * 64; i < n; i += 64 * gridDim.x) p[i] = 0u;
+}
+
+// pass 1: per (KV row, coordinate) the maximum |zc| over the tokens, as float bits (|zc| >= 0,
+// so the unsigned maximum of the bits is the float maximum)
+__global__ void __launch_bounds__(kCodeThreads) codes_amax_kernel(const uint16_t* K, long ksh, long kst,
+                                                                  int T, const float* U,
+                                                                  uint32_t* amax) {
+  __shared__ float sU[kD * kRQ];
+  __shared__ uint32_t s_m[kRQ];
+  const int h = blockIdx.y;
+  for (int i = threadIdx.x; i < kD * kRQ; i += kCodeThreads) sU[i] = U[(long)h * kD * kRQ + i];
+  if (threadIdx.x < kRQ) s_m[threadIdx.x] = 0u;
+  __syncthreads();
+  const int t = blockIdx.x * kCodeThreads + threadIdx.x;
+  float z[kRQ];
+  token_zc(K + (long)h * ksh + (long)min(t, T - 1) * kst, sU, z);
+  const bool in = t < T;
+#pragma unroll
+  for (int r = 0; r < kRQ; ++r) {
+    const unsigned m = oa::wave_max_u32(in ? __float_as_uint(fabsf(z[r])) : 0u);
+    if ((threadIdx.x & 63) == 0) atomicMax(&s_m[r], m);
+  }
+  __syncthreads();
+  if (threadIdx.x < kRQ) atomicMax(&amax[h * kRQ + threadIdx.x], s_m[threadIdx.x]);
+}
+
+// pass 2: the codes (32 bytes per token) and, from the first block of each KV row, the scale
+__global__ void __launch_bounds__(kCodeThreads) codes_write_kernel(const uint16_t* K, long ksh, long kst,
+                                                                   int T, const float* U,
+                                                                   const uint32_t* amax, int8_t* codes,
+                                                                   long csh, float* scale) {
+  __shared__ float sU[kD * kRQ];
+  __shared__ float s_sc[kRQ];
+  const int h = blockIdx.y;
+  for (int i = threadIdx.x; i < kD * kRQ; i += kCodeThreads) sU[i] = U[(long)h * kD * kRQ + i];
+  if (threadIdx.x < kRQ) {
+    const float sc = fmaxf(__uint_as_float(amax[h * kRQ + threadIdx.x]) / 127.0f, 1e-12f);
+    s_sc[threadIdx.x] = sc;
+    if (blockIdx.x == 0) scale[h * kRQ + threadIdx.x] = sc;
+  }
+  __syncthreads();
+  const int t = blockIdx.x * kCodeThreads + threadIdx.x;
+  if (t >= T) return;
+  float z[kRQ];
+  token_zc(K + (long)h * ksh + (long)t * kst, sU, z);
+  uint32_t packed[kRQ / 4];
+#pragma unroll
+  for (int r4 = 0; r4 < kRQ / 4; ++r4) {
+    uint32_t w = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q = fminf(fmaxf(rintf(z[4 * r4 + j] / s_sc[4 * r4 + j]), -127.f), 127.f);
+      w |= ((uint32_t)(uint8_t)(int8_t)(int)q) << (8 * j);
+    }
+    packed[r4] = w;
+  }
+  uint4* dst = reinterpret_cast<uint4*>(codes + (long)h * csh + (long)t * kRQ);
+  dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+}
+
+// ---------------------------------------------------------------------------------- projection
+// One wave per (64-token tile, query row).  Four 16-token blocks, each 16 tokens x 16 columns
+// from four v_mfma_f32_16x16x32_bf16 over d = 0..127 (A: token rows of K, B: the row's W).
+// Output layout of a 16x16 block: lane l holds tokens 4*(l/16) + i (i = 0..3) of column l % 16.
+// zraw = bf16(acc) is written (as fp32) into zP, and the tile's column sums (fp64, lane order
+// below) into tsum[row][tile][16].
+__global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long ksh, long kst, int G,
+                                                         int T, const uint16_t* W, float* zP,
+                                                         long zps, uint16_t* zraw_out, double* tsum,
+                                                         int ntiles) {
+  const int lane = threadIdx.x;
+  const int tile = blockIdx.x;
+  const int row = blockIdx.y;
+  const uint16_t* krow = K + (long)(row / G) * ksh;
+  const uint16_t* w = W + (long)row * kD * kRC;
+  // B operand of chunk ch: column j = lane % 16, dims ch*32 + 8*(lane/16) + e, e = 0..7
+  bf16x8 bw[4];
+#pragma unroll
+  for (int ch = 0; ch < 4; ++ch)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      bw[ch][e] = bits_bf16(w[(ch * 32 + 8 * (lane >> 4) + e) * kRC + (lane & 15)]);
+  double cs = 0.0;   // this lane's column (lane % 16) partial over its tokens, in block order
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int t0 = tile * 64 + blk * 16;
+    const int ta = min(t0 + (lane & 15), T - 1);          // A row: token t0 + lane % 16
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+      const uint4 av = *reinterpret_cast<const uint4*>(krow + (long)ta * kst + ch * 32 + 8 * (lane >> 4));
+      bf16x8 a = __builtin_bit_cast(bf16x8, av);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bw[ch], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + 4 * (lane >> 4) + i;
+      const uint16_t hb = oa::f32_to_bf16(acc[i]);
+      const float v = oa::bf16_to_f32(hb);
+      if (t < T) {
+        zP[(long)row * zps + (long)t * kRC + (lane & 15)] = v;
+        if (zraw_out) zraw_out[(long)row * zps + (long)t * kRC + (lane & 15)] = hb;
+        cs += (double)v;
+      }
+    }
+  }
+  // lanes j, 16 + j, 32 + j, 48 + j hold column j: ((g0 + g1) + (g2 + g3))
+  cs += __shfl_xor(cs, 16, 64);
+  cs += __shfl_xor(cs, 32, 64);
+  if (lane < 16) tsum[((long)row * ntiles + tile) * kRC + lane] = cs;
+}
+
+// colmean from the tile sums (tiles in order, fp64), then zP -= colmean in place
+__global__ void __launch_bounds__(256) qgc_center_kernel(float* zP, long zps, int T, const double* tsum,
+                                                         int ntiles, float* colmean) {
+  __shared__ float s_cm[kRC];
+  const int row = blockIdx.y;
+  if (threadIdx.x < kRC) {
+    double s = 0.0;
+    for (int k = 0; k < ntiles; ++k) s += tsum[((long)row * ntiles + k) * kRC + threadIdx.x];
+    const float cm = (float)(s / (double)T);
+    s_cm[threadIdx.x] = cm;
+    if (blockIdx.x == 0) colmean[row * kRC + threadIdx.x] = cm;
+  }
+  __syncthreads();
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < (long)T * kRC; i += (long)gridDim.x * 256)
+    zP[(long)row * zps + i] = zP[(long)row * zps + i] - s_cm[i & (kRC - 1)];
+}
+
+// ---------------------------------------------------------------------------------- k-means
+// bf16 ordered key: larger value -> larger key
+__device__ __forceinline__ uint32_t bf16_key(uint16_t h) {
+  return (uint32_t)(h ^ ((h & 0x8000u) ? 0xffffu : 0x8000u));
+}
+
+// One wave per (64-token tile, query row).  The row's centroids (bf16, B operands: centroid
+// lane % 16 of a 16-centroid block, dims 4*(lane/16)..+3) and bf16(|c|^2 / 2) stay in LDS.
+// Per 16-token block and centroid block one v_mfma_f32_16x16x16bf16_1k gives 16 x 16 dots;
+// the distance bf16(bf16(dot) - half) is ranked through the key (bf16 key << 8 | 255 - c), so the
+// maximum over the 16 centroid lanes (a DPP row) and over the blocks is the argmax with ties to
+// the lower cluster.
+__global__ void __launch_bounds__(64) kmeans_assign_kernel(const float* zP, long zps, int T,
+                                                           const float* cent, int C, int32_t* asg,
+                                                           long as, uint8_t* asg8, long a8s) {
+  __shared__ uint16_t s_cb[kMaxC * kRC];
+  __shared__ uint16_t s_half[kMaxC];
+  const int lane = threadIdx.x;
+  const int tile = blockIdx.x;
+  const int row = blockIdx.y;
+  const int CB = (C + 15) / 16;
+  const float* cr = cent + (long)row * C * kRC;
+  for (int i = lane; i < CB * 16 * kRC; i += 64) s_cb[i] = i < C * kRC ? oa::f32_to_bf16(cr[i]) : 0;
+  for (int c = lane; c < CB * 16; c += 64) {
+    uint16_t hv = 0;
+    if (c < C) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < kRC; ++j) {
+        const float x = cr[c * kRC + j];
+        s = s + x * x;
+      }
+      hv = oa::f32_to_bf16(0.5f * s);
+    }
+    s_half[c] = hv;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int t0 = tile * 64 + blk * 16;
+    const int ta = min(t0 + (lane & 15), T - 1);
+    const float4 zv = *reinterpret_cast<const float4*>(zP + (long)row * zps + (long)ta * kRC + 4 * (lane >> 4));
+    short4v a;
+    a[0] = (short)oa::f32_to_bf16(zv.x);
+    a[1] = (short)oa::f32_to_bf16(zv.y);
+    a[2] = (short)oa::f32_to_bf16(zv.z);
+    a[3] = (short)oa::f32_to_bf16(zv.w);
+    uint32_t best[4] = {0u, 0u, 0u, 0u};
+    for (int cb = 0; cb < CB; ++cb) {
+      const int c = cb * 16 + (lane & 15);
+      const uint16_t* bp = s_cb + c * kRC + 4 * (lane >> 4);
+      short4v b;
+      b[0] = (short)bp[0]; b[1] = (short)bp[1]; b[2] = (short)bp[2]; b[3] = (short)bp[3];
+      float4v acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+      const float hf = oa::bf16_to_f32(s_half[c]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dot = oa::bf16_to_f32(oa::f32_to_bf16(acc[i]));
+        uint16_t dist = oa::f32_to_bf16(dot - hf);
+        if ((dist & 0x7fffu) == 0) dist = 0;           // -0 ranks as +0
+        const uint32_t key = c < C ? (bf16_key(dist) << 8) | (uint32_t)(255 - c) : 0u;
+        best[i] = max(best[i], key);
+      }
+    }
+    // maximum over the 16 lanes of each DPP row (the 16 centroids of one block column set)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t v = best[i];
+      v = max(v, oa::dpp_u32<0xB1, 0xf>(v));
+      v = max(v, oa::dpp_u32<0x4E, 0xf>(v));
+      v = max(v, oa::dpp_u32<0x141, 0xf>(v));
+      v = max(v, oa::dpp_u32<0x140, 0xf>(v));
+      best[i] = v;
+    }
+    if ((lane & 15) < 4) {
+      const int i = lane & 15;
+      const int t = t0 + 4 * (lane >> 4) + i;
+      // lane (16g + i) holds token 4g + i of the block: best[i] of its row
+      uint32_t v = i == 0 ? best[0] : (i == 1 ? best[1] : (i == 2 ? best[2] : best[3]));
+      if (t < T) {
+        const int cid = 255 - (int)(v & 0xffu);
+        asg[(long)row * as + t] = cid;
+        asg8[(long)row * a8s + t] = (uint8_t)cid;
+      }
+    }
+  }
+}
+
+// One wave per (cluster, query row): the members in position order (a scan of the byte ids,
+// 256 positions per step), their zP rows summed in fp64 by lanes 0..15 (one column each) in
+// that order; centroid = fp32(sum / count), or the initial point when the cluster is empty.
+__global__ void __launch_bounds__(64) kmeans_update_kernel(const float* zP, long zps, int T,
+                                                           const uint8_t* asg8, long a8s, int C,
+                                                           const int32_t* init_idx, float* cent,
+                                                           float* cnt_out) {
+  __shared__ int s_pos[256];
+  const int lane = threadIdx.x;
+  const int c = blockIdx.x;
+  const int row = blockIdx.y;
+  const uint8_t* ar = asg8 + (long)row * a8s;
+  const float* zr = zP + (long)row * zps;
+  double acc = 0.0;
+  int cnt = 0;
+  for (int p0 = 0; p0 < T; p0 += 256) {
+    const int p = p0 + 4 * lane;
+    uint32_t ids = 0xffffffffu;
+    if (p + 3 < T) ids = *reinterpret_cast<const uint32_t*>(ar + p);
+    else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (p + e < T) ids = (ids & ~(0xffu << (8 * e))) | ((uint32_t)ar[p + e] << (8 * e));
+    }
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) ? 1 : 0;
+    // exclusive prefix of the per-lane member counts: the chunk's members in position order
+    int incl = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const int tot = __shfl(incl, 63, 64);
+    int o = incl - mine;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) s_pos[o++] = p + e;
+    __syncthreads();
+    if (lane < kRC) {
+      int k = 0;
+      for (; k + 4 <= tot; k += 4) {
+        const float v0 = zr[(long)s_pos[k] * kRC + lane], v1 = zr[(long)s_pos[k + 1] * kRC + lane];
+        const float v2 = zr[(long)s_pos[k + 2] * kRC + lane], v3 = zr[(long)s_pos[k + 3] * kRC + lane];
+        acc += (double)v0; acc += (double)v1; acc += (double)v2; acc += (double)v3;
+      }
+      for (; k < tot; ++k) acc += (double)zr[(long)s_pos[k] * kRC + lane];
+    }
+    cnt += tot;
+    __syncthreads();
+  }
+  if (lane < kRC) {
+    const float v = cnt > 0 ? (float)(acc / (double)cnt) : zr[(long)init_idx[c] * kRC + lane];
+    cent[((long)row * C + c) * kRC + lane] = v;
+  }
+  if (lane == 0 && cnt_out) cnt_out[row * C + c] = (float)cnt;
+}
+
+// ---------------------------------------------------------------------------------- sums + CSR
+// per query row: member count of every cluster, CSR start (exclusive prefix), nb
+__global__ void __launch_bounds__(256) cluster_count_kernel(int T, const uint8_t* asg8, long a8s, int C,
+                                                            float* nb, int32_t* cstart, int32_t* clen) {
+  __shared__ int s_cnt[kMaxC];
+  const int row = blockIdx.x;
+  for (int c = threadIdx.x; c < kMaxC; c += 256) s_cnt[c] = 0;
+  __syncthreads();
+  const uint8_t* ar = asg8 + (long)row * a8s;
+  for (int t = threadIdx.x; t < T; t += 256) atomicAdd(&s_cnt[ar[t]], 1);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int v[4], loc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = s_cnt[lane * 4 + i]; loc += v[i]; }
+    int incl = loc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    int run = incl - loc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = lane * 4 + i;
+      if (c < C) {
+        cstart[row * C + c] = run;
+        clen[row * C + c] = v[i];
+        nb[row * C + c] = (float)v[i];
+      }
+      run += v[i];
+    }
+  }
+}
+
+// One wave per (cluster, query row): members in position order -> mem[cstart + i], and the
+// fp64 sums of k, k*k and v over them in that order (lane l: dims 2l, 2l + 1).
+__global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, const uint16_t* V, long ksh,
+                                                          long kst, int G, int T, const uint8_t* asg8,
+                                                          long a8s, int C, const int32_t* cstart,
+                                                          float* Sk, float* Sk2, float* Sv, int32_t* mem,
+                                                          long ms) {
+  __shared__ int s_pos[256];
+  const int lane = threadIdx.x;
+  const int c = blockIdx.x;
+  const int row = blockIdx.y;
+  const uint8_t* ar = asg8 + (long)row * a8s;
+  const uint16_t* kr = K + (long)(row / G) * ksh;
+  const uint16_t* vr = V + (long)(row / G) * ksh;
+  int32_t* mr = mem + (long)row * ms + cstart[row * C + c];
+  double k0 = 0.0, k1 = 0.0, q0 = 0.0, q1 = 0.0, v0 = 0.0, v1 = 0.0;
+  int cnt = 0;
+  for (int p0 = 0; p0 < T; p0 += 256) {
+    const int p = p0 + 4 * lane;
+    uint32_t ids = 0xffffffffu;
+    if (p + 3 < T) ids = *reinterpret_cast<const uint32_t*>(ar + p);
+    else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (p + e < T) ids = (ids & ~(0xffu << (8 * e))) | ((uint32_t)ar[p + e] << (8 * e));
+    }
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) ? 1 : 0;
+    int incl = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const int tot = __shfl(incl, 63, 64);
+    int o = incl - mine;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) {
+        s_pos[o] = p + e;
+        mr[cnt + o] = p + e;
+        ++o;
+      }
+    __syncthreads();
+    int k = 0;
+    for (; k + 4 <= tot; k += 4) {
+      uint32_t kw[4], vw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kw[u] = *reinterpret_cast<const uint32_t*>(kr + (long)s_pos[k + u] * kst + 2 * lane);
+        vw[u] = *reinterpret_cast<const uint32_t*>(vr + (long)s_pos[k + u] * kst + 2 * lane);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const double a0 = (double)__uint_as_float(kw[u] << 16), a1 = (double)__uint_as_float(kw[u] & 0xffff0000u);
+        k0 += a0; k1 += a1; q0 += a0 * a0; q1 += a1 * a1;
+        v0 += (double)__uint_as_float(vw[u] << 16);
+        v1 += (double)__uint_as_float(vw[u] & 0xffff0000u);
+      }
+    }
+    for (; k < tot; ++k) {
+      const uint32_t kw = *reinterpret_cast<const uint32_t*>(kr + (long)s_pos[k] * kst + 2 * lane);
+      const uint32_t vw = *reinterpret_cast<const uint32_t*>(vr + (long)s_pos[k] * kst + 2 * lane);
+      const double a0 = (double)__uint_as_float(kw << 16), a1 = (double)__uint_as_float(kw & 0xffff0000u);
+      k0 += a0; k1 += a1; q0 += a0 * a0; q1 += a1 * a1;
+      v0 += (double)__uint_as_float(vw << 16);
+      v1 += (double)__uint_as_float(vw & 0xffff0000u);
+    }
+    cnt += tot;
+    __syncthreads();
+  }
+  const long o = ((long)row * C + c) * kD + 2 * lane;
+  Sk[o] = (float)k0; Sk[o + 1] = (float)k1;
+  Sk2[o] = (float)q0; Sk2[o + 1] = (float)q1;
+  Sv[o] = (float)v0; Sv[o + 1] = (float)v1;
+}
+
+}  // namespace
+
+extern "C" int oa_qgs_codes(const void* K, long k_stride_h, long k_stride_t, int kv_rows, int T,
+                            const float* U, int8_t* codes, long codes_stride_h, float* scale,
+                            uint32_t* amax_ws, void* stream) {
+  if (kv_rows <= 0 || T <= 0 || !K || !U || !codes || !scale || !amax_ws || k_stride_t < kD ||
+      k_stride_t % 8 || k_stride_h % 8 || codes_stride_h < (long)T * kRQ || codes_stride_h % 16 ||
+      (reinterpret_cast<uintptr_t>(K) & 15) || (reinterpret_cast<uintptr_t>(codes) & 15))
+    return OA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  const uint16_t* k = reinterpret_cast<const uint16_t*>(K);
+  hipLaunchKernelGGL(clear_u32_kernel, dim3(std::min(64, (kv_rows * kRQ + 63) / 64)), dim3(64), 0, s,
+                     amax_ws, kv_rows * kRQ);
+  const dim3 grid((T + kCodeThreads - 1) / kCodeThreads, kv_rows);
+  hipLaunchKernelGGL(codes_amax_kernel, grid, dim3(kCodeThreads), 0, s, k, k_stride_h, k_stride_t, T, U,
+                     amax_ws);
+  hipLaunchKernelGGL(codes_write_kernel, grid, dim3(kCodeThreads), 0, s, k, k_stride_h, k_stride_t, T, U,
+                     amax_ws, codes, codes_stride_h, scale);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, int rows, int G, int T,
+                              const void* W, float* zP, long zp_stride, float* colmean,
+                              double* tile_ws, uint16_t* zraw_out, void* stream) {
+  if (rows <= 0 || G <= 0 || rows % G || T <= 0 || !K || !W || !zP || !colmean || !tile_ws ||
+      k_stride_t < kD || k_stride_t % 8 || k_stride_h % 8 || zp_stride < (long)T * kRC ||
+      zp_stride % 4 || (reinterpret_cast<uintptr_t>(K) & 15) || (reinterpret_cast<uintptr_t>(zP) & 15))
+    return OA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  const int ntiles = (T + 63) / 64;
+  hipLaunchKernelGGL(qgc_project_kernel, dim3(ntiles, rows), dim3(64), 0, s,
+                     reinterpret_cast<const uint16_t*>(K), k_stride_h, k_stride_t, G, T,
+                     reinterpret_cast<const uint16_t*>(W), zP, zp_stride, zraw_out, tile_ws, ntiles);
+  const int nb = std::min(64, (T * kRC + 255) / 256);
+  hipLaunchKernelGGL(qgc_center_kernel, dim3(nb, rows), dim3(256), 0, s, zP, zp_stride, T, tile_ws,
+                     ntiles, colmean);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_kmeans_assign(const float* zP, long zp_stride, int rows, int T, const float* cent,
+                                int C, int32_t* asg, long asg_stride, uint8_t* asg8, long asg8_stride,
+                                void* stream) {
+  if (rows <= 0 || T <= 0 || C <= 0 || C > kMaxC || !zP || !cent || !asg || !asg8 ||
+      zp_stride < (long)T * kRC || zp_stride % 4 || asg_stride < T || asg8_stride < T ||
+      (reinterpret_cast<uintptr_t>(zP) & 15))
+    return OA_EINVAL;
+  hipLaunchKernelGGL(kmeans_assign_kernel, dim3((T + 63) / 64, rows), dim3(64), 0, (hipStream_t)stream,
+                     zP, zp_stride, T, cent, C, asg, asg_stride, asg8, asg8_stride);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_kmeans_update(const float* zP, long zp_stride, int rows, int T, const uint8_t* asg8,
+                                long asg8_stride, int C, const int32_t* init_idx, float* cent,
+                                float* cnt_out, void* stream) {
+  if (rows <= 0 || T <= 0 || C <= 0 || C > kMaxC || !zP || !asg8 || !init_idx || !cent ||
+      zp_stride < (long)T * kRC || asg8_stride < T || asg8_stride % 4 ||
+      (reinterpret_cast<uintptr_t>(asg8) & 3))
+    return OA_EINVAL;
+  hipLaunchKernelGGL(kmeans_update_kernel, dim3(C, rows), dim3(64), 0, (hipStream_t)stream, zP, zp_stride,
+                     T, asg8, asg8_stride, C, init_idx, cent, cnt_out);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_cluster_build(const void* K, const void* V, long kv_stride_h, long kv_stride_t, int rows,
+                                int G, int T, const uint8_t* asg8, long asg8_stride, int C, float* nb,
+                                float* Sk, float* Sk2, float* Sv, int32_t* mem, long mem_stride,
+                                int32_t* cstart, int32_t* clen, void* stream) {
+  if (rows <= 0 || G <= 0 || rows % G || T <= 0 || C <= 0 || C > kMaxC || !K || !V || !asg8 || !nb ||
+      !Sk || !Sk2 || !Sv || !mem || !cstart || !clen || kv_stride_t < kD || kv_stride_t % 2 ||
+      kv_stride_h % 2 || asg8_stride < T || asg8_stride % 4 || mem_stride < T ||
+      (reinterpret_cast<uintptr_t>(asg8) & 3) || (reinterpret_cast<uintptr_t>(K) & 3) ||
+      (reinterpret_cast<uintptr_t>(V) & 3))
+    return OA_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(cluster_count_kernel, dim3(rows), dim3(256), 0, s, T, asg8, asg8_stride, C, nb,
+                     cstart, clen);
+  hipLaunchKernelGGL(cluster_sums_kernel, dim3(C, rows), dim3(64), 0, s,
+                     reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
+                     kv_stride_h, kv_stride_t, G, T, asg8, asg8_stride, C, cstart, Sk, Sk2, Sv, mem,
+                     mem_stride);
+  return OA_LAUNCH_STATUS();
+}

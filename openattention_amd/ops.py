@@ -272,3 +272,70 @@ def dense_decode(q, K, V, n_dev, out=None, sm_scale: float | None = None, nsplit
              _ptr(ws[R * nsplit: 2 * R * nsplit]), _ptr(ws[2 * R * nsplit: need]), _ptr(out),
              out.stride(0), _stream(dev))
     return out
+
+
+# ================================================================== prefill index build
+def qgs_codes(K, T: int, U, codes, scale, amax_ws) -> None:
+    """a11 of one request: K (HKV, >=T, 128) bf16; U (HKV, 128, 32) fp32; codes (HKV, Lmax, 32)
+    int8 (rows written up to T); scale (HKV, 32); amax_ws >= HKV*32 int32 scratch."""
+    dev = _dev(K, U, codes, scale, amax_ws)
+    HKV = K.shape[0]
+    _need(K.dtype == torch.bfloat16 and K.stride(-1) == 1, "K: bf16 with contiguous rows")
+    _need(U.is_contiguous() and U.shape == (HKV, HEAD_DIM, RANK_Q), "U: (HKV, 128, 32) contiguous")
+    _need(scale.is_contiguous() and scale.shape == (HKV, RANK_Q), "scale: (HKV, 32) contiguous")
+    _need(codes.dtype == torch.int8 and codes.stride(2) == 1 and codes.stride(1) == RANK_Q,
+          "codes: (HKV, Lmax, 32) int8 rows")
+    _need(amax_ws.numel() >= HKV * RANK_Q, "amax_ws too small")
+    _need(T <= K.shape[1] and T <= codes.shape[1], "T beyond the rows")
+    lib.call("oa_qgs_codes", _ptr(K), K.stride(0), K.stride(1), HKV, T, _ptr(U), _ptr(codes),
+             codes.stride(0), _ptr(scale), _ptr(amax_ws), _stream(dev))
+
+
+def qgc_project(K, T: int, W, G: int, zP, colmean, zraw=None) -> None:
+    """a12 projection: zP (HQ, T, 16) fp32 = bf16(k W) - colmean; colmean (HQ, 16); zraw
+    (HQ, T, 16) int16/bf16 view of bf16(k W) or None."""
+    dev = _dev(K, W, zP, colmean)
+    HQ = W.shape[0]
+    _need(W.dtype == torch.bfloat16 and W.is_contiguous() and W.shape[1:] == (HEAD_DIM, RANK_C),
+          "W: (HQ, 128, 16) bf16 contiguous")
+    _need(K.shape[0] * G == HQ and T <= K.shape[1], "K: HQ / G rows of at least T tokens")
+    _need(zP.dtype == torch.float32 and zP.stride(2) == 1 and zP.stride(1) == RANK_C, "zP: (HQ, T, 16) fp32 rows")
+    _need(colmean.is_contiguous() and colmean.shape == (HQ, RANK_C), "colmean: (HQ, 16) contiguous")
+    if zraw is not None:
+        _need(zraw.stride() == zP.stride() and zraw.element_size() == 2, "zraw: 16-bit, zP's strides")
+    ntiles = -(-T // 64)
+    ws = torch.empty(HQ * ntiles * RANK_C, device=dev, dtype=torch.float64)
+    lib.call("oa_qgc_project", _ptr(K), K.stride(0), K.stride(1), HQ, G, T, _ptr(W), _ptr(zP),
+             zP.stride(0), _ptr(colmean), _ptr(ws), _ptr(zraw), _stream(dev))
+
+
+def kmeans_assign(zP, T: int, cent, asg, asg8) -> None:
+    """a12 assignment into asg (HQ, >=T) int32 and asg8 (HQ, >=T) uint8 rows."""
+    dev = _dev(zP, cent, asg, asg8)
+    HQ, C = cent.shape[0], cent.shape[1]
+    _need(cent.is_contiguous() and cent.shape[2] == RANK_C, "cent: (HQ, C, 16) contiguous")
+    _need(asg.stride(1) == 1 and asg8.stride(1) == 1, "asg rows must be contiguous")
+    lib.call("oa_kmeans_assign", _ptr(zP), zP.stride(0), HQ, T, _ptr(cent), C, _ptr(asg), asg.stride(0),
+             _ptr(asg8), asg8.stride(0), _stream(dev))
+
+
+def kmeans_update(zP, T: int, asg8, init, cent, cnt=None) -> None:
+    """a12 update of cent (HQ, C, 16) in place; init (C,) int32 initial positions."""
+    dev = _dev(zP, asg8, init, cent)
+    HQ, C = cent.shape[0], cent.shape[1]
+    _need(init.dtype == torch.int32 and init.numel() == C, "init: (C,) int32")
+    lib.call("oa_kmeans_update", _ptr(zP), zP.stride(0), HQ, T, _ptr(asg8), asg8.stride(0), C,
+             _ptr(init), _ptr(cent), _ptr(cnt), _stream(dev))
+
+
+def cluster_build(K, V, T: int, G: int, asg8, C: int, nb, Sk, Sk2, Sv, mem, cstart, clen) -> None:
+    """a13: nb (HQ, C), Sk/Sk2/Sv (HQ, C, 128), mem (HQ, >=T), cstart/clen (HQ, C)."""
+    dev = _dev(K, V, asg8, nb, Sk, Sk2, Sv, mem, cstart, clen)
+    HQ = nb.shape[0]
+    _need(K.stride() == V.stride() and K.stride(-1) == 1, "K, V: same strides, contiguous rows")
+    _need(K.shape[0] * G == HQ and T <= K.shape[1], "K: HQ / G rows of at least T tokens")
+    for t, nm in ((nb, "nb"), (Sk, "Sk"), (Sk2, "Sk2"), (Sv, "Sv"), (cstart, "cstart"), (clen, "clen")):
+        _need(t.is_contiguous(), f"{nm} must be contiguous")
+    lib.call("oa_cluster_build", _ptr(K), _ptr(V), K.stride(0), K.stride(1), HQ, G, T, _ptr(asg8),
+             asg8.stride(0), C, _ptr(nb), _ptr(Sk), _ptr(Sk2), _ptr(Sv), _ptr(mem), mem.stride(0),
+             _ptr(cstart), _ptr(clen), _stream(dev))

@@ -7,18 +7,19 @@ multibin.py:1894):
        positions (StaticTopKMasker._rot_avg, static_top_k.py:103-131); M_q from P <= 64
        question rows, each rotated to T (static_top_k.py:185-194); M = 1/2 nt(M_st) + 1/2
        nt(M_q), nt = trace normalisation; U = top-32 eigenvectors of the group-mean M per KV
-       head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.
-  a11  zc = k U (fp32); scale = max(max_t |zc| / 127, 1e-12) per (KV head, coordinate),
-       fixed at the build; codes = clamp(round(zc / scale), -127, 127) int8
-       (static_top_k.py:174-181).
-  a12  zP = bf16(k W) - colmean; 4 Lloyd iterations with the bf16 distance
-       bf16(bf16(zP_bf16 . c_bf16) - bf16(|c|^2 / 2)), argmax with ties to the lower cluster,
-       centroid = mean (an empty cluster keeps its initial point) (methods_eager.py:526-547).
-  a13  CSR member lists = stable argsort of the assignment; n_b, sum k, sum k^2, sum v per
-       cluster in fp32 (ours_fastbuild.py:293-301).
-The torch operations here run on whichever device the tensors live on.  torch.linalg.eigh and
-the fp32 scatter sums are not bitwise reproducible across devices/libraries, so the decode
-stage's parity tests inject one built state into both the GPU kernels and the CPU restatement.
+       head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.  Host torch
+       (rocSOLVER eigh on the device).
+  a11  codes: oa_qgs_codes (zc = k U, scale = max(max_t |zc| / 127, 1e-12), codes =
+       clamp(rint(zc / scale), -127, 127); static_top_k.py:174-181).
+  a12  oa_qgc_project (zP = bf16(k W) - colmean on the bf16 matrix cores), then 4 Lloyd
+       iterations of oa_kmeans_assign (bf16 distance bf16(bf16(zP . c) - bf16(|c|^2 / 2)), ties
+       to the lower cluster) and oa_kmeans_update (member means; an empty cluster keeps its
+       initial point) (methods_eager.py:526-547).
+  a13  oa_cluster_build: n_b, sum k, sum k^2, sum v per cluster and the CSR member lists
+       (ours_fastbuild.py:293-301).
+The a11-a13 stages run only on the HIP kernels (a tensor on another device raises).  The
+decode stage's parity tests inject one built state into both the GPU kernels and the CPU
+restatement; the build stages have their own parity tests.
 """
 from __future__ import annotations
 
@@ -116,71 +117,62 @@ def kmeans_seed(layer: int) -> int:
     return 1234 + 31 * (layer + 1)
 
 
+def bases(M: torch.Tensor, HKV: int, G: int):
+    """a10 bases from the per-query-head metric M (HQ, D, D): U (HKV, D, 32) = top-32
+    eigenvectors of the group mean (methods_eager.py:519-520), W (HQ, D, 16) bf16 = top-16
+    eigenvectors * sqrt(eigenvalue) (methods_eager.py:527-528)."""
+    _, Ukv = torch.linalg.eigh(M.view(HKV, G, D, D).mean(1))
+    U = Ukv[..., -RQ:].contiguous()
+    ev, Uq = torch.linalg.eigh(M)
+    W = (Uq[..., -RC:] * ev[..., -RC:].clamp(min=0).sqrt().unsqueeze(-2)).to(torch.bfloat16).contiguous()
+    return U, W
+
+
+def kmeans_init(T: int, C: int, layer: int) -> torch.Tensor:
+    """Initial centroid positions: the first C of a seeded permutation of the T tokens
+    (multibin.py:1894-1895; CPU generator, as the reference)."""
+    if T < C:
+        raise ValueError(f"the prefix ({T} tokens) must hold at least C = {C} tokens")
+    g = torch.Generator(device="cpu").manual_seed(kmeans_seed(layer))
+    return torch.randperm(T, generator=g)[:C]
+
+
 @torch.no_grad()
 def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int,
               M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, layer: int,
               G: int = 4) -> None:
-    """Build batch row b of one layer's index into `st` (a LayerState).
+    """Build batch row b of one layer's index into `st` (a LayerState on a HIP device).
 
     K, V: (HKV, >=T, D) bf16 of this batch row; qrows: (HQ, Qn, D) question rows.
     """
+    from openattention_amd import ops
     dev = K.device
+    if dev.type != "cuda":
+        raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
     HKV = K.shape[0]
     HQ = HKV * G
     C = st.C
-    k = K[:, :T]
-    v = V[:, :T]
     M = query_metric(M_pre.to(dev), qrows, T, inv_freq.to(dev), scaling)           # (HQ, D, D)
-    # QGS (a11): one U per KV head
-    _, Ukv = torch.linalg.eigh(M.view(HKV, G, D, D).mean(1))
-    U = Ukv[..., -RQ:].contiguous()
-    zc = torch.matmul(k.float(), U)
-    scale = (zc.abs().amax(1, keepdim=True) / 127.0).clamp(min=1e-12)
-    r0 = b * HKV
-    st.codes[r0:r0 + HKV, :T] = (zc / scale).round().clamp(-127, 127).to(torch.int8)
+    U, W = bases(M, HKV, G)
+    r0, q0 = b * HKV, b * HQ
     st.U[r0:r0 + HKV] = U
-    st.scale[r0:r0 + HKV] = scale[:, 0]
-    # QGC projection (a10/a12)
-    ev, Uq = torch.linalg.eigh(M)
-    W = (Uq[..., -RC:] * ev[..., -RC:].clamp(min=0).sqrt().unsqueeze(-2)).to(torch.bfloat16)
-    krep = k.repeat_interleave(G, 0).contiguous()
-    zP = torch.matmul(krep, W.contiguous()).float()                                  # bf16 matmul
-    colmean = zP.mean(1, keepdim=True)
-    zP = zP - colmean
-    g = torch.Generator(device="cpu").manual_seed(kmeans_seed(layer))
-    init = torch.randperm(T, generator=g)[:C].to(dev)
-    cent = zP.index_select(1, init).clone()
-    zb = zP.to(torch.bfloat16)
-    asg = torch.empty(HQ, T, device=dev, dtype=torch.long)
-    ones = torch.ones(HQ, T, device=dev)
-    for _ in range(ITERS):
-        half = (0.5 * (cent * cent).sum(-1)).to(torch.bfloat16).unsqueeze(1)
-        cb = cent.to(torch.bfloat16).transpose(1, 2).contiguous()
-        for h0 in range(0, HQ, 8):
-            asg[h0:h0 + 8] = (torch.matmul(zb[h0:h0 + 8], cb[h0:h0 + 8]) - half[h0:h0 + 8]).argmax(-1)
-        acc = torch.zeros(HQ, C, RC, device=dev).scatter_add_(1, asg.unsqueeze(-1).expand(-1, -1, RC), zP)
-        cnt = torch.zeros(HQ, C, device=dev).scatter_add_(1, asg, ones)
-        cent = torch.where(cnt.unsqueeze(-1) > 0, acc / cnt.clamp(min=1).unsqueeze(-1),
-                           zP.index_select(1, init))
-    q0 = b * HQ
-    st.asg[q0:q0 + HQ, :T] = asg.to(torch.int32)
-    st.asg8[q0:q0 + HQ, :T] = asg.to(torch.uint8)
     st.W[q0:q0 + HQ] = W
-    st.colmean[q0:q0 + HQ] = colmean[:, 0]
-    st.cent[q0:q0 + HQ] = cent
-    # cluster sums (a13) and CSR member lists
-    idx = asg.unsqueeze(-1).expand(-1, -1, D)
-    kf = krep.float()
-    vf = v.repeat_interleave(G, 0).float()
-    nb = torch.zeros(HQ, C, device=dev).scatter_add_(1, asg, ones)
-    st.nb[q0:q0 + HQ] = nb
-    st.Sk[q0:q0 + HQ] = torch.zeros(HQ, C, D, device=dev).scatter_add_(1, idx, kf)
-    st.Sk2[q0:q0 + HQ] = torch.zeros(HQ, C, D, device=dev).scatter_add_(1, idx, kf * kf)
-    st.Sv[q0:q0 + HQ] = torch.zeros(HQ, C, D, device=dev).scatter_add_(1, idx, vf)
-    st.mem[q0:q0 + HQ, :T] = torch.argsort(asg, dim=-1, stable=True).to(torch.int32)
-    cntc = nb.round().to(torch.int32)
-    st.cstart[q0:q0 + HQ] = (cntc.cumsum(-1) - cntc).to(torch.int32)
-    st.clen[q0:q0 + HQ] = cntc
+    # a11: QGS codes and scale
+    amax = torch.empty(HKV * RQ, device=dev, dtype=torch.int32)
+    ops.qgs_codes(K, T, st.U[r0:r0 + HKV], st.codes[r0:r0 + HKV], st.scale[r0:r0 + HKV], amax)
+    # a12: QGC projection and k-means
+    zP = torch.empty(HQ, T, RC, device=dev)
+    ops.qgc_project(K, T, st.W[q0:q0 + HQ], G, zP, st.colmean[q0:q0 + HQ])
+    init = kmeans_init(T, C, layer).to(device=dev, dtype=torch.int32)
+    cent = st.cent[q0:q0 + HQ]
+    cent.copy_(zP.index_select(1, init.long()))
+    asg, asg8 = st.asg[q0:q0 + HQ], st.asg8[q0:q0 + HQ]
+    for _ in range(ITERS):
+        ops.kmeans_assign(zP, T, cent, asg, asg8)
+        ops.kmeans_update(zP, T, asg8, init, cent)
+    # a13: cluster statistics and CSR member lists
+    ops.cluster_build(K, V, T, G, asg8, C, st.nb[q0:q0 + HQ], st.Sk[q0:q0 + HQ], st.Sk2[q0:q0 + HQ],
+                      st.Sv[q0:q0 + HQ], st.mem[q0:q0 + HQ], st.cstart[q0:q0 + HQ], st.clen[q0:q0 + HQ])
     st.reccnt[q0:q0 + HQ] = 0
 
 

@@ -601,3 +601,193 @@ void oa_ref_index_update(const uint16_t* K, const uint16_t* V, int Lmax, int pos
     reccnt[rc] += 1;
   }
 }
+
+/* ==================================================================================== prefill
+ * Index build of one request (KV rows h < HKV of K, V: (HKV, Lmax, 128) bf16; query rows
+ * r < R = G * HKV).  Orders as fixed by the device build (openattention_amd/csrc/oa_build.hip).
+ */
+
+/* QGS codes: ours_fastbuild.py:256-261, StaticTopKMasker._extend (static_top_k.py:174-181).
+ * zc_r = fma chain over d = 0..127 from 0; scale = max(max_t |zc| / 127, 1e-12);
+ * codes = clamp(rint(zc / scale), -127, 127).  codes (HKV, Lmax, 32), scale (HKV, 32). */
+void oa_ref_qgs_codes(const uint16_t* K, int Lmax, int HKV, int T, const float* U, int8_t* codes,
+                      float* scale) {
+  float* zc = (float*)malloc(sizeof(float) * (size_t)T * RQ);
+  for (int h = 0; h < HKV; ++h) {
+    const float* Uh = U + (long)h * D * RQ;
+    float amax[RQ];
+    for (int r = 0; r < RQ; ++r) amax[r] = 0.f;
+    for (int t = 0; t < T; ++t) {
+      const uint16_t* kr = K + ((long)h * Lmax + t) * D;
+      for (int r = 0; r < RQ; ++r) {
+        float z = 0.f;
+        for (int d = 0; d < D; ++d) z = fmaf(bf2f(kr[d]), Uh[d * RQ + r], z);
+        zc[(long)t * RQ + r] = z;
+        if (fabsf(z) > amax[r]) amax[r] = fabsf(z);
+      }
+    }
+    for (int r = 0; r < RQ; ++r) scale[h * RQ + r] = fmaxf(amax[r] / 127.0f, 1e-12f);
+    for (int t = 0; t < T; ++t)
+      for (int r = 0; r < RQ; ++r) {
+        const float q = fminf(fmaxf(rintf(zc[(long)t * RQ + r] / scale[h * RQ + r]), -127.f), 127.f);
+        codes[((long)h * Lmax + t) * RQ + r] = (int8_t)(int)q;
+      }
+  }
+  free(zc);
+}
+
+/* QGC projection before centring: zraw = bf16(k W) with the product's sum taken exactly and
+ * rounded once to fp32 (the device's bf16 matrix cores round their fp32 partials themselves, so
+ * the device agrees with this up to rare bf16 ties).  zraw (R, T, 16) bf16 bits. */
+void oa_ref_qgc_zraw(const uint16_t* K, int Lmax, int R, int G, int T, const uint16_t* W,
+                     uint16_t* zraw) {
+  for (int r = 0; r < R; ++r) {
+    const uint16_t* Wr = W + (long)r * D * RC;
+    for (int t = 0; t < T; ++t) {
+      const uint16_t* kr = K + ((long)(r / G) * Lmax + t) * D;
+      for (int j = 0; j < RC; ++j) {
+        long double s = 0.0L;
+        for (int d = 0; d < D; ++d) s += (long double)bf2f(kr[d]) * (long double)bf2f(Wr[d * RC + j]);
+        zraw[((long)r * T + t) * RC + j] = f2bf((float)s);
+      }
+    }
+  }
+}
+
+/* colmean and centring in the device's order: per 64-token tile and column, four lane partials
+ * g = 0..3 (tokens 64k + 16b + 4g + i, b then i ascending, fp64), combined (g0+g1)+(g2+g3);
+ * tiles summed in order; colmean = fp32(sum / T); zP = zraw - colmean (fp32). */
+void oa_ref_qgc_center(const uint16_t* zraw, int R, int T, float* zP, float* colmean) {
+  const int ntiles = (T + 63) / 64;
+  for (int r = 0; r < R; ++r) {
+    for (int j = 0; j < RC; ++j) {
+      double s = 0.0;
+      for (int k = 0; k < ntiles; ++k) {
+        double c[4];
+        for (int g = 0; g < 4; ++g) {
+          c[g] = 0.0;
+          for (int b = 0; b < 4; ++b)
+            for (int i = 0; i < 4; ++i) {
+              const int t = 64 * k + 16 * b + 4 * g + i;
+              if (t < T) c[g] += (double)bf2f(zraw[((long)r * T + t) * RC + j]);
+            }
+        }
+        s += (c[0] + c[1]) + (c[2] + c[3]);
+      }
+      colmean[r * RC + j] = (float)(s / (double)T);
+    }
+    for (int t = 0; t < T; ++t)
+      for (int j = 0; j < RC; ++j)
+        zP[((long)r * T + t) * RC + j] = bf2f(zraw[((long)r * T + t) * RC + j]) - colmean[r * RC + j];
+  }
+}
+
+/* k-means assignment (ours_fastbuild.py:52-82, methods_eager.py:536-540): a_t = argmax_c
+ * bf16(bf16(bf16(zP_t) . bf16(c)) - bf16(|c|^2 / 2)), the dot taken exactly and rounded once to
+ * fp32 (see oa_ref_qgc_zraw), |c|^2 = sequential fp32 sum of the rounded squares; ties to the
+ * lower cluster.  zP (R, T, 16); cent (R, C, 16); asg (R, T). */
+void oa_ref_kmeans_assign(const float* zP, int R, int T, const float* cent, int C, int32_t* asg) {
+  float* cb = (float*)malloc(sizeof(float) * (size_t)C * RC);
+  float* half = (float*)malloc(sizeof(float) * (size_t)C);
+  for (int r = 0; r < R; ++r) {
+    for (int c = 0; c < C; ++c) {
+      const float* cc = cent + ((long)r * C + c) * RC;
+      float s = 0.f;
+      for (int j = 0; j < RC; ++j) {
+        cb[c * RC + j] = bf_round(cc[j]);
+        s = s + cc[j] * cc[j];
+      }
+      half[c] = bf_round(0.5f * s);
+    }
+    for (int t = 0; t < T; ++t) {
+      float zb[RC];
+      for (int j = 0; j < RC; ++j) zb[j] = bf_round(zP[((long)r * T + t) * RC + j]);
+      int best_c = 0;
+      float best = 0.f;
+      for (int c = 0; c < C; ++c) {
+        double s = 0.0;   /* 16 products of bf16 values: exact in fp64 */
+        for (int j = 0; j < RC; ++j) s += (double)zb[j] * (double)cb[c * RC + j];
+        const float dist = bf_round(bf_round((float)s) - half[c]);
+        if (c == 0 || dist > best) { best = dist; best_c = c; }
+      }
+      asg[(long)r * T + t] = best_c;
+    }
+  }
+  free(cb);
+  free(half);
+}
+
+/* k-means update (ours_fastbuild.py:85-108, methods_eager.py:541-547): centroid = fp32(fp64 sum
+ * of the members' zP rows in position order / count); an empty cluster takes zP[init[c]].
+ * cnt (R, C) member counts. */
+void oa_ref_kmeans_update(const float* zP, int R, int T, const int32_t* asg, int C,
+                          const int32_t* init, float* cent, float* cnt) {
+  double* acc = (double*)malloc(sizeof(double) * (size_t)C * RC);
+  int* n = (int*)malloc(sizeof(int) * (size_t)C);
+  for (int r = 0; r < R; ++r) {
+    memset(acc, 0, sizeof(double) * (size_t)C * RC);
+    memset(n, 0, sizeof(int) * (size_t)C);
+    for (int t = 0; t < T; ++t) {
+      const int c = asg[(long)r * T + t];
+      n[c] += 1;
+      for (int j = 0; j < RC; ++j) acc[c * RC + j] += (double)zP[((long)r * T + t) * RC + j];
+    }
+    for (int c = 0; c < C; ++c) {
+      for (int j = 0; j < RC; ++j)
+        cent[((long)r * C + c) * RC + j] =
+            n[c] > 0 ? (float)(acc[c * RC + j] / (double)n[c]) : zP[((long)r * T + init[c]) * RC + j];
+      cnt[r * C + c] = (float)n[c];
+    }
+  }
+  free(acc);
+  free(n);
+}
+
+/* Cluster statistics and CSR lists (ours_fastbuild.py:111-139, 293-301): per cluster the
+ * members in position order; nb = count; Sk, Sk2, Sv = fp32 of the fp64 sums of k, k*k, v in that
+ * order; mem = members grouped by cluster (stable argsort), cstart = exclusive prefix, clen.
+ * nb (R, C); Sk, Sk2, Sv (R, C, 128); mem (R, T). */
+void oa_ref_cluster_build(const uint16_t* K, const uint16_t* V, int Lmax, int R, int G, int T,
+                          const int32_t* asg, int C, float* nb, float* Sk, float* Sk2, float* Sv,
+                          int32_t* mem, int32_t* cstart, int32_t* clen) {
+  double* acc = (double*)malloc(sizeof(double) * (size_t)C * D * 3);
+  int* n = (int*)malloc(sizeof(int) * (size_t)C);
+  int* fill = (int*)malloc(sizeof(int) * (size_t)C);
+  for (int r = 0; r < R; ++r) {
+    const int32_t* ar = asg + (long)r * T;
+    memset(acc, 0, sizeof(double) * (size_t)C * D * 3);
+    memset(n, 0, sizeof(int) * (size_t)C);
+    for (int t = 0; t < T; ++t) n[ar[t]] += 1;
+    int run = 0;
+    for (int c = 0; c < C; ++c) {
+      cstart[r * C + c] = run;
+      clen[r * C + c] = n[c];
+      nb[r * C + c] = (float)n[c];
+      fill[c] = run;
+      run += n[c];
+    }
+    for (int t = 0; t < T; ++t) {
+      const int c = ar[t];
+      mem[(long)r * T + fill[c]++] = t;
+      const uint16_t* kr = K + ((long)(r / G) * Lmax + t) * D;
+      const uint16_t* vr = V + ((long)(r / G) * Lmax + t) * D;
+      double* a = acc + (long)c * D * 3;
+      for (int d = 0; d < D; ++d) {
+        const double k = (double)bf2f(kr[d]);
+        a[d] += k;
+        a[D + d] += k * k;
+        a[2 * D + d] += (double)bf2f(vr[d]);
+      }
+    }
+    for (int c = 0; c < C; ++c)
+      for (int d = 0; d < D; ++d) {
+        const long o = ((long)r * C + c) * D + d;
+        Sk[o] = (float)acc[(long)c * D * 3 + d];
+        Sk2[o] = (float)acc[(long)c * D * 3 + D + d];
+        Sv[o] = (float)acc[(long)c * D * 3 + 2 * D + d];
+      }
+  }
+  free(acc);
+  free(n);
+  free(fill);
+}

@@ -201,6 +201,123 @@ def index_update(st: dict, pos: int, G: int, rmax: int) -> None:
                                _p(st["reclist"]), _p(st["reccnt"]), ct.c_int(rmax))
 
 
+# ------------------------------------------------------------------ prefill index build
+def qgs_codes(K_bf16: np.ndarray, T: int, U: np.ndarray):
+    """ours_fastbuild.py:256-261, static_top_k.py:174-181.  K (HKV, Lmax, 128) bf16 bits;
+    U (HKV, 128, 32).  Returns codes (HKV, Lmax, 32) int8 (zero past T), scale (HKV, 32)."""
+    K = _c(K_bf16, np.uint16)
+    HKV, Lmax = K.shape[0], K.shape[1]
+    U = _c(U, np.float32)
+    codes = np.zeros((HKV, Lmax, RQ), np.int8)
+    scale = np.zeros((HKV, RQ), np.float32)
+    _lib().oa_ref_qgs_codes(_p(K), ct.c_int(Lmax), ct.c_int(HKV), ct.c_int(T), _p(U), _p(codes), _p(scale))
+    return codes, scale
+
+
+def qgc_zraw(K_bf16: np.ndarray, T: int, W_bf16: np.ndarray, G: int) -> np.ndarray:
+    """bf16(k W) per query row (ours_fastbuild.py:264-275) with an exact product sum rounded once
+    to fp32.  W (R, 128, 16) bf16 bits.  Returns (R, T, 16) bf16 bits."""
+    K = _c(K_bf16, np.uint16)
+    W = _c(W_bf16, np.uint16)
+    R = W.shape[0]
+    out = np.zeros((R, T, RC), np.uint16)
+    _lib().oa_ref_qgc_zraw(_p(K), ct.c_int(K.shape[1]), ct.c_int(R), ct.c_int(G), ct.c_int(T), _p(W), _p(out))
+    return out
+
+
+def qgc_center(zraw_bf16: np.ndarray):
+    """colmean (the device's fixed fp64 order) and zP = zraw - colmean (methods_eager.py:529-531).
+    zraw (R, T, 16) bf16 bits.  Returns zP (R, T, 16) fp32, colmean (R, 16)."""
+    zr = _c(zraw_bf16, np.uint16)
+    R, T = zr.shape[0], zr.shape[1]
+    zP = np.zeros((R, T, RC), np.float32)
+    cm = np.zeros((R, RC), np.float32)
+    _lib().oa_ref_qgc_center(_p(zr), ct.c_int(R), ct.c_int(T), _p(zP), _p(cm))
+    return zP, cm
+
+
+def kmeans_assign(zP: np.ndarray, cent: np.ndarray) -> np.ndarray:
+    """ours_fastbuild.py:52-82 bf16 rule, ties to the lower cluster.  zP (R, T, 16); cent (R, C, 16)."""
+    zP = _c(zP, np.float32)
+    cent = _c(cent, np.float32)
+    R, T = zP.shape[0], zP.shape[1]
+    C = cent.shape[1]
+    asg = np.zeros((R, T), np.int32)
+    _lib().oa_ref_kmeans_assign(_p(zP), ct.c_int(R), ct.c_int(T), _p(cent), ct.c_int(C), _p(asg))
+    return asg
+
+
+def kmeans_update(zP: np.ndarray, asg: np.ndarray, C: int, init: np.ndarray):
+    """ours_fastbuild.py:85-108: member means (fp64 sums in position order), empty -> zP[init].
+    Returns cent (R, C, 16), cnt (R, C)."""
+    zP = _c(zP, np.float32)
+    asg = _c(asg, np.int32)
+    init = _c(init, np.int32)
+    R, T = zP.shape[0], zP.shape[1]
+    cent = np.zeros((R, C, RC), np.float32)
+    cnt = np.zeros((R, C), np.float32)
+    _lib().oa_ref_kmeans_update(_p(zP), ct.c_int(R), ct.c_int(T), _p(asg), ct.c_int(C), _p(init), _p(cent), _p(cnt))
+    return cent, cnt
+
+
+def cluster_build(K_bf16: np.ndarray, V_bf16: np.ndarray, T: int, asg: np.ndarray, C: int, G: int):
+    """ours_fastbuild.py:111-139, 293-301.  K, V (HKV, Lmax, 128) bf16 bits; asg (R, T).
+    Returns nb, Sk, Sk2, Sv, mem (R, T), cstart, clen."""
+    K, V = _c(K_bf16, np.uint16), _c(V_bf16, np.uint16)
+    asg = _c(asg, np.int32)
+    R = asg.shape[0]
+    nb = np.zeros((R, C), np.float32)
+    Sk, Sk2, Sv = (np.zeros((R, C, D), np.float32) for _ in range(3))
+    mem = np.zeros((R, T), np.int32)
+    cstart = np.zeros((R, C), np.int32)
+    clen = np.zeros((R, C), np.int32)
+    _lib().oa_ref_cluster_build(_p(K), _p(V), ct.c_int(K.shape[1]), ct.c_int(R), ct.c_int(G), ct.c_int(T),
+                                _p(asg), ct.c_int(C), _p(nb), _p(Sk), _p(Sk2), _p(Sv), _p(mem), _p(cstart),
+                                _p(clen))
+    return nb, Sk, Sk2, Sv, mem, cstart, clen
+
+
+def build_row(st, b: int, K, V, qrows, T: int, M_pre, inv_freq, scaling: float, layer: int,
+              G: int = 4, iters: int = 4) -> None:
+    """CPU counterpart of openattention_amd.prefill.build_row: the metric and bases (a10, host
+    torch code shared with the product) and the restated codes, projection, k-means and
+    cluster statistics (a11-a13).  st: a LayerState on the CPU; K, V: (HKV, >=T, 128) bf16."""
+    import torch
+    from openattention_amd import prefill
+    HKV = K.shape[0]
+    HQ = HKV * G
+    C = st.C
+    U, W = prefill.bases(prefill.query_metric(M_pre, qrows, T, inv_freq, scaling), HKV, G)
+    kb = K.contiguous().view(torch.int16).numpy().view(np.uint16)
+    vb = V.contiguous().view(torch.int16).numpy().view(np.uint16)
+    Wb = W.contiguous().view(torch.int16).numpy().view(np.uint16)
+    codes, scale = qgs_codes(kb, T, U.numpy())
+    zP, cm = qgc_center(qgc_zraw(kb, T, Wb, G))
+    init = prefill.kmeans_init(T, C, layer).numpy().astype(np.int32)
+    cent = zP[:, init].copy()
+    for _ in range(iters):
+        asg = kmeans_assign(zP, cent)
+        cent, _cnt = kmeans_update(zP, asg, C, init)
+    nb, Sk, Sk2, Sv, mem, cstart, clen = cluster_build(kb, vb, T, asg, C, G)
+    r0, q0 = b * HKV, b * HQ
+    st.codes[r0:r0 + HKV, :T] = torch.from_numpy(codes[:, :T])
+    st.U[r0:r0 + HKV] = U
+    st.scale[r0:r0 + HKV] = torch.from_numpy(scale)
+    st.W[q0:q0 + HQ] = W
+    st.colmean[q0:q0 + HQ] = torch.from_numpy(cm)
+    st.cent[q0:q0 + HQ] = torch.from_numpy(cent)
+    st.asg[q0:q0 + HQ, :T] = torch.from_numpy(asg)
+    st.asg8[q0:q0 + HQ, :T] = torch.from_numpy(asg.astype(np.uint8))
+    st.nb[q0:q0 + HQ] = torch.from_numpy(nb)
+    st.Sk[q0:q0 + HQ] = torch.from_numpy(Sk)
+    st.Sk2[q0:q0 + HQ] = torch.from_numpy(Sk2)
+    st.Sv[q0:q0 + HQ] = torch.from_numpy(Sv)
+    st.mem[q0:q0 + HQ, :T] = torch.from_numpy(mem)
+    st.cstart[q0:q0 + HQ] = torch.from_numpy(cstart)
+    st.clen[q0:q0 + HQ] = torch.from_numpy(clen)
+    st.reccnt[q0:q0 + HQ] = 0
+
+
 # ------------------------------------------------------------------ composition
 def decode_step(st: dict, q_bf16: np.ndarray, n: int, ns: int, nl: int, k: int, E: int, G: int,
                 sm: float, sm2: float, rmax: int = 256, update_index: bool = True) -> dict:

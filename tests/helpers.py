@@ -9,6 +9,7 @@ import torch
 from openattention_amd import synth
 from openattention_amd.budget import budget
 from openattention_amd.prefill import LayerState, build_row
+from oracle import oracle as O
 
 HQ, HKV, D, G = 32, 8, 128, 4
 SC = D ** -0.5
@@ -42,9 +43,11 @@ def build_layer(cfg: int, B: int, N: int, Lmax: int, C: int, n_centers: int, dev
         static = synth.static_metric(layer + 1, dev="cpu")
     st = LayerState(B, HKV, G, Lmax, C, rmax, dev)
     T = N - 1
+    # the product build runs on the HIP kernels; on the CPU the restatement builds the state
+    build = build_row if torch.device(dev).type == "cuda" else O.build_row
     for b in range(B):
-        build_row(st, b, K[b], V[b], qq[b], T, static["M"][layer], static["inv_freq"],
-                  float(static["attention_scaling"]), layer, G)
+        build(st, b, K[b], V[b], qq[b], T, static["M"][layer], static["inv_freq"],
+              float(static["attention_scaling"]), layer, G)
     return types.SimpleNamespace(K=K, V=V, q=q, qq=qq, st=st, T=T, N=N, Lmax=Lmax, B=B, C=C,
                                  static=static, npos=npos)
 

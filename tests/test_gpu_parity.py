@@ -456,3 +456,125 @@ def test_decode_step_graph_replay(lay4k):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {rep} differs from eager"
+
+
+# ------------------------------------------------------------------ prefill index build (a11-a13)
+def _bf16_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+@pytest.mark.parametrize("T", [4095, 777])
+def test_build_codes_bit_exact(T):
+    print(f"[case] build codes T={T}", flush=True)
+    rng = np.random.default_rng(T)
+    HKV_, Lmax = 8, 4160
+    K = f32_to_bf16(rng.standard_normal((HKV_, Lmax, D)).astype(np.float32))
+    U = np.linalg.qr(rng.standard_normal((HKV_, D, D)))[0][..., :32].astype(np.float32)
+    codes = torch.zeros(HKV_, Lmax, 32, device=DEV, dtype=torch.int8)
+    scale = torch.zeros(HKV_, 32, device=DEV)
+    ws = torch.empty(HKV_ * 32, device=DEV, dtype=torch.int32)
+    ops.qgs_codes(_bf16_dev(K), T, _f32(U), codes, scale, ws)
+    torch.cuda.synchronize()
+    rc, rs = O.qgs_codes(K, T, U)
+    assert np.array_equal(scale.cpu().numpy(), rs)
+    assert np.array_equal(codes.cpu().numpy(), rc)
+
+
+@pytest.mark.parametrize("T", [4095, 1000])
+def test_build_projection_and_kmeans(T):
+    """QGC projection on the bf16 matrix cores: bf16(k W) agrees with the exact-sum restatement
+    up to rare bf16 ties; colmean and zP are bit-exact given the device's bf16(k W).  k-means:
+    the assignment agrees with the restatement's on the same zP and centroids up to rare ties;
+    the update is bit-exact given the device's assignment."""
+    print(f"[case] build projection + k-means T={T}", flush=True)
+    rng = np.random.default_rng(7 + T)
+    HKV_, G_, Lmax, C = 2, 4, 4160, 64
+    R = HKV_ * G_
+    K = f32_to_bf16(rng.standard_normal((HKV_, Lmax, D)).astype(np.float32))
+    W = f32_to_bf16((rng.standard_normal((R, D, 16)) * 0.3).astype(np.float32))
+    zP = torch.empty(R, T, 16, device=DEV)
+    zraw = torch.empty(R, T, 16, device=DEV, dtype=torch.int16)
+    cm = torch.empty(R, 16, device=DEV)
+    ops.qgc_project(_bf16_dev(K), T, _bf16_dev(W), G_, zP, cm, zraw=zraw)
+    torch.cuda.synchronize()
+    zr_gpu = zraw.cpu().numpy().view(np.uint16)
+    zr_ref = O.qgc_zraw(K, T, W, G_)
+    agree = (zr_gpu == zr_ref).mean()
+    print(f"  bf16(kW) agreement {agree:.6f}")
+    assert agree > 0.999
+    zP_ref, cm_ref = O.qgc_center(zr_gpu)
+    assert np.array_equal(cm.cpu().numpy(), cm_ref)
+    assert np.array_equal(zP.cpu().numpy(), zP_ref)
+    init = rng.choice(T, C, replace=False).astype(np.int32)
+    cent = zP[:, torch.from_numpy(init).long().to(DEV)].contiguous()
+    asg = torch.full((R, Lmax), -1, device=DEV, dtype=torch.int32)
+    asg8 = torch.zeros(R, -(-Lmax // 64) * 64, device=DEV, dtype=torch.uint8)
+    zP_np = zP.cpu().numpy()
+    init_d = _i32(init)
+    for it in range(4):
+        cent_np = cent.cpu().numpy()
+        ops.kmeans_assign(zP, T, cent, asg, asg8)
+        torch.cuda.synchronize()
+        a_gpu = asg.cpu().numpy()[:, :T]
+        a_ref = O.kmeans_assign(zP_np, cent_np)
+        agree = (a_gpu == a_ref).mean()
+        print(f"  iteration {it}: assignment agreement {agree:.6f}")
+        assert agree > 0.999
+        assert np.array_equal(asg8.cpu().numpy()[:, :T], a_gpu.astype(np.uint8))
+        assert np.all(asg.cpu().numpy()[:, T:] == -1)
+        cnt = torch.empty(R, C, device=DEV)
+        ops.kmeans_update(zP, T, asg8, init_d, cent, cnt)
+        torch.cuda.synchronize()
+        c_ref, n_ref = O.kmeans_update(zP_np, a_gpu, C, init)
+        assert np.array_equal(cent.cpu().numpy(), c_ref)
+        assert np.array_equal(cnt.cpu().numpy(), n_ref)
+
+
+@pytest.mark.parametrize("T,C", [(4095, 64), (600, 8)])
+def test_build_cluster_stats_bit_exact(T, C):
+    print(f"[case] build cluster stats T={T} C={C}", flush=True)
+    rng = np.random.default_rng(T + C)
+    HKV_, G_, Lmax = 2, 4, 4160
+    R = HKV_ * G_
+    K = f32_to_bf16(rng.standard_normal((HKV_, Lmax, D)).astype(np.float32))
+    V = f32_to_bf16(rng.standard_normal((HKV_, Lmax, D)).astype(np.float32))
+    p = rng.dirichlet(np.ones(C) * 0.5)
+    asg = rng.choice(C, size=(R, T), p=p).astype(np.int32)
+    asg[0, :] = np.where(asg[0] == 1, 0, asg[0])                # an empty cluster in row 0
+    asg8 = torch.zeros(R, -(-Lmax // 64) * 64, device=DEV, dtype=torch.uint8)
+    asg8[:, :T] = torch.from_numpy(asg.astype(np.uint8)).to(DEV)
+    nb = torch.empty(R, C, device=DEV)
+    Sk, Sk2, Sv = (torch.empty(R, C, D, device=DEV) for _ in range(3))
+    mem = torch.full((R, Lmax), -1, device=DEV, dtype=torch.int32)
+    cstart = torch.empty(R, C, device=DEV, dtype=torch.int32)
+    clen = torch.empty(R, C, device=DEV, dtype=torch.int32)
+    ops.cluster_build(_bf16_dev(K), _bf16_dev(V), T, G_, asg8, C, nb, Sk, Sk2, Sv, mem, cstart, clen)
+    torch.cuda.synchronize()
+    ref = O.cluster_build(K, V, T, asg, C, G_)
+    got = (nb, Sk, Sk2, Sv, mem[:, :T], cstart, clen)
+    for name, g, r in zip(("nb", "Sk", "Sk2", "Sv", "mem", "cstart", "clen"), got, ref):
+        assert np.array_equal(g.cpu().numpy(), r), name
+    assert np.all(mem.cpu().numpy()[:, T:] == -1)
+
+
+def test_build_row_on_device_matches_restated_stages():
+    """prefill.build_row (HIP stages) on a fresh layer leaves a state whose codes are the
+    restated codes from its own U and whose statistics and member lists are the restated ones
+    over its own assignment."""
+    print("[case] build_row on device", flush=True)
+    lay = build_layer(cfg=1, B=1, N=2048, Lmax=2048 + 64, C=8, n_centers=64, dev=DEV)
+    st, T = lay.st, lay.T
+    s = st.to_numpy()
+    Kb = bf16_np(lay.K[0])
+    Vb = bf16_np(lay.V[0])
+    rc, rs = O.qgs_codes(Kb, T, s["U"][:HKV])
+    assert np.array_equal(s["scale"][:HKV], rs)
+    assert np.array_equal(s["codes"][:HKV], rc)
+    asg = s["asg"][:HQ, :T]
+    nb, Sk, Sk2, Sv, mem, cstart, clen = O.cluster_build(Kb, Vb, T, asg, lay.C, G)
+    assert np.array_equal(s["nb"][:HQ], nb)
+    assert np.array_equal(s["Sk"][:HQ], Sk) and np.array_equal(s["Sk2"][:HQ], Sk2)
+    assert np.array_equal(s["Sv"][:HQ], Sv)
+    assert np.array_equal(s["mem"][:HQ, :T], mem)
+    assert np.array_equal(s["cstart"][:HQ], cstart) and np.array_equal(s["clen"][:HQ], clen)
+    assert np.array_equal(s["asg8"][:HQ, :T], asg.astype(np.uint8))

@@ -447,3 +447,97 @@ def test_residual_closed_form():
                 assert abs(ln[r, c] - math.log(len(rest))) < 1e-12
             else:
                 assert ln[r, c] == -np.inf
+
+
+# ------------------------------------------------------------------ prefill index build (a11-a13)
+def _bf16_rows(shape, scale=1.0, rng=RNG):
+    return f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def test_qgs_codes_vs_fp64_projection():
+    """codes = clamp(rint(zc / scale)) with scale = max|zc| / 127: against an independent fp64
+    projection (codes may differ only where zc / scale sits within 1e-3 of a rounding midpoint)."""
+    HKV, Lmax, T = 2, 700, 650
+    K = _bf16_rows((HKV, Lmax, 128))
+    U = np.linalg.qr(RNG.standard_normal((HKV, 128, 128)))[0][..., :32].astype(np.float32)
+    codes, scale = O.qgs_codes(K, T, U)
+    zc = np.einsum("htd,hdr->htr", bf16_to_f32(K[:, :T]).astype(np.float64), U.astype(np.float64))
+    amax = np.abs(zc).max(1)
+    np.testing.assert_allclose(scale, (amax / 127.0).astype(np.float32), rtol=1e-6)
+    ratio = zc / scale[:, None, :].astype(np.float64)
+    ref = np.clip(np.rint(ratio), -127, 127)
+    near = np.abs(np.abs(ratio - np.floor(ratio)) - 0.5) < 1e-3
+    assert np.all((codes[:, :T] == ref) | near)
+    assert np.all(np.abs(codes[:, :T]).max(1) == 127)
+    assert np.all(codes[:, T:] == 0)
+
+
+def test_qgc_projection_vs_fp64_and_mean():
+    """zraw = bf16(k W) with the product sum exact (numpy fp64); colmean = mean of zraw;
+    zP = zraw - colmean."""
+    HKV, G, Lmax, T = 2, 4, 300, 257
+    R = HKV * G
+    K = _bf16_rows((HKV, Lmax, 128))
+    W = _bf16_rows((R, 128, 16), 0.3)
+    zr = O.qgc_zraw(K, T, W, G)
+    kf = bf16_to_f32(K[:, :T]).astype(np.float64)
+    Wf = bf16_to_f32(W).astype(np.float64)
+    exact = np.stack([kf[r // G] @ Wf[r] for r in range(R)])
+    assert np.array_equal(zr, f32_to_bf16(exact.astype(np.float32)))
+    zP, cm = O.qgc_center(zr)
+    zf = bf16_to_f32(zr).astype(np.float64)
+    assert np.array_equal(cm, (zf.sum(1) / T).astype(np.float32))
+    assert np.array_equal(zP, (bf16_to_f32(zr) - cm[:, None, :]).astype(np.float32))
+
+
+def test_kmeans_assign_vs_torch_bf16_rule():
+    """The assignment equals the reference formulation in torch's bf16 arithmetic
+    (methods_eager.py:536-540: bf16 matmul, bf16 half-norm, argmax) up to near-ties of the bf16
+    distance, and exactly on a hand case with a tie (lower cluster wins)."""
+    import torch
+    R, T, C = 3, 400, 12
+    zP = (RNG.standard_normal((R, T, 16)) * 2).astype(np.float32)
+    cent = (RNG.standard_normal((R, C, 16)) * 2).astype(np.float32)
+    got = O.kmeans_assign(zP, cent)
+    zt, ct_ = torch.from_numpy(zP), torch.from_numpy(cent)
+    half = (0.5 * (ct_ * ct_).sum(-1)).to(torch.bfloat16).unsqueeze(1)
+    ref = (torch.matmul(zt.to(torch.bfloat16), ct_.to(torch.bfloat16).transpose(1, 2)) - half).argmax(-1).numpy()
+    assert (got == ref).mean() > 0.99
+    # tie: two identical centroids -> the lower id
+    cent2 = cent.copy()
+    cent2[:, 7] = cent2[:, 3]
+    got2 = O.kmeans_assign(zP, cent2)
+    assert not np.any(got2 == 7)
+
+
+def test_kmeans_update_and_cluster_build_vs_numpy():
+    """Member means (fp64) / empty -> initial point; cluster sums, counts and CSR lists against
+    numpy's stable argsort and fp64 sums (exact for bf16 inputs)."""
+    HKV, G, Lmax, T, C = 2, 4, 520, 500, 9
+    R = HKV * G
+    zP = (RNG.standard_normal((R, T, 16))).astype(np.float32)
+    asg = RNG.integers(0, C - 1, size=(R, T)).astype(np.int32)     # cluster C-1 stays empty
+    init = RNG.choice(T, C, replace=False).astype(np.int32)
+    cent, cnt = O.kmeans_update(zP, asg, C, init)
+    for r in range(R):
+        for c in range(C):
+            m = asg[r] == c
+            assert cnt[r, c] == m.sum()
+            ref = zP[r, m].astype(np.float64).mean(0).astype(np.float32) if m.any() else zP[r, init[c]]
+            np.testing.assert_allclose(cent[r, c], ref, rtol=2e-7, atol=1e-7)
+    K = _bf16_rows((HKV, Lmax, 128))
+    V = _bf16_rows((HKV, Lmax, 128))
+    nb, Sk, Sk2, Sv, mem, cstart, clen = O.cluster_build(K, V, T, asg, C, G)
+    kf = bf16_to_f32(K[:, :T]).astype(np.float64)
+    vf = bf16_to_f32(V[:, :T]).astype(np.float64)
+    for r in range(R):
+        order = np.argsort(asg[r], kind="stable")
+        assert np.array_equal(mem[r], order)
+        cntr = np.bincount(asg[r], minlength=C)
+        assert np.array_equal(clen[r], cntr) and np.array_equal(nb[r], cntr.astype(np.float32))
+        assert np.array_equal(cstart[r], np.concatenate([[0], np.cumsum(cntr)[:-1]]))
+        for c in range(C):
+            m = asg[r] == c
+            assert np.array_equal(Sk[r, c], kf[r // G, m].sum(0).astype(np.float32))
+            assert np.array_equal(Sk2[r, c], (kf[r // G, m] ** 2).sum(0).astype(np.float32))
+            assert np.array_equal(Sv[r, c], vf[r // G, m].sum(0).astype(np.float32))
