@@ -31,6 +31,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HQ, HKV, D, G = 32, 8, 128, 4
+PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
 
 
@@ -82,6 +83,23 @@ def traffic_bytes(stage: str):
         return None
 
 
+def prefill_report(build_ms: dict, B: int, T: int, C: int):
+    """Per-stage time of one layer's index build (all B batch rows, prefix T) and the bf16
+    matrix-core utilisation of the projection (k W: 2*T*128*16 flops per query row) and of the
+    four k-means assignments (2*T*C16*16 flops per query row each, C16 = C rounded up to 16)."""
+    if not build_ms:
+        return None
+    R = B * HQ
+    tot = sum(build_ms.values())
+    proj_fl = 2.0 * R * T * D * 16
+    asg_fl = 4 * 2.0 * R * T * (-(-C // 16) * 16) * 16
+    return {"ms_per_layer": round(tot, 3), "rows": R, "prefix": T,
+            "stages_ms": {k: round(v, 3) for k, v in build_ms.items()},
+            "mfma_bf16_tflops": {"project": round(proj_fl / (build_ms["project"] * 1e-3) / 1e12, 1),
+                                 "kmeans_incl_update": round(asg_fl / (build_ms["kmeans"] * 1e-3) / 1e12, 1)},
+            "mfma_peak_tflops": PEAK_BF16_TFLOPS}
+
+
 def pmc_calibration():
     """A plain device copy of known size (1 GiB read, 1 GiB written) for scaling the
     FETCH_SIZE / WRITE_SIZE counters: run under rocprofv3 --pmc."""
@@ -125,15 +143,26 @@ def main():
     m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=L, static=static, groups=a.groups)
     Ks, Vs, Qs = [], [], []
     t0 = time.time()
+    build_ms = {}
     for l in range(L):
         K, V, q, qq, _ = synth.make_layer(3, B, N + n_steps, Lmax, 256, dev, layer=l)
+        bmarks = [] if l == L - 1 else None          # the last replica's build is timed per stage
         for b in range(B):
-            build_row(m.st[l], b, K[b], V[b], qq[b], T0, static["M"][l], static["inv_freq"], 1.0, l, G)
+            mk = [] if bmarks is not None else None
+            build_row(m.st[l], b, K[b], V[b], qq[b], T0, static["M"][l], static["inv_freq"], 1.0, l, G,
+                      marks=mk)
+            if mk is not None:
+                bmarks.append(mk)
         Ks.append(K)
         Vs.append(V)
         Qs.append(q)
         del qq
         torch.cuda.synchronize()
+        if bmarks is not None:
+            for mk in bmarks:
+                for (_, e0), (name, e1) in zip(mk[:-1], mk[1:]):
+                    key = "kmeans" if name.startswith("kmeans") else name
+                    build_ms[key] = build_ms.get(key, 0.0) + e0.elapsed_time(e1)
         log(f"[bench] layer {l} built ({time.time() - t0:.1f}s)")
     CTX.K, CTX.V = Ks, Vs
     n_arr = torch.arange(N, N + n_steps, device=dev, dtype=torch.int32)
@@ -335,6 +364,7 @@ def main():
         "dense_us": dense,
         "speedup_vs_dense": round(dense_best / us_layer, 2) if dense_best else None,
         "cpu_baseline": cpu,
+        "prefill_build": prefill_report(build_ms, B, T0, Cn),
     }
     print(json.dumps(rec), flush=True)
 

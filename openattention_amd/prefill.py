@@ -140,11 +140,19 @@ def kmeans_init(T: int, C: int, layer: int) -> torch.Tensor:
 @torch.no_grad()
 def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int,
               M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, layer: int,
-              G: int = 4) -> None:
+              G: int = 4, marks: list | None = None) -> None:
     """Build batch row b of one layer's index into `st` (a LayerState on a HIP device).
 
     K, V: (HKV, >=T, D) bf16 of this batch row; qrows: (HQ, Qn, D) question rows.
+    marks: if a list, (stage, event) pairs are appended, recorded on the current stream after
+    each stage (per-stage timing).
     """
+    def mark(name):
+        if marks is not None:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            marks.append((name, e))
+
     from openattention_amd import ops
     dev = K.device
     if dev.type != "cuda":
@@ -152,28 +160,36 @@ def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor,
     HKV = K.shape[0]
     HQ = HKV * G
     C = st.C
+    mark("start")
     M = query_metric(M_pre.to(dev), qrows, T, inv_freq.to(dev), scaling)           # (HQ, D, D)
     U, W = bases(M, HKV, G)
     r0, q0 = b * HKV, b * HQ
     st.U[r0:r0 + HKV] = U
     st.W[q0:q0 + HQ] = W
+    mark("metric_bases")
     # a11: QGS codes and scale
     amax = torch.empty(HKV * RQ, device=dev, dtype=torch.int32)
     ops.qgs_codes(K, T, st.U[r0:r0 + HKV], st.codes[r0:r0 + HKV], st.scale[r0:r0 + HKV], amax)
+    mark("codes")
     # a12: QGC projection and k-means
     zP = torch.empty(HQ, T, RC, device=dev)
     ops.qgc_project(K, T, st.W[q0:q0 + HQ], G, zP, st.colmean[q0:q0 + HQ])
+    mark("project")
     init = kmeans_init(T, C, layer).to(device=dev, dtype=torch.int32)
     cent = st.cent[q0:q0 + HQ]
     cent.copy_(zP.index_select(1, init.long()))
     asg, asg8 = st.asg[q0:q0 + HQ], st.asg8[q0:q0 + HQ]
+    mark("kmeans_init")
     for _ in range(ITERS):
         ops.kmeans_assign(zP, T, cent, asg, asg8)
+        mark("kmeans_assign")
         ops.kmeans_update(zP, T, asg8, init, cent)
+        mark("kmeans_update")
     # a13: cluster statistics and CSR member lists
     ops.cluster_build(K, V, T, G, asg8, C, st.nb[q0:q0 + HQ], st.Sk[q0:q0 + HQ], st.Sk2[q0:q0 + HQ],
                       st.Sv[q0:q0 + HQ], st.mem[q0:q0 + HQ], st.cstart[q0:q0 + HQ], st.clen[q0:q0 + HQ])
     st.reccnt[q0:q0 + HQ] = 0
+    mark("cluster_build")
 
 
 class LayerState:
