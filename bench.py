@@ -52,6 +52,10 @@ def parse():
                    help="split the batch into this many sequence groups on their own streams")
     p.add_argument("--pmc-calibration", action="store_true",
                    help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
+    p.add_argument("--config4", action="store_true",
+                   help="long-context sweep instead: B=8, N in {65536, 131072}, 1%% and 3%%, 512-centre "
+                        "mixture with 8 needles per KV head; one JSON line per point (us/layer-step, "
+                        "needle recall, agreement with the CPU restatement on sequence 0)")
     return p.parse_args()
 
 
@@ -100,6 +104,128 @@ def prefill_report(build_ms: dict, B: int, T: int, C: int):
             "mfma_peak_tflops": PEAK_BF16_TFLOPS}
 
 
+def config4_sweep(a):
+    """per (N, rho) one decode step's needle recall over all rows (sel U exp
+    of every query head against the two needles planted for it), the same step restated on the
+    CPU for sequence 0 (selection compared), then the hipGraph-timed layer-step over two layer
+    replicas.  (C, E) scale with N (run_multibin_hat_bench.py:397-413) with C capped at 256."""
+    import types
+
+    import numpy as np
+    import torch
+
+    from openattention_amd import _build, lib, synth
+    if not os.path.exists(_build.lib_path()):
+        _build.build()
+    lib.load()
+    from openattention_amd.method import C as CTX, OursHIP
+    from openattention_amd.prefill import build_row
+    from oracle import oracle as O
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    B, L, NEEDLES = 8, 2, 8
+
+    def np16(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+    for N in (65536, 131072):
+        for rho in (0.01, 0.03):
+            n_steps = a.warmup + a.steps
+            Lmax = N + n_steps + 1
+            T0 = N - 1
+            static = synth.static_metric(L)
+            m = OursHIP(types.SimpleNamespace(rho=rho), B, Lmax, dev, n_layers=L, static=static, ctx_len=N,
+                        groups=2)
+            Ks, Vs, Qs, npos = [], [], [], None
+            t0 = time.time()
+            for l in range(L):
+                K, V, q, qq, pos = synth.make_layer(4, B, N + n_steps, Lmax, 512, dev, layer=l, needles=NEEDLES)
+                for b in range(B):
+                    build_row(m.st[l], b, K[b], V[b], qq[b], T0, static["M"][l], static["inv_freq"], 1.0, l, G)
+                Ks.append(K)
+                Vs.append(V)
+                Qs.append(q)
+                if l == 0:
+                    npos = pos
+                del qq
+            torch.cuda.synchronize()
+            log(f"[config4] N={N} rho={rho}: {L} layers built ({time.time() - t0:.1f}s), C={m.Cn} E={m.E}")
+            CTX.K, CTX.V = Ks, Vs
+            CTX.n0_dev = torch.tensor([T0], device=dev, dtype=torch.int32)
+            n_buf = torch.tensor([N], device=dev, dtype=torch.int32)
+            CTX.n_dev = n_buf
+            # ---- needle recall at the first decode step (layer 0), and sequence 0 on the CPU
+            pre = {f: getattr(m.st[0], f)[slice(0, HKV) if f in ("codes", "U", "scale") else slice(0, HQ)]
+                   .detach().cpu().numpy().copy()
+                   for f in ("codes", "U", "scale", "colmean", "cent", "asg", "nb", "Sk", "Sk2", "Sv",
+                             "reclist", "reccnt")}
+            pre["W"] = np16(m.st[0].W[:HQ])
+            pre["K"], pre["V"] = np16(Ks[0][0]), np16(Vs[0][0])
+            m.decode(0, Qs[0], N, marks=[])
+            torch.cuda.synchronize()
+            sel = m.last_sel.cpu().numpy()
+            ex = m.exp_idx.cpu().numpy()[:, :m.E]
+            hit = tot = 0
+            for r in range(B * HQ):
+                bq, hq = divmod(r, HQ)
+                h, gq = divmod(hq, G)
+                read = set(sel[r].tolist()) | set(ex[r][ex[r] >= 0].tolist())
+                for j in range(NEEDLES):
+                    if j % G == gq:
+                        tot += 1
+                        hit += int(npos[bq, h, j]) in read
+            ns, nl, k = m.bud.counts(N)
+            ref = O.decode_step(pre, np16(Qs[0][0].reshape(-1, D)), N, ns, nl, k, m.E, G,
+                                np.float32(D ** -0.5), np.float32(float(np.float32(D ** -0.5)) ** 2))
+            same = bool(np.array_equal(sel[:HQ], ref["sel"]) and np.array_equal(ex[:HQ], ref["exp_idx"]))
+            hit0 = tot0 = 0
+            for r in range(HQ):
+                h, gq = divmod(r, G)
+                read = set(ref["sel"][r].tolist()) | set(ref["exp_idx"][r][ref["exp_idx"][r] >= 0].tolist())
+                for j in range(NEEDLES):
+                    if j % G == gq:
+                        tot0 += 1
+                        hit0 += int(npos[0, h, j]) in read
+            # ---- timing: one captured step of both replicas, K replays
+            n_arr = torch.arange(N + 1, N + 1 + n_steps, device=dev, dtype=torch.int32)
+            for i in range(a.warmup):
+                n_buf.copy_(n_arr[i:i + 1])
+                for l in range(L):
+                    m.decode(l, Qs[l], N + 1 + i)
+            torch.cuda.synchronize()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for l in range(L):
+                    m.decode(l, Qs[l], N + 1 + a.warmup)
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for l in range(L):
+                    m.decode(l, Qs[l], N + 1 + a.warmup)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(a.warmup, n_steps):
+                n_buf.copy_(n_arr[i:i + 1])
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (a.steps * L)
+            rec = {"config": "config4", "B": B, "N": N, "rho": rho, "C": m.Cn, "E": m.E,
+                   "sink_local_topk": [ns, nl, k], "realised_read": round(m.bud.realised_read(N), 5),
+                   "us_per_layer_step": round(us, 2), "tokens_per_s": round(B / (us * 1e-6), 1),
+                   "needle_recall": round(hit / tot, 4), "needles": tot,
+                   "seq0_recall": round(hit0 / tot0, 4), "seq0_recall_restatement": round(hit0 / tot0, 4),
+                   "seq0_selection_equals_restatement": same,
+                   "data": "synthetic (seeded 512-centre mixture per KV head, 8 needles per KV head at cosine 0.9)"}
+            print(json.dumps(rec), flush=True)
+            del m, Ks, Vs, Qs, graph
+            torch.cuda.empty_cache()
+
+
 def pmc_calibration():
     """A plain device copy of known size (1 GiB read, 1 GiB written) for scaling the
     FETCH_SIZE / WRITE_SIZE counters: run under rocprofv3 --pmc."""
@@ -119,6 +245,9 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): the sparse decode "
               "stage needs no collective and this build measures one GPU's share", flush=True)
         sys.exit(2)
+    if a.config4:
+        config4_sweep(a)
+        return
     if a.pmc_calibration:
         pmc_calibration()
         return

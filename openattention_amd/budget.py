@@ -51,8 +51,12 @@ class Budget:
         return (ns + nl + k + self.E + PROXY_ROWS * self.C) / n
 
 
-def budget(rho: float, ctx_len: int = CTX_LEN, rule: str = "multibin") -> Budget:
-    """The deployed (C, E) split for read fraction rho, scaled to the accounting context."""
+def budget(rho: float, ctx_len: int = CTX_LEN, rule: str = "multibin", c_max: int | None = None) -> Budget:
+    """The deployed (C, E) split for read fraction rho, scaled to the accounting context.
+
+    c_max caps the cluster count (this build keeps cluster ids as bytes: at most 256); the 1.5
+    rows of every proxy a capped split drops go to the exact-read budget E, so rho and the top-k
+    share are unchanged."""
     key = round(float(rho), 4)
     if key not in DEPLOYED:
         raise ValueError(f"no deployed (C, E) split for rho={rho}; known: {sorted(DEPLOYED)}")
@@ -64,6 +68,9 @@ def budget(rho: float, ctx_len: int = CTX_LEN, rule: str = "multibin") -> Budget
     else:
         C = max(1, int(round(C0 * ctx_len / CTX_LEN)))
         E = max(0, int(round(E0 * ctx_len / CTX_LEN)))
+    if c_max is not None and C > int(c_max):
+        E += int(round(PROXY_ROWS * (C - int(c_max))))
+        C = int(c_max)
     b = Budget(rho=float(rho), C=C, E=E, ctx_len=int(ctx_len), rule=rule)
     if b.heavy_frac() <= 0:
         raise ValueError(f"rho={rho} leaves no top-k budget at C={C}, E={E}")

@@ -73,4 +73,5 @@ def call(name: str, *args) -> None:
     st = getattr(lib, name)(*args)
     if st != 0:
         msg = lib.oa_error_string(st).decode()
-        raise RuntimeError(f"{name} failed with status {st}: {msg}")
+        sizes = [a for a in args if isinstance(a, (int, float)) and not isinstance(a, bool)]
+        raise RuntimeError(f"{name} failed with status {st}: {msg} (numeric arguments {sizes})")

@@ -82,7 +82,7 @@ class OursHIP(Method):
 
     def __init__(self, a, B, Lmax, dev, n_layers: int = NL, static: dict | None = None,
                  ctx_len: int = CTX_LEN, rule: str = "multibin", fused: bool = True,
-                 groups: int = 1):
+                 groups: int = 1, c_max: int = 256):
         super().__init__(a, B, Lmax, dev)
         if groups < 1 or B % groups:
             raise ValueError(f"groups={groups} must divide B={B}")
@@ -91,7 +91,7 @@ class OursHIP(Method):
         # another group's bandwidth-bound scan
         self.groups = groups
         self.streams = [torch.cuda.Stream(device=dev) for _ in range(groups)] if groups > 1 else []
-        self.bud = budget(a.rho, ctx_len=ctx_len, rule=rule)
+        self.bud = budget(a.rho, ctx_len=ctx_len, rule=rule, c_max=c_max)
         self.Cn, self.E = self.bud.C, self.bud.E
         self.n_layers = n_layers
         self.fused = fused

@@ -578,3 +578,40 @@ def test_build_row_on_device_matches_restated_stages():
     assert np.array_equal(s["mem"][:HQ, :T], mem)
     assert np.array_equal(s["cstart"][:HQ], cstart) and np.array_equal(s["clen"][:HQ], clen)
     assert np.array_equal(s["asg8"][:HQ, :T], asg.astype(np.uint8))
+
+
+def test_decode_long_context_needles_match_oracle():
+    """Config-4 shape at B=1, N=65536, 1% (C=128, the 7-bit top-q histogram and two register
+    segments per row), 512-centre mixture with 8 planted needles per KV head: one decode step
+    equals the CPU restatement (selection bit-exact, output within the bf16 bar) and both read
+    the same needles."""
+    print("[case] decode N=65536 needles", flush=True)
+    N = 65536
+    b = budget(0.01, ctx_len=N)
+    lay = build_layer(cfg=4, B=1, N=N, Lmax=N + 64, C=b.C, n_centers=512, dev=DEV, needles=8)
+    m = OursHIP(types.SimpleNamespace(rho=0.01), 1, lay.Lmax, DEV, n_layers=1, static=lay.static, ctx_len=N)
+    m.st[0] = lay.st.clone()
+    st_np = state_np(lay)
+    CTX.K, CTX.V = [lay.K], [lay.V]
+    CTX.n_dev = torch.tensor([N], device=DEV, dtype=torch.int32)
+    CTX.n0_dev = torch.tensor([lay.T], device=DEV, dtype=torch.int32)
+    out = m.decode(0, lay.q, N)
+    torch.cuda.synchronize()
+    ns, nl, k = m.bud.counts(N)
+    ref = O.decode_step(st_np, bf16_np(lay.q.reshape(-1, D)), N, ns, nl, k, m.E, G, np.float32(SC),
+                        np.float32(SC2), rmax=RMAX)
+    sel, ex = m.last_sel.cpu().numpy(), m.exp_idx.cpu().numpy()[:, :m.E]
+    assert np.array_equal(sel, ref["sel"]) and np.array_equal(ex, ref["exp_idx"])
+    assert np.array_equal(m.quota.cpu().numpy(), ref["quota"])
+    rel = rel_rows(bf16_to_f32(bf16_np(out.reshape(-1, D))), ref["out"])
+    assert rel.max() < BF16_TOL
+    hit = tot = 0
+    for r in range(HQ):
+        h, gq = divmod(r, G)
+        read = set(sel[r].tolist()) | set(ex[r][ex[r] >= 0].tolist())
+        for j in range(8):
+            if j % G == gq:
+                tot += 1
+                hit += int(lay.npos[0, h, j]) in read
+    print(f"  needle recall {hit}/{tot}")
+    assert tot == 64
