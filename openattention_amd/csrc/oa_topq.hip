@@ -16,27 +16,29 @@
 // cluster ids asg8, coalesced) into registers -- 1024 * PPT positions at a time, PPT per
 // thread -- and every selection step works on those registers and on LDS.  Scores are
 // compared through their order-preserving 32-bit key; its top 2*LB bits (LB = 8, 7 or 6 for
-// C <= 64, 128, 256) form the "prefix" of a member:
+// C <= 64, 128, 256) are the level-1 histogram bin of a member:
 //   L1  per-cluster histogram of the top LB key bits (LDS atomics).  Histogram rows carry one
 //       pad word after every NB/16 bins, so the 16 threads that scan a row read 16 banks;
-//   T1  16 threads per cluster: t = min(q_c, members, E - base_c) and the level-1 bin b1 holding
-//       the t-th best member.  Members of bins above b1 are chosen; when bin b1 must be split
-//       the cluster goes to level 2;
-//   L2  for clusters being split: histogram of the next LB key bits of bin b1's members.  The
-//       same pass gathers every member at or above its cluster's level-1 bound (b1 and above:
-//       a few thousand of the row's members) into an LDS list -- per-thread hit masks, one
-//       scan per wave and one LDS atomic per wave, no per-member atomics;
-//   T2  the prefix P_c holding the t-th best member, `above` = members with a larger prefix,
-//       `need` = t - above of the members with prefix P_c;
-//   F   one pass over the gathered list: members above P_c are chosen (written straight into
-//       their cluster's segment of the chosen-word list), members at P_c are staged as unique
-//       64-bit keys (score key << 32 | ~position) when some of them must be dropped.  When the
-//       level-1 set does not fit in LDS the gathering runs as its own pass after T2, with the
-//       final bounds;
+//   T1  16 threads per cluster: t = min(q_c, members, E - base_c) and the level-1 bin holding
+//       the t-th best member; every cluster now has a boundary bin [klo, khi] of keys.  Members
+//       above it are chosen; a cluster whose whole bin completes t is done, the others are split;
+//   G   every member at or above its cluster's boundary bin (a few thousand of the row's
+//       members) is gathered into an LDS list: per-thread hit masks, one scan per wave and one
+//       LDS atomic per wave, no per-member atomics;
+//   refinement levels, while any cluster is split: the histogram of the next LB key bits of
+//       each split cluster's boundary-bin members (built from the list, about 5 entries per
+//       thread), then the bin holding its t-th member.  A cluster whose new bin fits in the LDS
+//       staging space is staged; one that does not stays split for the next level; at full key
+//       depth (only equal keys left) it is resolved block-wide in P5.  When the level-1 set
+//       does not fit the list, the levels run over the registers instead and G follows them,
+//       with the final bins;
+//   F   one pass over the list: members above the boundary bin are chosen (written straight into
+//       their cluster's segment of the chosen-word list), members inside a staged cluster's bin
+//       become unique 64-bit keys (score key << 32 | ~position);
 //   P5  one wave per staged cluster picks the `need` best staged keys (repeated wave maxima for
-//       small `need`, an MSB-first bitwise search on ballot counts otherwise); a cluster whose
-//       prefix bin does not fit in LDS is resolved by the same bitwise search run block-wide
-//       over the row, streamed again;
+//       small `need`, an MSB-first bitwise search on ballot counts otherwise, over the key bits
+//       the bin leaves open); equal keys beyond the staging space are ranked by position in a
+//       block-wide bitwise search that streams the row again;
 //   P6  every chosen (cluster << 24 | position) word gets its rank among its cluster's words by
 //       position (counting, or a bitonic sort when more than 1024 were chosen), lands in an
 //       LDS copy of the exp_idx row, and the row is written out once (-1 where a segment is
@@ -63,7 +65,7 @@ constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
 constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster with no quota
 constexpr int kLdsLimit = 160 * 1024;
 
-enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3 };
+enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3, kModeSplit = 4 };
 
 struct TopqArgs {
   const float* S; long s_stride;
@@ -81,11 +83,16 @@ __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
   return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (unsigned)pos);
 }
 
-// Staged keys of one cluster share their top 2*LB bits (the prefix P) and, since positions are
-// below 2^24, bits 24..31 of the inverted position: a bitwise threshold search starts from those
-// bits (key64_floor) and decides only the others, from bit 63 - 2*LB down, skipping 31..24.
-__device__ __forceinline__ unsigned long long key64_floor(int P, int lb2) {
-  return ((unsigned long long)(unsigned)P << (64 - lb2)) | 0xff000000ull;
+// The staged keys of one cluster lie in its boundary bin [klo, khi] of score keys (khi = klo |
+// (2^w - 1)): they share klo's top 32 - w bits and, since positions are below 2^24, bits 24..31
+// of the inverted position.  A bitwise threshold search starts from those bits (bin_floor) and
+// decides only the others, from bit 31 + w down, skipping 31..24.
+__device__ __forceinline__ unsigned long long bin_floor(uint32_t klo) {
+  return ((unsigned long long)klo << 32) | 0xff000000ull;
+}
+__device__ __forceinline__ int bin_top_bit(uint32_t klo, uint32_t khi) {
+  const int w = __popc(klo ^ khi);
+  return w > 0 ? 31 + w : 23;
 }
 __device__ __forceinline__ int next_free_bit(int bit) { return bit == 32 ? 23 : bit - 1; }
 
@@ -103,8 +110,8 @@ __device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t
 
 // P5 on one staged cluster: the `need` largest of cnt unique keys, held KR per lane
 template <int KR>
-__device__ void select_staged(const unsigned long long* src, int cnt, int need, int c, int P,
-                              int lb2, uint32_t* cst, int* ctr, int lane) {
+__device__ void select_staged(const unsigned long long* src, int cnt, int need, int c,
+                              unsigned long long floor, int top, uint32_t* cst, int* ctr, int lane) {
   unsigned long long x[KR];
 #pragma unroll
   for (int j = 0; j < KR; ++j) x[j] = src[min(j * 64 + lane, cnt - 1)];
@@ -125,8 +132,8 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
       T = best;
     }
   } else {
-    T = key64_floor(P, lb2);
-    for (int bit = 63 - lb2; bit >= 0; bit = next_free_bit(bit)) {
+    T = floor;
+    for (int bit = top; bit >= 0; bit = next_free_bit(bit)) {
       const unsigned long long cnd = T | (1ull << bit);
       int k = 0;
 #pragma unroll
@@ -143,10 +150,11 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
 }
 
 // the same from LDS in a loop, for more than 1024 staged keys
-__device__ void select_staged_loop(const unsigned long long* src, int cnt, int need, int c, int P,
-                                   int lb2, uint32_t* cst, int* ctr, int lane) {
-  unsigned long long T = key64_floor(P, lb2);
-  for (int bit = 63 - lb2; bit >= 0; bit = next_free_bit(bit)) {
+__device__ void select_staged_loop(const unsigned long long* src, int cnt, int need, int c,
+                                   unsigned long long floor, int top, uint32_t* cst, int* ctr,
+                                   int lane) {
+  unsigned long long T = floor;
+  for (int bit = top; bit >= 0; bit = next_free_bit(bit)) {
     const unsigned long long cnd = T | (1ull << bit);
     int k = 0;
     for (int b0 = 0; b0 < cnt; b0 += 64) {
@@ -211,9 +219,10 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   __shared__ int s_t[kMaxC];              // members chosen
   __shared__ int s_above[kMaxC];          // members with a prefix above the boundary prefix
   __shared__ int s_bcnt[kMaxC];           // members in the boundary prefix bin
-  __shared__ int s_b1[kMaxC];             // level-1 bin split at level 2, or -1
-  __shared__ int s_thr[kMaxC];            // final boundary prefix P_c (2*LB bits)
-  __shared__ unsigned s_lo[kMaxC];        // members whose prefix is >= s_lo[c] are gathered
+  __shared__ unsigned s_klo[kMaxC];       // boundary bin [klo, khi] of score keys of each cluster
+  __shared__ unsigned s_khi[kMaxC];
+  __shared__ unsigned s_pref[kMaxC];      // refinement: boundary-bin prefix of a split cluster, or ~0
+  __shared__ unsigned s_lo[kMaxC];        // members whose key is > s_lo[c] are gathered
   __shared__ int s_mode[kMaxC];
   __shared__ int s_goff[kMaxC], s_gcur[kMaxC];   // staged keys: segment start, fill count
   __shared__ int s_ccur[kMaxC];           // chosen words written per cluster
@@ -236,8 +245,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int C = a.C, E = a.E;
-  constexpr int sh1 = 32 - LB, sh2 = 32 - 2 * LB;
-  constexpr int sh1p = sh1 + sb, sh2p = sh2 + sb;   // shifts giving a bin's pad-word count
+  constexpr int sh1 = 32 - LB;
+  constexpr int sh1p = sh1 + sb;          // shift giving a level-1 bin's pad-word count
   const int trash = C * HS + lane;        // per-lane histogram slot for non-members
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
@@ -271,7 +280,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (lane == 63) s_base[kMaxC] = incl;
   }
   for (int c = tid; c < kMaxC; c += kThreads) {
-    s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_b1[c] = -1; s_thr[c] = 0; s_lo[c] = kNoGather;
+    s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_klo[c] = 0u; s_khi[c] = 0u; s_pref[c] = ~0u;
+    s_lo[c] = kNoGather;
     s_mode[c] = kModeNone; s_goff[c] = 0; s_gcur[c] = 0; s_ccur[c] = 0;
   }
   for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
@@ -347,43 +357,6 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     }
   };
 
-  // T2 on the level-2 histogram: prefix P_c of the t-th best member of each split cluster and
-  // the staging plan for its boundary bin
-  auto t2 = [&]() {
-    for (int cb = 0; cb < C; cb += kThreads / 16) {
-      const int c = cb + (tid >> 4);
-      const int j = tid & 15;
-      const int b1 = c < C ? s_b1[c] : -1;
-      if (b1 < 0) continue;      // uniform over the cluster's 16 threads
-      RowScan<bpt> r;
-      scan_row(s_hist + c * HS, j, r);
-      const int t2 = s_t[c] - s_above[c];        // rank of the t-th member inside bin b1
-      if (r.sfx >= t2 && r.sfx - r.ls < t2) {
-        int b, acc, cnt;
-        find_bin(r, t2, b, acc, cnt);
-        const int need = t2 - acc;
-        const int P = (b1 << LB) | (j * bpt + b);
-        s_above[c] = s_above[c] + acc;
-        s_bcnt[c] = cnt;
-        s_thr[c] = P;
-        int mode = kModeAll;
-        unsigned lo = (unsigned)P;
-        if (need < cnt) {
-          const int off = atomicAdd(&s_gused, cnt);
-          if (off + cnt <= a.gcap) {
-            mode = kModeStaged;
-            s_goff[c] = off;
-          } else {               // boundary bin too large for LDS: resolved block-wide in P5
-            mode = kModeBlock;
-            lo = (unsigned)P + 1u;
-            s_fbl[atomicAdd(&s_nfb, 1)] = c;
-          }
-        }
-        s_mode[c] = mode;
-        s_lo[c] = lo;
-      }
-    }
-  };
   auto clear_hist = [&]() {
     for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
   };
@@ -413,22 +386,24 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       const int t = min(w, m);
       if (t > 0 && t == m) {     // every member is chosen
         if (j == 0) {
-          s_t[c] = t; s_mode[c] = kModeAll; s_thr[c] = 0; s_lo[c] = 1u;
+          s_t[c] = t; s_mode[c] = kModeAll; s_klo[c] = 0u; s_khi[c] = ~0u;
+          s_lo[c] = kNegInfKey;              // gathering bound - 1: every member
           atomicAdd(&s_hits1, t);
         }
       } else if (t > 0 && r.sfx >= t && r.sfx - r.ls < t) {
         int b, acc, cnt;
         find_bin(r, t, b, acc, cnt);
-        const int b1 = j * bpt + b;
+        const unsigned b1 = (unsigned)(j * bpt + b);
         s_t[c] = t;
         s_above[c] = acc;
         s_bcnt[c] = cnt;
-        // members have a prefix >= 8, so a bound of 1 gathers all of them and no non-member
-        s_lo[c] = max((unsigned)b1 << LB, 1u);
+        s_klo[c] = b1 << sh1;
+        s_khi[c] = (b1 << sh1) | ((1u << sh1) - 1u);
+        s_lo[c] = max(b1 << sh1, kNegInfKey + 1u) - 1u;   // gathering bound - 1 (members only)
         if (t - acc == cnt) {    // the whole level-1 bin completes t: no split
-          s_mode[c] = kModeAll; s_thr[c] = b1 << LB;
+          s_mode[c] = kModeAll;
         } else {
-          s_b1[c] = b1;
+          s_mode[c] = kModeSplit;
           atomicAdd(&s_nsplit, 1);
         }
         atomicAdd(&s_hits1, acc + cnt);
@@ -436,38 +411,118 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     }
   }
   __syncthreads();
-  const bool split = s_nsplit > 0;
   const bool fits = s_hits1 <= a.ucap;   // block-uniform: the level-1 set fits in the list
+  int ucnt = 0;
 
-  if (split && !fits) {
-    // ---- L2 (registers): next LB key bits of the members of each split level-1 bin, over the
-    // whole row; the gathering then runs with the final bounds
+  // One more histogram level for every split cluster: the next LB key bits of its boundary
+  // bin's members (from the gathered list, or from the registers when the list does not hold
+  // the level-1 set), then the bin of the t-th member.  A cluster whose new boundary bin fits
+  // in the staging space is staged, one at full key depth that does not is resolved
+  // block-wide in P5, the others stay split for the next level.
+  int depth = 1;
+  auto refine = [&](bool from_list) {
+    ++depth;
+    const int shp = max(32 - LB * (depth - 1), 0);   // the split bins' prefix shift (> 0)
+    const int shd = max(32 - LB * depth, 0);         // this level's bin shift
+    for (int c = tid; c < kMaxC; c += kThreads)
+      s_pref[c] = c < C && s_mode[c] == kModeSplit ? s_klo[c] >> shp : ~0u;
     clear_hist();
     __syncthreads();
-    for (int sg = 0; sg < nseg; ++sg) {
-      if (nseg > 1) load(sg);
+    // every thread has read s_nsplit for its loop test before the barrier above; the count is
+    // rebuilt in the scan below, after the next barrier
+    if (tid == 0) s_nsplit = 0;
+    if (from_list) {
+      for (int j0 = 0; j0 < ucnt; j0 += kThreads * kUPT) {
+        int cc[kUPT];
+        uint32_t k[kUPT];
 #pragma unroll
-      for (int i0 = 0; i0 < PPT; i0 += CH) {
-        int b1v[CH];
+        for (int u = 0; u < kUPT; ++u) {
+          const int j = min(j0 + u * kThreads + tid, ucnt - 1);
+          cc[u] = (int)(s_uw[j] >> 24);
+          k[u] = s_uk[j];
+        }
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
-          if (i0 + j < PPT) b1v[j] = s_b1[cid(i0 + j)];
+        for (int u = 0; u < kUPT; ++u) {
+          const bool in = j0 + u * kThreads + tid < ucnt && (k[u] >> shp) == s_pref[cc[u]];
+          const uint32_t bn = (k[u] >> shd) & (NB - 1);
+          atomicAdd(&s_hist[in ? cc[u] * HS + (int)bn + (int)(bn >> sb) : trash], 1);
+        }
+      }
+    } else {
+      for (int sg = 0; sg < nseg; ++sg) {
+        if (nseg > 1) load(sg);
 #pragma unroll
-        for (int j = 0; j < CH; ++j) {
-          if (i0 + j < PPT) {
-            const int i = i0 + j;
-            const uint32_t k = kk[i];
-            const bool in = k && (int)(k >> sh1) == b1v[j];
-            int slot = (int)__umul24(cid(i), HS) + (int)((k >> sh2) & (NB - 1)) +
-                       (int)((k >> sh2p) & 15u);
-            asm volatile("" : "+v"(slot));
-            atomicAdd(&s_hist[in ? slot : trash], 1);
+        for (int i0 = 0; i0 < PPT; i0 += CH) {
+          unsigned pv[CH];
+#pragma unroll
+          for (int j = 0; j < CH; ++j)
+            if (i0 + j < PPT) pv[j] = s_pref[cid(i0 + j)];
+#pragma unroll
+          for (int j = 0; j < CH; ++j) {
+            if (i0 + j < PPT) {
+              const int i = i0 + j;
+              const uint32_t k = kk[i];
+              const bool in = k && (k >> shp) == pv[j];
+              const uint32_t bn = (k >> shd) & (NB - 1);
+              int slot = (int)__umul24(cid(i), HS) + (int)bn + (int)(bn >> sb);
+              asm volatile("" : "+v"(slot));
+              atomicAdd(&s_hist[in ? slot : trash], 1);
+            }
           }
         }
       }
     }
     __syncthreads();
-    t2();
+    for (int cb = 0; cb < C; cb += kThreads / 16) {
+      const int c = cb + (tid >> 4);
+      const int j = tid & 15;
+      if (c >= C || s_pref[c] == ~0u) continue;     // uniform over the cluster's 16 threads
+      RowScan<bpt> r;
+      scan_row(s_hist + c * HS, j, r);
+      const int t2 = s_t[c] - s_above[c];           // rank of the t-th member inside the bin
+      if (r.sfx >= t2 && r.sfx - r.ls < t2) {
+        int b, acc, cnt;
+        find_bin(r, t2, b, acc, cnt);
+        // at the last level the bin index may repeat bits of the prefix: OR leaves them as is
+        const unsigned klo = s_klo[c] | ((unsigned)(j * bpt + b) << shd);
+        const int need = t2 - acc;
+        s_klo[c] = klo;
+        s_khi[c] = klo | ((1u << shd) - 1u);
+        s_above[c] = s_above[c] + acc;
+        s_bcnt[c] = cnt;
+        int mode = kModeAll;
+        if (need < cnt) {
+          const int off = atomicAdd(&s_gused, cnt);
+          if (off + cnt <= a.gcap) {
+            mode = kModeStaged;
+            s_goff[c] = off;
+          } else {
+            atomicSub(&s_gused, cnt);
+            if (shd == 0) {      // equal keys beyond the staging space: block-wide search in P5
+              mode = kModeBlock;
+              s_fbl[atomicAdd(&s_nfb, 1)] = c;
+            } else {
+              mode = kModeSplit;
+              atomicAdd(&s_nsplit, 1);
+            }
+          }
+        }
+        s_mode[c] = mode;
+      }
+    }
+    __syncthreads();
+  };
+
+  if (!fits) {
+    while (s_nsplit > 0) refine(false);       // block-uniform loop: s_nsplit read after a barrier
+    // final gathering bounds, stored as bound - 1 for a strict test (no key exceeds ~0, so a
+    // cluster without quota gathers nothing): the boundary bin and above (members only: keys
+    // > kNegInfKey), only the members above the bin for a block-wide cluster
+    for (int c = tid; c < kMaxC; c += kThreads) {
+      const int mode = c < C ? s_mode[c] : kModeNone;
+      s_lo[c] = mode == kModeNone ? kNoGather
+                : (mode == kModeBlock ? s_khi[c] : max(s_klo[c], kNegInfKey + 1u) - 1u);
+    }
     __syncthreads();
   }
 
@@ -487,8 +542,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (lane == 63) s_tpre[kMaxC] = incl;
   }
 
-  // ---- G: gather every member whose prefix reaches its cluster's bound (the level-1 bound, or
-  // the final one when the level-2 histogram came from the registers)
+  // ---- G: gather every member whose key reaches its cluster's bound
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
     unsigned long long hb = 0ull;
@@ -500,42 +554,21 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         if (i0 + j < PPT) lov[j] = s_lo[cid(i0 + j)];
 #pragma unroll
       for (int j = 0; j < CH; ++j)
-        if (i0 + j < PPT && (kk[i0 + j] >> sh2) >= lov[j]) hb |= 1ull << (i0 + j);
+        if (i0 + j < PPT && kk[i0 + j] > lov[j]) hb |= 1ull << (i0 + j);
     }
     gather(sg, hb);
   }
   __syncthreads();
-  const int ucnt = min(s_ucnt, a.ucap);
+  ucnt = min(s_ucnt, a.ucap);
 
-  if (split && fits) {
-    // ---- L2 (list): the gathered set holds every member of each split bin
-    clear_hist();
-    __syncthreads();
-    for (int j0 = 0; j0 < ucnt; j0 += kThreads * kUPT) {
-      int c[kUPT];
-      uint32_t k[kUPT];
-#pragma unroll
-      for (int u = 0; u < kUPT; ++u) {
-        const int j = min(j0 + u * kThreads + tid, ucnt - 1);
-        c[u] = (int)(s_uw[j] >> 24);
-        k[u] = s_uk[j];
-      }
-#pragma unroll
-      for (int u = 0; u < kUPT; ++u) {
-        const bool in = j0 + u * kThreads + tid < ucnt && (int)(k[u] >> sh1) == s_b1[c[u]];
-        const uint32_t b2 = (k[u] >> sh2) & (NB - 1);
-        atomicAdd(&s_hist[in ? c[u] * HS + (int)b2 + (int)(b2 >> sb) : trash], 1);
-      }
-    }
-    __syncthreads();
-    t2();
-    __syncthreads();
-  }
+  if (fits)
+    while (s_nsplit > 0) refine(true);
 
-  // ---- F: gathered members above P_c are chosen, members at P_c of a staged cluster staged
+  // ---- F: gathered members above the boundary bin are chosen (all of a whole-bin cluster's
+  // from klo up), members inside a staged cluster's bin are staged
   for (int j0 = 0; j0 < ucnt; j0 += kThreads * kUPT) {
-    uint32_t e[kUPT], key[kUPT];
-    int P[kUPT], mode[kUPT];
+    uint32_t e[kUPT], key[kUPT], lo[kUPT], hi[kUPT];
+    int mode[kUPT];
 #pragma unroll
     for (int u = 0; u < kUPT; ++u) {
       const int j = min(j0 + u * kThreads + tid, ucnt - 1);
@@ -545,43 +578,44 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 #pragma unroll
     for (int u = 0; u < kUPT; ++u) {
       const int c = (int)(e[u] >> 24);
-      P[u] = s_thr[c];
+      lo[u] = s_klo[c];
+      hi[u] = s_khi[c];
       mode[u] = j0 + u * kThreads + tid < ucnt ? s_mode[c] : kModeNone;
     }
 #pragma unroll
     for (int u = 0; u < kUPT; ++u) {
       const int c = (int)(e[u] >> 24);
-      const int pf = (int)(key[u] >> sh2);
-      if (mode[u] != kModeNone && (pf > P[u] || (pf == P[u] && mode[u] == kModeAll)))
+      if (mode[u] != kModeNone && (key[u] > hi[u] || (mode[u] == kModeAll && key[u] >= lo[u])))
         s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = e[u];
-      else if (pf == P[u] && mode[u] == kModeStaged)
+      else if (mode[u] == kModeStaged && key[u] >= lo[u] && key[u] <= hi[u])
         s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(key[u], (int)(e[u] & 0xffffffu));
     }
   }
   __syncthreads();
 
-  // ---- P5: resolve prefix P_c of the staged clusters, one wave per cluster
+  // ---- P5: the `need` best of each staged cluster's boundary bin, one wave per cluster
   for (int c = wave; c < C; c += kWaves) {
     if (s_mode[c] != kModeStaged) continue;
     const int cnt = s_bcnt[c];
     const int need = s_t[c] - s_above[c];
     const unsigned long long* src = s_g + s_goff[c];
     uint32_t* dst = s_cst + s_tpre[c];
-    const int P = s_thr[c];
-    if (cnt <= 64) select_staged<1>(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
-    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
-    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
-    else select_staged_loop(src, cnt, need, c, P, 2 * LB, dst, &s_ccur[c], lane);
+    const unsigned long long fl = bin_floor(s_klo[c]);
+    const int top = bin_top_bit(s_klo[c], s_khi[c]);
+    if (cnt <= 64) select_staged<1>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+    else select_staged_loop(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
   }
-  // clusters whose prefix bin did not fit in LDS: block-wide bitwise search, re-streaming the
-  // row (rare; keeps the row's registers dead during P5)
-  const int nfb = s_nfb;         // final since the T2 barrier
+  // clusters whose boundary bin holds more equal keys than the staging space: block-wide
+  // bitwise search over the positions, re-streaming the row (rare)
+  const int nfb = s_nfb;         // final since the last refinement barrier
   for (int f = 0; f < nfb; ++f) {
     const int c = s_fbl[f];
-    const int P = s_thr[c];
+    const uint32_t K0 = s_klo[c];   // the boundary key (khi == klo at full depth)
     const int need = s_t[c] - s_above[c];
-    unsigned long long T = key64_floor(P, 2 * LB);
-    for (int bit = 63 - 2 * LB, it = 0; bit >= 0; bit = next_free_bit(bit), ++it) {
+    unsigned long long T = bin_floor(K0);
+    for (int bit = 23, it = 0; bit >= 0; --bit, ++it) {
       const unsigned long long cnd = T | (1ull << bit);
       int k = 0;
       for (int sg = 0; sg < nseg; ++sg) {
@@ -589,8 +623,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
           const int p = pos_of(sg, i);
-          const bool in = kk[i] && cid(i) == c && (int)(kk[i] >> sh2) == P &&
-                          key64(kk[i], p) >= cnd;
+          const bool in = kk[i] == K0 && cid(i) == c && key64(kk[i], p) >= cnd;
           k += __popcll(__ballot(in));
         }
       }
@@ -605,8 +638,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
         const int p = pos_of(sg, i);
-        const bool take = kk[i] && cid(i) == c && (int)(kk[i] >> sh2) == P &&
-                          key64(kk[i], p) >= T;
+        const bool take = kk[i] == K0 && cid(i) == c && key64(kk[i], p) >= T;
         append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst + s_tpre[c], &s_ccur[c], lane);
       }
     }

@@ -323,17 +323,23 @@ def test_topq_adversarial_quotas(n, C, E, seed):
     assert np.array_equal(got, ref), f"rows differ: {np.nonzero((got != ref).any(1))[0]}"
 
 
-@pytest.mark.parametrize("n,C,E,seed", [(30000, 2, 300, 4), (60000, 4, 512, 5)])
-def test_topq_level1_set_exceeds_list(n, C, E, seed):
-    """Top-q when a row's level-1 boundary bins hold more members than the LDS gathering list:
-    every score sits in [1, 2) on a grid of eight values, so each cluster's level-1 bin holds all
-    of its members and each level-2 bin thousands (the register level-2 pass, the gathering with
-    final bounds, and the block-wide search for boundary bins too large to stage).  n = 60000 is
-    past one register segment (streamed twice per pass)."""
-    print(f"[case] topq level-1 overflow n={n} C={C} E={E}", flush=True)
+@pytest.mark.parametrize("n,C,E,seed,grid", [(30000, 2, 300, 4, "coarse"), (60000, 4, 512, 5, "coarse"),
+                                                (30000, 2, 300, 8, "fine"), (12000, 2, 300, 9, "fine"),
+                                                (60000, 256, 3000, 10, "fine")])
+def test_topq_deep_histogram_levels(n, C, E, seed, grid):
+    """Top-q when boundary bins stay too large for the LDS staging space after two histogram
+    levels.  "coarse": every score sits in [1, 2) on a grid of eight values, so each level-2 bin
+    holds thousands of equal keys: four levels, then the block-wide search over positions.
+    "fine": scores 1 + u 2^-20 (u < 2^16), so a third level separates them.  n = 30000 / 60000
+    put the level-1 set beyond the gathering list (register passes; 60000 is two register
+    segments), n = 12000 keeps it in the list (list passes); C = 256 runs the 6-bit levels."""
+    print(f"[case] topq deep levels n={n} C={C} E={E} grid={grid}", flush=True)
     rng = np.random.default_rng(seed)
     R, Lmax = 3, -(-(n + 300) // 64) * 64
-    S = (1.0 + rng.integers(0, 8, size=(R, Lmax)) / 8.0).astype(np.float32)
+    if grid == "coarse":
+        S = (1.0 + rng.integers(0, 8, size=(R, Lmax)) / 8.0).astype(np.float32)
+    else:
+        S = (1.0 + rng.integers(0, 1 << 16, size=(R, Lmax)) / float(1 << 20)).astype(np.float32)
     asg = rng.integers(0, C, size=(R, Lmax)).astype(np.int32)
     asg[:, n:] = 0
     sel = np.stack([rng.choice(n, 16, replace=False) for _ in range(R)]).astype(np.int32)
@@ -342,7 +348,7 @@ def test_topq_level1_set_exceeds_list(n, C, E, seed):
     quota = np.zeros((R, C), np.float32)
     quota[0] = E // C                  # every cluster split inside its level-1 bin
     quota[1, 0] = 7                    # one small quota
-    quota[2] = rng.integers(1, E // C, size=C)
+    quota[2] = rng.integers(1, max(E // C, 2), size=C)
     ref = O.topq(S, asg, sel, quota, n, E)
     exp_idx = torch.full((R, E), 12345, device=DEV, dtype=torch.int32)
     n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
