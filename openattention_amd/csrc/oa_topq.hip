@@ -15,8 +15,8 @@
 // quota and their members cover most of the row, so the row is streamed (scores S and byte
 // cluster ids asg8, coalesced) into registers -- 1024 * PPT positions at a time, PPT per
 // thread -- and every selection step works on those registers and on LDS.  Scores are
-// compared through their order-preserving 32-bit key; its top 2*LB bits (LB = 8, 7 or 6 for
-// C <= 64, 128, 256) are the level-1 histogram bin of a member:
+// compared through their order-preserving 32-bit key, whose bits are taken LB at a time (LB =
+// 8, 7 or 6 for C <= 64, 128, 256) by successive histogram levels:
 //   L1  per-cluster histogram of the top LB key bits (LDS atomics).  Histogram rows carry one
 //       pad word after every NB/16 bins, so the 16 threads that scan a row read 16 banks;
 //   T1  16 threads per cluster: t = min(q_c, members, E - base_c) and the level-1 bin holding
