@@ -52,6 +52,9 @@ def parse():
                    help="split the batch into this many sequence groups on their own streams")
     p.add_argument("--pmc-calibration", action="store_true",
                    help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
+    p.add_argument("--config5", action="store_true",
+                   help="whole decode step of a Llama-3.1-8B-shaped random-init model (32 layers) under one "
+                        "hipGraph, sparse vs dense attention, B in {1, 32}, N = 32768; one JSON line per B")
     p.add_argument("--config4", action="store_true",
                    help="long-context sweep instead: B=8, N in {65536, 131072}, 1%% and 3%%, 512-centre "
                         "mixture with 8 needles per KV head; one JSON line per point (us/layer-step, "
@@ -226,6 +229,99 @@ def config4_sweep(a):
             torch.cuda.empty_cache()
 
 
+def config5_run(a):
+    """a Llama-3.1-8B-shaped model (random-init bf16 weights, 32 layers) whose
+    KV cache holds a 32K-token prefix (the config-3 synthetic key/value mixture stands in for the
+    prompt's prefill), the index built for every layer and sequence (timed), then the whole
+    decode step -- embedding, 32 x (RMSNorm, QKV, RoPE, KV append, attention, O, RMSNorm,
+    SwiGLU), final norm, LM head, greedy token -- captured in one hipGraph and replayed, with the
+    sparse stage and with dense decode attention on the same cache."""
+    import torch
+
+    from openattention_amd import _build, lib, synth
+    if not os.path.exists(_build.lib_path()):
+        _build.build()
+    lib.load()
+    from openattention_amd.method import C as CTX, OursHIP
+    from openattention_amd.model import NLAYER, LlamaShaped
+    from openattention_amd.prefill import build_row
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    N = a.ctx
+    static = synth.static_metric(NLAYER)
+    for B in (1, 32):
+        n_total = 2 * (a.warmup + a.steps) + 4
+        Lmax = N + n_total
+        T0 = N - 1
+        t0 = time.time()
+        m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=NLAYER, static=static,
+                    groups=2 if B % 2 == 0 else 1)
+        CTX.K, CTX.V = [], []
+        build_ms = 0.0
+        for l in range(NLAYER):
+            K, V, _q, qq, _ = synth.make_layer(3, B, N, Lmax, 256, dev, layer=l)
+            CTX.K.append(K)
+            CTX.V.append(V)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for b in range(B):
+                build_row(m.st[l], b, K[b], V[b], qq[b], T0, static["M"][l], static["inv_freq"], 1.0, l, G)
+            e1.record()
+            torch.cuda.synchronize()
+            build_ms += e0.elapsed_time(e1)
+            del qq
+            if l % 8 == 7:
+                log(f"[config5] B={B}: {l + 1} layers of cache + index ({time.time() - t0:.1f}s)")
+        log(f"[config5] B={B}: cache + index of {NLAYER} layers ({time.time() - t0:.1f}s, build "
+            f"{build_ms:.0f} ms)")
+        model = LlamaShaped(B, Lmax, dev, method=m)
+        CTX.n0_dev = torch.tensor([T0], device=dev, dtype=torch.int32)
+        CTX.n_dev = torch.tensor([N], device=dev, dtype=torch.int32)
+        n = N
+        res = {}
+        for name, method in (("sparse", m), ("dense", None)):
+            model.method = method
+            for _ in range(a.warmup):
+                model.step(n)
+                CTX.n_dev.add_(1)
+                n += 1
+            torch.cuda.synchronize()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                model.step(n)
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                model.step(n)
+                CTX.n_dev.add_(1)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(a.steps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            n += a.steps
+            res[name] = e0.elapsed_time(e1) / a.steps
+            del graph
+        rec = {"config": "config5", "model": "Llama-3.1-8B-shaped, random-init bf16 weights",
+               "params": model.params(), "layers": NLAYER, "B": B, "N": N, "rho": a.rho, "C": m.Cn, "E": m.E,
+               "ms_per_step_sparse": round(res["sparse"], 3), "ms_per_step_dense": round(res["dense"], 3),
+               "speedup_vs_dense": round(res["dense"] / res["sparse"], 2),
+               "tokens_per_s_sparse": round(B / (res["sparse"] * 1e-3), 1),
+               "tokens_per_s_dense": round(B / (res["dense"] * 1e-3), 1),
+               "index_build_ms": round(build_ms, 1),
+               "data": "synthetic 32K prefix (config-3 mixture keys, N(0,1) values) in the KV cache; decode "
+                       "steps run through the full model"}
+        print(json.dumps(rec), flush=True)
+        del model, m
+        CTX.K, CTX.V = [], []
+        torch.cuda.empty_cache()
+
+
 def pmc_calibration():
     """A plain device copy of known size (1 GiB read, 1 GiB written) for scaling the
     FETCH_SIZE / WRITE_SIZE counters: run under rocprofv3 --pmc."""
@@ -247,6 +343,9 @@ def main():
         sys.exit(2)
     if a.config4:
         config4_sweep(a)
+        return
+    if a.config5:
+        config5_run(a)
         return
     if a.pmc_calibration:
         pmc_calibration()

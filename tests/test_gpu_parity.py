@@ -621,3 +621,57 @@ def test_decode_long_context_needles_match_oracle():
                 hit += int(lay.npos[0, h, j]) in read
     print(f"  needle recall {hit}/{tot}")
     assert tot == 64
+
+
+def test_model_step_graph_replay_matches_eager():
+    """A 2-layer Llama-shaped model on the sparse stage: three captured-step replays give the
+    same tokens and leave the same KV cache and index state as three eager steps (KV append at
+    the device-side n - 1, n advancing on the device)."""
+    print("[case] model step graph replay", flush=True)
+    from openattention_amd.model import LlamaShaped
+    B_, N, L = 2, 4096, 2
+    Lmax = N + 16
+    b = budget(0.01, ctx_len=N)
+    lays = [build_layer(cfg=1, B=B_, N=N, Lmax=Lmax, C=b.C, n_centers=64, dev=DEV, layer=l) for l in range(L)]
+    static = lays[0].static
+
+    def fresh():
+        m = OursHIP(types.SimpleNamespace(rho=0.01), B_, Lmax, DEV, n_layers=L, static=static, ctx_len=N)
+        m.st = [lays[l].st.clone() for l in range(L)]
+        CTX.K = [lays[l].K.clone() for l in range(L)]
+        CTX.V = [lays[l].V.clone() for l in range(L)]
+        CTX.n0_dev = torch.tensor([N - 1], device=DEV, dtype=torch.int32)
+        CTX.n_dev = torch.tensor([N], device=DEV, dtype=torch.int32)
+        return m
+
+    model = LlamaShaped(B_, Lmax, DEV, layers=L, method=None)
+    model.method = fresh()
+    model.tok.fill_(7)
+    eager = []
+    for i in range(3):
+        eager.append(model.step(N + i).clone())
+        CTX.n_dev.add_(1)
+    torch.cuda.synchronize()
+    e_state = [(CTX.K[l].clone(), model.method.st[l].Sk.clone(), model.method.st[l].asg.clone()) for l in range(L)]
+    model.method = fresh()
+    model.tok.fill_(7)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        model.step(N)
+        CTX.n_dev.add_(1)
+    torch.cuda.synchronize()
+    # capture ran nothing: the state is still the fresh one
+    got = []
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        got.append(model.tok.clone())
+    for a_, b_ in zip(eager, got):
+        assert torch.equal(a_, b_)
+    for l in range(L):
+        assert torch.equal(CTX.K[l], e_state[l][0])
+        assert torch.equal(model.method.st[l].Sk, e_state[l][1])
+        assert torch.equal(model.method.st[l].asg, e_state[l][2])
+    assert int(CTX.n_dev) == N + 3
