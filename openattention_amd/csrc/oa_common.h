@@ -180,6 +180,14 @@ __device__ __forceinline__ float dot128_canon(float a_lo, float b_lo, float a_hi
   return wave_sum(p);
 }
 
+// workgroup barrier that orders LDS only: waits for this wave's LDS operations, not for its
+// global loads still in flight (__syncthreads() also drains those)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // order-preserving uint32 image of a float (larger float -> larger key, -inf lowest)
 __device__ __forceinline__ uint32_t float_key(float s) {
   const uint32_t b = __float_as_uint(s);

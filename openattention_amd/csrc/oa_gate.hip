@@ -282,35 +282,92 @@ __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, dou
   }
 }
 
-// water-filling of one row by one wave (lane = threadIdx.x % 64); score/n_t rows may be in LDS
+// water-filling of one row by one wave (lane = threadIdx.x % 64); score/n_t rows may be in LDS.
+//
+// The 64 bisection steps run as rounds of DEPTH steps.  A round evaluates, in parallel, every
+// midpoint the next DEPTH sequential steps could visit: the probe tree in heap order (node 1 =
+// mid of (lo, hi); node 2n takes the left half (f > E: hi = mid), node 2n+1 the right half),
+// P = 2 NS lanes per node, node n in lanes [nP, nP + P).  Each node's interval is rebuilt from
+// (lo, hi) by the same 0.5 * (lo + hi) operations the sequential steps perform, so its midpoint
+// is the one the sequential bisection would probe if it reached that node.  f at a node is the
+// canonical sum: the lane partial of canonical lane l is its clusters l, l + 64, ... added in
+// slot order, the 64 lane partials are added by the balanced pairwise tree of the xor butterfly
+// (m = 1, 2, ..., 32; IEEE addition is commutative, so every lane of the butterfly holds that
+// tree's value).  Here each of a node's P lanes adds 64 / P consecutive lane partials by the
+// lower levels of that tree and the node's lanes add the P subtotals by its top levels.  The
+// walk down the tree then takes the sequential path from the ballot of f > E.
 template <int NS>
 __device__ __forceinline__ void waterfill_row(const float* score_row, const float* nt_row,
                                               float* quota_row, int C, double budget, int lane,
-                                              double* s_key) {
+                                              double* s_key, double2* s_cw) {
   // ---- live clusters, weights and the bracket of log(lambda)
   FillState<NS> f;
   fill_prologue<NS>(score_row, nt_row, C, lane, f);
-  // ---- 64 bisection steps, two per iteration: the step after mid probes 0.5*(lo+mid) or
-  // 0.5*(mid+hi), both evaluated beside mid, so the sequence of (lo, hi) is that of 64 single
-  // steps
-  double lo = f.lo, hi = f.hi;
-  for (int it = 0; it < 32; ++it) {
-    const double mid = 0.5 * (lo + hi);
-    const double m_lo = 0.5 * (lo + mid);
-    const double m_hi = 0.5 * (mid + hi);
-    // the three exponentials in lanes 0, 1, 2 of one det_exp pass (the value is uniform, so
-    // the other lanes would repeat it), then broadcast
-    const double e = oa::det_exp(lane == 0 ? mid : (lane == 1 ? m_lo : m_hi));
-    const double fm = fill_em<NS>(readlane_f64(e, 0), f.cap, f.w, C, lane);
-    const double f_lo = fill_em<NS>(readlane_f64(e, 1), f.cap, f.w, C, lane);
-    const double f_hi = fill_em<NS>(readlane_f64(e, 2), f.cap, f.w, C, lane);
-    if (fm > budget) {
-      hi = mid;
-      if (f_lo > budget) hi = m_lo; else lo = m_lo;
-    } else {
-      lo = mid;
-      if (f_hi > budget) hi = m_hi; else lo = m_hi;
+  constexpr int P = 2 * NS;                  // lanes per probe node
+  constexpr int NL = 64 / P;                 // canonical lane partials per lane (= nodes + 1)
+  constexpr int DEPTH = NS == 1 ? 5 : (NS == 2 ? 4 : 3);   // log2(NL): nodes 1 .. NL - 1
+  static_assert((1 << DEPTH) == NL, "probe tree shape");
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const int c = lane + 64 * j;
+    if (c < C) s_cw[c] = make_double2(f.cap[j], f.w[j]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  // this lane's share: canonical lane partials l = sub * NL + i, clusters l + 64 j (zero past C:
+  // min(0, em * 0) = +0 leaves a sum of non-negative terms unchanged)
+  const int sub = lane % P;
+  const int node = lane / P;
+  double cp[NL][NS], wp[NL][NS];
+#pragma unroll
+  for (int i = 0; i < NL; ++i)
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int c = sub * NL + i + 64 * j;
+      const double2 v = c < C ? s_cw[c] : make_double2(0.0, 0.0);
+      cp[i][j] = v.x;
+      wp[i][j] = v.y;
     }
+  const int lev = node > 0 ? 31 - __clz(node) : 0;   // depth of this lane's node (root 0)
+  // ---- 64 bisection steps, DEPTH per round
+  double lo = f.lo, hi = f.hi;
+  for (int done = 0; done < 64;) {
+    const int d = min(DEPTH, 64 - done);
+    double nlo = lo, nhi = hi;
+    double mid = 0.5 * (lo + hi);
+#pragma unroll
+    for (int b = DEPTH - 2; b >= 0; --b) {
+      if (b < lev) {
+        if ((node >> b) & 1) nlo = mid; else nhi = mid;
+        mid = 0.5 * (nlo + nhi);
+      }
+    }
+    const double em = oa::det_exp(mid);
+    double part[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      double p = fmin(cp[i][0], em * wp[i][0]);
+#pragma unroll
+      for (int j = 1; j < NS; ++j) p = p + fmin(cp[i][j], em * wp[i][j]);
+      part[i] = p;
+    }
+#pragma unroll
+    for (int st = 1; st < NL; st <<= 1)
+#pragma unroll
+      for (int i = 0; i < NL; i += 2 * st) part[i] = part[i] + part[i + st];
+    double fv = part[0];
+    fv = fv + oa::dpp_f64<0xB1>(fv);                   // node lanes xor 1
+    if (P >= 4) fv = fv + oa::dpp_f64<0x4E>(fv);       // xor 2
+    if (P >= 8) fv = fv + oa::dpp_f64<0x141>(fv);      // xor 4 (4-lane groups are uniform)
+    const unsigned long long gt = __ballot(fv > budget);
+    int nd = 1, lo_nd = 0, hi_nd = 0;
+    for (int k = 0; k < d; ++k) {
+      if ((gt >> (nd * P)) & 1ull) { hi_nd = nd; nd = 2 * nd; }
+      else { lo_nd = nd; nd = 2 * nd + 1; }
+    }
+    if (lo_nd) lo = readlane_f64(mid, lo_nd * P);
+    if (hi_nd) hi = readlane_f64(mid, hi_nd * P);
+    done += d;
   }
   f.lo = lo;
   f.hi = hi;
@@ -325,9 +382,10 @@ __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__
                                                        float* __restrict__ quota, long q_stride, int C,
                                                        double budget) {
   __shared__ double s_key[kMaxC];
+  __shared__ double2 s_cw[kMaxC];
   const int row = blockIdx.x;
   waterfill_row<NS>(score + (long)row * in_stride, n_t + (long)row * in_stride,
-                    quota + (long)row * q_stride, C, budget, threadIdx.x, s_key);
+                    quota + (long)row * q_stride, C, budget, threadIdx.x, s_key, s_cw);
 }
 
 int launch_fill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,

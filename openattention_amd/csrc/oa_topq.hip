@@ -253,44 +253,6 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
   int32_t* erow = a.exp_idx + (long)row * E;
 
-  // ---- P0: quota prefix, per-cluster state, histogram clear
-  if (wave == 0) {
-    int v[4], loc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (int)a.quota[(long)row * C + min(lane * 4 + i, C - 1)];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = lane * 4 + i < C ? v[i] : 0;
-      loc += v[i];
-    }
-    int incl = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += t;
-    }
-    int run = incl - loc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = lane * 4 + i;     // 0..255
-      s_base[c] = run;
-      s_w[c] = c < C ? max(0, min(v[i], E - run)) : 0;
-      run += v[i];
-    }
-    if (lane == 63) s_base[kMaxC] = incl;
-  }
-  for (int c = tid; c < kMaxC; c += kThreads) {
-    s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_klo[c] = 0u; s_khi[c] = 0u; s_pref[c] = ~0u;
-    s_lo[c] = kNoGather;
-    s_mode[c] = kModeNone; s_goff[c] = 0; s_gcur[c] = 0; s_ccur[c] = 0;
-  }
-  for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
-  if (tid == 0) {
-    s_gused = 0; s_nfb = 0; s_nsplit = 0; s_hits1 = 0; s_ucnt = 0;
-    s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0;
-  }
-  __syncthreads();
-
   // register i of a thread holds position sg*SEG + (i/4)*4096 + 4*tid + i%4: each group of four
   // consecutive positions arrives as one float4 of scores and one u32 of cluster ids
   constexpr int SEG = kThreads * PPT;
@@ -303,8 +265,9 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   auto pos_of = [&](int sg, int i) -> int { return sg * SEG + (i >> 2) * 4096 + 4 * tid + (i & 3); };
 
   // stream segment sg of the row into registers (clamped loads: all of them in flight); rows
-  // are read up to the multiple of 4 that follows n - 1
-  auto load = [&](int sg) {
+  // are read up to the multiple of 4 that follows n - 1.  issue() only starts the loads, keys()
+  // turns the arrived scores into keys (0 for a position that does not qualify)
+  auto issue = [&](int sg) {
     const int last4 = (n - 1) & ~3;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -316,6 +279,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       kk[4 * g + 2] = __float_as_uint(v.z);
       kk[4 * g + 3] = __float_as_uint(v.w);
     }
+  };
+  auto keys = [&](int sg) {
     const int lim = n - sg * SEG - 4 * tid;   // register i is in the row iff (i/4)*4096 + i%4 < lim
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
@@ -323,6 +288,10 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
       kk[i] = q ? key : 0u;
     }
+  };
+  auto load = [&](int sg) {
+    issue(sg);
+    keys(sg);
   };
   auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
 
@@ -361,9 +330,51 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
   };
 
+  // the first segment's loads are in flight while P0 runs (its barriers order LDS only)
+  if (nseg > 0) issue(0);
+
+  // ---- P0: quota prefix, per-cluster state, histogram clear
+  if (wave == 0) {
+    int v[4], loc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (int)a.quota[(long)row * C + min(lane * 4 + i, C - 1)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = lane * 4 + i < C ? v[i] : 0;
+      loc += v[i];
+    }
+    int incl = loc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    int run = incl - loc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = lane * 4 + i;     // 0..255
+      s_base[c] = run;
+      s_w[c] = c < C ? max(0, min(v[i], E - run)) : 0;
+      run += v[i];
+    }
+    if (lane == 63) s_base[kMaxC] = incl;
+  }
+  for (int c = tid; c < kMaxC; c += kThreads) {
+    s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_klo[c] = 0u; s_khi[c] = 0u; s_pref[c] = ~0u;
+    s_lo[c] = kNoGather;
+    s_mode[c] = kModeNone; s_goff[c] = 0; s_gcur[c] = 0; s_ccur[c] = 0;
+  }
+  for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
+  if (tid == 0) {
+    s_gused = 0; s_nfb = 0; s_nsplit = 0; s_hits1 = 0; s_ucnt = 0;
+    s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0;
+  }
+  oa::lds_barrier();
+
   // ---- L1: histogram of the top LB key bits per cluster
   for (int sg = 0; sg < nseg; ++sg) {
-    load(sg);
+    if (sg > 0) issue(sg);
+    keys(sg);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const uint32_t k = kk[i];
@@ -372,7 +383,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       atomicAdd(&s_hist[k ? slot : trash], 1);
     }
   }
-  __syncthreads();
+  oa::lds_barrier();
 
   // ---- T1: level-1 bin of the t-th best member, 16 threads per cluster
   for (int cb = 0; cb < C; cb += kThreads / 16) {
@@ -410,7 +421,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       }
     }
   }
-  __syncthreads();
+  oa::lds_barrier();
   const bool fits = s_hits1 <= a.ucap;   // block-uniform: the level-1 set fits in the list
   int ucnt = 0;
 
@@ -427,7 +438,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     for (int c = tid; c < kMaxC; c += kThreads)
       s_pref[c] = c < C && s_mode[c] == kModeSplit ? s_klo[c] >> shp : ~0u;
     clear_hist();
-    __syncthreads();
+    oa::lds_barrier();
     // every thread has read s_nsplit for its loop test before the barrier above; the count is
     // rebuilt in the scan below, after the next barrier
     if (tid == 0) s_nsplit = 0;
@@ -472,7 +483,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         }
       }
     }
-    __syncthreads();
+    oa::lds_barrier();
     for (int cb = 0; cb < C; cb += kThreads / 16) {
       const int c = cb + (tid >> 4);
       const int j = tid & 15;
@@ -510,7 +521,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         s_mode[c] = mode;
       }
     }
-    __syncthreads();
+    oa::lds_barrier();
   };
 
   if (!fits) {
@@ -523,7 +534,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       s_lo[c] = mode == kModeNone ? kNoGather
                 : (mode == kModeBlock ? s_khi[c] : max(s_klo[c], kNegInfKey + 1u) - 1u);
     }
-    __syncthreads();
+    oa::lds_barrier();
   }
 
   if (wave == 0) {               // prefix of t over clusters: chosen-word segment of each cluster
@@ -558,7 +569,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     }
     gather(sg, hb);
   }
-  __syncthreads();
+  oa::lds_barrier();
   ucnt = min(s_ucnt, a.ucap);
 
   if (fits)
@@ -591,7 +602,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(key[u], (int)(e[u] & 0xffffffu));
     }
   }
-  __syncthreads();
+  oa::lds_barrier();
 
   // ---- P5: the `need` best of each staged cluster's boundary bin, one wave per cluster
   for (int c = wave; c < C; c += kWaves) {
@@ -629,7 +640,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       }
       // three counters in rotation: the one cleared here is next added to two barriers later
       if (lane == 0 && k) atomicAdd(&s_fbcnt[it % 3], k);
-      __syncthreads();
+      oa::lds_barrier();
       if (s_fbcnt[it % 3] >= need) T = cnd;
       if (tid == 0) s_fbcnt[(it + 2) % 3] = 0;
     }
@@ -642,13 +653,13 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         append_chosen(take, ((uint32_t)c << 24) | (uint32_t)p, s_cst + s_tpre[c], &s_ccur[c], lane);
       }
     }
-    __syncthreads();
+    oa::lds_barrier();
     if (tid == 0) { s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0; }
-    __syncthreads();
+    oa::lds_barrier();
   }
-  __syncthreads();
+  oa::lds_barrier();
   for (int sl = tid; sl < E; sl += kThreads) s_out[sl] = -1;   // the staged keys are dead
-  __syncthreads();
+  oa::lds_barrier();
 
   // ---- P6: each chosen word's rank inside its cluster (by position), into the LDS row copy
   const int total = s_tpre[kMaxC];   // == sum_c t_c; every cluster's segment is full
@@ -672,7 +683,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     int P = 1;
     while (P < total) P <<= 1;
     for (int i = total + tid; i < P; i += kThreads) s_cst[i] = 0xffffffffu;
-    __syncthreads();
+    oa::lds_barrier();
     for (int k = 2; k <= P; k <<= 1) {
       for (int j = k >> 1; j > 0; j >>= 1) {
         for (int i = tid; i < P; i += kThreads) {
@@ -683,7 +694,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
             if ((x > y) == up) { s_cst[i] = y; s_cst[ixj] = x; }
           }
         }
-        __syncthreads();
+        oa::lds_barrier();
       }
     }
     for (int j = tid; j < total; j += kThreads) {
@@ -692,7 +703,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
       s_out[s_base[c] + (j - s_tpre[c])] = (int)(w & 0xffffffu);
     }
   }
-  __syncthreads();
+  oa::lds_barrier();
   for (int sl = tid; sl < E; sl += kThreads) erow[sl] = s_out[sl];
 }
 
