@@ -166,6 +166,18 @@ int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride
             const int* n_dev, void* stream);
 
 /*
+ * oa_topq with the algorithm chosen: path 0 (what oa_topq runs) bins scores linearly over each
+ * row's score range and leaves rows whose boundary bins overflow the staging space to the
+ * key-prefix histogram kernel; path 1 runs the key-prefix kernel on every row; path 2 runs the
+ * linear-bin kernel alone, and a row it leaves to the other kernel holds -2 in exp_idx[row][0]
+ * (its other slots are not written).  Paths 0 and 1 give the same exp_idx.  No counterpart in
+ * the reference: paths 1 and 2 exist so that each kernel can be checked on its own.
+ */
+int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
+                 const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
+                 const int* n_dev, int path, void* stream);
+
+/*
  * Residual proxies: kbar', vbar' (bf16, rows x C x 128) and ln n' (fp32, -inf = none) of the
  * tokens still unread.  Replaces _k_resid_scatter + _k_resid_norm
  * (inference/ours_fused.py:366-407).

@@ -64,6 +64,7 @@ constexpr int kUPT = 8;                        // gathered entries per thread ha
 constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
 constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster with no quota
 constexpr int kLdsLimit = 160 * 1024;
+constexpr int32_t kRowMarked = -2;              // exp_idx[row][0] of a row left to the key-prefix kernel
 
 enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3, kModeSplit = 4 };
 
@@ -77,7 +78,13 @@ struct TopqArgs {
   int hwords;      // ints of the area holding the histogram, then the staged keys, then the row
   int gcap;        // staged-key capacity (u64 entries)
   int cpow;        // power of two >= E: chosen-word list and the P6 sort
+  int marked_only; // key-prefix kernel: only rows the linear-bin kernel marked kRowMarked
 };
+
+// the float whose order-preserving key is k (inverse of oa::float_key)
+__device__ __forceinline__ float key_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
 
 __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
   return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (unsigned)pos);
@@ -211,6 +218,131 @@ __device__ __forceinline__ void find_bin(const RowScan<BPT>& r, int t, int& bin,
   }
 }
 
+
+// wave 0: exp_idx segment of each cluster (s_base, exclusive prefix of the quotas) and its
+// E-capped quota s_w = min(q_c, E - base_c), clamped at 0
+__device__ __forceinline__ void quota_prefix(const float* qrow, int C, int E, int lane, int* s_base,
+                                             int* s_w) {
+  int v[4], loc = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = (int)qrow[min(lane * 4 + i, C - 1)];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = lane * 4 + i < C ? v[i] : 0;
+    loc += v[i];
+  }
+  int incl = loc;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += t;
+  }
+  int run = incl - loc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = lane * 4 + i;     // 0..255
+    s_base[c] = run;
+    s_w[c] = c < C ? max(0, min(v[i], E - run)) : 0;
+    run += v[i];
+  }
+  if (lane == 63) s_base[kMaxC] = incl;
+}
+
+// wave 0: chosen-word segment of each cluster (exclusive prefix of s_t)
+__device__ __forceinline__ void chosen_prefix(const int* s_t, int* s_tpre, int lane) {
+  int v[4], loc = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { v[i] = s_t[lane * 4 + i]; loc += v[i]; }
+  int incl = loc;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += t;
+  }
+  int run = incl - loc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { s_tpre[lane * 4 + i] = run; run += v[i]; }
+  if (lane == 63) s_tpre[kMaxC] = incl;
+}
+
+// P5 for every staged cluster, one wave per cluster: the `need` best of its staged keys join
+// its chosen words
+__device__ __forceinline__ void select_all_staged(int C, int wave, int lane, const int* s_mode,
+                                                  const int* s_bcnt, const int* s_t,
+                                                  const int* s_above,
+                                                  const unsigned long long* s_g, const int* s_goff,
+                                                  uint32_t* s_cst, const int* s_tpre,
+                                                  const unsigned* s_klo, const unsigned* s_khi,
+                                                  int* s_ccur) {
+  for (int c = wave; c < C; c += kWaves) {
+    if (s_mode[c] != kModeStaged) continue;
+    const int cnt = s_bcnt[c];
+    const int need = s_t[c] - s_above[c];
+    const unsigned long long* src = s_g + s_goff[c];
+    uint32_t* dst = s_cst + s_tpre[c];
+    const unsigned long long fl = bin_floor(s_klo[c]);
+    const int top = bin_top_bit(s_klo[c], s_khi[c]);
+    if (cnt <= 64) select_staged<1>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+    else select_staged_loop(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+  }
+}
+
+// P6 and the write: each chosen word's rank inside its cluster (by position) places it in an
+// LDS copy of the exp_idx row (-1 where a segment is short), which is then written out once.
+// Starts and ends with a barrier; s_out may alias the staged keys (dead by then).
+__device__ __forceinline__ void rank_and_write(int E, int tid, const int* s_base, const int* s_t,
+                                               const int* s_tpre, uint32_t* s_cst, int* s_out,
+                                               int32_t* erow) {
+  oa::lds_barrier();
+  for (int sl = tid; sl < E; sl += kThreads) s_out[sl] = -1;
+  oa::lds_barrier();
+  const int total = s_tpre[kMaxC];   // == sum_c t_c; every cluster's segment is full
+  if (total <= kRankMax) {
+    for (int j = tid; j < total; j += kThreads) {
+      const uint32_t w = s_cst[j];
+      const int c = (int)(w >> 24);
+      const int b = s_tpre[c], t = s_t[c];
+      int rank = 0, k = b;
+      for (; k + 8 <= b + t; k += 8) {
+        uint32_t y[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) y[u] = s_cst[k + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rank += y[u] < w ? 1 : 0;
+      }
+      for (; k < b + t; ++k) rank += s_cst[k] < w ? 1 : 0;
+      s_out[s_base[c] + rank] = (int)(w & 0xffffffu);
+    }
+  } else {
+    int P = 1;
+    while (P < total) P <<= 1;
+    for (int i = total + tid; i < P; i += kThreads) s_cst[i] = 0xffffffffu;
+    oa::lds_barrier();
+    for (int k = 2; k <= P; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < P; i += kThreads) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const uint32_t x = s_cst[i], y = s_cst[ixj];
+            const bool up = (i & k) == 0;
+            if ((x > y) == up) { s_cst[i] = y; s_cst[ixj] = x; }
+          }
+        }
+        oa::lds_barrier();
+      }
+    }
+    for (int j = tid; j < total; j += kThreads) {
+      const uint32_t w = s_cst[j];
+      const int c = (int)(w >> 24);
+      s_out[s_base[c] + (j - s_tpre[c])] = (int)(w & 0xffffffu);
+    }
+  }
+  oa::lds_barrier();
+  for (int sl = tid; sl < E; sl += kThreads) erow[sl] = s_out[sl];
+}
+
 template <int PPT, int LB>
 __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
@@ -248,6 +380,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   constexpr int sh1 = 32 - LB;
   constexpr int sh1p = sh1 + sb;          // shift giving a level-1 bin's pad-word count
   const int trash = C * HS + lane;        // per-lane histogram slot for non-members
+  if (a.marked_only && a.exp_idx[(long)row * E] != kRowMarked) return;   // uniform
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
   const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
@@ -334,31 +467,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   if (nseg > 0) issue(0);
 
   // ---- P0: quota prefix, per-cluster state, histogram clear
-  if (wave == 0) {
-    int v[4], loc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (int)a.quota[(long)row * C + min(lane * 4 + i, C - 1)];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = lane * 4 + i < C ? v[i] : 0;
-      loc += v[i];
-    }
-    int incl = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += t;
-    }
-    int run = incl - loc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = lane * 4 + i;     // 0..255
-      s_base[c] = run;
-      s_w[c] = c < C ? max(0, min(v[i], E - run)) : 0;
-      run += v[i];
-    }
-    if (lane == 63) s_base[kMaxC] = incl;
-  }
+  if (wave == 0) quota_prefix(a.quota + (long)row * C, C, E, lane, s_base, s_w);
   for (int c = tid; c < kMaxC; c += kThreads) {
     s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_klo[c] = 0u; s_khi[c] = 0u; s_pref[c] = ~0u;
     s_lo[c] = kNoGather;
@@ -537,21 +646,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     oa::lds_barrier();
   }
 
-  if (wave == 0) {               // prefix of t over clusters: chosen-word segment of each cluster
-    int v[4], loc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { v[i] = s_t[lane * 4 + i]; loc += v[i]; }
-    int incl = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += t;
-    }
-    int run = incl - loc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { s_tpre[lane * 4 + i] = run; run += v[i]; }
-    if (lane == 63) s_tpre[kMaxC] = incl;
-  }
+  if (wave == 0) chosen_prefix(s_t, s_tpre, lane);   // chosen-word segment of each cluster
 
   // ---- G: gather every member whose key reaches its cluster's bound
   for (int sg = 0; sg < nseg; ++sg) {
@@ -605,19 +700,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   oa::lds_barrier();
 
   // ---- P5: the `need` best of each staged cluster's boundary bin, one wave per cluster
-  for (int c = wave; c < C; c += kWaves) {
-    if (s_mode[c] != kModeStaged) continue;
-    const int cnt = s_bcnt[c];
-    const int need = s_t[c] - s_above[c];
-    const unsigned long long* src = s_g + s_goff[c];
-    uint32_t* dst = s_cst + s_tpre[c];
-    const unsigned long long fl = bin_floor(s_klo[c]);
-    const int top = bin_top_bit(s_klo[c], s_khi[c]);
-    if (cnt <= 64) select_staged<1>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
-    else if (cnt <= 256) select_staged<4>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
-    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
-    else select_staged_loop(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
-  }
+  select_all_staged(C, wave, lane, s_mode, s_bcnt, s_t, s_above, s_g, s_goff, s_cst, s_tpre, s_klo,
+                    s_khi, s_ccur);
   // clusters whose boundary bin holds more equal keys than the staging space: block-wide
   // bitwise search over the positions, re-streaming the row (rare)
   const int nfb = s_nfb;         // final since the last refinement barrier
@@ -657,54 +741,217 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
     if (tid == 0) { s_fbcnt[0] = 0; s_fbcnt[1] = 0; s_fbcnt[2] = 0; }
     oa::lds_barrier();
   }
-  oa::lds_barrier();
-  for (int sl = tid; sl < E; sl += kThreads) s_out[sl] = -1;   // the staged keys are dead
-  oa::lds_barrier();
+  // ---- P6: each chosen word's rank inside its cluster (by position), then the row write
+  rank_and_write(E, tid, s_base, s_t, s_tpre, s_cst, s_out, erow);
+}
 
-  // ---- P6: each chosen word's rank inside its cluster (by position), into the LDS row copy
-  const int total = s_tpre[kMaxC];   // == sum_c t_c; every cluster's segment is full
-  if (total <= kRankMax) {
-    for (int j = tid; j < total; j += kThreads) {
-      const uint32_t w = s_cst[j];
-      const int c = (int)(w >> 24);
-      const int b = s_tpre[c], t = s_t[c];
-      int rank = 0, k = b;
-      for (; k + 8 <= b + t; k += 8) {
-        uint32_t y[8];
+
+// The linear-bin kernel: the common path.  Scores are binned linearly over the row's range of
+// qualifying scores, [smin, smax]: bin(s) = min(NB - 1, (int)((s - smin) * NB / (smax - smin)))
+// is non-decreasing in s, so a member in a higher bin beats every member in a lower one, and
+// the boundary bin of a cluster (the bin of its t-th best member) holds a handful of members
+// where the key-prefix bins hold hundreds.  One pass builds the per-cluster histograms (R, L1),
+// 16 threads per cluster find the boundary bins (T1), and one more pass over the registers (G)
+// sends members above the boundary straight to their cluster's chosen words and boundary-bin
+// members to the staged keys; P5 and P6 are shared with the key-prefix kernel.  A row whose
+// staged members do not fit the staging space is marked (exp_idx[row][0] = kRowMarked) and left
+// to the key-prefix kernel, launched next over the marked rows only.
+template <int PPT, int LB>
+__global__ void __launch_bounds__(kThreads) topq_linear_kernel(TopqArgs a) {
+  extern __shared__ unsigned long long dyn[];
+  __shared__ int s_w[kMaxC];
+  __shared__ int s_base[kMaxC + 1];
+  __shared__ int s_t[kMaxC];
+  __shared__ int s_above[kMaxC];
+  __shared__ int s_bcnt[kMaxC];
+  __shared__ unsigned s_klo[kMaxC], s_khi[kMaxC];   // 0, ~0: P5 searches all 32 key bits
+  __shared__ unsigned s_sel[kMaxC];       // first chosen bin (low half), staged bin (high half)
+  __shared__ int s_mode[kMaxC];
+  __shared__ int s_goff[kMaxC], s_gcur[kMaxC];
+  __shared__ int s_ccur[kMaxC];
+  __shared__ int s_tpre[kMaxC + 1];
+  __shared__ int s_gused, s_fail;
+  __shared__ uint32_t s_rlo[kWaves], s_rhi[kWaves];
+  constexpr int NB = 1 << LB;
+  constexpr int HS = NB + 16;
+  constexpr int sb = LB - 4;
+  constexpr int bpt = NB >> 4;
+  int* s_hist = reinterpret_cast<int*>(dyn);                                  // hwords
+  unsigned long long* s_g = reinterpret_cast<unsigned long long*>(s_hist);    // after T1
+  int* s_out = s_hist;                                                        // after P5
+  uint32_t* s_cst = reinterpret_cast<uint32_t*>(s_hist + a.hwords);           // cpow
+
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int C = a.C, E = a.E;
+  const int trash = C * HS + lane;
+  const int n = *a.n_dev;
+  const float* srow = a.S + (long)row * a.s_stride;
+  const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
+  int32_t* erow = a.exp_idx + (long)row * E;
+
+  constexpr int SEG = kThreads * PPT;
+  constexpr int NG = PPT / 4;
+  constexpr int CH = 12;
+  // the single-segment instantiations (PPT <= 36) are launched only for Lmax <= SEG
+  constexpr bool kMulti = PPT > 36;
+  const int nseg = n > 0 ? (kMulti ? (n + SEG - 1) / SEG : 1) : 0;
+  uint32_t kk[PPT];
+  uint32_t cp[NG];
+  auto pos_of = [&](int sg, int i) -> int { return sg * SEG + (i >> 2) * 4096 + 4 * tid + (i & 3); };
+  auto issue = [&](int sg) {
+    const int last4 = (n - 1) & ~3;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) y[u] = s_cst[k + u];
+    for (int g = 0; g < NG; ++g) {
+      const int p = min(sg * SEG + g * 4096 + 4 * tid, last4);
+      const float4 v = *reinterpret_cast<const float4*>(srow + p);
+      cp[g] = *reinterpret_cast<const uint32_t*>(arow + p);
+      kk[4 * g] = __float_as_uint(v.x);
+      kk[4 * g + 1] = __float_as_uint(v.y);
+      kk[4 * g + 2] = __float_as_uint(v.z);
+      kk[4 * g + 3] = __float_as_uint(v.w);
+    }
+  };
+  auto keys = [&](int sg) {
+    const int lim = n - sg * SEG - 4 * tid;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) rank += y[u] < w ? 1 : 0;
-      }
-      for (; k < b + t; ++k) rank += s_cst[k] < w ? 1 : 0;
-      s_out[s_base[c] + rank] = (int)(w & 0xffffffu);
+    for (int i = 0; i < PPT; ++i) {
+      const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
+      const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
+      kk[i] = q ? key : 0u;
     }
-  } else {
-    int P = 1;
-    while (P < total) P <<= 1;
-    for (int i = total + tid; i < P; i += kThreads) s_cst[i] = 0xffffffffu;
-    oa::lds_barrier();
-    for (int k = 2; k <= P; k <<= 1) {
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = tid; i < P; i += kThreads) {
-          const int ixj = i ^ j;
-          if (ixj > i) {
-            const uint32_t x = s_cst[i], y = s_cst[ixj];
-            const bool up = (i & k) == 0;
-            if ((x > y) == up) { s_cst[i] = y; s_cst[ixj] = x; }
-          }
-        }
-        oa::lds_barrier();
-      }
+  };
+  auto load = [&](int sg) { issue(sg); keys(sg); };
+  auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+
+  if (nseg > 0) issue(0);       // in flight while P0 runs
+
+  // ---- P0: quota prefix, per-cluster state, histogram clear
+  if (wave == 0) quota_prefix(a.quota + (long)row * C, C, E, lane, s_base, s_w);
+  for (int c = tid; c < kMaxC; c += kThreads) {
+    s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_klo[c] = 0u; s_khi[c] = ~0u;
+    s_sel[c] = 0xffffffffu; s_mode[c] = kModeNone; s_goff[c] = 0; s_gcur[c] = 0; s_ccur[c] = 0;
+  }
+  for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
+  if (tid == 0) { s_gused = 0; s_fail = 0; }
+
+  // ---- R: the range of the qualifying members' score keys
+  uint32_t klo = 0xffffffffu, khi = 0u;
+  for (int sg = 0; sg < nseg; ++sg) {
+    if (sg == 0) keys(0); else load(sg);
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      klo = min(klo, kk[i] ? kk[i] : 0xffffffffu);
+      khi = max(khi, kk[i]);
     }
-    for (int j = tid; j < total; j += kThreads) {
-      const uint32_t w = s_cst[j];
-      const int c = (int)(w >> 24);
-      s_out[s_base[c] + (j - s_tpre[c])] = (int)(w & 0xffffffu);
+  }
+  klo = ~oa::wave_max_u32(~klo);
+  khi = oa::wave_max_u32(khi);
+  if (lane == 0) { s_rlo[wave] = klo; s_rhi[wave] = khi; }
+  oa::lds_barrier();
+  klo = 0xffffffffu;
+  khi = 0u;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) { klo = min(klo, s_rlo[w]); khi = max(khi, s_rhi[w]); }
+  float smin = 0.f, scale = 0.f;
+  if (khi != 0u) {
+    smin = key_float(klo);
+    const float span = key_float(khi) - smin;
+    scale = span > 0.f && span < INFINITY ? (float)NB / span : 0.f;
+  }
+  auto fbin = [&](uint32_t k) -> int { return min(NB - 1, (int)((key_float(k) - smin) * scale)); };
+
+  // ---- L1: per-cluster histogram of the linear bins
+  for (int sg = 0; sg < nseg; ++sg) {
+    if (nseg > 1) load(sg);
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const uint32_t k = kk[i];
+      const int bn = fbin(k);
+      int slot = (int)__umul24(cid(i), HS) + bn + (bn >> sb);
+      asm volatile("" : "+v"(slot));
+      atomicAdd(&s_hist[k ? slot : trash], 1);
     }
   }
   oa::lds_barrier();
-  for (int sl = tid; sl < E; sl += kThreads) erow[sl] = s_out[sl];
+
+  // ---- T1: boundary bin b1 of every cluster with quota; bins above it are chosen, b1 itself
+  // is chosen whole when it completes t, else its members are staged
+  for (int cb = 0; cb < C; cb += kThreads / 16) {
+    const int c = cb + (tid >> 4);
+    const int j = tid & 15;
+    const int w = c < C ? s_w[c] : 0;
+    RowScan<bpt> r;
+    scan_row(s_hist + min(c, C - 1) * HS, j, r);
+    const int m = __shfl(r.sfx, 0, 16);
+    if (c < C && w > 0) {
+      const int t = min(w, m);
+      if (t > 0 && t == m) {     // every member is chosen
+        if (j == 0) { s_t[c] = t; s_mode[c] = kModeAll; s_sel[c] = 0xffff0000u; }
+      } else if (t > 0 && r.sfx >= t && r.sfx - r.ls < t) {
+        int b, acc, cnt;
+        find_bin(r, t, b, acc, cnt);
+        const unsigned b1 = (unsigned)(j * bpt + b);
+        s_t[c] = t;
+        s_above[c] = acc;
+        s_bcnt[c] = cnt;
+        if (t - acc == cnt) {
+          s_mode[c] = kModeAll;
+          s_sel[c] = 0xffff0000u | b1;
+        } else {
+          const int off = atomicAdd(&s_gused, cnt);
+          if (off + cnt <= a.gcap) {
+            s_mode[c] = kModeStaged;
+            s_goff[c] = off;
+            s_sel[c] = (b1 << 16) | (b1 + 1u);
+          } else {
+            s_fail = 1;
+          }
+        }
+      }
+    }
+  }
+  oa::lds_barrier();
+  if (s_fail) {                  // uniform: the key-prefix kernel takes the row
+    if (tid == 0) erow[0] = kRowMarked;
+    return;
+  }
+  if (wave == 0) chosen_prefix(s_t, s_tpre, lane);
+  oa::lds_barrier();
+
+  // ---- G: members in the chosen bins to their cluster's chosen words, members in a staged
+  // bin to its staged keys (the histogram is dead: the staged keys reuse it)
+  for (int sg = 0; sg < nseg; ++sg) {
+    if (nseg > 1) load(sg);
+#pragma unroll
+    for (int i0 = 0; i0 < PPT; i0 += CH) {
+      unsigned sv[CH];
+#pragma unroll
+      for (int j = 0; j < CH; ++j)
+        if (i0 + j < PPT) sv[j] = s_sel[cid(i0 + j)];
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        if (i0 + j < PPT) {
+          const int i = i0 + j;
+          const uint32_t k = kk[i];
+          const int bn = fbin(k);
+          const int c = cid(i);
+          if (k && bn >= (int)(sv[j] & 0xffffu))
+            s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos_of(sg, i);
+          else if (k && bn == (int)(sv[j] >> 16))
+            s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(k, pos_of(sg, i));
+        }
+      }
+    }
+  }
+  oa::lds_barrier();
+
+  // ---- P5, P6
+  select_all_staged(C, wave, lane, s_mode, s_bcnt, s_t, s_above, s_g, s_goff, s_cst, s_tpre, s_klo,
+                    s_khi, s_ccur);
+  rank_and_write(E, tid, s_base, s_t, s_tpre, s_cst, s_out, erow);
 }
 
 template <int PPT, int LB>
@@ -724,16 +971,36 @@ int launch_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStream_t s) 
   return launch_row<44, LB>(a, rows, lds, s);
 }
 
+template <int PPT, int LB>
+int launch_linear(const TopqArgs& a, int rows, size_t lds, hipStream_t s) {
+  const hipError_t e = hipFuncSetAttribute((const void*)topq_linear_kernel<PPT, LB>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((topq_linear_kernel<PPT, LB>), dim3(rows), dim3(kThreads), lds, s, a);
+  return OA_LAUNCH_STATUS();
+}
+
+template <int LB>
+int launch_linear_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStream_t s) {
+  if (Lmax <= kThreads * 8) return launch_linear<8, LB>(a, rows, lds, s);
+  if (Lmax <= kThreads * 16) return launch_linear<16, LB>(a, rows, lds, s);
+  if (Lmax <= kThreads * 36) return launch_linear<36, LB>(a, rows, lds, s);
+  return launch_linear<44, LB>(a, rows, lds, s);
+}
+
 }  // namespace
 
-extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
-                       const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
-                       const int* n_dev, void* stream) {
+// path 0: the linear-bin kernel on every row, then the key-prefix kernel on the rows it
+// marked; path 1: the key-prefix kernel on every row; path 2: the linear-bin kernel alone (a
+// row it leaves to the key-prefix kernel keeps the mark kRowMarked in exp_idx[row][0])
+extern "C" int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
+                            const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
+                            const int* n_dev, int path, void* stream) {
   const long lmax4 = ((long)Lmax + 3) & ~3L;
   if (rows <= 0 || C <= 0 || C > kMaxC || E < 0 || E > kMaxE || Lmax <= 0 || Lmax >= kMaxPos ||
       !S || !asg8 || !quota || !n_dev || (E > 0 && !exp_idx) || s_stride % 4 || asg8_stride % 4 ||
       s_stride < lmax4 || asg8_stride < lmax4 || (reinterpret_cast<uintptr_t>(S) & 15) ||
-      (reinterpret_cast<uintptr_t>(asg8) & 3))
+      (reinterpret_cast<uintptr_t>(asg8) & 3) || path < 0 || path > 2)
     return OA_EINVAL;
   if (E == 0) return 0;
   TopqArgs a;
@@ -743,8 +1010,8 @@ extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long 
   a.lb = C <= 64 ? 8 : (C <= 128 ? 7 : 6);
   a.cpow = 4;                   // >= 4: the LDS rows are cleared and scanned 4 words at a time
   while (a.cpow < E) a.cpow <<= 1;
-  // dynamic LDS: gathered list (ucap + 64 trash entries: a word array and a key array) |
-  // histogram -> staged keys -> output row (hwords ints) | chosen words (cpow u32)
+  // key-prefix kernel, dynamic LDS: gathered list (ucap + 64 trash entries: a word array and a
+  // key array) | histogram -> staged keys -> output row (hwords ints) | chosen words (cpow u32)
   const long hist = (long)C * ((1 << a.lb) + 16) + 64;
   a.hwords = (int)((std::max<long>(hist, a.cpow) + 3) & ~3L);
   const long static_lds = (long)sizeof(int) * (16 * kMaxC + 8);
@@ -754,7 +1021,27 @@ extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long 
   if (a.gcap < 64) return OA_EINVAL;
   const size_t lds = 8 * (size_t)(a.ucap + 64) + 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
   hipStream_t s = (hipStream_t)stream;
+  int st = 0;
+  a.marked_only = 0;
+  if (path != 1) {
+    // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words
+    TopqArgs al = a;
+    al.gcap = a.hwords / 2;
+    const size_t lds_lin = 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
+    if (a.lb == 8) st = launch_linear_lb<8>(al, rows, Lmax, lds_lin, s);
+    else if (a.lb == 7) st = launch_linear_lb<7>(al, rows, Lmax, lds_lin, s);
+    else st = launch_linear_lb<6>(al, rows, Lmax, lds_lin, s);
+    if (st || path == 2) return st;
+    a.marked_only = 1;
+  }
   if (a.lb == 8) return launch_lb<8>(a, rows, Lmax, lds, s);
   if (a.lb == 7) return launch_lb<7>(a, rows, Lmax, lds, s);
   return launch_lb<6>(a, rows, Lmax, lds, s);
+}
+
+extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
+                       const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
+                       const int* n_dev, void* stream) {
+  return oa_topq_path(S, s_stride, asg8, asg8_stride, quota, rows, C, Lmax, exp_idx, E, n_dev, 0,
+                      stream);
 }

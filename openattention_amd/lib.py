@@ -36,6 +36,7 @@ SIGNATURES = {
     "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P],
     "oa_waterfill": [P, P, I, I, I, P, P],
     "oa_topq": [P, L, P, L, P, I, I, I, P, I, P, P],
+    "oa_topq_path": [P, L, P, L, P, I, I, I, P, I, P, I, P],
     "oa_residual": [P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, P, P, P, P],
     "oa_residual_flash": [P, L, P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, F, P, L,
                           P],

@@ -221,14 +221,20 @@ def waterfill(score, n_t, quota, E: int) -> None:
     lib.call("oa_waterfill", _ptr(score), _ptr(n_t), R, C, int(E), _ptr(quota), _stream(dev))
 
 
-def topq(S, asg8, quota, exp_idx, n_dev) -> None:
-    """Within-cluster top-q (exp_idx segments grouped by cluster, position order inside)."""
+def topq(S, asg8, quota, exp_idx, n_dev, path: int | None = None) -> None:
+    """Within-cluster top-q (exp_idx segments grouped by cluster, position order inside).
+    path None: oa_topq; 0 / 1 / 2: oa_topq_path (both kernels / key-prefix only / linear-bin only,
+    a row left to the key-prefix kernel then holding -2 in exp_idx[row, 0])."""
     dev = _dev(S, asg8, quota, exp_idx, n_dev)
     R, C = quota.shape
     Lmax = asg8.shape[1]
     E = exp_idx.shape[1]
-    lib.call("oa_topq", _ptr(S), S.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R, C, Lmax,
-             _ptr(exp_idx), E, _ptr(n_dev), _stream(dev))
+    if path is None:
+        lib.call("oa_topq", _ptr(S), S.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R, C,
+                 Lmax, _ptr(exp_idx), E, _ptr(n_dev), _stream(dev))
+    else:
+        lib.call("oa_topq_path", _ptr(S), S.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R,
+                 C, Lmax, _ptr(exp_idx), E, _ptr(n_dev), int(path), _stream(dev))
 
 
 def residual(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n) -> None:

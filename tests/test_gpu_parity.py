@@ -288,15 +288,16 @@ def test_topq_generated_list_overflow_fallback(lay4k):
     assert np.any((cnt > 1) & (quota > 0)), "no overflowed cluster was expanded"
 
 
+@pytest.mark.parametrize("path", [None, 1])
 @pytest.mark.parametrize("n,C,E,seed", [(20000, 16, 300, 1), (8192, 4, 64, 2), (777, 8, 4096, 3),
                                            (20000, 100, 600, 6), (12000, 200, 1000, 7)])
-def test_topq_adversarial_quotas(n, C, E, seed):
+def test_topq_adversarial_quotas(n, C, E, seed, path):
     """Top-q on synthetic rows built to hit every branch: scores on a coarse grid (many ties,
     broken by position), one cluster holding ~60% of the row (more than 1024 members per
     8192-position chunk), quotas above the member count, quota sums above E (a segment cut at
     E), a partial last chunk, and an output buffer holding stale values.  C = 100 and 200 run
     the 7- and 6-bit histogram levels."""
-    print(f"[case] topq adversarial n={n} C={C} E={E}", flush=True)
+    print(f"[case] topq adversarial n={n} C={C} E={E} path={path}", flush=True)
     rng = np.random.default_rng(seed)
     R, Lmax = 6, -(-(n + 300) // 64) * 64     # row strides: multiples of 4 (oa_topq reads 4 at a time)
     S = np.round(rng.standard_normal((R, Lmax)) * 4) / 4
@@ -317,23 +318,24 @@ def test_topq_adversarial_quotas(n, C, E, seed):
     exp_idx = torch.full((R, E), 12345, device=DEV, dtype=torch.int32)
     n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
     asg8 = torch.from_numpy(asg.astype(np.uint8)).to(DEV)
-    ops.topq(_f32(S), asg8, _f32(quota), exp_idx, n_dev)
+    ops.topq(_f32(S), asg8, _f32(quota), exp_idx, n_dev, path=path)
     torch.cuda.synchronize()
     got = exp_idx.cpu().numpy()
     assert np.array_equal(got, ref), f"rows differ: {np.nonzero((got != ref).any(1))[0]}"
 
 
+@pytest.mark.parametrize("path", [None, 1])
 @pytest.mark.parametrize("n,C,E,seed,grid", [(30000, 2, 300, 4, "coarse"), (60000, 4, 512, 5, "coarse"),
                                                 (30000, 2, 300, 8, "fine"), (12000, 2, 300, 9, "fine"),
                                                 (60000, 256, 3000, 10, "fine")])
-def test_topq_deep_histogram_levels(n, C, E, seed, grid):
+def test_topq_deep_histogram_levels(n, C, E, seed, grid, path):
     """Top-q when boundary bins stay too large for the LDS staging space after two histogram
     levels.  "coarse": every score sits in [1, 2) on a grid of eight values, so each level-2 bin
     holds thousands of equal keys: four levels, then the block-wide search over positions.
     "fine": scores 1 + u 2^-20 (u < 2^16), so a third level separates them.  n = 30000 / 60000
     put the level-1 set beyond the gathering list (register passes; 60000 is two register
     segments), n = 12000 keeps it in the list (list passes); C = 256 runs the 6-bit levels."""
-    print(f"[case] topq deep levels n={n} C={C} E={E} grid={grid}", flush=True)
+    print(f"[case] topq deep levels n={n} C={C} E={E} grid={grid} path={path}", flush=True)
     rng = np.random.default_rng(seed)
     R, Lmax = 3, -(-(n + 300) // 64) * 64
     if grid == "coarse":
@@ -353,10 +355,50 @@ def test_topq_deep_histogram_levels(n, C, E, seed, grid):
     exp_idx = torch.full((R, E), 12345, device=DEV, dtype=torch.int32)
     n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
     asg8 = torch.from_numpy(asg.astype(np.uint8)).to(DEV)
-    ops.topq(_f32(S), asg8, _f32(quota), exp_idx, n_dev)
+    ops.topq(_f32(S), asg8, _f32(quota), exp_idx, n_dev, path=path)
     torch.cuda.synchronize()
     got = exp_idx.cpu().numpy()
     assert np.array_equal(got, ref), f"rows differ: {np.nonzero((got != ref).any(1))[0]}"
+
+
+@pytest.mark.parametrize("n,C,E,seed", [(32768, 64, 216, 11), (30000, 128, 700, 12), (50000, 256, 2000, 13)])
+def test_topq_linear_bins_and_marked_rows(n, C, E, seed):
+    """The linear-bin kernel alone (path 2) on Gaussian scores resolves every row and equals the
+    restatement; rows given one huge score (every other member then lands in the lowest linear
+    bin, so the boundary bins overflow the staging space) are marked -2 in slot 0 and left to
+    the key-prefix kernel, and the two kernels together (path 0) equal the restatement on
+    every row."""
+    print(f"[case] topq linear n={n} C={C} E={E}", flush=True)
+    rng = np.random.default_rng(seed)
+    R, Lmax = 8, -(-(n + 300) // 64) * 64
+    S = (rng.standard_normal((R, Lmax)) * 8).astype(np.float32)
+    asg = rng.integers(0, C, size=(R, Lmax)).astype(np.int32)
+    asg[:, n:] = 0
+    sel = np.stack([rng.choice(n, 16, replace=False) for _ in range(R)]).astype(np.int32)
+    for r in range(R):
+        S[r, sel[r]] = -np.inf
+    quota = rng.integers(0, 2 * max(E // C, 1) + 2, size=(R, C)).astype(np.float32)
+    outlier = [1, 4, 6]
+    for r in outlier:
+        p = n // 2
+        while p in sel[r]:
+            p += 1
+        S[r, p] = np.float32(3.0e37)
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    asg8 = torch.from_numpy(asg.astype(np.uint8)).to(DEV)
+    ref = O.topq(S, asg, sel, quota, n, E)
+    lin = torch.full((R, E), 12345, device=DEV, dtype=torch.int32)
+    ops.topq(_f32(S), asg8, _f32(quota), lin, n_dev, path=2)
+    both = torch.full((R, E), 12345, device=DEV, dtype=torch.int32)
+    ops.topq(_f32(S), asg8, _f32(quota), both, n_dev, path=0)
+    torch.cuda.synchronize()
+    lin, both = lin.cpu().numpy(), both.cpu().numpy()
+    marked = [r for r in range(R) if lin[r, 0] == -2]
+    assert marked == outlier, marked
+    for r in range(R):
+        if r not in outlier:
+            assert np.array_equal(lin[r], ref[r]), f"row {r}"
+    assert np.array_equal(both, ref), f"rows differ: {np.nonzero((both != ref).any(1))[0]}"
 
 
 def test_decode_sequence_groups_match_single_chain(lay4k):
