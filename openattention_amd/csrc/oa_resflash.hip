@@ -404,21 +404,27 @@ __global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
   __syncthreads();
 
   // ---- scalars: proxy logits (log2 units), block max, weights, coefficients
+  // Z_c = sum of q.k over the cluster's read tokens (its selected tokens and its expanded
+  // segment), one 16-lane group per cluster: lanes take every 16th token, a fixed DPP tree adds
+  // the 16 partials (a segment can hold hundreds of tokens)
   const float zs = a.sm_scale * kLog2e;
-  for (int c = tid; c < C; c += kRFThreads) {
+  for (int c = grp; c < C; c += kRFGroups) {
     float Z = 0.f;
-    for (int i = 0; i < a.n_sel; ++i)
+    for (int i = sub; i < a.n_sel; i += 16)
       if (s_cid[i] == c) Z += s_z[i];
     const int b1 = min(s_base[c] + s_q[c], a.E);
-    for (int j = s_base[c]; j < b1; ++j) {
+    for (int j = s_base[c] + sub; j < b1; j += 16) {
       const int i = a.n_sel + j;
       if (s_cid[i] == c) Z += s_z[i];
     }
-    const float nr = s_nt[c] - (float)s_q[c];
-    const float den = fmaxf(nr, 1.0f);
-    const bool live = nr > 0.5f;
-    s_l2[c] = live ? (((s_qsk[c] - Z) / den) * a.sm_scale + logf(den)) * kLog2e : -INFINITY;
-    s_cw[c] = den;
+    Z = oa::group16_sum(Z);
+    if (sub == 0) {
+      const float nr = s_nt[c] - (float)s_q[c];
+      const float den = fmaxf(nr, 1.0f);
+      const bool live = nr > 0.5f;
+      s_l2[c] = live ? (((s_qsk[c] - Z) / den) * a.sm_scale + logf(den)) * kLog2e : -INFINITY;
+      s_cw[c] = den;
+    }
   }
   __syncthreads();
   float mx = -INFINITY;
