@@ -757,7 +757,8 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 // staged members do not fit the staging space is marked (exp_idx[row][0] = kRowMarked) and left
 // to the key-prefix kernel, launched next over the marked rows only.
 template <int PPT, int LB>
-__global__ void __launch_bounds__(kThreads) topq_linear_kernel(TopqArgs a) {
+// up to 64 VGPRs for the single-segment instantiations: two workgroups (rows) per unit
+__global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
   __shared__ int s_w[kMaxC];
   __shared__ int s_base[kMaxC + 1];
@@ -798,7 +799,11 @@ __global__ void __launch_bounds__(kThreads) topq_linear_kernel(TopqArgs a) {
   // the single-segment instantiations (PPT <= 36) are launched only for Lmax <= SEG
   constexpr bool kMulti = PPT > 36;
   const int nseg = n > 0 ? (kMulti ? (n + SEG - 1) / SEG : 1) : 0;
-  uint32_t kk[PPT];
+  // Only the top 16 bits of each key stay in registers (two per register): h = key >> 16 is
+  // non-decreasing in the score, so bins of h order members as their scores do, and the few
+  // members of a staged bin get their exact keys from S again
+  uint32_t kk[PPT];             // the loaded scores, until keys() packs them
+  uint32_t kh[PPT / 2];         // 16-bit key heads of positions 2j (low half) and 2j + 1
   uint32_t cp[NG];
   auto pos_of = [&](int sg, int i) -> int { return sg * SEG + (i >> 2) * 4096 + 4 * tid + (i & 3); };
   auto issue = [&](int sg) {
@@ -817,13 +822,20 @@ __global__ void __launch_bounds__(kThreads) topq_linear_kernel(TopqArgs a) {
   auto keys = [&](int sg) {
     const int lim = n - sg * SEG - 4 * tid;
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
-      const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
-      kk[i] = q ? key : 0u;
+    for (int j = 0; j < PPT / 2; ++j) {
+      uint32_t h2 = 0u;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = 2 * j + u;
+        const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
+        const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
+        h2 |= (q ? key >> 16 : 0u) << (16 * u);
+      }
+      kh[j] = h2;
     }
   };
   auto load = [&](int sg) { issue(sg); keys(sg); };
+  auto hd = [&](int i) -> uint32_t { return (kh[i >> 1] >> (16 * (i & 1))) & 0xffffu; };
   auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
 
   if (nseg > 0) issue(0);       // in flight while P0 runs
@@ -843,8 +855,8 @@ __global__ void __launch_bounds__(kThreads) topq_linear_kernel(TopqArgs a) {
     if (sg == 0) keys(0); else load(sg);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      klo = min(klo, kk[i] ? kk[i] : 0xffffffffu);
-      khi = max(khi, kk[i]);
+      klo = min(klo, hd(i) ? hd(i) : 0xffffffffu);
+      khi = max(khi, hd(i));
     }
   }
   klo = ~oa::wave_max_u32(~klo);
@@ -857,18 +869,20 @@ __global__ void __launch_bounds__(kThreads) topq_linear_kernel(TopqArgs a) {
   for (int w = 0; w < kWaves; ++w) { klo = min(klo, s_rlo[w]); khi = max(khi, s_rhi[w]); }
   float smin = 0.f, scale = 0.f;
   if (khi != 0u) {
-    smin = key_float(klo);
-    const float span = key_float(khi) - smin;
+    smin = key_float(klo << 16);
+    const float span = key_float(khi << 16) - smin;
     scale = span > 0.f && span < INFINITY ? (float)NB / span : 0.f;
   }
-  auto fbin = [&](uint32_t k) -> int { return min(NB - 1, (int)((key_float(k) - smin) * scale)); };
+  // bin of a key head (a NaN's head lies above +inf's, 0xff80, and has no float order: with a
+  // NaN in the row the span is NaN, scale 0 and every member in bin 0, which is still ordered)
+  auto fbin = [&](uint32_t h) -> int { return min(NB - 1, (int)((key_float(h << 16) - smin) * scale)); };
 
   // ---- L1: per-cluster histogram of the linear bins
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const uint32_t k = kk[i];
+      const uint32_t k = hd(i);
       const int bn = fbin(k);
       int slot = (int)__umul24(cid(i), HS) + bn + (bn >> sb);
       asm volatile("" : "+v"(slot));
@@ -935,16 +949,23 @@ __global__ void __launch_bounds__(kThreads) topq_linear_kernel(TopqArgs a) {
       for (int j = 0; j < CH; ++j) {
         if (i0 + j < PPT) {
           const int i = i0 + j;
-          const uint32_t k = kk[i];
+          const uint32_t k = hd(i);
           const int bn = fbin(k);
           const int c = cid(i);
           if (k && bn >= (int)(sv[j] & 0xffffu))
             s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos_of(sg, i);
           else if (k && bn == (int)(sv[j] >> 16))
-            s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(k, pos_of(sg, i));
+            s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(0u, pos_of(sg, i));
         }
       }
     }
+  }
+  oa::lds_barrier();
+  // the staged members' exact keys, from S (they fill [0, s_gused) of the staged keys)
+  for (int j = tid; j < s_gused; j += kThreads) {
+    const unsigned long long e = s_g[j];
+    const int p = (int)(0xffffffffu - (uint32_t)e);
+    s_g[j] = key64(oa::float_key(srow[p]), p);
   }
   oa::lds_barrier();
 
@@ -1024,12 +1045,14 @@ extern "C" int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, 
   int st = 0;
   a.marked_only = 0;
   if (path != 1) {
-    // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words
+    // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words.
+    // 7 bits for C <= 64, else 6: up to C = 128 two workgroups' LDS fits one unit
     TopqArgs al = a;
-    al.gcap = a.hwords / 2;
-    const size_t lds_lin = 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
-    if (a.lb == 8) st = launch_linear_lb<8>(al, rows, Lmax, lds_lin, s);
-    else if (a.lb == 7) st = launch_linear_lb<7>(al, rows, Lmax, lds_lin, s);
+    al.lb = C <= 64 ? 7 : 6;
+    al.hwords = (int)((std::max<long>((long)C * ((1 << al.lb) + 16) + 64, a.cpow) + 3) & ~3L);
+    al.gcap = al.hwords / 2;
+    const size_t lds_lin = 4 * (size_t)al.hwords + 4 * (size_t)a.cpow;
+    if (al.lb == 7) st = launch_linear_lb<7>(al, rows, Lmax, lds_lin, s);
     else st = launch_linear_lb<6>(al, rows, Lmax, lds_lin, s);
     if (st || path == 2) return st;
     a.marked_only = 1;
