@@ -119,6 +119,17 @@ __device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t
 template <int KR>
 __device__ void select_staged(const unsigned long long* src, int cnt, int need, int c,
                               unsigned long long floor, int top, uint32_t* cst, int* ctr, int lane) {
+  if (KR == 1) {
+    // at most 64 keys, one per lane: each key's rank is the number of larger keys (the keys are
+    // distinct), counted over broadcast LDS reads; the `need` best have rank < need
+    const unsigned long long x = src[min(lane, cnt - 1)];
+    int rank = 0;
+    for (int m = 0; m < cnt; ++m) rank += src[m] > x ? 1 : 0;
+    const bool take = lane < cnt && rank < need;
+    const uint32_t pos = 0xffffffffu - (uint32_t)(x & 0xffffffffull);
+    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctr, lane);
+    return;
+  }
   unsigned long long x[KR];
 #pragma unroll
   for (int j = 0; j < KR; ++j) x[j] = src[min(j * 64 + lane, cnt - 1)];
