@@ -71,7 +71,8 @@ def log(*a):
 # (a stage may launch more than one kernel: its traffic is the sum)
 KERNELS = {"index_prep": ["index_prep_kernel"],
            "qgs_scan": ["qgs_scan_kernel"], "topk_select": ["topk_select_reg_kernel"],
-           "gate_fill": ["errorgate_kernel", "waterfill_kernel"], "topq": ["topq_row_kernel"],
+           "gate_fill": ["errorgate_kernel", "waterfill_kernel"],
+           "topq": ["topq_linear_kernel", "topq_row_kernel"],
            "residual_flash": ["resflash_kernel"]}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
 
