@@ -30,13 +30,12 @@ struct IdxArgs {
   const int* n_dev; int C; int G;
 };
 
-__device__ __forceinline__ void index_update_row(const IdxArgs& a, int r, int lane) {
+// the int8 QGS code of the token at n-1 of KV row r / G (written by query row r % G == 0)
+__device__ __forceinline__ void index_codes_row(const IdxArgs& a, int r, int lane) {
   const int kvr = r / a.G;
   const int pos = *a.n_dev - 1;
   const uint16_t* kp = a.K + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
-  const uint16_t* vp = a.V + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
   const float k_lo = oa::bf16_to_f32(kp[lane]), k_hi = oa::bf16_to_f32(kp[lane + 64]);
-  const float v_lo = oa::bf16_to_f32(vp[lane]), v_hi = oa::bf16_to_f32(vp[lane + 64]);
   if (r % a.G == 0) {
     const float* Ub = a.U + (long)kvr * OA_D * RQ;
     float ul[RQ], uh[RQ];
@@ -57,6 +56,17 @@ __device__ __forceinline__ void index_update_row(const IdxArgs& a, int r, int la
     }
     if (lane < RQ) a.codes[((long)kvr * a.Lmax_codes + pos) * RQ + lane] = mycode;
   }
+}
+
+// the token at n-1 joins query row r's nearest centroid: its asg / asg8 entry, the cluster's
+// Sk, Sk2, Sv, nb and recent-token list
+__device__ __forceinline__ void index_assign_row(const IdxArgs& a, int r, int lane) {
+  const int kvr = r / a.G;
+  const int pos = *a.n_dev - 1;
+  const uint16_t* kp = a.K + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
+  const uint16_t* vp = a.V + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
+  const float k_lo = oa::bf16_to_f32(kp[lane]), k_hi = oa::bf16_to_f32(kp[lane + 64]);
+  const float v_lo = oa::bf16_to_f32(vp[lane]), v_hi = oa::bf16_to_f32(vp[lane + 64]);
   // lane l holds rows l and l+64 of W (16 bf16 each, 32 contiguous bytes)
   const uint16_t* Wb = a.W + (long)r * OA_D * RC;
   float wl[RC], wh[RC];
@@ -116,21 +126,26 @@ __device__ __forceinline__ void index_update_row(const IdxArgs& a, int r, int la
 }
 
 __global__ void __launch_bounds__(64) index_update_kernel(IdxArgs a) {
-  index_update_row(a, blockIdx.x, threadIdx.x);
+  index_codes_row(a, blockIdx.x, threadIdx.x);
+  index_assign_row(a, blockIdx.x, threadIdx.x);
 }
 
 struct PrepArgs {
   const uint16_t* q; long q_stride; int8_t* limbs; int* fexp;
 };
 
-// one query-head row per 128-thread workgroup: wave 0 adds the token at n-1 to the index,
-// wave 1 projects the row's query (the two touch disjoint data)
-__global__ void __launch_bounds__(128) index_prep_kernel(IdxArgs a, PrepArgs p) {
-  if (threadIdx.x < 64)
-    index_update_row(a, blockIdx.x, threadIdx.x);
-  else
+// one query-head row per 192-thread workgroup: wave 0 adds the token at n-1 to the row's
+// clustering, wave 1 projects the row's query, wave 2 (of the first row of each KV row) writes
+// the token's code; the three touch disjoint data
+__global__ void __launch_bounds__(192) index_prep_kernel(IdxArgs a, PrepArgs p) {
+  const int w = threadIdx.x >> 6;
+  if (w == 0)
+    index_assign_row(a, blockIdx.x, threadIdx.x);
+  else if (w == 1)
     oa::qgs_prep_row(p.q, p.q_stride, a.U, a.scale, a.G, p.limbs, p.fexp, nullptr, blockIdx.x,
                      threadIdx.x - 64);
+  else if (blockIdx.x % a.G == 0)
+    index_codes_row(a, blockIdx.x, threadIdx.x - 128);
 }
 
 }  // namespace
@@ -178,6 +193,6 @@ extern "C" int oa_index_prep(const void* K, const void* V, long kv_stride_b, lon
   a.G = rows / kv_rows;
   PrepArgs p;
   p.q = (const uint16_t*)q; p.q_stride = q_stride; p.limbs = limbs; p.fexp = fexp;
-  hipLaunchKernelGGL(index_prep_kernel, dim3(rows), dim3(128), 0, (hipStream_t)stream, a, p);
+  hipLaunchKernelGGL(index_prep_kernel, dim3(rows), dim3(192), 0, (hipStream_t)stream, a, p);
   return OA_LAUNCH_STATUS();
 }
