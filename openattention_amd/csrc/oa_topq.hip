@@ -888,7 +888,8 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   // NaN in the row the span is NaN, scale 0 and every member in bin 0, which is still ordered)
   auto fbin = [&](uint32_t h) -> int { return min(NB - 1, (int)((key_float(h << 16) - smin) * scale)); };
 
-  // ---- L1: per-cluster histogram of the linear bins
+  // ---- L1: per-cluster histogram of the linear bins.  A single-segment row keeps each
+  // member's bin + 1 in place of its key head (0 still marks a non-member) for G
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
 #pragma unroll
@@ -898,6 +899,10 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
       int slot = (int)__umul24(cid(i), HS) + bn + (bn >> sb);
       asm volatile("" : "+v"(slot));
       atomicAdd(&s_hist[k ? slot : trash], 1);
+      if (!kMulti) {
+        const uint32_t v = k ? (uint32_t)bn + 1u : 0u;
+        kh[i >> 1] = (kh[i >> 1] & ~(0xffffu << (16 * (i & 1)))) | (v << (16 * (i & 1)));
+      }
     }
   }
   oa::lds_barrier();
@@ -960,8 +965,8 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
       for (int j = 0; j < CH; ++j) {
         if (i0 + j < PPT) {
           const int i = i0 + j;
-          const uint32_t k = hd(i);
-          const int bn = fbin(k);
+          const uint32_t k = hd(i);     // bin + 1 (single segment) or the key head
+          const int bn = kMulti ? fbin(k) : (int)k - 1;
           const int c = cid(i);
           if (k && bn >= (int)(sv[j] & 0xffffu))
             s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos_of(sg, i);
