@@ -480,7 +480,7 @@ def main():
         "qgs_scan": B * HKV * n_mid * 32,                      # int8 codes
         "topk_select": R * (-(-n_mid // 64)) * 4 + R * NSX * 4,  # tile maxima, sel out
         "gate_fill": R * Cn * (2 * D * 4 + 4) + R * NSX * D * 2,  # Sk, Sk2, n; K of sel
-        "topq": R * n_mid * (4 + 1) + R * E * 4,               # fp32 scores + byte ids; exp out
+        "topq": R * n_mid * (2 + 1) + R * E * 4,               # 16-bit score heads + byte ids; exp out
         "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * 2 * D * 4,  # K,V exact set; Sk, Sv
     }
     stage_alg = B * HKV * n_mid * 32 + R * (NSX + E) * 2 * D * 2 + R * Cn * (3 * D * 4 + 4)

@@ -111,6 +111,18 @@ int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8
                 const int* n_dev, int ns, int nl, void* stream);
 
 /*
+ * oa_qgs_scan writing the 16-bit head of every score's order-preserving key (the key's top 16
+ * bits: non-decreasing in the score; -inf is 0x007f) instead of the fp32 score: half the
+ * bytes, and all that the top-q binning uses.  TM is the same exact fp32 tile maximum.  The
+ * same stage as oa_qgs_scan (_k_qgs_scan_tm, inference/graph_runner.py:100-120); the reduced
+ * score rows have no counterpart in the reference.
+ *   H (rows, h_stride >= ceil(Lmax/64)*64, a multiple of 4) 16-bit, 8-byte aligned.
+ */
+int oa_qgs_scan_heads(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
+                      const int* fexp, uint16_t* H, long h_stride, float* TM, long tm_stride,
+                      const int* n_dev, int ns, int nl, void* stream);
+
+/*
  * Exact top-k per row (ties to the lower position) among the k tiles with the largest
  * maxima; sel = [0..ns) ++ [n-nl..n) ++ top; the selected scores in S are set to -inf.
  * Replaces _k_select (inference/graph_runner.py:123-159).
@@ -118,6 +130,18 @@ int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8
 int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int rows,
                    int ntiles, int32_t* sel, long sel_stride, const int* n_dev, int ns, int nl,
                    int k_top, void* stream);
+
+/*
+ * oa_topk_select over key-head rows (oa_qgs_scan_heads): the candidate tiles' exact scores are
+ * recomputed from the codes with the scan's integer arithmetic, so sel is the same; the
+ * selected tokens' heads are set to that of -inf.  Replaces _k_select
+ * (inference/graph_runner.py:123-159) in the head pipeline.
+ *   codes (kv_rows, Lmax, 32) int8, 16-byte aligned; limbs (kv_rows, 16, 32); fexp (rows,).
+ */
+int oa_topk_select_heads(uint16_t* H, long h_stride, const float* TM, long tm_stride, int rows,
+                         int ntiles, int32_t* sel, long sel_stride, const int* n_dev, int ns,
+                         int nl, int k_top, const int8_t* codes, int kv_rows, int Lmax,
+                         const int8_t* limbs, const int* fexp, void* stream);
 
 /*
  * ErrorGate: wl1 score and tail count of every cluster (pooled sums minus the selected
@@ -176,6 +200,22 @@ int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride
 int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
                  const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
                  const int* n_dev, int path, void* stream);
+
+/*
+ * Within-cluster top-q over key-head rows (oa_qgs_scan_heads, oa_topk_select_heads): the
+ * linear-bin kernel bins the heads, recomputes exact scores from the codes for the staged
+ * members, and writes a row it cannot resolve into S32 as exact fp32 scores for the key-prefix
+ * kernel.  Same result as oa_topq on the fp32 scores.  Replaces _k_topq_d2 + _topq_core
+ * (inference/ours_graph.py:93-166) in the head pipeline.  path 0: as described; 2: the
+ * linear-bin kernel alone (rows it leaves hold -2 in exp_idx[row][0]); 3 (tests): every row
+ * through S32 and the key-prefix kernel.
+ *   H as oa_qgs_scan_heads; S32 (rows, s32_stride >= round_up(Lmax, 4)) fp32, 16-byte aligned;
+ *   rows = 4 * kv_rows.
+ */
+int oa_topq_heads(const uint16_t* H, long h_stride, const uint8_t* asg8, long asg8_stride,
+                  const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
+                  const int* n_dev, const int8_t* codes, int kv_rows, const int8_t* limbs,
+                  const int* fexp, float* S32, long s32_stride, int path, void* stream);
 
 /*
  * Residual proxies: kbar', vbar' (bf16, rows x C x 128) and ln n' (fp32, -inf = none) of the

@@ -17,6 +17,7 @@
 // them exactly in fp64 (all values are integers below 2^53).
 // Top-k ties break to the lower position (graph_runner.py:127-151 rule).
 #include "oa_common.h"
+#include "oa_score.h"
 #include "oa_prep.h"
 
 typedef int oa_v4i __attribute__((ext_vector_type(4)));
@@ -44,9 +45,11 @@ __global__ void __launch_bounds__(64) qgs_prep_kernel(const uint16_t* __restrict
 constexpr int kScanThreads = 256;
 constexpr int kTokWG = 1024;
 
+// HEADS: the score rows hold 16-bit key heads (oa::score_head) instead of fp32 scores
+template <bool HEADS>
 __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
     const int8_t* __restrict__ codes, int Lmax, const int8_t* __restrict__ limbs,
-    const int* __restrict__ fexp, float* __restrict__ S, long s_stride, float* __restrict__ TM,
+    const int* __restrict__ fexp, void* __restrict__ Sv, long s_stride, float* __restrict__ TM,
     long tm_stride, const int* __restrict__ n_dev, int ns, int nl) {
   const int kvr = blockIdx.y;
   const int wave = threadIdx.x >> 6;
@@ -59,7 +62,8 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
   const long a_op = *reinterpret_cast<const long*>(limbs + (long)kvr * 16 * RQ + nn * RQ + kg * 8);
   const int row = kvr * GQ + kg;
   const double inv = ldexp(1.0, -fexp[row]);
-  float* Srow = S + (long)row * s_stride;
+  float* Srow = static_cast<float*>(Sv) + (long)row * s_stride;
+  uint16_t* Hrow = static_cast<uint16_t*>(Sv) + (long)row * s_stride;
   float* TMrow = TM + (long)row * tm_stride;
   const int8_t* cb = codes + (long)kvr * Lmax * RQ;
 
@@ -86,7 +90,8 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
       float sc = (float)(s * inv);
       const int tok = tile * 64 + b * 16 + nn;
       if (tok < ns || tok >= dead_hi) sc = -INFINITY;
-      Srow[tok] = sc;
+      if (HEADS) Hrow[tok] = oa::score_head(sc);
+      else Srow[tok] = sc;
       tmax = fmaxf(tmax, sc);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 8, 64));
@@ -110,11 +115,45 @@ __device__ __forceinline__ unsigned long long tile_key(float v, int t) {
   return ((unsigned long long)oa::float_key(v) << 32) | (0xffffffffu - (unsigned)t);
 }
 
-__global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, long s_stride,
+// With HEADS the score rows hold 16-bit key heads: the candidate tiles' exact scores are
+// recomputed from the codes (oa::qgs_score, the scan's arithmetic), and the selected tokens'
+// heads are set to that of -inf.
+struct Rescore {
+  const int8_t* codes; long lmax;   // (BH, Lmax, 32)
+  const int8_t* limbs;              // (BH, 16, 32)
+  const int* fexp;                  // (R,)
+};
+
+// candidate score of position pos of a query-head row (sink, local and unwritten: -inf)
+template <bool HEADS>
+__device__ __forceinline__ float cand_score(const void* Sv, long s_stride, int row, int pos, int ns,
+                                            int dead_hi, const Rescore& rs, const int* lw,
+                                            double inv) {
+  if (!HEADS) return static_cast<const float*>(Sv)[(long)row * s_stride + pos];
+  if (pos < ns || pos >= dead_hi) return -INFINITY;
+  return oa::qgs_score(rs.codes, rs.lmax, row / GQ, pos, lw, inv);
+}
+template <bool HEADS>
+__device__ __forceinline__ void mark_selected(void* Sv, long s_stride, int row, int pos) {
+  if (HEADS) static_cast<uint16_t*>(Sv)[(long)row * s_stride + pos] = oa::kNegInfHead;
+  else static_cast<float*>(Sv)[(long)row * s_stride + pos] = -INFINITY;
+}
+// the row's limb words (HEADS only) and 2^-F
+template <bool HEADS>
+__device__ __forceinline__ double load_limbs(const Rescore& rs, int row, int* lw) {
+  if (!HEADS) return 0.0;
+  const int* p = oa::limb_words(rs.limbs, row / GQ, row % GQ);
+#pragma unroll
+  for (int w = 0; w < 32; ++w) lw[w] = p[w];
+  return ldexp(1.0, -rs.fexp[row]);
+}
+
+template <bool HEADS>
+__global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, long s_stride,
                                                          const float* __restrict__ TM, long tm_stride,
                                                          int ntiles, int32_t* __restrict__ sel,
                                                          long sel_stride, const int* __restrict__ n_dev,
-                                                         int ns, int nl, int k_top) {
+                                                         int ns, int nl, int k_top, Rescore rs) {
   __shared__ float s_tm[kMaxTilesLds];
   __shared__ int s_tile[kMaxTop];
   __shared__ float s_sc[kMaxTop * 64];
@@ -122,7 +161,8 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
   const int n = *n_dev;
-  float* Srow = S + (long)row * s_stride;
+  int lw[HEADS ? 32 : 1];
+  const double inv = load_limbs<HEADS>(rs, row, lw);
   const float NaN = __uint_as_float(0x7fc00000u);
   // lane l owns tiles l, l+64, ...; it caches the best key among its untaken tiles.  Loads go
   // out 16 per lane at a time (clamped addresses), so a row's tile maxima arrive in one or two
@@ -164,7 +204,9 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
   for (int j0 = 0; j0 < k_top; j0 += 16) {
     float v[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = Srow[(long)s_tile[min(j0 + j, k_top - 1)] * 64 + lane];
+    for (int j = 0; j < 16; ++j)
+      v[j] = cand_score<HEADS>(Sv, s_stride, row, s_tile[min(j0 + j, k_top - 1)] * 64 + lane, ns,
+                               n - nl, rs, lw, inv);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       if (j0 + j < k_top) {
@@ -195,24 +237,25 @@ __global__ void __launch_bounds__(64) topk_select_kernel(float* __restrict__ S, 
   if (lane < ns) sr[lane] = lane;
   if (lane < nl) sr[ns + lane] = n - nl + lane;
   for (int i = lane; i < k_top; i += 64) sr[ns + nl + i] = s_top[i];
-  for (int i = lane; i < k_top; i += 64) Srow[s_top[i]] = -INFINITY;
+  for (int i = lane; i < k_top; i += 64) mark_selected<HEADS>(Sv, s_stride, row, s_top[i]);
 }
 
 // Register variant for rows of at most 64*TPL tiles and k_top <= KR: lane l keeps the keys of
 // tiles l, l+64, ... and later of column l of the k chosen tiles in registers; every extraction
 // step is one wave maximum (DPP) and an in-register update by the owning lane.
-template <int TPL, int KR>
-__global__ void __launch_bounds__(64) topk_select_reg_kernel(float* __restrict__ S, long s_stride,
+template <int TPL, int KR, bool HEADS>
+__global__ void __launch_bounds__(64) topk_select_reg_kernel(void* __restrict__ Sv, long s_stride,
                                                              const float* __restrict__ TM,
                                                              long tm_stride, int ntiles,
                                                              int32_t* __restrict__ sel,
                                                              long sel_stride,
                                                              const int* __restrict__ n_dev, int ns,
-                                                             int nl, int k_top) {
+                                                             int nl, int k_top, Rescore rs) {
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
   const int n = *n_dev;
-  float* Srow = S + (long)row * s_stride;
+  int lw[HEADS ? 32 : 1];
+  const double inv = load_limbs<HEADS>(rs, row, lw);
   unsigned long long tk[TPL];
   float tv[TPL];
 #pragma unroll
@@ -244,7 +287,7 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(float* __restrict__
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
     const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
-    cv[j] = Srow[(long)tj * 64 + lane];
+    cv[j] = cand_score<HEADS>(Sv, s_stride, row, tj * 64 + lane, ns, n - nl, rs, lw, inv);
   }
   mine = 0ull;
 #pragma unroll
@@ -272,7 +315,7 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(float* __restrict__
   if (lane < nl) sr[ns + lane] = n - nl + lane;
   if (lane < k_top) {
     sr[ns + nl + lane] = my_pos;
-    Srow[my_pos] = -INFINITY;
+    mark_selected<HEADS>(Sv, s_stride, row, my_pos);
   }
 }
 
@@ -287,36 +330,75 @@ extern "C" int oa_qgs_prep(const void* q, long q_stride, const float* U, const f
   return OA_LAUNCH_STATUS();
 }
 
-extern "C" int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
-                           const int* fexp, float* S, long s_stride, float* TM, long tm_stride,
-                           const int* n_dev, int ns, int nl, void* stream) {
+namespace {
+template <bool HEADS>
+int launch_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
+                const int* fexp, void* S, long s_stride, float* TM, long tm_stride,
+                const int* n_dev, int ns, int nl, void* stream) {
   if (rank != RQ || kv_rows <= 0 || Lmax <= 0) return OA_EINVAL;
   const int ntile = (Lmax + 63) / 64;
   if (s_stride < (long)ntile * 64 || tm_stride < ntile || ns < 0 || nl < 0) return OA_EINVAL;
   dim3 grid((Lmax + kTokWG - 1) / kTokWG, kv_rows);
-  hipLaunchKernelGGL(qgs_scan_kernel, grid, dim3(kScanThreads), 0, (hipStream_t)stream, codes, Lmax,
-                     limbs, fexp, S, s_stride, TM, tm_stride, n_dev, ns, nl);
+  hipLaunchKernelGGL(qgs_scan_kernel<HEADS>, grid, dim3(kScanThreads), 0, (hipStream_t)stream,
+                     codes, Lmax, limbs, fexp, S, s_stride, TM, tm_stride, n_dev, ns, nl);
   return OA_LAUNCH_STATUS();
 }
 
-extern "C" int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int rows,
-                              int ntiles, int32_t* sel, long sel_stride, const int* n_dev, int ns,
-                              int nl, int k_top, void* stream) {
+template <bool HEADS>
+int launch_topk(void* S, long s_stride, const float* TM, long tm_stride, int rows, int ntiles,
+                int32_t* sel, long sel_stride, const int* n_dev, int ns, int nl, int k_top,
+                Rescore rs, void* stream) {
   if (rows <= 0 || ntiles <= 0 || ntiles > kMaxTilesLds || k_top < 0 || k_top > kMaxTop ||
       k_top > ntiles || ns < 0 || nl < 0 || ns > 64 || nl > 64 || sel_stride < ns + nl + k_top)
     return OA_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   // register variants sized to the row: TPL tiles per lane, KR candidate columns
 #define OA_TOPK_REG(T, KK)                                                                     \
-  hipLaunchKernelGGL((topk_select_reg_kernel<T, KK>), dim3(rows), dim3(64), 0, st, S, s_stride,  \
-                     TM, tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top)
+  hipLaunchKernelGGL((topk_select_reg_kernel<T, KK, HEADS>), dim3(rows), dim3(64), 0, st, S,    \
+                     s_stride, TM, tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top, rs)
   const int tpl = (ntiles + 63) / 64;
   if (k_top <= 9 && tpl <= 9) OA_TOPK_REG(9, 9);
   else if (k_top <= 16 && tpl <= 16) OA_TOPK_REG(16, 16);
   else if (k_top <= 16 && tpl <= 32) OA_TOPK_REG(32, 16);
   else
-    hipLaunchKernelGGL(topk_select_kernel, dim3(rows), dim3(64), 0, st, S, s_stride, TM, tm_stride,
-                       ntiles, sel, sel_stride, n_dev, ns, nl, k_top);
+    hipLaunchKernelGGL(topk_select_kernel<HEADS>, dim3(rows), dim3(64), 0, st, S, s_stride, TM,
+                       tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top, rs);
 #undef OA_TOPK_REG
   return OA_LAUNCH_STATUS();
+}
+}  // namespace
+
+extern "C" int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
+                           const int* fexp, float* S, long s_stride, float* TM, long tm_stride,
+                           const int* n_dev, int ns, int nl, void* stream) {
+  return launch_scan<false>(codes, kv_rows, Lmax, rank, limbs, fexp, S, s_stride, TM, tm_stride,
+                            n_dev, ns, nl, stream);
+}
+
+extern "C" int oa_qgs_scan_heads(const int8_t* codes, int kv_rows, int Lmax, int rank,
+                                 const int8_t* limbs, const int* fexp, uint16_t* H, long h_stride,
+                                 float* TM, long tm_stride, const int* n_dev, int ns, int nl,
+                                 void* stream) {
+  if (!H || (reinterpret_cast<uintptr_t>(H) & 7) || h_stride % 4) return OA_EINVAL;
+  return launch_scan<true>(codes, kv_rows, Lmax, rank, limbs, fexp, H, h_stride, TM, tm_stride,
+                           n_dev, ns, nl, stream);
+}
+
+extern "C" int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int rows,
+                              int ntiles, int32_t* sel, long sel_stride, const int* n_dev, int ns,
+                              int nl, int k_top, void* stream) {
+  return launch_topk<false>(S, s_stride, TM, tm_stride, rows, ntiles, sel, sel_stride, n_dev, ns,
+                            nl, k_top, Rescore{nullptr, 0, nullptr, nullptr}, stream);
+}
+
+extern "C" int oa_topk_select_heads(uint16_t* H, long h_stride, const float* TM, long tm_stride,
+                                    int rows, int ntiles, int32_t* sel, long sel_stride,
+                                    const int* n_dev, int ns, int nl, int k_top,
+                                    const int8_t* codes, int kv_rows, int Lmax,
+                                    const int8_t* limbs, const int* fexp, void* stream) {
+  if (!H || !codes || !limbs || !fexp || kv_rows <= 0 || rows != kv_rows * GQ || Lmax <= 0 ||
+      (reinterpret_cast<uintptr_t>(codes) & 15) || (reinterpret_cast<uintptr_t>(limbs) & 3))
+    return OA_EINVAL;
+  return launch_topk<true>(H, h_stride, TM, tm_stride, rows, ntiles, sel, sel_stride, n_dev, ns,
+                           nl, k_top, Rescore{codes, (long)Lmax, limbs, fexp}, stream);
 }

@@ -49,6 +49,7 @@
 #include <algorithm>
 
 #include "oa_common.h"
+#include "oa_score.h"
 
 namespace {
 
@@ -79,6 +80,13 @@ struct TopqArgs {
   int gcap;        // staged-key capacity (u64 entries)
   int cpow;        // power of two >= E: chosen-word list and the P6 sort
   int marked_only; // key-prefix kernel: only rows the linear-bin kernel marked kRowMarked
+  // linear-bin kernel over 16-bit key heads (oa_topq_heads): the head rows, and what recomputes
+  // exact scores (the staged members', and a whole row into S32 when it is left to the
+  // key-prefix kernel, which then reads S32 as its S)
+  const uint16_t* H; long h_stride;
+  const int8_t* codes; long lmax_codes; const int8_t* limbs; const int* fexp;
+  float* S32; long s32_stride;
+  int force_mark;  // tests: every row is left to the key-prefix kernel
 };
 
 // the float whose order-preserving key is k (inverse of oa::float_key)
@@ -767,7 +775,10 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 // members to the staged keys; P5 and P6 are shared with the key-prefix kernel.  A row whose
 // staged members do not fit the staging space is marked (exp_idx[row][0] = kRowMarked) and left
 // to the key-prefix kernel, launched next over the marked rows only.
-template <int PPT, int LB>
+//
+// HEADS: the score rows hold 16-bit key heads (oa_qgs_scan_heads), which are all the kernel
+// keeps of a score anyway; exact scores come from the codes (oa::qgs_score).
+template <int PPT, int LB, bool HEADS>
 // up to 64 VGPRs for the single-segment instantiations: two workgroups (rows) per unit
 __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
@@ -784,6 +795,7 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   __shared__ int s_tpre[kMaxC + 1];
   __shared__ int s_gused, s_fail;
   __shared__ uint32_t s_rlo[kWaves], s_rhi[kWaves];
+  __shared__ int s_lw[HEADS ? 32 : 1];    // the row's limb words (exact scores)
   constexpr int NB = 1 << LB;
   constexpr int HS = NB + 16;
   constexpr int sb = LB - 4;
@@ -801,8 +813,10 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   const int trash = C * HS + lane;
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
+  const uint16_t* hrow = a.H + (long)row * a.h_stride;
   const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
   int32_t* erow = a.exp_idx + (long)row * E;
+  const int kvr = row / 4;
 
   constexpr int SEG = kThreads * PPT;
   constexpr int NG = PPT / 4;
@@ -822,12 +836,18 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const int p = min(sg * SEG + g * 4096 + 4 * tid, last4);
-      const float4 v = *reinterpret_cast<const float4*>(srow + p);
       cp[g] = *reinterpret_cast<const uint32_t*>(arow + p);
-      kk[4 * g] = __float_as_uint(v.x);
-      kk[4 * g + 1] = __float_as_uint(v.y);
-      kk[4 * g + 2] = __float_as_uint(v.z);
-      kk[4 * g + 3] = __float_as_uint(v.w);
+      if (HEADS) {
+        const uint2 v = *reinterpret_cast<const uint2*>(hrow + p);
+        kh[2 * g] = v.x;
+        kh[2 * g + 1] = v.y;
+      } else {
+        const float4 v = *reinterpret_cast<const float4*>(srow + p);
+        kk[4 * g] = __float_as_uint(v.x);
+        kk[4 * g + 1] = __float_as_uint(v.y);
+        kk[4 * g + 2] = __float_as_uint(v.z);
+        kk[4 * g + 3] = __float_as_uint(v.w);
+      }
     }
   };
   auto keys = [&](int sg) {
@@ -838,9 +858,15 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int i = 2 * j + u;
-        const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
-        const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
-        h2 |= (q ? key >> 16 : 0u) << (16 * u);
+        if (HEADS) {
+          const uint32_t h = (kh[j] >> (16 * u)) & 0xffffu;
+          const bool q = (i >> 2) * 4096 + (i & 3) < lim && h > oa::kNegInfHead;
+          h2 |= (q ? h : 0u) << (16 * u);
+        } else {
+          const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
+          const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
+          h2 |= (q ? key >> 16 : 0u) << (16 * u);
+        }
       }
       kh[j] = h2;
     }
@@ -858,7 +884,8 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
     s_sel[c] = 0xffffffffu; s_mode[c] = kModeNone; s_goff[c] = 0; s_gcur[c] = 0; s_ccur[c] = 0;
   }
   for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
-  if (tid == 0) { s_gused = 0; s_fail = 0; }
+  if (tid == 0) { s_gused = 0; s_fail = a.force_mark; }
+  if (HEADS && tid < 32) s_lw[tid] = oa::limb_words(a.limbs, kvr, row % 4)[tid];
 
   // ---- R: the range of the qualifying members' score keys
   uint32_t klo = 0xffffffffu, khi = 0u;
@@ -945,6 +972,13 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   }
   oa::lds_barrier();
   if (s_fail) {                  // uniform: the key-prefix kernel takes the row
+    if (HEADS) {                 // ... from exact fp32 scores: the row is recomputed into S32
+      const double inv = ldexp(1.0, -a.fexp[row]);
+      float* orow = a.S32 + (long)row * a.s32_stride;
+      for (int p = tid; p < n; p += kThreads)
+        orow[p] = hrow[p] > oa::kNegInfHead ? oa::qgs_score_lds(a.codes, a.lmax_codes, kvr, p, s_lw, inv)
+                                            : -INFINITY;
+    }
     if (tid == 0) erow[0] = kRowMarked;
     return;
   }
@@ -977,11 +1011,16 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
     }
   }
   oa::lds_barrier();
-  // the staged members' exact keys, from S (they fill [0, s_gused) of the staged keys)
-  for (int j = tid; j < s_gused; j += kThreads) {
-    const unsigned long long e = s_g[j];
-    const int p = (int)(0xffffffffu - (uint32_t)e);
-    s_g[j] = key64(oa::float_key(srow[p]), p);
+  // the staged members' exact keys, from S or recomputed from the codes (they fill [0, s_gused)
+  // of the staged keys)
+  {
+    const double inv = HEADS ? ldexp(1.0, -a.fexp[row]) : 0.0;
+    for (int j = tid; j < s_gused; j += kThreads) {
+      const unsigned long long e = s_g[j];
+      const int p = (int)(0xffffffffu - (uint32_t)e);
+      const float sc = HEADS ? oa::qgs_score_lds(a.codes, a.lmax_codes, kvr, p, s_lw, inv) : srow[p];
+      s_g[j] = key64(oa::float_key(sc), p);
+    }
   }
   oa::lds_barrier();
 
@@ -1008,41 +1047,32 @@ int launch_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStream_t s) 
   return launch_row<44, LB>(a, rows, lds, s);
 }
 
-template <int PPT, int LB>
+template <int PPT, int LB, bool HEADS>
 int launch_linear(const TopqArgs& a, int rows, size_t lds, hipStream_t s) {
-  const hipError_t e = hipFuncSetAttribute((const void*)topq_linear_kernel<PPT, LB>,
+  const hipError_t e = hipFuncSetAttribute((const void*)topq_linear_kernel<PPT, LB, HEADS>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((topq_linear_kernel<PPT, LB>), dim3(rows), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((topq_linear_kernel<PPT, LB, HEADS>), dim3(rows), dim3(kThreads), lds, s, a);
   return OA_LAUNCH_STATUS();
 }
 
-template <int LB>
+template <int LB, bool HEADS>
 int launch_linear_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStream_t s) {
-  if (Lmax <= kThreads * 8) return launch_linear<8, LB>(a, rows, lds, s);
-  if (Lmax <= kThreads * 16) return launch_linear<16, LB>(a, rows, lds, s);
-  if (Lmax <= kThreads * 36) return launch_linear<36, LB>(a, rows, lds, s);
-  return launch_linear<44, LB>(a, rows, lds, s);
+  if (Lmax <= kThreads * 8) return launch_linear<8, LB, HEADS>(a, rows, lds, s);
+  if (Lmax <= kThreads * 16) return launch_linear<16, LB, HEADS>(a, rows, lds, s);
+  if (Lmax <= kThreads * 36) return launch_linear<36, LB, HEADS>(a, rows, lds, s);
+  return launch_linear<44, LB, HEADS>(a, rows, lds, s);
 }
 
 }  // namespace
 
-// path 0: the linear-bin kernel on every row, then the key-prefix kernel on the rows it
-// marked; path 1: the key-prefix kernel on every row; path 2: the linear-bin kernel alone (a
-// row it leaves to the key-prefix kernel keeps the mark kRowMarked in exp_idx[row][0])
-extern "C" int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
-                            const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
-                            const int* n_dev, int path, void* stream) {
-  const long lmax4 = ((long)Lmax + 3) & ~3L;
-  if (rows <= 0 || C <= 0 || C > kMaxC || E < 0 || E > kMaxE || Lmax <= 0 || Lmax >= kMaxPos ||
-      !S || !asg8 || !quota || !n_dev || (E > 0 && !exp_idx) || s_stride % 4 || asg8_stride % 4 ||
-      s_stride < lmax4 || asg8_stride < lmax4 || (reinterpret_cast<uintptr_t>(S) & 15) ||
-      (reinterpret_cast<uintptr_t>(asg8) & 3) || path < 0 || path > 2)
-    return OA_EINVAL;
-  if (E == 0) return 0;
-  TopqArgs a;
-  a.S = S; a.s_stride = s_stride; a.asg8 = asg8; a.a_stride = asg8_stride; a.quota = quota;
-  a.C = C; a.E = E; a.n_dev = n_dev; a.exp_idx = exp_idx;
+namespace {
+
+// the launch sequence shared by oa_topq_path and oa_topq_heads: `a` carries the pointers; the
+// sizes are set here.  lin: run the linear-bin kernel (heads: its 16-bit variant); pre: run
+// the key-prefix kernel (after lin: on the rows lin marked only)
+int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool heads, bool pre,
+                hipStream_t s) {
   // bits per histogram level: 8, 7 or 6, so that C * (2^lb + 16) ints stay near 64 KiB
   a.lb = C <= 64 ? 8 : (C <= 128 ? 7 : 6);
   a.cpow = 4;                   // >= 4: the LDS rows are cleared and scanned 4 words at a time
@@ -1057,10 +1087,8 @@ extern "C" int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, 
   a.gcap = std::min(a.hwords / 2, a.ucap - E);             // the final gathering fits in ucap
   if (a.gcap < 64) return OA_EINVAL;
   const size_t lds = 8 * (size_t)(a.ucap + 64) + 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
-  hipStream_t s = (hipStream_t)stream;
-  int st = 0;
   a.marked_only = 0;
-  if (path != 1) {
+  if (lin) {
     // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words.
     // 7 bits for C <= 64, else 6: up to C = 128 two workgroups' LDS fits one unit
     TopqArgs al = a;
@@ -1068,9 +1096,12 @@ extern "C" int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, 
     al.hwords = (int)((std::max<long>((long)C * ((1 << al.lb) + 16) + 64, a.cpow) + 3) & ~3L);
     al.gcap = al.hwords / 2;
     const size_t lds_lin = 4 * (size_t)al.hwords + 4 * (size_t)a.cpow;
-    if (al.lb == 7) st = launch_linear_lb<7>(al, rows, Lmax, lds_lin, s);
-    else st = launch_linear_lb<6>(al, rows, Lmax, lds_lin, s);
-    if (st || path == 2) return st;
+    int st;
+    if (heads) st = al.lb == 7 ? launch_linear_lb<7, true>(al, rows, Lmax, lds_lin, s)
+                               : launch_linear_lb<6, true>(al, rows, Lmax, lds_lin, s);
+    else st = al.lb == 7 ? launch_linear_lb<7, false>(al, rows, Lmax, lds_lin, s)
+                         : launch_linear_lb<6, false>(al, rows, Lmax, lds_lin, s);
+    if (st || !pre) return st;
     a.marked_only = 1;
   }
   if (a.lb == 8) return launch_lb<8>(a, rows, Lmax, lds, s);
@@ -1078,9 +1109,60 @@ extern "C" int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, 
   return launch_lb<6>(a, rows, Lmax, lds, s);
 }
 
+bool topq_sizes_ok(int rows, int C, int E, int Lmax) {
+  return rows > 0 && C > 0 && C <= kMaxC && E >= 0 && E <= kMaxE && Lmax > 0 && Lmax < kMaxPos;
+}
+
+}  // namespace
+
+// path 0: the linear-bin kernel on every row, then the key-prefix kernel on the rows it
+// marked; path 1: the key-prefix kernel on every row; path 2: the linear-bin kernel alone (a
+// row it leaves to the key-prefix kernel keeps the mark kRowMarked in exp_idx[row][0])
+extern "C" int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
+                            const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
+                            const int* n_dev, int path, void* stream) {
+  const long lmax4 = ((long)Lmax + 3) & ~3L;
+  if (!topq_sizes_ok(rows, C, E, Lmax) || !S || !asg8 || !quota || !n_dev ||
+      (E > 0 && !exp_idx) || s_stride % 4 || asg8_stride % 4 || s_stride < lmax4 ||
+      asg8_stride < lmax4 || (reinterpret_cast<uintptr_t>(S) & 15) ||
+      (reinterpret_cast<uintptr_t>(asg8) & 3) || path < 0 || path > 2)
+    return OA_EINVAL;
+  if (E == 0) return 0;
+  TopqArgs a = {};
+  a.S = S; a.s_stride = s_stride; a.asg8 = asg8; a.a_stride = asg8_stride; a.quota = quota;
+  a.C = C; a.E = E; a.n_dev = n_dev; a.exp_idx = exp_idx;
+  return topq_launch(a, rows, C, Lmax, E, path != 1, false, path != 2, (hipStream_t)stream);
+}
+
 extern "C" int oa_topq(const float* S, long s_stride, const uint8_t* asg8, long asg8_stride,
                        const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
                        const int* n_dev, void* stream) {
   return oa_topq_path(S, s_stride, asg8, asg8_stride, quota, rows, C, Lmax, exp_idx, E, n_dev, 0,
                       stream);
+}
+
+// over 16-bit key heads (oa_qgs_scan_heads + oa_topk_select_heads).  path 0: as oa_topq (rows
+// the linear-bin kernel leaves are recomputed into S32 and selected by the key-prefix kernel);
+// path 2: the linear-bin kernel alone; path 3: every row is left to the key-prefix kernel
+extern "C" int oa_topq_heads(const uint16_t* H, long h_stride, const uint8_t* asg8,
+                             long asg8_stride, const float* quota, int rows, int C, int Lmax,
+                             int32_t* exp_idx, int E, const int* n_dev, const int8_t* codes,
+                             int kv_rows, const int8_t* limbs, const int* fexp, float* S32,
+                             long s32_stride, int path, void* stream) {
+  const long lmax4 = ((long)Lmax + 3) & ~3L;
+  if (!topq_sizes_ok(rows, C, E, Lmax) || !H || !asg8 || !quota || !n_dev || !codes || !limbs ||
+      !fexp || !S32 || (E > 0 && !exp_idx) || kv_rows <= 0 || rows != kv_rows * 4 ||
+      h_stride % 4 || asg8_stride % 4 || s32_stride % 4 || h_stride < lmax4 ||
+      asg8_stride < lmax4 || s32_stride < lmax4 || (reinterpret_cast<uintptr_t>(H) & 7) ||
+      (reinterpret_cast<uintptr_t>(S32) & 15) || (reinterpret_cast<uintptr_t>(asg8) & 3) ||
+      (reinterpret_cast<uintptr_t>(codes) & 15) || (reinterpret_cast<uintptr_t>(limbs) & 3) ||
+      !(path == 0 || path == 2 || path == 3))
+    return OA_EINVAL;
+  if (E == 0) return 0;
+  TopqArgs a = {};
+  a.S = S32; a.s_stride = s32_stride; a.asg8 = asg8; a.a_stride = asg8_stride; a.quota = quota;
+  a.C = C; a.E = E; a.n_dev = n_dev; a.exp_idx = exp_idx;
+  a.H = H; a.h_stride = h_stride; a.codes = codes; a.lmax_codes = Lmax; a.limbs = limbs;
+  a.fexp = fexp; a.S32 = S32; a.s32_stride = s32_stride; a.force_mark = path == 3;
+  return topq_launch(a, rows, C, Lmax, E, true, true, path != 2, (hipStream_t)stream);
 }

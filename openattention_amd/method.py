@@ -104,6 +104,9 @@ class OursHIP(Method):
         i32 = dict(device=dev, dtype=torch.int32)
         self.limbs = torch.zeros(BH, 16, 32, device=dev, dtype=torch.int8)
         self.fexp = torch.zeros(R, **i32)
+        # 16-bit key heads of the scores (what the scan writes and top-k / top-q read); S holds
+        # exact fp32 scores only for rows top-q leaves to its key-prefix kernel
+        self.H = torch.empty(R, self.SW, device=dev, dtype=torch.int16)
         self.S = torch.empty(R, self.SW, **f32)
         self.TM = torch.empty(R, self.ntiles, **f32)
         self.score = torch.empty(R, self.Cn, **f32)
@@ -171,14 +174,16 @@ class OursHIP(Method):
         mark("start")
         ops.index_prep(K, V, st, C.n_dev, RMAX, qr, self.limbs, self.fexp)
         mark("index_prep")
-        ops.qgs_scan(st.codes, self.limbs, self.fexp, self.S, self.TM, C.n_dev, ns, nl)
+        ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM, C.n_dev, ns, nl)
         mark("qgs_scan")
-        ops.topk_select(self.S, self.TM, sel, C.n_dev, ns, nl, k_top)
+        ops.topk_select_heads(self.H, self.TM, sel, C.n_dev, ns, nl, k_top, st.codes, self.limbs,
+                              self.fexp)
         mark("topk_select")
         ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota,
                       SC, self.E)
         mark("gate_fill")
-        ops.topq(self.S, st.asg8, self.quota, self.exp_idx, C.n_dev)
+        ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, C.n_dev, st.codes, self.limbs,
+                       self.fexp, self.S)
         mark("topq")
         if self.fused:
             ops.residual_flash(qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk,
@@ -202,11 +207,14 @@ class OursHIP(Method):
             Sk2=st.Sk2[rs], Sv=st.Sv[rs], reclist=st.reclist[rs], reccnt=st.reccnt[rs])
         Kg, Vg, qg, selg = K[ks], V[ks], qr[rs], sel[rs]
         ops.index_prep(Kg, Vg, sub, C.n_dev, RMAX, qg, self.limbs[ks], self.fexp[rs])
-        ops.qgs_scan(sub.codes, self.limbs[ks], self.fexp[rs], self.S[rs], self.TM[rs], C.n_dev, ns, nl)
-        ops.topk_select(self.S[rs], self.TM[rs], selg, C.n_dev, ns, nl, k_top)
+        ops.qgs_scan_heads(sub.codes, self.limbs[ks], self.fexp[rs], self.H[rs], self.TM[rs],
+                           C.n_dev, ns, nl)
+        ops.topk_select_heads(self.H[rs], self.TM[rs], selg, C.n_dev, ns, nl, k_top, sub.codes,
+                              self.limbs[ks], self.fexp[rs])
         ops.gate_fill(qg, Kg, sub.asg, selg, sub.Sk, sub.Sk2, sub.nb, self.score[rs], self.n_t[rs],
                       self.quota[rs], SC, self.E)
-        ops.topq(self.S[rs], sub.asg8, self.quota[rs], self.exp_idx[rs], C.n_dev)
+        ops.topq_heads(self.H[rs], sub.asg8, self.quota[rs], self.exp_idx[rs], C.n_dev, sub.codes,
+                       self.limbs[ks], self.fexp[rs], self.S[rs])
         if self.fused:
             ops.residual_flash(qg, Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs],
                                self.n_t[rs], sub.Sk, sub.Sv, self.out[rs], SC)

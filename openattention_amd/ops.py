@@ -192,6 +192,28 @@ def topk_select(S, TM, sel, n_dev, ns: int, nl: int, k_top: int) -> None:
              _ptr(sel), sel.stride(0), _ptr(n_dev), ns, nl, k_top, _stream(dev))
 
 
+def qgs_scan_heads(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int) -> None:
+    """The scan writing 16-bit key heads of the scores (int16 tensor H, raw bits) instead of
+    fp32 scores; TM (exact tile maxima) as oa_qgs_scan."""
+    dev = _dev(codes, limbs, fexp, H, TM, n_dev)
+    if H.dtype != torch.int16:
+        raise ValueError("H must be int16 (16-bit key heads)")
+    BH, Lmax, rq = codes.shape
+    lib.call("oa_qgs_scan_heads", _ptr(codes), BH, Lmax, rq, _ptr(limbs), _ptr(fexp), _ptr(H),
+             H.stride(0), _ptr(TM), TM.stride(0), _ptr(n_dev), ns, nl, _stream(dev))
+
+
+def topk_select_heads(H, TM, sel, n_dev, ns: int, nl: int, k_top: int, codes, limbs, fexp) -> None:
+    """Top-k over key-head rows: candidate scores recomputed exactly from the codes; the
+    selected tokens' heads are set to that of -inf."""
+    dev = _dev(H, TM, sel, n_dev, codes, limbs, fexp)
+    R = H.shape[0]
+    BH, Lmax, _ = codes.shape
+    lib.call("oa_topk_select_heads", _ptr(H), H.stride(0), _ptr(TM), TM.stride(0), R, TM.shape[1],
+             _ptr(sel), sel.stride(0), _ptr(n_dev), ns, nl, k_top, _ptr(codes), BH, Lmax,
+             _ptr(limbs), _ptr(fexp), _stream(dev))
+
+
 def errorgate(q, K, asg, sel, Sk, Sk2, nb, score, n_t, sm_scale: float) -> None:
     """wl1 cluster scores; sm_scale is the Python (double) scale, whose square is formed in
     double and rounded once, as the estimator does (multibin.py:643)."""
@@ -235,6 +257,19 @@ def topq(S, asg8, quota, exp_idx, n_dev, path: int | None = None) -> None:
     else:
         lib.call("oa_topq_path", _ptr(S), S.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R,
                  C, Lmax, _ptr(exp_idx), E, _ptr(n_dev), int(path), _stream(dev))
+
+
+def topq_heads(H, asg8, quota, exp_idx, n_dev, codes, limbs, fexp, S32, path: int = 0) -> None:
+    """Within-cluster top-q over key-head rows (oa_topq_heads); S32 (fp32, rows as H) receives
+    the exact scores of rows left to the key-prefix kernel.  path 2: the linear-bin kernel
+    alone; path 3: every row through the key-prefix kernel."""
+    dev = _dev(H, asg8, quota, exp_idx, n_dev, codes, limbs, fexp, S32)
+    R, C = quota.shape
+    Lmax = codes.shape[1]
+    E = exp_idx.shape[1]
+    lib.call("oa_topq_heads", _ptr(H), H.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R, C,
+             Lmax, _ptr(exp_idx), E, _ptr(n_dev), _ptr(codes), codes.shape[0], _ptr(limbs),
+             _ptr(fexp), _ptr(S32), S32.stride(0), int(path), _stream(dev))
 
 
 def residual(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n) -> None:

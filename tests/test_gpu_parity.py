@@ -150,12 +150,35 @@ def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
     ops.residual(K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, kbr, vbr, lnr)
     ops.residual_flash(qr, K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, out, SC)
     torch.cuda.synchronize()
+    # the same stages over 16-bit key heads (the pipeline the decode step runs)
+    H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
+    TMh = torch.empty_like(TM)
+    selh = torch.empty_like(sel)
+    S32 = torch.empty(R, ntiles * 64, device=DEV)
+    exph = torch.full_like(exp_idx, 777)
+    exph3 = torch.full_like(exp_idx, 777)
+    ops.qgs_scan_heads(st.codes, limbs, fexp, H, TMh, n_dev, ns, nl)
+    torch.cuda.synchronize()
+    r.update(H=H.cpu().numpy().view(np.uint16).copy(), TMh=TMh.cpu().numpy())
+    ops.topk_select_heads(H, TMh, selh, n_dev, ns, nl, k, st.codes, limbs, fexp)
+    ops.topq_heads(H, st.asg8, quota, exph, n_dev, st.codes, limbs, fexp, S32)
+    ops.topq_heads(H, st.asg8, quota, exph3, n_dev, st.codes, limbs, fexp, S32, path=3)
+    torch.cuda.synchronize()
+    r.update(H_after=H.cpu().numpy().view(np.uint16).copy(), selh=selh.cpu().numpy(),
+             exph=exph.cpu().numpy()[:, :E], exph3=exph3.cpu().numpy()[:, :E])
     r.update(S_after=S.cpu().numpy(), sel=sel.cpu().numpy(), score=score.cpu().numpy(),
              n_t=n_t.cpu().numpy(), quota=quota.cpu().numpy(), exp_idx=exp_idx.cpu().numpy()[:, :E],
              fused=(score2.cpu().numpy(), n_t2.cpu().numpy(), quota2.cpu().numpy()),
              kbar_r=bf16_to_f32(bf16_np(kbr)), vbar_r=bf16_to_f32(bf16_np(vbr)), log_n=lnr.cpu().numpy(),
              out=bf16_to_f32(bf16_np(out)))
     return r
+
+
+def score_heads(S):
+    """16-bit heads of the order-preserving keys of fp32 scores (the top 16 bits)."""
+    u = np.ascontiguousarray(S, dtype=np.float32).view(np.uint32)
+    key = np.where(u >> 31 == 1, ~u, u | np.uint32(0x80000000))
+    return (key >> 16).astype(np.uint16)
 
 
 def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
@@ -195,6 +218,14 @@ def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
     for got, want in zip(g["fused"], (g["score"], g["n_t"], g["quota"])):
         assert np.array_equal(got, want), "fused gate+fill differs from the separate kernels"
     assert np.array_equal(g["exp_idx"], ref["exp_idx"]), "expanded sets differ"
+    # the 16-bit key-head pipeline: heads of the exact scores, the same tile maxima, selection
+    # and expanded sets (also with every row through the exact-score rows and key-prefix kernel)
+    assert np.array_equal(g["H"][:, :n], score_heads(ref["S"][:, :n])), "score heads differ"
+    assert np.array_equal(g["TMh"][:, :ntile_n], tm_ref)
+    assert np.array_equal(g["selh"], ref["sel"]), "top-k over heads differs"
+    assert np.all(np.take_along_axis(g["H_after"], g["selh"].astype(np.int64), 1) == 0x007F)
+    assert np.array_equal(g["exph"], ref["exp_idx"]), "top-q over heads differs"
+    assert np.array_equal(g["exph3"], ref["exp_idx"]), "top-q over heads (key-prefix) differs"
     live = np.isfinite(ref["log_n"])
     assert np.array_equal(np.isfinite(g["log_n"]), live)
     assert np.allclose(g["log_n"][live], ref["log_n"][live], rtol=1e-6)
