@@ -18,8 +18,24 @@ __device__ __forceinline__ const int* limb_words(const int8_t* limbs, int kvr, i
   return reinterpret_cast<const int*>(limbs + ((long)kvr * 16 + g * 4) * 32);
 }
 
-// the exact score of token pos of KV row kvr (codes laid out (BH, Lmax, 32)); lw as above,
+// the exact score of a token from its 32-byte code (two 16-byte words c0, c1); lw as above,
 // inv = 2^-F of the query row
+__device__ __forceinline__ float qgs_score_words(uint4 c0, uint4 c1, const int* lw, double inv) {
+  const int cw[8] = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
+                     (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
+  int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int w = 0; w < 8; ++w) acc[k] = __builtin_amdgcn_sdot4(cw[w], lw[k * 8 + w], acc[k], false);
+  double s = (double)acc[3];
+  s = fma(s, 256.0, (double)acc[2]);
+  s = fma(s, 256.0, (double)acc[1]);
+  s = fma(s, 256.0, (double)acc[0]);
+  return (float)(s * inv);
+}
+
+// the exact score of token pos of KV row kvr (codes laid out (BH, Lmax, 32))
 __device__ __forceinline__ float qgs_score(const int8_t* codes, long lmax, int kvr, int pos,
                                            const int* lw, double inv) {
   const uint4* cp = reinterpret_cast<const uint4*>(codes + ((long)kvr * lmax + pos) * 32);

@@ -268,10 +268,12 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(void* __restrict__ 
     mine = tk[j] > mine ? tk[j] : mine;
   }
   int my_tile = 0;               // lane i < k_top: the i-th chosen tile
+  unsigned long long kth = 0ull; // the key of the k-th chosen tile's maximum
   for (int i = 0; i < k_top; ++i) {
     const unsigned long long best = oa::wave_max_u64(mine);
     const int t = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
     if (lane == i) my_tile = t;
+    kth = best;
     if (best == mine) {          // the owner lane drops the tile and refreshes its maximum
       mine = 0ull;
 #pragma unroll
@@ -284,10 +286,43 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(void* __restrict__ 
   // candidates: lane l holds column l of the k chosen tiles
   unsigned long long ck[KR];
   float cv[KR];
+  if (HEADS) {
+    // only candidates whose key head reaches that of the k-th chosen tile maximum can be in the
+    // top k (heads are non-decreasing in the score): their exact scores are recomputed, the
+    // others count as -inf
+    // (the heads and every candidate's code are loaded in one round)
+    const uint16_t* Hrow = static_cast<const uint16_t*>(Sv) + (long)row * s_stride;
+    const int kvr = row / GQ;
+    const int dead_hi = n - nl;
+    uint32_t hv[KR];
+    uint4 cw[KR][2];
 #pragma unroll
-  for (int j = 0; j < KR; ++j) {
-    const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
-    cv[j] = cand_score<HEADS>(Sv, s_stride, row, tj * 64 + lane, ns, n - nl, rs, lw, inv);
+    for (int j = 0; j < KR; ++j) {
+      const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+      const int pos = tj * 64 + lane;
+      hv[j] = j < k_top ? Hrow[pos] : 0u;
+      const uint4* cp = reinterpret_cast<const uint4*>(rs.codes + ((long)kvr * rs.lmax +
+                                                                   max(min(pos, dead_hi - 1), 0)) * 32);
+      cw[j][0] = cp[0];
+      cw[j][1] = cp[1];
+    }
+    // each chosen tile holds a token scoring at least the k-th chosen tile maximum, so the k-th
+    // best score reaches it, and so does every top-k token's head
+    const uint32_t T = (uint32_t)(kth >> 48);
+#pragma unroll
+    for (int j = 0; j < KR; ++j) {
+      const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+      const int pos = tj * 64 + lane;
+      cv[j] = -INFINITY;
+      if (j < k_top && hv[j] >= T && pos >= ns && pos < dead_hi)
+        cv[j] = oa::qgs_score_words(cw[j][0], cw[j][1], lw, inv);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KR; ++j) {
+      const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+      cv[j] = cand_score<HEADS>(Sv, s_stride, row, tj * 64 + lane, ns, n - nl, rs, lw, inv);
+    }
   }
   mine = 0ull;
 #pragma unroll
