@@ -67,6 +67,9 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
   float* TMrow = TM + (long)row * tm_stride;
   const int8_t* cb = codes + (long)kvr * Lmax * RQ;
 
+  // heads: each wave stages its tile's 4 x 64 heads in LDS and writes them back as 8-byte words
+  // (four consecutive positions per lane: whole 128-byte lines per store)
+  __shared__ uint16_t s_h[HEADS ? kScanThreads / 64 : 1][GQ][64];
   const int tile_begin = blockIdx.x * (kTokWG / 64) + wave * (kTokWG / 256);
   const int ntile_total = (Lmax + 63) / 64;
   for (int tt = 0; tt < kTokWG / 256; ++tt) {
@@ -90,9 +93,20 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
       float sc = (float)(s * inv);
       const int tok = tile * 64 + b * 16 + nn;
       if (tok < ns || tok >= dead_hi) sc = -INFINITY;
-      if (HEADS) Hrow[tok] = oa::score_head(sc);
+      if (HEADS) s_h[wave][kg][b * 16 + nn] = oa::score_head(sc);
       else Srow[tok] = sc;
       tmax = fmaxf(tmax, sc);
+    }
+    if (HEADS) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+      const uint2 hv = *reinterpret_cast<const uint2*>(&s_h[wave][kg][4 * nn]);
+      *reinterpret_cast<uint2*>(Hrow + (long)tile * 64 + 4 * nn) = hv;
+      // the staged heads are read before the next tile overwrites them
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 8, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 4, 64));
