@@ -481,7 +481,7 @@ def main():
         "topk_select": R * (-(-n_mid // 64)) * 4 + R * NSX * 4,  # tile maxima, sel out
         "gate_fill": R * Cn * (2 * D * 4 + 4) + R * NSX * D * 2,  # Sk, Sk2, n; K of sel
         "topq": R * n_mid * (2 + 1) + R * E * 4,               # 16-bit score heads + byte ids; exp out
-        "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * 2 * D * 4,  # K,V exact set; Sk, Sv
+        "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * (D * 4 + 4),  # K,V exact set; Sv, q.Sk
     }
     stage_alg = B * HKV * n_mid * 32 + R * (NSX + E) * 2 * D * 2 + R * Cn * (3 * D * 4 + 4)
     roof_kernel = max(stage_us, key=lambda k: stage_us[k])

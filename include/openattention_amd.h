@@ -166,14 +166,16 @@ int oa_waterfill(const float* score, const float* n_t, int rows, int C, int budg
                  void* stream);
 
 /*
- * ErrorGate and water-filling fused in one launch per row (scores kept on chip; score and n_t
- * are also written out).  Same results as oa_errorgate followed by oa_waterfill.
+ * ErrorGate and water-filling (two launches on the stream; score and n_t are also written
+ * out).  Same results as oa_errorgate followed by oa_waterfill.  qsk (rows, C) fp32, when not
+ * null, receives q . Sk_c of every cluster (pooled sums, before the selected tokens leave them)
+ * for oa_residual_flash; no counterpart in the reference.
  */
 int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, long k_stride_s,
                  int rows, int kv_rows, int head_dim, const int32_t* asg, long asg_stride,
                  const int32_t* sel, long sel_stride, int n_sel, const float* Sk, const float* Sk2,
                  const float* nb, int C, float sm_scale, float sm_scale_sq, int budget,
-                 float* score, float* n_t, float* quota, void* stream);
+                 float* score, float* n_t, float* quota, float* qsk, void* stream);
 
 /*
  * Within-cluster top-q: the q_c best tail members of every cluster by QGS score (ties to the
@@ -231,14 +233,15 @@ int oa_residual(const void* K, const void* V, long kv_stride_b, long kv_stride_s
 /*
  * Residual proxies fused with OpenAttention.flash: every K/V row read once, proxies kept in
  * registers (fp32).  Replaces the residual + ours_flash pair of the deployed step
- * (inference/ours_graph.py:324-344).   out (rows, 128) bf16.
+ * (inference/ours_graph.py:324-344).   out (rows, 128) bf16.  qsk (rows, C) from oa_gate_fill,
+ * when not null, stands in for the kernel's own q . Sk pass (Sk is then not read).
  */
 int oa_residual_flash(const void* q, long q_stride, const void* K, const void* V,
                       long kv_stride_b, long kv_stride_s, int rows, int kv_rows, int head_dim,
                       const int32_t* asg, long asg_stride, const int32_t* sel, long sel_stride,
                       int n_sel, const int32_t* exp_idx, int E, const float* quota,
                       const float* n_t, const float* Sk, const float* Sv, int C, float sm_scale,
-                      void* out, long out_stride, void* stream);
+                      void* out, long out_stride, const float* qsk, void* stream);
 
 /*
  * Dense bf16 decode attention over positions [0, n) (the comparator), split-K over nsplit key

@@ -31,6 +31,7 @@ struct GateArgs {
   const float* Sk; const float* Sk2; long st_stride_r;   // (R, C, D): row stride in floats
   const float* nb; long nb_stride;
   float* score; float* n_t; long out_stride;
+  float* qsk;                                         // optional: q . Sk_c of every cluster
   int C; float sc; float sc2;
 };
 
@@ -40,7 +41,10 @@ __device__ __forceinline__ void gate_dots(const GateArgs& a, float sk_lo, float 
                                           float s2_lo, float s2_hi, float nt, float q_lo,
                                           float q_hi, float qq_lo, float qq_hi,
                                           unsigned long long selmask, const float* s_k, int lane,
-                                          float* zbar_out, float* s2_out, float* nt_out) {
+                                          float* zbar_out, float* s2_out, float* nt_out,
+                                          float* qsk_out) {
+  // q . Sk of the pooled sums (before the selected tokens leave them), for the residual pass
+  *qsk_out = oa::dot128_canon(q_lo, sk_lo, q_hi, sk_hi);
   // the cluster's selected tokens, in selection order (bit i = selected token i)
   while (selmask) {
     const int i = __ffsll((long long)selmask) - 1;
@@ -80,7 +84,7 @@ __device__ __forceinline__ float gate_score(float zbar, float s2, float nt) {
 __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_score, float* s_nt) {
   extern __shared__ float s_k[];
   __shared__ unsigned long long s_selmask[kMaxC];
-  __shared__ float s_zbar[kMaxC], s_s2[kMaxC];
+  __shared__ float s_zbar[kMaxC], s_s2[kMaxC], s_qsk[kMaxC];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -127,20 +131,24 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
     for (int i = 0; i < kBatch; ++i) {
       const int c = c0 + kGateWaves * i;
       if (c < a.C) {
-        float zb, sv, nt;
+        float zb, sv, nt, qs;
         gate_dots(a, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
-                  s_selmask[c], s_k, lane, &zb, &sv, &nt);
+                  s_selmask[c], s_k, lane, &zb, &sv, &nt, &qs);
         if (lane == 0) {
           s_zbar[c] = zb;
           s_s2[c] = sv;
           s_nt[c] = nt;
+          s_qsk[c] = qs;
         }
       }
     }
   }
   __syncthreads();
   // ---- scalar tails, one cluster per thread
-  for (int c = tid; c < a.C; c += kGateThreads) s_score[c] = gate_score(s_zbar[c], s_s2[c], s_nt[c]);
+  for (int c = tid; c < a.C; c += kGateThreads) {
+    s_score[c] = gate_score(s_zbar[c], s_s2[c], s_nt[c]);
+    if (a.qsk) a.qsk[(long)row * a.C + c] = s_qsk[c];
+  }
   __syncthreads();
 }
 
@@ -422,7 +430,7 @@ extern "C" int oa_errorgate(const void* q, long q_stride, const void* K, long k_
   a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
   a.Sk = Sk; a.Sk2 = Sk2; a.st_stride_r = (long)C * OA_D;
   a.nb = nb; a.nb_stride = C;
-  a.score = score; a.n_t = n_t; a.out_stride = C;
+  a.score = score; a.n_t = n_t; a.out_stride = C; a.qsk = nullptr;
   a.C = C; a.sc = sm_scale;
   a.sc2 = sm_scale_sq;
   hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads),
@@ -435,7 +443,7 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
                             const int32_t* asg, long asg_stride, const int32_t* sel, long sel_stride,
                             int n_sel, const float* Sk, const float* Sk2, const float* nb, int C,
                             float sm_scale, float sm_scale_sq, int budget, float* score, float* n_t,
-                            float* quota, void* stream) {
+                            float* quota, float* qsk, void* stream) {
   if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || n_sel < 0 || n_sel > kMaxSel ||
       C <= 0 || C > kMaxC || budget < 0 || k_stride_b % 8 || k_stride_s % 8 ||
       (reinterpret_cast<uintptr_t>(K) & 15))
@@ -447,7 +455,7 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
   a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
   a.Sk = Sk; a.Sk2 = Sk2; a.st_stride_r = (long)C * OA_D;
   a.nb = nb; a.nb_stride = C;
-  a.score = score; a.n_t = n_t; a.out_stride = C;
+  a.score = score; a.n_t = n_t; a.out_stride = C; a.qsk = qsk;
   a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
   // the gate is wide and short, the fill one serial chain per row: as two launches every row of
   // each is resident at once instead of the fill holding the gate's workgroup slots

@@ -46,6 +46,7 @@ struct ResArgs {
   const int32_t* exq; int E;
   const float* quota; const float* n_t;
   const float* Sk; const float* Sv;
+  const float* qsk;                             // optional: q . Sk_c from the gate
   int C; float sm_scale;
   uint16_t* out; long out_stride;               // fused variant
   uint16_t* kbar_r; uint16_t* vbar_r; float* logn;  // residual-only variant
@@ -316,6 +317,8 @@ __global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
   }
   if (tid < C) s_nt[tid] = ntv;
   for (int c = tid + kRFThreads; c < C; c += kRFThreads) s_nt[c] = a.n_t[(long)row * C + c];
+  if (a.qsk)                       // q . Sk from the gate: no pass over Sk below
+    for (int c = tid; c < C; c += kRFThreads) s_qsk[c] = a.qsk[(long)row * C + c];
   if (tid < NI) s_tok[tid] = tok0;
   for (int i = tid + kRFThreads; i < NI; i += kRFThreads) {
     const int tok = i < a.n_sel ? a.sel[(long)row * a.sel_stride + i]
@@ -368,7 +371,7 @@ __global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
   };
   float4 skx[4][2];
   uint4 kw[kBatch];
-  load_stat(a.Sk, grp, skx);
+  if (!a.qsk) load_stat(a.Sk, grp, skx);
   if (NI > 0) load_k(grp, kw);
   int scid = -1;
   const int stok = a.n_sel > 0 ? s_tok[min(tid, a.n_sel - 1)] : -1;
@@ -396,10 +399,12 @@ __global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
     load_k(u0, kw);
     dots_k(u0, kw);
   }
-  dots_sk(grp, skx);
-  for (int c0 = grp + kRFGroups * 4; c0 < C; c0 += kRFGroups * 4) {
-    load_stat(a.Sk, c0, skx);
-    dots_sk(c0, skx);
+  if (!a.qsk) {
+    dots_sk(grp, skx);
+    for (int c0 = grp + kRFGroups * 4; c0 < C; c0 += kRFGroups * 4) {
+      load_stat(a.Sk, c0, skx);
+      dots_sk(c0, skx);
+    }
   }
   __syncthreads();
 
@@ -502,7 +507,7 @@ int launch(bool fused, const void* q, long q_stride, const void* K, const void* 
            const int32_t* sel, long sel_stride, int n_sel, const int32_t* exp_idx, int E,
            const float* quota, const float* n_t, const float* Sk, const float* Sv, int C,
            float sm_scale, void* out, long out_stride, void* kbar_r, void* vbar_r, float* logn,
-           void* stream) {
+           const float* qsk, void* stream) {
   if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || C <= 0 || C > kMaxC ||
       n_sel < 0 || n_sel > kMaxSel || E < 0 || E > kMaxE || (kv_ss % 8) != 0 || (kv_sb % 8) != 0)
     return OA_EINVAL;
@@ -512,7 +517,7 @@ int launch(bool fused, const void* q, long q_stride, const void* K, const void* 
   a.G = rows / kv_rows;
   a.asg = asg; a.asg_stride = asg_stride;
   a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
-  a.exq = exp_idx; a.E = E; a.quota = quota; a.n_t = n_t; a.Sk = Sk; a.Sv = Sv;
+  a.exq = exp_idx; a.E = E; a.quota = quota; a.n_t = n_t; a.Sk = Sk; a.Sv = Sv; a.qsk = qsk;
   a.C = C; a.sm_scale = sm_scale;
   a.out = (uint16_t*)out; a.out_stride = out_stride;
   a.kbar_r = (uint16_t*)kbar_r; a.vbar_r = (uint16_t*)vbar_r; a.logn = logn;
@@ -537,11 +542,12 @@ extern "C" int oa_residual_flash(const void* q, long q_stride, const void* K, co
                                  const int32_t* sel, long sel_stride, int n_sel,
                                  const int32_t* exp_idx, int E, const float* quota,
                                  const float* n_t, const float* Sk, const float* Sv, int C,
-                                 float sm_scale, void* out, long out_stride, void* stream) {
+                                 float sm_scale, void* out, long out_stride, const float* qsk,
+                                 void* stream) {
   if (!out || (q_stride % 8) != 0) return OA_EINVAL;
   return launch(true, q, q_stride, K, V, kv_stride_b, kv_stride_s, rows, kv_rows, head_dim, asg,
                 asg_stride, sel, sel_stride, n_sel, exp_idx, E, quota, n_t, Sk, Sv, C, sm_scale,
-                out, out_stride, nullptr, nullptr, nullptr, stream);
+                out, out_stride, nullptr, nullptr, nullptr, qsk, stream);
 }
 
 extern "C" int oa_residual(const void* K, const void* V, long kv_stride_b, long kv_stride_s,
@@ -554,5 +560,5 @@ extern "C" int oa_residual(const void* K, const void* V, long kv_stride_b, long 
   // the residual-only variant reads no query; K stands in so the pointer is valid
   return launch(false, K, 0, K, V, kv_stride_b, kv_stride_s, rows, kv_rows, head_dim, asg,
                 asg_stride, sel, sel_stride, n_sel, exp_idx, E, quota, n_t, Sk, Sv, C, 0.f,
-                nullptr, 0, kbar_r, vbar_r, log_n, stream);
+                nullptr, 0, kbar_r, vbar_r, log_n, nullptr, stream);
 }

@@ -35,14 +35,14 @@ SIGNATURES = {
     "oa_topk_select": [P, L, P, L, I, I, P, L, P, I, I, I, P],
     "oa_topk_select_heads": [P, L, P, L, I, I, P, L, P, I, I, I, P, I, I, P, P, P],
     "oa_errorgate": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, P, P, P],
-    "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P],
+    "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P, P],
     "oa_waterfill": [P, P, I, I, I, P, P],
     "oa_topq": [P, L, P, L, P, I, I, I, P, I, P, P],
     "oa_topq_path": [P, L, P, L, P, I, I, I, P, I, P, I, P],
     "oa_topq_heads": [P, L, P, L, P, I, I, I, P, I, P, P, I, P, P, P, L, I, P],
     "oa_residual": [P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, P, P, P, P],
     "oa_residual_flash": [P, L, P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, F, P, L,
-                          P],
+                          P, P],
     "oa_dense_decode": [P, L, P, P, L, L, I, I, I, I, P, F, I, P, P, P, P, L, P],
     "oa_qgs_codes": [P, L, L, I, I, P, P, L, P, P, P],
     "oa_qgc_project": [P, L, L, I, I, I, P, P, L, P, P, P, P],

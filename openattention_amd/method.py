@@ -112,6 +112,7 @@ class OursHIP(Method):
         self.score = torch.empty(R, self.Cn, **f32)
         self.n_t = torch.empty(R, self.Cn, **f32)
         self.quota = torch.empty(R, self.Cn, **f32)
+        self.qsk = torch.empty(R, self.Cn, **f32)      # q . Sk_c, from the gate to the residual
         self.exp_idx = torch.empty(R, max(self.E, 1), **i32)
         self.out = torch.empty(R, D, device=dev, dtype=torch.bfloat16)
         self._sel = {}
@@ -180,14 +181,14 @@ class OursHIP(Method):
                               self.fexp)
         mark("topk_select")
         ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota,
-                      SC, self.E)
+                      SC, self.E, qsk=self.qsk)
         mark("gate_fill")
         ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, C.n_dev, st.codes, self.limbs,
                        self.fexp, self.S)
         mark("topq")
         if self.fused:
             ops.residual_flash(qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk,
-                               st.Sv, self.out, SC)
+                               st.Sv, self.out, SC, qsk=self.qsk)
             mark("residual_flash")
         else:
             ops.residual(K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk, st.Sv,
@@ -212,12 +213,12 @@ class OursHIP(Method):
         ops.topk_select_heads(self.H[rs], self.TM[rs], selg, C.n_dev, ns, nl, k_top, sub.codes,
                               self.limbs[ks], self.fexp[rs])
         ops.gate_fill(qg, Kg, sub.asg, selg, sub.Sk, sub.Sk2, sub.nb, self.score[rs], self.n_t[rs],
-                      self.quota[rs], SC, self.E)
+                      self.quota[rs], SC, self.E, qsk=self.qsk[rs])
         ops.topq_heads(self.H[rs], sub.asg8, self.quota[rs], self.exp_idx[rs], C.n_dev, sub.codes,
                        self.limbs[ks], self.fexp[rs], self.S[rs])
         if self.fused:
             ops.residual_flash(qg, Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs],
-                               self.n_t[rs], sub.Sk, sub.Sv, self.out[rs], SC)
+                               self.n_t[rs], sub.Sk, sub.Sv, self.out[rs], SC, qsk=self.qsk[rs])
         else:
             ops.residual(Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs], self.n_t[rs],
                          sub.Sk, sub.Sv, self.kbar_r[rs], self.vbar_r[rs], self.log_n[rs])

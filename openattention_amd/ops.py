@@ -226,15 +226,19 @@ def errorgate(q, K, asg, sel, Sk, Sk2, nb, score, n_t, sm_scale: float) -> None:
              _ptr(score), _ptr(n_t), _stream(dev))
 
 
-def gate_fill(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota, sm_scale: float, E: int) -> None:
-    """ErrorGate + water-filling in one launch (same results as errorgate then waterfill)."""
+def gate_fill(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota, sm_scale: float, E: int,
+              qsk=None) -> None:
+    """ErrorGate + water-filling (same results as errorgate then waterfill); qsk (R, C) fp32,
+    when given, receives q . Sk of every cluster for residual_flash."""
     dev = _dev(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota)
     R, C = nb.shape
     BH = K.shape[0]
+    if qsk is not None and (qsk.shape != (R, C) or qsk.dtype != torch.float32 or not qsk.is_contiguous()):
+        raise ValueError("qsk must be a contiguous (rows, C) float32 tensor")
     lib.call("oa_gate_fill", _ptr(q), q.stride(0), _ptr(K), K.stride(0), K.stride(1), R, BH,
              q.shape[1], _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1],
              _ptr(Sk), _ptr(Sk2), _ptr(nb), C, float(sm_scale), float(sm_scale) * float(sm_scale),
-             int(E), _ptr(score), _ptr(n_t), _ptr(quota), _stream(dev))
+             int(E), _ptr(score), _ptr(n_t), _ptr(quota), _ptr(qsk), _stream(dev))
 
 
 def waterfill(score, n_t, quota, E: int) -> None:
@@ -282,14 +286,19 @@ def residual(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n)
              _ptr(vbar_r), _ptr(log_n), _stream(dev))
 
 
-def residual_flash(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out, sm_scale: float) -> None:
+def residual_flash(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out, sm_scale: float,
+                   qsk=None) -> None:
+    """Residual proxies + fused softmax; qsk (R, C) fp32 from gate_fill, when given, replaces the
+    kernel's own pass over Sk (same quantity, summed in another order)."""
     dev = _dev(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out)
     R, C = quota.shape
     BH = K.shape[0]
+    if qsk is not None and (qsk.shape != (R, C) or qsk.dtype != torch.float32 or not qsk.is_contiguous()):
+        raise ValueError("qsk must be a contiguous (rows, C) float32 tensor")
     lib.call("oa_residual_flash", _ptr(q), q.stride(0), _ptr(K), _ptr(V), K.stride(0), K.stride(1),
              R, BH, K.shape[2], _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1],
              _ptr(exp_idx), exp_idx.shape[1], _ptr(quota), _ptr(n_t), _ptr(Sk), _ptr(Sv), C,
-             float(sm_scale), _ptr(out), out.stride(0), _stream(dev))
+             float(sm_scale), _ptr(out), out.stride(0), _ptr(qsk), _stream(dev))
 
 
 def dense_decode(q, K, V, n_dev, out=None, sm_scale: float | None = None, nsplit: int | None = None,

@@ -145,11 +145,16 @@ def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
     ops.errorgate(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score, n_t, SC)
     ops.waterfill(score, n_t, quota, E)
     score2, n_t2, quota2 = torch.empty_like(score), torch.empty_like(n_t), torch.empty_like(quota)
-    ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score2, n_t2, quota2, SC, E)
+    qsk = torch.empty_like(score)
+    ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score2, n_t2, quota2, SC, E, qsk=qsk)
     ops.topq(S, st.asg8, quota, exp_idx, n_dev)
     ops.residual(K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, kbr, vbr, lnr)
     ops.residual_flash(qr, K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, out, SC)
+    out_q = torch.empty_like(out)
+    ops.residual_flash(qr, K, V, st.asg, sel, exp_idx, quota, n_t, st.Sk, st.Sv, out_q, SC, qsk=qsk)
     torch.cuda.synchronize()
+    r.update(qsk=qsk.cpu().numpy(), out_q=bf16_to_f32(bf16_np(out_q)),
+             Sk_np=st.Sk.cpu().numpy().astype(np.float64), q_np=bf16_to_f32(bf16_np(qr)).astype(np.float64))
     # the same stages over 16-bit key heads (the pipeline the decode step runs)
     H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
     TMh = torch.empty_like(TM)
@@ -236,6 +241,15 @@ def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
     print(f"  out rel err median {np.median(rel):.2e} max {rel.max():.2e}; "
           f"exact reads/row {(g['exp_idx'] >= 0).sum(1).mean():.1f} + {g['sel'].shape[1]}")
     assert rel.max() < BF16_TOL
+    # q . Sk handed from the gate to the residual pass: the dot against fp64, and the output
+    # with it within the same tolerance
+    Rr, Cc = g["qsk"].shape
+    want = np.einsum("rd,rcd->rc", g["q_np"], g["Sk_np"].reshape(Rr, Cc, -1))
+    err = np.abs(g["qsk"] - want) / np.maximum(np.abs(g["Sk_np"]).reshape(Rr, Cc, -1).sum(-1)
+                                               * np.abs(g["q_np"]).max(1, keepdims=True), 1e-30)
+    assert err.max() < 1e-6, err.max()
+    rel_q = rel_rows(g["out_q"], ref["out"])
+    assert rel_q.max() < BF16_TOL, rel_q.max()
     return g, ref
 
 
