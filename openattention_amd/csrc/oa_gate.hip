@@ -295,7 +295,7 @@ __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, dou
 // The 64 bisection steps run as rounds of DEPTH steps.  A round evaluates, in parallel, every
 // midpoint the next DEPTH sequential steps could visit: the probe tree in heap order (node 1 =
 // mid of (lo, hi); node 2n takes the left half (f > E: hi = mid), node 2n+1 the right half),
-// P = 2 NS lanes per node, node n in lanes [nP, nP + P).  Each node's interval is rebuilt from
+// P lanes per node, node n in lanes [nP, nP + P).  Each node's interval is rebuilt from
 // (lo, hi) by the same 0.5 * (lo + hi) operations the sequential steps perform, so its midpoint
 // is the one the sequential bisection would probe if it reached that node.  f at a node is the
 // canonical sum: the lane partial of canonical lane l is its clusters l, l + 64, ... added in
@@ -311,9 +311,11 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
   // ---- live clusters, weights and the bracket of log(lambda)
   FillState<NS> f;
   fill_prologue<NS>(score_row, nt_row, C, lane, f);
-  constexpr int P = 2 * NS;                  // lanes per probe node
+  // 8 lanes per probe node: each lane then adds only 8 canonical lane partials, and a round's
+  // fp64 work (not its latency) is what the lane count trades against the round count
+  constexpr int P = 8;                       // lanes per probe node
   constexpr int NL = 64 / P;                 // canonical lane partials per lane (= nodes + 1)
-  constexpr int DEPTH = NS == 1 ? 5 : (NS == 2 ? 4 : 3);   // log2(NL): nodes 1 .. NL - 1
+  constexpr int DEPTH = 3;                   // log2(NL): nodes 1 .. NL - 1
   static_assert((1 << DEPTH) == NL, "probe tree shape");
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
