@@ -39,11 +39,14 @@ __global__ void __launch_bounds__(64) qgs_prep_kernel(const uint16_t* __restrict
 }
 
 // ------------------------------------------------------------------------------------------
-// scan: grid (token chunks of kTokWG, BH).  4 waves; each wave streams 64-token tiles, four
-// MFMA blocks of 16 tokens per tile.  Writes the fp32 score of every position (sink/local and
-// positions >= n as -inf) and the maximum of every 64-token tile per query-head row.
+// scan: grid (token chunks of kTokWG, BH).  4 waves; each wave owns kTilesPerWave 64-token
+// tiles, four MFMA blocks of 16 tokens per tile, and requests all of their codes before the
+// first MFMA.  Writes the score of every position (sink/local and positions >= n as -inf) and
+// the maximum of every 64-token tile per query-head row.  The codes are read once per step, so
+// they are loaded non-temporally (and so are the head rows stored).
 constexpr int kScanThreads = 256;
-constexpr int kTokWG = 1024;
+constexpr int kTilesPerWave = 2;
+constexpr int kTokWG = kScanThreads / 64 * kTilesPerWave * 64;
 
 // HEADS: the score rows hold 16-bit key heads (oa::score_head) instead of fp32 scores
 template <bool HEADS>
@@ -56,42 +59,48 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 4;        // k-group for the operands; head g for the output
   const int nn = lane & 15;        // token inside a 16-token block; limb row for A
+  const int tile_begin = blockIdx.x * (kTokWG / 64) + wave * kTilesPerWave;
+  const int ntile_total = (Lmax + 63) / 64;
+  const int8_t* cb = codes + (long)kvr * Lmax * RQ;
+  // every code of the wave's tiles in flight at once (addresses clamped to the last token;
+  // tokens past Lmax are zeroed below)
+  long b_op[kTilesPerWave][4];
+#pragma unroll
+  for (int t = 0; t < kTilesPerWave; ++t)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int tok = (tile_begin + t) * 64 + b * 16 + nn;
+      b_op[t][b] = __builtin_nontemporal_load(
+          reinterpret_cast<const long*>(cb + (long)min(tok, Lmax - 1) * RQ + kg * 8));
+    }
   const int n = *n_dev;
   const int dead_hi = n - nl;      // positions >= dead_hi are local or not yet written
-
   const long a_op = *reinterpret_cast<const long*>(limbs + (long)kvr * 16 * RQ + nn * RQ + kg * 8);
   const int row = kvr * GQ + kg;
   const double inv = ldexp(1.0, -fexp[row]);
   float* Srow = static_cast<float*>(Sv) + (long)row * s_stride;
   uint16_t* Hrow = static_cast<uint16_t*>(Sv) + (long)row * s_stride;
   float* TMrow = TM + (long)row * tm_stride;
-  const int8_t* cb = codes + (long)kvr * Lmax * RQ;
 
   // heads: each wave stages its tile's 4 x 64 heads in LDS and writes them back as 8-byte words
   // (four consecutive positions per lane: whole 128-byte lines per store)
   __shared__ uint16_t s_h[HEADS ? kScanThreads / 64 : 1][GQ][64];
-  const int tile_begin = blockIdx.x * (kTokWG / 64) + wave * (kTokWG / 256);
-  const int ntile_total = (Lmax + 63) / 64;
-  for (int tt = 0; tt < kTokWG / 256; ++tt) {
-    const int tile = tile_begin + tt;
-    if (tile >= ntile_total) break;
-    long b_op[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int tok = tile * 64 + b * 16 + nn;
-      b_op[b] = (tok < Lmax) ? *reinterpret_cast<const long*>(cb + (long)tok * RQ + kg * 8) : 0L;
-    }
+  for (int t = 0; t < kTilesPerWave; ++t) {
+    const int tile = tile_begin + t;
+    if (tile >= ntile_total) break;
     float tmax = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
+      const int tok = tile * 64 + b * 16 + nn;
       oa_v4i zero = {0, 0, 0, 0};
-      oa_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_op, b_op[b], zero, 0, 0, 0);
+      oa_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_op, tok < Lmax ? b_op[t][b] : 0L,
+                                                         zero, 0, 0, 0);
       double s = (double)acc[3];
       s = fma(s, 256.0, (double)acc[2]);
       s = fma(s, 256.0, (double)acc[1]);
       s = fma(s, 256.0, (double)acc[0]);
       float sc = (float)(s * inv);
-      const int tok = tile * 64 + b * 16 + nn;
       if (tok < ns || tok >= dead_hi) sc = -INFINITY;
       if (HEADS) s_h[wave][kg][b * 16 + nn] = oa::score_head(sc);
       else Srow[tok] = sc;
@@ -102,7 +111,9 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
       const uint2 hv = *reinterpret_cast<const uint2*>(&s_h[wave][kg][4 * nn]);
-      *reinterpret_cast<uint2*>(Hrow + (long)tile * 64 + 4 * nn) = hv;
+      uint32_t* hp = reinterpret_cast<uint32_t*>(Hrow + (long)tile * 64 + 4 * nn);
+      __builtin_nontemporal_store(hv.x, hp);
+      __builtin_nontemporal_store(hv.y, hp + 1);
       // the staged heads are read before the next tile overwrites them
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
