@@ -128,6 +128,13 @@ __device__ __forceinline__ float group16_sum(float v) {
   v = v + dpp_f32<0x141>(v);
   return v + dpp_f32<0x140>(v);
 }
+// the maximum of each 16-lane row, in every lane of the row (the same DPP folds)
+__device__ __forceinline__ float group16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  return fmaxf(v, dpp_f32<0x140>(v));
+}
 
 // ---- order-independent reductions on the DPP network (no LDS round trips) ------------------
 // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror fold each 16-lane row;

@@ -80,11 +80,14 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
   const double inv = ldexp(1.0, -fexp[row]);
   float* Srow = static_cast<float*>(Sv) + (long)row * s_stride;
   uint16_t* Hrow = static_cast<uint16_t*>(Sv) + (long)row * s_stride;
-  float* TMrow = TM + (long)row * tm_stride;
 
   // heads: each wave stages its tile's 4 x 64 heads in LDS and writes them back as 8-byte words
   // (four consecutive positions per lane: whole 128-byte lines per store)
   __shared__ uint16_t s_h[HEADS ? kScanThreads / 64 : 1][GQ][64];
+  // the block's tile maxima, written out together at the end (consecutive lanes, consecutive
+  // tiles of a row: one store instead of four-lane scattered ones per tile)
+  constexpr int kTB = kTokWG / 64;
+  __shared__ float s_tm[GQ][kTB];
 #pragma unroll
   for (int t = 0; t < kTilesPerWave; ++t) {
     const int tile = tile_begin + t;
@@ -119,11 +122,15 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 8, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 4, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
-    if (nn == 0) TMrow[tile] = tmax;
+    // one 16-lane DPP row per head: the tile maximum in every lane of the row
+    tmax = oa::group16_max(tmax);
+    if (nn == 0) s_tm[kg][wave * kTilesPerWave + t] = tmax;
+  }
+  oa::lds_barrier();
+  if (threadIdx.x < GQ * kTB) {
+    const int g = threadIdx.x / kTB;
+    const int tile = blockIdx.x * kTB + threadIdx.x % kTB;
+    if (tile < ntile_total) TM[(long)(kvr * GQ + g) * tm_stride + tile] = s_tm[g][threadIdx.x % kTB];
   }
 }
 

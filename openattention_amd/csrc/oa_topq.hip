@@ -175,7 +175,7 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
   }
 }
 
-// the same from LDS in a loop, for more than 1024 staged keys
+// the same from LDS in a loop, for more than 512 staged keys
 __device__ void select_staged_loop(const unsigned long long* src, int cnt, int need, int c,
                                    unsigned long long floor, int top, uint32_t* cst, int* ctr,
                                    int lane) {
@@ -303,7 +303,7 @@ __device__ __forceinline__ void select_all_staged(int C, int wave, int lane, con
     const int top = bin_top_bit(s_klo[c], s_khi[c]);
     if (cnt <= 64) select_staged<1>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
     else if (cnt <= 256) select_staged<4>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
-    else if (cnt <= 1024) select_staged<16>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+    else if (cnt <= 512) select_staged<8>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
     else select_staged_loop(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
   }
 }
