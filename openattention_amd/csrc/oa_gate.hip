@@ -179,10 +179,26 @@ __device__ __forceinline__ double canon_sum(const double* x, int C, int lane) {
   return oa::wave_sum(p);
 }
 
+// the wave maximum on the DPP / permlane-swap network (no LDS round trips; the maximum does not
+// depend on the order, and a zero's sign does not matter where it is used)
+__device__ __forceinline__ double swap_max(unsigned lo0, unsigned hi0, unsigned lo1, unsigned hi1) {
+  const double x = __longlong_as_double((long long)(((unsigned long long)hi0 << 32) | lo0));
+  const double y = __longlong_as_double((long long)(((unsigned long long)hi1 << 32) | lo1));
+  return fmax(x, y);
+}
 __device__ __forceinline__ double wave_max_f64(double v) {
-#pragma unroll
-  for (int m = 1; m <= 32; m <<= 1) v = fmax(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmax(v, oa::dpp_f64<0xB1>(v));
+  v = fmax(v, oa::dpp_f64<0x4E>(v));
+  v = fmax(v, oa::dpp_f64<0x141>(v));
+  v = fmax(v, oa::dpp_f64<0x140>(v));
+  unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const auto l16 = __builtin_amdgcn_permlane16_swap((unsigned)b, (unsigned)b, false, false);
+  const auto h16 = __builtin_amdgcn_permlane16_swap((unsigned)(b >> 32), (unsigned)(b >> 32), false, false);
+  v = swap_max(l16[0], h16[0], l16[1], h16[1]);
+  b = (unsigned long long)__double_as_longlong(v);
+  const auto l32 = __builtin_amdgcn_permlane32_swap((unsigned)b, (unsigned)b, false, false);
+  const auto h32 = __builtin_amdgcn_permlane32_swap((unsigned)(b >> 32), (unsigned)(b >> 32), false, false);
+  return swap_max(l32[0], h32[0], l32[1], h32[1]);
 }
 
 __device__ __forceinline__ double readlane_f64(double v, int l) {
