@@ -530,6 +530,37 @@ def main():
         log(f"[bench] dense (us): {dense}")
     dense_best = min([v for v in dense.values() if isinstance(v, float)], default=None)
 
+    # ---- the flash step alone (what the reference's published 0.114 ms covers): exact set sel +
+    # exp_idx of the last decoded layer over layer 0's K/V, and one proxy per cluster with the
+    # stage's residual counts (proxy vectors seeded; the cost does not depend on their values)
+    flash_only = None
+    if not a.no_dense:
+        nres = m.n_t - m.quota
+        logn_f = torch.where(nres > 0.5, torch.log(nres.clamp_min(1.0)), torch.full_like(nres, float("-inf")))
+        gf = torch.Generator(device=dev)
+        gf.manual_seed(7)
+        kb_f = torch.randn(R, Cn, D, device=dev, generator=gf).to(torch.bfloat16)
+        vb_f = torch.randn(R, Cn, D, device=dev, generator=gf).to(torch.bfloat16)
+        out_f = torch.empty_like(q0)
+
+        def run_flash():
+            ops.flash_decode(q0, K0, V0, m.last_sel, m.exp_idx, kb_f, vb_f, logn_f, proxy_per_kv=False,
+                             sm_scale=D ** -0.5, out=out_f)
+
+        for _ in range(3):
+            run_flash()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(10):
+            x0, x1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            x0.record()
+            run_flash()
+            x1.record()
+            torch.cuda.synchronize()
+            ts.append(x0.elapsed_time(x1) * 1e3)
+        flash_only = round(statistics.median(ts), 1)
+        log(f"[bench] flash only (us): {flash_only}")
+
     # ---- CPU restatement on a bounded sample: sequence b=0 of layer 0
     cpu = None
     if not a.no_cpu_baseline:
@@ -593,6 +624,7 @@ def main():
         "roofline": roofline,
         "dense_us": dense,
         "speedup_vs_dense": round(dense_best / us_layer, 2) if dense_best else None,
+        "flash_only_us": flash_only,
         "cpu_baseline": cpu,
         "prefill_build": prefill_report(build_ms, B, T0, Cn),
     }
