@@ -74,6 +74,14 @@ __device__ __forceinline__ void index_assign_row(const IdxArgs& a, int r, int la
   oa::unpack8(*reinterpret_cast<const uint4*>(Wb + lane * RC + 8), wl + 8);
   oa::unpack8(*reinterpret_cast<const uint4*>(Wb + (lane + 64) * RC), wh);
   oa::unpack8(*reinterpret_cast<const uint4*>(Wb + (lane + 64) * RC + 8), wh + 8);
+  // the lane's first centroid is requested with W (its distance needs zp only later)
+  const float* cb = a.cent + (long)r * a.C * RC;
+  float c0[RC];
+#pragma unroll
+  for (int j = 0; j < RC; j += 4) {
+    const float4 x = *reinterpret_cast<const float4*>(cb + (long)min(lane, a.C - 1) * RC + j);
+    c0[j] = x.x; c0[j + 1] = x.y; c0[j + 2] = x.z; c0[j + 3] = x.w;
+  }
   float zp[RC];
 #pragma unroll
   for (int j = 0; j < RC; ++j) {
@@ -82,13 +90,17 @@ __device__ __forceinline__ void index_assign_row(const IdxArgs& a, int r, int la
   }
   float best = -INFINITY;
   int bidx = 0x7fffffff;
-  const float* cb = a.cent + (long)r * a.C * RC;
   for (int c = lane; c < a.C; c += 64) {
     float cc[RC];
+    if (c == lane) {
 #pragma unroll
-    for (int j = 0; j < RC; j += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(cb + (long)c * RC + j);
-      cc[j] = x.x; cc[j + 1] = x.y; cc[j + 2] = x.z; cc[j + 3] = x.w;
+      for (int j = 0; j < RC; ++j) cc[j] = c0[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < RC; j += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(cb + (long)c * RC + j);
+        cc[j] = x.x; cc[j + 1] = x.y; cc[j + 2] = x.z; cc[j + 3] = x.w;
+      }
     }
     float sim = zp[0] * cc[0];
     float h = cc[0] * cc[0];
@@ -100,11 +112,30 @@ __device__ __forceinline__ void index_assign_row(const IdxArgs& a, int r, int la
     const float dist = sim - 0.5f * h;
     if (dist > best || bidx == 0x7fffffff) { best = dist; bidx = c; }
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ob = __shfl_xor(best, m, 64);
-    const int oi = __shfl_xor(bidx, m, 64);
+  // the argmax (ties to the lower id) on the DPP / permlane network: the pairing of the xor
+  // butterfly (m = 1, 2, 4, 8, 16, 32; the mirrors pair groups that are uniform by then); the
+  // larger distance, then the lower id, is an order-free pick, so every lane ends with the winner
+  auto take = [&](float ob, int oi) {
     if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
+  };
+  take(oa::dpp_f32<0xB1>(best), __builtin_amdgcn_update_dpp(bidx, bidx, 0xB1, 0xf, 0xf, false));
+  take(oa::dpp_f32<0x4E>(best), __builtin_amdgcn_update_dpp(bidx, bidx, 0x4E, 0xf, 0xf, false));
+  take(oa::dpp_f32<0x141>(best), __builtin_amdgcn_update_dpp(bidx, bidx, 0x141, 0xf, 0xf, false));
+  take(oa::dpp_f32<0x140>(best), __builtin_amdgcn_update_dpp(bidx, bidx, 0x140, 0xf, 0xf, false));
+  // (a permlane swap returns the lane's own pair and its partner's; the pick is symmetric)
+  {
+    const auto b16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(best), __float_as_uint(best), false, false);
+    const auto i16 = __builtin_amdgcn_permlane16_swap((unsigned)bidx, (unsigned)bidx, false, false);
+    best = __uint_as_float(b16[0]);
+    bidx = (int)i16[0];
+    take(__uint_as_float(b16[1]), (int)i16[1]);
+  }
+  {
+    const auto b32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(best), __float_as_uint(best), false, false);
+    const auto i32 = __builtin_amdgcn_permlane32_swap((unsigned)bidx, (unsigned)bidx, false, false);
+    best = __uint_as_float(b32[0]);
+    bidx = (int)i32[0];
+    take(__uint_as_float(b32[1]), (int)i32[1]);
   }
   const int c = bidx;
   const long sb = ((long)r * a.C + c) * OA_D;
