@@ -240,11 +240,15 @@ __device__ __forceinline__ void find_bin(const RowScan<BPT>& r, int t, int& bin,
 
 // wave 0: exp_idx segment of each cluster (s_base, exclusive prefix of the quotas) and its
 // E-capped quota s_w = min(q_c, E - base_c), clamped at 0
-__device__ __forceinline__ void quota_prefix(const float* qrow, int C, int E, int lane, int* s_base,
-                                             int* s_w) {
+__device__ __forceinline__ void quota_load(const float* qrow, int C, int lane, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = qrow[min(lane * 4 + i, C - 1)];
+}
+__device__ __forceinline__ void quota_scan(const float* qv, int C, int E, int lane, int* s_base,
+                                           int* s_w) {
   int v[4], loc = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = (int)qrow[min(lane * 4 + i, C - 1)];
+  for (int i = 0; i < 4; ++i) v[i] = (int)qv[i];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     v[i] = lane * 4 + i < C ? v[i] : 0;
@@ -265,6 +269,12 @@ __device__ __forceinline__ void quota_prefix(const float* qrow, int C, int E, in
     run += v[i];
   }
   if (lane == 63) s_base[kMaxC] = incl;
+}
+__device__ __forceinline__ void quota_prefix(const float* qrow, int C, int E, int lane, int* s_base,
+                                             int* s_w) {
+  float qv[4];
+  quota_load(qrow, C, lane, qv);
+  quota_scan(qv, C, E, lane, s_base, s_w);
 }
 
 // wave 0: chosen-word segment of each cluster (exclusive prefix of s_t)
@@ -875,17 +885,23 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   auto hd = [&](int i) -> uint32_t { return (kh[i >> 1] >> (16 * (i & 1))) & 0xffffu; };
   auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
 
+  // the quotas and the limb words are requested ahead of the row (loads return in order, so
+  // the prefix would otherwise wait for the whole row)
+  float qv[4];
+  if (wave == 0) quota_load(a.quota + (long)row * C, C, lane, qv);
+  int lwv = 0;
+  if (HEADS && tid < 32) lwv = oa::limb_words(a.limbs, kvr, row % 4)[tid];
   if (nseg > 0) issue(0);       // in flight while P0 runs
 
   // ---- P0: quota prefix, per-cluster state, histogram clear
-  if (wave == 0) quota_prefix(a.quota + (long)row * C, C, E, lane, s_base, s_w);
+  if (wave == 0) quota_scan(qv, C, E, lane, s_base, s_w);
   for (int c = tid; c < kMaxC; c += kThreads) {
     s_t[c] = 0; s_above[c] = 0; s_bcnt[c] = 0; s_klo[c] = 0u; s_khi[c] = ~0u;
     s_sel[c] = 0xffffffffu; s_mode[c] = kModeNone; s_goff[c] = 0; s_gcur[c] = 0; s_ccur[c] = 0;
   }
   for (int i = tid; i < (C * HS) / 4; i += kThreads) reinterpret_cast<int4*>(s_hist)[i] = make_int4(0, 0, 0, 0);
   if (tid == 0) { s_gused = 0; s_fail = a.force_mark; }
-  if (HEADS && tid < 32) s_lw[tid] = oa::limb_words(a.limbs, kvr, row % 4)[tid];
+  if (HEADS && tid < 32) s_lw[tid] = lwv;
 
   // ---- R: the range of the qualifying members' score keys
   uint32_t klo = 0xffffffffu, khi = 0u;
