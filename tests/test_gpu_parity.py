@@ -493,6 +493,31 @@ def test_index_prep_matches_separate_calls(lay4k):
     assert np.array_equal(res[0][2], res[1][2])
 
 
+@pytest.mark.parametrize("C", [128, 200])
+def test_index_update_many_clusters(C):
+    """The index update with more clusters than lanes (C = 128, 200: each lane scores several
+    centroids before the argmax network) equals the restatement bit for bit: codes, cluster ids
+    (also the byte stream), counts, pooled sums and generated lists."""
+    print(f"[case] index update C={C}", flush=True)
+    lay = build_layer(cfg=1, B=1, N=2048, Lmax=2048 + 64, C=C, n_centers=64, dev=DEV)
+    K = lay.K.reshape(-1, lay.Lmax, D)
+    V = lay.V.reshape(-1, lay.Lmax, D)
+    n = lay.N
+    pre = state_np(lay)
+    st = lay.st.clone()
+    limbs = torch.zeros(lay.B * HKV, 16, 32, device=DEV, dtype=torch.int8)
+    fexp = torch.zeros(lay.B * HQ, device=DEV, dtype=torch.int32)
+    ops.index_prep(K, V, st, torch.tensor([n], device=DEV, dtype=torch.int32), RMAX,
+                   lay.q.reshape(-1, D).contiguous(), limbs, fexp)
+    torch.cuda.synchronize()
+    got = st.to_numpy()
+    O.index_update(pre, n - 1, G, RMAX)
+    for f in ("codes", "asg", "nb", "Sk", "Sk2", "Sv", "reclist", "reccnt"):
+        assert np.array_equal(got[f], pre[f]), f"index update: {f} differs"
+    assert np.array_equal(got["asg8"][:, :n], pre["asg"][:, :n].astype(np.uint8))
+    assert (pre["asg"][:, n - 1] >= 64).any()         # a winner past the first lane round
+
+
 def test_dense_decode_vs_oracle(lay4k):
     print("[case] dense", flush=True)
     lay = lay4k
