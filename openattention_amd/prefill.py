@@ -121,9 +121,11 @@ def bases(M: torch.Tensor, HKV: int, G: int):
     """a10 bases from the per-query-head metric M (HQ, D, D): U (HKV, D, 32) = top-32
     eigenvectors of the group mean (methods_eager.py:519-520), W (HQ, D, 16) bf16 = top-16
     eigenvectors * sqrt(eigenvalue) (methods_eager.py:527-528)."""
-    _, Ukv = torch.linalg.eigh(M.view(HKV, G, D, D).mean(1))
-    U = Ukv[..., -RQ:].contiguous()
-    ev, Uq = torch.linalg.eigh(M)
+    # one batched eigh over the HKV group means and the HQ metrics (each matrix is decomposed on
+    # its own; one solver call instead of two)
+    ev_all, U_all = torch.linalg.eigh(torch.cat([M.view(HKV, G, D, D).mean(1), M], 0))
+    U = U_all[:HKV, :, -RQ:].contiguous()
+    ev, Uq = ev_all[HKV:], U_all[HKV:]
     W = (Uq[..., -RC:] * ev[..., -RC:].clamp(min=0).sqrt().unsqueeze(-2)).to(torch.bfloat16).contiguous()
     return U, W
 
