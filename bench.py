@@ -246,7 +246,7 @@ def config5_run(a):
     lib.load()
     from openattention_amd.method import C as CTX, OursHIP
     from openattention_amd.model import NLAYER, LlamaShaped
-    from openattention_amd.prefill import build_row
+    from openattention_amd.prefill import build_rows
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
@@ -267,8 +267,7 @@ def config5_run(a):
             CTX.V.append(V)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            for b in range(B):
-                build_row(m.st[l], b, K[b], V[b], qq[b], T0, static["M"][l], static["inv_freq"], 1.0, l, G)
+            build_rows(m.st[l], K, V, qq, T0, static["M"][l], static["inv_freq"], 1.0, l, G)
             e1.record()
             torch.cuda.synchronize()
             build_ms += e0.elapsed_time(e1)
@@ -361,7 +360,7 @@ def main():
     lib.load()
     from openattention_amd import ops
     from openattention_amd.method import C as CTX, OursHIP
-    from openattention_amd.prefill import build_row
+    from openattention_amd.prefill import build_rows
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
@@ -377,22 +376,16 @@ def main():
     for l in range(L):
         K, V, q, qq, _ = synth.make_layer(3, B, N + n_steps, Lmax, 256, dev, layer=l)
         bmarks = [] if l == L - 1 else None          # the last replica's build is timed per stage
-        for b in range(B):
-            mk = [] if bmarks is not None else None
-            build_row(m.st[l], b, K[b], V[b], qq[b], T0, static["M"][l], static["inv_freq"], 1.0, l, G,
-                      marks=mk)
-            if mk is not None:
-                bmarks.append(mk)
+        build_rows(m.st[l], K, V, qq, T0, static["M"][l], static["inv_freq"], 1.0, l, G, marks=bmarks)
         Ks.append(K)
         Vs.append(V)
         Qs.append(q)
         del qq
         torch.cuda.synchronize()
         if bmarks is not None:
-            for mk in bmarks:
-                for (_, e0), (name, e1) in zip(mk[:-1], mk[1:]):
-                    key = "kmeans" if name.startswith("kmeans") else name
-                    build_ms[key] = build_ms.get(key, 0.0) + e0.elapsed_time(e1)
+            for (_, e0), (name, e1) in zip(bmarks[:-1], bmarks[1:]):
+                key = "kmeans" if name.startswith("kmeans") else name
+                build_ms[key] = build_ms.get(key, 0.0) + e0.elapsed_time(e1)
         log(f"[bench] layer {l} built ({time.time() - t0:.1f}s)")
     CTX.K, CTX.V = Ks, Vs
     n_arr = torch.arange(N, N + n_steps, device=dev, dtype=torch.int32)

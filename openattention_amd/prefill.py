@@ -155,20 +155,60 @@ def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor,
             e.record()
             marks.append((name, e))
 
-    from openattention_amd import ops
     dev = K.device
     if dev.type != "cuda":
         raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
     HKV = K.shape[0]
     HQ = HKV * G
-    C = st.C
-    mark("start")
+    if marks is not None:
+        mark("start")
     M = query_metric(M_pre.to(dev), qrows, T, inv_freq.to(dev), scaling)           # (HQ, D, D)
     U, W = bases(M, HKV, G)
-    r0, q0 = b * HKV, b * HQ
-    st.U[r0:r0 + HKV] = U
-    st.W[q0:q0 + HQ] = W
+    st.U[b * HKV:(b + 1) * HKV] = U
+    st.W[b * HQ:(b + 1) * HQ] = W
     mark("metric_bases")
+    _build_row_device(st, b, K, V, T, layer, G, mark)
+
+
+@torch.no_grad()
+def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int,
+               M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, layer: int,
+               G: int = 4, marks: list | None = None) -> None:
+    """build_row for every batch row of one layer, with the bases of all rows from one batched
+    eigh (the per-row solver call dominates the build otherwise).
+
+    K, V: (B, HKV, >=T, D) bf16; qrows: (B, HQ, Qn, D).  Same state as build_row row by row."""
+    def mark(name):
+        if marks is not None:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            marks.append((name, e))
+
+    dev = K.device
+    if dev.type != "cuda":
+        raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
+    B, HKV = K.shape[0], K.shape[1]
+    HQ = HKV * G
+    mark("start")
+    M = torch.stack([query_metric(M_pre.to(dev), qrows[b], T, inv_freq.to(dev), scaling)
+                     for b in range(B)])                                            # (B, HQ, D, D)
+    U, W = bases(M.reshape(B * HQ, D, D), B * HKV, G)
+    st.U[:B * HKV] = U
+    st.W[:B * HQ] = W
+    mark("metric_bases")
+    for b in range(B):
+        _build_row_device(st, b, K[b], V[b], T, layer, G, mark)
+
+
+def _build_row_device(st, b: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: int, G: int,
+                      mark) -> None:
+    """a11-a13 of batch row b on the HIP kernels, from the row's U and W already in st."""
+    from openattention_amd import ops
+    dev = K.device
+    HKV = K.shape[0]
+    HQ = HKV * G
+    C = st.C
+    r0, q0 = b * HKV, b * HQ
     # a11: QGS codes and scale
     amax = torch.empty(HKV * RQ, device=dev, dtype=torch.int32)
     ops.qgs_codes(K, T, st.U[r0:r0 + HKV], st.codes[r0:r0 + HKV], st.scale[r0:r0 + HKV], amax)

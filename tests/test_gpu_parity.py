@@ -675,6 +675,27 @@ def test_build_cluster_stats_bit_exact(T, C):
     assert np.all(mem.cpu().numpy()[:, T:] == -1)
 
 
+def test_build_rows_equals_build_row():
+    """prefill.build_rows (every row's bases from one batched eigh) leaves the same state as
+    build_row called row by row."""
+    print("[case] build_rows vs build_row", flush=True)
+    from openattention_amd import synth
+    from openattention_amd.prefill import build_row, build_rows
+    B, N, Lmax, C = 2, 2048, 2048 + 64, 8
+    K, V, _q, qq, _ = synth.make_layer(1, B, N, Lmax, 64, DEV)
+    static = synth.static_metric(1, dev="cpu")
+    args = (static["M"][0], static["inv_freq"], float(static["attention_scaling"]), 0, G)
+    a = LayerState(B, HKV, G, Lmax, C, RMAX, DEV)
+    b = LayerState(B, HKV, G, Lmax, C, RMAX, DEV)
+    for r in range(B):
+        build_row(a, r, K[r], V[r], qq[r], N - 1, *args)
+    build_rows(b, K, V, qq, N - 1, *args)
+    torch.cuda.synchronize()
+    sa, sb = a.to_numpy(), b.to_numpy()
+    for f in LayerState.FIELDS:
+        assert np.array_equal(sa[f], sb[f]), f
+
+
 def test_build_row_on_device_matches_restated_stages():
     """prefill.build_row (HIP stages) on a fresh layer leaves a state whose codes are the
     restated codes from its own U and whose statistics and member lists are the restated ones
