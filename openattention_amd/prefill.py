@@ -167,17 +167,20 @@ def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor,
     st.U[b * HKV:(b + 1) * HKV] = U
     st.W[b * HQ:(b + 1) * HQ] = W
     mark("metric_bases")
-    _build_row_device(st, b, K, V, T, layer, G, mark)
+    _build_device(st, b * HKV, K, V, T, layer, G, mark)
 
 
 @torch.no_grad()
 def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int,
                M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, layer: int,
                G: int = 4, marks: list | None = None) -> None:
-    """build_row for every batch row of one layer, with the bases of all rows from one batched
-    eigh (the per-row solver call dominates the build otherwise).
+    """build_row for every batch row of one layer at once: the bases of all rows from one
+    batched eigh (the per-row solver call dominates the build otherwise), then each HIP stage
+    over all B * HQ rows in one launch (the stages are row-parallel: one launch per stage
+    instead of one per stage and row).
 
-    K, V: (B, HKV, >=T, D) bf16; qrows: (B, HQ, Qn, D).  Same state as build_row row by row."""
+    K, V: (B, HKV, >=T, D) bf16, contiguous; qrows: (B, HQ, Qn, D).  Same state as build_row
+    row by row."""
     def mark(name):
         if marks is not None:
             e = torch.cuda.Event(enable_timing=True)
@@ -196,19 +199,20 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
     st.U[:B * HKV] = U
     st.W[:B * HQ] = W
     mark("metric_bases")
-    for b in range(B):
-        _build_row_device(st, b, K[b], V[b], T, layer, G, mark)
+    _build_device(st, 0, K.reshape(B * HKV, K.shape[2], D), V.reshape(B * HKV, V.shape[2], D), T,
+                  layer, G, mark)
 
 
-def _build_row_device(st, b: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: int, G: int,
-                      mark) -> None:
-    """a11-a13 of batch row b on the HIP kernels, from the row's U and W already in st."""
+def _build_device(st, r0: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: int, G: int,
+                  mark) -> None:
+    """a11-a13 on the HIP kernels for the KV rows r0 .. r0 + K.shape[0] of st (their query-head
+    rows G times as many, from G * r0), from the U and W already in st."""
     from openattention_amd import ops
     dev = K.device
     HKV = K.shape[0]
     HQ = HKV * G
     C = st.C
-    r0, q0 = b * HKV, b * HQ
+    q0 = r0 * G
     # a11: QGS codes and scale
     amax = torch.empty(HKV * RQ, device=dev, dtype=torch.int32)
     ops.qgs_codes(K, T, st.U[r0:r0 + HKV], st.codes[r0:r0 + HKV], st.scale[r0:r0 + HKV], amax)
