@@ -193,7 +193,11 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
     B, HKV = K.shape[0], K.shape[1]
     HQ = HKV * G
     mark("start")
-    M = torch.stack([query_metric(M_pre.to(dev), qrows[b], T, inv_freq.to(dev), scaling)
+    # the rotated static metric depends on the layer and T only: formed once for all rows, with
+    # query_metric's arithmetic
+    inv_freq = inv_freq.to(dev)
+    mst = 0.5 * trace_norm(rot_avg(M_pre.to(dev), inv_freq, scaling, T, WIN))
+    M = torch.stack([mst + 0.5 * trace_norm(question_moment(qrows[b], inv_freq, scaling))
                      for b in range(B)])                                            # (B, HQ, D, D)
     U, W = bases(M.reshape(B * HQ, D, D), B * HKV, G)
     st.U[:B * HKV] = U
