@@ -197,8 +197,8 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
     # query_metric's arithmetic
     inv_freq = inv_freq.to(dev)
     mst = 0.5 * trace_norm(rot_avg(M_pre.to(dev), inv_freq, scaling, T, WIN))
-    M = torch.stack([mst + 0.5 * trace_norm(question_moment(qrows[b], inv_freq, scaling))
-                     for b in range(B)])                                            # (B, HQ, D, D)
+    Mq = question_moment(qrows.reshape(B * HQ, qrows.shape[2], D), inv_freq, scaling)
+    M = mst + 0.5 * trace_norm(Mq).view(B, HQ, D, D)                                # (B, HQ, D, D)
     U, W = bases(M.reshape(B * HQ, D, D), B * HKV, G)
     st.U[:B * HKV] = U
     st.W[:B * HQ] = W
