@@ -192,6 +192,10 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
         raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
     B, HKV = K.shape[0], K.shape[1]
     HQ = HKV * G
+    if not (K.is_contiguous() and V.is_contiguous() and K.shape == V.shape and K.dim() == 4):
+        raise ValueError("build_rows: K and V must be contiguous (B, HKV, Lmax, D) tensors")
+    if B * HKV > st.U.shape[0] or qrows.shape[0] != B or qrows.shape[1] != HQ:
+        raise ValueError("build_rows: K, qrows and the state disagree on B, HKV or HQ")
     mark("start")
     # the rotated static metric depends on the layer and T only: formed once for all rows, with
     # query_metric's arithmetic
