@@ -79,7 +79,7 @@ __device__ __forceinline__ float gate_score(float zbar, float s2, float nt) {
 }
 
 // ErrorGate of one row by a 512-thread workgroup into LDS rows (score, n_t).  The wave-wide dot
-// products run eight clusters per wave with all loads in flight; the scalar tails (erf, logs)
+// products run six clusters per wave at a time with all their loads in flight; the scalar tails (erf, logs)
 // then run one cluster per thread.  Dynamic LDS: n_sel * 128 floats of selected keys.
 __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_score, float* s_nt) {
   extern __shared__ float s_k[];
@@ -113,8 +113,8 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
   const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
   const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
   const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
-  // ---- tail statistics and the two dot products, eight clusters per wave
-  constexpr int kBatch = 8;
+  // ---- tail statistics and the two dot products, six clusters per wave at a time
+  constexpr int kBatch = 6;     // 8 spills at the 64-VGPR cap
   for (int c0 = wave; c0 < a.C; c0 += kGateWaves * kBatch) {
     float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
 #pragma unroll
