@@ -904,15 +904,21 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   if (HEADS && tid < 32) s_lw[tid] = lwv;
 
   // ---- R: the range of the qualifying members' score keys
-  uint32_t klo = 0xffffffffu, khi = 0u;
+  // two heads per register on the packed 16-bit ALU: a non-member (head 0) becomes 0xffff after
+  // the wrapping - 1, so it never wins the minimum of the members' heads - 1
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 vlo = {0xffff, 0xffff}, vhi = {0, 0};
   for (int sg = 0; sg < nseg; ++sg) {
     if (sg == 0) keys(0); else load(sg);
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      klo = min(klo, hd(i) ? hd(i) : 0xffffffffu);
-      khi = max(khi, hd(i));
+    for (int j = 0; j < PPT / 2; ++j) {
+      const u16x2 h = __builtin_bit_cast(u16x2, kh[j]);
+      vhi = __builtin_elementwise_max(vhi, h);
+      vlo = __builtin_elementwise_min(vlo, (u16x2)(h - (u16x2){1, 1}));
     }
   }
+  uint32_t khi = max((uint32_t)vhi.x, (uint32_t)vhi.y);
+  uint32_t klo = min((uint32_t)vlo.x, (uint32_t)vlo.y) + 1u;   // with no member khi is 0
   klo = ~oa::wave_max_u32(~klo);
   khi = oa::wave_max_u32(khi);
   if (lane == 0) { s_rlo[wave] = klo; s_rhi[wave] = khi; }
