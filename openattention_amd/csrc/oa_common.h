@@ -195,6 +195,14 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// XCD-aware row of a one-row-per-workgroup launch: workgroups go to the 8 XCDs round-robin
+// (workgroup b to XCD b % 8), each XCD with its own L2; this bijection gives XCD x the rows
+// [x rows/8, (x+1) rows/8), so the query-head rows of one KV row (consecutive rows) share an L2.
+// Identity when rows is not a multiple of 8.
+__device__ __forceinline__ int xcd_row(int b, int rows) {
+  return (rows & 7) ? b : (b & 7) * (rows >> 3) + (b >> 3);
+}
+
 // order-preserving uint32 image of a float (larger float -> larger key, -inf lowest)
 __device__ __forceinline__ uint32_t float_key(float s) {
   const uint32_t b = __float_as_uint(s);

@@ -170,13 +170,14 @@ struct PrepArgs {
 // the token's code; the three touch disjoint data
 __global__ void __launch_bounds__(192) index_prep_kernel(IdxArgs a, PrepArgs p) {
   const int w = threadIdx.x >> 6;
+  const int r = oa::xcd_row(blockIdx.x, gridDim.x);   // a KV row's query rows share one L2 (U)
   if (w == 0)
-    index_assign_row(a, blockIdx.x, threadIdx.x);
+    index_assign_row(a, r, threadIdx.x);
   else if (w == 1)
-    oa::qgs_prep_row(p.q, p.q_stride, a.U, a.scale, a.G, p.limbs, p.fexp, nullptr, blockIdx.x,
+    oa::qgs_prep_row(p.q, p.q_stride, a.U, a.scale, a.G, p.limbs, p.fexp, nullptr, r,
                      threadIdx.x - 64);
-  else if (blockIdx.x % a.G == 0)
-    index_codes_row(a, blockIdx.x, threadIdx.x - 128);
+  else if (r % a.G == 0)
+    index_codes_row(a, r, threadIdx.x - 128);
 }
 
 }  // namespace

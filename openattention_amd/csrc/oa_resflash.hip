@@ -273,7 +273,7 @@ __global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
   int* s_tok = dyn_rf;                                        // NI
   int* s_cid = s_tok + NI;                                    // NI
   float* s_z = reinterpret_cast<float*>(s_cid + NI);          // NI: q.k, later the coefficient
-  const int row = blockIdx.x;
+  const int row = oa::xcd_row(blockIdx.x, gridDim.x);   // a KV row's query rows share one L2
   const int tid = threadIdx.x;
   const int grp = tid >> 4;
   const int sub = tid & 15;
