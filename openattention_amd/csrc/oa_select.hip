@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
   __shared__ int s_tile[kMaxTop];
   __shared__ float s_sc[kMaxTop * 64];
   __shared__ int s_top[kMaxTop];
-  const int row = blockIdx.x;
+  const int row = oa::xcd_row(blockIdx.x, gridDim.x);   // a KV row's query rows share one L2
   const int lane = threadIdx.x;
   const int n = *n_dev;
   int lw[HEADS ? 32 : 1];
@@ -283,7 +283,7 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(void* __restrict__ 
                                                              long sel_stride,
                                                              const int* __restrict__ n_dev, int ns,
                                                              int nl, int k_top, Rescore rs) {
-  const int row = blockIdx.x;
+  const int row = oa::xcd_row(blockIdx.x, gridDim.x);   // a KV row's query rows share one L2
   const int lane = threadIdx.x;
   const int n = *n_dev;
   int lw[HEADS ? 32 : 1];
