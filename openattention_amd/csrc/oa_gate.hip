@@ -114,7 +114,7 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
   const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
   const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
   // ---- tail statistics and the two dot products, six clusters per wave at a time
-  constexpr int kBatch = 6;     // 8 spills at the 64-VGPR cap
+  constexpr int kBatch = 6;     // eight clusters per batch spill at the 64-VGPR cap
   for (int c0 = wave; c0 < a.C; c0 += kGateWaves * kBatch) {
     float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
 #pragma unroll
