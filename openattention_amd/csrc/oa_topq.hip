@@ -830,7 +830,7 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
 
   constexpr int SEG = kThreads * PPT;
   constexpr int NG = PPT / 4;
-  constexpr int CH = 12;
+  constexpr int CH = 18;          // cluster lookups in flight per G batch (36 spills)
   // the single-segment instantiations (PPT <= 36) are launched only for Lmax <= SEG
   constexpr bool kMulti = PPT > 36;
   const int nseg = n > 0 ? (kMulti ? (n + SEG - 1) / SEG : 1) : 0;
