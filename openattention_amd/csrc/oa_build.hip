@@ -320,13 +320,8 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const float* zP, long
 #pragma unroll
     for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) ? 1 : 0;
     // exclusive prefix of the per-lane member counts: the chunk's members in position order
-    int incl = mine;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += y;
-    }
-    const int tot = __shfl(incl, 63, 64);
+    const int incl = oa::wave_incl_scan_i32(mine);
+    const int tot = __builtin_amdgcn_readlane(incl, 63);
     int o = incl - mine;
 #pragma unroll
     for (int e = 0; e < 4; ++e)

@@ -121,6 +121,17 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   const auto r32 = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
   return (int)(r32[0] + r32[1]);
 }
+// inclusive prefix sum over the wave's lanes on the DPP network (row shifts inside each 16-lane
+// row, then row_bcast15 / row_bcast31 carry the row totals upward); integers, so exact
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
 // sum inside each aligned 16-lane group (a DPP row), order m = 1, 2, 4, 8
 __device__ __forceinline__ float group16_sum(float v) {
   v = v + dpp_f32<0xB1>(v);
