@@ -104,12 +104,7 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(ResArgs a) {
       v[i] = c < a.C ? (int)a.quota[(long)row * a.C + c] : 0;
       loc += v[i];
     }
-    int incl = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (tid >= off) incl += t;
-    }
+    const int incl = oa::wave_incl_scan_i32(loc);
     int run = incl - loc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -301,12 +296,7 @@ __global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
       qv4[i] = tid * 4 + i < C ? qv4[i] : 0;
       loc += qv4[i];
     }
-    int incl = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (tid >= off) incl += t;
-    }
+    const int incl = oa::wave_incl_scan_i32(loc);
     int run = incl - loc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -254,12 +254,7 @@ __device__ __forceinline__ void quota_scan(const float* qv, int C, int E, int la
     v[i] = lane * 4 + i < C ? v[i] : 0;
     loc += v[i];
   }
-  int incl = loc;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += t;
-  }
+  const int incl = oa::wave_incl_scan_i32(loc);
   int run = incl - loc;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -282,12 +277,7 @@ __device__ __forceinline__ void chosen_prefix(const int* s_t, int* s_tpre, int l
   int v[4], loc = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) { v[i] = s_t[lane * 4 + i]; loc += v[i]; }
-  int incl = loc;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += t;
-  }
+  const int incl = oa::wave_incl_scan_i32(loc);
   int run = incl - loc;
 #pragma unroll
   for (int i = 0; i < 4; ++i) { s_tpre[lane * 4 + i] = run; run += v[i]; }
