@@ -119,7 +119,7 @@ __device__ __forceinline__ void append_chosen(bool take, uint32_t word, uint32_t
   const int leader = __ffsll((long long)bal) - 1;
   int off = 0;
   if (lane == leader) off = atomicAdd(ctr, __popcll(bal));
-  off = __shfl(off, leader, 64);
+  off = __builtin_amdgcn_readlane(off, leader);   // the leader is uniform
   if (take) cst[off + __popcll(bal & ((1ull << lane) - 1ull))] = word;
 }
 
