@@ -330,7 +330,7 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(void* __restrict__ 
     uint4 cw[KR][2];
 #pragma unroll
     for (int j = 0; j < KR; ++j) {
-      const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+      const int tj = __builtin_amdgcn_readlane(my_tile, min(j, max(k_top - 1, 0)));   // uniform lane
       const int pos = tj * 64 + lane;
       hv[j] = j < k_top ? Hrow[pos] : 0u;
       const uint4* cp = reinterpret_cast<const uint4*>(rs.codes + ((long)kvr * rs.lmax +
@@ -343,7 +343,7 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(void* __restrict__ 
     const uint32_t T = (uint32_t)(kth >> 48);
 #pragma unroll
     for (int j = 0; j < KR; ++j) {
-      const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+      const int tj = __builtin_amdgcn_readlane(my_tile, min(j, max(k_top - 1, 0)));   // uniform lane
       const int pos = tj * 64 + lane;
       cv[j] = -INFINITY;
       if (j < k_top && hv[j] >= T && pos >= ns && pos < dead_hi)
@@ -352,14 +352,14 @@ __global__ void __launch_bounds__(64) topk_select_reg_kernel(void* __restrict__ 
   } else {
 #pragma unroll
     for (int j = 0; j < KR; ++j) {
-      const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+      const int tj = __builtin_amdgcn_readlane(my_tile, min(j, max(k_top - 1, 0)));   // uniform lane
       cv[j] = cand_score<HEADS>(Sv, s_stride, row, tj * 64 + lane, ns, n - nl, rs, lw, inv);
     }
   }
   mine = 0ull;
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
-    const int tj = __shfl(my_tile, min(j, max(k_top - 1, 0)), 64);
+    const int tj = __builtin_amdgcn_readlane(my_tile, min(j, max(k_top - 1, 0)));   // uniform lane
     ck[j] = j < k_top ? tile_key(cv[j], tj * 64 + lane) : 0ull;
     mine = ck[j] > mine ? ck[j] : mine;
   }
