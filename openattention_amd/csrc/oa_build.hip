@@ -362,12 +362,7 @@ __global__ void __launch_bounds__(256) cluster_count_kernel(int T, const uint8_t
     int v[4], loc = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[i] = s_cnt[lane * 4 + i]; loc += v[i]; }
-    int incl = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += y;
-    }
+    const int incl = oa::wave_incl_scan_i32(loc);
     int run = incl - loc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -411,13 +406,8 @@ __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, con
     int mine = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) ? 1 : 0;
-    int incl = mine;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += y;
-    }
-    const int tot = __shfl(incl, 63, 64);
+    const int incl = oa::wave_incl_scan_i32(mine);
+    const int tot = __builtin_amdgcn_readlane(incl, 63);
     int o = incl - mine;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
