@@ -8,8 +8,9 @@
  *     decode step in a hipGraph.
  *   - the current length n (and n0, the prefix length at build time) are read from device
  *     memory (`n_dev`, `n0_dev`: one int32 each), as the reference's graph-safe kernels do.
- *   - return 0 on success, -22 (OA_EINVAL) when a shape/stride/size check fails, otherwise
- *     the hipError_t of the launch.  oa_error_string() gives the text.
+ *   - return 0 on success, -22 (OA_EINVAL) when a shape/stride/size check fails, -28
+ *     (OA_ENOSPC) when a request exceeds a fixed device scratch area, otherwise the hipError_t
+ *     of the launch.  oa_error_string() gives the text.
  *   - head_dim is 128, the QGS rank 32, the QGC rank 16 and the GQA group 4 (Llama-3.1-8B);
  *     other values are rejected.
  *   - rows R = B * HQ query-head rows; kv_rows = B * HKV; row r reads KV row r / (R / kv_rows).
@@ -28,6 +29,7 @@ extern "C" {
 #endif
 
 #define OA_EINVAL (-22)
+#define OA_ENOSPC (-28)
 
 /* ABI version of this header (1). */
 int oa_abi_version(void);
@@ -56,6 +58,25 @@ int oa_flash_decode(const void* q, long q_stride, const void* k, const void* v, 
                     int proxy_per_kv, const float* log_n, long log_n_stride, int n_bins, void* out,
                     long out_stride, int rows, int kv_rows, int head_dim, float sm_scale,
                     int n_split, float* ws_m, float* ws_l, float* ws_acc, void* stream);
+
+/*
+ * oa_flash_decode without workspaces, for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The split partials of n_split > 1 live in a fixed per-GPU
+ * device array of 4 MiB, so rows * n_split * 130 must not exceed 1048576 (else OA_ENOSPC,
+ * nothing launched).  The library allocates nothing: the array is part of the code object,
+ * held on each GPU until the process ends.  Calls that overlap on one GPU (concurrent streams)
+ * share that array and race; calls in stream order do not.  Results equal oa_flash_decode's
+ * with the same arguments.
+ */
+int oa_flash_decode_noalloc(const void* q, long q_stride, const void* k, const void* v,
+                            long kv_stride_b, long kv_stride_s, const int32_t* sel,
+                            long sel_stride, int n_sel, const int32_t* exp_idx, long exp_stride,
+                            int n_exp, const void* kbar, const void* vbar, long kbar_stride_b,
+                            long kbar_stride_n, int kbar_is_f32, int proxy_per_kv,
+                            const float* log_n, long log_n_stride, int n_bins, void* out,
+                            long out_stride, int rows, int kv_rows, int head_dim, float sm_scale,
+                            int n_split, void* stream);
 
 /*
  * Index update of the token at position n-1: its int8 QGS code (KV-head rows), its nearest

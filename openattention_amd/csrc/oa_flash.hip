@@ -16,6 +16,8 @@
 // in a fixed order.
 #include "oa_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -178,21 +180,17 @@ __global__ void __launch_bounds__(OA_D) flash_combine_kernel(const float* ws_m, 
 
 }  // namespace
 
-extern "C" int oa_flash_decode(const void* q, long q_stride,
-                               const void* k, const void* v, long kv_stride_b, long kv_stride_s,
-                               const int32_t* sel, long sel_stride, int n_sel,
-                               const int32_t* exp_idx, long exp_stride, int n_exp,
-                               const void* kbar, const void* vbar, long kbar_stride_b,
-                               long kbar_stride_n, int kbar_is_f32, int proxy_per_kv,
-                               const float* log_n, long log_n_stride, int n_bins,
-                               void* out, long out_stride,
-                               int rows, int kv_rows, int head_dim, float sm_scale,
-                               int n_split, float* ws_m, float* ws_l, float* ws_acc,
-                               void* stream) {
-  if (head_dim != OA_D || rows <= 0 || kv_rows <= 0 || rows % kv_rows != 0) return OA_EINVAL;
-  if (n_sel < 0 || n_exp < 0 || n_bins < 0 || n_split < 1) return OA_EINVAL;
-  if (n_split > 1 && (!ws_m || !ws_l || !ws_acc)) return OA_EINVAL;
-  if (n_bins > 0 && (!kbar || !vbar || !log_n)) return OA_EINVAL;
+namespace {
+
+// Validates the arguments and launches the flash kernel (plus the combine when n_split > 1)
+// with the split partials in ws_m, ws_l (rows * n_split) and ws_acc (rows * n_split * 128).
+int flash_launch(const void* q, long q_stride, const void* k, const void* v, long kv_stride_b,
+                 long kv_stride_s, const int32_t* sel, long sel_stride, int n_sel,
+                 const int32_t* exp_idx, long exp_stride, int n_exp, const void* kbar,
+                 const void* vbar, long kbar_stride_b, long kbar_stride_n, int kbar_is_f32,
+                 int proxy_per_kv, const float* log_n, long log_n_stride, int n_bins, void* out,
+                 long out_stride, int rows, int kv_rows, float sm_scale, int n_split, float* ws_m,
+                 float* ws_l, float* ws_acc, hipStream_t s) {
   FlashArgs a;
   a.q = (const uint16_t*)q; a.q_stride = q_stride;
   a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.kv_sb = kv_stride_b; a.kv_ss = kv_stride_s;
@@ -210,7 +208,6 @@ extern "C" int oa_flash_decode(const void* q, long q_stride,
   if (chunk < 16) chunk = 16;
   a.chunk = chunk;
   a.ws_m = ws_m; a.ws_l = ws_l; a.ws_acc = ws_acc;
-  hipStream_t s = (hipStream_t)stream;
   dim3 grid(rows, n_split);
   if (kbar_is_f32)
     hipLaunchKernelGGL(flash_decode_kernel<float>, grid, dim3(kThreads), 0, s, a);
@@ -221,4 +218,94 @@ extern "C" int oa_flash_decode(const void* q, long q_stride,
   hipLaunchKernelGGL(flash_combine_kernel, dim3(rows), dim3(OA_D), 0, s, ws_m, ws_l, ws_acc,
                      n_split, (uint16_t*)out, out_stride);
   return OA_LAUNCH_STATUS();
+}
+
+int flash_check(int rows, int kv_rows, int head_dim, int n_sel, int n_exp, int n_bins,
+                int n_split, const void* kbar, const void* vbar, const float* log_n) {
+  if (head_dim != OA_D || rows <= 0 || kv_rows <= 0 || rows % kv_rows != 0) return OA_EINVAL;
+  if (n_sel < 0 || n_exp < 0 || n_bins < 0 || n_split < 1) return OA_EINVAL;
+  if (n_bins > 0 && (!kbar || !vbar || !log_n)) return OA_EINVAL;
+  return 0;
+}
+
+// ---- no-allocation variant: the split partials live in a fixed device array ----------------
+// Each GPU holds its own copy of `scratch` for the life of the process.  Host code never uses
+// the array's name as an address: the device address comes from hipGetSymbolAddress, taken
+// once per device (with that device current) on the first call there, and kept in
+// g_scratch_dev.  Every call on one GPU shares that GPU's array, so calls that overlap on one
+// GPU (concurrent streams) race on it.  Each (row, split) slot is written in full by the flash
+// kernel before the combine reads it, so nothing needs clearing between calls.
+constexpr long kScratchFloats = 1L << 20;          // 4 MiB per GPU
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kScratchFloats];
+float* g_scratch_dev[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+int scratch_address(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return OA_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return (int)hipErrorInvalidSymbol;
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int oa_flash_decode(const void* q, long q_stride,
+                               const void* k, const void* v, long kv_stride_b, long kv_stride_s,
+                               const int32_t* sel, long sel_stride, int n_sel,
+                               const int32_t* exp_idx, long exp_stride, int n_exp,
+                               const void* kbar, const void* vbar, long kbar_stride_b,
+                               long kbar_stride_n, int kbar_is_f32, int proxy_per_kv,
+                               const float* log_n, long log_n_stride, int n_bins,
+                               void* out, long out_stride,
+                               int rows, int kv_rows, int head_dim, float sm_scale,
+                               int n_split, float* ws_m, float* ws_l, float* ws_acc,
+                               void* stream) {
+  int st = flash_check(rows, kv_rows, head_dim, n_sel, n_exp, n_bins, n_split, kbar, vbar, log_n);
+  if (st) return st;
+  if (n_split > 1 && (!ws_m || !ws_l || !ws_acc)) return OA_EINVAL;
+  return flash_launch(q, q_stride, k, v, kv_stride_b, kv_stride_s, sel, sel_stride, n_sel,
+                      exp_idx, exp_stride, n_exp, kbar, vbar, kbar_stride_b, kbar_stride_n,
+                      kbar_is_f32, proxy_per_kv, log_n, log_n_stride, n_bins, out, out_stride,
+                      rows, kv_rows, sm_scale, n_split, ws_m, ws_l, ws_acc, (hipStream_t)stream);
+}
+
+extern "C" int oa_flash_decode_noalloc(const void* q, long q_stride, const void* k, const void* v,
+                                       long kv_stride_b, long kv_stride_s, const int32_t* sel,
+                                       long sel_stride, int n_sel, const int32_t* exp_idx,
+                                       long exp_stride, int n_exp, const void* kbar,
+                                       const void* vbar, long kbar_stride_b, long kbar_stride_n,
+                                       int kbar_is_f32, int proxy_per_kv, const float* log_n,
+                                       long log_n_stride, int n_bins, void* out, long out_stride,
+                                       int rows, int kv_rows, int head_dim, float sm_scale,
+                                       int n_split, void* stream) {
+  int st = flash_check(rows, kv_rows, head_dim, n_sel, n_exp, n_bins, n_split, kbar, vbar, log_n);
+  if (st) return st;
+  const long slots = (long)rows * (long)n_split;
+  if (slots * (OA_D + 2) > kScratchFloats) return OA_ENOSPC;
+  float* ws_acc = nullptr;
+  float* ws_m = nullptr;
+  float* ws_l = nullptr;
+  if (n_split > 1) {
+    float* base = nullptr;
+    st = scratch_address(&base);
+    if (st) return st;
+    ws_acc = base;                       // slots * 128, 512-byte aligned rows
+    ws_m = base + slots * OA_D;
+    ws_l = ws_m + slots;
+  }
+  return flash_launch(q, q_stride, k, v, kv_stride_b, kv_stride_s, sel, sel_stride, n_sel,
+                      exp_idx, exp_stride, n_exp, kbar, vbar, kbar_stride_b, kbar_stride_n,
+                      kbar_is_f32, proxy_per_kv, log_n, log_n_stride, n_bins, out, out_stride,
+                      rows, kv_rows, sm_scale, n_split, ws_m, ws_l, ws_acc, (hipStream_t)stream);
 }

@@ -25,6 +25,8 @@ SIGNATURES = {
     "oa_error_string": [I],
     "oa_flash_decode": [P, L, P, P, L, L, P, L, I, P, L, I, P, P, L, L, I, I, P, L, I, P, L,
                         I, I, I, F, I, P, P, P, P],
+    "oa_flash_decode_noalloc": [P, L, P, P, L, L, P, L, I, P, L, I, P, P, L, L, I, I, P, L, I, P,
+                                L, I, I, I, F, I, P],
     "oa_index_update": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
                         P, I, P, P],
     "oa_qgs_prep": [P, L, P, P, I, I, I, I, P, P, P, P],

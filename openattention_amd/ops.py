@@ -67,8 +67,10 @@ def _contig(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
 # ================================================================== OpenAttention.flash
 def flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, *, proxy_per_kv: bool,
                  sm_scale: float, n_bins: int | None = None, n_split: int | None = None,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
-    """Shared body of ours_flash / decode_expand_attention."""
+                 out: torch.Tensor | None = None, noalloc: bool = False) -> torch.Tensor:
+    """Shared body of ours_flash / decode_expand_attention.  noalloc=True calls
+    oa_flash_decode_noalloc (split partials in the library's fixed device array; nothing is
+    allocated, so `out` must be given)."""
     dev = _dev(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n)
     R, D = q.shape
     _need(D == HEAD_DIM, f"head_dim must be {HEAD_DIM}")
@@ -93,6 +95,7 @@ def flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, *, proxy_per_kv: 
     _rows_contig(kbar, "kbar", 8 if kbar.dtype == torch.bfloat16 else 4)
     _need(log_n.dtype == torch.float32 and log_n.shape[0] == R and log_n.stride(-1) == 1,
           "log_n must be fp32 (R, C)")
+    _need(not noalloc or out is not None, "noalloc needs a caller-provided out")
     if out is None:
         out = torch.empty_like(q)
     T = sel_idx.shape[1] + exp_idx.shape[1] + NB
@@ -100,6 +103,16 @@ def flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, *, proxy_per_kv: 
         # few rows cannot fill the GPU: split each row's list (reference: ours_graph.py:276)
         n_split = 1 if R >= 512 else max(2, min(16, (4096 // max(R, 1)), -(-T // 32)))
     n_split = max(1, int(n_split))
+    if noalloc:
+        lib.call("oa_flash_decode_noalloc",
+                 _ptr(q), q.stride(0), _ptr(k), _ptr(v), k.stride(0), k.stride(1),
+                 _ptr(sel_idx), sel_idx.stride(0), sel_idx.shape[1],
+                 _ptr(exp_idx), exp_idx.stride(0), exp_idx.shape[1],
+                 _ptr(kbar), _ptr(vbar), kbar.stride(0), kbar.stride(1),
+                 1 if kbar.dtype == torch.float32 else 0, 1 if proxy_per_kv else 0,
+                 _ptr(log_n), log_n.stride(0), NB, _ptr(out), out.stride(0),
+                 R, BH, D, float(sm_scale), n_split, _stream(dev))
+        return out
     ws = None
     if n_split > 1:
         ws = torch.empty(R * n_split * (HEAD_DIM + 2), device=dev, dtype=torch.float32)

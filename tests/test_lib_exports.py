@@ -50,3 +50,13 @@ def test_argument_checks_reject_before_launch():
     assert L.oa_waterfill(None, None, 4, 300, 10, None, None) == -22          # C > 256
     assert L.oa_topk_select(None, 0, None, 0, 4, 10, None, 5, None, 0, 0, 20, None) == -22   # k > tiles
     assert L.oa_qgs_prep(None, 0, None, None, 32, 8, 128, 16, None, None, None, None) == -22  # rank 16
+
+
+def test_noalloc_flash_rejects_oversized_request_before_launch():
+    """oa_flash_decode_noalloc refuses rows * n_split beyond its fixed device array (-28) before
+    it resolves the array's address or launches anything."""
+    L = lib.load()
+    st = L.oa_flash_decode_noalloc(None, 0, None, None, 0, 0, None, 0, 1, None, 0, 1, None, None, 0,
+                                   0, 0, 0, None, 0, 0, None, 0, 1024, 256, 128, 0.1, 16, None)
+    assert st == -28
+    assert b"scratch" in L.oa_error_string(-28)
