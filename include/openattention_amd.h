@@ -28,10 +28,11 @@
 extern "C" {
 #endif
 
+#define OA_ABI_VERSION 2
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
-/* ABI version of this header (1). */
+/* ABI version of this header (2). */
 int oa_abi_version(void);
 
 /* Text for a status returned by any entry point. */
@@ -46,7 +47,8 @@ const char* oa_error_string(int status);
  *   q (rows, 128) bf16; k, v (kv_rows, Lmax, 128) bf16; sel (rows, n_sel), exp_idx
  *   (rows, n_exp) int32 with -1 padding; kbar, vbar (rows or kv_rows, n_bins, 128) bf16 or
  *   fp32 (kbar_is_f32); log_n (rows, n_bins) fp32 natural log, -inf = no proxy;
- *   out (rows, 128) bf16.  A row with nothing valid returns 0.
+ *   out (rows, 128) bf16, or fp32 when out_is_f32 (the fp32 accumulators unrounded).  A row
+ *   with nothing valid returns 0.
  *   n_split > 1 splits each row's list over n_split workgroups (the reference's split-K
  *   variant for few rows, inference/ours_graph.py:214-262 + graph_runner.py:299-312); the
  *   caller passes workspaces ws_m, ws_l (rows*n_split fp32) and ws_acc (rows*n_split*128).
@@ -56,8 +58,9 @@ int oa_flash_decode(const void* q, long q_stride, const void* k, const void* v, 
                     const int32_t* exp_idx, long exp_stride, int n_exp, const void* kbar,
                     const void* vbar, long kbar_stride_b, long kbar_stride_n, int kbar_is_f32,
                     int proxy_per_kv, const float* log_n, long log_n_stride, int n_bins, void* out,
-                    long out_stride, int rows, int kv_rows, int head_dim, float sm_scale,
-                    int n_split, float* ws_m, float* ws_l, float* ws_acc, void* stream);
+                    long out_stride, int out_is_f32, int rows, int kv_rows, int head_dim,
+                    float sm_scale, int n_split, float* ws_m, float* ws_l, float* ws_acc,
+                    void* stream);
 
 /*
  * oa_flash_decode without workspaces, for callers that cannot allocate device memory (code
@@ -75,8 +78,8 @@ int oa_flash_decode_noalloc(const void* q, long q_stride, const void* k, const v
                             int n_exp, const void* kbar, const void* vbar, long kbar_stride_b,
                             long kbar_stride_n, int kbar_is_f32, int proxy_per_kv,
                             const float* log_n, long log_n_stride, int n_bins, void* out,
-                            long out_stride, int rows, int kv_rows, int head_dim, float sm_scale,
-                            int n_split, void* stream);
+                            long out_stride, int out_is_f32, int rows, int kv_rows, int head_dim,
+                            float sm_scale, int n_split, void* stream);
 
 /*
  * Index update of the token at position n-1: its int8 QGS code (KV-head rows), its nearest
@@ -254,15 +257,16 @@ int oa_residual(const void* K, const void* V, long kv_stride_b, long kv_stride_s
 /*
  * Residual proxies fused with OpenAttention.flash: every K/V row read once, proxies kept in
  * registers (fp32).  Replaces the residual + ours_flash pair of the deployed step
- * (inference/ours_graph.py:324-344).   out (rows, 128) bf16.  qsk (rows, C) from oa_gate_fill,
- * when not null, stands in for the kernel's own q . Sk pass (Sk is then not read).
+ * (inference/ours_graph.py:324-344).   out (rows, 128) bf16, or fp32 when out_is_f32.  qsk
+ * (rows, C) from oa_gate_fill, when not null, stands in for the kernel's own q . Sk pass (Sk is
+ * then not read).
  */
 int oa_residual_flash(const void* q, long q_stride, const void* K, const void* V,
                       long kv_stride_b, long kv_stride_s, int rows, int kv_rows, int head_dim,
                       const int32_t* asg, long asg_stride, const int32_t* sel, long sel_stride,
                       int n_sel, const int32_t* exp_idx, int E, const float* quota,
                       const float* n_t, const float* Sk, const float* Sv, int C, float sm_scale,
-                      void* out, long out_stride, const float* qsk, void* stream);
+                      void* out, long out_stride, int out_is_f32, const float* qsk, void* stream);
 
 /*
  * Dense bf16 decode attention over positions [0, n) (the comparator), split-K over nsplit key

@@ -1,7 +1,7 @@
 // Library-level C-ABI helpers: version and error text.
 #include "oa_common.h"
 
-extern "C" int oa_abi_version(void) { return 1; }
+extern "C" int oa_abi_version(void) { return OA_ABI_VERSION; }
 
 extern "C" const char* oa_error_string(int status) {
   if (status == 0) return "success";

@@ -34,6 +34,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// one output element: fp32 as is, or rounded to bf16
+__device__ __forceinline__ void store_out(void* out, int out_f32, long idx, float v) {
+  if (out_f32)
+    static_cast<float*>(out)[idx] = v;
+  else
+    static_cast<uint16_t*>(out)[idx] = f32_to_bf16(v);
+}
+
 // unpack 8 bf16 (one 16-byte load) into floats
 __device__ __forceinline__ void unpack8(const uint4 w, float* x) {
   x[0] = __uint_as_float(w.x << 16); x[1] = __uint_as_float(w.x & 0xffff0000u);

@@ -31,7 +31,7 @@ struct FlashArgs {
   const int32_t* exq; long exp_stride; int n_exp;
   const void* kbar; const void* vbar; long kb_sb; long kb_sn; int proxy_per_kv;
   const float* logn; long logn_stride; int n_bins;
-  uint16_t* out; long out_stride;
+  void* out; long out_stride; int out_f32;
   int R; int G; float sm_scale;
   int n_split; int chunk;
   float* ws_m; float* ws_l; float* ws_acc;   // split partials: (R*n_split), (R*n_split), (R*n_split, D)
@@ -146,7 +146,7 @@ __global__ void __launch_bounds__(kThreads) flash_decode_kernel(FlashArgs a) {
     }
     if (a.n_split == 1) {
       float o = (L > 0.f) ? A / L : 0.f;
-      a.out[(long)row * a.out_stride + tid] = oa::f32_to_bf16(o);
+      oa::store_out(a.out, a.out_f32, (long)row * a.out_stride + tid, o);
     } else {
       long pr = (long)row * a.n_split + split;
       if (tid == 0) { a.ws_m[pr] = M; a.ws_l[pr] = L; }
@@ -157,7 +157,8 @@ __global__ void __launch_bounds__(kThreads) flash_decode_kernel(FlashArgs a) {
 
 __global__ void __launch_bounds__(OA_D) flash_combine_kernel(const float* ws_m, const float* ws_l,
                                                              const float* ws_acc, int n_split,
-                                                             uint16_t* out, long out_stride) {
+                                                             void* out, long out_stride,
+                                                             int out_f32) {
   const int row = blockIdx.x;
   const int d = threadIdx.x;
   const long base = (long)row * n_split;
@@ -175,22 +176,22 @@ __global__ void __launch_bounds__(OA_D) flash_combine_kernel(const float* ws_m, 
     }
   }
   float o = (L > 0.f) ? A / L : 0.f;
-  out[(long)row * out_stride + d] = oa::f32_to_bf16(o);
+  oa::store_out(out, out_f32, (long)row * out_stride + d, o);
 }
 
 }  // namespace
 
 namespace {
 
-// Validates the arguments and launches the flash kernel (plus the combine when n_split > 1)
-// with the split partials in ws_m, ws_l (rows * n_split) and ws_acc (rows * n_split * 128).
+// Launches the flash kernel (plus the combine when n_split > 1) with the split partials in
+// ws_m, ws_l (rows * n_split) and ws_acc (rows * n_split * 128); the arguments are checked.
 int flash_launch(const void* q, long q_stride, const void* k, const void* v, long kv_stride_b,
                  long kv_stride_s, const int32_t* sel, long sel_stride, int n_sel,
                  const int32_t* exp_idx, long exp_stride, int n_exp, const void* kbar,
                  const void* vbar, long kbar_stride_b, long kbar_stride_n, int kbar_is_f32,
                  int proxy_per_kv, const float* log_n, long log_n_stride, int n_bins, void* out,
-                 long out_stride, int rows, int kv_rows, float sm_scale, int n_split, float* ws_m,
-                 float* ws_l, float* ws_acc, hipStream_t s) {
+                 long out_stride, int out_is_f32, int rows, int kv_rows, float sm_scale,
+                 int n_split, float* ws_m, float* ws_l, float* ws_acc, hipStream_t s) {
   FlashArgs a;
   a.q = (const uint16_t*)q; a.q_stride = q_stride;
   a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.kv_sb = kv_stride_b; a.kv_ss = kv_stride_s;
@@ -199,7 +200,7 @@ int flash_launch(const void* q, long q_stride, const void* k, const void* v, lon
   a.kbar = kbar; a.vbar = vbar; a.kb_sb = kbar_stride_b; a.kb_sn = kbar_stride_n;
   a.proxy_per_kv = proxy_per_kv;
   a.logn = log_n; a.logn_stride = log_n_stride; a.n_bins = n_bins;
-  a.out = (uint16_t*)out; a.out_stride = out_stride;
+  a.out = out; a.out_stride = out_stride; a.out_f32 = out_is_f32 ? 1 : 0;
   a.R = rows; a.G = rows / kv_rows; a.sm_scale = sm_scale;
   a.n_split = n_split;
   const int T = n_sel + n_exp + n_bins;
@@ -216,7 +217,7 @@ int flash_launch(const void* q, long q_stride, const void* k, const void* v, lon
   int st = OA_LAUNCH_STATUS();
   if (st || n_split == 1) return st;
   hipLaunchKernelGGL(flash_combine_kernel, dim3(rows), dim3(OA_D), 0, s, ws_m, ws_l, ws_acc,
-                     n_split, (uint16_t*)out, out_stride);
+                     n_split, out, out_stride, a.out_f32);
   return OA_LAUNCH_STATUS();
 }
 
@@ -267,7 +268,7 @@ extern "C" int oa_flash_decode(const void* q, long q_stride,
                                const void* kbar, const void* vbar, long kbar_stride_b,
                                long kbar_stride_n, int kbar_is_f32, int proxy_per_kv,
                                const float* log_n, long log_n_stride, int n_bins,
-                               void* out, long out_stride,
+                               void* out, long out_stride, int out_is_f32,
                                int rows, int kv_rows, int head_dim, float sm_scale,
                                int n_split, float* ws_m, float* ws_l, float* ws_acc,
                                void* stream) {
@@ -277,7 +278,8 @@ extern "C" int oa_flash_decode(const void* q, long q_stride,
   return flash_launch(q, q_stride, k, v, kv_stride_b, kv_stride_s, sel, sel_stride, n_sel,
                       exp_idx, exp_stride, n_exp, kbar, vbar, kbar_stride_b, kbar_stride_n,
                       kbar_is_f32, proxy_per_kv, log_n, log_n_stride, n_bins, out, out_stride,
-                      rows, kv_rows, sm_scale, n_split, ws_m, ws_l, ws_acc, (hipStream_t)stream);
+                      out_is_f32, rows, kv_rows, sm_scale, n_split, ws_m, ws_l, ws_acc,
+                      (hipStream_t)stream);
 }
 
 extern "C" int oa_flash_decode_noalloc(const void* q, long q_stride, const void* k, const void* v,
@@ -287,8 +289,8 @@ extern "C" int oa_flash_decode_noalloc(const void* q, long q_stride, const void*
                                        const void* vbar, long kbar_stride_b, long kbar_stride_n,
                                        int kbar_is_f32, int proxy_per_kv, const float* log_n,
                                        long log_n_stride, int n_bins, void* out, long out_stride,
-                                       int rows, int kv_rows, int head_dim, float sm_scale,
-                                       int n_split, void* stream) {
+                                       int out_is_f32, int rows, int kv_rows, int head_dim,
+                                       float sm_scale, int n_split, void* stream) {
   int st = flash_check(rows, kv_rows, head_dim, n_sel, n_exp, n_bins, n_split, kbar, vbar, log_n);
   if (st) return st;
   const long slots = (long)rows * (long)n_split;
@@ -307,5 +309,6 @@ extern "C" int oa_flash_decode_noalloc(const void* q, long q_stride, const void*
   return flash_launch(q, q_stride, k, v, kv_stride_b, kv_stride_s, sel, sel_stride, n_sel,
                       exp_idx, exp_stride, n_exp, kbar, vbar, kbar_stride_b, kbar_stride_n,
                       kbar_is_f32, proxy_per_kv, log_n, log_n_stride, n_bins, out, out_stride,
-                      rows, kv_rows, sm_scale, n_split, ws_m, ws_l, ws_acc, (hipStream_t)stream);
+                      out_is_f32, rows, kv_rows, sm_scale, n_split, ws_m, ws_l, ws_acc,
+                      (hipStream_t)stream);
 }

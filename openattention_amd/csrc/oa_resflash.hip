@@ -48,7 +48,7 @@ struct ResArgs {
   const float* Sk; const float* Sv;
   const float* qsk;                             // optional: q . Sk_c from the gate
   int C; float sm_scale;
-  uint16_t* out; long out_stride;               // fused variant
+  void* out; long out_stride; int out_f32;      // fused variant
   uint16_t* kbar_r; uint16_t* vbar_r; float* logn;  // residual-only variant
 };
 
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(ResArgs a) {
       }
     }
     const float o = L > 0.f ? A / L : 0.f;
-    a.out[(long)row * a.out_stride + tid] = oa::f32_to_bf16(o);
+    oa::store_out(a.out, a.out_f32, (long)row * a.out_stride + tid, o);
   }
 }
 
@@ -488,7 +488,7 @@ __global__ void __launch_bounds__(kRFThreads, 8) resflash_kernel(ResArgs a) {
     float A = 0.f;
     for (int g = 0; g < kRFGroups; ++g) A += s_acc[g][tid];
     const float o = L > 0.f ? A / L : 0.f;
-    a.out[(long)row * a.out_stride + tid] = oa::f32_to_bf16(o);
+    oa::store_out(a.out, a.out_f32, (long)row * a.out_stride + tid, o);
   }
 }
 
@@ -496,8 +496,8 @@ int launch(bool fused, const void* q, long q_stride, const void* K, const void* 
            long kv_ss, int rows, int kv_rows, int head_dim, const int32_t* asg, long asg_stride,
            const int32_t* sel, long sel_stride, int n_sel, const int32_t* exp_idx, int E,
            const float* quota, const float* n_t, const float* Sk, const float* Sv, int C,
-           float sm_scale, void* out, long out_stride, void* kbar_r, void* vbar_r, float* logn,
-           const float* qsk, void* stream) {
+           float sm_scale, void* out, long out_stride, int out_f32, void* kbar_r, void* vbar_r,
+           float* logn, const float* qsk, void* stream) {
   if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || C <= 0 || C > kMaxC ||
       n_sel < 0 || n_sel > kMaxSel || E < 0 || E > kMaxE || (kv_ss % 8) != 0 || (kv_sb % 8) != 0)
     return OA_EINVAL;
@@ -509,7 +509,7 @@ int launch(bool fused, const void* q, long q_stride, const void* K, const void* 
   a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
   a.exq = exp_idx; a.E = E; a.quota = quota; a.n_t = n_t; a.Sk = Sk; a.Sv = Sv; a.qsk = qsk;
   a.C = C; a.sm_scale = sm_scale;
-  a.out = (uint16_t*)out; a.out_stride = out_stride;
+  a.out = out; a.out_stride = out_stride; a.out_f32 = out_f32 ? 1 : 0;
   a.kbar_r = (uint16_t*)kbar_r; a.vbar_r = (uint16_t*)vbar_r; a.logn = logn;
   if (fused) {
     const size_t lds = sizeof(int) * 3 * (size_t)(n_sel + E);
@@ -532,12 +532,12 @@ extern "C" int oa_residual_flash(const void* q, long q_stride, const void* K, co
                                  const int32_t* sel, long sel_stride, int n_sel,
                                  const int32_t* exp_idx, int E, const float* quota,
                                  const float* n_t, const float* Sk, const float* Sv, int C,
-                                 float sm_scale, void* out, long out_stride, const float* qsk,
-                                 void* stream) {
+                                 float sm_scale, void* out, long out_stride, int out_is_f32,
+                                 const float* qsk, void* stream) {
   if (!out || (q_stride % 8) != 0) return OA_EINVAL;
   return launch(true, q, q_stride, K, V, kv_stride_b, kv_stride_s, rows, kv_rows, head_dim, asg,
                 asg_stride, sel, sel_stride, n_sel, exp_idx, E, quota, n_t, Sk, Sv, C, sm_scale,
-                out, out_stride, nullptr, nullptr, nullptr, qsk, stream);
+                out, out_stride, out_is_f32, nullptr, nullptr, nullptr, qsk, stream);
 }
 
 extern "C" int oa_residual(const void* K, const void* V, long kv_stride_b, long kv_stride_s,
@@ -550,5 +550,5 @@ extern "C" int oa_residual(const void* K, const void* V, long kv_stride_b, long 
   // the residual-only variant reads no query; K stands in so the pointer is valid
   return launch(false, K, 0, K, V, kv_stride_b, kv_stride_s, rows, kv_rows, head_dim, asg,
                 asg_stride, sel, sel_stride, n_sel, exp_idx, E, quota, n_t, Sk, Sv, C, 0.f,
-                nullptr, 0, kbar_r, vbar_r, log_n, nullptr, stream);
+                nullptr, 0, 0, kbar_r, vbar_r, log_n, nullptr, stream);
 }

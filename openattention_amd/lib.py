@@ -24,9 +24,9 @@ SIGNATURES = {
     "oa_abi_version": [],
     "oa_error_string": [I],
     "oa_flash_decode": [P, L, P, P, L, L, P, L, I, P, L, I, P, P, L, L, I, I, P, L, I, P, L,
-                        I, I, I, F, I, P, P, P, P],
+                        I, I, I, I, F, I, P, P, P, P],
     "oa_flash_decode_noalloc": [P, L, P, P, L, L, P, L, I, P, L, I, P, P, L, L, I, I, P, L, I, P,
-                                L, I, I, I, F, I, P],
+                                L, I, I, I, I, F, I, P],
     "oa_index_update": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
                         P, I, P, P],
     "oa_qgs_prep": [P, L, P, P, I, I, I, I, P, P, P, P],
@@ -44,7 +44,7 @@ SIGNATURES = {
     "oa_topq_heads": [P, L, P, L, P, I, I, I, P, I, P, P, I, P, P, P, L, I, P],
     "oa_residual": [P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, P, P, P, P],
     "oa_residual_flash": [P, L, P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, F, P, L,
-                          P, P],
+                          I, P, P],
     "oa_dense_decode": [P, L, P, P, L, L, I, I, I, I, P, F, I, P, P, P, P, L, P],
     "oa_qgs_codes": [P, L, L, I, I, P, P, L, P, P, P],
     "oa_qgc_project": [P, L, L, I, I, I, P, P, L, P, P, P, P],
@@ -53,11 +53,16 @@ SIGNATURES = {
     "oa_cluster_build": [P, P, L, L, I, I, I, P, L, I, P, P, P, P, P, L, P, P, P],
 }
 
+# must equal oa_abi_version() of the loaded library (OA_ABI_VERSION in the header): a library
+# built from sources with other argument lists would be handed wrong pointers
+ABI_VERSION = 2
+
 _LIB = None
 
 
 def load() -> ct.CDLL:
-    """Load the kernel library; raises if it has not been built (run __graft_entry__.build())."""
+    """Load the kernel library; raises if it has not been built (run __graft_entry__.build()) or
+    was built for another ABI version."""
     global _LIB
     if _LIB is not None:
         return _LIB
@@ -65,6 +70,11 @@ def load() -> ct.CDLL:
     if not os.path.exists(path):
         raise RuntimeError(f"kernel library not built: {path} (run __graft_entry__.build())")
     lib = ct.CDLL(path)
+    lib.oa_abi_version.restype = ct.c_int
+    have = lib.oa_abi_version()
+    if have != ABI_VERSION:
+        raise RuntimeError(f"kernel library {path} has ABI {have}, this binding expects {ABI_VERSION}: "
+                           "rebuild it (__graft_entry__.build())")
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes

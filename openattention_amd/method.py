@@ -82,8 +82,10 @@ class OursHIP(Method):
 
     def __init__(self, a, B, Lmax, dev, n_layers: int = NL, static: dict | None = None,
                  ctx_len: int = CTX_LEN, rule: str = "multibin", fused: bool = True,
-                 groups: int = 1, c_max: int = 256):
+                 groups: int = 1, c_max: int = 256, out_dtype: torch.dtype = torch.bfloat16):
         super().__init__(a, B, Lmax, dev)
+        if out_dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("out_dtype must be torch.bfloat16 or torch.float32")
         if groups < 1 or B % groups:
             raise ValueError(f"groups={groups} must divide B={B}")
         # the batch is split into `groups` sets of whole sequences whose stage chains run on
@@ -114,7 +116,8 @@ class OursHIP(Method):
         self.quota = torch.empty(R, self.Cn, **f32)
         self.qsk = torch.empty(R, self.Cn, **f32)      # q . Sk_c, from the gate to the residual
         self.exp_idx = torch.empty(R, max(self.E, 1), **i32)
-        self.out = torch.empty(R, D, device=dev, dtype=torch.bfloat16)
+        # the step's output rows: bf16 as the reference's, or the fp32 accumulators unrounded
+        self.out = torch.empty(R, D, device=dev, dtype=out_dtype)
         self._sel = {}
         if not fused:
             self.kbar_r = torch.empty(R, self.Cn, D, device=dev, dtype=torch.bfloat16)
@@ -155,6 +158,8 @@ class OursHIP(Method):
         qr = q.reshape(self.R, D)
         if not qr.is_contiguous():
             qr = qr.contiguous()
+        if not 1 <= n <= self.Lmax:
+            raise ValueError(f"n={n} outside [1, Lmax={self.Lmax}]: the step writes position n-1")
         ns, nl, k_top = self.bud.counts(n)
         if n - ns - nl < k_top:
             raise ValueError(f"n={n} too small for sink {ns} + local {nl} + top-k {k_top}")

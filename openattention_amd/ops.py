@@ -98,6 +98,9 @@ def flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, *, proxy_per_kv: 
     _need(not noalloc or out is not None, "noalloc needs a caller-provided out")
     if out is None:
         out = torch.empty_like(q)
+    _need(out.shape == q.shape and out.dtype in (torch.bfloat16, torch.float32) and out.stride(1) == 1,
+          "out must be (R, 128) bf16 or fp32 with contiguous rows")
+    out_f32 = 1 if out.dtype == torch.float32 else 0
     T = sel_idx.shape[1] + exp_idx.shape[1] + NB
     if n_split is None:
         # few rows cannot fill the GPU: split each row's list (reference: ours_graph.py:276)
@@ -110,7 +113,7 @@ def flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, *, proxy_per_kv: 
                  _ptr(exp_idx), exp_idx.stride(0), exp_idx.shape[1],
                  _ptr(kbar), _ptr(vbar), kbar.stride(0), kbar.stride(1),
                  1 if kbar.dtype == torch.float32 else 0, 1 if proxy_per_kv else 0,
-                 _ptr(log_n), log_n.stride(0), NB, _ptr(out), out.stride(0),
+                 _ptr(log_n), log_n.stride(0), NB, _ptr(out), out.stride(0), out_f32,
                  R, BH, D, float(sm_scale), n_split, _stream(dev))
         return out
     ws = None
@@ -125,7 +128,7 @@ def flash_decode(q, k, v, sel_idx, exp_idx, kbar, vbar, log_n, *, proxy_per_kv: 
              _ptr(exp_idx), exp_idx.stride(0), exp_idx.shape[1],
              _ptr(kbar), _ptr(vbar), kbar.stride(0), kbar.stride(1),
              1 if kbar.dtype == torch.float32 else 0, 1 if proxy_per_kv else 0,
-             _ptr(log_n), log_n.stride(0), NB, _ptr(out), out.stride(0),
+             _ptr(log_n), log_n.stride(0), NB, _ptr(out), out.stride(0), out_f32,
              R, BH, D, float(sm_scale), n_split,
              _ptr(ws_m) if ws is not None else None, _ptr(ws_l) if ws is not None else None,
              _ptr(ws_acc) if ws is not None else None, _stream(dev))
@@ -308,10 +311,13 @@ def residual_flash(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out, sm_scale
     BH = K.shape[0]
     if qsk is not None and (qsk.shape != (R, C) or qsk.dtype != torch.float32 or not qsk.is_contiguous()):
         raise ValueError("qsk must be a contiguous (rows, C) float32 tensor")
+    _need(out.shape == (R, HEAD_DIM) and out.dtype in (torch.bfloat16, torch.float32) and out.stride(1) == 1,
+          "out must be (R, 128) bf16 or fp32 with contiguous rows")
     lib.call("oa_residual_flash", _ptr(q), q.stride(0), _ptr(K), _ptr(V), K.stride(0), K.stride(1),
              R, BH, K.shape[2], _ptr(asg), asg.stride(0), _ptr(sel), sel.stride(0), sel.shape[1],
              _ptr(exp_idx), exp_idx.shape[1], _ptr(quota), _ptr(n_t), _ptr(Sk), _ptr(Sv), C,
-             float(sm_scale), _ptr(out), out.stride(0), _ptr(qsk), _stream(dev))
+             float(sm_scale), _ptr(out), out.stride(0), 1 if out.dtype == torch.float32 else 0,
+             _ptr(qsk), _stream(dev))
 
 
 def dense_decode(q, K, V, n_dev, out=None, sm_scale: float | None = None, nsplit: int | None = None,

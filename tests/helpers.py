@@ -61,3 +61,16 @@ def state_np(lay) -> dict:
 
 def budget_for(rho: float, N: int):
     return budget(rho, ctx_len=N if N != 32768 else 32768)
+
+
+def seq_state_np(st, K: torch.Tensor, V: torch.Tensor, b: int) -> dict:
+    """Sequence b's slice of a batched LayerState (its HKV KV rows and HQ query-head rows) and
+    of K, V (B, HKV, Lmax, D), as the numpy dict the CPU restatement's decode_step takes."""
+    kv, qr = slice(b * HKV, (b + 1) * HKV), slice(b * HQ, (b + 1) * HQ)
+    d = {}
+    for f in st.FIELDS:
+        t = getattr(st, f)[kv if f in ("codes", "U", "scale") else qr].detach()
+        d[f] = bf16_np(t) if t.dtype == torch.bfloat16 else t.cpu().contiguous().numpy().copy()
+    d["K"] = bf16_np(K[b])
+    d["V"] = bf16_np(V[b])
+    return d

@@ -34,7 +34,7 @@ def test_binding_matches_header():
 
 def test_library_loads_and_reports():
     L = lib.load()
-    assert L.oa_abi_version() == 1
+    assert L.oa_abi_version() == lib.ABI_VERSION == 2
     assert b"invalid argument" in L.oa_error_string(-22)
     for name in lib.SIGNATURES:
         assert getattr(L, name) is not None
@@ -45,7 +45,7 @@ def test_argument_checks_reject_before_launch():
     L = lib.load()
     # head_dim 64 is rejected by every entry point that takes it
     st = L.oa_flash_decode(None, 0, None, None, 0, 0, None, 0, 1, None, 0, 1, None, None, 0, 0, 0, 0,
-                           None, 0, 0, None, 0, 32, 8, 64, 0.1, 1, None, None, None, None)
+                           None, 0, 0, None, 0, 0, 32, 8, 64, 0.1, 1, None, None, None, None)
     assert st == -22
     assert L.oa_waterfill(None, None, 4, 300, 10, None, None) == -22          # C > 256
     assert L.oa_topk_select(None, 0, None, 0, 4, 10, None, 5, None, 0, 0, 20, None) == -22   # k > tiles
@@ -57,6 +57,6 @@ def test_noalloc_flash_rejects_oversized_request_before_launch():
     it resolves the array's address or launches anything."""
     L = lib.load()
     st = L.oa_flash_decode_noalloc(None, 0, None, None, 0, 0, None, 0, 1, None, 0, 1, None, None, 0,
-                                   0, 0, 0, None, 0, 0, None, 0, 1024, 256, 128, 0.1, 16, None)
+                                   0, 0, 0, None, 0, 0, None, 0, 0, 1024, 256, 128, 0.1, 16, None)
     assert st == -28
     assert b"scratch" in L.oa_error_string(-28)
