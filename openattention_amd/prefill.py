@@ -3,8 +3,8 @@
 Follows the deployed build (inference/methods_eager.py:505-555, inference/ours_fastbuild.py:
 199-304) with the accuracy-path choices where the two differ (k-means seed 1234 + 31(l+1) of
 multibin.py:1894):
-  a10  M_st rotated to the decode position T by the closed-form window average over w = 32
-       positions (StaticTopKMasker._rot_avg, static_top_k.py:103-131); M_q from P <= 64
+  a10  M_st rotated to the decode position T and averaged over a window of w = 32 positions
+       (StaticTopKMasker._rot_avg, static_top_k.py:103-131); M_q from P <= 64
        question rows, each rotated to T (static_top_k.py:185-194); M = 1/2 nt(M_st) + 1/2
        nt(M_q), nt = trace normalisation; U = top-32 eigenvectors of the group-mean M per KV
        head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.  Host torch
@@ -32,77 +32,69 @@ P_ROWS = 64
 ITERS = 4
 
 
-def rope_cs(inv_freq: torch.Tensor, scaling: float, positions: torch.Tensor):
-    """static_top_k.py:91-95"""
-    freqs = positions.float().unsqueeze(-1) * inv_freq.unsqueeze(0)
-    emb = torch.cat([freqs, freqs], -1)
-    return emb.cos() * scaling, emb.sin() * scaling
+def rope_trig(inv_freq: torch.Tensor, positions: torch.Tensor):
+    """cos and sin of the RoPE angles t * theta_i (fp64), theta = [inv_freq, inv_freq]: the
+    rotation by t positions acts on x as R_t x = s (cos * x + sin * rotate_half(x)), s the
+    attention scaling (static_top_k.py:91-100 applies the same rotation to the question rows).
+    positions: (P,) -> two (P, D) tensors."""
+    theta = torch.cat([inv_freq, inv_freq]).to(torch.float64)
+    ang = positions.to(torch.float64).unsqueeze(-1) * theta.to(positions.device)
+    return ang.cos(), ang.sin()
 
 
-def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """static_top_k.py:97-100"""
-    h = x.shape[-1] // 2
-    return x * cos + torch.cat([-x[..., h:], x[..., :h]], -1) * sin
-
-
-def rot_coefs(inv_freq: torch.Tensor, scaling: float, p: int, w: int):
-    """fp64 window-average coefficients of R_t M R_t^T, t in [p, p+w) (static_top_k.py:108-126)."""
-    dev = inv_freq.device
-    th = torch.cat([inv_freq, inv_freq]).double()
-    a = th.unsqueeze(1)
-    b = th.unsqueeze(0)
-
-    def mean_exp(alpha):
-        if w <= 64:
-            t = torch.arange(p, p + w, device=dev, dtype=torch.float64)
-            ph = alpha.unsqueeze(-1) * t
-            return torch.complex(ph.cos().mean(-1), ph.sin().mean(-1))
-        z = torch.polar(torch.ones_like(alpha), alpha)
-        den = 1 - z
-        small = den.abs() < 1e-9
-        s = torch.where(small, torch.full_like(z, float(w)),
-                        (1 - z ** w) / torch.where(small, torch.ones_like(den), den))
-        return s * torch.polar(torch.ones_like(alpha), alpha * p) / w
-
-    Em = mean_exp(a - b)
-    Ep = mean_exp(a + b)
-    cc = 0.5 * (Em.real + Ep.real)
-    ss = 0.5 * (Em.real - Ep.real)
-    cs = 0.5 * (Ep.imag - Em.imag)
-    sc = 0.5 * (Ep.imag + Em.imag)
-    return [x.float() * (scaling * scaling) for x in (cc, ss, cs, sc)]
-
-
-def j_matrix(dim: int, dev) -> torch.Tensor:
-    h = dim // 2
-    J = torch.zeros(dim, dim, device=dev)
-    J[:h, h:] = -torch.eye(h, device=dev)
-    J[h:, :h] = torch.eye(h, device=dev)
-    return J
+def rotate_half(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    """J x along `dim`, J = [[0, -I], [I, 0]]: the second half, negated, then the first half.
+    Along dim -2 of a matrix it is J M; along dim -1 it is M J^T."""
+    a, b = x.chunk(2, dim=dim)
+    return torch.cat([-b, a], dim=dim)
 
 
 def rot_avg(M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, p: int, w: int = WIN):
-    """mean_{t in [p, p+w)} R_t M R_t^T, closed form (static_top_k.py:103-131)."""
-    cc, ss, cs, sc = rot_coefs(inv_freq, scaling, p, w)
-    J = j_matrix(M_pre.shape[-1], M_pre.device)
+    """The static metric seen from decode position p: mean over t in [p, p + w) of
+    R_t M R_t^T (StaticTopKMasker._rot_avg, static_top_k.py:103-131; the explicit loop of
+    multibin.py:1687-1692).
+
+    With R_t = s (diag(c_t) + diag(s_t) J), entry (i, j) of R_t M R_t^T is
+      s^2 (c_i c_j M + c_i s_j (M J^T) + s_i c_j (J M) + s_i s_j (J M J^T))_ij,
+    so the window mean needs only the four window means of the trigonometric outer products,
+    E[c c^T], E[c s^T], E[s c^T] = E[c s^T]^T and E[s s^T]: (w, D) x (D, w) products in fp64."""
+    t = torch.arange(p, p + w, device=M_pre.device, dtype=torch.float64)
+    c, sn = rope_trig(inv_freq.to(M_pre.device), t)                        # (w, D) each
+    s2 = float(scaling) * float(scaling) / w
+    a_cc = (c.T @ c) * s2
+    a_cs = (c.T @ sn) * s2
+    a_ss = (sn.T @ sn) * s2
     M = M_pre.float()
-    return cc * M + cs * (M @ J.T) + sc * (J @ M) + ss * (J @ M @ J.T)
+    JM = rotate_half(M, -2)
+    return (a_cc.float() * M + a_cs.float() * rotate_half(M, -1) + a_cs.T.float() * JM
+            + a_ss.float() * rotate_half(JM, -1))
+
+
+def question_picks(Qn: int, device) -> torch.Tensor:
+    """Indices of the question rows the moment uses: P = min(64, max(Qn - 2, 1)) points spread
+    evenly over [0, Qn - 3], truncated to integers, duplicates dropped -- the reference's pick
+    rule (static_top_k.py:188-189), with torch.linspace's fp32 points so the picks agree."""
+    P = min(P_ROWS, max(Qn - 2, 1))
+    return torch.linspace(0, max(Qn - 3, 0), P, device=device, dtype=torch.float32).long().unique()
 
 
 def question_moment(qrows: torch.Tensor, inv_freq: torch.Tensor, scaling: float) -> torch.Tensor:
-    """M_q from P <= 64 of the question rows (HQ, Qn, D), row i rotated by Qn - i positions
-    (static_top_k.py:185-194)."""
-    Qn = qrows.shape[1]
-    P = min(P_ROWS, max(Qn - 2, 1))
-    pi = torch.linspace(0, max(Qn - 3, 0), P, device=qrows.device).long().unique()
-    qsel = qrows.index_select(1, pi).float()
-    cos, sin = rope_cs(inv_freq, scaling, (Qn - pi).to(qrows.device))
-    qrot = rope_apply(qsel, cos, sin)
-    return torch.matmul(qrot.transpose(-1, -2), qrot) / qrot.shape[1]
+    """M_q = mean over the picked question rows of (R_{Qn-i} q_i)(R_{Qn-i} q_i)^T: row i sits at
+    position T - Qn + i and is advanced by Qn - i positions to the decode position T
+    (static_top_k.py:185-194).  qrows (H, Qn, D) -> (H, D, D) fp32 (rotation and products in
+    fp64)."""
+    Qn = qrows.shape[-2]
+    pick = question_picks(Qn, qrows.device)
+    q = qrows.index_select(-2, pick).to(torch.float64)                    # (H, P, D)
+    c, sn = rope_trig(inv_freq.to(qrows.device), (Qn - pick).to(qrows.device))
+    r = float(scaling) * (c * q + sn * rotate_half(q, -1))
+    return (r.transpose(-1, -2) @ r / pick.numel()).float()
 
 
 def trace_norm(x: torch.Tensor) -> torch.Tensor:
-    return x / torch.diagonal(x, dim1=-2, dim2=-1).sum(-1).clamp(min=1e-12)[..., None, None]
+    """x / tr(x) per matrix, the trace floored at 1e-12 (the blend of methods_eager.py:518)."""
+    tr = torch.diagonal(x, dim1=-2, dim2=-1).sum(-1)
+    return x / tr.clamp(min=1e-12).unsqueeze(-1).unsqueeze(-1)
 
 
 def query_metric(M_pre: torch.Tensor, qrows: torch.Tensor, T: int, inv_freq, scaling) -> torch.Tensor:

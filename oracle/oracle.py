@@ -277,23 +277,103 @@ def cluster_build(K_bf16: np.ndarray, V_bf16: np.ndarray, T: int, asg: np.ndarra
     return nb, Sk, Sk2, Sv, mem, cstart, clen
 
 
+# ------------------------------------------------------------------ a10: metric and bases (fp64)
+# An independent restatement with explicit rotation matrices and numpy's eigh; the product's
+# host code (openattention_amd/prefill.py) forms the same quantities another way, in fp32/fp64
+# torch on the device.  tests/test_a10_pins.py compares the two and pins this one to the
+# mathematics.
+WIN, P_ROWS = 32, 64
+
+
+def rope_matrix(inv_freq: np.ndarray, scaling: float, pos: int) -> np.ndarray:
+    """R_pos = s (diag(cos pos theta) + diag(sin pos theta) J), theta = [inv_freq, inv_freq],
+    J = [[0, -I], [I, 0]] (UTAMultiBinAttention._rope_matrix, multibin.py:1606-1615)."""
+    th = np.concatenate([inv_freq, inv_freq]).astype(np.float64)
+    h = th.size // 2
+    J = np.zeros((2 * h, 2 * h))
+    J[:h, h:] = -np.eye(h)
+    J[h:, :h] = np.eye(h)
+    ang = float(pos) * th
+    return float(scaling) * (np.diag(np.cos(ang)) + np.diag(np.sin(ang)) @ J)
+
+
+def static_metric_at(M_pre: np.ndarray, inv_freq, scaling: float, T: int, w: int = WIN) -> np.ndarray:
+    """mean_{t in [T, T+w)} R_t M R_t^T by the explicit loop (multibin.py:1687-1692), fp64."""
+    M = np.asarray(M_pre, np.float64)
+    acc = np.zeros_like(M)
+    for t in range(T, T + w):
+        R = rope_matrix(inv_freq, scaling, t)
+        acc += R @ M @ R.T
+    return acc / w
+
+
+def question_moment(qrows: np.ndarray, inv_freq, scaling: float) -> np.ndarray:
+    """M_q of static_top_k.py:185-194 / multibin.py:1674-1680: the picked question rows (H, Qn,
+    D), row i advanced by an explicit R_{Qn-i}, averaged outer products, fp64."""
+    import torch
+    Qn = qrows.shape[1]
+    P = min(P_ROWS, max(Qn - 2, 1))
+    picks = torch.linspace(0, max(Qn - 3, 0), P, dtype=torch.float32).long().unique().numpy()
+    q = np.asarray(qrows, np.float64)
+    out = np.zeros((q.shape[0], q.shape[2], q.shape[2]))
+    for i in picks:
+        r = q[:, i, :] @ rope_matrix(inv_freq, scaling, Qn - int(i)).T         # (H, D): R q_i
+        out += r[:, :, None] * r[:, None, :]
+    return out / len(picks)
+
+
+def query_metric(M_pre, qrows, T: int, inv_freq, scaling: float) -> np.ndarray:
+    """M = 1/2 M_st / tr(M_st) + 1/2 M_q / tr(M_q) (methods_eager.py:511-518), fp64."""
+    def nt(x):
+        return x / np.maximum(np.trace(x, axis1=-2, axis2=-1), 1e-12)[..., None, None]
+    return 0.5 * nt(static_metric_at(M_pre, inv_freq, scaling, T)) + 0.5 * nt(question_moment(qrows, inv_freq, scaling))
+
+
+def bases(M: np.ndarray, HKV: int, G: int):
+    """U (HKV, D, 32): eigenvectors of the 32 largest eigenvalues of the mean of each KV
+    group's G metrics (methods_eager.py:519-520, StaticTopKMasker._build share_kv,
+    static_top_k.py:155-162); W (HQ, D, 16): eigenvectors of the 16 largest eigenvalues of each
+    head's metric scaled by sqrt(max(lambda, 0)) (methods_eager.py:527-528,
+    multibin.py:1704-1712).  numpy eigh, fp64; eigenvalues ascending."""
+    Mg = M.reshape(HKV, G, *M.shape[-2:]).mean(1)
+    _, Ug = np.linalg.eigh(Mg)
+    ev, Uq = np.linalg.eigh(M)
+    U = Ug[..., -RQ:]
+    W = Uq[..., -RC:] * np.sqrt(np.maximum(ev[..., -RC:], 0.0))[..., None, :]
+    return U, W
+
+
+def kmeans_init(T: int, C: int, layer: int) -> np.ndarray:
+    """The first C of torch.randperm(T) under the generator seeded 1234 + 31 (layer + 1)
+    (multibin.py:1894-1895)."""
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(1234 + 31 * (layer + 1))
+    return torch.randperm(T, generator=g)[:C].numpy().astype(np.int32)
+
+
 def build_row(st, b: int, K, V, qrows, T: int, M_pre, inv_freq, scaling: float, layer: int,
               G: int = 4, iters: int = 4) -> None:
-    """CPU counterpart of openattention_amd.prefill.build_row: the metric and bases (a10, host
-    torch code shared with the product) and the restated codes, projection, k-means and
-    cluster statistics (a11-a13).  st: a LayerState on the CPU; K, V: (HKV, >=T, 128) bf16."""
+    """CPU counterpart of openattention_amd.prefill.build_row: the restated metric and bases
+    (a10, fp64 above; U stored in fp32 and W in bf16 as the state holds them) and the restated
+    codes, projection, k-means and cluster statistics (a11-a13).  st: a LayerState on the CPU;
+    K, V: (HKV, >=T, 128) bf16 torch tensors; qrows (HQ, Qn, 128)."""
     import torch
-    from openattention_amd import prefill
     HKV = K.shape[0]
     HQ = HKV * G
     C = st.C
-    U, W = prefill.bases(prefill.query_metric(M_pre, qrows, T, inv_freq, scaling), HKV, G)
+    M = query_metric(np.asarray(M_pre, np.float64), qrows.float().numpy(), T,
+                     np.asarray(inv_freq, np.float64), scaling)
+    U64, W64 = bases(M, HKV, G)
+    U = torch.from_numpy(U64.astype(np.float32))
+    W = torch.from_numpy(W64.astype(np.float32)).to(torch.bfloat16)
     kb = K.contiguous().view(torch.int16).numpy().view(np.uint16)
     vb = V.contiguous().view(torch.int16).numpy().view(np.uint16)
     Wb = W.contiguous().view(torch.int16).numpy().view(np.uint16)
     codes, scale = qgs_codes(kb, T, U.numpy())
     zP, cm = qgc_center(qgc_zraw(kb, T, Wb, G))
-    init = prefill.kmeans_init(T, C, layer).numpy().astype(np.int32)
+    if T < C:
+        raise ValueError(f"the prefix ({T} tokens) must hold at least C = {C} tokens")
+    init = kmeans_init(T, C, layer)
     cent = zP[:, init].copy()
     for _ in range(iters):
         asg = kmeans_assign(zP, cent)

@@ -712,6 +712,29 @@ def test_build_rows_equals_build_row():
         assert np.array_equal(sa[f], sb[f]), f
 
 
+def test_build_row_bases_match_fp64_restatement():
+    """The bases the device build stores (metric in torch on the device, rocSOLVER eigh in fp32)
+    span the subspaces of the oracle's fp64 restatement (explicit rotation matrices, numpy
+    eigh): projectors U U^T agree, and W W^T is the fp64 metric's best rank-16 part within the
+    bf16 bar."""
+    print("[case] build_row bases vs fp64 restatement", flush=True)
+    lay = build_layer(cfg=1, B=1, N=2048, Lmax=2048 + 64, C=8, n_centers=64, dev=DEV)
+    M = O.query_metric(lay.static["M"][0].double().numpy(), lay.qq[0].float().cpu().numpy(), lay.T,
+                       lay.static["inv_freq"].double().numpy(), float(lay.static["attention_scaling"]))
+    Uo, Wo = O.bases(M, HKV, G)
+    U = lay.st.U[:HKV].double().cpu().numpy()
+    W = lay.st.W[:HQ].float().double().cpu().numpy()
+    PU = U @ np.swapaxes(U, 1, 2)
+    PUo = Uo @ np.swapaxes(Uo, 1, 2)
+    du = np.abs(PU - PUo).max()
+    WW = W @ np.swapaxes(W, 1, 2)
+    WWo = Wo @ np.swapaxes(Wo, 1, 2)
+    dw = (np.linalg.norm(WW - WWo, axis=(1, 2)) / np.linalg.norm(WWo, axis=(1, 2))).max()
+    print(f"  projector max diff {du:.2e}; W W^T rel diff {dw:.2e}")
+    assert du < 1e-2
+    assert dw < BF16_TOL
+
+
 def test_build_row_on_device_matches_restated_stages():
     """prefill.build_row (HIP stages) on a fresh layer leaves a state whose codes are the
     restated codes from its own U and whose statistics and member lists are the restated ones

@@ -32,31 +32,6 @@ def test_budget_counts_match_reference_accounting():
         budget(0.02)
 
 
-# ------------------------------------------------------------------ metric (a10)
-def test_rot_avg_closed_form_vs_explicit_rotations():
-    """static_top_k.py:103-131 closed form == mean_t R_t M R_t^T with the explicit rotation
-    matrix of multibin.py:1606-1615."""
-    g = torch.Generator().manual_seed(0)
-    A = torch.randn(3, D, D, generator=g)
-    M = A @ A.transpose(-1, -2) / D
-    inv = synth.llama31_inv_freq()
-    p, w = 5000, 32
-    closed = prefill.rot_avg(M, inv, 1.0, p, w)
-    J = prefill.j_matrix(D, "cpu")
-    acc = torch.zeros_like(M, dtype=torch.float64)
-    for t in range(p, p + w):
-        cos, sin = prefill.rope_cs(inv.double(), 1.0, torch.tensor([t], dtype=torch.float64))
-        Rt = torch.diag(cos[0]) + torch.diag(sin[0]) @ J.double()
-        acc += Rt @ M.double() @ Rt.T
-    explicit = (acc / w).float()
-    assert torch.allclose(closed, explicit, atol=2e-5, rtol=1e-4)
-    # the rotation of a row vector by RoPE equals rope_apply
-    x = torch.randn(4, D, generator=g)
-    cos, sin = prefill.rope_cs(inv, 1.0, torch.tensor([37]))
-    Rt = torch.diag(cos[0]) + torch.diag(sin[0]) @ J
-    assert torch.allclose(prefill.rope_apply(x, cos, sin), x @ Rt.T, atol=1e-5)
-
-
 # ------------------------------------------------------------------ build (a11-a13)
 @pytest.fixture(scope="module")
 def lay():
