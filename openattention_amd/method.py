@@ -46,16 +46,52 @@ class Ctx:
 C = Ctx()
 
 
+def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scale: float,
+                      block: int = 512) -> torch.Tensor:
+    """Dense causal attention of the prefill rows of one sequence, as the deployed hook's prefill
+    branch computes it (graph_runner.py:472-475): query (1, HQ, Q, D) at positions K - Q .. K - 1
+    of key, value (1, HKV, K, D); returns (1, HQ, Q, D) in query's dtype.  GQA groups are
+    expanded.  When Q == K the fused flash / memory-efficient kernels run on the cache's dtype;
+    otherwise (or where those kernels are unavailable) blocks of query rows run in fp32, so the
+    score matrix never exceeds (HQ, block, K)."""
+    Gq = query.shape[1] // key.shape[1]
+    Q, K = query.shape[2], key.shape[2]
+    if Q == K:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return TF.scaled_dot_product_attention(query, key.repeat_interleave(Gq, 1),
+                                                       value.repeat_interleave(Gq, 1), is_causal=True,
+                                                       scale=scale)
+        except RuntimeError:
+            pass
+    out = torch.empty_like(query)
+    kf = key[0].float()                                                  # (HKV, K, D)
+    vf = value[0].float()
+    pos = torch.arange(K, device=key.device)
+    for r0 in range(0, Q, block):
+        r1 = min(Q, r0 + block)
+        qf = query[0, :, r0:r1].float().reshape(key.shape[1], Gq * (r1 - r0), -1)   # (HKV, G*b, D)
+        sc = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale              # (HKV, G*b, K)
+        last = (K - Q + torch.arange(r0, r1, device=key.device)).repeat(Gq)          # (G*b,)
+        sc.masked_fill_(pos[None, :] > last[:, None], float("-inf"))
+        o = torch.matmul(torch.softmax(sc, -1), vf)                                 # (HKV, G*b, D)
+        out[0, :, r0:r1] = o.reshape(query.shape[1], r1 - r0, -1).to(query.dtype)
+    return out
+
+
 def attn_hook(module, query, key, value, attention_mask, dropout=0.0, scaling=None, is_causal=None, **kw):
-    """Attention-function hook with device-side positions (graph_runner.py:469-482)."""
+    """Attention-function hook with device-side positions (graph_runner.py:469-482).  Prefill:
+    the batch row C.brow's K, V go into the cache, its causal attention is computed densely and
+    the method builds the row's index.  Decode: the new K, V go to C.kv_idx (= n - 1, on the
+    device) and the method's sparse step runs.  Returns (out (B, T, HQ, D), None)."""
     l = module.layer_idx
     T = query.shape[2]
     if C.phase == "prefill":
         b = C.brow
         C.K[l][b:b + 1, :, :T] = key
         C.V[l][b:b + 1, :, :T] = value
-        out = TF.scaled_dot_product_attention(query.float(), key.float(), value.float(), is_causal=True,
-                                              enable_gqa=True, scale=SC).to(query.dtype)
+        out = prefill_attention(query, key, value, SC if scaling is None else scaling)
         C.method.build(l, b, query, T)
         return out.transpose(1, 2).contiguous(), None
     C.K[l].index_copy_(2, C.kv_idx, key)
@@ -97,6 +133,7 @@ class OursHIP(Method):
         self.Cn, self.E = self.bud.C, self.bud.E
         self.n_layers = n_layers
         self.fused = fused
+        self.sm_scale = SC
         self.static = static
         self.st = [LayerState(B, HKV, G, Lmax, self.Cn, RMAX, dev) for _ in range(n_layers)]
         R, BH = self.R, B * HKV
@@ -143,28 +180,34 @@ class OursHIP(Method):
         return self._sel[NS]
 
     def decode(self, l, q, n, marks: list | None = None):
-        """One decode step of layer l.  `marks`, when given, receives (stage, event) pairs
-        recorded on the current stream after each stage (per-stage timing)."""
-        st = self.st[l]
+        """One decode step of layer l over the cache C.K[l], C.V[l] (the new K, V already at
+        n - 1; n also in C.n_dev).  `marks`, when given, receives (stage, event) pairs recorded
+        on the current stream after each stage (per-stage timing)."""
+        return self.step(self.st[l], C.K[l].view(-1, self.Lmax, D), C.V[l].view(-1, self.Lmax, D), q,
+                         C.n_dev, n, marks)
 
+    def step(self, st, K, V, q, n_dev, n, marks: list | None = None):
+        """The decode stages over an explicit index state and K, V (B * HKV, >= n, D) bf16 rows
+        (any row stride); n on the host (sink/local/top-k counts) and in n_dev on the device."""
         def mark(name):
             if marks is not None:
                 ev = torch.cuda.Event(enable_timing=True)
                 ev.record()
                 marks.append((name, ev))
 
-        K = C.K[l].view(-1, self.Lmax, D)
-        V = C.V[l].view(-1, self.Lmax, D)
         qr = q.reshape(self.R, D)
         if not qr.is_contiguous():
             qr = qr.contiguous()
         if not 1 <= n <= self.Lmax:
             raise ValueError(f"n={n} outside [1, Lmax={self.Lmax}]: the step writes position n-1")
+        if K.shape[0] != self.B * HKV or K.shape[1] < n or V.shape != K.shape:
+            raise ValueError(f"K, V must be ({self.B * HKV}, >= n={n}, {D}) with equal shapes")
         ns, nl, k_top = self.bud.counts(n)
         if n - ns - nl < k_top:
             raise ValueError(f"n={n} too small for sink {ns} + local {nl} + top-k {k_top}")
         NS = ns + nl + k_top
         sel = self.sel_buffer(NS)
+        sc = self.sm_scale
         if self.groups > 1 and marks is None:
             main = torch.cuda.current_stream()
             per = self.B // self.groups
@@ -172,60 +215,60 @@ class OursHIP(Method):
                 s.wait_stream(main)
                 with torch.cuda.stream(s):
                     self._chain(st, K, V, qr, sel, slice(g * per * HQ, (g + 1) * per * HQ),
-                                slice(g * per * HKV, (g + 1) * per * HKV), ns, nl, k_top)
+                                slice(g * per * HKV, (g + 1) * per * HKV), ns, nl, k_top, n_dev)
             for s in self.streams:
                 main.wait_stream(s)
             self.last_sel = sel
             return self.out.view(self.B, HQ, 1, D)
         mark("start")
-        ops.index_prep(K, V, st, C.n_dev, RMAX, qr, self.limbs, self.fexp)
+        ops.index_prep(K, V, st, n_dev, RMAX, qr, self.limbs, self.fexp)
         mark("index_prep")
-        ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM, C.n_dev, ns, nl)
+        ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM, n_dev, ns, nl)
         mark("qgs_scan")
-        ops.topk_select_heads(self.H, self.TM, sel, C.n_dev, ns, nl, k_top, st.codes, self.limbs,
+        ops.topk_select_heads(self.H, self.TM, sel, n_dev, ns, nl, k_top, st.codes, self.limbs,
                               self.fexp)
         mark("topk_select")
         ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota,
-                      SC, self.E, qsk=self.qsk)
+                      sc, self.E, qsk=self.qsk)
         mark("gate_fill")
-        ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, C.n_dev, st.codes, self.limbs,
+        ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, n_dev, st.codes, self.limbs,
                        self.fexp, self.S)
         mark("topq")
         if self.fused:
             ops.residual_flash(qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk,
-                               st.Sv, self.out, SC, qsk=self.qsk)
+                               st.Sv, self.out, sc, qsk=self.qsk)
             mark("residual_flash")
         else:
             ops.residual(K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk, st.Sv,
                          self.kbar_r, self.vbar_r, self.log_n)
             mark("residual")
             ops.flash_decode(qr, K, V, sel, self.exp_idx, self.kbar_r, self.vbar_r, self.log_n,
-                             proxy_per_kv=False, sm_scale=SC, out=self.out)
+                             proxy_per_kv=False, sm_scale=sc, out=self.out)
             mark("flash")
         self.last_sel = sel
         return self.out.view(self.B, HQ, 1, D)
 
-    def _chain(self, st, K, V, qr, sel, rs: slice, ks: slice, ns: int, nl: int, k_top: int):
+    def _chain(self, st, K, V, qr, sel, rs: slice, ks: slice, ns: int, nl: int, k_top: int, n_dev):
         """The decode stages on query-head rows `rs` and their KV rows `ks` (whole sequences)."""
         sub = types.SimpleNamespace(
             codes=st.codes[ks], U=st.U[ks], scale=st.scale[ks], W=st.W[rs], colmean=st.colmean[rs],
             cent=st.cent[rs], asg=st.asg[rs], asg8=st.asg8[rs], nb=st.nb[rs], Sk=st.Sk[rs],
             Sk2=st.Sk2[rs], Sv=st.Sv[rs], reclist=st.reclist[rs], reccnt=st.reccnt[rs])
         Kg, Vg, qg, selg = K[ks], V[ks], qr[rs], sel[rs]
-        ops.index_prep(Kg, Vg, sub, C.n_dev, RMAX, qg, self.limbs[ks], self.fexp[rs])
+        ops.index_prep(Kg, Vg, sub, n_dev, RMAX, qg, self.limbs[ks], self.fexp[rs])
         ops.qgs_scan_heads(sub.codes, self.limbs[ks], self.fexp[rs], self.H[rs], self.TM[rs],
-                           C.n_dev, ns, nl)
-        ops.topk_select_heads(self.H[rs], self.TM[rs], selg, C.n_dev, ns, nl, k_top, sub.codes,
+                           n_dev, ns, nl)
+        ops.topk_select_heads(self.H[rs], self.TM[rs], selg, n_dev, ns, nl, k_top, sub.codes,
                               self.limbs[ks], self.fexp[rs])
         ops.gate_fill(qg, Kg, sub.asg, selg, sub.Sk, sub.Sk2, sub.nb, self.score[rs], self.n_t[rs],
-                      self.quota[rs], SC, self.E, qsk=self.qsk[rs])
-        ops.topq_heads(self.H[rs], sub.asg8, self.quota[rs], self.exp_idx[rs], C.n_dev, sub.codes,
+                      self.quota[rs], self.sm_scale, self.E, qsk=self.qsk[rs])
+        ops.topq_heads(self.H[rs], sub.asg8, self.quota[rs], self.exp_idx[rs], n_dev, sub.codes,
                        self.limbs[ks], self.fexp[rs], self.S[rs])
         if self.fused:
             ops.residual_flash(qg, Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs],
-                               self.n_t[rs], sub.Sk, sub.Sv, self.out[rs], SC, qsk=self.qsk[rs])
+                               self.n_t[rs], sub.Sk, sub.Sv, self.out[rs], self.sm_scale, qsk=self.qsk[rs])
         else:
             ops.residual(Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs], self.n_t[rs],
                          sub.Sk, sub.Sv, self.kbar_r[rs], self.vbar_r[rs], self.log_n[rs])
             ops.flash_decode(qg, Kg, Vg, selg, self.exp_idx[rs], self.kbar_r[rs], self.vbar_r[rs],
-                             self.log_n[rs], proxy_per_kv=False, sm_scale=SC, out=self.out[rs])
+                             self.log_n[rs], proxy_per_kv=False, sm_scale=self.sm_scale, out=self.out[rs])

@@ -405,6 +405,10 @@ def decode_step(st: dict, q_bf16: np.ndarray, n: int, ns: int, nl: int, k: int, 
     semantics: index update of position n-1, QGS scores, top-k, ErrorGate, water-filling,
     within-cluster top-q, residual proxies, merge softmax.  Mutates the index state in st when
     update_index is set.  Returns every intermediate."""
+    Lk = st["K"].shape[1]
+    if not (st["asg"].shape[1] == st["codes"].shape[1] == st["V"].shape[1] == Lk):
+        raise ValueError("decode_step: K, V, asg and codes must share one Lmax (row length); got "
+                         f"{Lk}, {st['V'].shape[1]}, {st['asg'].shape[1]}, {st['codes'].shape[1]}")
     if update_index:
         index_update(st, n - 1, G, rmax)
     zq, fexp, Z = qgs_prep(q_bf16, st["U"], st["scale"], G)

@@ -71,6 +71,11 @@ def seq_state_np(st, K: torch.Tensor, V: torch.Tensor, b: int) -> dict:
     for f in st.FIELDS:
         t = getattr(st, f)[kv if f in ("codes", "U", "scale") else qr].detach()
         d[f] = bf16_np(t) if t.dtype == torch.bfloat16 else t.cpu().contiguous().numpy().copy()
-    d["K"] = bf16_np(K[b])
-    d["V"] = bf16_np(V[b])
+    # the restatement indexes K, V, asg and codes with one row length: K, V at the state's Lmax
+    L = st.Lmax
+    for name, X in (("K", K), ("V", V)):
+        x = bf16_np(X[b][:, :L])
+        if x.shape[1] < L:
+            x = np.concatenate([x, np.zeros((x.shape[0], L - x.shape[1], x.shape[2]), np.uint16)], 1)
+        d[name] = x
     return d

@@ -114,3 +114,25 @@ def test_oracle_decode_step_invariants_and_accuracy(lay):
         r2 = O.decode_step(st2, q, n, ns, nl, k, E, G, np.float32(SC), np.float32(SC2))
         rel = np.linalg.norm(r2["out"] - dense, axis=1) / np.linalg.norm(dense, axis=1)
         assert rel.max() < bound, (E, rel.max())
+
+
+# ------------------------------------------------------------------ accuracy-path surface
+def test_custom_attention_protocol_errors_on_the_host():
+    """UTAMultiBinHIP.custom_attention raises the reference's errors before touching a device:
+    no sparse_meta_data (multibin.py:2886-2887), no layer_idx (static_top_k.py:226-228), and a
+    HIP device is required for the kernels (no CPU fallback)."""
+    from openattention_amd.multibin import UTAMultiBinHIP
+    att = UTAMultiBinHIP(rho=0.01, static=synth.static_metric(1), ctx_len=4096)
+    q = torch.zeros(1, HQ, 1, D, dtype=torch.bfloat16)
+    k = torch.zeros(1, HKV, 4096, D, dtype=torch.bfloat16)
+    mod = object()
+    with pytest.raises(ValueError, match="sparse_meta_data"):
+        att.custom_attention(mod, q, k, k, None, SC, 0.0, layer_idx=0)
+    with pytest.raises(ValueError, match="layer_idx"):
+        att.custom_attention(mod, q, k, k, None, SC, 0.0, sparse_meta_data={})
+    with pytest.raises(ValueError, match="bfloat16"):
+        att.custom_attention(mod, q.float(), k, k, None, SC, 0.0, sparse_meta_data={}, layer_idx=0)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        att.custom_attention(mod, q, k, k, None, SC, 0.0, sparse_meta_data={}, layer_idx=0)
+    with pytest.raises(ValueError, match="static"):
+        UTAMultiBinHIP(rho=0.01)
