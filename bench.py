@@ -45,9 +45,12 @@ def parse():
     p.add_argument("--ctx", type=int, default=32768)
     p.add_argument("--layers", type=int, default=4, help="rotating layer replicas")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--sweep", action="store_true",
+                   help="config 3 at 1/3/5/10%% reads and config 2 (B=1, 1%%): one JSON line per point, "
+                        "no CPU restatement")
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a hipGraph")
-    p.add_argument("--cpu-reps", type=int, default=3)
+    p.add_argument("--cpu-reps", type=int, default=10)
     p.add_argument("--groups", type=int, default=1,
                    help="split the batch into this many sequence groups on their own streams (1, 2, 4 "
                         "measured 299 / 306 / 311 us per layer-step at config 3: one chain is best)")
@@ -323,6 +326,89 @@ def config5_run(a):
         torch.cuda.empty_cache()
 
 
+def cpu_threads() -> int:
+    """The host cores this process may use: the CPU share the box gives one GPU (OMP_NUM_THREADS
+    is set to it there), else every core."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(env))) if env and env.isdigit() else n
+
+
+def cpu_baseline(m, K, V, Q, n: int, B: int, E: int, reps: int, warm: int = 2) -> dict:
+    """The decode step of layer 0 at n restated on the CPU (oracle/, the checker's C restatement,
+    multibin semantics) for every one of the B sequences, index update of position n - 1
+    included, the sequences spread over a thread pool of the host's cores (the C calls release
+    the GIL; sequences are independent).  Median over `reps` timed runs after `warm`; each run
+    decodes from a fresh copy of the state (the copies are made outside the timed region).
+    Beside it, torch's dense attention on the CPU over the same B x 8 x n x 128 bf16 cache with
+    the same threads."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    st = m.st[0]
+    L = st.Lmax
+
+    def np16(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+    fields = ("codes", "U", "scale", "W", "colmean", "cent", "asg", "nb", "Sk", "Sk2", "Sv", "reclist", "reccnt")
+    seqs = []
+    for b in range(B):
+        kv, qr = slice(b * HKV, (b + 1) * HKV), slice(b * HQ, (b + 1) * HQ)
+        d = {}
+        for f in fields:
+            t = getattr(st, f)[kv if f in ("codes", "U", "scale") else qr]
+            d[f] = np16(t) if t.dtype == torch.bfloat16 else t.detach().cpu().contiguous().numpy().copy()
+        d["K"], d["V"] = np16(K[b][:, :L]), np16(V[b][:, :L])
+        seqs.append((d, np16(Q[b].reshape(-1, D))))
+    ns, nl, k = m.bud.counts(n)
+    sc = np.float32(D ** -0.5)
+    sc2 = np.float32(float(sc) ** 2)
+    threads = cpu_threads()
+    mutable = ("codes", "asg", "nb", "Sk", "Sk2", "Sv", "reclist", "reccnt")
+
+    def fresh():
+        return [({f: (v.copy() if f in mutable else v) for f, v in d.items()}, q) for d, q in seqs]
+
+    def one(item):
+        d, q = item
+        O.decode_step(d, q, n, ns, nl, k, E, G, sc, sc2)
+
+    times = []
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        for rep in range(warm + reps):
+            work = fresh()
+            t0 = time.perf_counter()
+            list(pool.map(one, work))
+            dt = time.perf_counter() - t0
+            if rep >= warm:
+                times.append(dt)
+    t_med = statistics.median(times)
+    # torch dense attention on the CPU, same cache and threads
+    torch.set_num_threads(threads)
+    kc = K[:, :, :n].detach().cpu()
+    vc = V[:, :, :n].detach().cpu()
+    qc = Q.detach().cpu()
+    dts = []
+    for rep in range(4):
+        t0 = time.perf_counter()
+        torch.nn.functional.scaled_dot_product_attention(qc, kc, vc, enable_gqa=True, scale=D ** -0.5)
+        if rep:
+            dts.append(time.perf_counter() - t0)
+    dense_cpu = statistics.median(dts)
+    log(f"[bench] cpu: restatement {t_med * 1e3:.1f} ms per layer-step over {B} sequences on {threads} threads; "
+        f"torch dense {dense_cpu * 1e3:.1f} ms")
+    return {"value": round(t_med * 1e6, 1), "unit": f"us/layer-step (B={B}, all sequences)", "cores": threads,
+            "kind": "port",
+            "sample": f"all {B} sequences of layer 0 at n={n}, index update of position n-1 included; "
+                      f"median of {reps} runs after {warm}, sequences over a pool of {threads} threads",
+            "torch_dense_cpu_us": round(dense_cpu * 1e6, 1)}
+
+
 def pmc_calibration():
     """A plain device copy of known size (1 GiB read, 1 GiB written) for scaling the
     FETCH_SIZE / WRITE_SIZE counters: run under rocprofv3 --pmc."""
@@ -351,6 +437,23 @@ def main():
     if a.pmc_calibration:
         pmc_calibration()
         return
+    if a.sweep:
+        # BASELINE config 3 at the reference's four reads, then config 2 (B=1): one line each
+        points = [(32, a.ctx, r, "config3") for r in (0.01, 0.03, 0.05, 0.10)] + [(1, a.ctx, 0.01, "config2")]
+        for B, N, rho, name in points:
+            rec = stage_point(a, B, N, rho, name, cpu=False)
+            print(json.dumps(rec), flush=True)
+            import torch
+            torch.cuda.empty_cache()
+        return
+    print(json.dumps(stage_point(a, a.batch, a.ctx, a.rho, "config3" if a.batch > 1 else "config2",
+                                 cpu=not a.no_cpu_baseline)), flush=True)
+
+
+def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
+    """One measured configuration of the sparse decode stage: build `a.layers` replicas, capture
+    one step of each in a hipGraph, time `a.steps` replays; per-stage breakdown, roofline,
+    dense comparators, optionally the CPU restatement.  Returns the JSON record."""
     import numpy as np
     import torch
 
@@ -364,12 +467,12 @@ def main():
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
-    B, N, L = a.batch, a.ctx, a.layers
+    L = a.layers
     n_steps = a.warmup + a.steps
     Lmax = N + n_steps + 1
     T0 = N - 1
     static = synth.static_metric(L)
-    m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=L, static=static, groups=a.groups)
+    m = OursHIP(types.SimpleNamespace(rho=rho), B, Lmax, dev, n_layers=L, static=static, groups=a.groups)
     Ks, Vs, Qs = [], [], []
     t0 = time.time()
     build_ms = {}
@@ -437,7 +540,7 @@ def main():
     gpu_ms = e0.elapsed_time(e1)
     layer_steps = a.steps * L
     us_layer = gpu_ms * 1e3 / layer_steps
-    log(f"[bench] timed {layer_steps} layer-steps: {us_layer:.1f} us/layer-step (wall {wall * 1e3 / layer_steps:.1f} us)")
+    log(f"[bench] timed {layer_steps} layer-steps: {us_layer:.1f} us/layer-step (wall {wall * 1e6 / layer_steps:.1f} us)")
 
     # ---- per-stage breakdown (eager, events between stages on the launch stream)
     per = {}
@@ -492,11 +595,11 @@ def main():
         K0, V0 = Ks[0].view(-1, Lmax, D), Vs[0].view(-1, Lmax, D)
         q0 = Qs[0].reshape(-1, D).contiguous()
         n_dense = torch.tensor([N], device=dev, dtype=torch.int32)
-        ws = torch.empty(R * 64 * (D + 2), device=dev)
+        ws = torch.empty(R * 256 * (D + 2), device=dev)
         outd = torch.empty_like(q0)
 
         def run_ours():
-            ops.dense_decode(q0, K0, V0, n_dense, out=outd, nsplit=64, ws=ws)
+            ops.dense_decode(q0, K0, V0, n_dense, out=outd, ws=ws)
 
         kd, vd = Ks[0][:, :, :N], Vs[0][:, :, :N]
 
@@ -554,43 +657,10 @@ def main():
         flash_only = round(statistics.median(ts), 1)
         log(f"[bench] flash only (us): {flash_only}")
 
-    # ---- CPU restatement on a bounded sample: sequence b=0 of layer 0
-    cpu = None
-    if not a.no_cpu_baseline:
-        from oracle import oracle as O
-        st = m.st[0]
-        n_cpu = N + n_steps  # every generated token has joined the index; decode one more step
-        rows = slice(0, HQ)
-        kvr = slice(0, HKV)
-
-        def np16(t):
-            return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).copy()
-
-        sub = {f: getattr(st, f)[kvr if f in ("codes", "U", "scale") else rows].detach().cpu().numpy().copy()
-               for f in ("codes", "U", "scale", "colmean", "cent", "asg", "nb", "Sk", "Sk2", "Sv",
-                         "reclist", "reccnt")}
-        sub["W"] = np16(st.W[rows])
-        sub["K"] = np16(Ks[0][0])
-        sub["V"] = np16(Vs[0][0])
-        qn = np16(Qs[0][0].reshape(-1, D))
-        sc = np.float32(D ** -0.5)
-        ns2, nl2, k2 = m.bud.counts(N)
-        times = []
-        for rep in range(a.cpu_reps + 1):
-            work = {k: v.copy() for k, v in sub.items()}
-            c0 = time.perf_counter()
-            O.decode_step(work, qn, N, ns2, nl2, k2, E, G, sc, np.float32(float(sc) ** 2),
-                          update_index=False)
-            dt = time.perf_counter() - c0
-            if rep > 0:
-                times.append(dt)
-        t_seq = statistics.median(times)
-        cpu = {"value": round(t_seq * B * 1e6, 1), "unit": "us/layer-step (B=%d, scaled from one sequence)" % B,
-               "cores": 1, "kind": "port",
-               "sample": f"1 of {B} sequences (32 query-head rows), layer 0, N={N}, decode stage without the "
-                         f"index update; median of {a.cpu_reps} runs, x{B}"}
-        log(f"[bench] cpu: {t_seq * 1e3:.1f} ms per sequence -> {cpu['value']:.0f} us per B={B} layer-step")
-        del n_cpu
+    # ---- CPU restatement of the same step on the host's cores, and torch CPU dense attention
+    cpu_rec = None
+    if cpu:
+        cpu_rec = cpu_baseline(m, Ks[0], Vs[0], Qs[0], N + n_steps, B, E, a.cpu_reps)
 
     rec = {
         "metric": "attn-stage us/layer at B=32, 32K ctx, 1% read; achieved HBM GB/s vs peak",
@@ -605,9 +675,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16 K/V + int8 codes, fp32 accumulate",
         "data": "synthetic (seeded Gaussian-mixture keys, 256 centres/KV head; N(0,1) values)",
-        "config": {"workload": f"config3 sparse decode stage, one layer-step: B={B}, N={N}, rho={a.rho}, "
+        "config": {"workload": f"{name} sparse decode stage, one layer-step: B={B}, N={N}, rho={rho}, "
                                f"C={Cn}, E={E}, sink/local/top-k {ns}/{nl}/{k_top}",
-                   "B": B, "N": N, "rho": a.rho, "C": Cn, "E": E, "layers_rotated": L,
+                   "B": B, "N": N, "rho": rho, "C": Cn, "E": E, "layers_rotated": L,
                    "mode": "eager" if graph is None else "hipgraph", "sequence_groups": a.groups},
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "stage_alg_bytes": stage_alg,
@@ -617,11 +687,14 @@ def main():
         "roofline": roofline,
         "dense_us": dense,
         "speedup_vs_dense": round(dense_best / us_layer, 2) if dense_best else None,
+        # the comparator's own roofline: K and V of every position read once per KV head
+        "dense_frac_of_peak": (round(B * HKV * N * D * 2 * 2 / (dense["ours_splitk"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)
+                               if isinstance(dense.get("ours_splitk"), float) else None),
         "flash_only_us": flash_only,
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_rec,
         "prefill_build": prefill_report(build_ms, B, T0, Cn),
     }
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 if __name__ == "__main__":

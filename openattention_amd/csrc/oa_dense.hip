@@ -6,10 +6,11 @@
 //
 // gfx950 decomposition: grid (splits, B*HKV); a 256-thread workgroup streams one contiguous
 // key chunk of one KV head for all G=4 query heads of that head, so every K/V byte is read
-// once per KV head.  16 lane groups of 16 lanes each take one key at a time (one 16-byte K
-// load and one 16-byte V load per lane), keep four online softmaxes (one per query head),
-// and merge in a fixed order; partial (m, l, acc) go to the caller's workspace and a combine
-// kernel finishes the rows.
+// once per KV head.  16 lane groups of 16 lanes each take four keys per round (one 16-byte K
+// and one 16-byte V load per lane and key, all eight issued first; q.k on the packed bf16 dot
+// instructions, fp32 accumulation), keep four online softmaxes
+// (one per query head, rescaled once per round), and merge in a fixed order; partial
+// (m, l, acc) go to the caller's workspace and a combine kernel finishes the rows.
 #include "oa_common.h"
 
 namespace {
@@ -18,6 +19,24 @@ constexpr int kThreads = 256;
 constexpr int kGroups = kThreads / 16;
 constexpr int GQ = 4;
 constexpr float kLog2e = 1.4426950408889634f;
+
+typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (read once: non-temporal)
+__device__ __forceinline__ uint4 load_nt16(const uint16_t* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// dot of 8 bf16 pairs held as four packed words (v_dot2_f32_bf16, fp32 accumulation)
+__device__ __forceinline__ float dot8_bf16(const uint4 a, const uint4 b) {
+  float p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.x), __builtin_bit_cast(bf16x2, b.x),
+                                            0.f, false);
+  p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.y), __builtin_bit_cast(bf16x2, b.y), p, false);
+  p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.z), __builtin_bit_cast(bf16x2, b.z), p, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.w), __builtin_bit_cast(bf16x2, b.w), p, false);
+}
 
 __global__ void __launch_bounds__(kThreads) dense_split_kernel(
     const uint16_t* __restrict__ q, long q_stride, const uint16_t* __restrict__ K,
@@ -33,12 +52,10 @@ __global__ void __launch_bounds__(kThreads) dense_split_kernel(
   const int n = *n_dev;
   const int t0 = split * chunk;
   const int t1 = min(n, t0 + chunk);
-  float qv[GQ][8];
+  uint4 qv[GQ];                       // the four query heads' 8 dims, packed bf16 pairs
 #pragma unroll
-  for (int g = 0; g < GQ; ++g) {
-    const uint4 w = *reinterpret_cast<const uint4*>(q + (long)(kvr * GQ + g) * q_stride + d0);
-    oa::unpack8(w, qv[g]);
-  }
+  for (int g = 0; g < GQ; ++g)
+    qv[g] = *reinterpret_cast<const uint4*>(q + (long)(kvr * GQ + g) * q_stride + d0);
   const float zs = sm_scale * kLog2e;
   float m[GQ], l[GQ], acc[GQ][8];
 #pragma unroll
@@ -49,25 +66,50 @@ __global__ void __launch_bounds__(kThreads) dense_split_kernel(
   }
   const uint16_t* Kb = K + (long)kvr * kv_sb + d0;
   const uint16_t* Vb = V + (long)kvr * kv_sb + d0;
-  for (int t = t0 + grp; t < t1; t += kGroups) {
-    const uint4 kw = *reinterpret_cast<const uint4*>(Kb + (long)t * kv_ss);
-    const uint4 vw = *reinterpret_cast<const uint4*>(Vb + (long)t * kv_ss);
-    float kx[8], vx[8];
-    oa::unpack8(kw, kx);
-    oa::unpack8(vw, vx);
+  // each lane group takes kKeys keys per round (keys t, t + 16, ...): all their K and V loads
+  // are issued before any arithmetic, and the running maximum is rescaled once per round
+  constexpr int kKeys = 4;
+  for (int tb = t0 + grp; tb < t1; tb += kGroups * kKeys) {
+    uint4 kw[kKeys], vw[kKeys];
+    bool ok[kKeys];
+#pragma unroll
+    for (int u = 0; u < kKeys; ++u) {
+      const int t = tb + u * kGroups;
+      ok[u] = t < t1;
+      const long off = (long)(ok[u] ? t : t0) * kv_ss;
+      kw[u] = load_nt16(Kb + off);
+      vw[u] = load_nt16(Vb + off);
+    }
+    float z[GQ][kKeys];
+#pragma unroll
+    for (int u = 0; u < kKeys; ++u) {
+#pragma unroll
+      for (int g = 0; g < GQ; ++g)
+        z[g][u] = ok[u] ? oa::group16_sum(dot8_bf16(qv[g], kw[u])) * zs : -INFINITY;
+    }
 #pragma unroll
     for (int g = 0; g < GQ; ++g) {
-      float p = 0.f;
+      float mn = m[g];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) p = fmaf(qv[g][i], kx[i], p);
-      const float z = oa::group16_sum(p) * zs;
-      const float mn = fmaxf(m[g], z);
+      for (int u = 0; u < kKeys; ++u) mn = fmaxf(mn, z[g][u]);
       const float al = exp2f(m[g] - mn);
-      const float pe = exp2f(z - mn);
+      l[g] *= al;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pe, vx[i], acc[g][i] * al);
-      l[g] = fmaf(l[g], al, pe);
+      for (int i = 0; i < 8; ++i) acc[g][i] *= al;
       m[g] = mn;
+    }
+#pragma unroll
+    for (int u = 0; u < kKeys; ++u) {
+      float vx[8];
+      oa::unpack8(vw[u], vx);
+#pragma unroll
+      for (int g = 0; g < GQ; ++g) {
+        // key u = 0 of a round is always valid, so m[g] is finite here; masked keys weigh 0
+        const float pe = ok[u] ? exp2f(z[g][u] - m[g]) : 0.f;
+        l[g] += pe;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pe, vx[i], acc[g][i]);
+      }
     }
   }
   __shared__ float s_m[GQ][kGroups], s_l[GQ][kGroups];
