@@ -261,11 +261,15 @@ __device__ __forceinline__ void fill_prologue(const float* score_row, const floa
 }
 
 // quotas floor(min(n_b, lambda w_b)) at the final lo, leftover tokens one each to the live
-// clusters with room in score order (dead clusters as -inf), ties to the lower id
+// clusters with room in score order (dead clusters as -inf), ties to the lower id.
+//
+// The leftover order is a radix select: every cluster with room has the distinct 40-bit key
+// (order-preserving key of its score << 8) | (255 - id), larger = earlier; the rem-th largest
+// key is found bit by bit from the top (40 wave-wide counts), and the clusters at or above it
+// take one more token -- the same set as ranking every cluster against every other.
 template <int NS>
 __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, double budget, int lane,
-                                              float* quota_row, double* s_key) {
-  const double NEG = __longlong_as_double((long long)0xfff0000000000000ULL);
+                                              float* quota_row) {
   double qv[NS];
   const double el = oa::det_exp(f.lo);
   for (int j = 0; j < NS; ++j) {
@@ -275,34 +279,37 @@ __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, dou
   const double qsum = canon_sum<NS>(qv, C, lane);
   double rem = fmin(f.tot, budget) - qsum;
   rem = rint(rem > 0.0 ? rem : 0.0);
-  // rank keys: live scores are floats (widened exactly), so the order-preserving 32-bit key of
-  // the float orders them; dead clusters take key 0 (below every live key, like -inf);
-  // clusters without room take no rank (0xffffffff marks them)
+  unsigned long long u[NS];
+  bool room[NS];
+  int total = 0;
+#pragma unroll
   for (int j = 0; j < NS; ++j) {
-    int c = lane + 64 * j;
-    if (c < C) {
-      const unsigned kf = f.ok[j] ? oa::float_key((float)f.sv[j]) : 0u;
-      s_key[c] = __longlong_as_double((long long)(qv[j] < f.cap[j] ? kf : 0xffffffffu));
+    const int c = lane + 64 * j;
+    // dead clusters rank below every live one (key 0; they have no room anyway); -0 and +0 are
+    // one score (a tie, settled by the id)
+    const float sf = (float)f.sv[j];
+    const unsigned kf = f.ok[j] ? oa::float_key(sf == 0.f ? 0.f : sf) : 0u;
+    room[j] = c < C && qv[j] < f.cap[j] && kf != 0xffffffffu;
+    u[j] = ((unsigned long long)kf << 8) | (unsigned long long)(255 - (c & 255));
+    total += __popcll(__ballot(room[j]));
+  }
+  unsigned long long t = 0ull;                      // keys >= t get one more
+  bool any = rem > 0.0;
+  if (any && rem < (double)total) {
+    int need = (int)rem;
+    for (int bit = 39; bit >= 0; --bit) {
+      const unsigned long long cand = t | (1ull << bit);
+      int cnt = 0;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) cnt += __popcll(__ballot(room[j] && (u[j] >> bit) == (cand >> bit)));
+      if (cnt >= need) t = cand;
+      else need -= cnt;
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  const unsigned* s_k32 = reinterpret_cast<const unsigned*>(s_key);   // low words
+#pragma unroll
   for (int j = 0; j < NS; ++j) {
-    int c = lane + 64 * j;
-    if (c >= C) continue;
-    double add = 0.0;
-    const unsigned kc = s_k32[2 * c];
-    if (kc != 0xffffffffu) {
-      int rank = 0;
-#pragma unroll 8
-      for (int c2 = 0; c2 < C; ++c2) {
-        const unsigned k2 = s_k32[2 * c2];
-        rank += (k2 != 0xffffffffu && (k2 > kc || (k2 == kc && c2 < c))) ? 1 : 0;
-      }
-      if ((double)rank < rem) add = 1.0;
-    }
-    quota_row[c] = (float)(qv[j] + add);
+    const int c = lane + 64 * j;
+    if (c < C) quota_row[c] = (float)(qv[j] + ((any && room[j] && u[j] >= t) ? 1.0 : 0.0));
   }
 }
 
@@ -323,7 +330,7 @@ __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, dou
 template <int NS>
 __device__ __forceinline__ void waterfill_row(const float* score_row, const float* nt_row,
                                               float* quota_row, int C, double budget, int lane,
-                                              double* s_key, double2* s_cw) {
+                                              double2* s_cw) {
   // ---- live clusters, weights and the bracket of log(lambda)
   FillState<NS> f;
   fill_prologue<NS>(score_row, nt_row, C, lane, f);
@@ -398,7 +405,7 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
   f.lo = lo;
   f.hi = hi;
   // ---- quotas, leftover tokens by score order
-  fill_epilogue<NS>(f, C, budget, lane, quota_row, s_key);
+  fill_epilogue<NS>(f, C, budget, lane, quota_row);
 }
 
 // one row per wave: the fill is a serial chain, so rows (not lanes) carry the parallelism
@@ -407,11 +414,10 @@ __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__
                                                        const float* __restrict__ n_t, long in_stride,
                                                        float* __restrict__ quota, long q_stride, int C,
                                                        double budget) {
-  __shared__ double s_key[kMaxC];
   __shared__ double2 s_cw[kMaxC];
   const int row = blockIdx.x;
   waterfill_row<NS>(score + (long)row * in_stride, n_t + (long)row * in_stride,
-                    quota + (long)row * q_stride, C, budget, threadIdx.x, s_key, s_cw);
+                    quota + (long)row * q_stride, C, budget, threadIdx.x, s_cw);
 }
 
 int launch_fill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,
@@ -422,6 +428,9 @@ int launch_fill(const float* score, const float* n_t, int rows, int C, int budge
                        (long)C, C, (double)budget);
   else if (ns == 2)
     hipLaunchKernelGGL(waterfill_kernel<2>, dim3(rows), dim3(64), 0, s, score, n_t, (long)C, quota,
+                       (long)C, C, (double)budget);
+  else if (ns == 3)
+    hipLaunchKernelGGL(waterfill_kernel<3>, dim3(rows), dim3(64), 0, s, score, n_t, (long)C, quota,
                        (long)C, C, (double)budget);
   else
     hipLaunchKernelGGL(waterfill_kernel<4>, dim3(rows), dim3(64), 0, s, score, n_t, (long)C, quota,

@@ -509,6 +509,34 @@ def test_index_prep_matches_separate_calls(lay4k):
     assert np.array_equal(res[0][2], res[1][2])
 
 
+@pytest.mark.parametrize("C,E", [(8, 27), (64, 216), (100, 679), (192, 1335), (256, 2877), (256, 40)])
+def test_waterfill_rows_with_ties_dead_and_full_clusters(C, E):
+    """Water-filling on rows built for the leftover tokens: scores on a coarse grid (ties go to
+    the lower cluster id), dead clusters (n_t <= 1), clusters that the fill leaves without room,
+    rows whose live total is below E (every cluster gets its whole tail), all-dead rows.  The
+    integer quotas equal the restatement's on every row, for 1 to 4 cluster slots per lane."""
+    print(f"[case] waterfill C={C} E={E}", flush=True)
+    rng = np.random.default_rng(1000 * C + E)
+    R = 96
+    score = rng.normal(0.0, 2.0, (R, C)).astype(np.float32)
+    score[::2] = np.round(score[::2] * 2.0) / 2.0
+    score[1::4] = 0.25                                    # every score tied
+    n_t = rng.integers(0, 3 * max(E // C, 2) + 4, (R, C)).astype(np.float32)
+    n_t[:, ::7] = 0.0
+    n_t[:, 3::11] = 1.0
+    n_t[5] = np.minimum(n_t[5], 2.0)                      # live total below E
+    n_t[6] = 0.0                                          # no live cluster
+    n_t[7] = 500.0                                        # every cluster far above its share
+    want = O.waterfill(score, n_t, E)
+    quota = torch.empty(R, C, device=DEV)
+    ops.waterfill(torch.from_numpy(score).to(DEV), torch.from_numpy(n_t).to(DEV), quota, E)
+    torch.cuda.synchronize()
+    got = quota.cpu().numpy()
+    bad = np.nonzero((got != want).any(1))[0]
+    assert bad.size == 0, f"rows {bad[:8]} differ"
+    assert (got.sum(1) <= E).all()
+
+
 @pytest.mark.parametrize("C", [128, 200])
 def test_index_update_many_clusters(C):
     """The index update with more clusters than lanes (C = 128, 200: each lane scores several
