@@ -38,9 +38,10 @@
 //   P5  one wave per staged cluster picks the `need` best staged keys (repeated wave maxima for
 //       small `need`, an MSB-first bitwise search on ballot counts otherwise, over the key bits
 //       the bin leaves open); equal keys beyond the staging space are ranked by position in a
-//       block-wide bitwise search that streams the row again;
+//       block-wide bitwise search that streams the row again.  (The linear-bin kernel below
+//       ranks the keys of clusters with at most 128 staged keys one thread per key instead);
 //   P6  every chosen (cluster << 24 | position) word gets its rank among its cluster's words by
-//       position (counting, or a bitonic sort when more than 1024 were chosen), lands in an
+//       position (counting, or a bitonic sort when one cluster has more than 1024), lands in an
 //       LDS copy of the exp_idx row, and the row is written out once (-1 where a segment is
 //       short).
 // Rows longer than 1024 * PPT positions are processed in segments that are re-read from
@@ -60,7 +61,7 @@ constexpr int kMaxE = 4096;
 constexpr int kMaxPos = 1 << 24;               // positions (< 2^24 - 1) are packed into 24 bits
 constexpr int kExtractMax = 40;                // need above this: bitwise threshold search
 constexpr int kUCapMax = 16384;                // gathered members (u64)
-constexpr int kRankMax = 1024;                 // above this many chosen words: bitonic sort
+constexpr int kRankTMax = 1024;                // a cluster with more chosen words: bitonic sort
 constexpr int kUPT = 8;                        // gathered entries per thread handled together
 constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
 constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster with no quota
@@ -102,8 +103,17 @@ __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
 // (2^w - 1)): they share klo's top 32 - w bits and, since positions are below 2^24, bits 24..31
 // of the inverted position.  A bitwise threshold search starts from those bits (bin_floor) and
 // decides only the others, from bit 31 + w down, skipping 31..24.
-__device__ __forceinline__ unsigned long long bin_floor(uint32_t klo) {
-  return ((unsigned long long)klo << 32) | 0xff000000ull;
+__device__ __forceinline__ unsigned long long bin_floor(uint32_t klo, uint32_t top8 = 0xffu) {
+  return ((unsigned long long)klo << 32) | ((unsigned long long)top8 << 24);
+}
+// the linear-bin kernel's staged keys carry 255 - cluster in bits 24..31 instead (constant within
+// a cluster, so the order of one cluster's keys is unchanged): one thread can then rank a key
+// against the rest of its cluster's keys
+__device__ __forceinline__ unsigned long long staged_key(uint32_t key, int c, int pos) {
+  return ((unsigned long long)key << 32) | ((uint32_t)(255 - c) << 24) | (0xffffffu - (uint32_t)pos);
+}
+__device__ __forceinline__ uint32_t key_pos(unsigned long long x) {
+  return 0xffffffu - (uint32_t)(x & 0xffffffull);
 }
 __device__ __forceinline__ int bin_top_bit(uint32_t klo, uint32_t khi) {
   const int w = __popc(klo ^ khi);
@@ -134,8 +144,7 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
     int rank = 0;
     for (int m = 0; m < cnt; ++m) rank += src[m] > x ? 1 : 0;
     const bool take = lane < cnt && rank < need;
-    const uint32_t pos = 0xffffffffu - (uint32_t)(x & 0xffffffffull);
-    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctr, lane);
+    append_chosen(take, ((uint32_t)c << 24) | key_pos(x), cst, ctr, lane);
     return;
   }
   unsigned long long x[KR];
@@ -170,8 +179,7 @@ __device__ void select_staged(const unsigned long long* src, int cnt, int need, 
 #pragma unroll
   for (int j = 0; j < KR; ++j) {
     const bool take = x[j] != 0ull && x[j] >= T;
-    const uint32_t pos = 0xffffffffu - (uint32_t)(x[j] & 0xffffffffull);
-    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctr, lane);
+    append_chosen(take, ((uint32_t)c << 24) | key_pos(x[j]), cst, ctr, lane);
   }
 }
 
@@ -193,8 +201,7 @@ __device__ void select_staged_loop(const unsigned long long* src, int cnt, int n
     const int j = b0 + lane;
     const unsigned long long x = src[min(j, cnt - 1)];
     const bool take = j < cnt && x >= T;
-    const uint32_t pos = 0xffffffffu - (uint32_t)(x & 0xffffffffull);
-    append_chosen(take, ((uint32_t)c << 24) | pos, cst, ctr, lane);
+    append_chosen(take, ((uint32_t)c << 24) | key_pos(x), cst, ctr, lane);
   }
 }
 
@@ -281,7 +288,8 @@ __device__ __forceinline__ void chosen_prefix(const int* s_t, int* s_tpre, int l
   int run = incl - loc;
 #pragma unroll
   for (int i = 0; i < 4; ++i) { s_tpre[lane * 4 + i] = run; run += v[i]; }
-  if (lane == 63) s_tpre[kMaxC] = incl;
+  const int mx = (int)oa::wave_max_u32((unsigned)max(max(v[0], v[1]), max(v[2], v[3])));
+  if (lane == 63) { s_tpre[kMaxC] = incl; s_tpre[kMaxC + 1] = mx; }
 }
 
 // P5 for every staged cluster, one wave per cluster: the `need` best of its staged keys join
@@ -292,19 +300,49 @@ __device__ __forceinline__ void select_all_staged(int C, int wave, int lane, con
                                                   const unsigned long long* s_g, const int* s_goff,
                                                   uint32_t* s_cst, const int* s_tpre,
                                                   const unsigned* s_klo, const unsigned* s_khi,
-                                                  int* s_ccur) {
+                                                  int* s_ccur, bool tagged = false,
+                                                  int min_cnt = -1) {
   for (int c = wave; c < C; c += kWaves) {
     if (s_mode[c] != kModeStaged) continue;
     const int cnt = s_bcnt[c];
+    if (cnt <= min_cnt) continue;
     const int need = s_t[c] - s_above[c];
     const unsigned long long* src = s_g + s_goff[c];
     uint32_t* dst = s_cst + s_tpre[c];
-    const unsigned long long fl = bin_floor(s_klo[c]);
+    const unsigned long long fl = bin_floor(s_klo[c], tagged ? 255u - (unsigned)c : 0xffu);
     const int top = bin_top_bit(s_klo[c], s_khi[c]);
     if (cnt <= 64) select_staged<1>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
     else if (cnt <= 256) select_staged<4>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
     else if (cnt <= 512) select_staged<8>(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
     else select_staged_loop(src, cnt, need, c, fl, top, dst, &s_ccur[c], lane);
+  }
+}
+
+// P5 for the staged clusters of at most kP5Thread keys, one thread per staged key (keys tagged
+// with their cluster, staged_key): a key's rank is the number of larger keys of its cluster
+// (the keys are distinct), counted over LDS reads that the lanes of a wave mostly share; the
+// `need` best (rank < need) join the cluster's chosen words.  Balanced over the block however
+// the keys fall into clusters.
+constexpr int kP5Thread = 128;
+__device__ __forceinline__ void select_small_staged(int tid, int gused, const int* s_bcnt,
+                                                    const int* s_t, const int* s_above,
+                                                    const unsigned long long* s_g,
+                                                    const int* s_goff, uint32_t* s_cst,
+                                                    const int* s_tpre, int* s_ccur) {
+  for (int j = tid; j < gused; j += kThreads) {
+    const unsigned long long x = s_g[j];
+    const int c = 255 - (int)(((uint32_t)x) >> 24);
+    const int cnt = s_bcnt[c];
+    if (cnt > kP5Thread) continue;
+    const unsigned long long* src = s_g + s_goff[c];
+    int rank = 0, m = 0;
+    for (; m + 4 <= cnt; m += 4) {
+      const unsigned long long y0 = src[m], y1 = src[m + 1], y2 = src[m + 2], y3 = src[m + 3];
+      rank += (y0 > x) + (y1 > x) + (y2 > x) + (y3 > x);
+    }
+    for (; m < cnt; ++m) rank += src[m] > x ? 1 : 0;
+    if (rank < s_t[c] - s_above[c])
+      s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | key_pos(x);
   }
 }
 
@@ -318,7 +356,9 @@ __device__ __forceinline__ void rank_and_write(int E, int tid, const int* s_base
   for (int sl = tid; sl < E; sl += kThreads) s_out[sl] = -1;
   oa::lds_barrier();
   const int total = s_tpre[kMaxC];   // == sum_c t_c; every cluster's segment is full
-  if (total <= kRankMax) {
+  // rank by counting costs each word its cluster's t reads (broadcast within a wave: words of
+  // one cluster read the same entries); only a cluster of more than kRankTMax words sorts
+  if (s_tpre[kMaxC + 1] <= kRankTMax) {
     for (int j = tid; j < total; j += kThreads) {
       const uint32_t w = s_cst[j];
       const int c = (int)(w >> 24);
@@ -377,7 +417,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   __shared__ int s_mode[kMaxC];
   __shared__ int s_goff[kMaxC], s_gcur[kMaxC];   // staged keys: segment start, fill count
   __shared__ int s_ccur[kMaxC];           // chosen words written per cluster
-  __shared__ int s_tpre[kMaxC + 1];       // chosen-word segment start per cluster
+  __shared__ int s_tpre[kMaxC + 2];       // chosen-word segment start per cluster; total, max
   __shared__ int s_fbl[kMaxC];
   __shared__ int s_gused, s_nfb, s_nsplit, s_hits1, s_ucnt, s_fbcnt[3];
   constexpr int NB = 1 << LB;
@@ -631,12 +671,19 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
         s_bcnt[c] = cnt;
         int mode = kModeAll;
         if (need < cnt) {
-          const int off = atomicAdd(&s_gused, cnt);
-          if (off + cnt <= a.gcap) {
+          // reserve [off, off + cnt) of the staging space only if it fits (compare-and-swap:
+          // a reservation taken back after the fact could overlap one made meanwhile)
+          int off = s_gused;
+          bool got = false;
+          while (off + cnt <= a.gcap) {
+            const int prev = atomicCAS(&s_gused, off, off + cnt);
+            if (prev == off) { got = true; break; }
+            off = prev;
+          }
+          if (got) {
             mode = kModeStaged;
             s_goff[c] = off;
           } else {
-            atomicSub(&s_gused, cnt);
             if (shd == 0) {      // equal keys beyond the staging space: block-wide search in P5
               mode = kModeBlock;
               s_fbl[atomicAdd(&s_nfb, 1)] = c;
@@ -792,7 +839,7 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   __shared__ int s_mode[kMaxC];
   __shared__ int s_goff[kMaxC], s_gcur[kMaxC];
   __shared__ int s_ccur[kMaxC];
-  __shared__ int s_tpre[kMaxC + 1];
+  __shared__ int s_tpre[kMaxC + 2];
   __shared__ int s_gused, s_fail;
   __shared__ uint32_t s_rlo[kWaves], s_rhi[kWaves];
   __shared__ int s_lw[HEADS ? 32 : 1];    // the row's limb words (exact scores)
@@ -1017,7 +1064,7 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
           if (k && bn >= (int)(sv[j] & 0xffffu))
             s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos_of(sg, i);
           else if (k && bn == (int)(sv[j] >> 16))
-            s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = key64(0u, pos_of(sg, i));
+            s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = staged_key(0u, c, pos_of(sg, i));
         }
       }
     }
@@ -1029,16 +1076,17 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
     const double inv = HEADS ? ldexp(1.0, -a.fexp[row]) : 0.0;
     for (int j = tid; j < s_gused; j += kThreads) {
       const unsigned long long e = s_g[j];
-      const int p = (int)(0xffffffffu - (uint32_t)e);
+      const int p = (int)key_pos(e);
       const float sc = HEADS ? oa::qgs_score_lds(a.codes, a.lmax_codes, kvr, p, s_lw, inv) : srow[p];
-      s_g[j] = key64(oa::float_key(sc), p);
+      s_g[j] = ((unsigned long long)oa::float_key(sc) << 32) | (e & 0xffffffffull);
     }
   }
   oa::lds_barrier();
 
-  // ---- P5, P6
+  // ---- P5 (small staged clusters one thread per key, the others one wave each), P6
+  select_small_staged(tid, s_gused, s_bcnt, s_t, s_above, s_g, s_goff, s_cst, s_tpre, s_ccur);
   select_all_staged(C, wave, lane, s_mode, s_bcnt, s_t, s_above, s_g, s_goff, s_cst, s_tpre, s_klo,
-                    s_khi, s_ccur);
+                    s_khi, s_ccur, true, kP5Thread);
   rank_and_write(E, tid, s_base, s_t, s_tpre, s_cst, s_out, erow);
 }
 
@@ -1102,17 +1150,19 @@ int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool hea
   a.marked_only = 0;
   if (lin) {
     // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words.
-    // 7 bits for C <= 64, else 6: up to C = 128 two workgroups' LDS fits one unit
+    // 7 bits for C <= 64, 6 for C <= 128, else 5: two workgroups' LDS fits one unit
     TopqArgs al = a;
-    al.lb = C <= 64 ? 7 : 6;
+    al.lb = C <= 64 ? 7 : (C <= 128 ? 6 : 5);
     al.hwords = (int)((std::max<long>((long)C * ((1 << al.lb) + 16) + 64, a.cpow) + 3) & ~3L);
     al.gcap = al.hwords / 2;
     const size_t lds_lin = 4 * (size_t)al.hwords + 4 * (size_t)a.cpow;
     int st;
     if (heads) st = al.lb == 7 ? launch_linear_lb<7, true>(al, rows, Lmax, lds_lin, s)
-                               : launch_linear_lb<6, true>(al, rows, Lmax, lds_lin, s);
+                    : al.lb == 6 ? launch_linear_lb<6, true>(al, rows, Lmax, lds_lin, s)
+                                 : launch_linear_lb<5, true>(al, rows, Lmax, lds_lin, s);
     else st = al.lb == 7 ? launch_linear_lb<7, false>(al, rows, Lmax, lds_lin, s)
-                         : launch_linear_lb<6, false>(al, rows, Lmax, lds_lin, s);
+              : al.lb == 6 ? launch_linear_lb<6, false>(al, rows, Lmax, lds_lin, s)
+                           : launch_linear_lb<5, false>(al, rows, Lmax, lds_lin, s);
     if (st || !pre) return st;
     a.marked_only = 1;
   }

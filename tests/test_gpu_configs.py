@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from openattention_amd import synth
+from openattention_amd import ops, synth
 from openattention_amd.budget import budget
 from openattention_amd.method import RMAX, C as CTX, OursHIP
 from openattention_amd.prefill import LayerState, build_rows
@@ -96,3 +96,18 @@ def test_config4_n131072_matches_oracle(rho):
     ref = O.decode_step(pre, bf16_np(lay.q.reshape(-1, D)), N, ns, nl, k, bud.E, G, np.float32(SC),
                         np.float32(SC2), rmax=RMAX)
     _check_rows(res, ref, slice(0, HQ), f"N={N}")
+    if rho == 0.03:
+        # every row through the key-prefix top-q kernel, several times: its refinement levels
+        # reserve staging space from many clusters at once (a reservation race once lost a member
+        # here now and then)
+        m = OursHIP(types.SimpleNamespace(rho=rho), 1, lay.Lmax, DEV, n_layers=1, static=lay.static, ctx_len=N)
+        m.st[0] = lay.st.clone()
+        m.decode(0, lay.q, N)
+        st = m.st[0]
+        for rep in range(6):
+            ex = torch.full_like(m.exp_idx, -2 if rep % 2 else 777)
+            ops.topq_heads(m.H, st.asg8, m.quota, ex, CTX.n_dev, st.codes, m.limbs, m.fexp, m.S, path=3)
+            torch.cuda.synchronize()
+            got = ex.cpu().numpy()[:, :bud.E]
+            bad = np.nonzero((got != ref["exp_idx"]).any(1))[0]
+            assert bad.size == 0, f"key-prefix top-q, repeat {rep}: rows {bad} differ"
