@@ -486,8 +486,8 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
         del qq
         torch.cuda.synchronize()
         if bmarks is not None:
-            for (_, e0), (name, e1) in zip(bmarks[:-1], bmarks[1:]):
-                key = "kmeans" if name.startswith("kmeans") else name
+            for (_, e0), (stage, e1) in zip(bmarks[:-1], bmarks[1:]):
+                key = "kmeans" if stage.startswith("kmeans") else stage
                 build_ms[key] = build_ms.get(key, 0.0) + e0.elapsed_time(e1)
         log(f"[bench] layer {l} built ({time.time() - t0:.1f}s)")
     CTX.K, CTX.V = Ks, Vs
@@ -607,7 +607,7 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
             return torch.nn.functional.scaled_dot_product_attention(Qs[0], kd, vd, enable_gqa=True,
                                                                     scale=D ** -0.5)
 
-        for name, fn in (("ours_splitk", run_ours), ("torch_sdpa", run_sdpa)):
+        for dname, fn in (("ours_splitk", run_ours), ("torch_sdpa", run_sdpa)):
             try:
                 for _ in range(3):
                     fn()
@@ -620,9 +620,9 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
                     x1.record()
                     torch.cuda.synchronize()
                     ts.append(x0.elapsed_time(x1) * 1e3)
-                dense[name] = round(statistics.median(ts), 1)
+                dense[dname] = round(statistics.median(ts), 1)
             except Exception as ex:  # noqa: BLE001
-                dense[name] = f"failed: {type(ex).__name__}: {ex}"[:200]
+                dense[dname] = f"failed: {type(ex).__name__}: {ex}"[:200]
         log(f"[bench] dense (us): {dense}")
     dense_best = min([v for v in dense.values() if isinstance(v, float)], default=None)
 

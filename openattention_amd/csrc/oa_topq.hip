@@ -1150,9 +1150,11 @@ int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool hea
   a.marked_only = 0;
   if (lin) {
     // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words.
-    // 7 bits for C <= 64, 6 for C <= 128, else 5: two workgroups' LDS fits one unit
+    // 7 bits for C <= 64, 6 for C <= 128, else 5: two workgroups' LDS fits one unit.  Rows
+    // longer than one register segment run one workgroup per unit anyway (their VGPRs), and
+    // keep 6 bits (smaller boundary bins: fewer rows overflow the staging space)
     TopqArgs al = a;
-    al.lb = C <= 64 ? 7 : (C <= 128 ? 6 : 5);
+    al.lb = C <= 64 ? 7 : (C <= 128 || Lmax > kThreads * 36 ? 6 : 5);
     al.hwords = (int)((std::max<long>((long)C * ((1 << al.lb) + 16) + 64, a.cpow) + 3) & ~3L);
     al.gcap = al.hwords / 2;
     const size_t lds_lin = 4 * (size_t)al.hwords + 4 * (size_t)a.cpow;
