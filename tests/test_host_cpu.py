@@ -136,3 +136,18 @@ def test_custom_attention_protocol_errors_on_the_host():
         att.custom_attention(mod, q, k, k, None, SC, 0.0, sparse_meta_data={}, layer_idx=0)
     with pytest.raises(ValueError, match="static"):
         UTAMultiBinHIP(rho=0.01)
+
+
+def test_kmeans_init_is_a_seeded_sample_of_distinct_positions():
+    """The initial centroid positions: C distinct prefix positions, the product's and the
+    restatement's the same, a different draw per layer, and a prefix of one permutation (so a
+    larger C extends a smaller one), which is what taking the first C of randperm(T) means."""
+    T, C = 4095, 64
+    for layer in (0, 5):
+        got = prefill.kmeans_init(T, C, layer).numpy()
+        assert np.array_equal(got, O.kmeans_init(T, C, layer))
+        assert len(set(got.tolist())) == C and got.min() >= 0 and got.max() < T
+        assert np.array_equal(prefill.kmeans_init(T, 2 * C, layer).numpy()[:C], got)
+    assert not np.array_equal(prefill.kmeans_init(T, C, 0).numpy(), prefill.kmeans_init(T, C, 1).numpy())
+    with pytest.raises(ValueError):
+        prefill.kmeans_init(10, 64, 0)
