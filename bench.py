@@ -249,7 +249,7 @@ def config5_run(a):
     lib.load()
     from openattention_amd.method import C as CTX, OursHIP
     from openattention_amd.model import NLAYER, LlamaShaped
-    from openattention_amd.prefill import build_rows
+    from openattention_amd.prefill import build_layers
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
@@ -263,20 +263,25 @@ def config5_run(a):
         m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=NLAYER, static=static,
                     groups=2 if B % 2 == 0 else 1)
         CTX.K, CTX.V = [], []
-        build_ms = 0.0
+        qqs = []
         for l in range(NLAYER):
             K, V, _q, qq, _ = synth.make_layer(3, B, N, Lmax, 256, dev, layer=l)
             CTX.K.append(K)
             CTX.V.append(V)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            build_rows(m.st[l], K, V, qq, T0, static["M"][l], static["inv_freq"], 1.0, l, G)
-            e1.record()
-            torch.cuda.synchronize()
-            build_ms += e0.elapsed_time(e1)
-            del qq
+            qqs.append(qq)
             if l % 8 == 7:
-                log(f"[config5] B={B}: {l + 1} layers of cache + index ({time.time() - t0:.1f}s)")
+                log(f"[config5] B={B}: {l + 1} layers of cache ({time.time() - t0:.1f}s)")
+        # the index of every layer: all layers' bases from one batched eigh, then each layer's
+        # HIP stages (prefill.build_layers)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        build_layers(m.st, CTX.K, CTX.V, qqs, T0, static["M"], static["inv_freq"], 1.0,
+                     list(range(NLAYER)), G)
+        e1.record()
+        torch.cuda.synchronize()
+        build_ms = e0.elapsed_time(e1)
+        del qqs
         log(f"[config5] B={B}: cache + index of {NLAYER} layers ({time.time() - t0:.1f}s, build "
             f"{build_ms:.0f} ms)")
         model = LlamaShaped(B, Lmax, dev, method=m)

@@ -186,21 +186,34 @@ __global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long
   if (lane < 16) tsum[((long)row * ntiles + tile) * kRC + lane] = cs;
 }
 
-// colmean from the tile sums (tiles in order, fp64), then zP -= colmean in place
-__global__ void __launch_bounds__(256) qgc_center_kernel(float* zP, long zps, int T, const double* tsum,
-                                                         int ntiles, float* colmean) {
-  __shared__ float s_cm[kRC];
-  const int row = blockIdx.y;
-  if (threadIdx.x < kRC) {
+// colmean from the tile sums (tiles in order, fp64): one wave per row, lane j < 16 a column
+__global__ void __launch_bounds__(64) qgc_colmean_kernel(int T, const double* tsum, int ntiles,
+                                                         float* colmean) {
+  const int row = blockIdx.x;
+  const int j = threadIdx.x;
+  if (j < kRC) {
     double s = 0.0;
-    for (int k = 0; k < ntiles; ++k) s += tsum[((long)row * ntiles + k) * kRC + threadIdx.x];
-    const float cm = (float)(s / (double)T);
-    s_cm[threadIdx.x] = cm;
-    if (blockIdx.x == 0) colmean[row * kRC + threadIdx.x] = cm;
+    for (int k = 0; k < ntiles; ++k) s += tsum[((long)row * ntiles + k) * kRC + j];
+    colmean[row * kRC + j] = (float)(s / (double)T);
   }
-  __syncthreads();
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < (long)T * kRC; i += (long)gridDim.x * 256)
-    zP[(long)row * zps + i] = zP[(long)row * zps + i] - s_cm[i & (kRC - 1)];
+}
+
+// zP -= colmean in place (float4 per thread: four columns of one token)
+__global__ void __launch_bounds__(256) qgc_center_kernel(float* zP, long zps, int T,
+                                                         const float* colmean) {
+  const int row = blockIdx.y;
+  const float* cm = colmean + row * kRC;
+  float4* z = reinterpret_cast<float4*>(zP + (long)row * zps);
+  const long n4 = (long)T * (kRC / 4);
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    const int c4 = (int)(i & 3) * 4;
+    float4 v = z[i];
+    v.x = v.x - cm[c4];
+    v.y = v.y - cm[c4 + 1];
+    v.z = v.z - cm[c4 + 2];
+    v.w = v.w - cm[c4 + 3];
+    z[i] = v;
+  }
 }
 
 // ---------------------------------------------------------------------------------- k-means
@@ -209,24 +222,30 @@ __device__ __forceinline__ uint32_t bf16_key(uint16_t h) {
   return (uint32_t)(h ^ ((h & 0x8000u) ? 0xffffu : 0x8000u));
 }
 
-// One wave per (64-token tile, query row).  The row's centroids (bf16, B operands: centroid
-// lane % 16 of a 16-centroid block, dims 4*(lane/16)..+3) and bf16(|c|^2 / 2) stay in LDS.
+// One 256-thread workgroup per (kAsgTiles 64-token tiles, query row): the row's centroids (bf16,
+// B operands: centroid lane % 16 of a 16-centroid block, dims 4*(lane/16)..+3) and
+// bf16(|c|^2 / 2) are staged in LDS once and every wave then takes every fourth tile.
 // Per 16-token block and centroid block one v_mfma_f32_16x16x16bf16_1k gives 16 x 16 dots;
 // the distance bf16(bf16(dot) - half) is ranked through the key (bf16 key << 8 | 255 - c), so the
 // maximum over the 16 centroid lanes (a DPP row) and over the blocks is the argmax with ties to
 // the lower cluster.
-__global__ void __launch_bounds__(64) kmeans_assign_kernel(const float* zP, long zps, int T,
-                                                           const float* cent, int C, int32_t* asg,
-                                                           long as, uint8_t* asg8, long a8s) {
+constexpr int kAsgThreads = 256;
+constexpr int kAsgTiles = 32;
+__global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const float* zP, long zps, int T,
+                                                                    const float* cent, int C,
+                                                                    int32_t* asg, long as,
+                                                                    uint8_t* asg8, long a8s) {
   __shared__ uint16_t s_cb[kMaxC * kRC];
   __shared__ uint16_t s_half[kMaxC];
-  const int lane = threadIdx.x;
-  const int tile = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int row = blockIdx.y;
   const int CB = (C + 15) / 16;
+  const int ntiles = (T + 63) / 64;
   const float* cr = cent + (long)row * C * kRC;
-  for (int i = lane; i < CB * 16 * kRC; i += 64) s_cb[i] = i < C * kRC ? oa::f32_to_bf16(cr[i]) : 0;
-  for (int c = lane; c < CB * 16; c += 64) {
+  for (int i = threadIdx.x; i < CB * 16 * kRC; i += kAsgThreads)
+    s_cb[i] = i < C * kRC ? oa::f32_to_bf16(cr[i]) : 0;
+  for (int c = threadIdx.x; c < CB * 16; c += kAsgThreads) {
     uint16_t hv = 0;
     if (c < C) {
       float s = 0.f;
@@ -240,66 +259,109 @@ __global__ void __launch_bounds__(64) kmeans_assign_kernel(const float* zP, long
     s_half[c] = hv;
   }
   __syncthreads();
+  const int tend = min(ntiles, (blockIdx.x + 1) * kAsgTiles);
+  for (int tile = blockIdx.x * kAsgTiles + wave; tile < tend; tile += kAsgThreads / 64) {
 #pragma unroll
-  for (int blk = 0; blk < 4; ++blk) {
-    const int t0 = tile * 64 + blk * 16;
-    const int ta = min(t0 + (lane & 15), T - 1);
-    const float4 zv = *reinterpret_cast<const float4*>(zP + (long)row * zps + (long)ta * kRC + 4 * (lane >> 4));
-    short4v a;
-    a[0] = (short)oa::f32_to_bf16(zv.x);
-    a[1] = (short)oa::f32_to_bf16(zv.y);
-    a[2] = (short)oa::f32_to_bf16(zv.z);
-    a[3] = (short)oa::f32_to_bf16(zv.w);
-    uint32_t best[4] = {0u, 0u, 0u, 0u};
-    for (int cb = 0; cb < CB; ++cb) {
-      const int c = cb * 16 + (lane & 15);
-      const uint16_t* bp = s_cb + c * kRC + 4 * (lane >> 4);
-      short4v b;
-      b[0] = (short)bp[0]; b[1] = (short)bp[1]; b[2] = (short)bp[2]; b[3] = (short)bp[3];
-      float4v acc = {0.f, 0.f, 0.f, 0.f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
-      const float hf = oa::bf16_to_f32(s_half[c]);
+    for (int blk = 0; blk < 4; ++blk) {
+      const int t0 = tile * 64 + blk * 16;
+      const int ta = min(t0 + (lane & 15), T - 1);
+      const float4 zv =
+          *reinterpret_cast<const float4*>(zP + (long)row * zps + (long)ta * kRC + 4 * (lane >> 4));
+      short4v a;
+      a[0] = (short)oa::f32_to_bf16(zv.x);
+      a[1] = (short)oa::f32_to_bf16(zv.y);
+      a[2] = (short)oa::f32_to_bf16(zv.z);
+      a[3] = (short)oa::f32_to_bf16(zv.w);
+      uint32_t best[4] = {0u, 0u, 0u, 0u};
+      for (int cb = 0; cb < CB; ++cb) {
+        const int c = cb * 16 + (lane & 15);
+        const uint16_t* bp = s_cb + c * kRC + 4 * (lane >> 4);
+        short4v b;
+        b[0] = (short)bp[0]; b[1] = (short)bp[1]; b[2] = (short)bp[2]; b[3] = (short)bp[3];
+        float4v acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+        const float hf = oa::bf16_to_f32(s_half[c]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float dot = oa::bf16_to_f32(oa::f32_to_bf16(acc[i]));
+          uint16_t dist = oa::f32_to_bf16(dot - hf);
+          if ((dist & 0x7fffu) == 0) dist = 0;           // -0 ranks as +0
+          const uint32_t key = c < C ? (bf16_key(dist) << 8) | (uint32_t)(255 - c) : 0u;
+          best[i] = max(best[i], key);
+        }
+      }
+      // maximum over the 16 lanes of each DPP row (the 16 centroids of one block column set)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float dot = oa::bf16_to_f32(oa::f32_to_bf16(acc[i]));
-        uint16_t dist = oa::f32_to_bf16(dot - hf);
-        if ((dist & 0x7fffu) == 0) dist = 0;           // -0 ranks as +0
-        const uint32_t key = c < C ? (bf16_key(dist) << 8) | (uint32_t)(255 - c) : 0u;
-        best[i] = max(best[i], key);
+        uint32_t v = best[i];
+        v = max(v, oa::dpp_u32<0xB1, 0xf>(v));
+        v = max(v, oa::dpp_u32<0x4E, 0xf>(v));
+        v = max(v, oa::dpp_u32<0x141, 0xf>(v));
+        v = max(v, oa::dpp_u32<0x140, 0xf>(v));
+        best[i] = v;
       }
-    }
-    // maximum over the 16 lanes of each DPP row (the 16 centroids of one block column set)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t v = best[i];
-      v = max(v, oa::dpp_u32<0xB1, 0xf>(v));
-      v = max(v, oa::dpp_u32<0x4E, 0xf>(v));
-      v = max(v, oa::dpp_u32<0x141, 0xf>(v));
-      v = max(v, oa::dpp_u32<0x140, 0xf>(v));
-      best[i] = v;
-    }
-    if ((lane & 15) < 4) {
-      const int i = lane & 15;
-      const int t = t0 + 4 * (lane >> 4) + i;
-      // lane (16g + i) holds token 4g + i of the block: best[i] of its row
-      uint32_t v = i == 0 ? best[0] : (i == 1 ? best[1] : (i == 2 ? best[2] : best[3]));
-      if (t < T) {
-        const int cid = 255 - (int)(v & 0xffu);
-        asg[(long)row * as + t] = cid;
-        asg8[(long)row * a8s + t] = (uint8_t)cid;
+      if ((lane & 15) < 4) {
+        const int i = lane & 15;
+        const int t = t0 + 4 * (lane >> 4) + i;
+        // lane (16g + i) holds token 4g + i of the block: best[i] of its row
+        uint32_t v = i == 0 ? best[0] : (i == 1 ? best[1] : (i == 2 ? best[2] : best[3]));
+        if (t < T) {
+          const int cid = 255 - (int)(v & 0xffu);
+          asg[(long)row * as + t] = cid;
+          asg8[(long)row * a8s + t] = (uint8_t)cid;
+        }
       }
     }
   }
 }
 
-// One wave per (cluster, query row): the members in position order (a scan of the byte ids,
-// 256 positions per step), their zP rows summed in fp64 by lanes 0..15 (one column each) in
-// that order; centroid = fp32(sum / count), or the initial point when the cluster is empty.
+// The byte ids of positions p .. p + 3 (0xff past T; callers test p + e < T before matching).
+__device__ __forceinline__ uint32_t load_ids(const uint8_t* ar, int T, int p) {
+  if (p + 3 < T) return *reinterpret_cast<const uint32_t*>(ar + p);
+  uint32_t ids = 0xffffffffu;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (p + e < T) ids = (ids & ~(0xffu << (8 * e))) | ((uint32_t)ar[p + e] << (8 * e));
+  return ids;
+}
+
+// One wave: the members of cluster c from position p0 on, in position order, appended to s_pos
+// (256 positions per step: an exclusive prefix of the per-lane counts places them) until the
+// row ends or the buffer could overflow on the next step; the next step's ids are requested
+// before this step's are matched.  Returns the number appended; p0 moves past the scanned part.
+constexpr int kMemBuf = 2048;
+__device__ __forceinline__ int gather_members(const uint8_t* ar, int T, int c, int& p0, int* s_pos,
+                                              int lane) {
+  int n = 0;
+  uint32_t ids = p0 < T ? load_ids(ar, T, p0 + 4 * lane) : 0u;
+  while (p0 < T && n <= kMemBuf - 256) {
+    const uint32_t cur = ids;
+    const int p = p0 + 4 * lane;
+    p0 += 256;
+    if (p0 < T) ids = load_ids(ar, T, p0 + 4 * lane);
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((cur >> (8 * e)) & 0xffu) == c) ? 1 : 0;
+    const int incl = oa::wave_incl_scan_i32(mine);
+    int o = n + incl - mine;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (p + e < T && (int)((cur >> (8 * e)) & 0xffu) == c) s_pos[o++] = p + e;
+    n += __builtin_amdgcn_readlane(incl, 63);
+  }
+  return n;
+}
+
+// One wave per (cluster, query row): the members in position order (gather_members), their zP
+// rows staged 64 at a time through LDS (one float4 per lane and member quarter, all loads of a
+// batch in flight) and summed in fp64 by lanes 0..15 (one column each) in that order;
+// centroid = fp32(sum / count), or the initial point when the cluster is empty.
 __global__ void __launch_bounds__(64) kmeans_update_kernel(const float* zP, long zps, int T,
                                                            const uint8_t* asg8, long a8s, int C,
                                                            const int32_t* init_idx, float* cent,
                                                            float* cnt_out) {
-  __shared__ int s_pos[256];
+  __shared__ int s_pos[kMemBuf];
+  __shared__ float4 s_stage[64 * (kRC / 4)];
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
   const int row = blockIdx.y;
@@ -307,37 +369,29 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const float* zP, long
   const float* zr = zP + (long)row * zps;
   double acc = 0.0;
   int cnt = 0;
-  for (int p0 = 0; p0 < T; p0 += 256) {
-    const int p = p0 + 4 * lane;
-    uint32_t ids = 0xffffffffu;
-    if (p + 3 < T) ids = *reinterpret_cast<const uint32_t*>(ar + p);
-    else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (p + e < T) ids = (ids & ~(0xffu << (8 * e))) | ((uint32_t)ar[p + e] << (8 * e));
-    }
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) ? 1 : 0;
-    // exclusive prefix of the per-lane member counts: the chunk's members in position order
-    const int incl = oa::wave_incl_scan_i32(mine);
-    const int tot = __builtin_amdgcn_readlane(incl, 63);
-    int o = incl - mine;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) s_pos[o++] = p + e;
+  int p0 = 0;
+  while (p0 < T) {
+    const int n = gather_members(ar, T, c, p0, s_pos, lane);
     __syncthreads();
-    if (lane < kRC) {
-      int k = 0;
-      for (; k + 4 <= tot; k += 4) {
-        const float v0 = zr[(long)s_pos[k] * kRC + lane], v1 = zr[(long)s_pos[k + 1] * kRC + lane];
-        const float v2 = zr[(long)s_pos[k + 2] * kRC + lane], v3 = zr[(long)s_pos[k + 3] * kRC + lane];
-        acc += (double)v0; acc += (double)v1; acc += (double)v2; acc += (double)v3;
+    for (int k0 = 0; k0 < n; k0 += 64) {
+      float4 v[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int m = k0 + (lane >> 2) + 16 * b;
+        v[b] = m < n ? *reinterpret_cast<const float4*>(zr + (long)s_pos[m] * kRC + 4 * (lane & 3))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      for (; k < tot; ++k) acc += (double)zr[(long)s_pos[k] * kRC + lane];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) s_stage[((lane >> 2) + 16 * b) * 4 + (lane & 3)] = v[b];
+      __syncthreads();
+      if (lane < kRC) {
+        const float* st = reinterpret_cast<const float*>(s_stage);
+        const int mm = min(64, n - k0);
+        for (int m = 0; m < mm; ++m) acc += (double)st[m * kRC + lane];
+      }
+      __syncthreads();
     }
-    cnt += tot;
-    __syncthreads();
+    cnt += n;
   }
   if (lane < kRC) {
     const float v = cnt > 0 ? (float)(acc / (double)cnt) : zr[(long)init_idx[c] * kRC + lane];
@@ -377,71 +431,50 @@ __global__ void __launch_bounds__(256) cluster_count_kernel(int T, const uint8_t
   }
 }
 
-// One wave per (cluster, query row): members in position order -> mem[cstart + i], and the
-// fp64 sums of k, k*k and v over them in that order (lane l: dims 2l, 2l + 1).
+// One wave per (cluster, query row): members in position order (gather_members) -> mem[cstart + i],
+// and the fp64 sums of k, k*k and v over them in that order (lane l: dims 2l, 2l + 1), the K and
+// V words of 16 members requested together.
 __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, const uint16_t* V, long ksh,
                                                           long kst, int G, int T, const uint8_t* asg8,
                                                           long a8s, int C, const int32_t* cstart,
                                                           float* Sk, float* Sk2, float* Sv, int32_t* mem,
                                                           long ms) {
-  __shared__ int s_pos[256];
+  __shared__ int s_pos[kMemBuf];
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
   const int row = blockIdx.y;
   const uint8_t* ar = asg8 + (long)row * a8s;
-  const uint16_t* kr = K + (long)(row / G) * ksh;
-  const uint16_t* vr = V + (long)(row / G) * ksh;
+  const uint16_t* kr = K + (long)(row / G) * ksh + 2 * lane;
+  const uint16_t* vr = V + (long)(row / G) * ksh + 2 * lane;
   int32_t* mr = mem + (long)row * ms + cstart[row * C + c];
   double k0 = 0.0, k1 = 0.0, q0 = 0.0, q1 = 0.0, v0 = 0.0, v1 = 0.0;
   int cnt = 0;
-  for (int p0 = 0; p0 < T; p0 += 256) {
-    const int p = p0 + 4 * lane;
-    uint32_t ids = 0xffffffffu;
-    if (p + 3 < T) ids = *reinterpret_cast<const uint32_t*>(ar + p);
-    else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (p + e < T) ids = (ids & ~(0xffu << (8 * e))) | ((uint32_t)ar[p + e] << (8 * e));
-    }
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) ? 1 : 0;
-    const int incl = oa::wave_incl_scan_i32(mine);
-    const int tot = __builtin_amdgcn_readlane(incl, 63);
-    int o = incl - mine;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (p + e < T && (int)((ids >> (8 * e)) & 0xffu) == c) {
-        s_pos[o] = p + e;
-        mr[cnt + o] = p + e;
-        ++o;
-      }
+  int p0 = 0;
+  constexpr int U = 16;
+  while (p0 < T) {
+    const int n = gather_members(ar, T, c, p0, s_pos, lane);
     __syncthreads();
-    int k = 0;
-    for (; k + 4 <= tot; k += 4) {
-      uint32_t kw[4], vw[4];
+    for (int m = lane; m < n; m += 64) mr[cnt + m] = s_pos[m];
+    for (int k = 0; k < n; k += U) {
+      uint32_t kw[U], vw[U];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        kw[u] = *reinterpret_cast<const uint32_t*>(kr + (long)s_pos[k + u] * kst + 2 * lane);
-        vw[u] = *reinterpret_cast<const uint32_t*>(vr + (long)s_pos[k + u] * kst + 2 * lane);
+      for (int u = 0; u < U; ++u) {
+        const long off = (long)s_pos[min(k + u, n - 1)] * kst;
+        kw[u] = *reinterpret_cast<const uint32_t*>(kr + off);
+        vw[u] = *reinterpret_cast<const uint32_t*>(vr + off);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const double a0 = (double)__uint_as_float(kw[u] << 16), a1 = (double)__uint_as_float(kw[u] & 0xffff0000u);
-        k0 += a0; k1 += a1; q0 += a0 * a0; q1 += a1 * a1;
-        v0 += (double)__uint_as_float(vw[u] << 16);
-        v1 += (double)__uint_as_float(vw[u] & 0xffff0000u);
+      for (int u = 0; u < U; ++u) {
+        if (k + u < n) {
+          const double a0 = (double)__uint_as_float(kw[u] << 16);
+          const double a1 = (double)__uint_as_float(kw[u] & 0xffff0000u);
+          k0 += a0; k1 += a1; q0 += a0 * a0; q1 += a1 * a1;
+          v0 += (double)__uint_as_float(vw[u] << 16);
+          v1 += (double)__uint_as_float(vw[u] & 0xffff0000u);
+        }
       }
     }
-    for (; k < tot; ++k) {
-      const uint32_t kw = *reinterpret_cast<const uint32_t*>(kr + (long)s_pos[k] * kst + 2 * lane);
-      const uint32_t vw = *reinterpret_cast<const uint32_t*>(vr + (long)s_pos[k] * kst + 2 * lane);
-      const double a0 = (double)__uint_as_float(kw << 16), a1 = (double)__uint_as_float(kw & 0xffff0000u);
-      k0 += a0; k1 += a1; q0 += a0 * a0; q1 += a1 * a1;
-      v0 += (double)__uint_as_float(vw << 16);
-      v1 += (double)__uint_as_float(vw & 0xffff0000u);
-    }
-    cnt += tot;
+    cnt += n;
     __syncthreads();
   }
   const long o = ((long)row * C + c) * kD + 2 * lane;
@@ -483,9 +516,9 @@ extern "C" int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, i
   hipLaunchKernelGGL(qgc_project_kernel, dim3(ntiles, rows), dim3(64), 0, s,
                      reinterpret_cast<const uint16_t*>(K), k_stride_h, k_stride_t, G, T,
                      reinterpret_cast<const uint16_t*>(W), zP, zp_stride, zraw_out, tile_ws, ntiles);
-  const int nb = std::min(64, (T * kRC + 255) / 256);
-  hipLaunchKernelGGL(qgc_center_kernel, dim3(nb, rows), dim3(256), 0, s, zP, zp_stride, T, tile_ws,
-                     ntiles, colmean);
+  hipLaunchKernelGGL(qgc_colmean_kernel, dim3(rows), dim3(64), 0, s, T, tile_ws, ntiles, colmean);
+  const int nb = std::min(16, (T * (kRC / 4) + 255) / 256);
+  hipLaunchKernelGGL(qgc_center_kernel, dim3(nb, rows), dim3(256), 0, s, zP, zp_stride, T, colmean);
   return OA_LAUNCH_STATUS();
 }
 
@@ -496,8 +529,10 @@ extern "C" int oa_kmeans_assign(const float* zP, long zp_stride, int rows, int T
       zp_stride < (long)T * kRC || zp_stride % 4 || asg_stride < T || asg8_stride < T ||
       (reinterpret_cast<uintptr_t>(zP) & 15))
     return OA_EINVAL;
-  hipLaunchKernelGGL(kmeans_assign_kernel, dim3((T + 63) / 64, rows), dim3(64), 0, (hipStream_t)stream,
-                     zP, zp_stride, T, cent, C, asg, asg_stride, asg8, asg8_stride);
+  const int ntiles = (T + 63) / 64;
+  hipLaunchKernelGGL(kmeans_assign_kernel, dim3((ntiles + kAsgTiles - 1) / kAsgTiles, rows),
+                     dim3(kAsgThreads), 0, (hipStream_t)stream, zP, zp_stride, T, cent, C, asg,
+                     asg_stride, asg8, asg8_stride);
   return OA_LAUNCH_STATUS();
 }
 

@@ -203,6 +203,40 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
                   layer, G, mark)
 
 
+def build_layers(states, Ks, Vs, qrows, T: int, M_pre: torch.Tensor, inv_freq: torch.Tensor,
+                 scaling: float, layers, G: int = 4) -> None:
+    """build_rows for several layers at once: every layer's metric first, then the bases of all
+    layers and rows from one batched eigh (at B = 1 a layer's 40 small matrices leave the solver
+    latency-bound; 32 layers in one call take about what one layer's call does), then each
+    layer's HIP stages.  states[i], Ks[i], Vs[i], qrows[i] belong to layer layers[i]; M_pre is
+    the (L, HQ, D, D) static metric of every layer."""
+    if not (len(states) == len(Ks) == len(Vs) == len(qrows) == len(layers)) or not layers:
+        raise ValueError("build_layers: one state, K, V, question block and layer index per layer")
+    dev = Ks[0].device
+    if dev.type != "cuda":
+        raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
+    B, HKV = Ks[0].shape[0], Ks[0].shape[1]
+    HQ = HKV * G
+    inv_freq = inv_freq.to(dev)
+    Ms = []
+    for st, K, V, q, layer in zip(states, Ks, Vs, qrows, layers):
+        if not (K.is_contiguous() and V.is_contiguous() and K.shape == V.shape and K.dim() == 4
+                and K.shape[:2] == (B, HKV)):
+            raise ValueError("build_layers: K and V must be contiguous (B, HKV, Lmax, D) tensors of one shape")
+        if B * HKV > st.U.shape[0] or q.shape[0] != B or q.shape[1] != HQ:
+            raise ValueError("build_layers: K, qrows and the state disagree on B, HKV or HQ")
+        mst = 0.5 * trace_norm(rot_avg(M_pre[layer].to(dev), inv_freq, scaling, T, WIN))
+        Mq = question_moment(q.reshape(B * HQ, q.shape[2], D), inv_freq, scaling)
+        Ms.append((mst + 0.5 * trace_norm(Mq).view(B, HQ, D, D)).reshape(B * HQ, D, D))
+    nl = len(layers)
+    U, W = bases(torch.cat(Ms, 0), nl * B * HKV, G)
+    for i, (st, K, V, layer) in enumerate(zip(states, Ks, Vs, layers)):
+        st.U[:B * HKV] = U[i * B * HKV:(i + 1) * B * HKV]
+        st.W[:B * HQ] = W[i * B * HQ:(i + 1) * B * HQ]
+        _build_device(st, 0, K.reshape(B * HKV, K.shape[2], D), V.reshape(B * HKV, V.shape[2], D), T,
+                      layer, G, lambda name: None)
+
+
 def _build_device(st, r0: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: int, G: int,
                   mark) -> None:
     """a11-a13 on the HIP kernels for the KV rows r0 .. r0 + K.shape[0] of st (their query-head

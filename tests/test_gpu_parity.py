@@ -740,6 +740,29 @@ def test_build_rows_equals_build_row():
         assert np.array_equal(sa[f], sb[f]), f
 
 
+def test_build_layers_equals_build_rows():
+    """prefill.build_layers (every layer's bases from one batched eigh) leaves each layer in the
+    state build_rows leaves it in."""
+    print("[case] build_layers vs build_rows", flush=True)
+    from openattention_amd import synth
+    from openattention_amd.prefill import build_layers, build_rows
+    B, N, Lmax, C, L = 1, 2048, 2048 + 64, 8, 3
+    static = synth.static_metric(L, dev="cpu")
+    sc = float(static["attention_scaling"])
+    lay = [synth.make_layer(1, B, N, Lmax, 64, DEV, layer=l) for l in range(L)]
+    a = [LayerState(B, HKV, G, Lmax, C, RMAX, DEV) for _ in range(L)]
+    b = [LayerState(B, HKV, G, Lmax, C, RMAX, DEV) for _ in range(L)]
+    for l in range(L):
+        build_rows(a[l], lay[l][0], lay[l][1], lay[l][3], N - 1, static["M"][l], static["inv_freq"], sc, l, G)
+    build_layers(b, [x[0] for x in lay], [x[1] for x in lay], [x[3] for x in lay], N - 1, static["M"],
+                 static["inv_freq"], sc, list(range(L)), G)
+    torch.cuda.synchronize()
+    for l in range(L):
+        sa, sb = a[l].to_numpy(), b[l].to_numpy()
+        for f in LayerState.FIELDS:
+            assert np.array_equal(sa[f], sb[f]), (l, f)
+
+
 def test_build_row_bases_match_fp64_restatement():
     """The bases the device build stores (metric in torch on the device, rocSOLVER eigh in fp32)
     span the subspaces of the oracle's fp64 restatement (explicit rotation matrices, numpy
