@@ -92,7 +92,7 @@ class LlamaShaped:
                 o = self.method.decode(l, q.reshape(B, HQ, 1, D), n).reshape(B, HQ * D)
             else:
                 R = B * HQ
-                need = R * max(4, min(256, 8192 // (B * HKV))) * (D + 2)
+                need = R * ops.DENSE_SPLITS * (D + 2)
                 if self.ws is None or self.ws.numel() < need:
                     self.ws = torch.empty(need, device=self.dev, dtype=torch.float32)
                 o = ops.dense_decode(q.reshape(R, D).contiguous(), CTX.K[l].view(-1, self.Lmax, D),
