@@ -871,8 +871,9 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   // the single-segment instantiations (PPT <= 36) are launched only for Lmax <= SEG
   constexpr bool kMulti = PPT > 36;
   const int nseg = n > 0 ? (kMulti ? (n + SEG - 1) / SEG : 1) : 0;
-  // Only the top 16 bits of each key stay in registers (two per register): h = key >> 16 is
-  // non-decreasing in the score, so bins of h order members as their scores do, and the few
+  // Only the top 16 bits of each key stay in registers (two per register), as t = h - 0x7f for a
+  // member (h = key >> 16 >= 0x80 for every finite score) and 0 for anything else: t is
+  // non-decreasing in the score, so bins of t order members as their scores do, and the few
   // members of a staged bin get their exact keys from S again
   uint32_t kk[PPT];             // the loaded scores, until keys() packs them
   uint32_t kh[PPT / 2];         // 16-bit key heads of positions 2j (low half) and 2j + 1
@@ -897,25 +898,38 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
       }
     }
   };
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   auto keys = [&](int sg) {
     const int lim = n - sg * SEG - 4 * tid;
 #pragma unroll
-    for (int j = 0; j < PPT / 2; ++j) {
-      uint32_t h2 = 0u;
+    for (int g = 0; g < NG; ++g) {
+      if (HEADS && g * 4096 + 3 < lim) {
+        // the group lies inside the row: a saturating subtract of 0x7f maps the heads of -inf
+        // (0x7f) to 0 and a member's head h to h - 0x7f, two positions per instruction
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int i = 2 * j + u;
-        if (HEADS) {
-          const uint32_t h = (kh[j] >> (16 * u)) & 0xffffu;
-          const bool q = (i >> 2) * 4096 + (i & 3) < lim && h > oa::kNegInfHead;
-          h2 |= (q ? h : 0u) << (16 * u);
-        } else {
-          const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
-          const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
-          h2 |= (q ? key >> 16 : 0u) << (16 * u);
-        }
+        for (int w = 0; w < 2; ++w)
+          kh[2 * g + w] = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(
+                              __builtin_bit_cast(u16x2, kh[2 * g + w]), (u16x2){0x7f, 0x7f}));
+        continue;
       }
-      kh[j] = h2;
+#pragma unroll
+      for (int j = 2 * g; j < 2 * g + 2; ++j) {
+        uint32_t h2 = 0u;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int i = 2 * j + u;
+          if (HEADS) {
+            const uint32_t h = (kh[j] >> (16 * u)) & 0xffffu;
+            const bool q = (i >> 2) * 4096 + (i & 3) < lim && h > oa::kNegInfHead;
+            h2 |= (q ? h - oa::kNegInfHead : 0u) << (16 * u);
+          } else {
+            const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
+            const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
+            h2 |= (q ? (key >> 16) - oa::kNegInfHead : 0u) << (16 * u);
+          }
+        }
+        kh[j] = h2;
+      }
     }
   };
   auto load = [&](int sg) { issue(sg); keys(sg); };
@@ -943,7 +957,6 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   // ---- R: the range of the qualifying members' score keys
   // two heads per register on the packed 16-bit ALU: a non-member (head 0) becomes 0xffff after
   // the wrapping - 1, so it never wins the minimum of the members' heads - 1
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   u16x2 vlo = {0xffff, 0xffff}, vhi = {0, 0};
   for (int sg = 0; sg < nseg; ++sg) {
     if (sg == 0) keys(0); else load(sg);
@@ -965,14 +978,20 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) { klo = min(klo, s_rlo[w]); khi = max(khi, s_rhi[w]); }
   float smin = 0.f, scale = 0.f;
+  float smin_sc = 0.f;
   if (khi != 0u) {
-    smin = key_float(klo << 16);
-    const float span = key_float(khi << 16) - smin;
+    smin = key_float((klo + oa::kNegInfHead) << 16);
+    const float span = key_float((khi + oa::kNegInfHead) << 16) - smin;
     scale = span > 0.f && span < INFINITY ? (float)NB / span : 0.f;
+    smin_sc = smin * scale;
   }
   // bin of a key head (a NaN's head lies above +inf's, 0xff80, and has no float order: with a
   // NaN in the row the span is NaN, scale 0 and every member in bin 0, which is still ordered)
-  auto fbin = [&](uint32_t h) -> int { return min(NB - 1, (int)((key_float(h << 16) - smin) * scale)); };
+  // (t + 0x7f) << 16 is the head's key with its low bits 0; x * scale - smin * scale in one fma
+  // is as monotone as (x - smin) * scale
+  auto fbin = [&](uint32_t t) -> int {
+    return min(NB - 1, (int)fmaf(key_float((t << 16) + (oa::kNegInfHead << 16)), scale, -smin_sc));
+  };
 
   // ---- L1: per-cluster histogram of the linear bins.  A single-segment row keeps each
   // member's bin + 1 in place of its key head (0 still marks a non-member) for G
