@@ -22,6 +22,7 @@ constexpr int kGateThreads = 512;
 constexpr int kGateWaves = kGateThreads / 64;
 constexpr int kMaxSel = 64;
 constexpr int kMaxC = 256;
+constexpr int kFuseRows = 256;       // oa_gate_fill: one fused launch below this many rows
 
 struct GateArgs {
   const uint16_t* q; long q_stride;
@@ -420,6 +421,25 @@ __global__ void __launch_bounds__(64) waterfill_kernel(const float* __restrict__
                     quota + (long)row * q_stride, C, budget, threadIdx.x, s_cw);
 }
 
+// fewer rows than compute units: the gate and the fill of a row in one workgroup.  The launch
+// saved is worth more than the gate's workgroup slots the fill holds when every row is resident
+// anyway; the fill reads the gate's scores and n_t from LDS (the same fp32 values it would read
+// back from the outputs, which are still written)
+template <int NS>
+__global__ void __launch_bounds__(kGateThreads) gate_fill_kernel(GateArgs a, float* __restrict__ quota,
+                                                                 double budget) {
+  __shared__ float s_score[kMaxC], s_nt[kMaxC];
+  __shared__ double2 s_cw[kMaxC];
+  const int row = blockIdx.x;
+  gate_row(a, row, s_score, s_nt);
+  for (int c = threadIdx.x; c < a.C; c += kGateThreads) {
+    a.score[(long)row * a.out_stride + c] = s_score[c];
+    a.n_t[(long)row * a.out_stride + c] = s_nt[c];
+  }
+  if (threadIdx.x < 64)
+    waterfill_row<NS>(s_score, s_nt, quota + (long)row * a.C, a.C, budget, threadIdx.x, s_cw);
+}
+
 int launch_fill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,
                 hipStream_t s) {
   const int ns = (C + 63) / 64;
@@ -484,10 +504,20 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
   a.nb = nb; a.nb_stride = C;
   a.score = score; a.n_t = n_t; a.out_stride = C; a.qsk = qsk;
   a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
+  const size_t lds = sizeof(float) * (size_t)n_sel * OA_D;
+  if (rows < kFuseRows) {
+    const int ns = (C + 63) / 64;
+    const dim3 g(rows), blk(kGateThreads);
+    hipStream_t s = (hipStream_t)stream;
+    if (ns == 1) hipLaunchKernelGGL(gate_fill_kernel<1>, g, blk, lds, s, a, quota, (double)budget);
+    else if (ns == 2) hipLaunchKernelGGL(gate_fill_kernel<2>, g, blk, lds, s, a, quota, (double)budget);
+    else if (ns == 3) hipLaunchKernelGGL(gate_fill_kernel<3>, g, blk, lds, s, a, quota, (double)budget);
+    else hipLaunchKernelGGL(gate_fill_kernel<4>, g, blk, lds, s, a, quota, (double)budget);
+    return OA_LAUNCH_STATUS();
+  }
   // the gate is wide and short, the fill one serial chain per row: as two launches every row of
   // each is resident at once instead of the fill holding the gate's workgroup slots
-  hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads),
-                     sizeof(float) * (size_t)n_sel * OA_D, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(errorgate_kernel, dim3(rows), dim3(kGateThreads), lds, (hipStream_t)stream, a);
   const int st = OA_LAUNCH_STATUS();
   if (st) return st;
   return launch_fill(score, n_t, rows, C, budget, quota, (hipStream_t)stream);
