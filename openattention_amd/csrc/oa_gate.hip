@@ -36,6 +36,20 @@ struct GateArgs {
   int C; float sc; float sc2;
 };
 
+// x / den for den >= 1, given r = 1 / den correctly rounded: q = RN(x r) lies within one ulp of
+// x / den and r within half an ulp of 1 / den, so fma(fma(-q, den, x), r, q) is x / den correctly
+// rounded (Markstein's theorem; the residual fma(-q, den, x) is exact) as long as nothing
+// underflows or overflows.  Zeros (whose sign the residual step loses), tiny, huge and
+// non-finite x take the division itself.
+__device__ __forceinline__ bool div_fast_ok(float x) {
+  const float ax = fabsf(x);
+  return ax >= 0x1p-100f && ax <= 0x1p100f;
+}
+__device__ __forceinline__ float div_den(float x, float den, float r) {
+  const float q = x * r;
+  return fmaf(fmaf(-q, den, x), r, q);
+}
+
 // the two wave-wide parts of one cluster's score (lane holds dims lane and lane+64): the tail
 // sums minus the selected tokens, then zbar = sc q.kbar and the raw sc2 (q*q).var
 __device__ __forceinline__ void gate_dots(const GateArgs& a, float sk_lo, float sk_hi,
@@ -60,8 +74,15 @@ __device__ __forceinline__ void gate_dots(const GateArgs& a, float sk_lo, float 
     }
   }
   const float den = fmaxf(nt, 1.0f);
-  const float kb_lo = sk_lo / den, kb_hi = sk_hi / den;
-  const float ks_lo = s2_lo / den, ks_hi = s2_hi / den;
+  float kb_lo, kb_hi, ks_lo, ks_hi;
+  if (__all(div_fast_ok(sk_lo) && div_fast_ok(sk_hi) && div_fast_ok(s2_lo) && div_fast_ok(s2_hi))) {
+    const float r = 1.0f / den;          // uniform: one division per cluster
+    kb_lo = div_den(sk_lo, den, r); kb_hi = div_den(sk_hi, den, r);
+    ks_lo = div_den(s2_lo, den, r); ks_hi = div_den(s2_hi, den, r);
+  } else {
+    kb_lo = sk_lo / den; kb_hi = sk_hi / den;
+    ks_lo = s2_lo / den; ks_hi = s2_hi / den;
+  }
   const float v_lo = fmaxf(ks_lo - kb_lo * kb_lo, 0.f);
   const float v_hi = fmaxf(ks_hi - kb_hi * kb_hi, 0.f);
   *zbar_out = a.sc * oa::dot128_canon(q_lo, kb_lo, q_hi, kb_hi);
@@ -90,6 +111,23 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int kvr = row / a.G;
+  // the wave's first batch of statistics is requested before the selected keys are staged (it
+  // does not depend on them)
+  constexpr int kBatch = 4;     // larger batches spill at the 64-VGPR cap
+  float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
+  auto issue = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int c = min(c0 + kGateWaves * i, a.C - 1);
+      const long base = (long)row * a.st_stride_r + (long)c * OA_D;
+      sk[i][0] = a.Sk[base + lane];
+      sk[i][1] = a.Sk[base + lane + 64];
+      s2[i][0] = a.Sk2[base + lane];
+      s2[i][1] = a.Sk2[base + lane + 64];
+      nbv[i] = a.nb[(long)row * a.nb_stride + c];
+    }
+  };
+  if (wave < a.C) issue(wave);
   // ---- selected keys into LDS; per cluster, the mask of its selected tokens
   for (int c = tid; c < a.C; c += kGateThreads) s_selmask[c] = 0ull;
   __syncthreads();
@@ -115,19 +153,8 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
   const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
   const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
   // ---- tail statistics and the two dot products, six clusters per wave at a time
-  constexpr int kBatch = 6;     // eight clusters per batch spill at the 64-VGPR cap
   for (int c0 = wave; c0 < a.C; c0 += kGateWaves * kBatch) {
-    float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {          // the batch's statistics, all loads in flight
-      const int c = min(c0 + kGateWaves * i, a.C - 1);
-      const long base = (long)row * a.st_stride_r + (long)c * OA_D;
-      sk[i][0] = a.Sk[base + lane];
-      sk[i][1] = a.Sk[base + lane + 64];
-      s2[i][0] = a.Sk2[base + lane];
-      s2[i][1] = a.Sk2[base + lane + 64];
-      nbv[i] = a.nb[(long)row * a.nb_stride + c];
-    }
+    if (c0 != wave) issue(c0);                  // the batch's statistics, all loads in flight
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const int c = c0 + kGateWaves * i;

@@ -92,7 +92,10 @@ struct TopqArgs {
 
 // the float whose order-preserving key is k (inverse of oa::float_key)
 __device__ __forceinline__ float key_float(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+  // k & 0x7fffffff for a key with its top bit set, ~k otherwise: ~(k ^ (m & 0x7fffffff)) with
+  // m the top bit spread over the word (one 3-input bit operation)
+  const uint32_t m = (uint32_t)((int32_t)k >> 31);
+  return __uint_as_float(~(k ^ (m & 0x7fffffffu)));
 }
 
 __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
