@@ -51,6 +51,28 @@ def _need(cond: bool, msg: str) -> None:
         raise ValueError(msg)
 
 
+def _chk(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple | None = None,
+         contiguous: bool = False) -> None:
+    """dtype, exact shape (None entries: any extent; a negative entry -m: at least m) and, when
+    asked, contiguity -- the layout the kernels index without further checks."""
+    _need(t.dtype == dtype, f"{name}: dtype must be {dtype} (got {t.dtype})")
+    if shape is not None:
+        ok = t.dim() == len(shape) and all(
+            want is None or (got == want if want >= 0 else got >= -want)
+            for got, want in zip(t.shape, shape))
+        _need(ok, f"{name}: shape {tuple(t.shape)} does not match {shape} (-m: at least m)")
+    if contiguous:
+        _need(t.is_contiguous(), f"{name}: must be contiguous")
+    else:
+        _need(t.dim() == 0 or t.stride(-1) == 1, f"{name}: last dimension must be contiguous")
+
+
+def _stats(R: int, C: int, *named) -> None:
+    """pooled statistics (R, C, 128) fp32, contiguous (the kernels step rows by C * 128)"""
+    for t, name in named:
+        _chk(t, name, torch.float32, (R, C, HEAD_DIM), contiguous=True)
+
+
 def _rows_contig(t: torch.Tensor, name: str, align_elems: int = 1) -> None:
     _need(t.stride(-1) == 1, f"{name}: last dimension must be contiguous")
     for s in t.stride()[:-1]:
@@ -176,6 +198,17 @@ def index_prep(K, V, st, n_dev: torch.Tensor, rmax: int, q, limbs, fexp) -> None
     BH, Lmax, D = K.shape
     R = st.nb.shape[0]
     C = st.nb.shape[1]
+    _chk(K, "K", torch.bfloat16, (BH, Lmax, HEAD_DIM))
+    _need(V.shape == K.shape and V.stride() == K.stride() and V.dtype == K.dtype, "V must match K")
+    _chk(st.codes, "codes", torch.int8, (BH, -Lmax, RANK_Q), contiguous=True)
+    _chk(st.asg, "asg", torch.int32, (R, -Lmax))
+    _chk(st.asg8, "asg8", torch.uint8, (R, -Lmax))
+    _chk(st.nb, "nb", torch.float32, (R, C), contiguous=True)
+    _stats(R, C, (st.Sk, "Sk"), (st.Sk2, "Sk2"), (st.Sv, "Sv"))
+    _chk(q, "q", torch.bfloat16, (R, HEAD_DIM))
+    _chk(n_dev, "n_dev", torch.int32)
+    _chk(limbs, "limbs", torch.int8, (BH, 16, RANK_Q), contiguous=True)
+    _chk(fexp, "fexp", torch.int32, (R,), contiguous=True)
     _rows_contig(q, "q")
     lib.call("oa_index_prep", _ptr(K), _ptr(V), K.stride(0), K.stride(1), R, BH, D,
              _ptr(st.codes), st.codes.shape[1], RANK_Q, _ptr(st.U), _ptr(st.scale), _ptr(st.W),
@@ -215,6 +248,12 @@ def qgs_scan_heads(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int) -> None:
     if H.dtype != torch.int16:
         raise ValueError("H must be int16 (16-bit key heads)")
     BH, Lmax, rq = codes.shape
+    _chk(codes, "codes", torch.int8, (BH, Lmax, RANK_Q), contiguous=True)
+    _chk(H, "H", torch.int16, (GROUP * BH, -Lmax))
+    _chk(TM, "TM", torch.float32, (GROUP * BH, None))
+    _chk(limbs, "limbs", torch.int8, (BH, 16, RANK_Q), contiguous=True)
+    _chk(fexp, "fexp", torch.int32, (GROUP * BH,), contiguous=True)
+    _chk(n_dev, "n_dev", torch.int32)
     lib.call("oa_qgs_scan_heads", _ptr(codes), BH, Lmax, rq, _ptr(limbs), _ptr(fexp), _ptr(H),
              H.stride(0), _ptr(TM), TM.stride(0), _ptr(n_dev), ns, nl, _stream(dev))
 
@@ -249,6 +288,13 @@ def gate_fill(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota, sm_scale: float, E
     dev = _dev(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota)
     R, C = nb.shape
     BH = K.shape[0]
+    _chk(q, "q", torch.bfloat16, (R, HEAD_DIM))
+    _chk(K, "K", torch.bfloat16, (BH, None, HEAD_DIM))
+    _chk(asg, "asg", torch.int32, (R, None))
+    _chk(sel, "sel", torch.int32, (R, None))
+    _stats(R, C, (Sk, "Sk"), (Sk2, "Sk2"))
+    for t, name in ((nb, "nb"), (score, "score"), (n_t, "n_t"), (quota, "quota")):
+        _chk(t, name, torch.float32, (R, C), contiguous=True)
     if qsk is not None and (qsk.shape != (R, C) or qsk.dtype != torch.float32 or not qsk.is_contiguous()):
         raise ValueError("qsk must be a contiguous (rows, C) float32 tensor")
     lib.call("oa_gate_fill", _ptr(q), q.stride(0), _ptr(K), K.stride(0), K.stride(1), R, BH,
@@ -287,6 +333,14 @@ def topq_heads(H, asg8, quota, exp_idx, n_dev, codes, limbs, fexp, S32, path: in
     R, C = quota.shape
     Lmax = codes.shape[1]
     E = exp_idx.shape[1]
+    _chk(H, "H", torch.int16, (R, -Lmax))
+    _chk(asg8, "asg8", torch.uint8, (R, -Lmax))
+    _chk(quota, "quota", torch.float32, (R, C), contiguous=True)
+    _chk(exp_idx, "exp_idx", torch.int32, (R, E), contiguous=True)
+    _chk(codes, "codes", torch.int8, (R // GROUP, Lmax, RANK_Q), contiguous=True)
+    _chk(limbs, "limbs", torch.int8, (R // GROUP, 16, RANK_Q), contiguous=True)
+    _chk(fexp, "fexp", torch.int32, (R,), contiguous=True)
+    _chk(S32, "S32", torch.float32, (R, -Lmax))
     lib.call("oa_topq_heads", _ptr(H), H.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R, C,
              Lmax, _ptr(exp_idx), E, _ptr(n_dev), _ptr(codes), codes.shape[0], _ptr(limbs),
              _ptr(fexp), _ptr(S32), S32.stride(0), int(path), _stream(dev))
@@ -309,6 +363,15 @@ def residual_flash(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out, sm_scale
     dev = _dev(q, K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, out)
     R, C = quota.shape
     BH = K.shape[0]
+    _chk(q, "q", torch.bfloat16, (R, HEAD_DIM))
+    _chk(K, "K", torch.bfloat16, (BH, None, HEAD_DIM))
+    _need(V.shape == K.shape and V.stride() == K.stride() and V.dtype == K.dtype, "V must match K")
+    _chk(asg, "asg", torch.int32, (R, None))
+    _chk(sel, "sel", torch.int32, (R, None))
+    _chk(exp_idx, "exp_idx", torch.int32, (R, None), contiguous=True)
+    for t, name in ((quota, "quota"), (n_t, "n_t")):
+        _chk(t, name, torch.float32, (R, C), contiguous=True)
+    _stats(R, C, (Sk, "Sk"), (Sv, "Sv"))
     if qsk is not None and (qsk.shape != (R, C) or qsk.dtype != torch.float32 or not qsk.is_contiguous()):
         raise ValueError("qsk must be a contiguous (rows, C) float32 tensor")
     _need(out.shape == (R, HEAD_DIM) and out.dtype in (torch.bfloat16, torch.float32) and out.stride(1) == 1,

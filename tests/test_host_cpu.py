@@ -151,3 +151,25 @@ def test_kmeans_init_is_a_seeded_sample_of_distinct_positions():
     assert not np.array_equal(prefill.kmeans_init(T, C, 0).numpy(), prefill.kmeans_init(T, C, 1).numpy())
     with pytest.raises(ValueError):
         prefill.kmeans_init(10, 64, 0)
+
+
+def test_wrapper_layout_checks_reject_wrong_dtype_shape_and_strides():
+    """The decode-stage wrappers' host checks (ops._chk): dtype, exact and minimum extents,
+    contiguity -- the layouts the kernels index without checking."""
+    import torch
+    from openattention_amd import ops
+    t = torch.zeros(4, 8, 128, dtype=torch.float32)
+    ops._chk(t, "t", torch.float32, (4, 8, 128), contiguous=True)
+    ops._chk(t, "t", torch.float32, (4, -6, None))
+    with pytest.raises(ValueError, match="dtype"):
+        ops._chk(t, "t", torch.bfloat16)
+    with pytest.raises(ValueError, match="shape"):
+        ops._chk(t, "t", torch.float32, (4, -9, 128))
+    with pytest.raises(ValueError, match="shape"):
+        ops._chk(t, "t", torch.float32, (4, 8))
+    with pytest.raises(ValueError, match="contiguous"):
+        ops._chk(t[:, ::2], "t", torch.float32, contiguous=True)
+    with pytest.raises(ValueError, match="last dimension"):
+        ops._chk(t.transpose(1, 2), "t", torch.float32)
+    with pytest.raises(ValueError, match="contiguous"):
+        ops._stats(4, 4, (t[:, :4], "Sk"))
