@@ -180,96 +180,119 @@ __device__ __forceinline__ double load_limbs(const Rescore& rs, int row, int* lw
   return ldexp(1.0, -rs.fexp[row]);
 }
 
-template <bool HEADS>
+__device__ __forceinline__ int lanes_below(unsigned long long m, int lane) {
+  return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+}
+
+// Radix-select variant for rows of at most 64*TPL tiles and k_top <= kMaxTop.  The k-th largest
+// tile key T is found bit by bit from ballot counts over the tile keys held in registers (lane
+// l: tiles l, l + 64, ...); the chosen tiles are those above T and the lowest-index ones equal
+// to it.  Every top-k token scores at least T (k chosen tiles each hold a token that does), so
+// only candidates whose key reaches T join the candidate list (with HEADS: whose head reaches
+// T's head, exact scores then recomputed for the list alone).  The k-th largest candidate key
+// (score key << 32 | ~position: distinct) is found the same way, and the k winners are written
+// in descending key order, as repeated wave maxima would give them.
+template <int TPL, bool HEADS>
 __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, long s_stride,
                                                          const float* __restrict__ TM, long tm_stride,
                                                          int ntiles, int32_t* __restrict__ sel,
                                                          long sel_stride, const int* __restrict__ n_dev,
                                                          int ns, int nl, int k_top, Rescore rs) {
-  __shared__ float s_tm[kMaxTilesLds];
   __shared__ int s_tile[kMaxTop];
-  __shared__ float s_sc[kMaxTop * 64];
-  __shared__ int s_top[kMaxTop];
+  __shared__ unsigned long long s_ck[kMaxTop * 64];   // candidate positions, then their keys
+  __shared__ unsigned long long s_win[kMaxTop];
   const int row = oa::xcd_row(blockIdx.x, gridDim.x);   // a KV row's query rows share one L2
   const int lane = threadIdx.x;
   const int n = *n_dev;
+  const int dead_hi = n - nl;
   int lw[HEADS ? 32 : 1];
   const double inv = load_limbs<HEADS>(rs, row, lw);
-  const float NaN = __uint_as_float(0x7fc00000u);
-  // lane l owns tiles l, l+64, ...; it caches the best key among its untaken tiles.  Loads go
-  // out 16 per lane at a time (clamped addresses), so a row's tile maxima arrive in one or two
-  // rounds.
-  unsigned long long mine = 0ull;
-  for (int t0 = 0; t0 < ntiles; t0 += 64 * 16) {
-    float v[16];
+  uint32_t tk[TPL];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = TM[(long)row * tm_stride + min(t0 + j * 64 + lane, ntiles - 1)];
+  for (int j = 0; j < TPL; ++j) {
+    const int t = j * 64 + lane;
+    tk[j] = t < ntiles ? oa::float_key(TM[(long)row * tm_stride + min(t, ntiles - 1)]) : 0u;
+  }
+  // ---- T: the largest key value reached by at least k tiles
+  uint32_t T = 0u;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int t = t0 + j * 64 + lane;
-      if (t < ntiles) {
-        s_tm[t] = v[j];
-        const unsigned long long kk = tile_key(v[j], t);
-        mine = kk > mine ? kk : mine;
-      }
-    }
+    for (int j = 0; j < TPL; ++j) cnt += __popcll(__ballot(tk[j] >= cand));
+    if (cnt >= k_top) T = cand;
+  }
+  int need = k_top;
+#pragma unroll
+  for (int j = 0; j < TPL; ++j) need -= __popcll(__ballot(tk[j] > T));
+  // ---- the chosen tiles, in tile order: above T, then equal to T while need lasts
+  int nt = 0;
+#pragma unroll
+  for (int j = 0; j < TPL; ++j) {
+    const unsigned long long meq = __ballot(tk[j] == T);
+    const bool take = tk[j] > T || (tk[j] == T && lanes_below(meq, lane) < need);
+    need -= min(need, __popcll(meq));
+    const unsigned long long mt = __ballot(take);
+    if (take) s_tile[nt + lanes_below(mt, lane)] = j * 64 + lane;
+    nt += __popcll(mt);
   }
   __syncthreads();
-  for (int i = 0; i < k_top; ++i) {
-    const unsigned long long best = oa::wave_max_u64(mine);
-    const int t = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
-    if (lane == 0) s_tile[i] = t;
-    if (best == mine) {            // the owner lane: mark taken and rescan its tiles
-      s_tm[t] = NaN;
-      mine = 0ull;
-      for (int u = lane; u < ntiles; u += 64) {
-        const float v = s_tm[u];
-        if (v != v) continue;
-        const unsigned long long kk = tile_key(v, u);
-        mine = kk > mine ? kk : mine;
-      }
+  // ---- candidates: column lane of every chosen tile whose key (head) reaches T's
+  int nc = 0;
+  for (int j = 0; j < k_top; ++j) {
+    const int pos = s_tile[j] * 64 + lane;
+    bool q;
+    unsigned long long key = 0ull;
+    if (HEADS) {
+      const uint32_t h = static_cast<const uint16_t*>(Sv)[(long)row * s_stride + pos];
+      q = h >= (T >> 16) && pos >= ns && pos < dead_hi;
+    } else {
+      const float v = cand_score<false>(Sv, s_stride, row, pos, ns, dead_hi, rs, lw, inv);
+      key = tile_key(v, pos);
+      q = (uint32_t)(key >> 32) >= T;
     }
+    const unsigned long long m = __ballot(q);
+    if (q) s_ck[nc + lanes_below(m, lane)] = HEADS ? (unsigned long long)pos : key;
+    nc += __popcll(m);
   }
   __syncthreads();
-  // candidates: lane l holds column l of the k chosen tiles (loads 16 tiles at a time)
-  mine = 0ull;
-  for (int j0 = 0; j0 < k_top; j0 += 16) {
-    float v[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      v[j] = cand_score<HEADS>(Sv, s_stride, row, s_tile[min(j0 + j, k_top - 1)] * 64 + lane, ns,
-                               n - nl, rs, lw, inv);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (j0 + j < k_top) {
-        s_sc[(j0 + j) * 64 + lane] = v[j];
-        const unsigned long long kk = tile_key(v[j], s_tile[j0 + j] * 64 + lane);
-        mine = kk > mine ? kk : mine;
-      }
+  if (HEADS) {
+    const int kvr = row / GQ;
+    for (int i = lane; i < nc; i += 64) {
+      const int pos = (int)s_ck[i];
+      s_ck[i] = tile_key(oa::qgs_score(rs.codes, rs.lmax, kvr, pos, lw, inv), pos);
     }
+    __syncthreads();
   }
-  for (int i = 0; i < k_top; ++i) {
-    const unsigned long long best = oa::wave_max_u64(mine);
-    const int pos = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
-    if (lane == 0) s_top[i] = pos;
-    if (best == mine) {
-      mine = 0ull;
-      for (int j = 0; j < k_top; ++j) {
-        const int pj = s_tile[j] * 64 + lane;
-        if (pj == pos) s_sc[j * 64 + lane] = NaN;
-        const float v = s_sc[j * 64 + lane];
-        if (v != v) continue;
-        const unsigned long long kk = tile_key(v, pj);
-        mine = kk > mine ? kk : mine;
-      }
-    }
+  // ---- the k-th largest candidate key: 32 score bits, then the position bits (positions are
+  // below 2^24, so bits 24..31 of ~position are all ones)
+  unsigned long long T2 = 0xff000000ull;
+  for (int bit = 63; bit >= 0; bit = bit == 32 ? 23 : bit - 1) {
+    const unsigned long long cand = T2 | (1ull << bit);
+    int cnt = 0;
+    for (int i0 = 0; i0 < nc; i0 += 64) cnt += __popcll(__ballot(i0 + lane < nc && s_ck[i0 + lane] >= cand));
+    if (cnt >= k_top) T2 = cand;
+  }
+  // ---- the k winners (keys >= T2), then each one's rank among them (descending keys)
+  int nw = 0;
+  for (int i0 = 0; i0 < nc; i0 += 64) {
+    const bool w = i0 + lane < nc && s_ck[i0 + lane] >= T2;
+    const unsigned long long m = __ballot(w);
+    if (w) s_win[nw + lanes_below(m, lane)] = s_ck[i0 + lane];
+    nw += __popcll(m);
   }
   __syncthreads();
   int32_t* sr = sel + (long)row * sel_stride;
   if (lane < ns) sr[lane] = lane;
   if (lane < nl) sr[ns + lane] = n - nl + lane;
-  for (int i = lane; i < k_top; i += 64) sr[ns + nl + i] = s_top[i];
-  for (int i = lane; i < k_top; i += 64) mark_selected<HEADS>(Sv, s_stride, row, s_top[i]);
+  if (lane < k_top) {
+    const unsigned long long x = s_win[lane];
+    int rank = 0;
+    for (int i = 0; i < k_top; ++i) rank += s_win[i] > x ? 1 : 0;
+    const int pos = (int)(0xffffffffu - (unsigned)(x & 0xffffffffull));
+    sr[ns + nl + rank] = pos;
+    mark_selected<HEADS>(Sv, s_stride, row, pos);
+  }
 }
 
 // Register variant for rows of at most 64*TPL tiles and k_top <= KR: lane l keeps the keys of
@@ -427,9 +450,16 @@ int launch_topk(void* S, long s_stride, const float* TM, long tm_stride, int row
   if (k_top <= 9 && tpl <= 9) OA_TOPK_REG(9, 9);
   else if (k_top <= 16 && tpl <= 16) OA_TOPK_REG(16, 16);
   else if (k_top <= 16 && tpl <= 32) OA_TOPK_REG(32, 16);
-  else
-    hipLaunchKernelGGL(topk_select_kernel<HEADS>, dim3(rows), dim3(64), 0, st, S, s_stride, TM,
-                       tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top, rs);
+  else {
+    // the radix-select variant, sized to the row's tiles
+#define OA_TOPK_RS(T)                                                                          \
+  hipLaunchKernelGGL((topk_select_kernel<T, HEADS>), dim3(rows), dim3(64), 0, st, S, s_stride,  \
+                     TM, tm_stride, ntiles, sel, sel_stride, n_dev, ns, nl, k_top, rs)
+    if (tpl <= 16) OA_TOPK_RS(16);
+    else if (tpl <= 32) OA_TOPK_RS(32);
+    else OA_TOPK_RS(64);
+#undef OA_TOPK_RS
+  }
 #undef OA_TOPK_REG
   return OA_LAUNCH_STATUS();
 }

@@ -509,6 +509,41 @@ def test_index_prep_matches_separate_calls(lay4k):
     assert np.array_equal(res[0][2], res[1][2])
 
 
+@pytest.mark.parametrize("n,k", [(4096, 9), (40000, 17), (70000, 40), (200000, 64)])
+def test_topk_rows_with_ties_large_k(n, k):
+    """Top-k over fp32 score rows built for ties: scores on a coarse grid (many equal tile maxima
+    and equal scores, ties to the lower position), a few rows of one repeated value, sink and
+    local positions and the unwritten tail at -inf as the scan leaves them.  sel (in order) and
+    the rows after marking equal the restatement; k > 16 and long rows take the radix-select
+    kernel, up to 4096 tiles and k = 64."""
+    print(f"[case] topk ties n={n} k={k}", flush=True)
+    rng = np.random.default_rng(n + k)
+    R, ns, nl = 8, 3, 5
+    Lmax = n + 100
+    ncols = -(-Lmax // 64) * 64
+    S = np.round(rng.normal(0.0, 2.0, (R, ncols)) * 4.0).astype(np.float32) / np.float32(4.0)
+    S[1] = 0.5                                            # one value everywhere
+    S[2, ::7] = 9.0                                       # many equal maxima
+    S[3, : n // 2] = -3.0                                 # half the row tied low
+    S[:, :ns] = -np.inf
+    S[:, n - nl:] = -np.inf                               # local positions and the unwritten tail
+    TM = S.reshape(R, -1, 64).max(axis=2)
+    want = O.topk_select(S, n, ns, nl, k)
+    St = torch.from_numpy(S).to(DEV)
+    TMt = torch.from_numpy(np.ascontiguousarray(TM)).to(DEV)
+    sel = torch.empty(R, ns + nl + k, device=DEV, dtype=torch.int32)
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    ops.topk_select(St, TMt, sel, n_dev, ns, nl, k)
+    torch.cuda.synchronize()
+    got = sel.cpu().numpy()
+    assert np.array_equal(got, want), f"rows {np.nonzero((got != want).any(1))[0]} differ"
+    after = St.cpu().numpy()
+    marked = S.copy()
+    for r in range(R):
+        marked[r, want[r, ns + nl:]] = -np.inf
+    assert np.array_equal(after, marked)
+
+
 @pytest.mark.parametrize("C,E", [(8, 27), (64, 216), (100, 679), (192, 1335), (256, 2877), (256, 40)])
 def test_waterfill_rows_with_ties_dead_and_full_clusters(C, E):
     """Water-filling on rows built for the leftover tokens: scores on a coarse grid (ties go to
