@@ -208,11 +208,11 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
   int lw[HEADS ? 32 : 1];
   const double inv = load_limbs<HEADS>(rs, row, lw);
   uint32_t tk[TPL];
+  float tv[TPL];
 #pragma unroll
-  for (int j = 0; j < TPL; ++j) {
-    const int t = j * 64 + lane;
-    tk[j] = t < ntiles ? oa::float_key(TM[(long)row * tm_stride + min(t, ntiles - 1)]) : 0u;
-  }
+  for (int j = 0; j < TPL; ++j) tv[j] = TM[(long)row * tm_stride + min(j * 64 + lane, ntiles - 1)];
+#pragma unroll
+  for (int j = 0; j < TPL; ++j) tk[j] = j * 64 + lane < ntiles ? oa::float_key(tv[j]) : 0u;
   // ---- T: the largest key value reached by at least k tiles
   uint32_t T = 0u;
   for (int bit = 31; bit >= 0; --bit) {
@@ -237,18 +237,27 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
     nt += __popcll(mt);
   }
   __syncthreads();
-  // ---- candidates: column lane of every chosen tile whose key (head) reaches T's
+  // ---- candidates: column lane of every chosen tile whose key (head) reaches T's (every
+  // tile's value is requested before any is used: one round of loads)
+  uint32_t cv[kMaxTop];
+#pragma unroll
+  for (int j = 0; j < kMaxTop; ++j) {
+    const int pos = s_tile[min(j, k_top - 1)] * 64 + lane;     // past k_top: a repeat, unused
+    cv[j] = HEADS ? (uint32_t)static_cast<const uint16_t*>(Sv)[(long)row * s_stride + pos]
+                  : __float_as_uint(static_cast<const float*>(Sv)[(long)row * s_stride + pos]);
+  }
   int nc = 0;
-  for (int j = 0; j < k_top; ++j) {
+#pragma unroll
+  for (int j = 0; j < kMaxTop; ++j) {
+    if (j >= k_top) continue;                       // uniform
     const int pos = s_tile[j] * 64 + lane;
+    const bool live = pos >= ns && pos < dead_hi;
     bool q;
     unsigned long long key = 0ull;
     if (HEADS) {
-      const uint32_t h = static_cast<const uint16_t*>(Sv)[(long)row * s_stride + pos];
-      q = h >= (T >> 16) && pos >= ns && pos < dead_hi;
+      q = cv[j] >= (T >> 16) && live;
     } else {
-      const float v = cand_score<false>(Sv, s_stride, row, pos, ns, dead_hi, rs, lw, inv);
-      key = tile_key(v, pos);
+      key = tile_key(live ? __uint_as_float(cv[j]) : -INFINITY, pos);
       q = (uint32_t)(key >> 32) >= T;
     }
     const unsigned long long m = __ballot(q);
@@ -257,10 +266,24 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
   }
   __syncthreads();
   if (HEADS) {
+    // exact scores of the list, four candidates' codes in flight per lane
     const int kvr = row / GQ;
-    for (int i = lane; i < nc; i += 64) {
-      const int pos = (int)s_ck[i];
-      s_ck[i] = tile_key(oa::qgs_score(rs.codes, rs.lmax, kvr, pos, lw, inv), pos);
+    for (int i0 = 0; i0 < nc; i0 += 256) {
+      int pos[4];
+      uint4 c0[4], c1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = min(i0 + u * 64 + lane, nc - 1);
+        pos[u] = (int)s_ck[i];
+        const uint4* cp = reinterpret_cast<const uint4*>(rs.codes + ((long)kvr * rs.lmax + pos[u]) * 32);
+        c0[u] = cp[0];
+        c1[u] = cp[1];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * 64 + lane;
+        if (i < nc) s_ck[i] = tile_key(oa::qgs_score_words(c0[u], c1[u], lw, inv), pos[u]);
+      }
     }
     __syncthreads();
   }
