@@ -283,9 +283,11 @@ __device__ __forceinline__ void fill_prologue(const float* score_row, const floa
     if (lane + 64 * j < C) rmax = fmax(rmax, ratio);
   }
   rmax = wave_max_f64(rmax);
-  f.tot = canon_sum<NS>(f.cap, C, lane);
+  // the butterfly leaves one value on every lane; lane 0's copy lets the compiler branch on it
+  // as a wave-uniform value
+  f.tot = readlane_f64(canon_sum<NS>(f.cap, C, lane), 0);
   f.lo = -3.0 * 2.302585092994046;
-  f.hi = oa::det_log(fmax(rmax, 1e-3)) + 1.0;
+  f.hi = readlane_f64(oa::det_log(fmax(rmax, 1e-3)) + 1.0, 0);
 }
 
 // quotas floor(min(n_b, lambda w_b)) at the final lo, leftover tokens one each to the live
@@ -304,7 +306,7 @@ __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, dou
     qv[j] = floor(fmin(f.cap[j], el * f.w[j]));
     if (f.tot <= budget) qv[j] = f.cap[j];
   }
-  const double qsum = canon_sum<NS>(qv, C, lane);
+  const double qsum = readlane_f64(canon_sum<NS>(qv, C, lane), 0);
   double rem = fmin(f.tot, budget) - qsum;
   rem = rint(rem > 0.0 ? rem : 0.0);
   unsigned long long u[NS];
@@ -355,6 +357,17 @@ __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, dou
 // tree's value).  Here each of a node's P lanes adds 64 / P consecutive lane partials by the
 // lower levels of that tree and the node's lanes add the P subtotals by its top levels.  The
 // walk down the tree then takes the sequential path from the ballot of f > E.
+//
+// Most steps need no probe.  The computed f is a non-decreasing function F of em = exp(mid)
+// (min(cap, RN(em w)) with w >= 0, and IEEE sums of non-negative terms in a fixed order, are
+// monotone), and det_exp is within 2^-51 of exp, so det_exp(x) <= det_exp(a) (1 + 2^-49.9) for
+// every x <= a.  One round probes F at em = det_exp(x) (1 + 2^-47) for points x = a below the
+// water level's estimate and at det_exp(x) (1 - 2^-47) for points x = b above it: F <= E there
+// proves f(mid) <= E for every mid <= a, F > E proves f(mid) > E for every mid >= b.  The
+// sequential steps whose midpoint lies outside (a, b) then take their branch without a probe,
+// and a step whose midpoint is a bound already probed changes nothing (neither can any later
+// one).  The estimate is the fixed point of lambda = (E - sum of the capped n_b) / (sum of the
+// other w_b); a bracket not proven leaves every step to the probes.
 template <int NS>
 __device__ __forceinline__ void waterfill_row(const float* score_row, const float* nt_row,
                                               float* quota_row, int C, double budget, int lane,
@@ -362,6 +375,11 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
   // ---- live clusters, weights and the bracket of log(lambda)
   FillState<NS> f;
   fill_prologue<NS>(score_row, nt_row, C, lane, f);
+  // the tail fits the budget: every quota is its cap, the bisection's result is not used
+  if (!(f.tot > budget)) {
+    fill_epilogue<NS>(f, C, budget, lane, quota_row);
+    return;
+  }
   // 8 lanes per probe node: each lane then adds only 8 canonical lane partials, and a round's
   // fp64 work (not its latency) is what the lane count trades against the round count
   constexpr int P = 8;                       // lanes per probe node
@@ -389,21 +407,8 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
       cp[i][j] = v.x;
       wp[i][j] = v.y;
     }
-  const int lev = node > 0 ? 31 - __clz(node) : 0;   // depth of this lane's node (root 0)
-  // ---- 64 bisection steps, DEPTH per round
-  double lo = f.lo, hi = f.hi;
-  for (int done = 0; done < 64;) {
-    const int d = min(DEPTH, 64 - done);
-    double nlo = lo, nhi = hi;
-    double mid = 0.5 * (lo + hi);
-#pragma unroll
-    for (int b = DEPTH - 2; b >= 0; --b) {
-      if (b < lev) {
-        if ((node >> b) & 1) nlo = mid; else nhi = mid;
-        mid = 0.5 * (nlo + nhi);
-      }
-    }
-    const double em = oa::det_exp(mid);
+  // f at em for this lane's node (the same value on the node's P lanes)
+  auto probe = [&](double em) {
     double part[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -420,14 +425,110 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
     fv = fv + oa::dpp_f64<0xB1>(fv);                   // node lanes xor 1
     if (P >= 4) fv = fv + oa::dpp_f64<0x4E>(fv);       // xor 2
     if (P >= 8) fv = fv + oa::dpp_f64<0x141>(fv);      // xor 4 (4-lane groups are uniform)
-    const unsigned long long gt = __ballot(fv > budget);
+    return fv;
+  };
+  // ---- the proven bracket (a, b)
+  const double INF = __longlong_as_double(0x7ff0000000000000LL);
+  double a = -INF, b = INF;
+  {
+    bool capped[NS];
+    double lam = 0.0;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) capped[j] = false;
+    for (int it = 0; it < 16; ++it) {
+      double sc = 0.0, sw = 0.0;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        if (capped[j]) sc += f.cap[j];
+        else sw += f.w[j];
+      }
+      sc = readlane_f64(oa::wave_sum(sc), 0);
+      sw = readlane_f64(oa::wave_sum(sw), 0);
+      const double l = (budget - sc) / sw;
+      if (!(l > 0.0 && l < INF)) break;
+      lam = l;
+      bool changed = false;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const bool cj = f.cap[j] <= l * f.w[j];
+        changed = changed || cj != capped[j];
+        capped[j] = cj;
+      }
+      if (!__any(changed)) break;
+    }
+    const double x0 = oa::det_log(lam);
+    if (x0 > -600.0 && x0 < 600.0) {
+      // nodes 0-3 probe below x0, nodes 4-7 above, nearest first
+      const int rung = node & 3;
+      const bool up = node >= 4;
+      const double dl = fmax(fabs(x0), 0.0625) *
+                        (rung == 0 ? 0x1p-46 : rung == 1 ? 0x1p-43 : rung == 2 ? 0x1p-38 : 0x1p-26);
+      const double xk = up ? x0 + dl : x0 - dl;
+      const double em = oa::det_exp(xk) * (up ? 1.0 - 0x1p-47 : 1.0 + 0x1p-47);
+      const unsigned long long gt = __ballot(probe(em) > budget);
+      for (int k = 0; k < 4; ++k)
+        if (!((gt >> (k * P)) & 1ull)) { a = readlane_f64(xk, k * P); break; }
+      for (int k = 4; k < 8; ++k)
+        if ((gt >> (k * P)) & 1ull) { b = readlane_f64(xk, k * P); break; }
+    }
+  }
+  const int lev = node > 0 ? 31 - __clz(node) : 0;   // depth of this lane's node (root 0)
+  // ---- 64 bisection steps: decided by the bracket, or DEPTH per round of probes
+  double lo = f.lo, hi = f.hi;
+  bool lo_probed = false, hi_probed = false;          // f at lo (hi) known to be <= E (> E)
+  int done = 0;
+  while (done < 64) {
+    double m = 0.5 * (lo + hi);
+    if ((m == lo && lo_probed) || (m == hi && hi_probed)) break;   // a fixed point
+    // steps the bracket decides, 8 at a time and without branches: a step it cannot decide
+    // changes nothing, so every step after it stays undecided as well.  The bounds are carried
+    // halved: 0.5 lo + 0.5 hi is 0.5 (lo + hi) exactly (halving is exact and commutes with
+    // rounding), and the halving of a new bound then runs beside its comparisons
+    if (64 - done >= 8) {
+      double lh = 0.5 * lo, hh = 0.5 * hi;
+      int dec = 0;
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        const double mm = lh + hh;
+        const double mh = 0.5 * mm;
+        const bool L = mm <= a;
+        const bool H = mm >= b;
+        lh = L ? mh : lh;
+        hh = H ? mh : hh;
+        lo_probed = lo_probed || L;
+        hi_probed = hi_probed || H;
+        dec += (L || H) ? 1 : 0;
+      }
+      lo = 2.0 * lh;
+      hi = 2.0 * hh;
+      done += dec;
+      if (dec == 8) continue;
+    } else if (m <= a || m >= b) {
+      if (m <= a) { lo = m; lo_probed = true; } else { hi = m; hi_probed = true; }
+      ++done;
+      continue;
+    }
+    m = 0.5 * (lo + hi);
+    if ((m == lo && lo_probed) || (m == hi && hi_probed)) break;
+    // the next step needs a probe: one round of DEPTH steps
+    const int d = min(DEPTH, 64 - done);
+    double nlo = lo, nhi = hi;
+    double mid = m;
+#pragma unroll
+    for (int bt = DEPTH - 2; bt >= 0; --bt) {
+      if (bt < lev) {
+        if ((node >> bt) & 1) nlo = mid; else nhi = mid;
+        mid = 0.5 * (nlo + nhi);
+      }
+    }
+    const unsigned long long gt = __ballot(probe(oa::det_exp(mid)) > budget);
     int nd = 1, lo_nd = 0, hi_nd = 0;
     for (int k = 0; k < d; ++k) {
       if ((gt >> (nd * P)) & 1ull) { hi_nd = nd; nd = 2 * nd; }
       else { lo_nd = nd; nd = 2 * nd + 1; }
     }
-    if (lo_nd) lo = readlane_f64(mid, lo_nd * P);
-    if (hi_nd) hi = readlane_f64(mid, hi_nd * P);
+    if (lo_nd) { lo = readlane_f64(mid, lo_nd * P); lo_probed = true; }
+    if (hi_nd) { hi = readlane_f64(mid, hi_nd * P); hi_probed = true; }
     done += d;
   }
   f.lo = lo;

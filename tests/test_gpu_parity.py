@@ -572,6 +572,30 @@ def test_waterfill_rows_with_ties_dead_and_full_clusters(C, E):
     assert (got.sum(1) <= E).all()
 
 
+@pytest.mark.parametrize("C", [64, 256])
+def test_waterfill_wide_score_spreads(C):
+    """Water-filling where many clusters reach their cap at different levels (scores spread over
+    40 units, tails from 2 to 1024 tokens) and budgets from one token to nearly the whole tail:
+    the water level's estimate needs several capping rounds and, for some rows, proves no bracket,
+    so every step is probed.  Quotas equal the restatement's on every row."""
+    print(f"[case] waterfill wide C={C}", flush=True)
+    rng = np.random.default_rng(77 + C)
+    R = 256
+    score = rng.uniform(-20.0, 20.0, (R, C)).astype(np.float32)
+    n_t = rng.integers(2, 1025, (R, C)).astype(np.float32)
+    tot = n_t.astype(np.float64).sum(1)
+    for E_frac in (0.0, 0.01, 0.3, 0.97):
+        E = max(1, int(E_frac * float(tot.min())))
+        want = O.waterfill(score, n_t, E)
+        quota = torch.empty(R, C, device=DEV)
+        ops.waterfill(torch.from_numpy(score).to(DEV), torch.from_numpy(n_t).to(DEV), quota, E)
+        torch.cuda.synchronize()
+        got = quota.cpu().numpy()
+        bad = np.nonzero((got != want).any(1))[0]
+        assert bad.size == 0, f"E={E}: rows {bad[:8]} differ"
+        assert (got.sum(1) == E).all()
+
+
 @pytest.mark.parametrize("C", [128, 200])
 def test_index_update_many_clusters(C):
     """The index update with more clusters than lanes (C = 128, 200: each lane scores several

@@ -27,6 +27,33 @@ def test_det_exp_vs_libm(x):
     assert _ulp_err(O.det_exp(x), math.exp(x)) <= 2.0
 
 
+def test_det_exp_relative_error_below_2_pow_51():
+    """The water-fill kernel proves which bisection steps need no probe from det_exp staying
+    within 2^-51 of exp (so det_exp(x) <= det_exp(a) (1 + 2^-49.9) for every x <= a).  Checked
+    against 64-bit-mantissa exp on random points and on both sides of every reduction switch
+    x = (k + 1/2) ln 2 over the range the fill uses."""
+    if np.finfo(np.longdouble).nmant < 63:
+        pytest.skip("no extended-precision exp on this host")
+    xs = list(RNG.uniform(-700.0, 700.0, 20000))
+    ln2 = math.log(2.0)
+    for k in range(-1010, 1011, 7):
+        x = (k + 0.5) * ln2
+        for _ in range(3):
+            xs.append(x)
+            x = math.nextafter(x, -math.inf)
+        x = (k + 0.5) * ln2
+        for _ in range(3):
+            x = math.nextafter(x, math.inf)
+            xs.append(x)
+    worst = 0.0
+    for x in xs:
+        if not -700.0 <= x <= 700.0:
+            continue
+        ref = np.exp(np.longdouble(x))
+        worst = max(worst, float(abs((np.longdouble(O.det_exp(x)) - ref) / ref)))
+    assert worst < 2.0 ** -51, worst
+
+
 def test_det_exp_specials():
     assert O.det_exp(-1000.0) == 0.0
     assert math.isinf(O.det_exp(1000.0))
