@@ -75,6 +75,7 @@ def log(*a):
 KERNELS = {"index_prep": ["index_prep_kernel"],
            "qgs_scan": ["qgs_scan_kernel"], "topk_select": ["topk_select_reg_kernel"],
            "gate_fill": ["errorgate_kernel", "waterfill_kernel"],
+           "topk_gate_fill": ["topk_gate_fill_kernel"],
            "topq": ["topq_linear_kernel", "topq_row_kernel"],
            "residual_flash": ["resflash_kernel"]}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
@@ -601,6 +602,9 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
         "qgs_scan": B * HKV * n_mid * 32,                      # int8 codes
         "topk_select": R * (-(-n_mid // 64)) * 4 + R * NSX * 4,  # tile maxima, sel out
         "gate_fill": R * Cn * (2 * D * 4 + 4) + R * NSX * D * 2,  # Sk, Sk2, n; K of sel
+        # below 256 rows: top-k, gate and fill in one launch
+        "topk_gate_fill": (R * (-(-n_mid // 64)) * 4 + R * NSX * 4
+                           + R * Cn * (2 * D * 4 + 4) + R * NSX * D * 2),
         "topq": R * n_mid * (2 + 1) + R * E * 4,               # 16-bit score heads + byte ids; exp out
         "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * (D * 4 + 4),  # K,V exact set; Sv, q.Sk
     }

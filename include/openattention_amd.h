@@ -190,8 +190,8 @@ int oa_waterfill(const float* score, const float* n_t, int rows, int C, int budg
                  void* stream);
 
 /*
- * ErrorGate and water-filling (two launches on the stream; score and n_t are also written
- * out).  Same results as oa_errorgate followed by oa_waterfill.  qsk (rows, C) fp32, when not
+ * ErrorGate and water-filling (one launch below 256 rows, two above; score and n_t are also
+ * written out).  Same results as oa_errorgate followed by oa_waterfill.  qsk (rows, C) fp32, when not
  * null, receives q . Sk_c of every cluster (pooled sums, before the selected tokens leave them)
  * for oa_residual_flash; no counterpart in the reference.
  */
@@ -200,6 +200,24 @@ int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, l
                  const int32_t* sel, long sel_stride, int n_sel, const float* Sk, const float* Sk2,
                  const float* nb, int C, float sm_scale, float sm_scale_sq, int budget,
                  float* score, float* n_t, float* quota, float* qsk, void* stream);
+
+/*
+ * oa_topk_select_heads followed by oa_gate_fill (n_sel = ns + nl + k_top, sel written as by
+ * oa_topk_select_heads): the same sel, marked heads, score, n_t, quota and qsk.  Below 256 rows
+ * with a register top-k (k_top <= 16 and at most 1024 score tiles) it is one launch in which
+ * each row's workgroup runs its top-k and then its gate and fill; otherwise the two calls.
+ * Replaces the consecutive _k_select and _k_errorgate / _k_waterfill steps of the deployed decode
+ * graph (inference/graph_runner.py:123-159, inference/ours_fused.py:122-216); the fusion itself
+ * has no counterpart in the reference.
+ */
+int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, long tm_stride, int ntiles,
+                      const int* n_dev, int ns, int nl, int k_top, const int8_t* codes, int Lmax,
+                      const int8_t* limbs, const int* fexp, const void* q, long q_stride,
+                      const void* K, long k_stride_b, long k_stride_s, int rows, int kv_rows,
+                      int head_dim, const int32_t* asg, long asg_stride, int32_t* sel,
+                      long sel_stride, const float* Sk, const float* Sk2, const float* nb, int C,
+                      float sm_scale, float sm_scale_sq, int budget, float* score, float* n_t,
+                      float* quota, float* qsk, void* stream);
 
 /*
  * Within-cluster top-q: the q_c best tail members of every cluster by QGS score (ties to the

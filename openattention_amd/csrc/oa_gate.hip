@@ -15,6 +15,7 @@
 // are reproducible bit for bit on the CPU.
 #include "oa_common.h"
 #include "oa_detmath.h"
+#include "oa_topk_row.h"
 
 namespace {
 
@@ -568,6 +569,38 @@ __global__ void __launch_bounds__(kGateThreads) gate_fill_kernel(GateArgs a, flo
     waterfill_row<NS>(s_score, s_nt, quota + (long)row * a.C, a.C, budget, threadIdx.x, s_cw);
 }
 
+// fewer rows than compute units, with a register top-k: the row's top-k (wave 0), then its gate
+// and fill, in one workgroup.  The top-k's sel row is written to global memory and read back by
+// the gate after the barrier (one workgroup, one compute unit: the barrier orders it); the
+// marked score heads are read by the next launch.
+struct TopkArgs {
+  uint16_t* H; long h_stride;
+  const float* TM; long tm_stride; int ntiles;
+  const int* n_dev; int ns, nl, k_top;
+  oa_sel::Rescore rs;
+};
+template <int NS, int TPL, int KR>
+__global__ void __launch_bounds__(kGateThreads) topk_gate_fill_kernel(TopkArgs t, GateArgs a,
+                                                                      int32_t* __restrict__ sel,
+                                                                      float* __restrict__ quota,
+                                                                      double budget) {
+  __shared__ float s_score[kMaxC], s_nt[kMaxC];
+  __shared__ double2 s_cw[kMaxC];
+  const int row = blockIdx.x;
+  if (threadIdx.x < 64)
+    oa_sel::topk_reg_row<TPL, KR, true>(t.H, t.h_stride, t.TM, t.tm_stride, t.ntiles, sel,
+                                        a.sel_stride, *t.n_dev, t.ns, t.nl, t.k_top, t.rs, row,
+                                        threadIdx.x);
+  __syncthreads();
+  gate_row(a, row, s_score, s_nt);
+  for (int c = threadIdx.x; c < a.C; c += kGateThreads) {
+    a.score[(long)row * a.out_stride + c] = s_score[c];
+    a.n_t[(long)row * a.out_stride + c] = s_nt[c];
+  }
+  if (threadIdx.x < 64)
+    waterfill_row<NS>(s_score, s_nt, quota + (long)row * a.C, a.C, budget, threadIdx.x, s_cw);
+}
+
 int launch_fill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,
                 hipStream_t s) {
   const int ns = (C + 63) / 64;
@@ -649,6 +682,69 @@ extern "C" int oa_gate_fill(const void* q, long q_stride, const void* K, long k_
   const int st = OA_LAUNCH_STATUS();
   if (st) return st;
   return launch_fill(score, n_t, rows, C, budget, quota, (hipStream_t)stream);
+}
+
+extern "C" int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, long tm_stride,
+                                 int ntiles, const int* n_dev, int ns, int nl, int k_top,
+                                 const int8_t* codes, int Lmax, const int8_t* limbs,
+                                 const int* fexp, const void* q, long q_stride, const void* K,
+                                 long k_stride_b, long k_stride_s, int rows, int kv_rows,
+                                 int head_dim, const int32_t* asg, long asg_stride, int32_t* sel,
+                                 long sel_stride, const float* Sk, const float* Sk2,
+                                 const float* nb, int C, float sm_scale, float sm_scale_sq,
+                                 int budget, float* score, float* n_t, float* quota, float* qsk,
+                                 void* stream) {
+  const int n_sel = ns + nl + k_top;
+  const int tpl = (ntiles + 63) / 64;
+  const bool reg = (k_top <= 9 && tpl <= 9) || (k_top <= 16 && tpl <= 16);
+  if (rows >= kFuseRows || !reg) {
+    // two launches: the top-k variant the row length needs, then the gate and fill
+    int st = oa_topk_select_heads(H, h_stride, TM, tm_stride, rows, ntiles, sel, sel_stride, n_dev,
+                                  ns, nl, k_top, codes, kv_rows, Lmax, limbs, fexp, stream);
+    if (st) return st;
+    return oa_gate_fill(q, q_stride, K, k_stride_b, k_stride_s, rows, kv_rows, head_dim, asg,
+                        asg_stride, sel, sel_stride, n_sel, Sk, Sk2, nb, C, sm_scale, sm_scale_sq,
+                        budget, score, n_t, quota, qsk, stream);
+  }
+  // the checks of both launches it replaces
+  if (!H || !codes || !limbs || !fexp || kv_rows <= 0 || rows != kv_rows * oa_sel::GQ ||
+      Lmax <= 0 || (reinterpret_cast<uintptr_t>(codes) & 15) ||
+      (reinterpret_cast<uintptr_t>(limbs) & 3) || ntiles <= 0 || k_top < 0 || k_top > ntiles ||
+      ns < 0 || nl < 0 || ns > 64 || nl > 64 || sel_stride < n_sel || head_dim != OA_D ||
+      n_sel > kMaxSel || C <= 0 || C > kMaxC || budget < 0 || k_stride_b % 8 || k_stride_s % 8 ||
+      (reinterpret_cast<uintptr_t>(K) & 15))
+    return OA_EINVAL;
+  TopkArgs t;
+  t.H = H; t.h_stride = h_stride; t.TM = TM; t.tm_stride = tm_stride; t.ntiles = ntiles;
+  t.n_dev = n_dev; t.ns = ns; t.nl = nl; t.k_top = k_top;
+  t.rs = oa_sel::Rescore{codes, (long)Lmax, limbs, fexp};
+  GateArgs a;
+  a.q = (const uint16_t*)q; a.q_stride = q_stride;
+  a.K = (const uint16_t*)K; a.k_sb = k_stride_b; a.k_ss = k_stride_s; a.G = rows / kv_rows;
+  a.asg = asg; a.asg_stride = asg_stride;
+  a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
+  a.Sk = Sk; a.Sk2 = Sk2; a.st_stride_r = (long)C * OA_D;
+  a.nb = nb; a.nb_stride = C;
+  a.score = score; a.n_t = n_t; a.out_stride = C; a.qsk = qsk;
+  a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
+  const size_t lds = sizeof(float) * (size_t)n_sel * OA_D;
+  const int nsl = (C + 63) / 64;
+  const dim3 g(rows), blk(kGateThreads);
+  hipStream_t s = (hipStream_t)stream;
+  const double bd = (double)budget;
+#define OA_TGF(NS)                                                                              \
+  do {                                                                                          \
+    if (k_top <= 9 && tpl <= 9)                                                                 \
+      hipLaunchKernelGGL((topk_gate_fill_kernel<NS, 9, 9>), g, blk, lds, s, t, a, sel, quota, bd); \
+    else                                                                                        \
+      hipLaunchKernelGGL((topk_gate_fill_kernel<NS, 16, 16>), g, blk, lds, s, t, a, sel, quota, bd); \
+  } while (0)
+  if (nsl == 1) OA_TGF(1);
+  else if (nsl == 2) OA_TGF(2);
+  else if (nsl == 3) OA_TGF(3);
+  else OA_TGF(4);
+#undef OA_TGF
+  return OA_LAUNCH_STATUS();
 }
 
 extern "C" int oa_waterfill(const float* score, const float* n_t, int rows, int C, int budget,

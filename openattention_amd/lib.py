@@ -38,6 +38,8 @@ SIGNATURES = {
     "oa_topk_select_heads": [P, L, P, L, I, I, P, L, P, I, I, I, P, I, I, P, P, P],
     "oa_errorgate": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, P, P, P],
     "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P, P],
+    "oa_topk_gate_fill": [P, L, P, L, I, P, I, I, I, P, I, P, P, P, L, P, L, L, I, I, I, P, L, P, L,
+                          P, P, P, I, F, F, I, P, P, P, P, P],
     "oa_waterfill": [P, P, I, I, I, P, P],
     "oa_topq": [P, L, P, L, P, I, I, I, P, I, P, P],
     "oa_topq_path": [P, L, P, L, P, I, I, I, P, I, P, I, P],

@@ -27,6 +27,7 @@ G = HQ // HKV
 SC = D ** -0.5
 RMAX = 256
 SCAN_TILE = 64
+FUSE_ROWS = 256      # below this many query-head rows: top-k, gate and fill in one launch
 
 
 class Ctx:
@@ -225,12 +226,19 @@ class OursHIP(Method):
         mark("index_prep")
         ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM, n_dev, ns, nl)
         mark("qgs_scan")
-        ops.topk_select_heads(self.H, self.TM, sel, n_dev, ns, nl, k_top, st.codes, self.limbs,
-                              self.fexp)
-        mark("topk_select")
-        ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota,
-                      sc, self.E, qsk=self.qsk)
-        mark("gate_fill")
+        if self.R < FUSE_ROWS:
+            # fewer rows than compute units: each row's top-k, gate and fill in one workgroup
+            ops.topk_gate_fill(self.H, self.TM, n_dev, ns, nl, k_top, st.codes, self.limbs,
+                               self.fexp, qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score,
+                               self.n_t, self.quota, sc, self.E, qsk=self.qsk)
+            mark("topk_gate_fill")
+        else:
+            ops.topk_select_heads(self.H, self.TM, sel, n_dev, ns, nl, k_top, st.codes, self.limbs,
+                                  self.fexp)
+            mark("topk_select")
+            ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t,
+                          self.quota, sc, self.E, qsk=self.qsk)
+            mark("gate_fill")
         ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, n_dev, st.codes, self.limbs,
                        self.fexp, self.S)
         mark("topq")

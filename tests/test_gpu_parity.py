@@ -167,6 +167,17 @@ def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
     ops.qgs_scan_heads(st.codes, limbs, fexp, H, TMh, n_dev, ns, nl)
     torch.cuda.synchronize()
     r.update(H=H.cpu().numpy().view(np.uint16).copy(), TMh=TMh.cpu().numpy())
+    # top-k, gate and fill in one call (one launch below 256 rows) on a copy of the heads
+    Hf = H.clone()
+    self_ = torch.full_like(sel, -7)
+    scf, ntf, qf, qskf = (torch.empty_like(score2), torch.empty_like(n_t2), torch.empty_like(quota2),
+                          torch.empty_like(qsk))
+    ops.topk_gate_fill(Hf, TMh, n_dev, ns, nl, k, st.codes, limbs, fexp, qr, K, st.asg, self_, st.Sk,
+                       st.Sk2, st.nb, scf, ntf, qf, SC, E, qsk=qskf)
+    torch.cuda.synchronize()
+    r.update(tgf=dict(sel=self_.cpu().numpy(), H=Hf.cpu().numpy().view(np.uint16).copy(),
+                      score=scf.cpu().numpy(), n_t=ntf.cpu().numpy(), quota=qf.cpu().numpy(),
+                      qsk=qskf.cpu().numpy()))
     ops.topk_select_heads(H, TMh, selh, n_dev, ns, nl, k, st.codes, limbs, fexp)
     ops.topq_heads(H, st.asg8, quota, exph, n_dev, st.codes, limbs, fexp, S32)
     ops.topq_heads(H, st.asg8, quota, exph3, n_dev, st.codes, limbs, fexp, S32, path=3)
@@ -233,6 +244,13 @@ def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
     assert np.all(np.take_along_axis(g["H_after"], g["selh"].astype(np.int64), 1) == 0x007F)
     assert np.array_equal(g["exph"], ref["exp_idx"]), "top-q over heads differs"
     assert np.array_equal(g["exph3"], ref["exp_idx"]), "top-q over heads (key-prefix) differs"
+    # top-k + gate + fill in one call: the same selection, marked heads, gate and fill outputs
+    t = g["tgf"]
+    assert np.array_equal(t["sel"], ref["sel"]), "top-k + gate + fill: selection differs"
+    assert np.array_equal(t["H"], g["H_after"]), "top-k + gate + fill: marked heads differ"
+    for name, want in (("score", g["score"]), ("n_t", g["n_t"]), ("quota", g["quota"]),
+                       ("qsk", g["qsk"])):
+        assert np.array_equal(t[name], want), f"top-k + gate + fill: {name} differs"
     live = np.isfinite(ref["log_n"])
     assert np.array_equal(np.isfinite(g["log_n"]), live)
     assert np.allclose(g["log_n"][live], ref["log_n"][live], rtol=1e-6)
