@@ -66,6 +66,9 @@ constexpr int kUPT = 8;                        // gathered entries per thread ha
 constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
 constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster with no quota
 constexpr int kLdsLimit = 160 * 1024;
+constexpr int kSmallRows = 256;               // below: oa_topq_heads path 0 in one launch
+// static LDS of the linear-bin algorithm (13.6 KB measured; held beside the key-prefix one's)
+constexpr long kLinStaticLds = 4L * (14 * 256 + 128);
 constexpr int32_t kRowMarked = -2;              // exp_idx[row][0] of a row left to the key-prefix kernel
 
 enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3, kModeSplit = 4 };
@@ -406,8 +409,7 @@ __device__ __forceinline__ void rank_and_write(int E, int tid, const int* s_base
 }
 
 template <int PPT, int LB>
-__global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
-  extern __shared__ unsigned long long dyn[];
+__device__ __forceinline__ void topq_row_body(const TopqArgs& a, int row, unsigned long long* dyn) {
   __shared__ int s_w[kMaxC];              // min(q_c, E - base_c), clamped at 0
   __shared__ int s_base[kMaxC + 1];       // first exp_idx slot of each cluster
   __shared__ int s_t[kMaxC];              // members chosen
@@ -434,7 +436,6 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   int* s_out = s_hist;                                                        // after P5
   uint32_t* s_cst = reinterpret_cast<uint32_t*>(s_hist + a.hwords);           // cpow
 
-  const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -814,6 +815,12 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   rank_and_write(E, tid, s_base, s_t, s_tpre, s_cst, s_out, erow);
 }
 
+template <int PPT, int LB>
+__global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
+  extern __shared__ unsigned long long dyn[];
+  topq_row_body<PPT, LB>(a, blockIdx.x, dyn);
+}
+
 
 // The linear-bin kernel: the common path.  Scores are binned linearly over the row's range of
 // qualifying scores, [smin, smax]: bin(s) = min(NB - 1, (int)((s - smin) * NB / (smax - smin)))
@@ -828,10 +835,9 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 //
 // HEADS: the score rows hold 16-bit key heads (oa_qgs_scan_heads), which are all the kernel
 // keeps of a score anyway; exact scores come from the codes (oa::qgs_score).
+// Returns true for a row it leaves to the key-prefix algorithm (marked kRowMarked).
 template <int PPT, int LB, bool HEADS>
-// up to 64 VGPRs for the single-segment instantiations: two workgroups (rows) per unit
-__global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kernel(TopqArgs a) {
-  extern __shared__ unsigned long long dyn[];
+__device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, unsigned long long* dyn) {
   __shared__ int s_w[kMaxC];
   __shared__ int s_base[kMaxC + 1];
   __shared__ int s_t[kMaxC];
@@ -855,7 +861,6 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   int* s_out = s_hist;                                                        // after P5
   uint32_t* s_cst = reinterpret_cast<uint32_t*>(s_hist + a.hwords);           // cpow
 
-  const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -1061,7 +1066,7 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
                                             : -INFINITY;
     }
     if (tid == 0) erow[0] = kRowMarked;
-    return;
+    return true;
   }
   if (wave == 0) chosen_prefix(s_t, s_tpre, lane);
   oa::lds_barrier();
@@ -1110,6 +1115,29 @@ __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kerne
   select_all_staged(C, wave, lane, s_mode, s_bcnt, s_t, s_above, s_g, s_goff, s_cst, s_tpre, s_klo,
                     s_khi, s_ccur, true, kP5Thread);
   rank_and_write(E, tid, s_base, s_t, s_tpre, s_cst, s_out, erow);
+  return false;
+}
+
+template <int PPT, int LB, bool HEADS>
+// up to 64 VGPRs for the single-segment instantiations: two workgroups (rows) per unit
+__global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kernel(TopqArgs a) {
+  extern __shared__ unsigned long long dyn[];
+  topq_linear_body<PPT, LB, HEADS>(a, blockIdx.x, dyn);
+}
+
+// Fewer rows than compute units (one workgroup per unit, so its LDS and registers are free):
+// the linear-bin algorithm and, on a row it cannot finish, the key-prefix algorithm in the same
+// workgroup, instead of a second launch over every row.  lin and pre are the two algorithms'
+// arguments (LDS layouts); the dynamic LDS holds either's.
+template <int PPT, int LB, int PLB>
+__global__ void __launch_bounds__(kThreads) topq_small_kernel(TopqArgs lin, TopqArgs pre) {
+  extern __shared__ unsigned long long dyn[];
+  if (topq_linear_body<PPT, LB, true>(lin, blockIdx.x, dyn)) {   // uniform
+    // the row's exact scores (S32) written above are read back by every wave
+    __threadfence();
+    __syncthreads();
+    topq_row_body<PPT, PLB>(pre, blockIdx.x, dyn);
+  }
 }
 
 template <int PPT, int LB>
@@ -1146,6 +1174,22 @@ int launch_linear_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStrea
   return launch_linear<44, LB, HEADS>(a, rows, lds, s);
 }
 
+template <int PPT, int LB, int PLB>
+int launch_small(const TopqArgs& lin, const TopqArgs& pre, int rows, size_t lds, hipStream_t s) {
+  const hipError_t e = hipFuncSetAttribute((const void*)topq_small_kernel<PPT, LB, PLB>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((topq_small_kernel<PPT, LB, PLB>), dim3(rows), dim3(kThreads), lds, s, lin, pre);
+  return OA_LAUNCH_STATUS();
+}
+template <int LB, int PLB>
+int launch_small_ppt(const TopqArgs& lin, const TopqArgs& pre, int rows, int Lmax, size_t lds,
+                     hipStream_t s) {
+  if (Lmax <= kThreads * 8) return launch_small<8, LB, PLB>(lin, pre, rows, lds, s);
+  if (Lmax <= kThreads * 16) return launch_small<16, LB, PLB>(lin, pre, rows, lds, s);
+  return launch_small<36, LB, PLB>(lin, pre, rows, lds, s);
+}
+
 }  // namespace
 
 namespace {
@@ -1180,6 +1224,22 @@ int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool hea
     al.hwords = (int)((std::max<long>((long)C * ((1 << al.lb) + 16) + 64, a.cpow) + 3) & ~3L);
     al.gcap = al.hwords / 2;
     const size_t lds_lin = 4 * (size_t)al.hwords + 4 * (size_t)a.cpow;
+    if (heads && pre && rows < kSmallRows && Lmax <= kThreads * 36) {
+      // one launch: the key-prefix algorithm's gathered list shrinks by the linear-bin
+      // algorithm's static LDS, which the same workgroup holds (path 3, every row marked, then
+      // runs every row through the key-prefix algorithm in this kernel)
+      TopqArgs ak = a;
+      const long room2 = room - kLinStaticLds;
+      ak.ucap = (int)std::min<long>(kUCapMax, room2 / 8) & ~3;
+      ak.gcap = std::min(ak.hwords / 2, ak.ucap - E);
+      if (ak.gcap >= 64) {
+        const size_t lds_pre = 8 * (size_t)(ak.ucap + 64) + 4 * (size_t)ak.hwords + 4 * (size_t)ak.cpow;
+        const size_t lds_small = std::max(lds_lin, lds_pre);
+        if (al.lb == 7 && ak.lb == 8) return launch_small_ppt<7, 8>(al, ak, rows, Lmax, lds_small, s);
+        if (al.lb == 6 && ak.lb == 7) return launch_small_ppt<6, 7>(al, ak, rows, Lmax, lds_small, s);
+        if (al.lb == 5 && ak.lb == 6) return launch_small_ppt<5, 6>(al, ak, rows, Lmax, lds_small, s);
+      }
+    }
     int st;
     if (heads) st = al.lb == 7 ? launch_linear_lb<7, true>(al, rows, Lmax, lds_lin, s)
                     : al.lb == 6 ? launch_linear_lb<6, true>(al, rows, Lmax, lds_lin, s)
