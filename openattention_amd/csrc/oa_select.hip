@@ -101,10 +101,11 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
       oa_v4i zero = {0, 0, 0, 0};
       oa_v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_op, tok < Lmax ? b_op[t][b] : 0L,
                                                          zero, 0, 0, 0);
-      double s = (double)acc[3];
-      s = fma(s, 256.0, (double)acc[2]);
-      s = fma(s, 256.0, (double)acc[1]);
-      s = fma(s, 256.0, (double)acc[0]);
+      // the exact integer sum: limb partials are below 2^19 in magnitude, so each pair joins
+      // exactly in int32 (< 2^28) and the two pairs exactly in fp64 (< 2^44)
+      const int xh = acc[3] * 256 + acc[2];
+      const int xl = acc[1] * 256 + acc[0];
+      const double s = fma((double)xh, 65536.0, (double)xl);
       float sc = (float)(s * inv);
       if (tok < ns || tok >= dead_hi) sc = -INFINITY;
       if (HEADS) s_h[wave][kg][b * 16 + nn] = oa::score_head(sc);
