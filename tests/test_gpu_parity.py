@@ -562,6 +562,70 @@ def test_topk_rows_with_ties_large_k(n, k):
     assert np.array_equal(after, marked)
 
 
+@pytest.mark.parametrize("N,C,k_top", [(4096, 64, 16), (8192, 100, 12), (16384, 192, 9),
+                                         (32768, 256, 16)])
+def test_small_batch_fused_launches(N, C, k_top):
+    """Below 256 rows (one sequence, 32 query-head rows): oa_topk_gate_fill (top-k, gate and
+    fill in one launch; here 1 to 4 cluster slots per lane and the k <= 16 register top-k) equals
+    oa_topk_select_heads + oa_gate_fill bit for bit and the restatement's sel, scores, tail counts
+    and quotas; the one-launch top-q (7/8-, 6/7- and 5/6-bit histogram pairs, 8 / 16 / 36
+    positions per thread) gives the restatement's expanded sets on its linear path (path 0), with
+    every row in its key-prefix branch (path 3), and the standalone linear kernel (path 2) agrees
+    on every row it does not mark."""
+    print(f"[case] small-batch fused N={N} C={C} k={k_top}", flush=True)
+    lay = build_layer(cfg=2, B=1, N=N, Lmax=N + 64, C=C, n_centers=256, dev=DEV)
+    st = lay.st
+    R = HQ
+    n = lay.T
+    ns, nl = 3, 3
+    E = max(4 * k_top, N // 50)
+    ref = O.decode_step(state_np(lay), bf16_np(lay.q.reshape(-1, D)), n, ns, nl, k_top, E, G,
+                        np.float32(SC), np.float32(SC2), rmax=RMAX, update_index=False)
+    K = lay.K.reshape(-1, lay.Lmax, D)
+    qr = lay.q.reshape(R, D).contiguous()
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    ntiles = -(-lay.Lmax // 64)
+    limbs = torch.zeros(HKV, 16, 32, device=DEV, dtype=torch.int8)
+    fexp = torch.zeros(R, device=DEV, dtype=torch.int32)
+    zq = torch.zeros(R, 32, device=DEV)
+    ops.qgs_prep(qr, st.U, st.scale, limbs, fexp, zq)
+    H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
+    TM = torch.empty(R, ntiles, device=DEV)
+    ops.qgs_scan_heads(st.codes, limbs, fexp, H, TM, n_dev, ns, nl)
+    got = {}
+    for fused in (False, True):
+        Hx = H.clone()
+        sel = torch.full((R, ns + nl + k_top), -7, device=DEV, dtype=torch.int32)
+        score, n_t, quota, qsk = (torch.empty(R, C, device=DEV) for _ in range(4))
+        if fused:
+            ops.topk_gate_fill(Hx, TM, n_dev, ns, nl, k_top, st.codes, limbs, fexp, qr, K, st.asg,
+                               sel, st.Sk, st.Sk2, st.nb, score, n_t, quota, SC, E, qsk=qsk)
+        else:
+            ops.topk_select_heads(Hx, TM, sel, n_dev, ns, nl, k_top, st.codes, limbs, fexp)
+            ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score, n_t, quota, SC, E, qsk=qsk)
+        torch.cuda.synchronize()
+        got[fused] = dict(Ht=Hx, quota_t=quota, H=Hx.cpu().numpy(), sel=sel.cpu().numpy(),
+                          score=score.cpu().numpy(), n_t=n_t.cpu().numpy(),
+                          quota=quota.cpu().numpy(), qsk=qsk.cpu().numpy())
+    for name in ("H", "sel", "score", "n_t", "quota", "qsk"):
+        assert np.array_equal(got[True][name], got[False][name]), f"fused {name} differs"
+    assert np.array_equal(got[True]["sel"], ref["sel"]), "selection differs from the restatement"
+    for name in ("score", "n_t", "quota"):
+        assert np.array_equal(got[True][name], ref[name]), f"{name} differs from the restatement"
+    Hq, quota = got[True]["Ht"], got[True]["quota_t"]
+    S32 = torch.empty(R, ntiles * 64, device=DEV)
+    e = {}
+    for path in (0, 2, 3):
+        ex = torch.full((R, E), 777, device=DEV, dtype=torch.int32)
+        ops.topq_heads(Hq, st.asg8, quota, ex, n_dev, st.codes, limbs, fexp, S32, path=path)
+        torch.cuda.synchronize()
+        e[path] = ex.cpu().numpy()
+    assert np.array_equal(e[0], ref["exp_idx"]), "one-launch top-q (path 0) differs"
+    assert np.array_equal(e[3], ref["exp_idx"]), "one-launch top-q, key-prefix branch (path 3) differs"
+    done = e[2][:, 0] != -2
+    assert np.array_equal(e[2][done], ref["exp_idx"][done]), "linear-bin kernel alone differs"
+
+
 @pytest.mark.parametrize("C,E", [(8, 27), (64, 216), (100, 679), (192, 1335), (256, 2877), (256, 40)])
 def test_waterfill_rows_with_ties_dead_and_full_clusters(C, E):
     """Water-filling on rows built for the leftover tokens: scores on a coarse grid (ties go to
