@@ -112,8 +112,6 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int kvr = row / a.G;
-  // the wave's first batch of statistics is requested before the selected keys are staged (it
-  // does not depend on them)
   constexpr int kBatch = 4;     // larger batches spill at the 64-VGPR cap
   float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
   auto issue = [&](int c0) {
@@ -128,48 +126,73 @@ __device__ __forceinline__ void gate_row(const GateArgs& a, int row, float* s_sc
       nbv[i] = a.nb[(long)row * a.nb_stride + c];
     }
   };
-  if (wave < a.C) issue(wave);
-  // ---- selected keys into LDS; per cluster, the mask of its selected tokens
   for (int c = tid; c < a.C; c += kGateThreads) s_selmask[c] = 0ull;
   __syncthreads();
-  for (int i = tid; i < a.n_sel; i += kGateThreads) {
-    const int tok = a.sel[(long)row * a.sel_stride + i];
-    if (tok >= 0) atomicOr(&s_selmask[a.asg[(long)row * a.asg_stride + tok]], 1ull << i);
-  }
-  for (int e = tid; e < a.n_sel * (OA_D / 8); e += kGateThreads) {
-    const int i = e / (OA_D / 8), d8 = (e % (OA_D / 8)) * 8;
-    const int tok = a.sel[(long)row * a.sel_stride + i];
-    float x[8];
-    if (tok >= 0) {
-      oa::unpack8(*reinterpret_cast<const uint4*>(a.K + (long)kvr * a.k_sb + (long)tok * a.k_ss + d8), x);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s_k[i * OA_D + d8 + j] = x[j];
-  }
-  __syncthreads();
+  if (wave < a.C) issue(wave);
+  // the selected positions (one per thread for the cluster masks, up to two 16-byte key words per
+  // thread for the staged keys), then their cluster ids and key words, all requested before the
+  // first batch is computed
+  constexpr int kW = OA_D / 8;
+  const long srow = (long)row * a.sel_stride;
+  const int n_sel = a.n_sel;
+  const int e0 = tid, e1 = tid + kGateThreads;
+  const int tokm = tid < n_sel ? a.sel[srow + tid] : -1;
+  const int tok0 = e0 < n_sel * kW ? a.sel[srow + e0 / kW] : -1;
+  const int tok1 = e1 < n_sel * kW ? a.sel[srow + e1 / kW] : -1;
   const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
   const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
   const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
-  // ---- tail statistics and the two dot products, six clusters per wave at a time
-  for (int c0 = wave; c0 < a.C; c0 += kGateWaves * kBatch) {
-    if (c0 != wave) issue(c0);                  // the batch's statistics, all loads in flight
+  const int cm = tokm >= 0 ? a.asg[(long)row * a.asg_stride + tokm] : -1;
+  uint4 kw0 = make_uint4(0u, 0u, 0u, 0u), kw1 = kw0;
+  if (tok0 >= 0)
+    kw0 = *reinterpret_cast<const uint4*>(a.K + (long)kvr * a.k_sb + (long)tok0 * a.k_ss + (e0 % kW) * 8);
+  if (tok1 >= 0)
+    kw1 = *reinterpret_cast<const uint4*>(a.K + (long)kvr * a.k_sb + (long)tok1 * a.k_ss + (e1 % kW) * 8);
+  auto dots = [&](float k0, float k1, float t0, float t1, float nbc, int c,
+                  unsigned long long mask) {
+    float zb, sv, nt, qs;
+    gate_dots(a, k0, k1, t0, t1, nbc, q_lo, q_hi, qq_lo, qq_hi, mask, s_k, lane, &zb, &sv, &nt, &qs);
+    if (lane == 0) {
+      s_zbar[c] = zb;
+      s_s2[c] = sv;
+      s_nt[c] = nt;
+      s_qsk[c] = qs;
+    }
+  };
+  // ---- the first batch as if its clusters held no selected token (most do not) while the
+  // selected keys arrive; a cluster that holds one is done again below
+#pragma unroll
+  for (int i = 0; i < kBatch; ++i) {
+    const int c = wave + kGateWaves * i;
+    if (c < a.C) dots(sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], c, 0ull);
+  }
+  // ---- selected keys into LDS; per cluster, the mask of its selected tokens
+  if (cm >= 0) atomicOr(&s_selmask[cm], 1ull << tid);
+  if (e0 < n_sel * kW) {
+    float x[8];
+    oa::unpack8(kw0, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_k[(e0 / kW) * OA_D + (e0 % kW) * 8 + j] = x[j];
+  }
+  if (e1 < n_sel * kW) {
+    float x[8];
+    oa::unpack8(kw1, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_k[(e1 / kW) * OA_D + (e1 % kW) * 8 + j] = x[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kBatch; ++i) {
+    const int c = wave + kGateWaves * i;
+    if (c < a.C && s_selmask[c]) dots(sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], c, s_selmask[c]);
+  }
+  // ---- the other batches, all loads of a batch in flight
+  for (int c0 = wave + kGateWaves * kBatch; c0 < a.C; c0 += kGateWaves * kBatch) {
+    issue(c0);
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const int c = c0 + kGateWaves * i;
-      if (c < a.C) {
-        float zb, sv, nt, qs;
-        gate_dots(a, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
-                  s_selmask[c], s_k, lane, &zb, &sv, &nt, &qs);
-        if (lane == 0) {
-          s_zbar[c] = zb;
-          s_s2[c] = sv;
-          s_nt[c] = nt;
-          s_qsk[c] = qs;
-        }
-      }
+      if (c < a.C) dots(sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], c, s_selmask[c]);
     }
   }
   __syncthreads();
