@@ -12,10 +12,11 @@ timed loop replays a hipGraph of one step of every replica, as the deployed path
 (graph_runner.py:639-655); n advances by one token per step.
 
 Reported (one JSON line): us per layer-step (value), tokens/s (B / t_layer), the roofline of
-the dominant kernel (algorithmic bytes per launch / its average duration from HIP events),
-the stage-level algorithmic bandwidth, the per-stage breakdown, the dense bf16 decode
-comparator (this library's split-K kernel and torch SDPA, the faster is the denominator) and
-the CPU restatement timed on one sequence of the same workload (cpu_baseline, scaled to B).
+the dominant kernel (algorithmic bytes per launch / its launch time, that stage alone over the
+replicas in one hipGraph, as the step is timed), the stage-level algorithmic bandwidth, the
+per-stage breakdown (each stage graph-timed the same way), the dense bf16 decode comparator
+(this library's split-K kernel, graph-timed, and torch SDPA, eager) and the CPU restatement of
+the same step over all B sequences on the host's cores (cpu_baseline).
 """
 from __future__ import annotations
 
@@ -70,10 +71,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def dense_graph_us(calls, reps: int = 10) -> float:
-    """The dense comparator timed as the sparse step is: `calls` (one dense decode per layer
-    replica) captured in one hipGraph after an eager warm-up, `reps` replays; microseconds per
-    call."""
+def graph_us(calls, reps: int = 10) -> float:
+    """Launches timed as the sparse step is: `calls` (one launch sequence per layer replica)
+    captured in one hipGraph after an eager warm-up, `reps` replays; microseconds per call."""
     import torch
     for _ in range(2):
         for c in calls:
@@ -264,7 +264,7 @@ def config4_sweep(a):
             dq = [Qs[l].reshape(-1, D).contiguous() for l in range(L)]
             dk = [(Ks[l].view(-1, Lmax, D), Vs[l].view(-1, Lmax, D)) for l in range(L)]
             douts = [torch.empty_like(x) for x in dq]
-            dense_us = dense_graph_us([
+            dense_us = graph_us([
                 (lambda l=l: ops.dense_decode(dq[l], dk[l][0], dk[l][1], n_dense, out=douts[l], ws=ws))
                 for l in range(L)])
             rec = {"config": "config4", "B": B, "N": N, "rho": rho, "C": m.Cn, "E": m.E,
@@ -595,22 +595,26 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
     us_layer = gpu_ms * 1e3 / layer_steps
     log(f"[bench] timed {layer_steps} layer-steps: {us_layer:.1f} us/layer-step (wall {wall * 1e6 / layer_steps:.1f} us)")
 
-    # ---- per-stage breakdown (eager, events between stages on the launch stream)
-    per = {}
-    for rep in range(3):
-        marks = []
-        i = a.warmup + (rep % a.steps)
-        n_buf.copy_(n_arr[i:i + 1])
-        for l in range(L):
-            mk = []
-            m.decode(l, Qs[l], N + i, marks=mk)
-            marks.append(mk)
-        torch.cuda.synchronize()
-        for mk in marks:
-            for (n0, e_a), (n1, e_b) in zip(mk[:-1], mk[1:]):
-                per.setdefault(n1, []).append(e_a.elapsed_time(e_b) * 1e3)
-    stage_us = {k: statistics.median(v) for k, v in per.items()}
-    log("[bench] stages (us): " + ", ".join(f"{k} {v:.1f}" for k, v in stage_us.items()))
+    # ---- per-stage breakdown: each stage alone, one launch per layer replica captured in one
+    # hipGraph and replayed, as the whole step is timed (eager events around microsecond-scale
+    # launches would add the launch overhead).  The stages re-run over the state of the last
+    # timed step; index_prep re-adds its token each time, so the mutable index fields are
+    # restored afterwards.
+    mutable = ("codes", "asg", "asg8", "nb", "Sk", "Sk2", "Sv", "reclist", "reccnt")
+    snap = [{f: getattr(m.st[l], f).clone() for f in mutable} for l in range(L)]
+    i_last = n_steps - 1
+    n_buf.copy_(n_arr[i_last:i_last + 1])
+    per_layer = [m.decode_stages(l, Qs[l], N + i_last) for l in range(L)]
+    stage_us = {}
+    for j, (nm, _) in enumerate(per_layer[0]):
+        stage_us[nm] = graph_us([per_layer[l][j][1] for l in range(L)])
+    for l in range(L):
+        for f in mutable:
+            getattr(m.st[l], f).copy_(snap[l][f])
+    del snap, per_layer
+    torch.cuda.synchronize()
+    log("[bench] stages (us, graph-timed): " + ", ".join(f"{k} {v:.1f}" for k, v in stage_us.items())
+        + f"; sum {sum(stage_us.values()):.1f}")
 
     # ---- algorithmic bytes per launch of every stage kernel, and of the stage as a whole
     # (stage: int8 codes + bf16 K,V of the exact set + fp32 Sk, Sk2, Sv and n, each read once)
@@ -639,6 +643,7 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
     roof_kernel = max(stage_us, key=lambda k: stage_us[k])
     dom_bytes = alg[roof_kernel]
     achieved = dom_bytes / (stage_us[roof_kernel] * 1e-6) / 1e9
+    # (the dominant stage's launch time is its own hipGraph's, like the step's)
     roofline = {"kernel": roof_kernel, "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
                 "traffic": traffic_bytes(roof_kernel), "bytes_per_launch": dom_bytes,
@@ -669,7 +674,7 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
             dq = [Qs[l].reshape(-1, D).contiguous() for l in range(L)]
             dk = [(Ks[l].view(-1, Lmax, D), Vs[l].view(-1, Lmax, D)) for l in range(L)]
             douts = [torch.empty_like(x) for x in dq]
-            dense["ours_splitk"] = round(dense_graph_us([
+            dense["ours_splitk"] = round(graph_us([
                 (lambda l=l: ops.dense_decode(dq[l], dk[l][0], dk[l][1], n_dense, out=douts[l], ws=ws))
                 for l in range(L)]), 1)
             del dq, dk, douts
@@ -696,36 +701,27 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
     # eager and far slower, is reported beside it only)
     dense_best = dense.get("ours_splitk") if isinstance(dense.get("ours_splitk"), float) else None
 
-    # ---- the flash step alone (what the reference's published 0.114 ms covers): exact set sel +
-    # exp_idx of the last decoded layer over layer 0's K/V, and one proxy per cluster with the
-    # stage's residual counts (proxy vectors seeded; the cost does not depend on their values)
+    # ---- the flash step alone (what the reference's published 0.114 ms covers): the exact set
+    # sel + exp_idx of the last decoded layer and one proxy per cluster with the stage's residual
+    # counts (proxy vectors seeded per replica; the cost does not depend on their values), over
+    # every replica's K/V, one hipGraph of one launch per replica
     flash_only = None
     if not a.no_dense:
         nres = m.n_t - m.quota
         logn_f = torch.where(nres > 0.5, torch.log(nres.clamp_min(1.0)), torch.full_like(nres, float("-inf")))
         gf = torch.Generator(device=dev)
         gf.manual_seed(7)
-        kb_f = torch.randn(R, Cn, D, device=dev, generator=gf).to(torch.bfloat16)
-        vb_f = torch.randn(R, Cn, D, device=dev, generator=gf).to(torch.bfloat16)
-        out_f = torch.empty_like(q0)
-
-        def run_flash():
-            ops.flash_decode(q0, K0, V0, m.last_sel, m.exp_idx, kb_f, vb_f, logn_f, proxy_per_kv=False,
-                             sm_scale=D ** -0.5, out=out_f)
-
-        for _ in range(3):
-            run_flash()
-        torch.cuda.synchronize()
-        ts = []
-        for _ in range(10):
-            x0, x1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            x0.record()
-            run_flash()
-            x1.record()
-            torch.cuda.synchronize()
-            ts.append(x0.elapsed_time(x1) * 1e3)
-        flash_only = round(statistics.median(ts), 1)
-        log(f"[bench] flash only (us): {flash_only}")
+        kb_f = [torch.randn(R, Cn, D, device=dev, generator=gf).to(torch.bfloat16) for _ in range(L)]
+        vb_f = [torch.randn(R, Cn, D, device=dev, generator=gf).to(torch.bfloat16) for _ in range(L)]
+        q_f = [Qs[l].reshape(-1, D).contiguous() for l in range(L)]
+        out_f = [torch.empty_like(x) for x in q_f]
+        flash_only = round(graph_us([
+            (lambda l=l: ops.flash_decode(q_f[l], Ks[l].view(-1, Lmax, D), Vs[l].view(-1, Lmax, D), m.last_sel,
+                                          m.exp_idx, kb_f[l], vb_f[l], logn_f, proxy_per_kv=False,
+                                          sm_scale=D ** -0.5, out=out_f[l]))
+            for l in range(L)]), 1)
+        del kb_f, vb_f, q_f, out_f
+        log(f"[bench] flash only (us, graph-timed): {flash_only}")
 
     # ---- CPU restatement of the same step on the host's cores, and torch CPU dense attention
     cpu_rec = None
@@ -754,6 +750,7 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
         "stage_alg_GBps": round(stage_gbps, 1),
         "stage_frac_of_peak": round(stage_gbps / PEAK_HBM_GBPS, 4),
         "stages_us": {k: round(v, 2) for k, v in stage_us.items()},
+        "stages_sum_us": round(sum(stage_us.values()), 2),
         "roofline": roofline,
         "dense_us": dense,
         "speedup_vs_dense": round(dense_best / us_layer, 2) if dense_best else None,

@@ -150,6 +150,10 @@ int oa_qgs_scan_heads(const int8_t* codes, int kv_rows, int Lmax, int rank, cons
  * Exact top-k per row (ties to the lower position) among the k tiles with the largest
  * maxima; sel = [0..ns) ++ [n-nl..n) ++ top; the selected scores in S are set to -inf.
  * Replaces _k_select (inference/graph_runner.py:123-159).
+ *   0 <= k_top <= min(64, ntiles), ns, nl <= 64; the decode step keeps k_top <= n - ns - nl.
+ *   A row with fewer live positions ([ns, n - nl)) than k_top is filled, after every live
+ *   position, with the lowest sink, local or unwritten positions (scored -inf, as the
+ *   reference's -inf candidates): every selected position is below ntiles * 64.
  */
 int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int rows,
                    int ntiles, int32_t* sel, long sel_stride, const int* n_dev, int ns, int nl,

@@ -540,8 +540,8 @@ extern "C" int oa_kmeans_update(const float* zP, long zp_stride, int rows, int T
                                 long asg8_stride, int C, const int32_t* init_idx, float* cent,
                                 float* cnt_out, void* stream) {
   if (rows <= 0 || T <= 0 || C <= 0 || C > kMaxC || !zP || !asg8 || !init_idx || !cent ||
-      zp_stride < (long)T * kRC || asg8_stride < T || asg8_stride % 4 ||
-      (reinterpret_cast<uintptr_t>(asg8) & 3))
+      zp_stride < (long)T * kRC || zp_stride % 4 || (reinterpret_cast<uintptr_t>(zP) & 15) ||
+      asg8_stride < T || asg8_stride % 4 || (reinterpret_cast<uintptr_t>(asg8) & 3))
     return OA_EINVAL;
   hipLaunchKernelGGL(kmeans_update_kernel, dim3(C, rows), dim3(64), 0, (hipStream_t)stream, zP, zp_stride,
                      T, asg8, asg8_stride, C, init_idx, cent, cnt_out);

@@ -603,8 +603,9 @@ struct TopkArgs {
   oa_sel::Rescore rs;
 };
 template <int NS, int TPL, int KR>
+// (sel is written here and read by gate_row through a.sel, the same memory: no __restrict__)
 __global__ void __launch_bounds__(kGateThreads) topk_gate_fill_kernel(TopkArgs t, GateArgs a,
-                                                                      int32_t* __restrict__ sel,
+                                                                      int32_t* sel,
                                                                       float* __restrict__ quota,
                                                                       double budget) {
   __shared__ float s_score[kMaxC], s_nt[kMaxC];

@@ -156,6 +156,10 @@ __device__ __forceinline__ int lanes_below(unsigned long long m, int lane) {
 // T's head, exact scores then recomputed for the list alone).  The k-th largest candidate key
 // (score key << 32 | ~position: distinct) is found the same way, and the k winners are written
 // in descending key order, as repeated wave maxima would give them.
+// Sink, local and unwritten positions are candidates scoring -inf (the register variant's and
+// graph_runner.py:145-151's rule): a row with fewer than k_top live positions is filled with the
+// lowest such positions, so the list always holds at least k_top candidates, each below
+// ntiles * 64.
 template <int TPL, bool HEADS>
 __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, long s_stride,
                                                          const float* __restrict__ TM, long tm_stride,
@@ -169,6 +173,12 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
   const int lane = threadIdx.x;
   const int n = *n_dev;
   const int dead_hi = n - nl;
+  if (k_top == 0) {                                     // uniform: sink and local only
+    int32_t* sr = sel + (long)row * sel_stride;
+    if (lane < ns) sr[lane] = lane;
+    if (lane < nl) sr[ns + lane] = n - nl + lane;
+    return;
+  }
   int lw[HEADS ? 32 : 1];
   const double inv = load_limbs<HEADS>(rs, row, lw);
   uint32_t tk[TPL];
@@ -219,7 +229,8 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
     bool q;
     unsigned long long key = 0ull;
     if (HEADS) {
-      q = cv[j] >= (T >> 16) && live;
+      // a dead position's head is that of -inf: it qualifies only when T is -inf itself
+      q = cv[j] >= (T >> 16);
     } else {
       key = tile_key(live ? __uint_as_float(cv[j]) : -INFINITY, pos);
       q = (uint32_t)(key >> 32) >= T;
@@ -230,7 +241,8 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
   }
   __syncthreads();
   if (HEADS) {
-    // exact scores of the list, four candidates' codes in flight per lane
+    // exact scores of the list, four candidates' codes in flight per lane (a dead candidate
+    // scores -inf; its code address is clamped into the row's written positions)
     const int kvr = row / GQ;
     for (int i0 = 0; i0 < nc; i0 += 256) {
       int pos[4];
@@ -239,14 +251,17 @@ __global__ void __launch_bounds__(64) topk_select_kernel(void* __restrict__ Sv, 
       for (int u = 0; u < 4; ++u) {
         const int i = min(i0 + u * 64 + lane, nc - 1);
         pos[u] = (int)s_ck[i];
-        const uint4* cp = reinterpret_cast<const uint4*>(rs.codes + ((long)kvr * rs.lmax + pos[u]) * 32);
+        const long cpos = max(min(pos[u], dead_hi - 1), 0);
+        const uint4* cp = reinterpret_cast<const uint4*>(rs.codes + ((long)kvr * rs.lmax + cpos) * 32);
         c0[u] = cp[0];
         c1[u] = cp[1];
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int i = i0 + u * 64 + lane;
-        if (i < nc) s_ck[i] = tile_key(oa::qgs_score_words(c0[u], c1[u], lw, inv), pos[u]);
+        const bool live = pos[u] >= ns && pos[u] < dead_hi;
+        if (i < nc)
+          s_ck[i] = tile_key(live ? oa::qgs_score_words(c0[u], c1[u], lw, inv) : -INFINITY, pos[u]);
       }
     }
     __syncthreads();

@@ -67,8 +67,6 @@ constexpr unsigned kNegInfKey = 0x007fffffu;   // float_key(-inf)
 constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster with no quota
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int kSmallRows = 256;               // below: oa_topq_heads path 0 in one launch
-// static LDS of the linear-bin algorithm (13.6 KB measured; held beside the key-prefix one's)
-constexpr long kLinStaticLds = 4L * (14 * 256 + 128);
 constexpr int32_t kRowMarked = -2;              // exp_idx[row][0] of a row left to the key-prefix kernel
 
 enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3, kModeSplit = 4 };
@@ -1174,20 +1172,35 @@ int launch_linear_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStrea
   return launch_linear<44, LB, HEADS>(a, rows, lds, s);
 }
 
+// The one-launch kernel holds both algorithms' static LDS; the key-prefix algorithm's gathered
+// list takes what the unit's LDS leaves beside it, sized from the compiled kernel's own static
+// LDS (hipFuncGetAttributes).  Returns kNotLaunched when the list would be too short to run the
+// key-prefix algorithm in the same workgroup: the caller then takes two launches.
+constexpr int kNotLaunched = -1001;
 template <int PPT, int LB, int PLB>
-int launch_small(const TopqArgs& lin, const TopqArgs& pre, int rows, size_t lds, hipStream_t s) {
-  const hipError_t e = hipFuncSetAttribute((const void*)topq_small_kernel<PPT, LB, PLB>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+int launch_small(const TopqArgs& lin, TopqArgs pre, int rows, size_t lds_lin, hipStream_t s) {
+  const void* fn = (const void*)topq_small_kernel<PPT, LB, PLB>;
+  hipFuncAttributes fa;
+  const hipError_t ea = hipFuncGetAttributes(&fa, fn);
+  if (ea != hipSuccess) return (int)ea;
+  const long room = (long)kLdsLimit - (long)fa.sharedSizeBytes - 4L * pre.hwords - 4L * pre.cpow - 8L * 64;
+  pre.ucap = (int)std::min<long>(kUCapMax, std::max<long>(room, 0) / 8) & ~3;
+  pre.gcap = std::min(pre.hwords / 2, pre.ucap - pre.E);
+  if (pre.gcap < 64) return kNotLaunched;
+  const size_t lds_pre = 8 * (size_t)(pre.ucap + 64) + 4 * (size_t)pre.hwords + 4 * (size_t)pre.cpow;
+  const size_t lds = std::max(lds_lin, lds_pre);
+  if ((long)lds + (long)fa.sharedSizeBytes > kLdsLimit) return kNotLaunched;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL((topq_small_kernel<PPT, LB, PLB>), dim3(rows), dim3(kThreads), lds, s, lin, pre);
   return OA_LAUNCH_STATUS();
 }
 template <int LB, int PLB>
-int launch_small_ppt(const TopqArgs& lin, const TopqArgs& pre, int rows, int Lmax, size_t lds,
+int launch_small_ppt(const TopqArgs& lin, const TopqArgs& pre, int rows, int Lmax, size_t lds_lin,
                      hipStream_t s) {
-  if (Lmax <= kThreads * 8) return launch_small<8, LB, PLB>(lin, pre, rows, lds, s);
-  if (Lmax <= kThreads * 16) return launch_small<16, LB, PLB>(lin, pre, rows, lds, s);
-  return launch_small<36, LB, PLB>(lin, pre, rows, lds, s);
+  if (Lmax <= kThreads * 8) return launch_small<8, LB, PLB>(lin, pre, rows, lds_lin, s);
+  if (Lmax <= kThreads * 16) return launch_small<16, LB, PLB>(lin, pre, rows, lds_lin, s);
+  return launch_small<36, LB, PLB>(lin, pre, rows, lds_lin, s);
 }
 
 }  // namespace
@@ -1228,17 +1241,11 @@ int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool hea
       // one launch: the key-prefix algorithm's gathered list shrinks by the linear-bin
       // algorithm's static LDS, which the same workgroup holds (path 3, every row marked, then
       // runs every row through the key-prefix algorithm in this kernel)
-      TopqArgs ak = a;
-      const long room2 = room - kLinStaticLds;
-      ak.ucap = (int)std::min<long>(kUCapMax, room2 / 8) & ~3;
-      ak.gcap = std::min(ak.hwords / 2, ak.ucap - E);
-      if (ak.gcap >= 64) {
-        const size_t lds_pre = 8 * (size_t)(ak.ucap + 64) + 4 * (size_t)ak.hwords + 4 * (size_t)ak.cpow;
-        const size_t lds_small = std::max(lds_lin, lds_pre);
-        if (al.lb == 7 && ak.lb == 8) return launch_small_ppt<7, 8>(al, ak, rows, Lmax, lds_small, s);
-        if (al.lb == 6 && ak.lb == 7) return launch_small_ppt<6, 7>(al, ak, rows, Lmax, lds_small, s);
-        if (al.lb == 5 && ak.lb == 6) return launch_small_ppt<5, 6>(al, ak, rows, Lmax, lds_small, s);
-      }
+      int st1 = kNotLaunched;
+      if (al.lb == 7 && a.lb == 8) st1 = launch_small_ppt<7, 8>(al, a, rows, Lmax, lds_lin, s);
+      else if (al.lb == 6 && a.lb == 7) st1 = launch_small_ppt<6, 7>(al, a, rows, Lmax, lds_lin, s);
+      else if (al.lb == 5 && a.lb == 6) st1 = launch_small_ppt<5, 6>(al, a, rows, Lmax, lds_lin, s);
+      if (st1 != kNotLaunched) return st1;
     }
     int st;
     if (heads) st = al.lb == 7 ? launch_linear_lb<7, true>(al, rows, Lmax, lds_lin, s)

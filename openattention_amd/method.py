@@ -187,15 +187,20 @@ class OursHIP(Method):
         return self.step(self.st[l], C.K[l].view(-1, self.Lmax, D), C.V[l].view(-1, self.Lmax, D), q,
                          C.n_dev, n, marks)
 
-    def step(self, st, K, V, q, n_dev, n, marks: list | None = None):
-        """The decode stages over an explicit index state and K, V (B * HKV, >= n, D) bf16 rows
-        (any row stride); n on the host (sink/local/top-k counts) and in n_dev on the device."""
-        def mark(name):
-            if marks is not None:
-                ev = torch.cuda.Event(enable_timing=True)
-                ev.record()
-                marks.append((name, ev))
+    def decode_stages(self, l, q, n) -> list:
+        """The stages of decode(l, q, n) as (name, call) pairs in launch order: each call
+        launches that stage alone on the current stream (its inputs are the previous stages'
+        outputs in the method's work buffers)."""
+        return self.stages(self.st[l], C.K[l].view(-1, self.Lmax, D), C.V[l].view(-1, self.Lmax, D), q,
+                           C.n_dev, n)[0]
 
+    def stages(self, st, K, V, q, n_dev, n, counts: tuple | None = None, update_index: bool = True):
+        """The decode stages over an explicit index state and K, V (B * HKV, >= n, D) bf16 rows
+        (any row stride), as (name, call) pairs in launch order, and the step's sel buffer.
+        n on the host fixes the sink / local / top-k counts unless `counts` = (ns, nl, k_top)
+        gives them; n_dev holds n on the device.  update_index: the first stage adds the token
+        at n - 1 to the index (the decode step); otherwise it only projects the queries (a row
+        of a multi-row call over an index that already holds its keys)."""
         qr = q.reshape(self.R, D)
         if not qr.is_contiguous():
             qr = qr.contiguous()
@@ -203,13 +208,67 @@ class OursHIP(Method):
             raise ValueError(f"n={n} outside [1, Lmax={self.Lmax}]: the step writes position n-1")
         if K.shape[0] != self.B * HKV or K.shape[1] < n or V.shape != K.shape:
             raise ValueError(f"K, V must be ({self.B * HKV}, >= n={n}, {D}) with equal shapes")
-        ns, nl, k_top = self.bud.counts(n)
+        ns, nl, k_top = self.bud.counts(n) if counts is None else counts
         if n - ns - nl < k_top:
             raise ValueError(f"n={n} too small for sink {ns} + local {nl} + top-k {k_top}")
         NS = ns + nl + k_top
         sel = self.sel_buffer(NS)
         sc = self.sm_scale
-        if self.groups > 1 and marks is None:
+        out = []
+        if update_index:
+            out.append(("index_prep", lambda: ops.index_prep(K, V, st, n_dev, RMAX, qr, self.limbs, self.fexp)))
+        else:
+            out.append(("qgs_prep", lambda: ops.qgs_prep(qr, st.U, st.scale, self.limbs, self.fexp)))
+        out.append(("qgs_scan", lambda: ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM,
+                                                           n_dev, ns, nl)))
+        if self.R < FUSE_ROWS:
+            # fewer rows than compute units: each row's top-k, gate and fill in one workgroup
+            out.append(("topk_gate_fill", lambda: ops.topk_gate_fill(
+                self.H, self.TM, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp, qr, K, st.asg,
+                sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E, qsk=self.qsk)))
+        else:
+            out.append(("topk_select", lambda: ops.topk_select_heads(
+                self.H, self.TM, sel, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp)))
+            out.append(("gate_fill", lambda: ops.gate_fill(
+                qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E,
+                qsk=self.qsk)))
+        out.append(("topq", lambda: ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, n_dev, st.codes,
+                                                   self.limbs, self.fexp, self.S)))
+        if self.fused:
+            out.append(("residual_flash", lambda: ops.residual_flash(
+                qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk, st.Sv, self.out, sc,
+                qsk=self.qsk)))
+        else:
+            out.append(("residual", lambda: ops.residual(K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t,
+                                                         st.Sk, st.Sv, self.kbar_r, self.vbar_r, self.log_n)))
+            out.append(("flash", lambda: ops.flash_decode(qr, K, V, sel, self.exp_idx, self.kbar_r, self.vbar_r,
+                                                          self.log_n, proxy_per_kv=False, sm_scale=sc,
+                                                          out=self.out)))
+        return out, sel
+
+    def step(self, st, K, V, q, n_dev, n, marks: list | None = None, counts: tuple | None = None,
+             update_index: bool = True):
+        """The decode stages (`stages`) launched in order; returns the output rows
+        (B, HQ, 1, D).  `marks`, when given, receives (stage, event) pairs recorded on the current
+        stream after each stage."""
+        def mark(name):
+            if marks is not None:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record()
+                marks.append((name, ev))
+
+        if self.groups > 1 and marks is None and counts is None and update_index:
+            qr = q.reshape(self.R, D)
+            if not qr.is_contiguous():
+                qr = qr.contiguous()
+            if not 1 <= n <= self.Lmax:
+                raise ValueError(f"n={n} outside [1, Lmax={self.Lmax}]: the step writes position n-1")
+            if K.shape[0] != self.B * HKV or K.shape[1] < n or V.shape != K.shape:
+                raise ValueError(f"K, V must be ({self.B * HKV}, >= n={n}, {D}) with equal shapes")
+            ns, nl, k_top = self.bud.counts(n)
+            if n - ns - nl < k_top:
+                raise ValueError(f"n={n} too small for sink {ns} + local {nl} + top-k {k_top}")
+            sel = self.sel_buffer(ns + nl + k_top)
             main = torch.cuda.current_stream()
             per = self.B // self.groups
             for g, s in enumerate(self.streams):
@@ -221,38 +280,11 @@ class OursHIP(Method):
                 main.wait_stream(s)
             self.last_sel = sel
             return self.out.view(self.B, HQ, 1, D)
+        calls, sel = self.stages(st, K, V, q, n_dev, n, counts=counts, update_index=update_index)
         mark("start")
-        ops.index_prep(K, V, st, n_dev, RMAX, qr, self.limbs, self.fexp)
-        mark("index_prep")
-        ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM, n_dev, ns, nl)
-        mark("qgs_scan")
-        if self.R < FUSE_ROWS:
-            # fewer rows than compute units: each row's top-k, gate and fill in one workgroup
-            ops.topk_gate_fill(self.H, self.TM, n_dev, ns, nl, k_top, st.codes, self.limbs,
-                               self.fexp, qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score,
-                               self.n_t, self.quota, sc, self.E, qsk=self.qsk)
-            mark("topk_gate_fill")
-        else:
-            ops.topk_select_heads(self.H, self.TM, sel, n_dev, ns, nl, k_top, st.codes, self.limbs,
-                                  self.fexp)
-            mark("topk_select")
-            ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t,
-                          self.quota, sc, self.E, qsk=self.qsk)
-            mark("gate_fill")
-        ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, n_dev, st.codes, self.limbs,
-                       self.fexp, self.S)
-        mark("topq")
-        if self.fused:
-            ops.residual_flash(qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk,
-                               st.Sv, self.out, sc, qsk=self.qsk)
-            mark("residual_flash")
-        else:
-            ops.residual(K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk, st.Sv,
-                         self.kbar_r, self.vbar_r, self.log_n)
-            mark("residual")
-            ops.flash_decode(qr, K, V, sel, self.exp_idx, self.kbar_r, self.vbar_r, self.log_n,
-                             proxy_per_kv=False, sm_scale=sc, out=self.out)
-            mark("flash")
+        for name, fn in calls:
+            fn()
+            mark(name)
         self.last_sel = sel
         return self.out.view(self.B, HQ, 1, D)
 

@@ -233,7 +233,11 @@ void oa_ref_qgs_scores(const int8_t* codes, int Lmax, const int32_t* Z, const in
  * SinkMasker (basic_fixed.py:354-363), LocalMasker.update_core (basic_fixed.py:48-67) and
  * TopKMasker._get_topk_indices_from_inactive_positions (fixed/base.py:74-85): the k highest
  * scores among positions [ns, n - nl), ties to the lower position (the deployed rule,
- * graph_runner.py:127-151).  sel row = [0..ns) ++ [n-nl..n) ++ top in rank order. */
+ * graph_runner.py:127-151).  The masker sets the sink and local positions to -inf before its
+ * torch.topk (fixed/base.py:80-81) and the deployed kernel keeps them, and positions past n, as
+ * -inf candidates (graph_runner.py:133,145-151): a row with fewer than k live positions takes the
+ * lowest-position -inf ones after every live one.  sel row = [0..ns) ++ [n-nl..n) ++ top in
+ * rank order. */
 static int cmp_desc_key(const void* a, const void* b) {
   const uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
   return x < y ? 1 : (x > y ? -1 : 0);
@@ -241,20 +245,19 @@ static int cmp_desc_key(const void* a, const void* b) {
 
 void oa_ref_topk_select(const float* S, int ncols, int R, int n, int ns, int nl, int k, int32_t* sel) {
   const int NS = ns + nl + k;
-  if (k < 0 || k > 256) abort();
-  uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)(n > 0 ? n : 1));
+  if (k < 0 || k > 256 || k > ncols) abort();
   for (int r = 0; r < R; ++r) {
     int32_t* out = sel + (long)r * NS;
     for (int i = 0; i < ns; ++i) out[i] = i;
     for (int i = 0; i < nl; ++i) out[ns + i] = n - nl + i;
-    int m = 0;
-    for (int i = ns; i < n - nl; ++i)
-      keys[m++] = ((uint64_t)fkey(S[(long)r * ncols + i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-    /* partial selection: keep the best k with a simple insertion buffer */
+    /* partial selection over every position of the row: keep the best k with an insertion
+     * buffer (distinct keys: the low word is ~position) */
     uint64_t best[256];
     int nb = 0;
-    for (int i = 0; i < m; ++i) {
-      uint64_t x = keys[i];
+    for (int i = 0; i < ncols; ++i) {
+      const int live = i >= ns && i < n - nl;
+      const uint64_t x = ((uint64_t)fkey(live ? S[(long)r * ncols + i] : -INFINITY) << 32) |
+                         (uint64_t)(0xffffffffu - (uint32_t)i);
       if (nb < k) {
         int p = nb++;
         while (p > 0 && best[p - 1] < x) { best[p] = best[p - 1]; --p; }
@@ -267,7 +270,6 @@ void oa_ref_topk_select(const float* S, int ncols, int R, int n, int ns, int nl,
     }
     for (int i = 0; i < k; ++i) out[ns + nl + i] = (int32_t)(0xffffffffu - (uint32_t)(best[i] & 0xffffffffu));
   }
-  free(keys);
 }
 
 /* ------------------------------------------------------------------ ErrorGate (wl1)

@@ -562,6 +562,54 @@ def test_topk_rows_with_ties_large_k(n, k):
     assert np.array_equal(after, marked)
 
 
+@pytest.mark.parametrize("Lmax,n,ns,nl,k", [
+    (140000, 12, 3, 3, 20),      # radix kernel (k > 16, 2188 tiles): 6 live positions for 20
+    (140000, 500, 3, 3, 0),      # radix kernel at k = 0: sink and local only
+    (140000, 40, 3, 3, 40),      # radix kernel: 34 live for 40
+    (4096, 10, 3, 3, 9),         # register kernel: 4 live for 9
+    (4096, 300, 3, 3, 0),        # register kernel at k = 0
+])
+def test_topk_heads_underfull_rows(Lmax, n, ns, nl, k):
+    """The scan over heads, then top-k over heads, on rows with fewer live positions than k_top
+    (and k_top = 0): every live position is selected first, then the lowest dead ones (sink,
+    local, unwritten) as -inf candidates; sel equals the restatement's, every selected position
+    lies below ntiles * 64 and its head is marked, and nothing else in the head rows changes."""
+    print(f"[case] topk heads underfull Lmax={Lmax} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(Lmax + n + k)
+    BH = 2
+    R = BH * G
+    codes = np.zeros((BH, Lmax, 32), np.int8)
+    codes[:, :n] = rng.integers(-127, 128, (BH, n, 32), dtype=np.int8)
+    U = rng.normal(size=(BH, D, 32)).astype(np.float32)
+    scale = rng.uniform(0.5, 2.0, (BH, 32)).astype(np.float32)
+    q16 = f32_to_bf16(rng.normal(size=(R, D)).astype(np.float32))
+    _, fexp_ref, Z = O.qgs_prep(q16, U, scale, G)
+    S = O.qgs_scores(codes, Z, fexp_ref, G, n, ns, nl)
+    want = O.topk_select(S, n, ns, nl, k)
+    ntiles = -(-Lmax // 64)
+    codes_t = torch.from_numpy(codes).to(DEV)
+    limbs = torch.zeros(BH, 16, 32, device=DEV, dtype=torch.int8)
+    fexp = torch.zeros(R, device=DEV, dtype=torch.int32)
+    ops.qgs_prep(np_bf16(q16, DEV), _f32(U), _f32(scale), limbs, fexp)
+    H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
+    TM = torch.empty(R, ntiles, device=DEV, dtype=torch.float32)
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    ops.qgs_scan_heads(codes_t, limbs, fexp, H, TM, n_dev, ns, nl)
+    torch.cuda.synchronize()
+    before = H.cpu().numpy().copy()
+    sel = torch.full((R, ns + nl + k), -7, device=DEV, dtype=torch.int32)
+    ops.topk_select_heads(H, TM, sel, n_dev, ns, nl, k, codes_t, limbs, fexp)
+    torch.cuda.synchronize()
+    got = sel.cpu().numpy()
+    assert np.array_equal(got, want), f"rows {np.nonzero((got != want).any(1))[0]} differ"
+    assert got.min() >= 0 and got.max() < ntiles * 64
+    after = H.cpu().numpy()
+    marked = before.copy()
+    for r in range(R):
+        marked[r, want[r, ns + nl:]] = np.int16(0x007F)
+    assert np.array_equal(after, marked)
+
+
 @pytest.mark.parametrize("N,C,k_top", [(4096, 64, 16), (8192, 100, 12), (16384, 192, 9),
                                          (32768, 256, 16)])
 def test_small_batch_fused_launches(N, C, k_top):

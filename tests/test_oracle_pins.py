@@ -150,6 +150,29 @@ def test_topk_brute_force_and_ties():
         assert list(sel[r, ns + nl:]) == order[:k]
 
 
+def test_topk_underfull_rows_take_lowest_dead_positions():
+    """Fewer live positions than k: the masker's topk over scores with sink and local at -inf
+    (fixed/base.py:80-84) and the deployed kernel's -inf candidates past n rank every live
+    position first, then the dead ones by position.  The brute force here sorts the whole row
+    with the dead positions at -inf; k = 0 leaves sink and local only."""
+    ncols = 256
+    for n, ns, nl, k in ((10, 2, 3, 9), (5, 1, 1, 9), (8, 3, 5, 4), (70, 64, 4, 6), (40, 3, 3, 0)):
+        S = RNG.normal(size=(3, ncols)).astype(np.float32)
+        S[1, ns:n - nl] = 0.5                      # tied live positions
+        sel = O.topk_select(S, n, ns, nl, k)
+        assert sel.shape == (3, ns + nl + k)
+        for r in range(3):
+            full = np.where((np.arange(ncols) >= ns) & (np.arange(ncols) < n - nl), S[r], -np.inf)
+            order = sorted(range(ncols), key=lambda i: (-full[i], i))
+            assert list(sel[r, ns + nl:]) == order[:k], (n, ns, nl, k, r)
+            live = max(0, n - nl - ns)
+            # every live position is taken before any dead one, and the dead ones are the lowest
+            assert set(sel[r, ns + nl:ns + nl + min(k, live)]) <= set(range(ns, n - nl))
+            if k > live:
+                dead = [i for i in range(ncols) if not ns <= i < n - nl][:k - live]
+                assert list(sel[r, ns + nl + live:]) == dead
+
+
 # ------------------------------------------------------------------ ErrorGate
 def _gate_ref_fp64(q, K, asg, sel, Sk, Sk2, nb, G):
     R, C = nb.shape
