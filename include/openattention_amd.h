@@ -28,11 +28,11 @@
 extern "C" {
 #endif
 
-#define OA_ABI_VERSION 2
+#define OA_ABI_VERSION 3
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
-/* ABI version of this header (2). */
+/* ABI version of this header (3). */
 int oa_abi_version(void);
 
 /* Text for a status returned by any entry point. */
@@ -97,6 +97,21 @@ int oa_index_update(const void* K, const void* V, long kv_stride_b, long kv_stri
                     int rank_c, const float* cent, int C, int32_t* asg, long asg_stride,
                     uint8_t* asg8, long asg8_stride, float* nb, float* Sk, float* Sk2, float* Sv,
                     int32_t* reclist, int32_t* reccnt, int rmax, const int* n_dev, void* stream);
+
+/*
+ * The token at position n-1 leaves the cluster statistics of every query row: n_c -= 1,
+ * Sk_c -= k, Sk2_c -= k*k, Sv_c -= v in fp32, c = asg[row][n-1] (the index update's statistics
+ * step, undone; codes, cluster ids and lists are untouched).  A multi-row call (the question
+ * chunk) takes its keys back one at a time from the last, so that its causal row i, which
+ * attends the keys before n_i = K - Q + i + 1, sees the statistics of exactly those keys: the
+ * reference's estimator keeps only positions with raw > NEG in each row's tail
+ * (multibin.py:2210-2218, the causal mask added to the logits).  No kernel of the reference's
+ * deployed path does this: its question chunk runs dense (graph_runner.py:472-475).
+ *   asg (rows, asg_stride) int32; nb (rows, C), Sk, Sk2, Sv (rows, C, 128) fp32; C <= 256.
+ */
+int oa_index_downdate(const void* K, const void* V, long kv_stride_b, long kv_stride_s, int rows,
+                      int kv_rows, int head_dim, const int32_t* asg, long asg_stride, float* nb,
+                      float* Sk, float* Sk2, float* Sv, int C, const int* n_dev, void* stream);
 
 /*
  * QGS query projection zq = (q U) * scale and its exact fixed-point form (exponent fexp per

@@ -180,6 +180,40 @@ __global__ void __launch_bounds__(192) index_prep_kernel(IdxArgs a, PrepArgs p) 
     index_codes_row(a, r, threadIdx.x - 128);
 }
 
+// The token at position n-1 leaves every query row's cluster statistics: the inverse of the
+// statistics part of the index update, in the same fp32 terms (n_c -= 1, Sk_c -= k,
+// Sk2_c -= k*k, Sv_c -= v; c = asg[row][n-1]).  Codes, cluster ids and lists stay as they are:
+// every decode stage reads positions below n only.  A multi-row call takes its later keys back
+// this way, so that each causal row sees the statistics of the keys before it.
+struct DownArgs {
+  const uint16_t* K; const uint16_t* V; long kv_sb; long kv_ss;
+  const int32_t* asg; long asg_stride;
+  float* nb; float* Sk; float* Sk2; float* Sv;
+  const int* n_dev; int C; int G;
+};
+
+__global__ void __launch_bounds__(64) index_downdate_kernel(DownArgs a) {
+  const int r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int kvr = r / a.G;
+  const int pos = *a.n_dev - 1;
+  if (pos < 0) return;                                        // uniform
+  const int c = a.asg[(long)r * a.asg_stride + pos];
+  if (c < 0 || c >= a.C) return;                              // uniform
+  const uint16_t* kp = a.K + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
+  const uint16_t* vp = a.V + (long)kvr * a.kv_sb + (long)pos * a.kv_ss;
+  const float k_lo = oa::bf16_to_f32(kp[lane]), k_hi = oa::bf16_to_f32(kp[lane + 64]);
+  const float v_lo = oa::bf16_to_f32(vp[lane]), v_hi = oa::bf16_to_f32(vp[lane + 64]);
+  const long sb = ((long)r * a.C + c) * OA_D;
+  a.Sk[sb + lane] -= k_lo;
+  a.Sk[sb + lane + 64] -= k_hi;
+  a.Sk2[sb + lane] -= k_lo * k_lo;
+  a.Sk2[sb + lane + 64] -= k_hi * k_hi;
+  a.Sv[sb + lane] -= v_lo;
+  a.Sv[sb + lane + 64] -= v_hi;
+  if (lane == 0) a.nb[(long)r * a.C + c] -= 1.0f;
+}
+
 }  // namespace
 
 extern "C" int oa_index_update(const void* K, const void* V, long kv_stride_b, long kv_stride_s,
@@ -226,5 +260,20 @@ extern "C" int oa_index_prep(const void* K, const void* V, long kv_stride_b, lon
   PrepArgs p;
   p.q = (const uint16_t*)q; p.q_stride = q_stride; p.limbs = limbs; p.fexp = fexp;
   hipLaunchKernelGGL(index_prep_kernel, dim3(rows), dim3(192), 0, (hipStream_t)stream, a, p);
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_index_downdate(const void* K, const void* V, long kv_stride_b, long kv_stride_s,
+                                 int rows, int kv_rows, int head_dim, const int32_t* asg,
+                                 long asg_stride, float* nb, float* Sk, float* Sk2, float* Sv, int C,
+                                 const int* n_dev, void* stream) {
+  if (head_dim != OA_D || kv_rows <= 0 || rows % kv_rows != 0 || C <= 0 || C > 256 || !K || !V ||
+      !asg || !nb || !Sk || !Sk2 || !Sv || !n_dev)
+    return OA_EINVAL;
+  DownArgs a;
+  a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.kv_sb = kv_stride_b; a.kv_ss = kv_stride_s;
+  a.asg = asg; a.asg_stride = asg_stride; a.nb = nb; a.Sk = Sk; a.Sk2 = Sk2; a.Sv = Sv;
+  a.n_dev = n_dev; a.C = C; a.G = rows / kv_rows;
+  hipLaunchKernelGGL(index_downdate_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, a);
   return OA_LAUNCH_STATUS();
 }

@@ -29,6 +29,7 @@ SIGNATURES = {
                                 L, I, I, I, I, F, I, P],
     "oa_index_update": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
                         P, I, P, P],
+    "oa_index_downdate": [P, P, L, L, I, I, I, P, L, P, P, P, P, I, P, P],
     "oa_qgs_prep": [P, L, P, P, I, I, I, I, P, P, P, P],
     "oa_index_prep": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
                       P, I, P, P, L, P, P, P],
@@ -57,7 +58,7 @@ SIGNATURES = {
 
 # must equal oa_abi_version() of the loaded library (OA_ABI_VERSION in the header): a library
 # built from sources with other argument lists would be handed wrong pointers
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _LIB = None
 

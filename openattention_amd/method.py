@@ -288,6 +288,43 @@ class OursHIP(Method):
         self.last_sel = sel
         return self.out.view(self.B, HQ, 1, D)
 
+    def rows_step(self, st, K, V, q, n_dev, n_keys: int, out: torch.Tensor,
+                  record: list | None = None) -> torch.Tensor:
+        """A multi-row call of the estimator over an index that already holds all n_keys keys
+        (UTAMultiBinAttention.custom_attention with Q rows, multibin.py:2875-2970): row i of
+        q (B, HQ, Q, D) sits at position n_keys - Q + i and, under the causal mask, attends the
+        n_i = n_keys - Q + i + 1 keys before it (multibin.py:2210-2218 keeps raw > NEG only);
+        the sink / local / top-k sizes come from the call's key count, as the maskers size them
+        from seq_len_keys (maskers/base.py:152-158), and the local window ends at the row.
+        The rows run from the last to the first; after row i the key at n_i - 1 leaves the
+        cluster statistics (ops.index_downdate), so row i - 1 sees those of [0, n_{i-1}); the
+        statistics are restored afterwards and n_dev is left at n_keys.  Writes and returns out
+        (B, HQ, Q, D).  record, when a list, receives (i, sel, quota, exp_idx) copies per row."""
+        B, H, Q, _ = q.shape
+        if H != HQ or B != self.B or out.shape != q.shape:
+            raise ValueError(f"q and out must be ({self.B}, {HQ}, Q, {D})")
+        counts = self.bud.counts(n_keys)
+        ns, nl, k_top = counts
+        if n_keys - Q + 1 - ns - nl < k_top:
+            raise ValueError(f"{n_keys} keys leave the first of {Q} causal rows too few positions for "
+                             f"sink {ns} + local {nl} + top-k {k_top}")
+        snap = (st.nb.clone(), st.Sk.clone(), st.Sk2.clone(), st.Sv.clone())
+        try:
+            for i in range(Q - 1, -1, -1):
+                n_i = n_keys - Q + i + 1
+                n_dev.fill_(n_i)
+                o = self.step(st, K, V, q[:, :, i], n_dev, n_i, counts=counts, update_index=False)
+                out[:, :, i] = o.view(B, H, D)
+                if record is not None:
+                    record.append((i, self.last_sel.clone(), self.quota.clone(), self.exp_idx.clone()))
+                if i > 0:
+                    ops.index_downdate(K, V, st, n_dev)
+        finally:
+            for t, s in zip((st.nb, st.Sk, st.Sk2, st.Sv), snap):
+                t.copy_(s)
+            n_dev.fill_(n_keys)
+        return out
+
     def _chain(self, st, K, V, qr, sel, rs: slice, ks: slice, ns: int, nl: int, k_top: int, n_dev):
         """The decode stages on query-head rows `rs` and their KV rows `ks` (whole sequences)."""
         sub = types.SimpleNamespace(

@@ -14,19 +14,30 @@ multibin.py:2098-2120):
   * a call with Q >= 8 rows is the request's question chunk: the layer's index is (re)built over
     all K keys, the question rows give the query moment, and the metric is rotated to position
     K (build_rows: QGS codes, QGC clusters, cluster sums);
-  * a call with Q == 1 is a decode step at n = K: the index is extended with the keys appended
-    since the last call, and the sparse step (QGS scan, top-k, ErrorGate, water-fill, top-q,
-    residual proxies, fused softmax) gives the output;
+  * a call with fewer rows extends the index with the keys appended since the last call
+    (ops.index_update, the deployed step's index update);
+  * every row then gets the estimator's output (multibin.py:2195-2747 with the masks of
+    basic_fixed.py:180-214, 384-418 and static_top_k.py:221-262): row i sits at position
+    K - Q + i and, under the causal mask, attends the n_i = K - Q + i + 1 keys before it --
+    sink, the local window ending at the row, top-k of the QGS scores over the rest, ErrorGate
+    and water-filling over its tail's clusters, within-cluster top-q, residual proxies and the
+    fused softmax.  The sink / local / top-k sizes come from K, as the maskers size them from
+    seq_len_keys (maskers/base.py:152-158).  A one-row call is the deployed decode step
+    (OursHIP.step); a multi-row call runs its rows through OursHIP.rows_step;
+  * when a masker would return the full mask (K <= local + Q or K <= top-k,
+    basic_fixed.py:208-214, static_top_k.py:233-234) every row gets dense causal attention,
+    as the reference returns get_true_attention_output (multibin.py:2916-2920): this library's
+    dense decode kernel, one launch per row at n_i;
   * a decode-sized call with no index for the layer -> ValueError, as the reference's profile
     cache raises.
 
-Where this surface differs from the accuracy path, and why:
-  * the question chunk's own rows get dense causal attention (the deployed path's prefill
-    branch, graph_runner.py:472-475): this build implements the sparse estimator for the
-    decode step only;
-  * keys and values must be bfloat16 (the kernels read bf16 rows); Q between 2 and 7 and
-    additive masks with nonzero entries are refused (the kernels decode one row per head and
-    take no padding mask).
+What the surface accepts, and why:
+  * keys, values and queries in bfloat16 (the kernels read bf16 rows);
+  * attention_mask None for a one-row call, or HF's additive causal mask (0 where a row may
+    attend, <= -3e4 -- the dtype's minimum or -inf -- where it may not; any broadcastable
+    (B|1, H|1, Q, >=K) layout).  A
+    multi-row call needs the causal mask: without it the reference's rows would attend later
+    keys as well.  Other masks (padding) raise NotImplementedError.
 The index state lives in sparse_meta_data["oa_hip"][layer_idx] (one request's cache, as the
 reference keeps its own caches in sparse_meta_data).
 """
@@ -38,24 +49,45 @@ import torch
 
 from openattention_amd import ops
 from openattention_amd.budget import CTX_LEN
-from openattention_amd.method import D, G, HKV, HQ, RMAX, OursHIP, prefill_attention
+from openattention_amd.method import D, G, HKV, HQ, RMAX, OursHIP
 from openattention_amd.prefill import build_rows
 
 QUESTION_ROWS = 8       # calls with at least this many query rows build the index
+MASKED = -3e4           # an additive mask entry at or below this removes the position: the
+                        # estimator keeps raw = q.k * scale + mask > -1e4 (multibin.py:2213-2218)
+
+
+def causal_mask_ok(attention_mask, Q: int, K: int) -> bool:
+    """True when attention_mask[..., :K] is the additive causal mask of Q rows ending at K - 1
+    (row i may attend j <= K - Q + i: entry 0; the rest <= MASKED, as HF's minimum of bf16, fp16
+    or fp32 and -inf are), or None for one row."""
+    if attention_mask is None:
+        return Q == 1
+    m = attention_mask[..., :K]
+    if m.dim() < 2 or m.shape[-2] != Q or m.shape[-1] != K:
+        return False
+    i = torch.arange(Q, device=m.device).view(Q, 1)
+    j = torch.arange(K, device=m.device).view(1, K)
+    allowed = j <= (K - Q) + i
+    mf = m.float()
+    return bool(torch.where(allowed, mf == 0, mf <= MASKED).all())
 
 
 class UTAMultiBinHIP:
     """OpenAttention's estimator at read fraction rho, deployed split (C, E), on the gfx950
     kernels; `static` is the static query metric dict (M (L, HQ, D, D), inv_freq, attention_
     scaling).  `headroom` tokens can be decoded after each build before the layer's state is
-    full (the reference rebuilds its profile past 4096 new keys, multibin.py:2103)."""
+    full (the reference rebuilds its profile past 4096 new keys, multibin.py:2103).  record_rows,
+    when set, keeps each row's (sel, quota, exp_idx) of the last call per layer in
+    sparse_meta_data["oa_hip"][layer]["rows"] (inspection and tests)."""
 
     def __init__(self, rho: float = 0.01, static: dict | None = None, ctx_len: int = CTX_LEN,
-                 rule: str = "multibin", headroom: int = 4096, out_dtype=torch.bfloat16):
+                 rule: str = "multibin", headroom: int = 4096, out_dtype=torch.bfloat16,
+                 record_rows: bool = False):
         if static is None:
             raise ValueError("UTAMultiBinHIP needs the static query metric (M, inv_freq, attention_scaling)")
         self.rho, self.static, self.ctx_len, self.rule = rho, static, ctx_len, rule
-        self.headroom, self.out_dtype = headroom, out_dtype
+        self.headroom, self.out_dtype, self.record_rows = headroom, out_dtype, record_rows
 
     # ------------------------------------------------------------------ surface
     def custom_attention(self, module, queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
@@ -75,22 +107,35 @@ class UTAMultiBinHIP:
             raise ValueError("the HIP path reads bfloat16 queries, keys and values")
         if keys.device.type != "cuda":
             raise RuntimeError("the HIP path needs the tensors on a HIP device")
-        if attention_mask is not None and bool((attention_mask[..., :keys.shape[2]] != 0).any()):
-            raise NotImplementedError("additive masks with nonzero entries (padding) are not supported")
+        Kn = keys.shape[2]
+        if Q < 1 or Q > Kn:
+            raise ValueError(f"{Q} query rows over {Kn} keys")
+        if not causal_mask_ok(attention_mask, Q, Kn):
+            if attention_mask is None:
+                raise NotImplementedError(f"a {Q}-row call needs the additive causal mask: without it the "
+                                          "reference's rows would attend later keys too")
+            raise NotImplementedError("only the additive causal mask (0 / <= -3e4) is supported, not padding")
         cache = meta.setdefault("oa_hip", {})
+        layer = int(layer_idx)
         if Q >= QUESTION_ROWS:
-            out = self._question_chunk(cache, int(layer_idx), queries, keys, values, scaling)
-        elif Q == 1:
-            out = self._decode(cache, int(layer_idx), queries, keys, values, scaling)
+            ent = self._build(cache, layer, queries, keys, values)
         else:
-            raise ValueError(f"{Q} query rows: this path takes a question chunk (>= {QUESTION_ROWS} "
-                             "rows) or one decode row per call")
+            ent = cache.get(layer)
+            if ent is None:
+                raise ValueError(f"a decode-sized call with no index for layer {layer}: the request's "
+                                 f"question chunk (>= {QUESTION_ROWS} rows) must come first")
+            if queries.shape[0] != ent["m"].B:
+                raise ValueError(f"batch {queries.shape[0]} differs from the build's {ent['m'].B}")
+            if Kn < ent["n"] or Kn > ent["m"].Lmax:
+                raise ValueError(f"{Kn} keys after an index of {ent['n']} (capacity {ent['m'].Lmax}): "
+                                 "rebuild with a question chunk")
+        out = self._rows(ent, queries, keys, values, scaling)
         return out.transpose(1, 2).contiguous(), None
 
     # ------------------------------------------------------------------ phases
     @torch.no_grad()
-    def _question_chunk(self, cache: dict, layer: int, queries, keys, values, scaling):
-        B, _, Q, _ = queries.shape
+    def _build(self, cache: dict, layer: int, queries, keys, values) -> dict:
+        B = queries.shape[0]
         T = keys.shape[2]
         dev = keys.device
         ent = cache.get(layer)
@@ -100,40 +145,52 @@ class UTAMultiBinHIP:
                         ctx_len=self.ctx_len, rule=self.rule, out_dtype=self.out_dtype)
             ent = {"m": m, "n_dev": torch.zeros(1, device=dev, dtype=torch.int32)}
             cache[layer] = ent
-        m = ent["m"]
-        build_rows(m.st[0], keys.contiguous(), values.contiguous(), queries, T,
+        build_rows(ent["m"].st[0], keys.contiguous(), values.contiguous(), queries, T,
                    self.static["M"][layer], self.static["inv_freq"],
                    float(self.static.get("attention_scaling", 1.0)), layer, G)
         ent["n"] = T
-        out = torch.empty_like(queries)
-        for b in range(B):
-            out[b:b + 1] = prefill_attention(queries[b:b + 1], keys[b:b + 1], values[b:b + 1], scaling)
-        return out
+        return ent
 
     @torch.no_grad()
-    def _decode(self, cache: dict, layer: int, queries, keys, values, scaling):
-        ent = cache.get(layer)
-        n = keys.shape[2]
-        if ent is None:
-            raise ValueError(f"a decode-sized call with no index for layer {layer}: the request's "
-                             f"question chunk (>= {QUESTION_ROWS} rows) must come first")
+    def _rows(self, ent: dict, queries, keys, values, scaling) -> torch.Tensor:
+        """Every query row's output (B, HQ, Q, D) over the layer's index (see the module text)."""
         m = ent["m"]
-        if queries.shape[0] != m.B:
-            raise ValueError(f"batch {queries.shape[0]} differs from the build's {m.B}")
-        if n <= ent["n"] or n > m.Lmax:
-            raise ValueError(f"{n} keys after an index of {ent['n']} (capacity {m.Lmax}): rebuild with a "
-                             "question chunk")
-        K = keys.reshape(m.B * HKV, n, D)
-        V = values.reshape(m.B * HKV, n, D)
+        B, _, Q, _ = queries.shape
+        n = keys.shape[2]
+        K = keys.reshape(B * HKV, n, D)
+        V = values.reshape(B * HKV, n, D)
         if not (K.is_contiguous() and V.is_contiguous()):
             K, V = K.contiguous(), V.contiguous()
         st = m.st[0]
         n_dev = ent["n_dev"]
-        for pos in range(ent["n"], n - 1):      # keys appended without a decode call
+        m.sm_scale = float(scaling)
+        ns, nl, k_top = m.bud.counts(n)
+        full = n <= nl + Q or n <= k_top
+        step_row = Q == 1 and not full and n > ent["n"]
+        # keys appended since the last call join the index (the deployed decode step adds the
+        # last one itself)
+        for pos in range(ent["n"], n - 1 if step_row else n):
             n_dev.fill_(pos + 1)
             ops.index_update(K, V, st, n_dev, RMAX)
-        n_dev.fill_(n)
-        m.sm_scale = float(scaling)
-        out = m.step(st, K, V, queries, n_dev, n)
         ent["n"] = n
-        return out.view(m.B, HQ, 1, D)
+        record = [] if self.record_rows else None
+        if full:
+            out = torch.empty(B, HQ, Q, D, device=queries.device, dtype=m.out.dtype)
+            q = queries.to(torch.bfloat16)
+            for i in range(Q):
+                n_dev.fill_(n - Q + i + 1)
+                o = ops.dense_decode(q[:, :, i].reshape(B * HQ, D).contiguous(), K, V, n_dev,
+                                     sm_scale=float(scaling))
+                out[:, :, i] = o.view(B, HQ, D)
+            n_dev.fill_(n)
+        elif step_row:
+            n_dev.fill_(n)
+            out = m.step(st, K, V, queries, n_dev, n).view(B, HQ, 1, D).clone()
+            if record is not None:
+                record.append((0, m.last_sel.clone(), m.quota.clone(), m.exp_idx.clone()))
+        else:
+            out = torch.empty(B, HQ, Q, D, device=queries.device, dtype=m.out.dtype)
+            m.rows_step(st, K, V, queries, n_dev, n, out, record=record)
+        if record is not None:
+            ent["rows"] = sorted(record, key=lambda t: t[0])
+        return out

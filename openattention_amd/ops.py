@@ -192,6 +192,25 @@ def index_update(K, V, st, n_dev: torch.Tensor, rmax: int) -> None:
              _ptr(st.reccnt), rmax, _ptr(n_dev), _stream(dev))
 
 
+def index_downdate(K, V, st, n_dev: torch.Tensor) -> None:
+    """The token at n-1 leaves the cluster statistics (nb, Sk, Sk2, Sv) of every query row: the
+    statistics step of index_update undone, so that a causal row ending before it sees the
+    statistics of the keys it attends (multibin.py:2210-2218)."""
+    dev = _dev(K, V, n_dev)
+    BH, Lmax, D = K.shape
+    R = st.nb.shape[0]
+    C = st.nb.shape[1]
+    _chk(K, "K", torch.bfloat16, (BH, Lmax, HEAD_DIM))
+    _need(V.shape == K.shape and V.stride() == K.stride() and V.dtype == K.dtype, "V must match K")
+    _chk(st.asg, "asg", torch.int32, (R, -Lmax))
+    _chk(st.nb, "nb", torch.float32, (R, C), contiguous=True)
+    _stats(R, C, (st.Sk, "Sk"), (st.Sk2, "Sk2"), (st.Sv, "Sv"))
+    _chk(n_dev, "n_dev", torch.int32)
+    lib.call("oa_index_downdate", _ptr(K), _ptr(V), K.stride(0), K.stride(1), R, BH, D, _ptr(st.asg),
+             st.asg.stride(0), _ptr(st.nb), _ptr(st.Sk), _ptr(st.Sk2), _ptr(st.Sv), C, _ptr(n_dev),
+             _stream(dev))
+
+
 def index_prep(K, V, st, n_dev: torch.Tensor, rmax: int, q, limbs, fexp) -> None:
     """index_update and qgs_prep in one launch (same results as the two calls)."""
     dev = _dev(K, V, n_dev, q, limbs, fexp)

@@ -604,6 +604,30 @@ void oa_ref_index_update(const uint16_t* K, const uint16_t* V, int Lmax, int pos
   }
 }
 
+/* Removal of the token at pos from every query row's cluster statistics, in the fp32 terms of
+ * oa_ref_index_update's statistics step (n_c -= 1, Sk_c -= k, Sk2_c -= k*k, Sv_c -= v with
+ * c = asg[r][pos]).  A multi-row call's causal row i keeps only the keys before
+ * n_i = K - Q + i + 1 in its tail (valid = raw > NEG with the causal mask added,
+ * multibin.py:2210-2218); the statistics of [0, n_i) are those of [0, K) with the keys
+ * K-1, ..., n_i taken back in that order. */
+void oa_ref_index_downdate(const uint16_t* K, const uint16_t* V, int Lmax, int pos, int R, int G,
+                           int C, const int32_t* asg, float* nb, float* Sk, float* Sk2, float* Sv) {
+  for (int r = 0; r < R; ++r) {
+    const int kvr = r / G;
+    const int c = asg[(long)r * Lmax + pos];
+    if (c < 0 || c >= C) continue;
+    const long sb = ((long)r * C + c) * D;
+    for (int d = 0; d < D; ++d) {
+      const float k = bf2f(K[((long)kvr * Lmax + pos) * D + d]);
+      const float v = bf2f(V[((long)kvr * Lmax + pos) * D + d]);
+      Sk[sb + d] -= k;
+      Sk2[sb + d] -= k * k;
+      Sv[sb + d] -= v;
+    }
+    nb[(long)r * C + c] -= 1.0f;
+  }
+}
+
 /* ==================================================================================== prefill
  * Index build of one request (KV rows h < HKV of K, V: (HKV, Lmax, 128) bf16; query rows
  * r < R = G * HKV).  Orders as fixed by the device build (openattention_amd/csrc/oa_build.hip).

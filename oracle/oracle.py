@@ -201,6 +201,19 @@ def index_update(st: dict, pos: int, G: int, rmax: int) -> None:
                                _p(st["reclist"]), _p(st["reccnt"]), ct.c_int(rmax))
 
 
+def index_downdate(st: dict, pos: int, G: int) -> None:
+    """The token at pos leaves every query row's cluster statistics (multibin.py:2210-2218 tail
+    validity, in the index update's fp32 terms); mutates st['nb','Sk','Sk2','Sv']"""
+    for k in ("nb", "Sk", "Sk2", "Sv"):
+        assert st[k].flags["C_CONTIGUOUS"] and st[k].dtype == np.float32
+    K, V = _c(st["K"], np.uint16), _c(st["V"], np.uint16)
+    R, C = st["nb"].shape
+    asg = _c(st["asg"], np.int32)
+    assert asg.shape[1] == K.shape[1]
+    _lib().oa_ref_index_downdate(_p(K), _p(V), ct.c_int(K.shape[1]), ct.c_int(pos), ct.c_int(R), ct.c_int(G),
+                                 ct.c_int(C), _p(asg), _p(st["nb"]), _p(st["Sk"]), _p(st["Sk2"]), _p(st["Sv"]))
+
+
 # ------------------------------------------------------------------ prefill index build
 def qgs_codes(K_bf16: np.ndarray, T: int, U: np.ndarray):
     """ours_fastbuild.py:256-261, static_top_k.py:174-181.  K (HKV, Lmax, 128) bf16 bits;
@@ -421,3 +434,32 @@ def decode_step(st: dict, q_bf16: np.ndarray, n: int, ns: int, nl: int, k: int, 
     out = flash(q_bf16, st["K"], st["V"], sel, exp_idx, kb, vb, ln, G, sm)
     return dict(zq=zq, fexp=fexp, Z=Z, S=S, sel=sel, score=score, n_t=n_t, quota=quota,
                 exp_idx=exp_idx, kbar_r=kb, vbar_r=vb, log_n=ln, out=out)
+
+
+def rows_step(st: dict, q_rows: np.ndarray, n_keys: int, ns: int, nl: int, k: int, E: int, G: int,
+              sm: float, sm2: float, rows=None) -> dict:
+    """A multi-row call of the estimator (UTAMultiBinAttention.custom_attention with Q query rows,
+    multibin.py:2875-2970 over the masks of basic_fixed.py:180-214, 384-418 and
+    static_top_k.py:221-262): query row i (q_rows[i], (R, 128) bf16 bits) sits at position
+    n_keys - Q + i and, with the causal mask, attends the n_i = n_keys - Q + i + 1 keys before it:
+    sink, local window [n_i - nl, n_i) and top-k over [ns, n_i - nl), sizes fixed by the call's
+    key count (ns, nl, k); its tail, bins and statistics hold keys below n_i only.  The index in
+    st holds all n_keys keys; row i's statistics are those of [0, n_keys) with the keys
+    n_keys - 1, ..., n_i taken back (index_downdate), and the rows run from the last to the
+    first.  st is not modified.  Returns {i: decode_step results of row i} for the rows asked
+    (all by default)."""
+    Q = q_rows.shape[0]
+    want = set(range(Q)) if rows is None else set(rows)
+    s = dict(st)
+    for f in ("nb", "Sk", "Sk2", "Sv"):
+        s[f] = st[f].copy()
+    res = {}
+    for i in range(Q - 1, -1, -1):
+        n_i = n_keys - Q + i + 1
+        if i in want:
+            res[i] = decode_step(s, q_rows[i], n_i, ns, nl, k, E, G, sm, sm2, update_index=False)
+        if i > 0:
+            index_downdate(s, n_i - 1, G)
+        if not any(j < i for j in want):
+            break
+    return res

@@ -173,3 +173,31 @@ def test_wrapper_layout_checks_reject_wrong_dtype_shape_and_strides():
         ops._chk(t.transpose(1, 2), "t", torch.float32)
     with pytest.raises(ValueError, match="contiguous"):
         ops._stats(4, 4, (t[:, :4], "Sk"))
+
+
+def test_causal_mask_check_accepts_hf_causal_masks_only():
+    """The accuracy-path surface accepts HF's additive causal mask (0 where row i may attend
+    j <= K - Q + i, the dtype's minimum or -inf elsewhere; any broadcastable leading dims, longer
+    masks sliced to K as multibin.py:2213 does) and None for one row; padding masks are refused."""
+    from openattention_amd.multibin import causal_mask_ok
+
+    def causal(Q, K, fill, dtype=torch.bfloat16, lead=(1, 1), extra=0):
+        i = torch.arange(Q).view(Q, 1)
+        j = torch.arange(K + extra).view(1, K + extra)
+        m = torch.zeros(*lead, Q, K + extra, dtype=dtype)
+        return m.masked_fill_(j > (K - Q) + i, fill)
+
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        assert causal_mask_ok(causal(5, 40, torch.finfo(dtype).min, dtype), 5, 40)
+    assert causal_mask_ok(causal(64, 300, float("-inf"), torch.float32, lead=(2, 32)), 64, 300)
+    assert causal_mask_ok(causal(3, 50, float("-inf"), torch.float32, extra=7), 3, 50)
+    assert causal_mask_ok(None, 1, 50) and not causal_mask_ok(None, 2, 50)
+    assert causal_mask_ok(torch.zeros(1, 1, 1, 50), 1, 50)
+    bad = causal(5, 40, torch.finfo(torch.float32).min, torch.float32)
+    bad[..., 2, 3] = torch.finfo(torch.float32).min              # a padded position
+    assert not causal_mask_ok(bad, 5, 40)
+    off = causal(5, 40, torch.finfo(torch.float32).min, torch.float32)
+    off[..., 4, 39] = -1.0                                        # not a removal, not zero
+    assert not causal_mask_ok(off, 5, 40)
+    assert not causal_mask_ok(causal(5, 40, -1e4, torch.float32), 5, 40)   # too weak to remove
+    assert not causal_mask_ok(causal(4, 40, float("-inf"), torch.float32), 5, 40)
