@@ -20,7 +20,7 @@ import torch.nn.functional as TF
 
 from openattention_amd import ops
 from openattention_amd.budget import CTX_LEN, budget
-from openattention_amd.prefill import LayerState, build_row
+from openattention_amd.prefill import LayerState, build_row, build_rows
 
 HQ, HKV, D, NL = 32, 8, 128, 32
 G = HQ // HKV
@@ -157,6 +157,7 @@ class OursHIP(Method):
         # the step's output rows: bf16 as the reference's, or the fp32 accumulators unrounded
         self.out = torch.empty(R, D, device=dev, dtype=out_dtype)
         self._sel = {}
+        self._pending = {}          # layer -> {batch row: (question rows, T, K, V)} awaiting build
         if not fused:
             self.kbar_r = torch.empty(R, self.Cn, D, device=dev, dtype=torch.bfloat16)
             self.vbar_r = torch.empty(R, self.Cn, D, device=dev, dtype=torch.bfloat16)
@@ -165,14 +166,44 @@ class OursHIP(Method):
     # ---------------------------------------------------------------- prefill
     def build(self, l, b, q, T):
         """Index build of layer l, batch row b after K,V of the prefix are in C.K[l][b, :, :T].
-        q: (1, HQ, Tq, D) prefill queries; the last C.qlen[b] rows are the question chunk."""
+        q: (1, HQ, Tq, D) prefill queries; the last C.qlen[b] rows are the question chunk.
+
+        The rows of a layer are collected and built together (prefill.build_rows: one batched
+        eigh and one launch per stage for all of them) once the layer's last batch row arrives;
+        the state is the one build_row gives row by row.  A decode step first builds any row
+        still waiting (flush_builds), so the order of calls stays free."""
         if self.static is None:
             raise RuntimeError("OursHIP needs the static query metric (dict with M, inv_freq, "
                                "attention_scaling)")
         Qn = C.qlen[b]
-        qrows = q[0, :, q.shape[2] - Qn:, :]
-        build_row(self.st[l], b, C.K[l][b], C.V[l][b], qrows, T, self.static["M"][l],
-                  self.static["inv_freq"], float(self.static.get("attention_scaling", 1.0)), l, G)
+        qrows = q[0, :, q.shape[2] - Qn:, :].clone()
+        pend = self._pending.setdefault(l, {})
+        pend[b] = (qrows, T, C.K[l], C.V[l])
+        if len(pend) == self.B:
+            self._build_layer(l)
+
+    def _build_layer(self, l):
+        pend = self._pending.pop(l, {})
+        if not pend:
+            return
+        scal = float(self.static.get("attention_scaling", 1.0))
+        M, inv = self.static["M"][l], self.static["inv_freq"]
+        rows = sorted(pend)
+        Ts = {pend[b][1] for b in rows}
+        Qs = {pend[b][0].shape[1] for b in rows}
+        K, V = pend[rows[0]][2], pend[rows[0]][3]
+        if (rows == list(range(self.B)) and len(Ts) == 1 and len(Qs) == 1 and K.is_contiguous()
+                and V.is_contiguous() and all(pend[b][2] is K and pend[b][3] is V for b in rows)):
+            build_rows(self.st[l], K, V, torch.stack([pend[b][0] for b in rows]), Ts.pop(), M, inv, scal, l, G)
+        else:
+            for b in rows:
+                qrows, T, Kc, Vc = pend[b]
+                build_row(self.st[l], b, Kc[b], Vc[b], qrows, T, M, inv, scal, l, G)
+
+    def flush_builds(self):
+        """Build every row whose build() call is still waiting for the rest of its layer."""
+        for l in list(self._pending):
+            self._build_layer(l)
 
     # ---------------------------------------------------------------- decode
     def sel_buffer(self, NS: int) -> torch.Tensor:
@@ -184,6 +215,8 @@ class OursHIP(Method):
         """One decode step of layer l over the cache C.K[l], C.V[l] (the new K, V already at
         n - 1; n also in C.n_dev).  `marks`, when given, receives (stage, event) pairs recorded
         on the current stream after each stage (per-stage timing)."""
+        if self._pending:
+            self.flush_builds()
         return self.step(self.st[l], C.K[l].view(-1, self.Lmax, D), C.V[l].view(-1, self.Lmax, D), q,
                          C.n_dev, n, marks)
 

@@ -11,13 +11,22 @@ token -- is captured once in a hipGraph and replayed with n advancing on the dev
 
 With `method` an OursHIP the attention is its decode (the gfx950 sparse stage); with
 method = None it is the dense split-K decode kernel over [0, n) on the same cache.
+
+`prefill` runs a prompt through the model one batch row at a time, as the reference's runner
+does (graph_runner.py:615-622): every layer's attention goes through the hook's prefill branch
+(method.attn_hook: K, V into the cache, dense causal attention, the method's index build with the
+prompt's last `qlen` query rows as the question chunk).  `probe(layers)` makes each decode step
+copy the attention's inputs and decisions of those layers into per-layer buffers (inside a
+captured graph too): the query rows, sel, quota, exp_idx and the attention output.
 """
 from __future__ import annotations
 
 import torch
 
+import types
+
 from openattention_amd import ops
-from openattention_amd.method import C as CTX
+from openattention_amd.method import C as CTX, Method, attn_hook
 from openattention_amd.synth import llama31_inv_freq
 
 HID, NLAYER, HQ, HKV, D, FFN, VOCAB = 4096, 32, 32, 8, 128, 14336, 128256
@@ -30,7 +39,8 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
 
 
 def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """x (B, H, D) at one position per row; cos, sin (B, 1, D)."""
+    """x (N, H, D) at one position per row n; cos, sin (N, 1, D) (or (1, 1, D) for one shared
+    position)."""
     h = D // 2
     xf = x.float()
     rot = torch.cat([-xf[..., h:], xf[..., :h]], -1)
@@ -65,10 +75,65 @@ class LlamaShaped:
         self.cos, self.sin = emb.cos(), emb.sin()                       # (Lmax, D) fp32
         self.tok = torch.zeros(B, device=dev, dtype=torch.long)         # token at position n - 1
         self.ws = None
+        self.mods = [types.SimpleNamespace(layer_idx=l) for l in range(layers)]
+        self.probes = {}
 
     def params(self) -> int:
         per = HID * (HQ + 2 * HKV) * D + HQ * D * HID + HID * 2 * FFN + FFN * HID + 2 * HID
         return self.L * per + 2 * VOCAB * HID + HID
+
+    def probe(self, layers) -> dict:
+        """Per-layer probe buffers that every later decode step fills (inside a captured graph
+        too): q (B*HQ, D) bf16, and with a sparse method sel, quota, exp_idx and the attention
+        output out (B*HQ, D) in the method's output dtype.  Returns {layer: {name: tensor}}."""
+        R = self.B * HQ
+        self.probes = {}
+        for l in layers:
+            p = {"q": torch.empty(R, D, device=self.dev, dtype=torch.bfloat16)}
+            if self.method is not None:
+                m = self.method
+                p["quota"] = torch.empty_like(m.quota)
+                p["exp_idx"] = torch.empty_like(m.exp_idx)
+                p["out"] = torch.empty_like(m.out)
+                p["sel"] = None          # sized at the first step (the sel width follows n)
+            self.probes[l] = p
+        return self.probes
+
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor, qlen: int = 64) -> torch.Tensor:
+        """Prompt prefill of every batch row (tokens (B, T) int64), one row at a time through all
+        layers (graph_runner.py:615-622).  Each layer's attention is attn_hook's prefill branch:
+        the row's K, V are written to C.K[l][b, :, :T], its causal attention is dense and the
+        method builds the row's index (C.qlen[b] = qlen question rows).  Leaves C.phase at
+        "decode" and the greedy next token of every row in self.tok; returns it."""
+        B, T = tokens.shape
+        if B != self.B or T > self.Lmax:
+            raise ValueError(f"tokens must be ({self.B}, <= {self.Lmax})")
+        CTX.phase = "prefill"
+        CTX.qlen = [qlen] * B
+        CTX.method = self.method if self.method is not None else Method(None, B, self.Lmax, self.dev)
+        cos, sin = self.cos[:T].unsqueeze(1), self.sin[:T].unsqueeze(1)           # (T, 1, D)
+        for b in range(B):
+            CTX.brow = b
+            x = self.embed.index_select(0, tokens[b])                              # (T, HID)
+            for l in range(self.L):
+                h = rmsnorm(x, self.ln1[l])
+                qkv = h @ self.wqkv[l]
+                q = rope(qkv[:, :HQ * D].view(T, HQ, D), cos, sin).transpose(0, 1).unsqueeze(0)
+                k = rope(qkv[:, HQ * D:(HQ + HKV) * D].view(T, HKV, D), cos, sin).transpose(0, 1).unsqueeze(0)
+                v = qkv[:, (HQ + HKV) * D:].view(T, HKV, D).transpose(0, 1).unsqueeze(0)
+                del qkv
+                o, _ = attn_hook(self.mods[l], q, k, v, None)                       # (1, T, HQ, D)
+                x = x + o.reshape(T, HQ * D) @ self.wo[l]
+                del q, k, v, o
+                h = rmsnorm(x, self.ln2[l])
+                gu = h @ self.w13[l]
+                x = x + (torch.nn.functional.silu(gu[:, :FFN]) * gu[:, FFN:]) @ self.w2[l]
+                del gu
+            logits = rmsnorm(x[-1:], self.lnf) @ self.lm_head
+            self.tok[b] = logits.argmax(-1)[0]
+        CTX.phase = "decode"
+        return self.tok
 
     @torch.no_grad()
     def step(self, n: int) -> torch.Tensor:
@@ -88,8 +153,20 @@ class LlamaShaped:
             v = qkv[:, (HQ + HKV) * D:].view(B, HKV, D)
             CTX.K[l].index_copy_(2, pos, k.unsqueeze(2))
             CTX.V[l].index_copy_(2, pos, v.unsqueeze(2))
+            p = self.probes.get(l)
+            if p is not None:
+                p["q"].copy_(q.reshape(B * HQ, D))
             if self.method is not None:
-                o = self.method.decode(l, q.reshape(B, HQ, 1, D), n).reshape(B, HQ * D)
+                o = self.method.decode(l, q.reshape(B, HQ, 1, D), n)
+                if p is not None:
+                    m = self.method
+                    if p["sel"] is None or p["sel"].shape != m.last_sel.shape:
+                        p["sel"] = torch.empty_like(m.last_sel)
+                    p["sel"].copy_(m.last_sel)
+                    p["quota"].copy_(m.quota)
+                    p["exp_idx"].copy_(m.exp_idx)
+                    p["out"].copy_(o.reshape(B * HQ, D))
+                o = o.reshape(B, HQ * D).to(x.dtype)
             else:
                 R = B * HQ
                 need = R * ops.DENSE_SPLITS * (D + 2)
