@@ -51,6 +51,9 @@ def parse():
                         "no CPU restatement")
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a hipGraph")
+    p.add_argument("--gate-mode", default="fused", choices=("fused", "split", "separate"),
+                   help="launch layout of top-k, ErrorGate and water-fill (same results): fused = one launch "
+                        "after the scan, split = pooled ErrorGate in the scan launch, separate = three stages")
     p.add_argument("--cpu-reps", type=int, default=10)
     p.add_argument("--groups", type=int, default=1,
                    help="split the batch into this many sequence groups on their own streams (1, 2, 4 "
@@ -109,6 +112,8 @@ KERNELS = {"index_prep": ["index_prep_kernel"],
            "gate_fill": ["errorgate_kernel", "waterfill_kernel"],
            "topk_gate_fill": ["topk_gate_fill_kernel"],
            "topq": ["topq_linear_kernel", "topq_row_kernel"],
+           "qgs_scan_gate": ["qgs_scan_gate_kernel"],
+           "topk_fix_fill": ["topk_fix_fill_kernel"],
            "residual_flash": ["resflash_kernel"]}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
 
@@ -281,12 +286,13 @@ def config4_sweep(a):
 
 
 def config5_run(a):
-    """a Llama-3.1-8B-shaped model (random-init bf16 weights, 32 layers) whose
-    KV cache holds a 32K-token prefix (the config-3 synthetic key/value mixture stands in for the
-    prompt's prefill), the index built for every layer and sequence (timed), then the whole
-    decode step -- embedding, 32 x (RMSNorm, QKV, RoPE, KV append, attention, O, RMSNorm,
-    SwiGLU), final norm, LM head, greedy token -- captured in one hipGraph and replayed, with the
-    sparse stage and with dense decode attention on the same cache."""
+    """a Llama-3.1-8B-shaped model (random-init bf16 weights, 32 layers), a
+    32K-token random prompt prefilled through the model one batch row at a time (every layer's
+    attention through the hook's prefill branch: K/V into the cache, dense causal attention, the
+    index built per layer; the build is timed on its own), then the whole decode step --
+    embedding, 32 x (RMSNorm, QKV, RoPE, KV append, attention, O, RMSNorm, SwiGLU), final norm,
+    LM head, greedy token -- captured in one hipGraph and replayed, with the sparse stage and
+    with dense decode attention on the same cache."""
     import torch
 
     from openattention_amd import _build, lib, synth
@@ -294,8 +300,7 @@ def config5_run(a):
         _build.build()
     lib.load()
     from openattention_amd.method import C as CTX, OursHIP
-    from openattention_amd.model import NLAYER, LlamaShaped
-    from openattention_amd.prefill import build_layers
+    from openattention_amd.model import NLAYER, VOCAB, LlamaShaped
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
@@ -304,38 +309,30 @@ def config5_run(a):
     for B in (1, 32):
         n_total = 2 * (a.warmup + a.steps) + 4
         Lmax = N + n_total
-        T0 = N - 1
         t0 = time.time()
         m = OursHIP(types.SimpleNamespace(rho=a.rho), B, Lmax, dev, n_layers=NLAYER, static=static)
-        CTX.K, CTX.V = [], []
-        qqs = []
-        for l in range(NLAYER):
-            K, V, _q, qq, _ = synth.make_layer(3, B, N, Lmax, 256, dev, layer=l)
-            CTX.K.append(K)
-            CTX.V.append(V)
-            qqs.append(qq)
-            if l % 8 == 7:
-                log(f"[config5] B={B}: {l + 1} layers of cache ({time.time() - t0:.1f}s)")
-        # the index of every layer: all layers' bases from one batched eigh, then each layer's
-        # HIP stages (prefill.build_layers).  One untimed build of layer 0 first: the solver's
-        # and the kernels' first-call set-up is not part of a request's build
-        build_layers(m.st[:1], CTX.K[:1], CTX.V[:1], qqs[:1], T0, static["M"], static["inv_freq"], 1.0,
-                     [0], G)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        build_layers(m.st, CTX.K, CTX.V, qqs, T0, static["M"], static["inv_freq"], 1.0,
-                     list(range(NLAYER)), G)
-        e1.record()
-        torch.cuda.synchronize()
-        build_ms = e0.elapsed_time(e1)
-        del qqs
-        log(f"[config5] B={B}: cache + index of {NLAYER} layers ({time.time() - t0:.1f}s, build "
-            f"{build_ms:.0f} ms)")
+        CTX.K = [torch.zeros(B, HKV, Lmax, D, device=dev, dtype=torch.bfloat16) for _ in range(NLAYER)]
+        CTX.V = [torch.zeros(B, HKV, Lmax, D, device=dev, dtype=torch.bfloat16) for _ in range(NLAYER)]
         model = LlamaShaped(B, Lmax, dev, method=m)
-        CTX.n0_dev = torch.tensor([T0], device=dev, dtype=torch.int32)
-        CTX.n_dev = torch.tensor([N], device=dev, dtype=torch.int32)
-        n = N
+        gen = torch.Generator(device="cpu").manual_seed(1000 + B)
+        tokens = torch.randint(0, VOCAB, (B, N), generator=gen).to(dev)
+        if B == 1:
+            # one untimed prefill of a short prompt first: the first-call set-up of the solver and
+            # the kernels is not part of a request's prefill
+            model.prefill(tokens[:, :4096], qlen=64)
+            torch.cuda.synchronize()
+        m.build_events = []
+        torch.cuda.synchronize()
+        p0 = time.time()
+        model.prefill(tokens, qlen=64)
+        torch.cuda.synchronize()
+        prefill_s = time.time() - p0
+        build_ms = sum(e0.elapsed_time(e1) for e0, e1 in m.build_events)
+        m.build_events = None
+        log(f"[config5] B={B}: prompt of {N} tokens prefilled through {NLAYER} layers in {prefill_s:.1f}s "
+            f"(index build {build_ms:.0f} ms; {time.time() - t0:.1f}s with the model set-up)")
+        CTX.n_dev = torch.tensor([N + 1], device=dev, dtype=torch.int32)
+        n = N + 1
         res = {}
         for name, method in (("sparse", m), ("dense", None)):
             model.method = method
@@ -370,9 +367,10 @@ def config5_run(a):
                "speedup_vs_dense": round(res["dense"] / res["sparse"], 2),
                "tokens_per_s_sparse": round(B / (res["sparse"] * 1e-3), 1),
                "tokens_per_s_dense": round(B / (res["dense"] * 1e-3), 1),
+               "prefill_s": round(prefill_s, 2), "prefill_tokens_per_s": round(B * N / prefill_s, 1),
                "index_build_ms": round(build_ms, 1),
-               "data": "synthetic 32K prefix (config-3 mixture keys, N(0,1) values) in the KV cache; decode "
-                       "steps run through the full model"}
+               "data": "synthetic: a 32K random-token prompt per sequence prefilled through the model (K/V and "
+                       "the index from the prefill); decode steps run through the full model"}
         print(json.dumps(rec), flush=True)
         del model, m
         CTX.K, CTX.V = [], []
@@ -525,7 +523,8 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
     Lmax = N + n_steps + 1
     T0 = N - 1
     static = synth.static_metric(L)
-    m = OursHIP(types.SimpleNamespace(rho=rho), B, Lmax, dev, n_layers=L, static=static, groups=a.groups)
+    m = OursHIP(types.SimpleNamespace(rho=rho), B, Lmax, dev, n_layers=L, static=static, groups=a.groups,
+                gate_mode=a.gate_mode)
     Ks, Vs, Qs = [], [], []
     t0 = time.time()
     build_ms = {}
@@ -637,6 +636,12 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
         "topk_gate_fill": (R * (-(-n_mid // 64)) * 4 + R * NSX * 4
                            + R * Cn * (2 * D * 4 + 4) + R * NSX * D * 2),
         "topq": R * n_mid * (2 + 1) + R * E * 4,               # 16-bit score heads + byte ids; exp out
+        # the scan's codes and the pooled ErrorGate's Sk, Sk2 and n of every cluster
+        "qgs_scan_gate": B * HKV * n_mid * 32 + R * Cn * (2 * D * 4 + 4),
+        # tile maxima and sel; K of sel, the pooled score / n_t rows, Sk, Sk2 of the clusters the
+        # selected tokens fall in (at most NSX per row)
+        "topk_fix_fill": (R * (-(-n_mid // 64)) * 4 + R * NSX * 4 + R * NSX * D * 2 + R * Cn * 8
+                          + R * min(NSX, Cn) * (2 * D * 4 + 4)),
         "residual_flash": R * (NSX + E) * 2 * D * 2 + R * Cn * (D * 4 + 4),  # K,V exact set; Sv, q.Sk
     }
     stage_alg = B * HKV * n_mid * 32 + R * (NSX + E) * 2 * D * 2 + R * Cn * (3 * D * 4 + 4)
@@ -744,7 +749,8 @@ def stage_point(a, B: int, N: int, rho: float, name: str, cpu: bool) -> dict:
         "config": {"workload": f"{name} sparse decode stage, one layer-step: B={B}, N={N}, rho={rho}, "
                                f"C={Cn}, E={E}, sink/local/top-k {ns}/{nl}/{k_top}",
                    "B": B, "N": N, "rho": rho, "C": Cn, "E": E, "layers_rotated": L,
-                   "mode": "eager" if graph is None else "hipgraph", "sequence_groups": a.groups},
+                   "mode": "eager" if graph is None else "hipgraph", "sequence_groups": a.groups,
+                   "gate_mode": a.gate_mode},
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "stage_alg_bytes": stage_alg,
         "stage_alg_GBps": round(stage_gbps, 1),

@@ -28,11 +28,11 @@
 extern "C" {
 #endif
 
-#define OA_ABI_VERSION 3
+#define OA_ABI_VERSION 4
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
-/* ABI version of this header (3). */
+/* ABI version of this header (4). */
 int oa_abi_version(void);
 
 /* Text for a status returned by any entry point. */
@@ -222,9 +222,11 @@ int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, l
 
 /*
  * oa_topk_select_heads followed by oa_gate_fill (n_sel = ns + nl + k_top, sel written as by
- * oa_topk_select_heads): the same sel, marked heads, score, n_t, quota and qsk.  Below 256 rows
- * with a register top-k (k_top <= 16 and at most 1024 score tiles) it is one launch in which
- * each row's workgroup runs its top-k and then its gate and fill; otherwise the two calls.
+ * oa_topk_select_heads): the same sel, marked heads, score, n_t, quota and qsk.  With a register
+ * top-k (k_top <= 16 and at most 2048 score tiles) it is one launch: each row's workgroup runs
+ * its top-k on one wave while its other waves compute every cluster's ErrorGate from the pooled
+ * sums, then the clusters holding a selected token are computed again without those tokens
+ * (the same arithmetic) and the row's water-fill runs; otherwise the two calls.
  * Replaces the consecutive _k_select and _k_errorgate / _k_waterfill steps of the deployed decode
  * graph (inference/graph_runner.py:123-159, inference/ours_fused.py:122-216); the fusion itself
  * has no counterpart in the reference.
@@ -237,6 +239,44 @@ int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, long tm_strid
                       long sel_stride, const float* Sk, const float* Sk2, const float* nb, int C,
                       float sm_scale, float sm_scale_sq, int budget, float* score, float* n_t,
                       float* quota, float* qsk, void* stream);
+
+/*
+ * oa_qgs_scan_heads and the pooled part of the ErrorGate in one launch: besides the key heads
+ * and tile maxima, every cluster's wl1 score and tail count as if it held no selected token
+ * (the pooled sums; score, n_t (rows, C)) and q . Sk_c (qsk, or NULL).  Scan blocks and gate
+ * blocks (one row, 16 clusters each) are interleaved in one grid, so the gate's dependent chains
+ * run under the code stream.  For the clusters that hold no selected token these are the final
+ * ErrorGate outputs (the same arithmetic as oa_errorgate); oa_topk_fix_fill corrects the others
+ * once the selection is known.  The fusion has no counterpart in the reference: it splits
+ * _k_errorgate (inference/ours_fused.py:122-154) into its selection-independent part, run with
+ * the scan (inference/graph_runner.py:100-120), and the selected tokens' part.
+ *   Arguments: those of oa_qgs_scan_heads, then q (rows = 4 * kv_rows, 128) bf16, Sk, Sk2
+ *   (rows, C, 128), nb (rows, C) fp32, C <= 256, the softmax scale and its square.
+ */
+int oa_qgs_scan_gate(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
+                     const int* fexp, uint16_t* H, long h_stride, float* TM, long tm_stride,
+                     const int* n_dev, int ns, int nl, const void* q, long q_stride, const float* Sk,
+                     const float* Sk2, const float* nb, int C, float sm_scale, float sm_scale_sq,
+                     float* score, float* n_t, float* qsk, void* stream);
+
+/*
+ * After oa_qgs_scan_gate: the top-k over the key heads (as oa_topk_select_heads), then the
+ * ErrorGate of the clusters holding a selected token done again from the pooled sums minus
+ * their selected keys (score and n_t updated in place; the others keep the pooled values), then
+ * the water-filling.  The same sel, marked heads, score, n_t and quota as oa_topk_select_heads
+ * followed by oa_gate_fill.  One launch (a workgroup per row: its top-k, correction and fill)
+ * with a register top-k (k_top <= 16 and at most 2048 score tiles), else the radix top-k and a
+ * second launch.  Replaces the consecutive _k_select and _k_errorgate / _k_waterfill steps
+ * (inference/graph_runner.py:123-159, inference/ours_fused.py:122-216).
+ */
+int oa_topk_fix_fill(uint16_t* H, long h_stride, const float* TM, long tm_stride, int ntiles,
+                     const int* n_dev, int ns, int nl, int k_top, const int8_t* codes, int Lmax,
+                     const int8_t* limbs, const int* fexp, const void* q, long q_stride,
+                     const void* K, long k_stride_b, long k_stride_s, int rows, int kv_rows,
+                     int head_dim, const int32_t* asg, long asg_stride, int32_t* sel,
+                     long sel_stride, const float* Sk, const float* Sk2, const float* nb, int C,
+                     float sm_scale, float sm_scale_sq, int budget, float* score, float* n_t,
+                     float* quota, void* stream);
 
 /*
  * Within-cluster top-q: the q_c best tail members of every cluster by QGS score (ties to the

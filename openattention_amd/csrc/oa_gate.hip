@@ -16,90 +16,17 @@
 #include "oa_common.h"
 #include "oa_detmath.h"
 #include "oa_topk_row.h"
+#include "oa_gate_row.h"
 
 namespace {
+
+using namespace oa_gate;
 
 constexpr int kGateThreads = 512;
 constexpr int kGateWaves = kGateThreads / 64;
 constexpr int kMaxSel = 64;
 constexpr int kMaxC = 256;
 constexpr int kFuseRows = 256;       // oa_gate_fill: one fused launch below this many rows
-
-struct GateArgs {
-  const uint16_t* q; long q_stride;
-  const uint16_t* K; long k_sb; long k_ss; int G;
-  const int32_t* asg; long asg_stride;
-  const int32_t* sel; long sel_stride; int n_sel;
-  const float* Sk; const float* Sk2; long st_stride_r;   // (R, C, D): row stride in floats
-  const float* nb; long nb_stride;
-  float* score; float* n_t; long out_stride;
-  float* qsk;                                         // optional: q . Sk_c of every cluster
-  int C; float sc; float sc2;
-};
-
-// x / den for den >= 1, given r = 1 / den correctly rounded: q = RN(x r) lies within one ulp of
-// x / den and r within half an ulp of 1 / den, so fma(fma(-q, den, x), r, q) is x / den correctly
-// rounded (Markstein's theorem; the residual fma(-q, den, x) is exact) as long as nothing
-// underflows or overflows.  Zeros (whose sign the residual step loses), tiny, huge and
-// non-finite x take the division itself.
-__device__ __forceinline__ bool div_fast_ok(float x) {
-  const float ax = fabsf(x);
-  return ax >= 0x1p-100f && ax <= 0x1p100f;
-}
-__device__ __forceinline__ float div_den(float x, float den, float r) {
-  const float q = x * r;
-  return fmaf(fmaf(-q, den, x), r, q);
-}
-
-// the two wave-wide parts of one cluster's score (lane holds dims lane and lane+64): the tail
-// sums minus the selected tokens, then zbar = sc q.kbar and the raw sc2 (q*q).var
-__device__ __forceinline__ void gate_dots(const GateArgs& a, float sk_lo, float sk_hi,
-                                          float s2_lo, float s2_hi, float nt, float q_lo,
-                                          float q_hi, float qq_lo, float qq_hi,
-                                          unsigned long long selmask, const float* s_k, int lane,
-                                          float* zbar_out, float* s2_out, float* nt_out,
-                                          float* qsk_out) {
-  // q . Sk of the pooled sums (before the selected tokens leave them), for the residual pass
-  *qsk_out = oa::dot128_canon(q_lo, sk_lo, q_hi, sk_hi);
-  // the cluster's selected tokens, in selection order (bit i = selected token i)
-  while (selmask) {
-    const int i = __ffsll((long long)selmask) - 1;
-    selmask &= selmask - 1ull;
-    {
-      const float k_lo = s_k[i * OA_D + lane], k_hi = s_k[i * OA_D + lane + 64];
-      sk_lo = sk_lo - k_lo;
-      sk_hi = sk_hi - k_hi;
-      s2_lo = s2_lo - k_lo * k_lo;
-      s2_hi = s2_hi - k_hi * k_hi;
-      nt = nt - 1.0f;
-    }
-  }
-  const float den = fmaxf(nt, 1.0f);
-  float kb_lo, kb_hi, ks_lo, ks_hi;
-  if (__all(div_fast_ok(sk_lo) && div_fast_ok(sk_hi) && div_fast_ok(s2_lo) && div_fast_ok(s2_hi))) {
-    const float r = 1.0f / den;          // uniform: one division per cluster
-    kb_lo = div_den(sk_lo, den, r); kb_hi = div_den(sk_hi, den, r);
-    ks_lo = div_den(s2_lo, den, r); ks_hi = div_den(s2_hi, den, r);
-  } else {
-    kb_lo = sk_lo / den; kb_hi = sk_hi / den;
-    ks_lo = s2_lo / den; ks_hi = s2_hi / den;
-  }
-  const float v_lo = fmaxf(ks_lo - kb_lo * kb_lo, 0.f);
-  const float v_hi = fmaxf(ks_hi - kb_hi * kb_hi, 0.f);
-  *zbar_out = a.sc * oa::dot128_canon(q_lo, kb_lo, q_hi, kb_hi);
-  *s2_out = a.sc2 * oa::dot128_canon(qq_lo, v_lo, qq_hi, v_hi);
-  *nt_out = nt;
-}
-
-// the scalar tail of one cluster's wl1 score
-__device__ __forceinline__ float gate_score(float zbar, float s2, float nt) {
-  if (!(nt >= 2.0f)) s2 = 0.f;
-  const float s2c = fmaxf(s2, 0.f);
-  const float sig = sqrtf(s2c);
-  const float er = oa::det_erff(sig * 0.70710677f);
-  const float log_d = 0.5f * s2c + oa::det_logf(fmaxf(er, 1e-30f));
-  return (zbar + oa::det_logf(fmaxf(nt, 1.0f))) + log_d;
-}
 
 // ErrorGate of one row by a 512-thread workgroup into LDS rows (score, n_t).  The wave-wide dot
 // products run six clusters per wave at a time with all their loads in flight; the scalar tails (erf, logs)
@@ -592,37 +519,244 @@ __global__ void __launch_bounds__(kGateThreads) gate_fill_kernel(GateArgs a, flo
     waterfill_row<NS>(s_score, s_nt, quota + (long)row * a.C, a.C, budget, threadIdx.x, s_cw);
 }
 
-// fewer rows than compute units, with a register top-k: the row's top-k (wave 0), then its gate
-// and fill, in one workgroup.  The top-k's sel row is written to global memory and read back by
-// the gate after the barrier (one workgroup, one compute unit: the barrier orders it); the
-// marked score heads are read by the next launch.
+// the row's top-k arguments (the register top-k of oa_topk_row.h over key heads)
 struct TopkArgs {
   uint16_t* H; long h_stride;
   const float* TM; long tm_stride; int ntiles;
   const int* n_dev; int ns, nl, k_top;
   oa_sel::Rescore rs;
 };
-template <int NS, int TPL, int KR>
-// (sel is written here and read by gate_row through a.sel, the same memory: no __restrict__)
-__global__ void __launch_bounds__(kGateThreads) topk_gate_fill_kernel(TopkArgs t, GateArgs a,
-                                                                      int32_t* sel,
-                                                                      float* __restrict__ quota,
-                                                                      double budget) {
-  __shared__ float s_score[kMaxC], s_nt[kMaxC];
-  __shared__ double2 s_cw[kMaxC];
+
+// ---- the ErrorGate finished after the selection, with the water-fill ------------------------
+// oa_qgs_scan_gate left every cluster's score and n_t as if no token were selected (and q . Sk).
+// Once sel is known only the clusters holding a selected token change: they are computed again
+// from the pooled sums minus their selected keys, in selection order (gate_dots with the
+// cluster's mask: the arithmetic of gate_row), and the fill runs on the completed rows.
+constexpr int kFixThreads = 256;
+
+struct FixLds {
+  float score[kMaxC], nt[kMaxC];
+  double2 cw[kMaxC];
+  unsigned long long selmask[kMaxC];
+  int sel[kMaxSel];
+  int hit[kMaxSel];
+  float zb[kMaxSel], s2[kMaxSel], hnt[kMaxSel];
+  int nhit;
+};
+
+// the pooled score and n_t rows into LDS, the masks cleared (threads [t0, t0 + nthreads)); with
+// load_sel the row's sel from global memory as well (else the top-k leaves it in L.sel)
+__device__ __forceinline__ void fix_load(const GateArgs& a, int row, FixLds& L, int t0, int nthreads,
+                                         bool load_sel) {
+  const int t = (int)threadIdx.x - t0;
+  for (int c = t; c < a.C; c += nthreads) {
+    L.score[c] = a.score[(long)row * a.out_stride + c];
+    L.nt[c] = a.n_t[(long)row * a.out_stride + c];
+    L.selmask[c] = 0ull;
+  }
+  if (load_sel && t < a.n_sel) L.sel[t] = a.sel[(long)row * a.sel_stride + t];
+  if (t == 0) L.nhit = 0;
+}
+
+// after fix_load (and the top-k) and a barrier: the clusters holding a selected token done again,
+// then the fill (wave 0).  Dynamic LDS: n_sel * 128 floats of selected keys.
+template <int NS, int kThr = kFixThreads>
+__device__ __forceinline__ void fix_finish(const GateArgs& a, int row, FixLds& L, float* quota_row,
+                                           double budget) {
+  constexpr int kWv = kThr / 64;
+  extern __shared__ float s_k[];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int kvr = row / a.G;
+  constexpr int kW = OA_D / 8;
+  const int n_sel = a.n_sel;
+  // selected tokens: cluster ids (one per thread) and key words (16 bytes each, up to four per
+  // thread), all requested together
+  const int tokm = tid < n_sel ? L.sel[tid] : -1;
+  const int cm = tokm >= 0 ? a.asg[(long)row * a.asg_stride + tokm] : -1;
+  uint4 kw[4];
+  int ke[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + u * kThr;
+    ke[u] = e < n_sel * kW ? e : -1;
+    kw[u] = make_uint4(0u, 0u, 0u, 0u);
+    if (ke[u] >= 0)
+      kw[u] = *reinterpret_cast<const uint4*>(a.K + (long)kvr * a.k_sb + (long)L.sel[e / kW] * a.k_ss +
+                                              (e % kW) * 8);
+  }
+  const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
+  const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
+  if (cm >= 0) {
+    const unsigned long long old = atomicOr(&L.selmask[cm], 1ull << tid);
+    if (old == 0ull) L.hit[atomicAdd(&L.nhit, 1)] = cm;
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (ke[u] < 0) continue;
+    float x[8];
+    oa::unpack8(kw[u], x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_k[(ke[u] / kW) * OA_D + (ke[u] % kW) * 8 + j] = x[j];
+  }
+  __syncthreads();
+  // the hit clusters' dot products: wave w takes hits w, w + 4, ..., kBatch of them with all
+  // their loads in flight at a time
+  const int nhit = L.nhit;
+  const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
+  constexpr int kBatch = 4;
+  for (int h0 = wave; h0 < nhit; h0 += kWv * kBatch) {
+    float sk[kBatch][2], s2[kBatch][2], nbv[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int h = min(h0 + kWv * i, nhit - 1);
+      const int c = L.hit[h];
+      const long base = (long)row * a.st_stride_r + (long)c * OA_D;
+      sk[i][0] = a.Sk[base + lane];
+      sk[i][1] = a.Sk[base + lane + 64];
+      s2[i][0] = a.Sk2[base + lane];
+      s2[i][1] = a.Sk2[base + lane + 64];
+      nbv[i] = a.nb[(long)row * a.nb_stride + c];
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int h = h0 + kWv * i;
+      if (h < nhit) {
+        float zb, sv, nt, qs;
+        gate_dots(a, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi,
+                  L.selmask[L.hit[h]], s_k, lane, &zb, &sv, &nt, &qs);
+        if (lane == 0) {
+          L.zb[h] = zb;
+          L.s2[h] = sv;
+          L.hnt[h] = nt;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // the scalar tails, one hit cluster per thread
+  if (tid < nhit) {
+    const int c = L.hit[tid];
+    const float sc = gate_score(L.zb[tid], L.s2[tid], L.hnt[tid]);
+    L.score[c] = sc;
+    L.nt[c] = L.hnt[tid];
+    a.score[(long)row * a.out_stride + c] = sc;
+    a.n_t[(long)row * a.out_stride + c] = L.hnt[tid];
+  }
+  __syncthreads();
+  if (wave == 0) waterfill_row<NS>(L.score, L.nt, quota_row, a.C, budget, lane, L.cw);
+}
+
+template <int NS>
+__global__ void __launch_bounds__(kFixThreads) fix_fill_kernel(GateArgs a, float* __restrict__ quota,
+                                                               double budget) {
+  __shared__ FixLds L;
   const int row = blockIdx.x;
+  fix_load(a, row, L, 0, kFixThreads, true);
+  __syncthreads();
+  fix_finish<NS>(a, row, L, quota + (long)row * a.C, budget);
+}
+
+// the row's register top-k (wave 0, its sel row also into LDS) while the other waves stage the
+// pooled rows, then the correction and the fill
+template <int NS, int TPL, int KR>
+__global__ void __launch_bounds__(kFixThreads) topk_fix_fill_kernel(TopkArgs t, GateArgs a, int32_t* sel,
+                                                                    float* __restrict__ quota,
+                                                                    double budget) {
+  __shared__ FixLds L;
+  const int row = oa::xcd_row(blockIdx.x, gridDim.x);   // a KV row's query rows share one L2
   if (threadIdx.x < 64)
     oa_sel::topk_reg_row<TPL, KR, true>(t.H, t.h_stride, t.TM, t.tm_stride, t.ntiles, sel,
                                         a.sel_stride, *t.n_dev, t.ns, t.nl, t.k_top, t.rs, row,
-                                        threadIdx.x);
+                                        threadIdx.x, L.sel);
+  else
+    fix_load(a, row, L, 64, kFixThreads - 64, false);
   __syncthreads();
-  gate_row(a, row, s_score, s_nt);
-  for (int c = threadIdx.x; c < a.C; c += kGateThreads) {
-    a.score[(long)row * a.out_stride + c] = s_score[c];
-    a.n_t[(long)row * a.out_stride + c] = s_nt[c];
+  fix_finish<NS>(a, row, L, quota + (long)row * a.C, budget);
+}
+
+// ---- top-k, ErrorGate and water-fill of a row in one workgroup, the gate's pooled part
+// concurrent with the top-k -----------------------------------------------------------------
+// Wave 0 runs the row's register top-k while waves 1 .. W-1 compute the clusters' pooled
+// ErrorGate dot products (gate_dots with an empty mask): wave w takes the batches of kPoolBatch
+// consecutive clusters w - 1, w - 1 + (W - 1), ... (a fixed split: every loop bound depends on
+// the wave index and C only), all of a batch's loads in flight.  Then every cluster's scalar
+// tail (one per thread), the clusters holding a selected token done again with their masks
+// (fix_finish), and the fill on wave 0.  Every cluster's score and n_t, and q . Sk, are
+// written out.
+constexpr int kPoolBatch = 8;
+struct Gate2Lds {
+  FixLds f;
+  float zb[kMaxC], s2[kMaxC], nt[kMaxC];
+};
+
+template <int W>
+__device__ __forceinline__ void pooled_batches(const GateArgs& a, int row, Gate2Lds& L) {
+  constexpr int nGW = W - 1;
+  const int gw = (int)(threadIdx.x >> 6) - 1;       // 0 .. W-2
+  const int lane = threadIdx.x & 63;
+  const float q_lo = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane]);
+  const float q_hi = oa::bf16_to_f32(a.q[(long)row * a.q_stride + lane + 64]);
+  const float qq_lo = q_lo * q_lo, qq_hi = q_hi * q_hi;
+  for (int c0 = gw * kPoolBatch; c0 < a.C; c0 += nGW * kPoolBatch) {
+    float sk[kPoolBatch][2], s2[kPoolBatch][2], nbv[kPoolBatch];
+#pragma unroll
+    for (int i = 0; i < kPoolBatch; ++i) {
+      const int c = min(c0 + i, a.C - 1);
+      const long base = (long)row * a.st_stride_r + (long)c * OA_D;
+      sk[i][0] = a.Sk[base + lane];
+      sk[i][1] = a.Sk[base + lane + 64];
+      s2[i][0] = a.Sk2[base + lane];
+      s2[i][1] = a.Sk2[base + lane + 64];
+      nbv[i] = a.nb[(long)row * a.nb_stride + c];
+    }
+#pragma unroll
+    for (int i = 0; i < kPoolBatch; ++i) {
+      const int c = c0 + i;
+      if (c < a.C) {
+        float zb, sv, nt, qs;
+        gate_dots(a, sk[i][0], sk[i][1], s2[i][0], s2[i][1], nbv[i], q_lo, q_hi, qq_lo, qq_hi, 0ull,
+                  nullptr, lane, &zb, &sv, &nt, &qs);
+        if (lane == 0) {
+          L.zb[c] = zb;
+          L.s2[c] = sv;
+          L.nt[c] = nt;
+          if (a.qsk) a.qsk[(long)row * a.C + c] = qs;
+        }
+      }
+    }
   }
-  if (threadIdx.x < 64)
-    waterfill_row<NS>(s_score, s_nt, quota + (long)row * a.C, a.C, budget, threadIdx.x, s_cw);
+}
+
+template <int NS, int TPL, int KR, int W>
+__global__ void __launch_bounds__(64 * W) topk_gate2_fill_kernel(TopkArgs t, GateArgs a, int32_t* sel,
+                                                                  float* __restrict__ quota, double budget) {
+  __shared__ Gate2Lds L;
+  constexpr int kThr = 64 * W;
+  const int row = oa::xcd_row(blockIdx.x, gridDim.x);   // a KV row's query rows share one L2
+  const int tid = threadIdx.x;
+  if (tid < 64)
+    oa_sel::topk_reg_row<TPL, KR, true>(t.H, t.h_stride, t.TM, t.tm_stride, t.ntiles, sel,
+                                        a.sel_stride, *t.n_dev, t.ns, t.nl, t.k_top, t.rs, row, tid,
+                                        L.f.sel);
+  else
+    pooled_batches<W>(a, row, L);
+  if (tid == 0) L.f.nhit = 0;
+  __syncthreads();
+  for (int c = tid; c < a.C; c += kThr) {
+    L.f.score[c] = gate_score(L.zb[c], L.s2[c], L.nt[c]);
+    L.f.nt[c] = L.nt[c];
+    L.f.selmask[c] = 0ull;
+  }
+  __syncthreads();
+  fix_finish<NS, kThr>(a, row, L.f, quota + (long)row * a.C, budget);
+  // the rows' pooled values of the clusters no selected token touched (fix_finish wrote the others)
+  for (int c = tid; c < a.C; c += kThr) {
+    if (L.f.selmask[c]) continue;
+    a.score[(long)row * a.out_stride + c] = L.f.score[c];
+    a.n_t[(long)row * a.out_stride + c] = L.f.nt[c];
+  }
 }
 
 int launch_fill(const float* score, const float* n_t, int rows, int C, int budget, float* quota,
@@ -720,9 +854,9 @@ extern "C" int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, lo
                                  void* stream) {
   const int n_sel = ns + nl + k_top;
   const int tpl = (ntiles + 63) / 64;
-  const bool reg = (k_top <= 9 && tpl <= 9) || (k_top <= 16 && tpl <= 16);
-  if (rows >= kFuseRows || !reg) {
-    // two launches: the top-k variant the row length needs, then the gate and fill
+  const int reg = (k_top <= 9 && tpl <= 9) ? 1 : (k_top <= 16 && tpl <= 16) ? 2 : (k_top <= 16 && tpl <= 32) ? 3 : 0;
+  if (!reg) {
+    // two launches: the radix top-k the row length needs, then the gate and fill
     int st = oa_topk_select_heads(H, h_stride, TM, tm_stride, rows, ntiles, sel, sel_stride, n_dev,
                                   ns, nl, k_top, codes, kv_rows, Lmax, limbs, fexp, stream);
     if (st) return st;
@@ -731,7 +865,8 @@ extern "C" int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, lo
                         budget, score, n_t, quota, qsk, stream);
   }
   // the checks of both launches it replaces
-  if (!H || !codes || !limbs || !fexp || kv_rows <= 0 || rows != kv_rows * oa_sel::GQ ||
+  if (!H || !codes || !limbs || !fexp || !q || !K || !asg || (!sel && n_sel > 0) || !Sk || !Sk2 ||
+      !nb || !score || !n_t || !quota || kv_rows <= 0 || rows != kv_rows * oa_sel::GQ ||
       Lmax <= 0 || (reinterpret_cast<uintptr_t>(codes) & 15) ||
       (reinterpret_cast<uintptr_t>(limbs) & 3) || ntiles <= 0 || k_top < 0 || k_top > ntiles ||
       ns < 0 || nl < 0 || ns > 64 || nl > 64 || sel_stride < n_sel || head_dim != OA_D ||
@@ -742,7 +877,7 @@ extern "C" int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, lo
   t.H = H; t.h_stride = h_stride; t.TM = TM; t.tm_stride = tm_stride; t.ntiles = ntiles;
   t.n_dev = n_dev; t.ns = ns; t.nl = nl; t.k_top = k_top;
   t.rs = oa_sel::Rescore{codes, (long)Lmax, limbs, fexp};
-  GateArgs a;
+  GateArgs a{};
   a.q = (const uint16_t*)q; a.q_stride = q_stride;
   a.K = (const uint16_t*)K; a.k_sb = k_stride_b; a.k_ss = k_stride_s; a.G = rows / kv_rows;
   a.asg = asg; a.asg_stride = asg_stride;
@@ -753,21 +888,31 @@ extern "C" int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, lo
   a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
   const size_t lds = sizeof(float) * (size_t)n_sel * OA_D;
   const int nsl = (C + 63) / 64;
-  const dim3 g(rows), blk(kGateThreads);
   hipStream_t s = (hipStream_t)stream;
   const double bd = (double)budget;
-#define OA_TGF(NS)                                                                              \
+  // below kFuseRows rows every row is resident anyway: eight waves per row (seven on the pooled
+  // gate); above, four, so that every row of a B = 32 batch stays resident
+  const bool wide = rows < kFuseRows;
+  const dim3 g(rows);
+#define OA_TG2(NS, T, KK)                                                                       \
   do {                                                                                          \
-    if (k_top <= 9 && tpl <= 9)                                                                 \
-      hipLaunchKernelGGL((topk_gate_fill_kernel<NS, 9, 9>), g, blk, lds, s, t, a, sel, quota, bd); \
+    if (wide)                                                                                   \
+      hipLaunchKernelGGL((topk_gate2_fill_kernel<NS, T, KK, 8>), g, dim3(512), lds, s, t, a, sel, quota, bd); \
     else                                                                                        \
-      hipLaunchKernelGGL((topk_gate_fill_kernel<NS, 16, 16>), g, blk, lds, s, t, a, sel, quota, bd); \
+      hipLaunchKernelGGL((topk_gate2_fill_kernel<NS, T, KK, 4>), g, dim3(256), lds, s, t, a, sel, quota, bd); \
   } while (0)
-  if (nsl == 1) OA_TGF(1);
-  else if (nsl == 2) OA_TGF(2);
-  else if (nsl == 3) OA_TGF(3);
-  else OA_TGF(4);
-#undef OA_TGF
+#define OA_TG2_NS(NS)                                                                           \
+  do {                                                                                          \
+    if (reg == 1) OA_TG2(NS, 9, 9);                                                             \
+    else if (reg == 2) OA_TG2(NS, 16, 16);                                                      \
+    else OA_TG2(NS, 32, 16);                                                                    \
+  } while (0)
+  if (nsl == 1) OA_TG2_NS(1);
+  else if (nsl == 2) OA_TG2_NS(2);
+  else if (nsl == 3) OA_TG2_NS(3);
+  else OA_TG2_NS(4);
+#undef OA_TG2_NS
+#undef OA_TG2
   return OA_LAUNCH_STATUS();
 }
 
@@ -775,4 +920,69 @@ extern "C" int oa_waterfill(const float* score, const float* n_t, int rows, int 
                             float* quota, void* stream) {
   if (rows <= 0 || C <= 0 || C > kMaxC || budget < 0) return OA_EINVAL;
   return launch_fill(score, n_t, rows, C, budget, quota, (hipStream_t)stream);
+}
+
+extern "C" int oa_topk_fix_fill(uint16_t* H, long h_stride, const float* TM, long tm_stride,
+                                int ntiles, const int* n_dev, int ns, int nl, int k_top,
+                                const int8_t* codes, int Lmax, const int8_t* limbs, const int* fexp,
+                                const void* q, long q_stride, const void* K, long k_stride_b,
+                                long k_stride_s, int rows, int kv_rows, int head_dim,
+                                const int32_t* asg, long asg_stride, int32_t* sel, long sel_stride,
+                                const float* Sk, const float* Sk2, const float* nb, int C,
+                                float sm_scale, float sm_scale_sq, int budget, float* score,
+                                float* n_t, float* quota, void* stream) {
+  const int n_sel = ns + nl + k_top;
+  if (!H || !codes || !limbs || !fexp || !q || !K || !asg || (!sel && n_sel > 0) || !Sk || !Sk2 || !nb || !score ||
+      !n_t || !quota || kv_rows <= 0 || rows != kv_rows * oa_sel::GQ || Lmax <= 0 ||
+      (reinterpret_cast<uintptr_t>(codes) & 15) || (reinterpret_cast<uintptr_t>(limbs) & 3) ||
+      ntiles <= 0 || k_top < 0 || k_top > ntiles || ns < 0 || nl < 0 || ns > 64 || nl > 64 ||
+      sel_stride < n_sel || head_dim != OA_D || n_sel > kMaxSel || C <= 0 || C > kMaxC ||
+      budget < 0 || k_stride_b % 8 || k_stride_s % 8 || (reinterpret_cast<uintptr_t>(K) & 15))
+    return OA_EINVAL;
+  GateArgs a{};
+  a.q = (const uint16_t*)q; a.q_stride = q_stride;
+  a.K = (const uint16_t*)K; a.k_sb = k_stride_b; a.k_ss = k_stride_s; a.G = rows / kv_rows;
+  a.asg = asg; a.asg_stride = asg_stride;
+  a.sel = sel; a.sel_stride = sel_stride; a.n_sel = n_sel;
+  a.Sk = Sk; a.Sk2 = Sk2; a.st_stride_r = (long)C * OA_D;
+  a.nb = nb; a.nb_stride = C;
+  a.score = score; a.n_t = n_t; a.out_stride = C; a.qsk = nullptr;
+  a.C = C; a.sc = sm_scale; a.sc2 = sm_scale_sq;
+  const size_t lds = sizeof(float) * (size_t)n_sel * OA_D;
+  const int nsl = (C + 63) / 64;
+  const int tpl = (ntiles + 63) / 64;
+  const dim3 g(rows), blk(kFixThreads);
+  hipStream_t s = (hipStream_t)stream;
+  const double bd = (double)budget;
+  const int reg = (k_top <= 9 && tpl <= 9) ? 1 : (k_top <= 16 && tpl <= 16) ? 2 : (k_top <= 16 && tpl <= 32) ? 3 : 0;
+  if (!reg) {
+    // the radix-select top-k the row needs, then the correction and the fill
+    const int st = oa_topk_select_heads(H, h_stride, TM, tm_stride, rows, ntiles, sel, sel_stride,
+                                        n_dev, ns, nl, k_top, codes, kv_rows, Lmax, limbs, fexp, stream);
+    if (st) return st;
+    if (nsl == 1) hipLaunchKernelGGL(fix_fill_kernel<1>, g, blk, lds, s, a, quota, bd);
+    else if (nsl == 2) hipLaunchKernelGGL(fix_fill_kernel<2>, g, blk, lds, s, a, quota, bd);
+    else if (nsl == 3) hipLaunchKernelGGL(fix_fill_kernel<3>, g, blk, lds, s, a, quota, bd);
+    else hipLaunchKernelGGL(fix_fill_kernel<4>, g, blk, lds, s, a, quota, bd);
+    return OA_LAUNCH_STATUS();
+  }
+  TopkArgs t;
+  t.H = H; t.h_stride = h_stride; t.TM = TM; t.tm_stride = tm_stride; t.ntiles = ntiles;
+  t.n_dev = n_dev; t.ns = ns; t.nl = nl; t.k_top = k_top;
+  t.rs = oa_sel::Rescore{codes, (long)Lmax, limbs, fexp};
+#define OA_TFF(NS)                                                                              \
+  do {                                                                                          \
+    if (reg == 1)                                                                               \
+      hipLaunchKernelGGL((topk_fix_fill_kernel<NS, 9, 9>), g, blk, lds, s, t, a, sel, quota, bd); \
+    else if (reg == 2)                                                                          \
+      hipLaunchKernelGGL((topk_fix_fill_kernel<NS, 16, 16>), g, blk, lds, s, t, a, sel, quota, bd); \
+    else                                                                                        \
+      hipLaunchKernelGGL((topk_fix_fill_kernel<NS, 32, 16>), g, blk, lds, s, t, a, sel, quota, bd); \
+  } while (0)
+  if (nsl == 1) OA_TFF(1);
+  else if (nsl == 2) OA_TFF(2);
+  else if (nsl == 3) OA_TFF(3);
+  else OA_TFF(4);
+#undef OA_TFF
+  return OA_LAUNCH_STATUS();
 }

@@ -20,6 +20,7 @@
 #include "oa_score.h"
 #include "oa_prep.h"
 #include "oa_topk_row.h"
+#include "oa_gate_row.h"
 
 typedef int oa_v4i __attribute__((ext_vector_type(4)));
 
@@ -50,18 +51,30 @@ constexpr int kScanThreads = 256;
 constexpr int kTilesPerWave = 2;
 constexpr int kTokWG = kScanThreads / 64 * kTilesPerWave * 64;
 
-// HEADS: the score rows hold 16-bit key heads (oa::score_head) instead of fp32 scores
+struct ScanArgs {
+  const int8_t* codes; int Lmax; const int8_t* limbs; const int* fexp;
+  void* Sv; long s_stride; float* TM; long tm_stride;
+  const int* n_dev; int ns; int nl;
+};
+
+// HEADS: the score rows hold 16-bit key heads (oa::score_head) instead of fp32 scores.
+// One block: token chunk `chunk` (kTokWG tokens) of KV row kvr.
 template <bool HEADS>
-__global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
-    const int8_t* __restrict__ codes, int Lmax, const int8_t* __restrict__ limbs,
-    const int* __restrict__ fexp, void* __restrict__ Sv, long s_stride, float* __restrict__ TM,
-    long tm_stride, const int* __restrict__ n_dev, int ns, int nl) {
-  const int kvr = blockIdx.y;
+__device__ __forceinline__ void scan_block(const ScanArgs& sa, int chunk, int kvr) {
+  const int8_t* __restrict__ codes = sa.codes;
+  const int Lmax = sa.Lmax;
+  const int8_t* __restrict__ limbs = sa.limbs;
+  const int* __restrict__ fexp = sa.fexp;
+  void* __restrict__ Sv = sa.Sv;
+  const long s_stride = sa.s_stride;
+  float* __restrict__ TM = sa.TM;
+  const long tm_stride = sa.tm_stride;
+  const int ns = sa.ns, nl = sa.nl;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 4;        // k-group for the operands; head g for the output
   const int nn = lane & 15;        // token inside a 16-token block; limb row for A
-  const int tile_begin = blockIdx.x * (kTokWG / 64) + wave * kTilesPerWave;
+  const int tile_begin = chunk * (kTokWG / 64) + wave * kTilesPerWave;
   const int ntile_total = (Lmax + 63) / 64;
   const int8_t* cb = codes + (long)kvr * Lmax * RQ;
   // every code of the wave's tiles in flight at once (addresses clamped to the last token;
@@ -75,7 +88,7 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
       b_op[t][b] = __builtin_nontemporal_load(
           reinterpret_cast<const long*>(cb + (long)min(tok, Lmax - 1) * RQ + kg * 8));
     }
-  const int n = *n_dev;
+  const int n = *sa.n_dev;
   const int dead_hi = n - nl;      // positions >= dead_hi are local or not yet written
   const long a_op = *reinterpret_cast<const long*>(limbs + (long)kvr * 16 * RQ + nn * RQ + kg * 8);
   const int row = kvr * GQ + kg;
@@ -132,8 +145,36 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(
   oa::lds_barrier();
   if (threadIdx.x < GQ * kTB) {
     const int g = threadIdx.x / kTB;
-    const int tile = blockIdx.x * kTB + threadIdx.x % kTB;
+    const int tile = chunk * kTB + threadIdx.x % kTB;
     if (tile < ntile_total) TM[(long)(kvr * GQ + g) * tm_stride + tile] = s_tm[g][threadIdx.x % kTB];
+  }
+}
+
+template <bool HEADS>
+__global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(ScanArgs sa) {
+  scan_block<HEADS>(sa, blockIdx.x, blockIdx.y);
+}
+
+// The scan over heads and the pooled part of the ErrorGate in one launch: n_scan blocks of
+// scan_block<true> (chunk-fastest order, as qgs_scan_kernel's grid) and n_gate blocks of
+// gate_pooled_unit (row r, clusters 16 u .. 16 u + 15), spread evenly through the block order
+// so that the gate's short dependent chains run under the scan's code stream.  Both read state
+// the index update left (codes, limbs; Sk, Sk2, n) and write disjoint outputs.
+__global__ void __launch_bounds__(kScanThreads) qgs_scan_gate_kernel(ScanArgs sa, oa_gate::GateArgs ga,
+                                                                     int nchunks, int n_scan, int n_gate) {
+  const long b = blockIdx.x;
+  const long tot = (long)n_scan + n_gate;
+  const long g0 = b * n_gate / tot;
+  const long g1 = (b + 1) * n_gate / tot;
+  if (g1 > g0) {                                    // uniform: gate unit g0
+    __shared__ float s_zb[oa_gate::kPoolClusters], s_s2[oa_gate::kPoolClusters],
+        s_nt[oa_gate::kPoolClusters];
+    const int units = (ga.C + oa_gate::kPoolClusters - 1) / oa_gate::kPoolClusters;
+    const int row = (int)(g0 / units);
+    oa_gate::gate_pooled_unit(ga, row, (int)(g0 % units) * oa_gate::kPoolClusters, s_zb, s_s2, s_nt);
+  } else {
+    const long si = b - g0;                         // scan blocks before this one
+    scan_block<true>(sa, (int)(si % nchunks), (int)(si / nchunks));
   }
 }
 
@@ -332,8 +373,8 @@ int launch_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8
   const int ntile = (Lmax + 63) / 64;
   if (s_stride < (long)ntile * 64 || tm_stride < ntile || ns < 0 || nl < 0) return OA_EINVAL;
   dim3 grid((Lmax + kTokWG - 1) / kTokWG, kv_rows);
-  hipLaunchKernelGGL(qgs_scan_kernel<HEADS>, grid, dim3(kScanThreads), 0, (hipStream_t)stream,
-                     codes, Lmax, limbs, fexp, S, s_stride, TM, tm_stride, n_dev, ns, nl);
+  const ScanArgs sa{codes, Lmax, limbs, fexp, S, s_stride, TM, tm_stride, n_dev, ns, nl};
+  hipLaunchKernelGGL(qgs_scan_kernel<HEADS>, grid, dim3(kScanThreads), 0, (hipStream_t)stream, sa);
   return OA_LAUNCH_STATUS();
 }
 
@@ -401,4 +442,32 @@ extern "C" int oa_topk_select_heads(uint16_t* H, long h_stride, const float* TM,
     return OA_EINVAL;
   return launch_topk<true>(H, h_stride, TM, tm_stride, rows, ntiles, sel, sel_stride, n_dev, ns,
                            nl, k_top, Rescore{codes, (long)Lmax, limbs, fexp}, stream);
+}
+
+extern "C" int oa_qgs_scan_gate(const int8_t* codes, int kv_rows, int Lmax, int rank,
+                                const int8_t* limbs, const int* fexp, uint16_t* H, long h_stride,
+                                float* TM, long tm_stride, const int* n_dev, int ns, int nl,
+                                const void* q, long q_stride, const float* Sk, const float* Sk2,
+                                const float* nb, int C, float sm_scale, float sm_scale_sq,
+                                float* score, float* n_t, float* qsk, void* stream) {
+  if (!H || (reinterpret_cast<uintptr_t>(H) & 7) || h_stride % 4 || rank != RQ || kv_rows <= 0 ||
+      Lmax <= 0 || !q || !Sk || !Sk2 || !nb || !score || !n_t || C <= 0 || C > 256)
+    return OA_EINVAL;
+  const int ntile = (Lmax + 63) / 64;
+  if (h_stride < (long)ntile * 64 || tm_stride < ntile || ns < 0 || nl < 0) return OA_EINVAL;
+  const ScanArgs sa{codes, Lmax, limbs, fexp, H, h_stride, TM, tm_stride, n_dev, ns, nl};
+  oa_gate::GateArgs ga{};
+  ga.q = (const uint16_t*)q; ga.q_stride = q_stride;
+  ga.Sk = Sk; ga.Sk2 = Sk2; ga.st_stride_r = (long)C * OA_D;
+  ga.nb = nb; ga.nb_stride = C;
+  ga.score = score; ga.n_t = n_t; ga.out_stride = C; ga.qsk = qsk;
+  ga.C = C; ga.sc = sm_scale; ga.sc2 = sm_scale_sq;
+  const int rows = kv_rows * GQ;
+  const int nchunks = (Lmax + kTokWG - 1) / kTokWG;
+  const long n_scan = (long)nchunks * kv_rows;
+  const long n_gate = (long)rows * ((C + oa_gate::kPoolClusters - 1) / oa_gate::kPoolClusters);
+  if (n_scan + n_gate > 0x7fffffffL) return OA_EINVAL;
+  hipLaunchKernelGGL(qgs_scan_gate_kernel, dim3((unsigned)(n_scan + n_gate)), dim3(kScanThreads), 0,
+                     (hipStream_t)stream, sa, ga, nchunks, (int)n_scan, (int)n_gate);
+  return OA_LAUNCH_STATUS();
 }

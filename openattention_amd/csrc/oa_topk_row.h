@@ -53,12 +53,13 @@ __device__ __forceinline__ double load_limbs(const Rescore& rs, int row, int* lw
 // Lane l keeps the keys of tiles l, l+64, ... and later of column l of the k chosen tiles in
 // registers; every extraction step is one wave maximum (DPP) and an in-register update by the
 // owning lane.  Writes sel = [0..ns) ++ [n-nl..n) ++ top and marks the selected scores.
+// lds_sel, when not null, receives the same sel row (for the rest of the workgroup).
 template <int TPL, int KR, bool HEADS>
 __device__ __forceinline__ void topk_reg_row(void* __restrict__ Sv, long s_stride,
                                              const float* __restrict__ TM, long tm_stride,
                                              int ntiles, int32_t* __restrict__ sel, long sel_stride,
                                              int n, int ns, int nl, int k_top, const Rescore& rs,
-                                             int row, int lane) {
+                                             int row, int lane, int32_t* lds_sel = nullptr) {
   int lw[HEADS ? 32 : 1];
   const double inv = load_limbs<HEADS>(rs, row, lw);
   unsigned long long tk[TPL];
@@ -156,6 +157,11 @@ __device__ __forceinline__ void topk_reg_row(void* __restrict__ Sv, long s_strid
   if (lane < k_top) {
     sr[ns + nl + lane] = my_pos;
     mark_selected<HEADS>(Sv, s_stride, row, my_pos);
+  }
+  if (lds_sel) {
+    if (lane < ns) lds_sel[lane] = lane;
+    if (lane < nl) lds_sel[ns + lane] = n - nl + lane;
+    if (lane < k_top) lds_sel[ns + nl + lane] = my_pos;
   }
 }
 

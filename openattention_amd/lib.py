@@ -41,6 +41,9 @@ SIGNATURES = {
     "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P, P],
     "oa_topk_gate_fill": [P, L, P, L, I, P, I, I, I, P, I, P, P, P, L, P, L, L, I, I, I, P, L, P, L,
                           P, P, P, I, F, F, I, P, P, P, P, P],
+    "oa_qgs_scan_gate": [P, I, I, I, P, P, P, L, P, L, P, I, I, P, L, P, P, P, I, F, F, P, P, P, P],
+    "oa_topk_fix_fill": [P, L, P, L, I, P, I, I, I, P, I, P, P, P, L, P, L, L, I, I, I, P, L, P, L,
+                         P, P, P, I, F, F, I, P, P, P, P],
     "oa_waterfill": [P, P, I, I, I, P, P],
     "oa_topq": [P, L, P, L, P, I, I, I, P, I, P, P],
     "oa_topq_path": [P, L, P, L, P, I, I, I, P, I, P, I, P],
@@ -58,7 +61,7 @@ SIGNATURES = {
 
 # must equal oa_abi_version() of the loaded library (OA_ABI_VERSION in the header): a library
 # built from sources with other argument lists would be handed wrong pointers
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _LIB = None
 

@@ -27,7 +27,6 @@ G = HQ // HKV
 SC = D ** -0.5
 RMAX = 256
 SCAN_TILE = 64
-FUSE_ROWS = 256      # below this many query-head rows: top-k, gate and fill in one launch
 
 
 class Ctx:
@@ -119,8 +118,17 @@ class OursHIP(Method):
 
     def __init__(self, a, B, Lmax, dev, n_layers: int = NL, static: dict | None = None,
                  ctx_len: int = CTX_LEN, rule: str = "multibin", fused: bool = True,
-                 groups: int = 1, c_max: int = 256, out_dtype: torch.dtype = torch.bfloat16):
+                 groups: int = 1, c_max: int = 256, out_dtype: torch.dtype = torch.bfloat16,
+                 gate_mode: str = "fused"):
         super().__init__(a, B, Lmax, dev)
+        # how the top-k, ErrorGate and water-fill are launched (the results are the same):
+        #   "fused": one launch after the scan (each row's top-k beside its pooled ErrorGate, then
+        #            the selected tokens' correction and the fill);
+        #   "split": the pooled ErrorGate in the scan's launch, then top-k + correction + fill;
+        #   "separate": top-k, then ErrorGate and fill
+        if gate_mode not in ("fused", "split", "separate"):
+            raise ValueError(f"gate_mode must be 'fused', 'split' or 'separate', got {gate_mode!r}")
+        self.gate_mode = gate_mode
         if out_dtype not in (torch.bfloat16, torch.float32):
             raise ValueError("out_dtype must be torch.bfloat16 or torch.float32")
         if groups < 1 or B % groups:
@@ -158,6 +166,7 @@ class OursHIP(Method):
         self.out = torch.empty(R, D, device=dev, dtype=out_dtype)
         self._sel = {}
         self._pending = {}          # layer -> {batch row: (question rows, T, K, V)} awaiting build
+        self.build_events = None    # a list: (start, end) events around every layer's build
         if not fused:
             self.kbar_r = torch.empty(R, self.Cn, D, device=dev, dtype=torch.bfloat16)
             self.vbar_r = torch.empty(R, self.Cn, D, device=dev, dtype=torch.bfloat16)
@@ -186,6 +195,16 @@ class OursHIP(Method):
         pend = self._pending.pop(l, {})
         if not pend:
             return
+        if self.build_events is not None:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+        self._build_rows_of(l, pend)
+        if self.build_events is not None:
+            e1 = torch.cuda.Event(enable_timing=True)
+            e1.record()
+            self.build_events.append((e0, e1))
+
+    def _build_rows_of(self, l, pend):
         scal = float(self.static.get("attention_scaling", 1.0))
         M, inv = self.static["M"][l], self.static["inv_freq"]
         rows = sorted(pend)
@@ -252,19 +271,29 @@ class OursHIP(Method):
             out.append(("index_prep", lambda: ops.index_prep(K, V, st, n_dev, RMAX, qr, self.limbs, self.fexp)))
         else:
             out.append(("qgs_prep", lambda: ops.qgs_prep(qr, st.U, st.scale, self.limbs, self.fexp)))
-        out.append(("qgs_scan", lambda: ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM,
-                                                           n_dev, ns, nl)))
-        if self.R < FUSE_ROWS:
-            # fewer rows than compute units: each row's top-k, gate and fill in one workgroup
-            out.append(("topk_gate_fill", lambda: ops.topk_gate_fill(
-                self.H, self.TM, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp, qr, K, st.asg,
-                sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E, qsk=self.qsk)))
+        if self.gate_mode == "split":
+            # the pooled ErrorGate with the scan, the selected tokens' correction with the top-k
+            # and the fill
+            out.append(("qgs_scan_gate", lambda: ops.qgs_scan_gate(
+                st.codes, self.limbs, self.fexp, self.H, self.TM, n_dev, ns, nl, qr, st.Sk, st.Sk2, st.nb,
+                self.score, self.n_t, sc, qsk=self.qsk)))
+            out.append(("topk_fix_fill", lambda: ops.topk_fix_fill(
+                self.H, self.TM, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp, qr, K, st.asg, sel,
+                st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E)))
         else:
-            out.append(("topk_select", lambda: ops.topk_select_heads(
-                self.H, self.TM, sel, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp)))
-            out.append(("gate_fill", lambda: ops.gate_fill(
-                qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E,
-                qsk=self.qsk)))
+            out.append(("qgs_scan", lambda: ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM,
+                                                               n_dev, ns, nl)))
+            if self.gate_mode == "fused":
+                # each row's top-k beside its pooled ErrorGate, then the correction and the fill
+                out.append(("topk_gate_fill", lambda: ops.topk_gate_fill(
+                    self.H, self.TM, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp, qr, K, st.asg,
+                    sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E, qsk=self.qsk)))
+            else:
+                out.append(("topk_select", lambda: ops.topk_select_heads(
+                    self.H, self.TM, sel, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp)))
+                out.append(("gate_fill", lambda: ops.gate_fill(
+                    qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E,
+                    qsk=self.qsk)))
         out.append(("topq", lambda: ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, n_dev, st.codes,
                                                    self.limbs, self.fexp, self.S)))
         if self.fused:

@@ -325,8 +325,8 @@ def gate_fill(q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota, sm_scale: float, E
 def topk_gate_fill(H, TM, n_dev, ns: int, nl: int, k_top: int, codes, limbs, fexp, q, K, asg, sel,
                    Sk, Sk2, nb, score, n_t, quota, sm_scale: float, E: int, qsk=None) -> None:
     """topk_select_heads then gate_fill (the same sel, marked heads, score, n_t, quota, qsk); one
-    launch below 256 rows when the row fits the register top-k.  sel has ns + nl + k_top
-    columns."""
+    launch when the row fits the register top-k (its pooled ErrorGate computed while the top-k
+    runs, then the selected tokens' correction and the fill).  sel has ns + nl + k_top columns."""
     dev = _dev(H, TM, n_dev, codes, limbs, fexp, q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota)
     R, C = nb.shape
     BH, Lmax, _ = codes.shape
@@ -350,6 +350,60 @@ def topk_gate_fill(H, TM, n_dev, ns: int, nl: int, k_top: int, codes, limbs, fex
              asg.stride(0), _ptr(sel), sel.stride(0), _ptr(Sk), _ptr(Sk2), _ptr(nb), C,
              float(sm_scale), float(sm_scale) * float(sm_scale), int(E), _ptr(score), _ptr(n_t),
              _ptr(quota), _ptr(qsk), _stream(dev))
+
+
+def qgs_scan_gate(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int, q, Sk, Sk2, nb, score, n_t,
+                  sm_scale: float, qsk=None) -> None:
+    """qgs_scan_heads and the pooled part of the ErrorGate in one launch: score, n_t (rows, C)
+    of every cluster as if it held no selected token, and q . Sk_c into qsk."""
+    dev = _dev(codes, limbs, fexp, H, TM, n_dev, q, Sk, Sk2, nb, score, n_t)
+    BH, Lmax, rq = codes.shape
+    R, C = nb.shape
+    _chk(codes, "codes", torch.int8, (BH, Lmax, RANK_Q), contiguous=True)
+    _chk(H, "H", torch.int16, (GROUP * BH, -Lmax))
+    _chk(TM, "TM", torch.float32, (GROUP * BH, None))
+    _chk(limbs, "limbs", torch.int8, (BH, 16, RANK_Q), contiguous=True)
+    _chk(fexp, "fexp", torch.int32, (GROUP * BH,), contiguous=True)
+    _chk(n_dev, "n_dev", torch.int32)
+    _chk(q, "q", torch.bfloat16, (R, HEAD_DIM))
+    _need(R == GROUP * BH, "nb must have one row per query-head row")
+    _stats(R, C, (Sk, "Sk"), (Sk2, "Sk2"))
+    for t, name in ((nb, "nb"), (score, "score"), (n_t, "n_t")):
+        _chk(t, name, torch.float32, (R, C), contiguous=True)
+    if qsk is not None and (qsk.shape != (R, C) or qsk.dtype != torch.float32 or not qsk.is_contiguous()):
+        raise ValueError("qsk must be a contiguous (rows, C) float32 tensor")
+    lib.call("oa_qgs_scan_gate", _ptr(codes), BH, Lmax, rq, _ptr(limbs), _ptr(fexp), _ptr(H), H.stride(0),
+             _ptr(TM), TM.stride(0), _ptr(n_dev), ns, nl, _ptr(q), q.stride(0), _ptr(Sk), _ptr(Sk2), _ptr(nb),
+             C, float(sm_scale), float(sm_scale) * float(sm_scale), _ptr(score), _ptr(n_t), _ptr(qsk),
+             _stream(dev))
+
+
+def topk_fix_fill(H, TM, n_dev, ns: int, nl: int, k_top: int, codes, limbs, fexp, q, K, asg, sel, Sk,
+                  Sk2, nb, score, n_t, quota, sm_scale: float, E: int) -> None:
+    """After qgs_scan_gate: the top-k over the heads, the ErrorGate of the clusters holding a
+    selected token done again (score, n_t updated in place), the water-fill.  The same sel,
+    marked heads, score, n_t and quota as topk_select_heads followed by gate_fill."""
+    dev = _dev(H, TM, n_dev, codes, limbs, fexp, q, K, asg, sel, Sk, Sk2, nb, score, n_t, quota)
+    R, C = nb.shape
+    BH, Lmax, _ = codes.shape
+    _chk(H, "H", torch.int16, (R, -Lmax))
+    _chk(TM, "TM", torch.float32, (R, None))
+    _chk(codes, "codes", torch.int8, (BH, Lmax, RANK_Q), contiguous=True)
+    _chk(limbs, "limbs", torch.int8, (BH, 16, RANK_Q), contiguous=True)
+    _chk(fexp, "fexp", torch.int32, (R,), contiguous=True)
+    _chk(q, "q", torch.bfloat16, (R, HEAD_DIM))
+    _chk(K, "K", torch.bfloat16, (K.shape[0], None, HEAD_DIM))
+    _chk(asg, "asg", torch.int32, (R, None))
+    _chk(sel, "sel", torch.int32, (R, ns + nl + k_top))
+    _stats(R, C, (Sk, "Sk"), (Sk2, "Sk2"))
+    for t, name in ((nb, "nb"), (score, "score"), (n_t, "n_t"), (quota, "quota")):
+        _chk(t, name, torch.float32, (R, C), contiguous=True)
+    lib.call("oa_topk_fix_fill", _ptr(H), H.stride(0), _ptr(TM), TM.stride(0), TM.shape[1],
+             _ptr(n_dev), ns, nl, k_top, _ptr(codes), Lmax, _ptr(limbs), _ptr(fexp), _ptr(q),
+             q.stride(0), _ptr(K), K.stride(0), K.stride(1), R, K.shape[0], q.shape[1], _ptr(asg),
+             asg.stride(0), _ptr(sel), sel.stride(0), _ptr(Sk), _ptr(Sk2), _ptr(nb), C,
+             float(sm_scale), float(sm_scale) * float(sm_scale), int(E), _ptr(score), _ptr(n_t),
+             _ptr(quota), _stream(dev))
 
 
 def waterfill(score, n_t, quota, E: int) -> None:

@@ -1087,3 +1087,65 @@ def test_model_step_graph_replay_matches_eager():
         assert torch.equal(model.method.st[l].Sk, e_state[l][1])
         assert torch.equal(model.method.st[l].asg, e_state[l][2])
     assert int(CTX.n_dev) == N + 3
+
+
+@pytest.mark.parametrize("B,N,rho", [(1, 32768, 0.01), (32, 32768, 0.01), (2, 32768, 0.03),
+                                     (2, 32768, 0.10), (1, 131072, 0.01), (1, 131072, 0.03)])
+def test_split_gate_equals_whole_gate(B, N, rho):
+    """The three launch layouts of top-k, ErrorGate and water-fill from one index update:
+    oa_qgs_scan_heads + oa_topk_select_heads + oa_gate_fill ("whole"); oa_qgs_scan_gate +
+    oa_topk_fix_fill (the pooled ErrorGate in the scan launch, the selected tokens' correction
+    with the top-k and the fill: "split"); oa_qgs_scan_heads + oa_topk_gate_fill (each row's top-k
+    beside its pooled ErrorGate in one workgroup: "fused").  Key heads, tile maxima, sel, marked
+    heads, ErrorGate scores, tail counts, quotas and q . Sk agree bit for bit.  Covers 1 to 4
+    cluster slots per lane (C = 64, 192, 256), the register top-k over up to 2048 tiles, the
+    radix top-k with the separate launches, and both workgroup widths of the fused launch."""
+    bud = budget(rho, ctx_len=N, c_max=256)
+    n = N
+    ns, nl, k = bud.counts(n)
+    E, C = bud.E, bud.C
+    print(f"[case] split gate B={B} N={N} rho={rho} C={C} E={E} k={k}", flush=True)
+    lay = build_layer(cfg=3 if N == 32768 else 4, B=B, N=N, Lmax=N + 64, C=C,
+                      n_centers=256 if N == 32768 else 512, dev=DEV)
+    R, BH = B * HQ, B * HKV
+    st = lay.st
+    K = lay.K.reshape(BH, lay.Lmax, D)
+    V = lay.V.reshape(BH, lay.Lmax, D)
+    qr = lay.q.reshape(R, D).contiguous()
+    limbs = torch.zeros(BH, 16, 32, device=DEV, dtype=torch.int8)
+    fexp = torch.zeros(R, device=DEV, dtype=torch.int32)
+    n_dev = torch.tensor([n], device=DEV, dtype=torch.int32)
+    ops.index_prep(K, V, st, n_dev, RMAX, qr, limbs, fexp)
+    ntiles = -(-lay.Lmax // 64)
+    res = {}
+    for mode in ("whole", "split", "fused"):
+        H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
+        TM = torch.empty(R, ntiles, device=DEV)
+        sel = torch.full((R, ns + nl + k), -7, device=DEV, dtype=torch.int32)
+        score, n_t, quota, qsk = (torch.full((R, C), float("nan"), device=DEV) for _ in range(4))
+        if mode == "whole":
+            ops.qgs_scan_heads(st.codes, limbs, fexp, H, TM, n_dev, ns, nl)
+            H0 = H.clone()
+            ops.topk_select_heads(H, TM, sel, n_dev, ns, nl, k, st.codes, limbs, fexp)
+            ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score, n_t, quota, SC, E, qsk=qsk)
+        elif mode == "split":
+            ops.qgs_scan_gate(st.codes, limbs, fexp, H, TM, n_dev, ns, nl, qr, st.Sk, st.Sk2, st.nb, score, n_t,
+                              SC, qsk=qsk)
+            H0 = H.clone()
+            ops.topk_fix_fill(H, TM, n_dev, ns, nl, k, st.codes, limbs, fexp, qr, K, st.asg, sel, st.Sk, st.Sk2,
+                              st.nb, score, n_t, quota, SC, E)
+        else:
+            ops.qgs_scan_heads(st.codes, limbs, fexp, H, TM, n_dev, ns, nl)
+            H0 = H.clone()
+            ops.topk_gate_fill(H, TM, n_dev, ns, nl, k, st.codes, limbs, fexp, qr, K, st.asg, sel, st.Sk, st.Sk2,
+                               st.nb, score, n_t, quota, SC, E, qsk=qsk)
+        torch.cuda.synchronize()
+        res[mode] = {name: t.cpu().numpy() for name, t in (("H0", H0), ("H", H), ("TM", TM), ("sel", sel),
+                                                            ("score", score), ("n_t", n_t), ("quota", quota),
+                                                            ("qsk", qsk))}
+    for other in ("split", "fused"):
+        for name in ("H0", "H", "TM", "sel", "score", "n_t", "quota", "qsk"):
+            a, b = res["whole"][name], res[other][name]
+            assert np.array_equal(a, b, equal_nan=False), f"{other}: {name} differs"
+    hits = (res["split"]["sel"] >= 0).sum()
+    print(f"  bit-exact over {R} rows ({hits} selected tokens)", flush=True)
