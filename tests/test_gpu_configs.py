@@ -111,3 +111,22 @@ def test_config4_n131072_matches_oracle(rho):
             got = ex.cpu().numpy()[:, :bud.E]
             bad = np.nonzero((got != ref["exp_idx"]).any(1))[0]
             assert bad.size == 0, f"key-prefix top-q, repeat {rep}: rows {bad} differ"
+
+
+@pytest.mark.parametrize("N,rho", [(65536, 0.03), (131072, 0.01)])
+def test_config4_batch8_matches_oracle(N, rho):
+    """Config 4 at its own batch, B = 8 (256 query-head rows: the two-launch ErrorGate path and the
+    full-batch top-q), 512-centre mixture with 8 needles per KV head: one decode step of every
+    sequence; sequences 0 and 7 restated on the CPU, selection bit-exact, outputs within 2e-2
+    (bf16) and 1e-3 (fp32 rows)."""
+    B = 8
+    bud = budget(rho, ctx_len=N, c_max=256)
+    print(f"[case] config4 B={B} N={N} rho={rho} C={bud.C} E={bud.E}", flush=True)
+    lay = build_layer(cfg=4, B=B, N=N, Lmax=N + 64, C=bud.C, n_centers=512, dev=DEV, needles=8)
+    pres = {b: seq_state_np(lay.st, lay.K, lay.V, b) for b in (0, 7)}
+    res = _decode_both_dtypes(lay.st, lay.K, lay.V, lay.q, rho, N, lay.Lmax, B, lay.static)
+    ns, nl, k = res[torch.bfloat16]["counts"]
+    for b, pre in pres.items():
+        ref = O.decode_step(pre, bf16_np(lay.q[b].reshape(-1, D)), N, ns, nl, k, bud.E, G, np.float32(SC),
+                            np.float32(SC2), rmax=RMAX)
+        _check_rows(res, ref, slice(b * HQ, (b + 1) * HQ), f"N={N} b={b}")

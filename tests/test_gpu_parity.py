@@ -77,6 +77,38 @@ def test_flash_vs_oracle(proxy_per_kv, kb_dtype, n_split, out_dtype):
     assert rel.max() < (1e-3 if out_dtype == torch.float32 else BF16_TOL)
 
 
+def test_decode_expand_attention_surface():
+    """ops.decode_expand_attention with the reference's call shape (triton_expand_decode.py:139-165):
+    proxies per KV head, sm_scale defaulting to D**-0.5, the Triton tuning arguments accepted and
+    ignored (two different settings give the same output), -1 / -inf entries no-ops; against the
+    fp64 restatement within 2e-2 (bf16 rows)."""
+    print("[case] decode_expand_attention", flush=True)
+    g = torch.Generator().manual_seed(11)
+    B, Lmax, Cn, Ns, Ne = 2, 2048, 32, 15, 96
+    R, BH = B * HQ, B * HKV
+    k = torch.randn(BH, Lmax, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(BH, Lmax, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(R, D, generator=g).to(torch.bfloat16)
+    perm = torch.stack([torch.randperm(Lmax, generator=g) for _ in range(R)])
+    sel, ex = perm[:, :Ns].int(), perm[:, Ns:Ns + Ne].int().clone()
+    ex[:, -5:] = -1
+    kb = torch.randn(BH, Cn, D, generator=g).to(torch.bfloat16)
+    vb = torch.randn(BH, Cn, D, generator=g).to(torch.bfloat16)
+    ln = torch.rand(R, Cn, generator=g) * 4
+    ln[:, ::7] = -math.inf
+    args = [t.to(DEV) for t in (q, k, v, sel, ex, kb, vb, ln)]
+    out1 = ops.decode_expand_attention(*args)
+    out2 = ops.decode_expand_attention(*args, sm_scale=D ** -0.5, block_n=32, block_b=128, num_warps=8)
+    torch.cuda.synchronize()
+    assert out1.shape == (R, D) and out1.dtype == torch.bfloat16
+    assert torch.equal(out1, out2)
+    ref = O.flash(bf16_np(q), bf16_np(k), bf16_np(v), sel.numpy(), ex.numpy(), kb.double().numpy(),
+                  vb.double().numpy(), ln.double().numpy(), HQ // HKV, SC, proxy_per_kv=True)
+    rel = rel_rows(out1.float().cpu().numpy(), ref)
+    print(f"  decode_expand_attention rel err max {rel.max():.2e}", flush=True)
+    assert rel.max() < BF16_TOL
+
+
 def test_ours_flash_nb_zero_is_plain_sparse_softmax():
     print("[case] ours_flash nb=0", flush=True)
     from openattention_amd import ours_flash
