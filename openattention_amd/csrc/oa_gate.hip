@@ -890,13 +890,15 @@ extern "C" int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, lo
   const int nsl = (C + 63) / 64;
   hipStream_t s = (hipStream_t)stream;
   const double bd = (double)budget;
-  // below kFuseRows rows every row is resident anyway: eight waves per row (seven on the pooled
-  // gate); above, four, so that every row of a B = 32 batch stays resident
-  const bool wide = rows < kFuseRows;
+  // waves per row: every row stays resident (4 at B = 32); with few rows, enough waves that each
+  // takes one batch of kPoolBatch clusters (16 up to 64 rows, 8 up to kFuseRows)
+  const int wv = rows <= 64 ? 16 : rows < kFuseRows ? 8 : 4;
   const dim3 g(rows);
 #define OA_TG2(NS, T, KK)                                                                       \
   do {                                                                                          \
-    if (wide)                                                                                   \
+    if (wv == 16)                                                                               \
+      hipLaunchKernelGGL((topk_gate2_fill_kernel<NS, T, KK, 16>), g, dim3(1024), lds, s, t, a, sel, quota, bd); \
+    else if (wv == 8)                                                                           \
       hipLaunchKernelGGL((topk_gate2_fill_kernel<NS, T, KK, 8>), g, dim3(512), lds, s, t, a, sel, quota, bd); \
     else                                                                                        \
       hipLaunchKernelGGL((topk_gate2_fill_kernel<NS, T, KK, 4>), g, dim3(256), lds, s, t, a, sel, quota, bd); \
