@@ -223,10 +223,11 @@ int oa_gate_fill(const void* q, long q_stride, const void* K, long k_stride_b, l
 /*
  * oa_topk_select_heads followed by oa_gate_fill (n_sel = ns + nl + k_top, sel written as by
  * oa_topk_select_heads): the same sel, marked heads, score, n_t, quota and qsk.  With a register
- * top-k (k_top <= 16 and at most 2048 score tiles) it is one launch: each row's workgroup runs
- * its top-k on one wave while its other waves compute every cluster's ErrorGate from the pooled
- * sums, then the clusters holding a selected token are computed again without those tokens
- * (the same arithmetic) and the row's water-fill runs; otherwise the two calls.
+ * top-k (k_top <= 16 and at most 2048 score tiles), and below 256 rows or at C <= 64, it is one
+ * launch: each row's workgroup runs its top-k on one wave while its other waves compute every
+ * cluster's ErrorGate from the pooled sums, then the clusters holding a selected token are
+ * computed again without those tokens (the same arithmetic) and the row's water-fill runs;
+ * otherwise the two calls.
  * Replaces the consecutive _k_select and _k_errorgate / _k_waterfill steps of the deployed decode
  * graph (inference/graph_runner.py:123-159, inference/ours_fused.py:122-216); the fusion itself
  * has no counterpart in the reference.

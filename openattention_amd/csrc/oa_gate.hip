@@ -855,8 +855,11 @@ extern "C" int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, lo
   const int n_sel = ns + nl + k_top;
   const int tpl = (ntiles + 63) / 64;
   const int reg = (k_top <= 9 && tpl <= 9) ? 1 : (k_top <= 16 && tpl <= 16) ? 2 : (k_top <= 16 && tpl <= 32) ? 3 : 0;
-  if (!reg) {
-    // two launches: the radix top-k the row length needs, then the gate and fill
+  // one launch needs the register top-k; at kFuseRows rows or more also a single cluster slot per
+  // lane (C <= 64): the fill's slots take 130-214 VGPRs at C = 65..256, which would leave half of
+  // a B = 32 batch's rows waiting for a workgroup slot (measured slower than two launches)
+  if (!reg || (rows >= kFuseRows && C > 64)) {
+    // two launches: the top-k the row needs, then the gate and fill
     int st = oa_topk_select_heads(H, h_stride, TM, tm_stride, rows, ntiles, sel, sel_stride, n_dev,
                                   ns, nl, k_top, codes, kv_rows, Lmax, limbs, fexp, stream);
     if (st) return st;
