@@ -68,6 +68,7 @@ constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster w
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int kSmallRows = 256;               // below: oa_topq_heads path 0 in one launch
 constexpr int32_t kRowMarked = -2;              // exp_idx[row][0] of a row left to the key-prefix kernel
+constexpr int kRowGrid = 256;                   // key-prefix kernel over marked rows: one workgroup per unit
 
 enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3, kModeSplit = 4 };
 
@@ -82,6 +83,7 @@ struct TopqArgs {
   int gcap;        // staged-key capacity (u64 entries)
   int cpow;        // power of two >= E: chosen-word list and the P6 sort
   int marked_only; // key-prefix kernel: only rows the linear-bin kernel marked kRowMarked
+  int rows;        // rows of the launch (the marked-only grid walks them)
   // linear-bin kernel over 16-bit key heads (oa_topq_heads): the head rows, and what recomputes
   // exact scores (the staged members', and a whole row into S32 when it is left to the
   // key-prefix kernel, which then reads S32 as its S)
@@ -434,14 +436,17 @@ __device__ __forceinline__ void topq_row_body(const TopqArgs& a, int row, unsign
   int* s_out = s_hist;                                                        // after P5
   uint32_t* s_cst = reinterpret_cast<uint32_t*>(s_hist + a.hwords);           // cpow
 
-  const int tid = threadIdx.x;
+  // an opaque copy of the thread index: in topq_marked_kernel's row loop, nothing derived from it
+  // is hoisted out of the loop to stay live across the body (that spills at the register cap)
+  int tid_v = (int)threadIdx.x;
+  asm volatile("" : "+v"(tid_v));
+  const int tid = tid_v;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int C = a.C, E = a.E;
   constexpr int sh1 = 32 - LB;
   constexpr int sh1p = sh1 + sb;          // shift giving a level-1 bin's pad-word count
   const int trash = C * HS + lane;        // per-lane histogram slot for non-members
-  if (a.marked_only && a.exp_idx[(long)row * E] != kRowMarked) return;   // uniform
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
   const uint8_t* arow = a.asg8 + (long)row * a.a_stride;
@@ -819,6 +824,36 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
   topq_row_body<PPT, LB>(a, blockIdx.x, dyn);
 }
 
+// After the linear-bin kernel: a grid of at most kRowGrid workgroups runs the rows it marked
+// (usually none), so an empty pass dispatches one workgroup per unit, not one per row.  Wave 0
+// reads the marks of 64 of the workgroup's rows (blockIdx.x + j * gridDim.x) at once; their
+// ballot reaches every wave through LDS.
+template <int PPT, int LB>
+__global__ void __launch_bounds__(kThreads) topq_marked_kernel(TopqArgs a) {
+  extern __shared__ unsigned long long dyn[];
+  __shared__ unsigned long long s_marks;
+  bool ran = false;
+  for (int base = 0; base < a.rows; base += 64 * gridDim.x) {
+    if (threadIdx.x < 64) {
+      const int row = base + blockIdx.x + (int)threadIdx.x * gridDim.x;
+      const unsigned long long m = __ballot(row < a.rows && a.exp_idx[(long)row * a.E] == kRowMarked);
+      if (threadIdx.x == 0) s_marks = m;
+    }
+    __syncthreads();
+    // uniform (read at full exec): the rows and their pointers stay in scalar registers
+    const unsigned long long m = s_marks;
+    unsigned long long mk = ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(m >> 32)) << 32) |
+                            (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)m);
+    __syncthreads();                     // every wave holds the mask before the next batch's
+    while (mk) {
+      const int j = __ffsll((long long)mk) - 1;
+      mk &= mk - 1;
+      if (ran) __syncthreads();          // the previous row's LDS is dead before P0 reuses it
+      topq_row_body<PPT, LB>(a, base + blockIdx.x + j * gridDim.x, dyn);
+      ran = true;
+    }
+  }
+}
 
 // The linear-bin kernel: the common path.  Scores are binned linearly over the row's range of
 // qualifying scores, [smin, smax]: bin(s) = min(NB - 1, (int)((s - smin) * NB / (smax - smin)))
@@ -1140,10 +1175,13 @@ __global__ void __launch_bounds__(kThreads) topq_small_kernel(TopqArgs lin, Topq
 
 template <int PPT, int LB>
 int launch_row(const TopqArgs& a, int rows, size_t lds, hipStream_t s) {
-  const hipError_t e = hipFuncSetAttribute((const void*)topq_row_kernel<PPT, LB>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  const void* fn = a.marked_only ? (const void*)topq_marked_kernel<PPT, LB> : (const void*)topq_row_kernel<PPT, LB>;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((topq_row_kernel<PPT, LB>), dim3(rows), dim3(kThreads), lds, s, a);
+  if (a.marked_only)
+    hipLaunchKernelGGL((topq_marked_kernel<PPT, LB>), dim3(std::min(rows, kRowGrid)), dim3(kThreads), lds, s, a);
+  else
+    hipLaunchKernelGGL((topq_row_kernel<PPT, LB>), dim3(rows), dim3(kThreads), lds, s, a);
   return OA_LAUNCH_STATUS();
 }
 
@@ -1227,6 +1265,7 @@ int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool hea
   if (a.gcap < 64) return OA_EINVAL;
   const size_t lds = 8 * (size_t)(a.ucap + 64) + 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
   a.marked_only = 0;
+  a.rows = rows;
   if (lin) {
     // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words.
     // 7 bits for C <= 64, 6 for C <= 128, else 5: two workgroups' LDS fits one unit.  Rows

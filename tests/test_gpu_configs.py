@@ -31,8 +31,10 @@ def rel_rows(got, ref):
     return np.linalg.norm(got - ref, axis=-1) / np.maximum(np.linalg.norm(ref, axis=-1), 1e-30)
 
 
-def _decode_both_dtypes(st, K, V, q, rho, N, Lmax, B, static):
-    """One decode step from (clones of) st with bf16 and with fp32 output rows."""
+def _decode_both_dtypes(st, K, V, q, rho, N, Lmax, B, static, prefix_topq=False):
+    """One decode step from (clones of) st with bf16 and with fp32 output rows.  prefix_topq: after
+    the bf16 step, top-q again over the step's heads and quotas with every row left to the
+    key-prefix kernel (path 3), whose expanded sets land in res["exp_idx_prefix"]."""
     CTX.K, CTX.V = [K], [V]
     CTX.n_dev = torch.tensor([N], device=DEV, dtype=torch.int32)
     CTX.n0_dev = torch.tensor([N - 1], device=DEV, dtype=torch.int32)
@@ -46,6 +48,12 @@ def _decode_both_dtypes(st, K, V, q, rho, N, Lmax, B, static):
         res[dt] = dict(out=out.float().reshape(-1, D).cpu().numpy(), sel=m.last_sel.cpu().numpy(),
                        quota=m.quota.cpu().numpy(), exp_idx=m.exp_idx.cpu().numpy()[:, :m.E],
                        E=m.E, counts=m.bud.counts(N))
+        if prefix_topq and dt == torch.bfloat16:
+            ex = torch.full_like(m.exp_idx, 777)
+            ops.topq_heads(m.H, m.st[0].asg8, m.quota, ex, CTX.n_dev, m.st[0].codes, m.limbs, m.fexp, m.S,
+                           path=3)
+            torch.cuda.synchronize()
+            res["exp_idx_prefix"] = ex.cpu().numpy()[:, :m.E]
         del m
         torch.cuda.empty_cache()
     return res
@@ -76,8 +84,13 @@ def test_config3_batch32_matches_oracle(rho):
     torch.cuda.synchronize()
     seqs = (0, 15, 31)
     pre = {b: seq_state_np(st, K, V, b) for b in seqs}
-    res = _decode_both_dtypes(st, K, V, q, rho, N, Lmax, B, static)
+    res = _decode_both_dtypes(st, K, V, q, rho, N, Lmax, B, static, prefix_topq=rho in (0.01, 0.10))
     ns, nl, k = res[torch.bfloat16]["counts"]
+    if "exp_idx_prefix" in res:
+        # all 1024 rows through the key-prefix kernel (one workgroup per unit walking four rows
+        # each) equal the step's linear-bin top-q on every row
+        bad = np.nonzero((res["exp_idx_prefix"] != res[torch.bfloat16]["exp_idx"]).any(1))[0]
+        assert bad.size == 0, f"key-prefix top-q over every row: rows {bad[:8]} differ"
     for b in seqs:
         ref = O.decode_step(pre[b], bf16_np(q[b].reshape(-1, D)), N, ns, nl, k, bud.E, G, np.float32(SC),
                             np.float32(SC2), rmax=RMAX)
