@@ -93,13 +93,8 @@ struct TopqArgs {
   int force_mark;  // tests: every row is left to the key-prefix kernel
 };
 
-// the float whose order-preserving key is k (inverse of oa::float_key)
-__device__ __forceinline__ float key_float(uint32_t k) {
-  // k & 0x7fffffff for a key with its top bit set, ~k otherwise: ~(k ^ (m & 0x7fffffff)) with
-  // m the top bit spread over the word (one 3-input bit operation)
-  const uint32_t m = (uint32_t)((int32_t)k >> 31);
-  return __uint_as_float(~(k ^ (m & 0x7fffffffu)));
-}
+// the largest t = head - 0x7f of a finite float (head 0xff7f): the linear-bin kernel caps t here
+constexpr uint16_t kTopT = 0xff00;
 
 __device__ __forceinline__ unsigned long long key64(uint32_t key, int pos) {
   return ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (unsigned)pos);
@@ -211,6 +206,16 @@ __device__ void select_staged_loop(const unsigned long long* src, int cnt, int n
   }
 }
 
+// the float of the key head t + 0x7f (low 16 key bits 0): k & 0x7fffffff for a key with its top
+// bit set, ~k otherwise, as an arithmetic shift and one 3-input bit operation
+__device__ __forceinline__ float head_float(uint32_t t) {
+  uint32_t k = (t + oa::kNegInfHead) << 16;
+  asm("" : "+v"(k));      // one key feeds both operands (not a key and its complement)
+  uint32_t m = (uint32_t)((int32_t)k >> 31);
+  asm("" : "+v"(m));      // keeps the shift (not a compare and select) feeding the bit operation
+  return __uint_as_float(~(k ^ (m & 0x7fffffffu)));
+}
+
 // 16 threads (one DPP row) scan one padded histogram row of NB = 16 * BPT bins from the top:
 // thread j holds bins [j*BPT, (j+1)*BPT) in x[], ls = their sum, sfx = members in its bins and
 // all bins above (a suffix scan on row_shl DPP moves: lanes past the row's end read 0)
@@ -226,6 +231,24 @@ __device__ __forceinline__ void scan_row(const int* row, int j, RowScan<BPT>& r)
 #pragma unroll
   for (int b = 0; b < BPT; ++b) {
     r.x[b] = h[b];
+    r.ls += r.x[b];
+  }
+  int v = r.ls;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x101, 0xf, 0xf, false);   // row_shl:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x102, 0xf, 0xf, false);   // row_shl:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0xf, false);   // row_shl:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0xf, false);   // row_shl:8
+  r.sfx = v;
+}
+// the same over one of the linear-bin kernel's rows of 16 * BPT bins without pad words: thread j
+// holds bins [j*BPT, (j+1)*BPT); bin 0 (non-members) counts nothing
+template <int BPT>
+__device__ __forceinline__ void scan_row_dense(const int* row, int j, RowScan<BPT>& r) {
+  const int* h = row + j * BPT;
+  r.ls = 0;
+#pragma unroll
+  for (int b = 0; b < BPT; ++b) {
+    r.x[b] = (b == 0 && j == 0) ? 0 : h[b];
     r.ls += r.x[b];
   }
   int v = r.ls;
@@ -856,8 +879,9 @@ __global__ void __launch_bounds__(kThreads) topq_marked_kernel(TopqArgs a) {
 }
 
 // The linear-bin kernel: the common path.  Scores are binned linearly over the row's range of
-// qualifying scores, [smin, smax]: bin(s) = min(NB - 1, (int)((s - smin) * NB / (smax - smin)))
-// is non-decreasing in s, so a member in a higher bin beats every member in a lower one, and
+// qualifying (head-truncated) scores, [smin, smax]: bin(s) = 1 + (int)((s - smin) * (HS - 2) /
+// (smax - smin)), bin 0 for a position that is no member; any binning non-decreasing in s keeps
+// the selection exact, since a member in a higher bin beats every member in a lower one, and
 // the boundary bin of a cluster (the bin of its t-th best member) holds a handful of members
 // where the key-prefix bins hold hundreds.  One pass builds the per-cluster histograms (R, L1),
 // 16 threads per cluster find the boundary bins (T1), and one more pass over the registers (G)
@@ -885,10 +909,12 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   __shared__ int s_gused, s_fail;
   __shared__ uint32_t s_rlo[kWaves], s_rhi[kWaves];
   __shared__ int s_lw[HEADS ? 32 : 1];    // the row's limb words (exact scores)
+  // a cluster's histogram row holds HS = 2^LB + 16 bins: bin 0 counts the positions that are no
+  // member (ignored), a member's bin is 1 .. HS - 1; 16 threads scan a row, HS / 16 bins each
+  // (HS / 16 is odd, so the 16 threads' first bins lie in 16 different banks)
   constexpr int NB = 1 << LB;
   constexpr int HS = NB + 16;
-  constexpr int sb = LB - 4;
-  constexpr int bpt = NB >> 4;
+  constexpr int bpt = HS / 16;
   int* s_hist = reinterpret_cast<int*>(dyn);                                  // hwords
   unsigned long long* s_g = reinterpret_cast<unsigned long long*>(s_hist);    // after T1
   int* s_out = s_hist;                                                        // after P5
@@ -898,7 +924,6 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int C = a.C, E = a.E;
-  const int trash = C * HS + lane;
   const int n = *a.n_dev;
   const float* srow = a.S + (long)row * a.s_stride;
   const uint16_t* hrow = a.H + (long)row * a.h_stride;
@@ -913,9 +938,11 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   constexpr bool kMulti = PPT > 36;
   const int nseg = n > 0 ? (kMulti ? (n + SEG - 1) / SEG : 1) : 0;
   // Only the top 16 bits of each key stay in registers (two per register), as t = h - 0x7f for a
-  // member (h = key >> 16 >= 0x80 for every finite score) and 0 for anything else: t is
-  // non-decreasing in the score, so bins of t order members as their scores do, and the few
-  // members of a staged bin get their exact keys from S again
+  // member (h = key >> 16 >= 0x80 for every finite score) and 0 for anything else, with t capped
+  // at kTopT (the head of the largest finite floats: +inf and NaN share their bin, so every
+  // member's t stands for a finite float): t is non-decreasing in the score, so bins of t order
+  // members as their scores do, and the few members of a staged bin get their exact keys from S
+  // again
   uint32_t kk[PPT];             // the loaded scores, until keys() packs them
   uint32_t kh[PPT / 2];         // 16-bit key heads of positions 2j (low half) and 2j + 1
   uint32_t cp[NG];
@@ -949,8 +976,10 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
         // (0x7f) to 0 and a member's head h to h - 0x7f, two positions per instruction
 #pragma unroll
         for (int w = 0; w < 2; ++w)
-          kh[2 * g + w] = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(
-                              __builtin_bit_cast(u16x2, kh[2 * g + w]), (u16x2){0x7f, 0x7f}));
+          kh[2 * g + w] = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(
+                              __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, kh[2 * g + w]),
+                                                            (u16x2){0x7f, 0x7f}),
+                              (u16x2){kTopT, kTopT}));
         continue;
       }
 #pragma unroll
@@ -962,11 +991,11 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
           if (HEADS) {
             const uint32_t h = (kh[j] >> (16 * u)) & 0xffffu;
             const bool q = (i >> 2) * 4096 + (i & 3) < lim && h > oa::kNegInfHead;
-            h2 |= (q ? h - oa::kNegInfHead : 0u) << (16 * u);
+            h2 |= (q ? min(h - (uint32_t)oa::kNegInfHead, (uint32_t)kTopT) : 0u) << (16 * u);
           } else {
             const uint32_t key = oa::float_key(__uint_as_float(kk[i]));
             const bool q = (i >> 2) * 4096 + (i & 3) < lim && key > kNegInfKey;
-            h2 |= (q ? (key >> 16) - oa::kNegInfHead : 0u) << (16 * u);
+            h2 |= (q ? min((key >> 16) - (uint32_t)oa::kNegInfHead, (uint32_t)kTopT) : 0u) << (16 * u);
           }
         }
         kh[j] = h2;
@@ -1018,36 +1047,49 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   khi = 0u;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) { klo = min(klo, s_rlo[w]); khi = max(khi, s_rhi[w]); }
-  float smin = 0.f, scale = 0.f;
-  float smin_sc = 0.f;
+  // bin of a member's t: 1 + (x - smin) * (HS - 2) / (smax - smin), truncated, with x the float
+  // of the head (t + 0x7f) << 16 -- in one fma, rounded once, so non-decreasing in t and inside
+  // [1, HS - 1] (the heads carry 8 significant bits, so |smin| * scale stays below 2^15 and
+  // the fma's error far below 1/2).  A non-member's t = 0 gives a NaN float (below -inf's key):
+  // the fma keeps it NaN and fmaxf(NaN, 0) = 0, bin 0.  With one distinct member head (or a span
+  // that overflows) scale is 0 and every member lands in bin 1
+  float scale = 0.f, off = 1.5f;
   if (khi != 0u) {
-    smin = key_float((klo + oa::kNegInfHead) << 16);
-    const float span = key_float((khi + oa::kNegInfHead) << 16) - smin;
-    scale = span > 0.f && span < INFINITY ? (float)NB / span : 0.f;
-    smin_sc = smin * scale;
+    const float smin = head_float(klo);
+    const float span = head_float(khi) - smin;
+    if (span > 0.f && span < INFINITY) {
+      scale = (float)(HS - 2) / span;
+      off = 1.5f - smin * scale;
+    }
   }
-  // bin of a key head (a NaN's head lies above +inf's, 0xff80, and has no float order: with a
-  // NaN in the row the span is NaN, scale 0 and every member in bin 0, which is still ordered)
-  // (t + 0x7f) << 16 is the head's key with its low bits 0; x * scale - smin * scale in one fma
-  // is as monotone as (x - smin) * scale
-  auto fbin = [&](uint32_t t) -> int {
-    return min(NB - 1, (int)fmaf(key_float((t << 16) + (oa::kNegInfHead << 16)), scale, -smin_sc));
-  };
+  auto fbin = [&](uint32_t t) -> int { return (int)fmaxf(fmaf(head_float(t), scale, off), 0.f); };
 
   // ---- L1: per-cluster histogram of the linear bins.  A single-segment row keeps each
-  // member's bin + 1 in place of its key head (0 still marks a non-member) for G
+  // position's bin in place of its t for G (0 still marks a non-member).  Groups of four
+  // positions wholly past n are skipped (uniform); in the group holding n the positions past it
+  // (clamped loads: copies of one cluster id) count in per-lane trash words, not all in one bin 0
+  const int trash = C * HS + lane;
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
+    const int lim0 = n - sg * SEG;
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const uint32_t k = hd(i);
-      const int bn = fbin(k);
-      int slot = (int)__umul24(cid(i), HS) + bn + (bn >> sb);
-      asm volatile("" : "+v"(slot));
-      atomicAdd(&s_hist[k ? slot : trash], 1);
-      if (!kMulti) {
-        const uint32_t v = k ? (uint32_t)bn + 1u : 0u;
-        kh[i >> 1] = (kh[i >> 1] & ~(0xffffu << (16 * (i & 1)))) | (v << (16 * (i & 1)));
+    for (int g = 0; g < NG; ++g) {
+      if (g * 4096 >= lim0) continue;
+      const bool full = (g + 1) * 4096 <= lim0;
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const int j = 2 * g + w;
+        const int b0 = fbin(kh[j] & 0xffffu);
+        const int b1 = fbin(kh[j] >> 16);
+        int a0 = (int)__umul24(cid(2 * j), HS) + b0;
+        int a1 = (int)__umul24(cid(2 * j + 1), HS) + b1;
+        if (!full) {
+          a0 = b0 ? a0 : trash;
+          a1 = b1 ? a1 : trash;
+        }
+        atomicAdd(&s_hist[a0], 1);
+        atomicAdd(&s_hist[a1], 1);
+        if (!kMulti) kh[j] = (uint32_t)b0 | ((uint32_t)b1 << 16);
       }
     }
   }
@@ -1060,12 +1102,12 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
     const int j = tid & 15;
     const int w = c < C ? s_w[c] : 0;
     RowScan<bpt> r;
-    scan_row(s_hist + min(c, C - 1) * HS, j, r);
+    scan_row_dense(s_hist + min(c, C - 1) * HS, j, r);
     const int m = __shfl(r.sfx, 0, 16);
     if (c < C && w > 0) {
       const int t = min(w, m);
-      if (t > 0 && t == m) {     // every member is chosen
-        if (j == 0) { s_t[c] = t; s_mode[c] = kModeAll; s_sel[c] = 0xffff0000u; }
+      if (t > 0 && t == m) {     // every member is chosen (bins 1 and up: no non-member)
+        if (j == 0) { s_t[c] = t; s_mode[c] = kModeAll; s_sel[c] = 0xffff0001u; }
       } else if (t > 0 && r.sfx >= t && r.sfx - r.ls < t) {
         int b, acc, cnt;
         find_bin(r, t, b, acc, cnt);
@@ -1108,22 +1150,24 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   // bin to its staged keys (the histogram is dead: the staged keys reuse it)
   for (int sg = 0; sg < nseg; ++sg) {
     if (nseg > 1) load(sg);
+    const int lim0 = n - sg * SEG;       // groups of four positions wholly past n are skipped
 #pragma unroll
     for (int i0 = 0; i0 < PPT; i0 += CH) {
       unsigned sv[CH];
 #pragma unroll
       for (int j = 0; j < CH; ++j)
-        if (i0 + j < PPT) sv[j] = s_sel[cid(i0 + j)];
+        if (i0 + j < PPT && ((i0 + j) >> 2) * 4096 < lim0) sv[j] = s_sel[cid(i0 + j)];
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        if (i0 + j < PPT) {
+        if (i0 + j < PPT && ((i0 + j) >> 2) * 4096 < lim0) {
           const int i = i0 + j;
-          const uint32_t k = hd(i);     // bin + 1 (single segment) or the key head
-          const int bn = kMulti ? fbin(k) : (int)k - 1;
+          // the bin (single segment) or t; a non-member's bin 0 is below every chosen or staged
+          // bin (those are 1 or more)
+          const int bn = kMulti ? fbin(hd(i)) : (int)hd(i);
           const int c = cid(i);
-          if (k && bn >= (int)(sv[j] & 0xffffu))
+          if (bn >= (int)(sv[j] & 0xffffu))
             s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos_of(sg, i);
-          else if (k && bn == (int)(sv[j] >> 16))
+          else if (bn == (int)(sv[j] >> 16))
             s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = staged_key(0u, c, pos_of(sg, i));
         }
       }
