@@ -901,7 +901,7 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   __shared__ int s_above[kMaxC];
   __shared__ int s_bcnt[kMaxC];
   __shared__ unsigned s_klo[kMaxC], s_khi[kMaxC];   // 0, ~0: P5 searches all 32 key bits
-  __shared__ unsigned s_sel[kMaxC];       // first chosen bin (low half), staged bin (high half)
+  __shared__ unsigned s_sel[kMaxC];       // lowest gathered bin (low half), first chosen bin (high half)
   __shared__ int s_mode[kMaxC];
   __shared__ int s_goff[kMaxC], s_gcur[kMaxC];
   __shared__ int s_ccur[kMaxC];
@@ -1107,7 +1107,7 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
     if (c < C && w > 0) {
       const int t = min(w, m);
       if (t > 0 && t == m) {     // every member is chosen (bins 1 and up: no non-member)
-        if (j == 0) { s_t[c] = t; s_mode[c] = kModeAll; s_sel[c] = 0xffff0001u; }
+        if (j == 0) { s_t[c] = t; s_mode[c] = kModeAll; s_sel[c] = 0x00010001u; }
       } else if (t > 0 && r.sfx >= t && r.sfx - r.ls < t) {
         int b, acc, cnt;
         find_bin(r, t, b, acc, cnt);
@@ -1117,13 +1117,13 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
         s_bcnt[c] = cnt;
         if (t - acc == cnt) {
           s_mode[c] = kModeAll;
-          s_sel[c] = 0xffff0000u | b1;
+          s_sel[c] = (b1 << 16) | b1;
         } else {
           const int off = atomicAdd(&s_gused, cnt);
           if (off + cnt <= a.gcap) {
             s_mode[c] = kModeStaged;
             s_goff[c] = off;
-            s_sel[c] = (b1 << 16) | (b1 + 1u);
+            s_sel[c] = ((b1 + 1u) << 16) | b1;
           } else {
             s_fail = 1;
           }
@@ -1163,12 +1163,16 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
           const int i = i0 + j;
           // the bin (single segment) or t; a non-member's bin 0 is below every chosen or staged
           // bin (those are 1 or more)
+          // bin (one compare, rarely true); a gathered member at or above the first chosen bin is
+          // chosen, one below it sits in the staged bin
           const int bn = kMulti ? fbin(hd(i)) : (int)hd(i);
-          const int c = cid(i);
-          if (bn >= (int)(sv[j] & 0xffffu))
-            s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos_of(sg, i);
-          else if (bn == (int)(sv[j] >> 16))
-            s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = staged_key(0u, c, pos_of(sg, i));
+          if (bn >= (int)(sv[j] & 0xffffu)) {
+            const int c = cid(i);
+            if (bn >= (int)(sv[j] >> 16))
+              s_cst[s_tpre[c] + atomicAdd(&s_ccur[c], 1)] = ((uint32_t)c << 24) | (uint32_t)pos_of(sg, i);
+            else
+              s_g[s_goff[c] + atomicAdd(&s_gcur[c], 1)] = staged_key(0u, c, pos_of(sg, i));
+          }
         }
       }
     }
