@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define OA_ABI_VERSION 4
+#define OA_ABI_VERSION 5
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
@@ -156,10 +156,12 @@ int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8
  * same stage as oa_qgs_scan (_k_qgs_scan_tm, inference/graph_runner.py:100-120); the reduced
  * score rows have no counterpart in the reference.
  *   H (rows, h_stride >= ceil(Lmax/64)*64, a multiple of 4) 16-bit, 8-byte aligned.
+ *   TMn (NULL, or like TM): each tile's least finite score, +inf for a tile without one -- the
+ *   row range oa_topq_heads bins with, known before the row is read.  No reference counterpart.
  */
 int oa_qgs_scan_heads(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
                       const int* fexp, uint16_t* H, long h_stride, float* TM, long tm_stride,
-                      const int* n_dev, int ns, int nl, void* stream);
+                      float* TMn, const int* n_dev, int ns, int nl, void* stream);
 
 /*
  * Exact top-k per row (ties to the lower position) among the k tiles with the largest
@@ -256,7 +258,7 @@ int oa_topk_gate_fill(uint16_t* H, long h_stride, const float* TM, long tm_strid
  */
 int oa_qgs_scan_gate(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
                      const int* fexp, uint16_t* H, long h_stride, float* TM, long tm_stride,
-                     const int* n_dev, int ns, int nl, const void* q, long q_stride, const float* Sk,
+                     float* TMn, const int* n_dev, int ns, int nl, const void* q, long q_stride, const float* Sk,
                      const float* Sk2, const float* nb, int C, float sm_scale, float sm_scale_sq,
                      float* score, float* n_t, float* qsk, void* stream);
 
@@ -314,12 +316,15 @@ int oa_topq_path(const float* S, long s_stride, const uint8_t* asg8, long asg8_s
  * linear-bin kernel alone (rows it leaves hold -2 in exp_idx[row][0]); 3 (tests): every row
  * through S32 and the key-prefix kernel.
  *   H as oa_qgs_scan_heads; S32 (rows, s32_stride >= round_up(Lmax, 4)) fp32, 16-byte aligned;
- *   rows = 4 * kv_rows.
+ *   rows = 4 * kv_rows.  TM, TMn (both NULL, or both the scan's, tm_stride >= ceil(Lmax/64)):
+ *   the row's range is taken from the tile extremes instead of a pass over the row, and each
+ *   group of positions is binned as it arrives (same result).
  */
 int oa_topq_heads(const uint16_t* H, long h_stride, const uint8_t* asg8, long asg8_stride,
                   const float* quota, int rows, int C, int Lmax, int32_t* exp_idx, int E,
                   const int* n_dev, const int8_t* codes, int kv_rows, const int8_t* limbs,
-                  const int* fexp, float* S32, long s32_stride, int path, void* stream);
+                  const int* fexp, float* S32, long s32_stride, const float* TM, const float* TMn,
+                  long tm_stride, int path, void* stream);
 
 /*
  * Residual proxies: kbar', vbar' (bf16, rows x C x 128) and ln n' (fp32, -inf = none) of the

@@ -154,6 +154,12 @@ __device__ __forceinline__ float group16_max(float v) {
   v = fmaxf(v, dpp_f32<0x141>(v));
   return fmaxf(v, dpp_f32<0x140>(v));
 }
+__device__ __forceinline__ float group16_min(float v) {
+  v = fminf(v, dpp_f32<0xB1>(v));
+  v = fminf(v, dpp_f32<0x4E>(v));
+  v = fminf(v, dpp_f32<0x141>(v));
+  return fminf(v, dpp_f32<0x140>(v));
+}
 
 // ---- order-independent reductions on the DPP network (no LDS round trips) ------------------
 // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror fold each 16-lane row;

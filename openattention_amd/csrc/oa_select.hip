@@ -55,11 +55,13 @@ struct ScanArgs {
   const int8_t* codes; int Lmax; const int8_t* limbs; const int* fexp;
   void* Sv; long s_stride; float* TM; long tm_stride;
   const int* n_dev; int ns; int nl;
+  float* TMn;      // optional: each tile's least finite score (+inf for a tile without one)
 };
 
 // HEADS: the score rows hold 16-bit key heads (oa::score_head) instead of fp32 scores.
 // One block: token chunk `chunk` (kTokWG tokens) of KV row kvr.
-template <bool HEADS>
+// MIN: the tile minima of the finite scores too (sa.TMn)
+template <bool HEADS, bool MIN = false>
 __device__ __forceinline__ void scan_block(const ScanArgs& sa, int chunk, int kvr) {
   const int8_t* __restrict__ codes = sa.codes;
   const int Lmax = sa.Lmax;
@@ -68,6 +70,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& sa, int chunk, int kv
   void* __restrict__ Sv = sa.Sv;
   const long s_stride = sa.s_stride;
   float* __restrict__ TM = sa.TM;
+  float* __restrict__ TMn = sa.TMn;
   const long tm_stride = sa.tm_stride;
   const int ns = sa.ns, nl = sa.nl;
   const int wave = threadIdx.x >> 6;
@@ -103,11 +106,12 @@ __device__ __forceinline__ void scan_block(const ScanArgs& sa, int chunk, int kv
   // tiles of a row: one store instead of four-lane scattered ones per tile)
   constexpr int kTB = kTokWG / 64;
   __shared__ float s_tm[GQ][kTB];
+  __shared__ float s_tmn[GQ][kTB];
 #pragma unroll
   for (int t = 0; t < kTilesPerWave; ++t) {
     const int tile = tile_begin + t;
     if (tile >= ntile_total) break;
-    float tmax = -INFINITY;
+    float tmax = -INFINITY, tmin = INFINITY;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int tok = tile * 64 + b * 16 + nn;
@@ -120,7 +124,9 @@ __device__ __forceinline__ void scan_block(const ScanArgs& sa, int chunk, int kv
       const int xl = acc[1] * 256 + acc[0];
       const double s = fma((double)xh, 65536.0, (double)xl);
       float sc = (float)(s * inv);
-      if (tok < ns || tok >= dead_hi) sc = -INFINITY;
+      const bool dead = tok < ns || tok >= dead_hi;
+      if (MIN) tmin = fminf(tmin, dead ? INFINITY : sc);
+      if (dead) sc = -INFINITY;
       if (HEADS) s_h[wave][kg][b * 16 + nn] = oa::score_head(sc);
       else Srow[tok] = sc;
       tmax = fmaxf(tmax, sc);
@@ -141,18 +147,25 @@ __device__ __forceinline__ void scan_block(const ScanArgs& sa, int chunk, int kv
     // one 16-lane DPP row per head: the tile maximum in every lane of the row
     tmax = oa::group16_max(tmax);
     if (nn == 0) s_tm[kg][wave * kTilesPerWave + t] = tmax;
+    if (MIN) {
+      tmin = oa::group16_min(tmin);
+      if (nn == 0) s_tmn[kg][wave * kTilesPerWave + t] = tmin;
+    }
   }
   oa::lds_barrier();
   if (threadIdx.x < GQ * kTB) {
     const int g = threadIdx.x / kTB;
     const int tile = chunk * kTB + threadIdx.x % kTB;
-    if (tile < ntile_total) TM[(long)(kvr * GQ + g) * tm_stride + tile] = s_tm[g][threadIdx.x % kTB];
+    if (tile < ntile_total) {
+      TM[(long)(kvr * GQ + g) * tm_stride + tile] = s_tm[g][threadIdx.x % kTB];
+      if (MIN) TMn[(long)(kvr * GQ + g) * tm_stride + tile] = s_tmn[g][threadIdx.x % kTB];
+    }
   }
 }
 
-template <bool HEADS>
+template <bool HEADS, bool MIN>
 __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(ScanArgs sa) {
-  scan_block<HEADS>(sa, blockIdx.x, blockIdx.y);
+  scan_block<HEADS, MIN>(sa, blockIdx.x, blockIdx.y);
 }
 
 // The scan over heads and the pooled part of the ErrorGate in one launch: n_scan blocks of
@@ -160,6 +173,7 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_kernel(ScanArgs sa) {
 // gate_pooled_unit (row r, clusters 16 u .. 16 u + 15), spread evenly through the block order
 // so that the gate's short dependent chains run under the scan's code stream.  Both read state
 // the index update left (codes, limbs; Sk, Sk2, n) and write disjoint outputs.
+template <bool MIN>
 __global__ void __launch_bounds__(kScanThreads) qgs_scan_gate_kernel(ScanArgs sa, oa_gate::GateArgs ga,
                                                                      int nchunks, int n_scan, int n_gate) {
   const long b = blockIdx.x;
@@ -174,7 +188,7 @@ __global__ void __launch_bounds__(kScanThreads) qgs_scan_gate_kernel(ScanArgs sa
     oa_gate::gate_pooled_unit(ga, row, (int)(g0 % units) * oa_gate::kPoolClusters, s_zb, s_s2, s_nt);
   } else {
     const long si = b - g0;                         // scan blocks before this one
-    scan_block<true>(sa, (int)(si % nchunks), (int)(si / nchunks));
+    scan_block<true, MIN>(sa, (int)(si % nchunks), (int)(si / nchunks));
   }
 }
 
@@ -367,14 +381,17 @@ extern "C" int oa_qgs_prep(const void* q, long q_stride, const float* U, const f
 namespace {
 template <bool HEADS>
 int launch_scan(const int8_t* codes, int kv_rows, int Lmax, int rank, const int8_t* limbs,
-                const int* fexp, void* S, long s_stride, float* TM, long tm_stride,
+                const int* fexp, void* S, long s_stride, float* TM, long tm_stride, float* TMn,
                 const int* n_dev, int ns, int nl, void* stream) {
   if (rank != RQ || kv_rows <= 0 || Lmax <= 0) return OA_EINVAL;
   const int ntile = (Lmax + 63) / 64;
   if (s_stride < (long)ntile * 64 || tm_stride < ntile || ns < 0 || nl < 0) return OA_EINVAL;
   dim3 grid((Lmax + kTokWG - 1) / kTokWG, kv_rows);
-  const ScanArgs sa{codes, Lmax, limbs, fexp, S, s_stride, TM, tm_stride, n_dev, ns, nl};
-  hipLaunchKernelGGL(qgs_scan_kernel<HEADS>, grid, dim3(kScanThreads), 0, (hipStream_t)stream, sa);
+  const ScanArgs sa{codes, Lmax, limbs, fexp, S, s_stride, TM, tm_stride, n_dev, ns, nl, TMn};
+  if (TMn)
+    hipLaunchKernelGGL((qgs_scan_kernel<HEADS, true>), grid, dim3(kScanThreads), 0, (hipStream_t)stream, sa);
+  else
+    hipLaunchKernelGGL((qgs_scan_kernel<HEADS, false>), grid, dim3(kScanThreads), 0, (hipStream_t)stream, sa);
   return OA_LAUNCH_STATUS();
 }
 
@@ -413,16 +430,16 @@ extern "C" int oa_qgs_scan(const int8_t* codes, int kv_rows, int Lmax, int rank,
                            const int* fexp, float* S, long s_stride, float* TM, long tm_stride,
                            const int* n_dev, int ns, int nl, void* stream) {
   return launch_scan<false>(codes, kv_rows, Lmax, rank, limbs, fexp, S, s_stride, TM, tm_stride,
-                            n_dev, ns, nl, stream);
+                            nullptr, n_dev, ns, nl, stream);
 }
 
 extern "C" int oa_qgs_scan_heads(const int8_t* codes, int kv_rows, int Lmax, int rank,
                                  const int8_t* limbs, const int* fexp, uint16_t* H, long h_stride,
-                                 float* TM, long tm_stride, const int* n_dev, int ns, int nl,
-                                 void* stream) {
+                                 float* TM, long tm_stride, float* TMn, const int* n_dev, int ns,
+                                 int nl, void* stream) {
   if (!H || (reinterpret_cast<uintptr_t>(H) & 7) || h_stride % 4) return OA_EINVAL;
   return launch_scan<true>(codes, kv_rows, Lmax, rank, limbs, fexp, H, h_stride, TM, tm_stride,
-                           n_dev, ns, nl, stream);
+                           TMn, n_dev, ns, nl, stream);
 }
 
 extern "C" int oa_topk_select(float* S, long s_stride, const float* TM, long tm_stride, int rows,
@@ -446,8 +463,8 @@ extern "C" int oa_topk_select_heads(uint16_t* H, long h_stride, const float* TM,
 
 extern "C" int oa_qgs_scan_gate(const int8_t* codes, int kv_rows, int Lmax, int rank,
                                 const int8_t* limbs, const int* fexp, uint16_t* H, long h_stride,
-                                float* TM, long tm_stride, const int* n_dev, int ns, int nl,
-                                const void* q, long q_stride, const float* Sk, const float* Sk2,
+                                float* TM, long tm_stride, float* TMn, const int* n_dev, int ns,
+                                int nl, const void* q, long q_stride, const float* Sk, const float* Sk2,
                                 const float* nb, int C, float sm_scale, float sm_scale_sq,
                                 float* score, float* n_t, float* qsk, void* stream) {
   if (!H || (reinterpret_cast<uintptr_t>(H) & 7) || h_stride % 4 || rank != RQ || kv_rows <= 0 ||
@@ -455,7 +472,7 @@ extern "C" int oa_qgs_scan_gate(const int8_t* codes, int kv_rows, int Lmax, int 
     return OA_EINVAL;
   const int ntile = (Lmax + 63) / 64;
   if (h_stride < (long)ntile * 64 || tm_stride < ntile || ns < 0 || nl < 0) return OA_EINVAL;
-  const ScanArgs sa{codes, Lmax, limbs, fexp, H, h_stride, TM, tm_stride, n_dev, ns, nl};
+  const ScanArgs sa{codes, Lmax, limbs, fexp, H, h_stride, TM, tm_stride, n_dev, ns, nl, TMn};
   oa_gate::GateArgs ga{};
   ga.q = (const uint16_t*)q; ga.q_stride = q_stride;
   ga.Sk = Sk; ga.Sk2 = Sk2; ga.st_stride_r = (long)C * OA_D;
@@ -467,7 +484,8 @@ extern "C" int oa_qgs_scan_gate(const int8_t* codes, int kv_rows, int Lmax, int 
   const long n_scan = (long)nchunks * kv_rows;
   const long n_gate = (long)rows * ((C + oa_gate::kPoolClusters - 1) / oa_gate::kPoolClusters);
   if (n_scan + n_gate > 0x7fffffffL) return OA_EINVAL;
-  hipLaunchKernelGGL(qgs_scan_gate_kernel, dim3((unsigned)(n_scan + n_gate)), dim3(kScanThreads), 0,
+  hipLaunchKernelGGL(TMn ? qgs_scan_gate_kernel<true> : qgs_scan_gate_kernel<false>,
+                     dim3((unsigned)(n_scan + n_gate)), dim3(kScanThreads), 0,
                      (hipStream_t)stream, sa, ga, nchunks, (int)n_scan, (int)n_gate);
   return OA_LAUNCH_STATUS();
 }

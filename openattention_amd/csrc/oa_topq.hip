@@ -68,6 +68,7 @@ constexpr unsigned kNoGather = 0xffffffffu;    // gathering bound of a cluster w
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int kSmallRows = 256;               // below: oa_topq_heads path 0 in one launch
 constexpr int32_t kRowMarked = -2;              // exp_idx[row][0] of a row left to the key-prefix kernel
+constexpr int kTileLd = 3;                      // tile extremes per thread (linear-bin kernel)
 constexpr int kRowGrid = 256;                   // key-prefix kernel over marked rows: one workgroup per unit
 
 enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3, kModeSplit = 4 };
@@ -91,6 +92,10 @@ struct TopqArgs {
   const int8_t* codes; long lmax_codes; const int8_t* limbs; const int* fexp;
   float* S32; long s32_stride;
   int force_mark;  // tests: every row is left to the key-prefix kernel
+  // optional (linear-bin kernel over heads): each 64-position tile's greatest score (TM) and
+  // least finite score (TMn) from the scan; then the row's range comes from them instead of a
+  // pass over the row, and every group of positions is binned as soon as it arrives
+  const float* TM; const float* TMn; long tm_stride;
 };
 
 // the largest t = head - 0x7f of a finite float (head 0xff7f): the linear-bin kernel caps t here
@@ -893,8 +898,9 @@ __global__ void __launch_bounds__(kThreads) topq_marked_kernel(TopqArgs a) {
 // HEADS: the score rows hold 16-bit key heads (oa_qgs_scan_heads), which are all the kernel
 // keeps of a score anyway; exact scores come from the codes (oa::qgs_score).
 // Returns true for a row it leaves to the key-prefix algorithm (marked kRowMarked).
-template <int PPT, int LB, bool HEADS>
+template <int PPT, int LB, bool HEADS, bool TILE>
 __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, unsigned long long* dyn) {
+  static_assert(HEADS || !TILE, "the tile range comes with the head rows");
   __shared__ int s_w[kMaxC];
   __shared__ int s_base[kMaxC + 1];
   __shared__ int s_t[kMaxC];
@@ -967,10 +973,10 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
     }
   };
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  auto keys = [&](int sg) {
+  // t of the four positions of group g of segment sg (two registers), in place
+  auto key_group = [&](int sg, int g) {
     const int lim = n - sg * SEG - 4 * tid;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
+    {
       if (HEADS && g * 4096 + 3 < lim) {
         // the group lies inside the row: a saturating subtract of 0x7f maps the heads of -inf
         // (0x7f) to 0 and a member's head h to h - 0x7f, two positions per instruction
@@ -980,7 +986,7 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
                               __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, kh[2 * g + w]),
                                                             (u16x2){0x7f, 0x7f}),
                               (u16x2){kTopT, kTopT}));
-        continue;
+        return;
       }
 #pragma unroll
       for (int j = 2 * g; j < 2 * g + 2; ++j) {
@@ -1002,16 +1008,36 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
       }
     }
   };
+  auto keys = [&](int sg) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) key_group(sg, g);
+  };
   auto load = [&](int sg) { issue(sg); keys(sg); };
   auto hd = [&](int i) -> uint32_t { return (kh[i >> 1] >> (16 * (i & 1))) & 0xffffu; };
   auto cid = [&](int i) -> int { return (int)((cp[i >> 2] >> (8 * (i & 3))) & 0xffu); };
 
   // the quotas and the limb words are requested ahead of the row (loads return in order, so
-  // the prefix would otherwise wait for the whole row)
+  // the prefix would otherwise wait for the whole row); so are (TILE) the row's tile extremes --
+  // the tiles holding a position below n; a single-segment row has at most 16 PPT <= kThreads of
+  // them, one per thread.  With them no pass over the row precedes the binning (a row of several
+  // segments is then read twice, not three times)
   float qv[4];
   if (wave == 0) quota_load(a.quota + (long)row * C, C, lane, qv);
   int lwv = 0;
   if (HEADS && tid < 32) lwv = oa::limb_words(a.limbs, kvr, row % 4)[tid];
+  const int ntu = (n + 63) / 64;
+  constexpr int TL = kMulti ? kTileLd : 1;
+  float tx[TL], tn[TL];
+  if (TILE) {
+    const float* tm_row = a.TM + (long)row * a.tm_stride;
+    const float* tmn_row = a.TMn + (long)row * a.tm_stride;
+#pragma unroll
+    for (int u = 0; u < TL; ++u) {
+      const int j = max(min(tid + u * kThreads, ntu - 1), 0);
+      tx[u] = tm_row[j];
+      tn[u] = tmn_row[j];
+    }
+  }
   if (nseg > 0) issue(0);       // in flight while P0 runs
 
   // ---- P0: quota prefix, per-cluster state, histogram clear
@@ -1027,18 +1053,36 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   // ---- R: the range of the qualifying members' score keys
   // two heads per register on the packed 16-bit ALU: a non-member (head 0) becomes 0xffff after
   // the wrapping - 1, so it never wins the minimum of the members' heads - 1
-  u16x2 vlo = {0xffff, 0xffff}, vhi = {0, 0};
-  for (int sg = 0; sg < nseg; ++sg) {
-    if (sg == 0) keys(0); else load(sg);
+  // (with the tile extremes: the t of the least and greatest finite score below n, a range that
+  // holds every member's t -- the selected positions' scores only widen it)
+  uint32_t khi = 0u, klo = 0xffffffffu;
+  if (TILE) {
+    float tmx = -INFINITY, tmn = INFINITY;
 #pragma unroll
-    for (int j = 0; j < PPT / 2; ++j) {
-      const u16x2 h = __builtin_bit_cast(u16x2, kh[j]);
-      vhi = __builtin_elementwise_max(vhi, h);
-      vlo = __builtin_elementwise_min(vlo, (u16x2)(h - (u16x2){1, 1}));
+    for (int u = 0; u < TL; ++u) {
+      if (tid + u * kThreads < ntu) {
+        tmx = fmaxf(tmx, tx[u]);
+        tmn = fminf(tmn, tn[u]);
+      }
     }
+    if (tmx > -INFINITY) {
+      khi = min((oa::float_key(tmx) >> 16) - (uint32_t)oa::kNegInfHead, (uint32_t)kTopT);
+      klo = min((oa::float_key(tmn) >> 16) - (uint32_t)oa::kNegInfHead, (uint32_t)kTopT);
+    }
+  } else {
+    u16x2 vlo = {0xffff, 0xffff}, vhi = {0, 0};
+    for (int sg = 0; sg < nseg; ++sg) {
+      if (sg == 0) keys(0); else load(sg);
+#pragma unroll
+      for (int j = 0; j < PPT / 2; ++j) {
+        const u16x2 h = __builtin_bit_cast(u16x2, kh[j]);
+        vhi = __builtin_elementwise_max(vhi, h);
+        vlo = __builtin_elementwise_min(vlo, (u16x2)(h - (u16x2){1, 1}));
+      }
+    }
+    khi = max((uint32_t)vhi.x, (uint32_t)vhi.y);
+    klo = min((uint32_t)vlo.x, (uint32_t)vlo.y) + 1u;   // with no member khi is 0
   }
-  uint32_t khi = max((uint32_t)vhi.x, (uint32_t)vhi.y);
-  uint32_t klo = min((uint32_t)vlo.x, (uint32_t)vlo.y) + 1u;   // with no member khi is 0
   klo = ~oa::wave_max_u32(~klo);
   khi = oa::wave_max_u32(khi);
   if (lane == 0) { s_rlo[wave] = klo; s_rhi[wave] = khi; }
@@ -1062,7 +1106,11 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
       off = 1.5f - smin * scale;
     }
   }
-  auto fbin = [&](uint32_t t) -> int { return (int)fmaxf(fmaf(head_float(t), scale, off), 0.f); };
+  // (clamped into the row as well: a member outside the range -- only if the caller's tile
+  // extremes do not hold its score -- stays inside the cluster's histogram row)
+  auto fbin = [&](uint32_t t) -> int {
+    return (int)fminf(fmaxf(fmaf(head_float(t), scale, off), 0.f), (float)(HS - 1));
+  };
 
   // ---- L1: per-cluster histogram of the linear bins.  A single-segment row keeps each
   // position's bin in place of its t for G (0 still marks a non-member).  Groups of four
@@ -1070,11 +1118,14 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   // (clamped loads: copies of one cluster id) count in per-lane trash words, not all in one bin 0
   const int trash = C * HS + lane;
   for (int sg = 0; sg < nseg; ++sg) {
-    if (nseg > 1) load(sg);
+    // with the tile range the row's t are formed here, group by group as the loads arrive
+    if (TILE ? sg > 0 : nseg > 1) issue(sg);
+    if (!TILE && nseg > 1) keys(sg);
     const int lim0 = n - sg * SEG;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       if (g * 4096 >= lim0) continue;
+      if (TILE) key_group(sg, g);
       const bool full = (g + 1) * 4096 <= lim0;
 #pragma unroll
       for (int w = 0; w < 2; ++w) {
@@ -1199,21 +1250,21 @@ __device__ __forceinline__ bool topq_linear_body(const TopqArgs& a, int row, uns
   return false;
 }
 
-template <int PPT, int LB, bool HEADS>
+template <int PPT, int LB, bool HEADS, bool TILE>
 // up to 64 VGPRs for the single-segment instantiations: two workgroups (rows) per unit
 __global__ void __launch_bounds__(kThreads, PPT <= 36 ? 8 : 4) topq_linear_kernel(TopqArgs a) {
   extern __shared__ unsigned long long dyn[];
-  topq_linear_body<PPT, LB, HEADS>(a, blockIdx.x, dyn);
+  topq_linear_body<PPT, LB, HEADS, TILE>(a, blockIdx.x, dyn);
 }
 
 // Fewer rows than compute units (one workgroup per unit, so its LDS and registers are free):
 // the linear-bin algorithm and, on a row it cannot finish, the key-prefix algorithm in the same
 // workgroup, instead of a second launch over every row.  lin and pre are the two algorithms'
 // arguments (LDS layouts); the dynamic LDS holds either's.
-template <int PPT, int LB, int PLB>
+template <int PPT, int LB, int PLB, bool TILE>
 __global__ void __launch_bounds__(kThreads) topq_small_kernel(TopqArgs lin, TopqArgs pre) {
   extern __shared__ unsigned long long dyn[];
-  if (topq_linear_body<PPT, LB, true>(lin, blockIdx.x, dyn)) {   // uniform
+  if (topq_linear_body<PPT, LB, true, TILE>(lin, blockIdx.x, dyn)) {   // uniform
     // the row's exact scores (S32) written above are read back by every wave
     __threadfence();
     __syncthreads();
@@ -1241,21 +1292,21 @@ int launch_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStream_t s) 
   return launch_row<44, LB>(a, rows, lds, s);
 }
 
-template <int PPT, int LB, bool HEADS>
+template <int PPT, int LB, bool HEADS, bool TILE>
 int launch_linear(const TopqArgs& a, int rows, size_t lds, hipStream_t s) {
-  const hipError_t e = hipFuncSetAttribute((const void*)topq_linear_kernel<PPT, LB, HEADS>,
+  const hipError_t e = hipFuncSetAttribute((const void*)topq_linear_kernel<PPT, LB, HEADS, TILE>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((topq_linear_kernel<PPT, LB, HEADS>), dim3(rows), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((topq_linear_kernel<PPT, LB, HEADS, TILE>), dim3(rows), dim3(kThreads), lds, s, a);
   return OA_LAUNCH_STATUS();
 }
 
-template <int LB, bool HEADS>
+template <int LB, bool HEADS, bool TILE>
 int launch_linear_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStream_t s) {
-  if (Lmax <= kThreads * 8) return launch_linear<8, LB, HEADS>(a, rows, lds, s);
-  if (Lmax <= kThreads * 16) return launch_linear<16, LB, HEADS>(a, rows, lds, s);
-  if (Lmax <= kThreads * 36) return launch_linear<36, LB, HEADS>(a, rows, lds, s);
-  return launch_linear<44, LB, HEADS>(a, rows, lds, s);
+  if (Lmax <= kThreads * 8) return launch_linear<8, LB, HEADS, TILE>(a, rows, lds, s);
+  if (Lmax <= kThreads * 16) return launch_linear<16, LB, HEADS, TILE>(a, rows, lds, s);
+  if (Lmax <= kThreads * 36) return launch_linear<36, LB, HEADS, TILE>(a, rows, lds, s);
+  return launch_linear<44, LB, HEADS, TILE>(a, rows, lds, s);
 }
 
 // The one-launch kernel holds both algorithms' static LDS; the key-prefix algorithm's gathered
@@ -1263,9 +1314,9 @@ int launch_linear_lb(const TopqArgs& a, int rows, int Lmax, size_t lds, hipStrea
 // LDS (hipFuncGetAttributes).  Returns kNotLaunched when the list would be too short to run the
 // key-prefix algorithm in the same workgroup: the caller then takes two launches.
 constexpr int kNotLaunched = -1001;
-template <int PPT, int LB, int PLB>
+template <int PPT, int LB, int PLB, bool TILE>
 int launch_small(const TopqArgs& lin, TopqArgs pre, int rows, size_t lds_lin, hipStream_t s) {
-  const void* fn = (const void*)topq_small_kernel<PPT, LB, PLB>;
+  const void* fn = (const void*)topq_small_kernel<PPT, LB, PLB, TILE>;
   hipFuncAttributes fa;
   const hipError_t ea = hipFuncGetAttributes(&fa, fn);
   if (ea != hipSuccess) return (int)ea;
@@ -1278,15 +1329,15 @@ int launch_small(const TopqArgs& lin, TopqArgs pre, int rows, size_t lds_lin, hi
   if ((long)lds + (long)fa.sharedSizeBytes > kLdsLimit) return kNotLaunched;
   const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((topq_small_kernel<PPT, LB, PLB>), dim3(rows), dim3(kThreads), lds, s, lin, pre);
+  hipLaunchKernelGGL((topq_small_kernel<PPT, LB, PLB, TILE>), dim3(rows), dim3(kThreads), lds, s, lin, pre);
   return OA_LAUNCH_STATUS();
 }
-template <int LB, int PLB>
+template <int LB, int PLB, bool TILE>
 int launch_small_ppt(const TopqArgs& lin, const TopqArgs& pre, int rows, int Lmax, size_t lds_lin,
                      hipStream_t s) {
-  if (Lmax <= kThreads * 8) return launch_small<8, LB, PLB>(lin, pre, rows, lds_lin, s);
-  if (Lmax <= kThreads * 16) return launch_small<16, LB, PLB>(lin, pre, rows, lds_lin, s);
-  return launch_small<36, LB, PLB>(lin, pre, rows, lds_lin, s);
+  if (Lmax <= kThreads * 8) return launch_small<8, LB, PLB, TILE>(lin, pre, rows, lds_lin, s);
+  if (Lmax <= kThreads * 16) return launch_small<16, LB, PLB, TILE>(lin, pre, rows, lds_lin, s);
+  return launch_small<36, LB, PLB, TILE>(lin, pre, rows, lds_lin, s);
 }
 
 }  // namespace
@@ -1314,6 +1365,8 @@ int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool hea
   const size_t lds = 8 * (size_t)(a.ucap + 64) + 4 * (size_t)a.hwords + 4 * (size_t)a.cpow;
   a.marked_only = 0;
   a.rows = rows;
+  // the tile range: head rows with the scan's tile extremes, at most kTileLd tiles per thread
+  const bool tile = heads && a.TM != nullptr && (Lmax + 63) / 64 <= kTileLd * kThreads;
   if (lin) {
     // linear-bin kernel, dynamic LDS: histogram -> staged keys -> output row | chosen words.
     // 7 bits for C <= 64, 6 for C <= 128, else 5: two workgroups' LDS fits one unit.  Rows
@@ -1329,18 +1382,27 @@ int topq_launch(TopqArgs a, int rows, int C, int Lmax, int E, bool lin, bool hea
       // algorithm's static LDS, which the same workgroup holds (path 3, every row marked, then
       // runs every row through the key-prefix algorithm in this kernel)
       int st1 = kNotLaunched;
-      if (al.lb == 7 && a.lb == 8) st1 = launch_small_ppt<7, 8>(al, a, rows, Lmax, lds_lin, s);
-      else if (al.lb == 6 && a.lb == 7) st1 = launch_small_ppt<6, 7>(al, a, rows, Lmax, lds_lin, s);
-      else if (al.lb == 5 && a.lb == 6) st1 = launch_small_ppt<5, 6>(al, a, rows, Lmax, lds_lin, s);
+      if (tile) {
+        if (al.lb == 7 && a.lb == 8) st1 = launch_small_ppt<7, 8, true>(al, a, rows, Lmax, lds_lin, s);
+        else if (al.lb == 6 && a.lb == 7) st1 = launch_small_ppt<6, 7, true>(al, a, rows, Lmax, lds_lin, s);
+        else if (al.lb == 5 && a.lb == 6) st1 = launch_small_ppt<5, 6, true>(al, a, rows, Lmax, lds_lin, s);
+      } else {
+        if (al.lb == 7 && a.lb == 8) st1 = launch_small_ppt<7, 8, false>(al, a, rows, Lmax, lds_lin, s);
+        else if (al.lb == 6 && a.lb == 7) st1 = launch_small_ppt<6, 7, false>(al, a, rows, Lmax, lds_lin, s);
+        else if (al.lb == 5 && a.lb == 6) st1 = launch_small_ppt<5, 6, false>(al, a, rows, Lmax, lds_lin, s);
+      }
       if (st1 != kNotLaunched) return st1;
     }
     int st;
-    if (heads) st = al.lb == 7 ? launch_linear_lb<7, true>(al, rows, Lmax, lds_lin, s)
-                    : al.lb == 6 ? launch_linear_lb<6, true>(al, rows, Lmax, lds_lin, s)
-                                 : launch_linear_lb<5, true>(al, rows, Lmax, lds_lin, s);
-    else st = al.lb == 7 ? launch_linear_lb<7, false>(al, rows, Lmax, lds_lin, s)
-              : al.lb == 6 ? launch_linear_lb<6, false>(al, rows, Lmax, lds_lin, s)
-                           : launch_linear_lb<5, false>(al, rows, Lmax, lds_lin, s);
+    if (tile) st = al.lb == 7 ? launch_linear_lb<7, true, true>(al, rows, Lmax, lds_lin, s)
+                   : al.lb == 6 ? launch_linear_lb<6, true, true>(al, rows, Lmax, lds_lin, s)
+                                : launch_linear_lb<5, true, true>(al, rows, Lmax, lds_lin, s);
+    else if (heads) st = al.lb == 7 ? launch_linear_lb<7, true, false>(al, rows, Lmax, lds_lin, s)
+                    : al.lb == 6 ? launch_linear_lb<6, true, false>(al, rows, Lmax, lds_lin, s)
+                                 : launch_linear_lb<5, true, false>(al, rows, Lmax, lds_lin, s);
+    else st = al.lb == 7 ? launch_linear_lb<7, false, false>(al, rows, Lmax, lds_lin, s)
+              : al.lb == 6 ? launch_linear_lb<6, false, false>(al, rows, Lmax, lds_lin, s)
+                           : launch_linear_lb<5, false, false>(al, rows, Lmax, lds_lin, s);
     if (st || !pre) return st;
     a.marked_only = 1;
   }
@@ -1388,10 +1450,12 @@ extern "C" int oa_topq_heads(const uint16_t* H, long h_stride, const uint8_t* as
                              long asg8_stride, const float* quota, int rows, int C, int Lmax,
                              int32_t* exp_idx, int E, const int* n_dev, const int8_t* codes,
                              int kv_rows, const int8_t* limbs, const int* fexp, float* S32,
-                             long s32_stride, int path, void* stream) {
+                             long s32_stride, const float* TM, const float* TMn, long tm_stride,
+                             int path, void* stream) {
   const long lmax4 = ((long)Lmax + 3) & ~3L;
   if (!topq_sizes_ok(rows, C, E, Lmax) || !H || !asg8 || !quota || !n_dev || !codes || !limbs ||
       !fexp || !S32 || (E > 0 && !exp_idx) || kv_rows <= 0 || rows != kv_rows * 4 ||
+      (!TM != !TMn) || (TM && tm_stride < ((long)Lmax + 63) / 64) ||
       h_stride % 4 || asg8_stride % 4 || s32_stride % 4 || h_stride < lmax4 ||
       asg8_stride < lmax4 || s32_stride < lmax4 || (reinterpret_cast<uintptr_t>(H) & 7) ||
       (reinterpret_cast<uintptr_t>(S32) & 15) || (reinterpret_cast<uintptr_t>(asg8) & 3) ||
@@ -1404,5 +1468,6 @@ extern "C" int oa_topq_heads(const uint16_t* H, long h_stride, const uint8_t* as
   a.C = C; a.E = E; a.n_dev = n_dev; a.exp_idx = exp_idx;
   a.H = H; a.h_stride = h_stride; a.codes = codes; a.lmax_codes = Lmax; a.limbs = limbs;
   a.fexp = fexp; a.S32 = S32; a.s32_stride = s32_stride; a.force_mark = path == 3;
+  a.TM = TM; a.TMn = TMn; a.tm_stride = tm_stride;
   return topq_launch(a, rows, C, Lmax, E, true, true, path != 2, (hipStream_t)stream);
 }

@@ -34,20 +34,20 @@ SIGNATURES = {
     "oa_index_prep": [P, P, L, L, I, I, I, P, I, I, P, P, P, P, I, P, I, P, L, P, L, P, P, P, P, P,
                       P, I, P, P, L, P, P, P],
     "oa_qgs_scan": [P, I, I, I, P, P, P, L, P, L, P, I, I, P],
-    "oa_qgs_scan_heads": [P, I, I, I, P, P, P, L, P, L, P, I, I, P],
+    "oa_qgs_scan_heads": [P, I, I, I, P, P, P, L, P, L, P, P, I, I, P],
     "oa_topk_select": [P, L, P, L, I, I, P, L, P, I, I, I, P],
     "oa_topk_select_heads": [P, L, P, L, I, I, P, L, P, I, I, I, P, I, I, P, P, P],
     "oa_errorgate": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, P, P, P],
     "oa_gate_fill": [P, L, P, L, L, I, I, I, P, L, P, L, I, P, P, P, I, F, F, I, P, P, P, P, P],
     "oa_topk_gate_fill": [P, L, P, L, I, P, I, I, I, P, I, P, P, P, L, P, L, L, I, I, I, P, L, P, L,
                           P, P, P, I, F, F, I, P, P, P, P, P],
-    "oa_qgs_scan_gate": [P, I, I, I, P, P, P, L, P, L, P, I, I, P, L, P, P, P, I, F, F, P, P, P, P],
+    "oa_qgs_scan_gate": [P, I, I, I, P, P, P, L, P, L, P, P, I, I, P, L, P, P, P, I, F, F, P, P, P, P],
     "oa_topk_fix_fill": [P, L, P, L, I, P, I, I, I, P, I, P, P, P, L, P, L, L, I, I, I, P, L, P, L,
                          P, P, P, I, F, F, I, P, P, P, P],
     "oa_waterfill": [P, P, I, I, I, P, P],
     "oa_topq": [P, L, P, L, P, I, I, I, P, I, P, P],
     "oa_topq_path": [P, L, P, L, P, I, I, I, P, I, P, I, P],
-    "oa_topq_heads": [P, L, P, L, P, I, I, I, P, I, P, P, I, P, P, P, L, I, P],
+    "oa_topq_heads": [P, L, P, L, P, I, I, I, P, I, P, P, I, P, P, P, L, P, P, L, I, P],
     "oa_residual": [P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, P, P, P, P],
     "oa_residual_flash": [P, L, P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, F, P, L,
                           I, P, P],
@@ -61,7 +61,7 @@ SIGNATURES = {
 
 # must equal oa_abi_version() of the loaded library (OA_ABI_VERSION in the header): a library
 # built from sources with other argument lists would be handed wrong pointers
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _LIB = None
 

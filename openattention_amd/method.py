@@ -27,6 +27,7 @@ G = HQ // HKV
 SC = D ** -0.5
 RMAX = 256
 SCAN_TILE = 64
+TOPQ_SEGMENT = 36 * 1024   # positions the top-q kernel holds in registers at once (36 per thread)
 
 
 class Ctx:
@@ -157,6 +158,10 @@ class OursHIP(Method):
         self.H = torch.empty(R, self.SW, device=dev, dtype=torch.int16)
         self.S = torch.empty(R, self.SW, **f32)
         self.TM = torch.empty(R, self.ntiles, **f32)
+        # tile minima of the scores, the row range top-q bins with, for rows of several top-q
+        # register segments (longer than 36864): there they spare a pass over the row
+        self.TMn = torch.empty(R, self.ntiles, **f32) if Lmax > TOPQ_SEGMENT else None
+        self.TMt = self.TM if self.TMn is not None else None
         self.score = torch.empty(R, self.Cn, **f32)
         self.n_t = torch.empty(R, self.Cn, **f32)
         self.quota = torch.empty(R, self.Cn, **f32)
@@ -276,13 +281,13 @@ class OursHIP(Method):
             # and the fill
             out.append(("qgs_scan_gate", lambda: ops.qgs_scan_gate(
                 st.codes, self.limbs, self.fexp, self.H, self.TM, n_dev, ns, nl, qr, st.Sk, st.Sk2, st.nb,
-                self.score, self.n_t, sc, qsk=self.qsk)))
+                self.score, self.n_t, sc, qsk=self.qsk, TMn=self.TMn)))
             out.append(("topk_fix_fill", lambda: ops.topk_fix_fill(
                 self.H, self.TM, n_dev, ns, nl, k_top, st.codes, self.limbs, self.fexp, qr, K, st.asg, sel,
                 st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E)))
         else:
             out.append(("qgs_scan", lambda: ops.qgs_scan_heads(st.codes, self.limbs, self.fexp, self.H, self.TM,
-                                                               n_dev, ns, nl)))
+                                                               n_dev, ns, nl, TMn=self.TMn)))
             if self.gate_mode == "fused":
                 # each row's top-k beside its pooled ErrorGate, then the correction and the fill
                 out.append(("topk_gate_fill", lambda: ops.topk_gate_fill(
@@ -295,7 +300,7 @@ class OursHIP(Method):
                     qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, self.score, self.n_t, self.quota, sc, self.E,
                     qsk=self.qsk)))
         out.append(("topq", lambda: ops.topq_heads(self.H, st.asg8, self.quota, self.exp_idx, n_dev, st.codes,
-                                                   self.limbs, self.fexp, self.S)))
+                                                   self.limbs, self.fexp, self.S, TM=self.TMt, TMn=self.TMn)))
         if self.fused:
             out.append(("residual_flash", lambda: ops.residual_flash(
                 qr, K, V, st.asg, sel, self.exp_idx, self.quota, self.n_t, st.Sk, st.Sv, self.out, sc,
@@ -396,13 +401,15 @@ class OursHIP(Method):
         Kg, Vg, qg, selg = K[ks], V[ks], qr[rs], sel[rs]
         ops.index_prep(Kg, Vg, sub, n_dev, RMAX, qg, self.limbs[ks], self.fexp[rs])
         ops.qgs_scan_heads(sub.codes, self.limbs[ks], self.fexp[rs], self.H[rs], self.TM[rs],
-                           n_dev, ns, nl)
+                           n_dev, ns, nl, TMn=None if self.TMn is None else self.TMn[rs])
         ops.topk_select_heads(self.H[rs], self.TM[rs], selg, n_dev, ns, nl, k_top, sub.codes,
                               self.limbs[ks], self.fexp[rs])
         ops.gate_fill(qg, Kg, sub.asg, selg, sub.Sk, sub.Sk2, sub.nb, self.score[rs], self.n_t[rs],
                       self.quota[rs], self.sm_scale, self.E, qsk=self.qsk[rs])
         ops.topq_heads(self.H[rs], sub.asg8, self.quota[rs], self.exp_idx[rs], n_dev, sub.codes,
-                       self.limbs[ks], self.fexp[rs], self.S[rs])
+                       self.limbs[ks], self.fexp[rs], self.S[rs],
+                       TM=None if self.TMn is None else self.TM[rs],
+                       TMn=None if self.TMn is None else self.TMn[rs])
         if self.fused:
             ops.residual_flash(qg, Kg, Vg, sub.asg, selg, self.exp_idx[rs], self.quota[rs],
                                self.n_t[rs], sub.Sk, sub.Sv, self.out[rs], self.sm_scale, qsk=self.qsk[rs])

@@ -260,9 +260,10 @@ def topk_select(S, TM, sel, n_dev, ns: int, nl: int, k_top: int) -> None:
              _ptr(sel), sel.stride(0), _ptr(n_dev), ns, nl, k_top, _stream(dev))
 
 
-def qgs_scan_heads(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int) -> None:
+def qgs_scan_heads(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int, TMn=None) -> None:
     """The scan writing 16-bit key heads of the scores (int16 tensor H, raw bits) instead of
-    fp32 scores; TM (exact tile maxima) as oa_qgs_scan."""
+    fp32 scores; TM (exact tile maxima) as oa_qgs_scan; TMn (optional, like TM): each tile's
+    least finite score (+inf without one), the range topq_heads bins with."""
     dev = _dev(codes, limbs, fexp, H, TM, n_dev)
     if H.dtype != torch.int16:
         raise ValueError("H must be int16 (16-bit key heads)")
@@ -270,11 +271,19 @@ def qgs_scan_heads(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int) -> None:
     _chk(codes, "codes", torch.int8, (BH, Lmax, RANK_Q), contiguous=True)
     _chk(H, "H", torch.int16, (GROUP * BH, -Lmax))
     _chk(TM, "TM", torch.float32, (GROUP * BH, None))
+    _tile_min(TM, TMn)
     _chk(limbs, "limbs", torch.int8, (BH, 16, RANK_Q), contiguous=True)
     _chk(fexp, "fexp", torch.int32, (GROUP * BH,), contiguous=True)
     _chk(n_dev, "n_dev", torch.int32)
     lib.call("oa_qgs_scan_heads", _ptr(codes), BH, Lmax, rq, _ptr(limbs), _ptr(fexp), _ptr(H),
-             H.stride(0), _ptr(TM), TM.stride(0), _ptr(n_dev), ns, nl, _stream(dev))
+             H.stride(0), _ptr(TM), TM.stride(0), _ptr(TMn), _ptr(n_dev), ns, nl, _stream(dev))
+
+
+def _tile_min(TM, TMn) -> None:
+    """TMn, when given, is laid out as TM (same shape and row stride)."""
+    if TMn is not None and (TMn.dtype != torch.float32 or TMn.shape != TM.shape
+                            or TMn.stride() != TM.stride() or TMn.device != TM.device):
+        raise ValueError("TMn must be a float32 tensor with TM's shape, strides and device")
 
 
 def topk_select_heads(H, TM, sel, n_dev, ns: int, nl: int, k_top: int, codes, limbs, fexp) -> None:
@@ -353,7 +362,7 @@ def topk_gate_fill(H, TM, n_dev, ns: int, nl: int, k_top: int, codes, limbs, fex
 
 
 def qgs_scan_gate(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int, q, Sk, Sk2, nb, score, n_t,
-                  sm_scale: float, qsk=None) -> None:
+                  sm_scale: float, qsk=None, TMn=None) -> None:
     """qgs_scan_heads and the pooled part of the ErrorGate in one launch: score, n_t (rows, C)
     of every cluster as if it held no selected token, and q . Sk_c into qsk."""
     dev = _dev(codes, limbs, fexp, H, TM, n_dev, q, Sk, Sk2, nb, score, n_t)
@@ -362,6 +371,7 @@ def qgs_scan_gate(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int, q, Sk, Sk2
     _chk(codes, "codes", torch.int8, (BH, Lmax, RANK_Q), contiguous=True)
     _chk(H, "H", torch.int16, (GROUP * BH, -Lmax))
     _chk(TM, "TM", torch.float32, (GROUP * BH, None))
+    _tile_min(TM, TMn)
     _chk(limbs, "limbs", torch.int8, (BH, 16, RANK_Q), contiguous=True)
     _chk(fexp, "fexp", torch.int32, (GROUP * BH,), contiguous=True)
     _chk(n_dev, "n_dev", torch.int32)
@@ -373,7 +383,7 @@ def qgs_scan_gate(codes, limbs, fexp, H, TM, n_dev, ns: int, nl: int, q, Sk, Sk2
     if qsk is not None and (qsk.shape != (R, C) or qsk.dtype != torch.float32 or not qsk.is_contiguous()):
         raise ValueError("qsk must be a contiguous (rows, C) float32 tensor")
     lib.call("oa_qgs_scan_gate", _ptr(codes), BH, Lmax, rq, _ptr(limbs), _ptr(fexp), _ptr(H), H.stride(0),
-             _ptr(TM), TM.stride(0), _ptr(n_dev), ns, nl, _ptr(q), q.stride(0), _ptr(Sk), _ptr(Sk2), _ptr(nb),
+             _ptr(TM), TM.stride(0), _ptr(TMn), _ptr(n_dev), ns, nl, _ptr(q), q.stride(0), _ptr(Sk), _ptr(Sk2), _ptr(nb),
              C, float(sm_scale), float(sm_scale) * float(sm_scale), _ptr(score), _ptr(n_t), _ptr(qsk),
              _stream(dev))
 
@@ -428,10 +438,12 @@ def topq(S, asg8, quota, exp_idx, n_dev, path: int | None = None) -> None:
                  C, Lmax, _ptr(exp_idx), E, _ptr(n_dev), int(path), _stream(dev))
 
 
-def topq_heads(H, asg8, quota, exp_idx, n_dev, codes, limbs, fexp, S32, path: int = 0) -> None:
+def topq_heads(H, asg8, quota, exp_idx, n_dev, codes, limbs, fexp, S32, path: int = 0, TM=None,
+               TMn=None) -> None:
     """Within-cluster top-q over key-head rows (oa_topq_heads); S32 (fp32, rows as H) receives
     the exact scores of rows left to the key-prefix kernel.  path 2: the linear-bin kernel
-    alone; path 3: every row through the key-prefix kernel."""
+    alone; path 3: every row through the key-prefix kernel.  TM, TMn (both or neither): the
+    scan's tile maxima and minima, the row range taken from them (same result)."""
     dev = _dev(H, asg8, quota, exp_idx, n_dev, codes, limbs, fexp, S32)
     R, C = quota.shape
     Lmax = codes.shape[1]
@@ -444,9 +456,15 @@ def topq_heads(H, asg8, quota, exp_idx, n_dev, codes, limbs, fexp, S32, path: in
     _chk(limbs, "limbs", torch.int8, (R // GROUP, 16, RANK_Q), contiguous=True)
     _chk(fexp, "fexp", torch.int32, (R,), contiguous=True)
     _chk(S32, "S32", torch.float32, (R, -Lmax))
+    if (TM is None) != (TMn is None):
+        raise ValueError("TM and TMn are given together")
+    if TM is not None:
+        _chk(TM, "TM", torch.float32, (R, -((Lmax + 63) // 64)))
+        _tile_min(TM, TMn)
     lib.call("oa_topq_heads", _ptr(H), H.stride(0), _ptr(asg8), asg8.stride(0), _ptr(quota), R, C,
              Lmax, _ptr(exp_idx), E, _ptr(n_dev), _ptr(codes), codes.shape[0], _ptr(limbs),
-             _ptr(fexp), _ptr(S32), S32.stride(0), int(path), _stream(dev))
+             _ptr(fexp), _ptr(S32), S32.stride(0), _ptr(TM), _ptr(TMn),
+             TM.stride(0) if TM is not None else 0, int(path), _stream(dev))
 
 
 def residual(K, V, asg, sel, exp_idx, quota, n_t, Sk, Sv, kbar_r, vbar_r, log_n) -> None:

@@ -192,13 +192,15 @@ def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
     # the same stages over 16-bit key heads (the pipeline the decode step runs)
     H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
     TMh = torch.empty_like(TM)
+    TMnh = torch.empty_like(TM)
     selh = torch.empty_like(sel)
     S32 = torch.empty(R, ntiles * 64, device=DEV)
     exph = torch.full_like(exp_idx, 777)
     exph3 = torch.full_like(exp_idx, 777)
-    ops.qgs_scan_heads(st.codes, limbs, fexp, H, TMh, n_dev, ns, nl)
+    expht = torch.full_like(exp_idx, 777)
+    ops.qgs_scan_heads(st.codes, limbs, fexp, H, TMh, n_dev, ns, nl, TMn=TMnh)
     torch.cuda.synchronize()
-    r.update(H=H.cpu().numpy().view(np.uint16).copy(), TMh=TMh.cpu().numpy())
+    r.update(H=H.cpu().numpy().view(np.uint16).copy(), TMh=TMh.cpu().numpy(), TMnh=TMnh.cpu().numpy())
     # top-k, gate and fill in one call (one launch below 256 rows) on a copy of the heads
     Hf = H.clone()
     self_ = torch.full_like(sel, -7)
@@ -213,9 +215,11 @@ def _stages_gpu(lay, q, n, ns, nl, k, E, rmax=RMAX):
     ops.topk_select_heads(H, TMh, selh, n_dev, ns, nl, k, st.codes, limbs, fexp)
     ops.topq_heads(H, st.asg8, quota, exph, n_dev, st.codes, limbs, fexp, S32)
     ops.topq_heads(H, st.asg8, quota, exph3, n_dev, st.codes, limbs, fexp, S32, path=3)
+    ops.topq_heads(H, st.asg8, quota, expht, n_dev, st.codes, limbs, fexp, S32, TM=TMh, TMn=TMnh)
     torch.cuda.synchronize()
     r.update(H_after=H.cpu().numpy().view(np.uint16).copy(), selh=selh.cpu().numpy(),
-             exph=exph.cpu().numpy()[:, :E], exph3=exph3.cpu().numpy()[:, :E])
+             exph=exph.cpu().numpy()[:, :E], exph3=exph3.cpu().numpy()[:, :E],
+             expht=expht.cpu().numpy()[:, :E])
     r.update(S_after=S.cpu().numpy(), sel=sel.cpu().numpy(), score=score.cpu().numpy(),
              n_t=n_t.cpu().numpy(), quota=quota.cpu().numpy(), exp_idx=exp_idx.cpu().numpy()[:, :E],
              fused=(score2.cpu().numpy(), n_t2.cpu().numpy(), quota2.cpu().numpy()),
@@ -272,10 +276,16 @@ def _compare_step(lay, rho, rule, step_q=None, n=None, tag=""):
     # and expanded sets (also with every row through the exact-score rows and key-prefix kernel)
     assert np.array_equal(g["H"][:, :n], score_heads(ref["S"][:, :n])), "score heads differ"
     assert np.array_equal(g["TMh"][:, :ntile_n], tm_ref)
+    # tile minima of the finite scores (+inf for a tile without one)
+    Sf = np.full((S.shape[0], ntile_n * 64), np.inf, np.float32)
+    Sf[:, :n] = np.where(S > -np.inf, S, np.inf)
+    assert np.array_equal(g["TMnh"][:, :ntile_n], Sf.reshape(S.shape[0], ntile_n, 64).min(-1)), \
+        "tile minima differ"
     assert np.array_equal(g["selh"], ref["sel"]), "top-k over heads differs"
     assert np.all(np.take_along_axis(g["H_after"], g["selh"].astype(np.int64), 1) == 0x007F)
     assert np.array_equal(g["exph"], ref["exp_idx"]), "top-q over heads differs"
     assert np.array_equal(g["exph3"], ref["exp_idx"]), "top-q over heads (key-prefix) differs"
+    assert np.array_equal(g["expht"], ref["exp_idx"]), "top-q over heads (tile range) differs"
     # top-k + gate + fill in one call: the same selection, marked heads, gate and fill outputs
     t = g["tgf"]
     assert np.array_equal(t["sel"], ref["sel"]), "top-k + gate + fill: selection differs"
@@ -651,7 +661,8 @@ def test_small_batch_fused_launches(N, C, k_top):
     and quotas; the one-launch top-q (7/8-, 6/7- and 5/6-bit histogram pairs, 8 / 16 / 36
     positions per thread) gives the restatement's expanded sets on its linear path (path 0), with
     every row in its key-prefix branch (path 3), and the standalone linear kernel (path 2) agrees
-    on every row it does not mark."""
+    on every row it does not mark; path 0 and 3 again with the row range from the scan's tile
+    maxima and minima."""
     print(f"[case] small-batch fused N={N} C={C} k={k_top}", flush=True)
     lay = build_layer(cfg=2, B=1, N=N, Lmax=N + 64, C=C, n_centers=256, dev=DEV)
     st = lay.st
@@ -671,7 +682,8 @@ def test_small_batch_fused_launches(N, C, k_top):
     ops.qgs_prep(qr, st.U, st.scale, limbs, fexp, zq)
     H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
     TM = torch.empty(R, ntiles, device=DEV)
-    ops.qgs_scan_heads(st.codes, limbs, fexp, H, TM, n_dev, ns, nl)
+    TMn = torch.empty(R, ntiles, device=DEV)
+    ops.qgs_scan_heads(st.codes, limbs, fexp, H, TM, n_dev, ns, nl, TMn=TMn)
     got = {}
     for fused in (False, True):
         Hx = H.clone()
@@ -695,13 +707,17 @@ def test_small_batch_fused_launches(N, C, k_top):
     Hq, quota = got[True]["Ht"], got[True]["quota_t"]
     S32 = torch.empty(R, ntiles * 64, device=DEV)
     e = {}
-    for path in (0, 2, 3):
+    for path in (0, 2, 3, "t0", "t3"):
         ex = torch.full((R, E), 777, device=DEV, dtype=torch.int32)
-        ops.topq_heads(Hq, st.asg8, quota, ex, n_dev, st.codes, limbs, fexp, S32, path=path)
+        tiles = dict(TM=TM, TMn=TMn) if isinstance(path, str) else {}
+        ops.topq_heads(Hq, st.asg8, quota, ex, n_dev, st.codes, limbs, fexp, S32,
+                       path=int(str(path)[-1]), **tiles)
         torch.cuda.synchronize()
         e[path] = ex.cpu().numpy()
     assert np.array_equal(e[0], ref["exp_idx"]), "one-launch top-q (path 0) differs"
     assert np.array_equal(e[3], ref["exp_idx"]), "one-launch top-q, key-prefix branch (path 3) differs"
+    assert np.array_equal(e["t0"], ref["exp_idx"]), "top-q with the scan's tile range (path 0) differs"
+    assert np.array_equal(e["t3"], ref["exp_idx"]), "top-q with the tile range, key-prefix branch differs"
     done = e[2][:, 0] != -2
     assert np.array_equal(e[2][done], ref["exp_idx"][done]), "linear-bin kernel alone differs"
 
@@ -1153,16 +1169,17 @@ def test_split_gate_equals_whole_gate(B, N, rho):
     for mode in ("whole", "split", "fused"):
         H = torch.empty(R, ntiles * 64, device=DEV, dtype=torch.int16)
         TM = torch.empty(R, ntiles, device=DEV)
+        TMn = torch.full((R, ntiles), float("nan"), device=DEV)     # tile minima: whole and split
         sel = torch.full((R, ns + nl + k), -7, device=DEV, dtype=torch.int32)
         score, n_t, quota, qsk = (torch.full((R, C), float("nan"), device=DEV) for _ in range(4))
         if mode == "whole":
-            ops.qgs_scan_heads(st.codes, limbs, fexp, H, TM, n_dev, ns, nl)
+            ops.qgs_scan_heads(st.codes, limbs, fexp, H, TM, n_dev, ns, nl, TMn=TMn)
             H0 = H.clone()
             ops.topk_select_heads(H, TM, sel, n_dev, ns, nl, k, st.codes, limbs, fexp)
             ops.gate_fill(qr, K, st.asg, sel, st.Sk, st.Sk2, st.nb, score, n_t, quota, SC, E, qsk=qsk)
         elif mode == "split":
             ops.qgs_scan_gate(st.codes, limbs, fexp, H, TM, n_dev, ns, nl, qr, st.Sk, st.Sk2, st.nb, score, n_t,
-                              SC, qsk=qsk)
+                              SC, qsk=qsk, TMn=TMn)
             H0 = H.clone()
             ops.topk_fix_fill(H, TM, n_dev, ns, nl, k, st.codes, limbs, fexp, qr, K, st.asg, sel, st.Sk, st.Sk2,
                               st.nb, score, n_t, quota, SC, E)
@@ -1174,10 +1191,11 @@ def test_split_gate_equals_whole_gate(B, N, rho):
         torch.cuda.synchronize()
         res[mode] = {name: t.cpu().numpy() for name, t in (("H0", H0), ("H", H), ("TM", TM), ("sel", sel),
                                                             ("score", score), ("n_t", n_t), ("quota", quota),
-                                                            ("qsk", qsk))}
+                                                            ("qsk", qsk), ("TMn", TMn))}
     for other in ("split", "fused"):
         for name in ("H0", "H", "TM", "sel", "score", "n_t", "quota", "qsk"):
             a, b = res["whole"][name], res[other][name]
             assert np.array_equal(a, b, equal_nan=False), f"{other}: {name} differs"
+    assert np.array_equal(res["whole"]["TMn"], res["split"]["TMn"]), "split: tile minima differ"
     hits = (res["split"]["sel"] >= 0).sum()
     print(f"  bit-exact over {R} rows ({hits} selected tokens)", flush=True)

@@ -34,7 +34,7 @@ def test_binding_matches_header():
 
 def test_library_loads_and_reports():
     L = lib.load()
-    assert L.oa_abi_version() == lib.ABI_VERSION == 4
+    assert L.oa_abi_version() == lib.ABI_VERSION == 5
     assert b"invalid argument" in L.oa_error_string(-22)
     for name in lib.SIGNATURES:
         assert getattr(L, name) is not None
@@ -50,6 +50,10 @@ def test_argument_checks_reject_before_launch():
     assert L.oa_waterfill(None, None, 4, 300, 10, None, None) == -22          # C > 256
     assert L.oa_topk_select(None, 0, None, 0, 4, 10, None, 5, None, 0, 0, 20, None) == -22   # k > tiles
     assert L.oa_qgs_prep(None, 0, None, None, 32, 8, 128, 16, None, None, None, None) == -22  # rank 16
+    # top-q over heads: the scan's tile maxima without its tile minima (or the reverse)
+    for tm, tmn in ((16, None), (None, 16)):
+        assert L.oa_topq_heads(16, 64, 16, 64, 16, 4, 8, 64, 16, 8, 16, 16, 1, 16, 16, 16, 64, tm, tmn, 1, 0,
+                               None) == -22
 
 
 def test_noalloc_flash_rejects_oversized_request_before_launch():
