@@ -111,7 +111,7 @@ KERNELS = {"index_prep": ["index_prep_kernel"],
            "qgs_scan": ["qgs_scan_kernel"], "topk_select": ["topk_select_reg_kernel"],
            "gate_fill": ["errorgate_kernel", "waterfill_kernel"],
            "topk_gate_fill": ["topk_gate2_fill_kernel"],
-           "topq": ["topq_linear_kernel", "topq_row_kernel"],
+           "topq": ["topq_linear_kernel", "topq_marked_kernel"],
            "qgs_scan_gate": ["qgs_scan_gate_kernel"],
            "topk_fix_fill": ["topk_fix_fill_kernel"],
            "residual_flash": ["resflash_kernel"]}
