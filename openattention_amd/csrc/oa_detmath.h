@@ -43,6 +43,34 @@ __device__ __forceinline__ double det_exp(double x) {
   return ldexp(p, (int)k);
 }
 
+// det_exp without branches, the same bits for every input: the polynomial runs on x clamped into
+// the finite range (x itself there) and the out-of-range results are selected afterwards, so the
+// lanes of a wave that hold different x never split the wave
+__device__ __forceinline__ double det_exp_v(double x) {
+  const double xc = fmin(fmax(x, -745.2), 709.782712893384);
+  const double k = rint(xc * 0x1.71547652b82fep+0);
+  double r = fma(-k, 0x1.62e42fee00000p-1, xc);
+  r = fma(-k, 0x1.a39ef35793c76p-33, r);
+  double p = 0x1.6124613a86d09p-33;
+  p = fma(p, r, 0x1.1eed8eff8d898p-29);
+  p = fma(p, r, 0x1.ae64567f544e4p-26);
+  p = fma(p, r, 0x1.27e4fb7789f5cp-22);
+  p = fma(p, r, 0x1.71de3a556c734p-19);
+  p = fma(p, r, 0x1.a01a01a01a01ap-16);
+  p = fma(p, r, 0x1.a01a01a01a01ap-13);
+  p = fma(p, r, 0x1.6c16c16c16c17p-10);
+  p = fma(p, r, 0x1.1111111111111p-7);
+  p = fma(p, r, 0x1.5555555555555p-5);
+  p = fma(p, r, 0x1.5555555555555p-3);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  double e = ldexp(p, (int)k);
+  e = x > 709.782712893384 ? __longlong_as_double(0x7ff0000000000000LL) : e;
+  e = x < -745.2 ? 0.0 : e;
+  return x != x ? x : e;
+}
+
 __device__ __forceinline__ double det_log(double x) {
   if (x != x) return x;
   if (x < 0.0) return __longlong_as_double(0x7ff8000000000000LL);

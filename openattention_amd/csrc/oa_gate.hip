@@ -244,13 +244,15 @@ __device__ __forceinline__ void fill_prologue(const float* score_row, const floa
 // quotas floor(min(n_b, lambda w_b)) at the final lo, leftover tokens one each to the live
 // clusters with room in score order (dead clusters as -inf), ties to the lower id.
 //
-// The leftover order is a radix select: every cluster with room has the distinct 40-bit key
-// (order-preserving key of its score << 8) | (255 - id), larger = earlier; the rem-th largest
-// key is found bit by bit from the top (40 wave-wide counts), and the clusters at or above it
-// take one more token -- the same set as ranking every cluster against every other.
+// The leftover order: every cluster with room has the distinct 40-bit key (order-preserving key
+// of its score << 8) | (255 - id), larger = earlier, and the rem largest keys take one more
+// token.  With one cluster per lane (C <= 64) each lane counts the keys above its own (every
+// lane's key staged in s_key, keys of clusters without room as 0, which no key is below); with
+// more, the rem-th largest key is found bit by bit from the top (40 wave-wide counts).  Both
+// give the set that ranking every cluster against every other gives.
 template <int NS>
 __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, double budget, int lane,
-                                              float* quota_row) {
+                                              float* quota_row, unsigned long long* s_key) {
   double qv[NS];
   const double el = oa::det_exp(f.lo);
   for (int j = 0; j < NS; ++j) {
@@ -272,10 +274,29 @@ __device__ __forceinline__ void fill_epilogue(const FillState<NS>& f, int C, dou
     const unsigned kf = f.ok[j] ? oa::float_key(sf == 0.f ? 0.f : sf) : 0u;
     room[j] = c < C && qv[j] < f.cap[j] && kf != 0xffffffffu;
     u[j] = ((unsigned long long)kf << 8) | (unsigned long long)(255 - (c & 255));
-    total += __popcll(__ballot(room[j]));
+    if (NS > 1) total += __popcll(__ballot(room[j]));
+  }
+  const bool any = rem > 0.0;
+  if (NS == 1) {
+    const unsigned long long mk = room[0] ? u[0] : 0ull;
+    s_key[lane] = mk;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(s_key);
+    int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll 2
+    for (int i = 0; i < 32; i += 2) {
+      const ulonglong2 x = kp[i], y = kp[i + 1];
+      c0 += x.x > mk ? 1 : 0;
+      c1 += x.y > mk ? 1 : 0;
+      c2 += y.x > mk ? 1 : 0;
+      c3 += y.y > mk ? 1 : 0;
+    }
+    const double rank = (double)((c0 + c1) + (c2 + c3));
+    if (lane < C) quota_row[lane] = (float)(qv[0] + ((any && room[0] && rank < rem) ? 1.0 : 0.0));
+    return;
   }
   unsigned long long t = 0ull;                      // keys >= t get one more
-  bool any = rem > 0.0;
   if (any && rem < (double)total) {
     int need = (int)rem;
     for (int bit = 39; bit >= 0; --bit) {
@@ -328,7 +349,7 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
   fill_prologue<NS>(score_row, nt_row, C, lane, f);
   // the tail fits the budget: every quota is its cap, the bisection's result is not used
   if (!(f.tot > budget)) {
-    fill_epilogue<NS>(f, C, budget, lane, quota_row);
+    fill_epilogue<NS>(f, C, budget, lane, quota_row, reinterpret_cast<unsigned long long*>(s_cw));
     return;
   }
   // 8 lanes per probe node: each lane then adds only 8 canonical lane partials, and a round's
@@ -472,7 +493,7 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
         mid = 0.5 * (nlo + nhi);
       }
     }
-    const unsigned long long gt = __ballot(probe(oa::det_exp(mid)) > budget);
+    const unsigned long long gt = __ballot(probe(oa::det_exp_v(mid)) > budget);
     int nd = 1, lo_nd = 0, hi_nd = 0;
     for (int k = 0; k < d; ++k) {
       if ((gt >> (nd * P)) & 1ull) { hi_nd = nd; nd = 2 * nd; }
@@ -485,7 +506,7 @@ __device__ __forceinline__ void waterfill_row(const float* score_row, const floa
   f.lo = lo;
   f.hi = hi;
   // ---- quotas, leftover tokens by score order
-  fill_epilogue<NS>(f, C, budget, lane, quota_row);
+  fill_epilogue<NS>(f, C, budget, lane, quota_row, reinterpret_cast<unsigned long long*>(s_cw));
 }
 
 // one row per wave: the fill is a serial chain, so rows (not lanes) carry the parallelism
