@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define OA_ABI_VERSION 5
+#define OA_ABI_VERSION 6
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
@@ -376,11 +376,12 @@ int oa_qgs_codes(const void* K, long k_stride_h, long k_stride_t, int kv_rows, i
                  uint32_t* amax_ws, void* stream);
 
 /*
- * QGC projection zP = bf16(k W) - colmean on the bf16 matrix cores; colmean = mean over the T
- * tokens of bf16(k W) (fp64 tile sums in a fixed order).  W (rows, 128, 16) bf16 (per query
- * row); zP (rows, zp_stride) fp32 with zp_stride >= 16 T; colmean (rows, 16); tile_ws
- * (rows * ceil(T/64) * 16) fp64 scratch; zraw_out (rows, zp_stride) bf16 bits of k W, or NULL.
- * Replaces the projection of inference/ours_fastbuild.py:264-275 and methods_eager.py:526-531.
+ * QGC projection bf16(k W) on the bf16 matrix cores and colmean = mean over the T tokens of
+ * bf16(k W) (fp64 tile sums in a fixed order); zP = bf16(k W) - colmean.  W (rows, 128, 16)
+ * bf16 (per query row); zraw_out (rows, zp_stride) the bf16 bits of k W (what the k-means entry
+ * points read), zP (rows, zp_stride) fp32, either may be NULL but not both; zp_stride >= 16 T;
+ * colmean (rows, 16); tile_ws (rows * ceil(T/64) * 16) fp64 scratch.  Replaces the projection
+ * of inference/ours_fastbuild.py:264-275 and methods_eager.py:526-531.
  */
 int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, int rows, int G, int T,
                    const void* W, float* zP, long zp_stride, float* colmean, double* tile_ws,
@@ -388,20 +389,27 @@ int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, int rows, in
 
 /*
  * k-means assignment: asg_t = argmax_c bf16(bf16(bf16(zP_t) . bf16(c)) - bf16(|c|^2 / 2)), ties
- * to the lower cluster, written as int32 and uint8.  cent (rows, C, 16) fp32.  Replaces
- * _k_km_assign (inference/ours_fastbuild.py:52-82) and methods_eager.py:536-540.
+ * to the lower cluster, written as int32 and uint8; zP_t = zraw_t - colmean (fp32, formed from
+ * the stored bf16 projection).  zraw (rows, z_stride) as oa_qgc_project writes it; cent
+ * (rows, C, 16) fp32.  Replaces _k_km_assign (inference/ours_fastbuild.py:52-82) and
+ * methods_eager.py:536-540.
  */
-int oa_kmeans_assign(const float* zP, long zp_stride, int rows, int T, const float* cent, int C,
-                     int32_t* asg, long asg_stride, uint8_t* asg8, long asg8_stride, void* stream);
+int oa_kmeans_assign(const uint16_t* zraw, const float* colmean, long z_stride, int rows, int T,
+                     const float* cent, int C, int32_t* asg, long asg_stride, uint8_t* asg8,
+                     long asg8_stride, void* stream);
 
 /*
  * k-means update: centroid = mean of the members' zP rows (fp64 sum in position order, one
- * rounding), or zP[init_idx[c]] for an empty cluster; cnt_out (rows, C) member counts or NULL.
- * Replaces _k_km_update (inference/ours_fastbuild.py:85-108) and methods_eager.py:541-547.
+ * rounding), or zP[init_idx[c]] for an empty cluster; zP = zraw - colmean as in
+ * oa_kmeans_assign; cnt_out (rows, C) member counts or NULL.  mem_ws (rows, mem_stride >= T),
+ * cstart_ws, clen_ws (rows, C) int32 receive the assignment's member lists (the layout
+ * oa_cluster_build writes) on the way.  Replaces _k_km_update (inference/ours_fastbuild.py:85-108)
+ * and methods_eager.py:541-547.
  */
-int oa_kmeans_update(const float* zP, long zp_stride, int rows, int T, const uint8_t* asg8,
-                     long asg8_stride, int C, const int32_t* init_idx, float* cent, float* cnt_out,
-                     void* stream);
+int oa_kmeans_update(const uint16_t* zraw, const float* colmean, long z_stride, int rows, int T,
+                     const uint8_t* asg8, long asg8_stride, int C, const int32_t* init_idx,
+                     float* cent, float* cnt_out, int32_t* mem_ws, long mem_stride,
+                     int32_t* cstart_ws, int32_t* clen_ws, void* stream);
 
 /*
  * Cluster statistics and CSR member lists: nb = member count, Sk = sum k, Sk2 = sum k*k,

@@ -171,10 +171,10 @@ __global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = t0 + 4 * (lane >> 4) + i;
-      const uint16_t hb = oa::f32_to_bf16(acc[i]);
+      const uint16_t hb = oa::f32_to_bf16_rn(acc[i]);
       const float v = oa::bf16_to_f32(hb);
       if (t < T) {
-        zP[(long)row * zps + (long)t * kRC + (lane & 15)] = v;
+        if (zP) zP[(long)row * zps + (long)t * kRC + (lane & 15)] = v;
         if (zraw_out) zraw_out[(long)row * zps + (long)t * kRC + (lane & 15)] = hb;
         cs += (double)v;
       }
@@ -231,7 +231,8 @@ __device__ __forceinline__ uint32_t bf16_key(uint16_t h) {
 // the lower cluster.
 constexpr int kAsgThreads = 256;
 constexpr int kAsgTiles = 32;
-__global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const float* zP, long zps, int T,
+__global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16_t* zraw,
+                                                                    const float* colmean, long zps, int T,
                                                                     const float* cent, int C,
                                                                     int32_t* asg, long as,
                                                                     uint8_t* asg8, long a8s) {
@@ -259,19 +260,23 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const float*
     s_half[c] = hv;
   }
   __syncthreads();
+  // zP = bf16(k W) - colmean, formed from the stored bf16 projection (the same fp32 values)
+  float cm[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) cm[e] = colmean[row * kRC + 4 * (lane >> 4) + e];
   const int tend = min(ntiles, (blockIdx.x + 1) * kAsgTiles);
   for (int tile = blockIdx.x * kAsgTiles + wave; tile < tend; tile += kAsgThreads / 64) {
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       const int t0 = tile * 64 + blk * 16;
       const int ta = min(t0 + (lane & 15), T - 1);
-      const float4 zv =
-          *reinterpret_cast<const float4*>(zP + (long)row * zps + (long)ta * kRC + 4 * (lane >> 4));
+      const uint2 zr =
+          *reinterpret_cast<const uint2*>(zraw + (long)row * zps + (long)ta * kRC + 4 * (lane >> 4));
       short4v a;
-      a[0] = (short)oa::f32_to_bf16(zv.x);
-      a[1] = (short)oa::f32_to_bf16(zv.y);
-      a[2] = (short)oa::f32_to_bf16(zv.z);
-      a[3] = (short)oa::f32_to_bf16(zv.w);
+      a[0] = (short)oa::f32_to_bf16_rn(__uint_as_float(zr.x << 16) - cm[0]);
+      a[1] = (short)oa::f32_to_bf16_rn(__uint_as_float(zr.x & 0xffff0000u) - cm[1]);
+      a[2] = (short)oa::f32_to_bf16_rn(__uint_as_float(zr.y << 16) - cm[2]);
+      a[3] = (short)oa::f32_to_bf16_rn(__uint_as_float(zr.y & 0xffff0000u) - cm[3]);
       uint32_t best[4] = {0u, 0u, 0u, 0u};
       for (int cb = 0; cb < CB; ++cb) {
         const int c = cb * 16 + (lane & 15);
@@ -283,8 +288,8 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const float*
         const float hf = oa::bf16_to_f32(s_half[c]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float dot = oa::bf16_to_f32(oa::f32_to_bf16(acc[i]));
-          uint16_t dist = oa::f32_to_bf16(dot - hf);
+          const float dot = oa::bf16_to_f32(oa::f32_to_bf16_rn(acc[i]));
+          uint16_t dist = oa::f32_to_bf16_rn(dot - hf);
           if ((dist & 0x7fffu) == 0) dist = 0;           // -0 ranks as +0
           const uint32_t key = c < C ? (bf16_key(dist) << 8) | (uint32_t)(255 - c) : 0u;
           best[i] = max(best[i], key);
@@ -315,78 +320,72 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const float*
   }
 }
 
-// The byte ids of positions p .. p + 3 (0xff past T; callers test p + e < T before matching).
-__device__ __forceinline__ uint32_t load_ids(const uint8_t* ar, int T, int p) {
-  if (p + 3 < T) return *reinterpret_cast<const uint32_t*>(ar + p);
-  uint32_t ids = 0xffffffffu;
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    if (p + e < T) ids = (ids & ~(0xffu << (8 * e))) | ((uint32_t)ar[p + e] << (8 * e));
-  return ids;
-}
+constexpr int kMemBuf = 2048;   // member positions staged in LDS at a time
 
-// One wave: the members of cluster c from position p0 on, in position order, appended to s_pos
-// (256 positions per step: an exclusive prefix of the per-lane counts places them) until the
-// row ends or the buffer could overflow on the next step; the next step's ids are requested
-// before this step's are matched.  Returns the number appended; p0 moves past the scanned part.
-constexpr int kMemBuf = 2048;
-__device__ __forceinline__ int gather_members(const uint8_t* ar, int T, int c, int& p0, int* s_pos,
-                                              int lane) {
-  int n = 0;
-  uint32_t ids = p0 < T ? load_ids(ar, T, p0 + 4 * lane) : 0u;
-  while (p0 < T && n <= kMemBuf - 256) {
-    const uint32_t cur = ids;
-    const int p = p0 + 4 * lane;
-    p0 += 256;
-    if (p0 < T) ids = load_ids(ar, T, p0 + 4 * lane);
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) mine += (p + e < T && (int)((cur >> (8 * e)) & 0xffu) == c) ? 1 : 0;
-    const int incl = oa::wave_incl_scan_i32(mine);
-    int o = n + incl - mine;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (p + e < T && (int)((cur >> (8 * e)) & 0xffu) == c) s_pos[o++] = p + e;
-    n += __builtin_amdgcn_readlane(incl, 63);
-  }
-  return n;
-}
-
-// One wave per (cluster, query row): the members in position order (gather_members), their zP
-// rows staged 64 at a time through LDS (one float4 per lane and member quarter, all loads of a
-// batch in flight) and summed in fp64 by lanes 0..15 (one column each) in that order;
+// One wave per (cluster, query row): the members in position order (the row's member lists of
+// csr_sort_kernel), their zP rows staged kUB at a time through LDS (the next batch requested
+// while one is summed) and summed in fp64 by lanes 0..15 (one column each) in that order;
 // centroid = fp32(sum / count), or the initial point when the cluster is empty.
-__global__ void __launch_bounds__(64) kmeans_update_kernel(const float* zP, long zps, int T,
-                                                           const uint8_t* asg8, long a8s, int C,
+__global__ void __launch_bounds__(64) kmeans_update_kernel(const uint16_t* zraw, const float* colmean,
+                                                           long zps, int C, const int32_t* mem, long ms,
+                                                           const int32_t* cstart, const int32_t* clen,
                                                            const int32_t* init_idx, float* cent,
                                                            float* cnt_out) {
+  constexpr int kUB = 128;                     // members per staged batch
   __shared__ int s_pos[kMemBuf];
-  __shared__ float4 s_stage[64 * (kRC / 4)];
+  __shared__ float4 s_stage[kUB * (kRC / 4)];
   const int lane = threadIdx.x;
-  const int c = blockIdx.x;
-  const int row = blockIdx.y;
-  const uint8_t* ar = asg8 + (long)row * a8s;
-  const float* zr = zP + (long)row * zps;
+  // the C workgroups of a row run on one XCD (workgroups are dealt to the 8 XCDs in turn), so the
+  // row's projection lines, each holding the rows of members of several clusters, are fetched
+  // into that XCD's L2 once rather than by every XCD
+  int c, row;
+  {
+    const int b = blockIdx.x, rows = gridDim.x / C;
+    if (rows % 8 == 0) {
+      const int k = b >> 3;
+      row = (k / C) * 8 + (b & 7);
+      c = k % C;
+    } else {
+      row = b / C;
+      c = b % C;
+    }
+  }
+  const int32_t* ml = mem + (long)row * ms + cstart[row * C + c];
+  const int cl = clen[row * C + c];
+  const uint16_t* zr = zraw + (long)row * zps;
+  // zP = bf16(k W) - colmean from the stored bf16 projection: this lane's quarter of a row
+  float cq[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) cq[e] = colmean[row * kRC + 4 * (lane & 3) + e];
   double acc = 0.0;
   int cnt = 0;
-  int p0 = 0;
-  while (p0 < T) {
-    const int n = gather_members(ar, T, c, p0, s_pos, lane);
+  // lane l reads member quarter l % 4 of members l / 4 + 16 b of a batch
+  auto load = [&](uint2* w, int k0, int n) {
+#pragma unroll
+    for (int b = 0; b < kUB / 16; ++b) {
+      const int m = k0 + (lane >> 2) + 16 * b;
+      w[b] = m < n ? *reinterpret_cast<const uint2*>(zr + (long)s_pos[m] * kRC + 4 * (lane & 3))
+                   : make_uint2(0u, 0u);
+    }
+  };
+  for (int i0 = 0; i0 < cl; i0 += kMemBuf) {
+    const int n = min(kMemBuf, cl - i0);
+    for (int i = lane; i < n; i += 64) s_pos[i] = ml[i0 + i];
     __syncthreads();
-    for (int k0 = 0; k0 < n; k0 += 64) {
-      float4 v[4];
+    uint2 w[kUB / 16];
+    if (n > 0) load(w, 0, n);
+    for (int k0 = 0; k0 < n; k0 += kUB) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int m = k0 + (lane >> 2) + 16 * b;
-        v[b] = m < n ? *reinterpret_cast<const float4*>(zr + (long)s_pos[m] * kRC + 4 * (lane & 3))
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int b = 0; b < 4; ++b) s_stage[((lane >> 2) + 16 * b) * 4 + (lane & 3)] = v[b];
+      for (int b = 0; b < kUB / 16; ++b)
+        s_stage[((lane >> 2) + 16 * b) * 4 + (lane & 3)] =
+            make_float4(__uint_as_float(w[b].x << 16) - cq[0], __uint_as_float(w[b].x & 0xffff0000u) - cq[1],
+                        __uint_as_float(w[b].y << 16) - cq[2], __uint_as_float(w[b].y & 0xffff0000u) - cq[3]);
       __syncthreads();
+      // the next batch's rows are requested while this one is summed
+      if (k0 + kUB < n) load(w, k0 + kUB, n);
       if (lane < kRC) {
         const float* st = reinterpret_cast<const float*>(s_stage);
-        const int mm = min(64, n - k0);
+        const int mm = min(kUB, n - k0);
         for (int m = 0; m < mm; ++m) acc += (double)st[m * kRC + lane];
       }
       __syncthreads();
@@ -394,28 +393,40 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const float* zP, long
     cnt += n;
   }
   if (lane < kRC) {
-    const float v = cnt > 0 ? (float)(acc / (double)cnt) : zr[(long)init_idx[c] * kRC + lane];
+    const float v = cnt > 0 ? (float)(acc / (double)cnt)
+                            : oa::bf16_to_f32(zr[(long)init_idx[c] * kRC + lane]) - colmean[row * kRC + lane];
     cent[((long)row * C + c) * kRC + lane] = v;
   }
   if (lane == 0 && cnt_out) cnt_out[row * C + c] = (float)cnt;
 }
 
 // ---------------------------------------------------------------------------------- sums + CSR
-// per query row: member count of every cluster, CSR start (exclusive prefix), nb
-__global__ void __launch_bounds__(256) cluster_count_kernel(int T, const uint8_t* asg8, long a8s, int C,
-                                                            float* nb, int32_t* cstart, int32_t* clen) {
-  __shared__ int s_cnt[kMaxC];
+// One 1024-thread workgroup per query row: nb, clen (member counts), cstart (exclusive prefix)
+// and mem, every cluster's members in position order (a stable counting sort of the row's ids).
+// The row is taken 1024 positions at a time, wave w holding positions 64 w .. 64 w + 63 of the
+// step.  A lane's equal-id lanes are the AND over the 8 id bits of that bit's ballot (or its
+// complement); its rank among them orders it, their count goes to LDS per (cluster, wave), and
+// a 16-lane scan per cluster turns the counts into the waves' starts in wave order -- so equal
+// ids keep their position order inside a step, and the steps follow each other.
+constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / 64;
+__global__ void __launch_bounds__(kSortThreads) csr_sort_kernel(int T, const uint8_t* asg8, long a8s, int C,
+                                                               float* nb, int32_t* cstart, int32_t* clen,
+                                                               int32_t* mem, long ms) {
+  __shared__ int s_base[kMaxC];
+  __shared__ int s_wcnt[kMaxC][kSortWaves];
   const int row = blockIdx.x;
-  for (int c = threadIdx.x; c < kMaxC; c += 256) s_cnt[c] = 0;
-  __syncthreads();
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint8_t* ar = asg8 + (long)row * a8s;
-  for (int t = threadIdx.x; t < T; t += 256) atomicAdd(&s_cnt[ar[t]], 1);
+  int32_t* mr = mem + (long)row * ms;
+  for (int c = tid; c < kMaxC; c += kSortThreads) s_base[c] = 0;
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
+  for (int t = tid; t < T; t += kSortThreads) atomicAdd(&s_base[ar[t]], 1);
+  __syncthreads();
+  if (wave == 0) {
     int v[4], loc = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { v[i] = s_cnt[lane * 4 + i]; loc += v[i]; }
+    for (int i = 0; i < 4; ++i) { v[i] = s_base[lane * 4 + i]; loc += v[i]; }
     const int incl = oa::wave_incl_scan_i32(loc);
     int run = incl - loc;
 #pragma unroll
@@ -424,37 +435,68 @@ __global__ void __launch_bounds__(256) cluster_count_kernel(int T, const uint8_t
       if (c < C) {
         cstart[row * C + c] = run;
         clen[row * C + c] = v[i];
-        nb[row * C + c] = (float)v[i];
+        if (nb) nb[row * C + c] = (float)v[i];
       }
+      s_base[c] = run;
       run += v[i];
     }
   }
+  const unsigned long long lower = (1ull << lane) - 1ull;
+  for (int p0 = 0; p0 < T; p0 += kSortThreads) {
+    for (int i = tid; i < kSortWaves * kMaxC; i += kSortThreads) (&s_wcnt[0][0])[i] = 0;
+    __syncthreads();
+    const int p = p0 + tid;
+    const bool valid = p < T;
+    const int x = valid ? (int)ar[p] : 0;
+    unsigned long long m = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const unsigned long long bb = __ballot((x >> bit) & 1);
+      m &= ((x >> bit) & 1) ? bb : ~bb;
+    }
+    const int rank = __popcll(m & lower);
+    if (valid && rank == 0) s_wcnt[x][wave] = __popcll(m);
+    __syncthreads();
+    // the waves' starts per cluster: thread (c, w) of 16-lane groups, an inclusive scan over w
+    for (int e = tid; e < C * kSortWaves; e += kSortThreads) {
+      const int c = e >> 4, w = e & 15;
+      const int v = s_wcnt[c][w];
+      int incl = v;
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, true);   // row_shr:1
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, true);   // row_shr:2
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, true);   // row_shr:4
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, true);   // row_shr:8
+      const int base = s_base[c];
+      s_wcnt[c][w] = base + incl - v;
+      if (w == kSortWaves - 1) s_base[c] = base + incl;
+    }
+    __syncthreads();
+    if (valid) mr[s_wcnt[x][wave] + rank] = p;
+    __syncthreads();
+  }
 }
 
-// One wave per (cluster, query row): members in position order (gather_members) -> mem[cstart + i],
-// and the fp64 sums of k, k*k and v over them in that order (lane l: dims 2l, 2l + 1), the K and
-// V words of 16 members requested together.
+// One wave per (cluster, query row): the fp64 sums of k, k*k and v over the members in position
+// order (mem, written by csr_sort_kernel; lane l: dims 2l, 2l + 1), the K and V words of 16
+// members requested together.
 __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, const uint16_t* V, long ksh,
-                                                          long kst, int G, int T, const uint8_t* asg8,
-                                                          long a8s, int C, const int32_t* cstart,
-                                                          float* Sk, float* Sk2, float* Sv, int32_t* mem,
-                                                          long ms) {
+                                                          long kst, int G, int C, const int32_t* cstart,
+                                                          const int32_t* clen, float* Sk, float* Sk2,
+                                                          float* Sv, const int32_t* mem, long ms) {
   __shared__ int s_pos[kMemBuf];
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
   const int row = blockIdx.y;
-  const uint8_t* ar = asg8 + (long)row * a8s;
   const uint16_t* kr = K + (long)(row / G) * ksh + 2 * lane;
   const uint16_t* vr = V + (long)(row / G) * ksh + 2 * lane;
-  int32_t* mr = mem + (long)row * ms + cstart[row * C + c];
+  const int32_t* ml = mem + (long)row * ms + cstart[row * C + c];
+  const int cl = clen[row * C + c];
   double k0 = 0.0, k1 = 0.0, q0 = 0.0, q1 = 0.0, v0 = 0.0, v1 = 0.0;
-  int cnt = 0;
-  int p0 = 0;
   constexpr int U = 16;
-  while (p0 < T) {
-    const int n = gather_members(ar, T, c, p0, s_pos, lane);
+  for (int i0 = 0; i0 < cl; i0 += kMemBuf) {
+    const int n = min(kMemBuf, cl - i0);
+    for (int i = lane; i < n; i += 64) s_pos[i] = ml[i0 + i];
     __syncthreads();
-    for (int m = lane; m < n; m += 64) mr[cnt + m] = s_pos[m];
     for (int k = 0; k < n; k += U) {
       uint32_t kw[U], vw[U];
 #pragma unroll
@@ -474,7 +516,6 @@ __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, con
         }
       }
     }
-    cnt += n;
     __syncthreads();
   }
   const long o = ((long)row * C + c) * kD + 2 * lane;
@@ -507,9 +548,10 @@ extern "C" int oa_qgs_codes(const void* K, long k_stride_h, long k_stride_t, int
 extern "C" int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, int rows, int G, int T,
                               const void* W, float* zP, long zp_stride, float* colmean,
                               double* tile_ws, uint16_t* zraw_out, void* stream) {
-  if (rows <= 0 || G <= 0 || rows % G || T <= 0 || !K || !W || !zP || !colmean || !tile_ws ||
-      k_stride_t < kD || k_stride_t % 8 || k_stride_h % 8 || zp_stride < (long)T * kRC ||
-      zp_stride % 4 || (reinterpret_cast<uintptr_t>(K) & 15) || (reinterpret_cast<uintptr_t>(zP) & 15))
+  if (rows <= 0 || G <= 0 || rows % G || T <= 0 || !K || !W || (!zP && !zraw_out) || !colmean ||
+      !tile_ws || k_stride_t < kD || k_stride_t % 8 || k_stride_h % 8 || zp_stride < (long)T * kRC ||
+      zp_stride % 4 || (reinterpret_cast<uintptr_t>(K) & 15) || (reinterpret_cast<uintptr_t>(zP) & 15) ||
+      (reinterpret_cast<uintptr_t>(zraw_out) & 7))
     return OA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   const int ntiles = (T + 63) / 64;
@@ -517,34 +559,40 @@ extern "C" int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, i
                      reinterpret_cast<const uint16_t*>(K), k_stride_h, k_stride_t, G, T,
                      reinterpret_cast<const uint16_t*>(W), zP, zp_stride, zraw_out, tile_ws, ntiles);
   hipLaunchKernelGGL(qgc_colmean_kernel, dim3(rows), dim3(64), 0, s, T, tile_ws, ntiles, colmean);
-  const int nb = std::min(16, (T * (kRC / 4) + 255) / 256);
-  hipLaunchKernelGGL(qgc_center_kernel, dim3(nb, rows), dim3(256), 0, s, zP, zp_stride, T, colmean);
+  if (zP) {
+    const int nb = std::min(16, (T * (kRC / 4) + 255) / 256);
+    hipLaunchKernelGGL(qgc_center_kernel, dim3(nb, rows), dim3(256), 0, s, zP, zp_stride, T, colmean);
+  }
   return OA_LAUNCH_STATUS();
 }
 
-extern "C" int oa_kmeans_assign(const float* zP, long zp_stride, int rows, int T, const float* cent,
-                                int C, int32_t* asg, long asg_stride, uint8_t* asg8, long asg8_stride,
-                                void* stream) {
-  if (rows <= 0 || T <= 0 || C <= 0 || C > kMaxC || !zP || !cent || !asg || !asg8 ||
-      zp_stride < (long)T * kRC || zp_stride % 4 || asg_stride < T || asg8_stride < T ||
-      (reinterpret_cast<uintptr_t>(zP) & 15))
+extern "C" int oa_kmeans_assign(const uint16_t* zraw, const float* colmean, long z_stride, int rows,
+                                int T, const float* cent, int C, int32_t* asg, long asg_stride,
+                                uint8_t* asg8, long asg8_stride, void* stream) {
+  if (rows <= 0 || T <= 0 || C <= 0 || C > kMaxC || !zraw || !colmean || !cent || !asg || !asg8 ||
+      z_stride < (long)T * kRC || z_stride % 4 || asg_stride < T || asg8_stride < T ||
+      (reinterpret_cast<uintptr_t>(zraw) & 7))
     return OA_EINVAL;
   const int ntiles = (T + 63) / 64;
   hipLaunchKernelGGL(kmeans_assign_kernel, dim3((ntiles + kAsgTiles - 1) / kAsgTiles, rows),
-                     dim3(kAsgThreads), 0, (hipStream_t)stream, zP, zp_stride, T, cent, C, asg,
+                     dim3(kAsgThreads), 0, (hipStream_t)stream, zraw, colmean, z_stride, T, cent, C, asg,
                      asg_stride, asg8, asg8_stride);
   return OA_LAUNCH_STATUS();
 }
 
-extern "C" int oa_kmeans_update(const float* zP, long zp_stride, int rows, int T, const uint8_t* asg8,
-                                long asg8_stride, int C, const int32_t* init_idx, float* cent,
-                                float* cnt_out, void* stream) {
-  if (rows <= 0 || T <= 0 || C <= 0 || C > kMaxC || !zP || !asg8 || !init_idx || !cent ||
-      zp_stride < (long)T * kRC || zp_stride % 4 || (reinterpret_cast<uintptr_t>(zP) & 15) ||
-      asg8_stride < T || asg8_stride % 4 || (reinterpret_cast<uintptr_t>(asg8) & 3))
+extern "C" int oa_kmeans_update(const uint16_t* zraw, const float* colmean, long z_stride, int rows,
+                                int T, const uint8_t* asg8, long asg8_stride, int C,
+                                const int32_t* init_idx, float* cent, float* cnt_out, int32_t* mem_ws,
+                                long mem_stride, int32_t* cstart_ws, int32_t* clen_ws, void* stream) {
+  if (rows <= 0 || T <= 0 || C <= 0 || C > kMaxC || !zraw || !colmean || !asg8 || !init_idx || !cent ||
+      !mem_ws || !cstart_ws || !clen_ws || mem_stride < T || z_stride < (long)T * kRC ||
+      z_stride % 4 || (reinterpret_cast<uintptr_t>(zraw) & 7) || asg8_stride < T)
     return OA_EINVAL;
-  hipLaunchKernelGGL(kmeans_update_kernel, dim3(C, rows), dim3(64), 0, (hipStream_t)stream, zP, zp_stride,
-                     T, asg8, asg8_stride, C, init_idx, cent, cnt_out);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(csr_sort_kernel, dim3(rows), dim3(kSortThreads), 0, s, T, asg8, asg8_stride, C,
+                     nullptr, cstart_ws, clen_ws, mem_ws, mem_stride);
+  hipLaunchKernelGGL(kmeans_update_kernel, dim3(C * rows), dim3(64), 0, s, zraw, colmean, z_stride, C,
+                     mem_ws, mem_stride, cstart_ws, clen_ws, init_idx, cent, cnt_out);
   return OA_LAUNCH_STATUS();
 }
 
@@ -554,16 +602,14 @@ extern "C" int oa_cluster_build(const void* K, const void* V, long kv_stride_h, 
                                 int32_t* cstart, int32_t* clen, void* stream) {
   if (rows <= 0 || G <= 0 || rows % G || T <= 0 || C <= 0 || C > kMaxC || !K || !V || !asg8 || !nb ||
       !Sk || !Sk2 || !Sv || !mem || !cstart || !clen || kv_stride_t < kD || kv_stride_t % 2 ||
-      kv_stride_h % 2 || asg8_stride < T || asg8_stride % 4 || mem_stride < T ||
-      (reinterpret_cast<uintptr_t>(asg8) & 3) || (reinterpret_cast<uintptr_t>(K) & 3) ||
+      kv_stride_h % 2 || asg8_stride < T || mem_stride < T || (reinterpret_cast<uintptr_t>(K) & 3) ||
       (reinterpret_cast<uintptr_t>(V) & 3))
     return OA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(cluster_count_kernel, dim3(rows), dim3(256), 0, s, T, asg8, asg8_stride, C, nb,
-                     cstart, clen);
+  hipLaunchKernelGGL(csr_sort_kernel, dim3(rows), dim3(kSortThreads), 0, s, T, asg8, asg8_stride, C, nb,
+                     cstart, clen, mem, mem_stride);
   hipLaunchKernelGGL(cluster_sums_kernel, dim3(C, rows), dim3(64), 0, s,
                      reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
-                     kv_stride_h, kv_stride_t, G, T, asg8, asg8_stride, C, cstart, Sk, Sk2, Sv, mem,
-                     mem_stride);
+                     kv_stride_h, kv_stride_t, G, C, cstart, clen, Sk, Sk2, Sv, mem, mem_stride);
   return OA_LAUNCH_STATUS();
 }

@@ -54,14 +54,14 @@ SIGNATURES = {
     "oa_dense_decode": [P, L, P, P, L, L, I, I, I, I, P, F, I, P, P, P, P, L, P],
     "oa_qgs_codes": [P, L, L, I, I, P, P, L, P, P, P],
     "oa_qgc_project": [P, L, L, I, I, I, P, P, L, P, P, P, P],
-    "oa_kmeans_assign": [P, L, I, I, P, I, P, L, P, L, P],
-    "oa_kmeans_update": [P, L, I, I, P, L, I, P, P, P, P],
+    "oa_kmeans_assign": [P, P, L, I, I, P, I, P, L, P, L, P],
+    "oa_kmeans_update": [P, P, L, I, I, P, L, I, P, P, P, P, L, P, P, P],
     "oa_cluster_build": [P, P, L, L, I, I, I, P, L, I, P, P, P, P, P, L, P, P, P],
 }
 
 # must equal oa_abi_version() of the loaded library (OA_ABI_VERSION in the header): a library
 # built from sources with other argument lists would be handed wrong pointers
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _LIB = None
 

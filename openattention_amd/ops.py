@@ -550,41 +550,57 @@ def qgs_codes(K, T: int, U, codes, scale, amax_ws) -> None:
              codes.stride(0), _ptr(scale), _ptr(amax_ws), _stream(dev))
 
 
-def qgc_project(K, T: int, W, G: int, zP, colmean, zraw=None) -> None:
-    """a12 projection: zP (HQ, T, 16) fp32 = bf16(k W) - colmean; colmean (HQ, 16); zraw
-    (HQ, T, 16) int16/bf16 view of bf16(k W) or None."""
-    dev = _dev(K, W, zP, colmean)
+def qgc_project(K, T: int, W, G: int, zraw, colmean, zP=None) -> None:
+    """a12 projection: zraw (HQ, T, 16) int16/bf16 = bf16(k W) (what kmeans_assign and
+    kmeans_update read); colmean (HQ, 16); zP (HQ, T, 16) fp32 = bf16(k W) - colmean, or None."""
+    dev = _dev(K, W, zraw, colmean)
     HQ = W.shape[0]
     _need(W.dtype == torch.bfloat16 and W.is_contiguous() and W.shape[1:] == (HEAD_DIM, RANK_C),
           "W: (HQ, 128, 16) bf16 contiguous")
     _need(K.shape[0] * G == HQ and T <= K.shape[1], "K: HQ / G rows of at least T tokens")
-    _need(zP.dtype == torch.float32 and zP.stride(2) == 1 and zP.stride(1) == RANK_C, "zP: (HQ, T, 16) fp32 rows")
+    _zraw(zraw, HQ, T)
     _need(colmean.is_contiguous() and colmean.shape == (HQ, RANK_C), "colmean: (HQ, 16) contiguous")
-    if zraw is not None:
-        _need(zraw.stride() == zP.stride() and zraw.element_size() == 2, "zraw: 16-bit, zP's strides")
+    if zP is not None:
+        _need(zP.dtype == torch.float32 and zP.stride() == zraw.stride(), "zP: fp32, zraw's strides")
     ntiles = -(-T // 64)
     ws = torch.empty(HQ * ntiles * RANK_C, device=dev, dtype=torch.float64)
     lib.call("oa_qgc_project", _ptr(K), K.stride(0), K.stride(1), HQ, G, T, _ptr(W), _ptr(zP),
-             zP.stride(0), _ptr(colmean), _ptr(ws), _ptr(zraw), _stream(dev))
+             zraw.stride(0), _ptr(colmean), _ptr(ws), _ptr(zraw), _stream(dev))
 
 
-def kmeans_assign(zP, T: int, cent, asg, asg8) -> None:
-    """a12 assignment into asg (HQ, >=T) int32 and asg8 (HQ, >=T) uint8 rows."""
-    dev = _dev(zP, cent, asg, asg8)
+def _zraw(zraw, HQ: int, T: int) -> None:
+    _need(zraw.element_size() == 2 and zraw.dim() == 3 and zraw.shape[0] == HQ and zraw.shape[1] >= T
+          and zraw.shape[2] == RANK_C and zraw.stride(2) == 1 and zraw.stride(1) == RANK_C,
+          "zraw: (HQ, >=T, 16) 16-bit rows")
+
+
+def kmeans_assign(zraw, colmean, T: int, cent, asg, asg8) -> None:
+    """a12 assignment into asg (HQ, >=T) int32 and asg8 (HQ, >=T) uint8 rows; zP = zraw - colmean
+    formed on the fly from the bf16 projection."""
+    dev = _dev(zraw, colmean, cent, asg, asg8)
     HQ, C = cent.shape[0], cent.shape[1]
+    _zraw(zraw, HQ, T)
+    _need(colmean.is_contiguous() and colmean.shape == (HQ, RANK_C), "colmean: (HQ, 16) contiguous")
     _need(cent.is_contiguous() and cent.shape[2] == RANK_C, "cent: (HQ, C, 16) contiguous")
     _need(asg.stride(1) == 1 and asg8.stride(1) == 1, "asg rows must be contiguous")
-    lib.call("oa_kmeans_assign", _ptr(zP), zP.stride(0), HQ, T, _ptr(cent), C, _ptr(asg), asg.stride(0),
-             _ptr(asg8), asg8.stride(0), _stream(dev))
+    lib.call("oa_kmeans_assign", _ptr(zraw), _ptr(colmean), zraw.stride(0), HQ, T, _ptr(cent), C, _ptr(asg),
+             asg.stride(0), _ptr(asg8), asg8.stride(0), _stream(dev))
 
 
-def kmeans_update(zP, T: int, asg8, init, cent, cnt=None) -> None:
-    """a12 update of cent (HQ, C, 16) in place; init (C,) int32 initial positions."""
-    dev = _dev(zP, asg8, init, cent)
+def kmeans_update(zraw, colmean, T: int, asg8, init, cent, mem, cstart, clen, cnt=None) -> None:
+    """a12 update of cent (HQ, C, 16) in place; init (C,) int32 initial positions; zP as in
+    kmeans_assign; mem (HQ, >=T), cstart, clen (HQ, C) int32 receive the assignment's member lists."""
+    dev = _dev(zraw, colmean, asg8, init, cent, mem, cstart, clen)
     HQ, C = cent.shape[0], cent.shape[1]
+    _zraw(zraw, HQ, T)
+    _need(colmean.is_contiguous() and colmean.shape == (HQ, RANK_C), "colmean: (HQ, 16) contiguous")
     _need(init.dtype == torch.int32 and init.numel() == C, "init: (C,) int32")
-    lib.call("oa_kmeans_update", _ptr(zP), zP.stride(0), HQ, T, _ptr(asg8), asg8.stride(0), C,
-             _ptr(init), _ptr(cent), _ptr(cnt), _stream(dev))
+    _chk(mem, "mem", torch.int32, (HQ, -T))
+    _chk(cstart, "cstart", torch.int32, (HQ, C), contiguous=True)
+    _chk(clen, "clen", torch.int32, (HQ, C), contiguous=True)
+    lib.call("oa_kmeans_update", _ptr(zraw), _ptr(colmean), zraw.stride(0), HQ, T, _ptr(asg8), asg8.stride(0),
+             C, _ptr(init), _ptr(cent), _ptr(cnt), _ptr(mem), mem.stride(0), _ptr(cstart), _ptr(clen),
+             _stream(dev))
 
 
 def cluster_build(K, V, T: int, G: int, asg8, C: int, nb, Sk, Sk2, Sv, mem, cstart, clen) -> None:

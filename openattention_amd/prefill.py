@@ -252,18 +252,22 @@ def _build_device(st, r0: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: 
     ops.qgs_codes(K, T, st.U[r0:r0 + HKV], st.codes[r0:r0 + HKV], st.scale[r0:r0 + HKV], amax)
     mark("codes")
     # a12: QGC projection and k-means
-    zP = torch.empty(HQ, T, RC, device=dev)
-    ops.qgc_project(K, T, st.W[q0:q0 + HQ], G, zP, st.colmean[q0:q0 + HQ])
+    # the projection is kept as its bf16 values; the k-means kernels form zP = bf16(k W) - colmean
+    # (fp32) as they read it
+    zraw = torch.empty(HQ, T, RC, device=dev, dtype=torch.bfloat16)
+    colmean = st.colmean[q0:q0 + HQ]
+    ops.qgc_project(K, T, st.W[q0:q0 + HQ], G, zraw, colmean)
     mark("project")
     init = kmeans_init(T, C, layer).to(device=dev, dtype=torch.int32)
     cent = st.cent[q0:q0 + HQ]
-    cent.copy_(zP.index_select(1, init.long()))
+    cent.copy_(zraw.index_select(1, init.long()).float() - colmean[:, None, :])
     asg, asg8 = st.asg[q0:q0 + HQ], st.asg8[q0:q0 + HQ]
     mark("kmeans_init")
     for _ in range(ITERS):
-        ops.kmeans_assign(zP, T, cent, asg, asg8)
+        ops.kmeans_assign(zraw, colmean, T, cent, asg, asg8)
         mark("kmeans_assign")
-        ops.kmeans_update(zP, T, asg8, init, cent)
+        ops.kmeans_update(zraw, colmean, T, asg8, init, cent, st.mem[q0:q0 + HQ], st.cstart[q0:q0 + HQ],
+                          st.clen[q0:q0 + HQ])
         mark("kmeans_update")
     # a13: cluster statistics and CSR member lists
     ops.cluster_build(K, V, T, G, asg8, C, st.nb[q0:q0 + HQ], st.Sk[q0:q0 + HQ], st.Sk2[q0:q0 + HQ],

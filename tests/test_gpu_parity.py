@@ -882,9 +882,11 @@ def test_build_codes_bit_exact(T):
 @pytest.mark.parametrize("T", [4095, 1000])
 def test_build_projection_and_kmeans(T):
     """QGC projection on the bf16 matrix cores: bf16(k W) agrees with the exact-sum restatement
-    up to rare bf16 ties; colmean and zP are bit-exact given the device's bf16(k W).  k-means:
-    the assignment agrees with the restatement's on the same zP and centroids up to rare ties;
-    the update is bit-exact given the device's assignment."""
+    up to rare bf16 ties; colmean and zP are bit-exact given the device's bf16(k W), and the
+    projection without the fp32 zP writes the same bf16(k W) and colmean.  k-means (zP formed from
+    the bf16 projection and colmean as the kernels read it): the assignment agrees with the
+    restatement's on the same zP and centroids up to rare ties; the update is bit-exact given the
+    device's assignment."""
     print(f"[case] build projection + k-means T={T}", flush=True)
     rng = np.random.default_rng(7 + T)
     HKV_, G_, Lmax, C = 2, 4, 4160, 64
@@ -894,8 +896,12 @@ def test_build_projection_and_kmeans(T):
     zP = torch.empty(R, T, 16, device=DEV)
     zraw = torch.empty(R, T, 16, device=DEV, dtype=torch.int16)
     cm = torch.empty(R, 16, device=DEV)
-    ops.qgc_project(_bf16_dev(K), T, _bf16_dev(W), G_, zP, cm, zraw=zraw)
+    ops.qgc_project(_bf16_dev(K), T, _bf16_dev(W), G_, zraw, cm, zP=zP)
+    zraw2 = torch.full((R, T, 16), 7, device=DEV, dtype=torch.int16)
+    cm2 = torch.full((R, 16), float("nan"), device=DEV)
+    ops.qgc_project(_bf16_dev(K), T, _bf16_dev(W), G_, zraw2, cm2)
     torch.cuda.synchronize()
+    assert torch.equal(zraw, zraw2) and torch.equal(cm, cm2)
     zr_gpu = zraw.cpu().numpy().view(np.uint16)
     zr_ref = O.qgc_zraw(K, T, W, G_)
     agree = (zr_gpu == zr_ref).mean()
@@ -912,7 +918,7 @@ def test_build_projection_and_kmeans(T):
     init_d = _i32(init)
     for it in range(4):
         cent_np = cent.cpu().numpy()
-        ops.kmeans_assign(zP, T, cent, asg, asg8)
+        ops.kmeans_assign(zraw, cm, T, cent, asg, asg8)
         torch.cuda.synchronize()
         a_gpu = asg.cpu().numpy()[:, :T]
         a_ref = O.kmeans_assign(zP_np, cent_np)
@@ -922,11 +928,19 @@ def test_build_projection_and_kmeans(T):
         assert np.array_equal(asg8.cpu().numpy()[:, :T], a_gpu.astype(np.uint8))
         assert np.all(asg.cpu().numpy()[:, T:] == -1)
         cnt = torch.empty(R, C, device=DEV)
-        ops.kmeans_update(zP, T, asg8, init_d, cent, cnt)
+        mem_ws = torch.full((R, Lmax), -9, device=DEV, dtype=torch.int32)
+        cs_ws, cl_ws = (torch.full((R, C), -9, device=DEV, dtype=torch.int32) for _ in range(2))
+        ops.kmeans_update(zraw, cm, T, asg8, init_d, cent, mem_ws, cs_ws, cl_ws, cnt)
         torch.cuda.synchronize()
         c_ref, n_ref = O.kmeans_update(zP_np, a_gpu, C, init)
         assert np.array_equal(cent.cpu().numpy(), c_ref)
         assert np.array_equal(cnt.cpu().numpy(), n_ref)
+        # the member lists the update went through: a stable sort of the assignment by cluster
+        counts = np.stack([np.bincount(a_gpu[r], minlength=C) for r in range(R)]).astype(np.int32)
+        assert np.array_equal(cl_ws.cpu().numpy(), counts)
+        assert np.array_equal(cs_ws.cpu().numpy(), np.cumsum(counts, axis=1) - counts)
+        mem_ref = np.argsort(a_gpu, axis=1, kind="stable").astype(np.int32)
+        assert np.array_equal(mem_ws.cpu().numpy()[:, :T], mem_ref)
 
 
 @pytest.mark.parametrize("T,C", [(4095, 64), (600, 8)])

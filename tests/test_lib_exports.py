@@ -34,7 +34,7 @@ def test_binding_matches_header():
 
 def test_library_loads_and_reports():
     L = lib.load()
-    assert L.oa_abi_version() == lib.ABI_VERSION == 5
+    assert L.oa_abi_version() == lib.ABI_VERSION == 6
     assert b"invalid argument" in L.oa_error_string(-22)
     for name in lib.SIGNATURES:
         assert getattr(L, name) is not None
