@@ -368,12 +368,14 @@ int oa_dense_decode(const void* q, long q_stride, const void* K, const void* V, 
  * 1e-12) per (KV row, coordinate), codes = clamp(rint(zc / scale), -127, 127).  K: kv_rows
  * rows of (T, 128) bf16 at k_stride_h / k_stride_t; U (kv_rows, 128, 32) fp32; codes
  * (kv_rows, codes_stride_h / 32, 32) int8; scale (kv_rows, 32); amax_ws (kv_rows * 32) uint32
- * scratch.  Replaces the code step of inference/ours_fastbuild.py:256-261 and
- * methods_eager.py:519-525 (StaticTopKMasker._extend, static_top_k.py:174-181).
+ * scratch; zc_ws (kv_rows * T * 32) fp32 scratch, 16-byte aligned, or NULL: with it zc is formed
+ * once and kept between the two passes, without it the second pass forms it again (same codes).
+ * Replaces the code step of inference/ours_fastbuild.py:256-261 and methods_eager.py:519-525
+ * (StaticTopKMasker._extend, static_top_k.py:174-181).
  */
 int oa_qgs_codes(const void* K, long k_stride_h, long k_stride_t, int kv_rows, int T,
                  const float* U, int8_t* codes, long codes_stride_h, float* scale,
-                 uint32_t* amax_ws, void* stream);
+                 uint32_t* amax_ws, float* zc_ws, void* stream);
 
 /*
  * QGC projection bf16(k W) on the bf16 matrix cores and colmean = mean over the T tokens of

@@ -76,10 +76,11 @@ __global__ void __launch_bounds__(64) clear_u32_kernel(uint32_t* p, int n) {
 }
 
 // pass 1: per (KV row, coordinate) the maximum |zc| over the tokens, as float bits (|zc| >= 0,
-// so the unsigned maximum of the bits is the float maximum)
+// so the unsigned maximum of the bits is the float maximum); zc itself into zc_ws when given
+// (128 bytes per token), so that pass 2 quantizes without a second fma chain
 __global__ void __launch_bounds__(kCodeThreads) codes_amax_kernel(const uint16_t* K, long ksh, long kst,
                                                                   int T, const float* U,
-                                                                  uint32_t* amax) {
+                                                                  uint32_t* amax, float* zc_ws) {
   __shared__ float sU[kD * kRQ];
   __shared__ uint32_t s_m[kRQ];
   const int h = blockIdx.y;
@@ -90,6 +91,11 @@ __global__ void __launch_bounds__(kCodeThreads) codes_amax_kernel(const uint16_t
   float z[kRQ];
   token_zc(K + (long)h * ksh + (long)min(t, T - 1) * kst, sU, z);
   const bool in = t < T;
+  if (zc_ws && in) {
+    float4* zo = reinterpret_cast<float4*>(zc_ws + ((long)h * T + t) * kRQ);
+#pragma unroll
+    for (int r4 = 0; r4 < kRQ / 4; ++r4) zo[r4] = make_float4(z[4 * r4], z[4 * r4 + 1], z[4 * r4 + 2], z[4 * r4 + 3]);
+  }
 #pragma unroll
   for (int r = 0; r < kRQ; ++r) {
     const unsigned m = oa::wave_max_u32(in ? __float_as_uint(fabsf(z[r])) : 0u);
@@ -103,7 +109,8 @@ __global__ void __launch_bounds__(kCodeThreads) codes_amax_kernel(const uint16_t
 __global__ void __launch_bounds__(kCodeThreads) codes_write_kernel(const uint16_t* K, long ksh, long kst,
                                                                    int T, const float* U,
                                                                    const uint32_t* amax, int8_t* codes,
-                                                                   long csh, float* scale) {
+                                                                   long csh, float* scale,
+                                                                   const float* zc_ws) {
   __shared__ float sU[kD * kRQ];
   __shared__ float s_sc[kRQ];
   const int h = blockIdx.y;
@@ -117,7 +124,16 @@ __global__ void __launch_bounds__(kCodeThreads) codes_write_kernel(const uint16_
   const int t = blockIdx.x * kCodeThreads + threadIdx.x;
   if (t >= T) return;
   float z[kRQ];
-  token_zc(K + (long)h * ksh + (long)t * kst, sU, z);
+  if (zc_ws) {
+    const float4* zi = reinterpret_cast<const float4*>(zc_ws + ((long)h * T + t) * kRQ);
+#pragma unroll
+    for (int r4 = 0; r4 < kRQ / 4; ++r4) {
+      const float4 v = zi[r4];
+      z[4 * r4] = v.x; z[4 * r4 + 1] = v.y; z[4 * r4 + 2] = v.z; z[4 * r4 + 3] = v.w;
+    }
+  } else {
+    token_zc(K + (long)h * ksh + (long)t * kst, sU, z);
+  }
   uint32_t packed[kRQ / 4];
 #pragma unroll
   for (int r4 = 0; r4 < kRQ / 4; ++r4) {
@@ -217,16 +233,19 @@ __global__ void __launch_bounds__(256) qgc_center_kernel(float* zP, long zps, in
 }
 
 // ---------------------------------------------------------------------------------- k-means
-// bf16 ordered key: larger value -> larger key
-__device__ __forceinline__ uint32_t bf16_key(uint16_t h) {
-  return (uint32_t)(h ^ ((h & 0x8000u) ? 0xffffu : 0x8000u));
+// two fp32 values rounded to bf16 (nearest even) in one conversion: a in the low half
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2v;
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
 }
 
 // One 256-thread workgroup per (kAsgTiles 64-token tiles, query row): the row's centroids (bf16,
 // B operands: centroid lane % 16 of a 16-centroid block, dims 4*(lane/16)..+3) and
 // bf16(|c|^2 / 2) are staged in LDS once and every wave then takes every fourth tile.
 // Per 16-token block and centroid block one v_mfma_f32_16x16x16bf16_1k gives 16 x 16 dots;
-// the distance bf16(bf16(dot) - half) is ranked through the key (bf16 key << 8 | 255 - c), so the
+// the distance bf16(bf16(dot) - half) is ranked through the key (bf16 key << 16 | 255 - c), so the
 // maximum over the 16 centroid lanes (a DPP row) and over the blocks is the argmax with ties to
 // the lower cluster.
 constexpr int kAsgThreads = 256;
@@ -247,7 +266,7 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
   for (int i = threadIdx.x; i < CB * 16 * kRC; i += kAsgThreads)
     s_cb[i] = i < C * kRC ? oa::f32_to_bf16(cr[i]) : 0;
   for (int c = threadIdx.x; c < CB * 16; c += kAsgThreads) {
-    uint16_t hv = 0;
+    uint16_t hv = 0x7f80u;   // padding centroids: +inf, a distance of -inf ranks below every real one
     if (c < C) {
       float s = 0.f;
 #pragma unroll
@@ -286,14 +305,17 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
         float4v acc = {0.f, 0.f, 0.f, 0.f};
         acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
         const float hf = oa::bf16_to_f32(s_half[c]);
+        // bf16(bf16(dot) - half), two values per conversion; + 0 turns -0 into +0 (one score); the
+        // key is the distance's order-preserving key (its top 16 bits: the bf16 key) with the tag
+        // 255 - c below it
+        const uint32_t tag = (uint32_t)(255 - c);
+        const uint32_t p01 = cvt_pk_bf16(acc[0], acc[1]), p23 = cvt_pk_bf16(acc[2], acc[3]);
+        const uint32_t q01 = cvt_pk_bf16(__uint_as_float(p01 << 16) - hf, __uint_as_float(p01 & 0xffff0000u) - hf);
+        const uint32_t q23 = cvt_pk_bf16(__uint_as_float(p23 << 16) - hf, __uint_as_float(p23 & 0xffff0000u) - hf);
+        const float e[4] = {__uint_as_float(q01 << 16) + 0.f, __uint_as_float(q01 & 0xffff0000u) + 0.f,
+                            __uint_as_float(q23 << 16) + 0.f, __uint_as_float(q23 & 0xffff0000u) + 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float dot = oa::bf16_to_f32(oa::f32_to_bf16_rn(acc[i]));
-          uint16_t dist = oa::f32_to_bf16_rn(dot - hf);
-          if ((dist & 0x7fffu) == 0) dist = 0;           // -0 ranks as +0
-          const uint32_t key = c < C ? (bf16_key(dist) << 8) | (uint32_t)(255 - c) : 0u;
-          best[i] = max(best[i], key);
-        }
+        for (int i = 0; i < 4; ++i) best[i] = max(best[i], (oa::float_key(e[i]) & 0xffff0000u) | tag);
       }
       // maximum over the 16 lanes of each DPP row (the 16 centroids of one block column set)
 #pragma unroll
@@ -311,7 +333,7 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
         // lane (16g + i) holds token 4g + i of the block: best[i] of its row
         uint32_t v = i == 0 ? best[0] : (i == 1 ? best[1] : (i == 2 ? best[2] : best[3]));
         if (t < T) {
-          const int cid = 255 - (int)(v & 0xffu);
+          const int cid = 255 - (int)(v & 0xffu);   // (every real distance key exceeds 0)
           asg[(long)row * as + t] = cid;
           asg8[(long)row * a8s + t] = (uint8_t)cid;
         }
@@ -528,10 +550,11 @@ __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, con
 
 extern "C" int oa_qgs_codes(const void* K, long k_stride_h, long k_stride_t, int kv_rows, int T,
                             const float* U, int8_t* codes, long codes_stride_h, float* scale,
-                            uint32_t* amax_ws, void* stream) {
+                            uint32_t* amax_ws, float* zc_ws, void* stream) {
   if (kv_rows <= 0 || T <= 0 || !K || !U || !codes || !scale || !amax_ws || k_stride_t < kD ||
       k_stride_t % 8 || k_stride_h % 8 || codes_stride_h < (long)T * kRQ || codes_stride_h % 16 ||
-      (reinterpret_cast<uintptr_t>(K) & 15) || (reinterpret_cast<uintptr_t>(codes) & 15))
+      (reinterpret_cast<uintptr_t>(K) & 15) || (reinterpret_cast<uintptr_t>(codes) & 15) ||
+      (reinterpret_cast<uintptr_t>(zc_ws) & 15))
     return OA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   const uint16_t* k = reinterpret_cast<const uint16_t*>(K);
@@ -539,9 +562,9 @@ extern "C" int oa_qgs_codes(const void* K, long k_stride_h, long k_stride_t, int
                      amax_ws, kv_rows * kRQ);
   const dim3 grid((T + kCodeThreads - 1) / kCodeThreads, kv_rows);
   hipLaunchKernelGGL(codes_amax_kernel, grid, dim3(kCodeThreads), 0, s, k, k_stride_h, k_stride_t, T, U,
-                     amax_ws);
+                     amax_ws, zc_ws);
   hipLaunchKernelGGL(codes_write_kernel, grid, dim3(kCodeThreads), 0, s, k, k_stride_h, k_stride_t, T, U,
-                     amax_ws, codes, codes_stride_h, scale);
+                     amax_ws, codes, codes_stride_h, scale, zc_ws);
   return OA_LAUNCH_STATUS();
 }
 

@@ -52,7 +52,7 @@ SIGNATURES = {
     "oa_residual_flash": [P, L, P, P, L, L, I, I, I, P, L, P, L, I, P, I, P, P, P, P, I, F, P, L,
                           I, P, P],
     "oa_dense_decode": [P, L, P, P, L, L, I, I, I, I, P, F, I, P, P, P, P, L, P],
-    "oa_qgs_codes": [P, L, L, I, I, P, P, L, P, P, P],
+    "oa_qgs_codes": [P, L, L, I, I, P, P, L, P, P, P, P],
     "oa_qgc_project": [P, L, L, I, I, I, P, P, L, P, P, P, P],
     "oa_kmeans_assign": [P, P, L, I, I, P, I, P, L, P, L, P],
     "oa_kmeans_update": [P, P, L, I, I, P, L, I, P, P, P, P, L, P, P, P],

@@ -534,9 +534,10 @@ def dense_decode(q, K, V, n_dev, out=None, sm_scale: float | None = None, nsplit
 
 
 # ================================================================== prefill index build
-def qgs_codes(K, T: int, U, codes, scale, amax_ws) -> None:
+def qgs_codes(K, T: int, U, codes, scale, amax_ws, zc_ws=None) -> None:
     """a11 of one request: K (HKV, >=T, 128) bf16; U (HKV, 128, 32) fp32; codes (HKV, Lmax, 32)
-    int8 (rows written up to T); scale (HKV, 32); amax_ws >= HKV*32 int32 scratch."""
+    int8 (rows written up to T); scale (HKV, 32); amax_ws >= HKV*32 int32 scratch; zc_ws >= HKV*T*32
+    fp32 scratch or None (then k U is formed twice; the same codes)."""
     dev = _dev(K, U, codes, scale, amax_ws)
     HKV = K.shape[0]
     _need(K.dtype == torch.bfloat16 and K.stride(-1) == 1, "K: bf16 with contiguous rows")
@@ -546,8 +547,11 @@ def qgs_codes(K, T: int, U, codes, scale, amax_ws) -> None:
           "codes: (HKV, Lmax, 32) int8 rows")
     _need(amax_ws.numel() >= HKV * RANK_Q, "amax_ws too small")
     _need(T <= K.shape[1] and T <= codes.shape[1], "T beyond the rows")
+    if zc_ws is not None:
+        _need(zc_ws.dtype == torch.float32 and zc_ws.is_contiguous() and zc_ws.numel() >= HKV * T * RANK_Q,
+              "zc_ws: >= HKV*T*32 fp32, contiguous")
     lib.call("oa_qgs_codes", _ptr(K), K.stride(0), K.stride(1), HKV, T, _ptr(U), _ptr(codes),
-             codes.stride(0), _ptr(scale), _ptr(amax_ws), _stream(dev))
+             codes.stride(0), _ptr(scale), _ptr(amax_ws), _ptr(zc_ws), _stream(dev))
 
 
 def qgc_project(K, T: int, W, G: int, zraw, colmean, zP=None) -> None:

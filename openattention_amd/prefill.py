@@ -249,7 +249,9 @@ def _build_device(st, r0: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: 
     q0 = r0 * G
     # a11: QGS codes and scale
     amax = torch.empty(HKV * RQ, device=dev, dtype=torch.int32)
-    ops.qgs_codes(K, T, st.U[r0:r0 + HKV], st.codes[r0:r0 + HKV], st.scale[r0:r0 + HKV], amax)
+    zc = torch.empty(HKV * T * RQ, device=dev)          # k U kept between the two passes
+    ops.qgs_codes(K, T, st.U[r0:r0 + HKV], st.codes[r0:r0 + HKV], st.scale[r0:r0 + HKV], amax, zc)
+    del zc
     mark("codes")
     # a12: QGC projection and k-means
     # the projection is kept as its bf16 values; the k-means kernels form zP = bf16(k W) - colmean

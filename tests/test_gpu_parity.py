@@ -872,11 +872,15 @@ def test_build_codes_bit_exact(T):
     codes = torch.zeros(HKV_, Lmax, 32, device=DEV, dtype=torch.int8)
     scale = torch.zeros(HKV_, 32, device=DEV)
     ws = torch.empty(HKV_ * 32, device=DEV, dtype=torch.int32)
-    ops.qgs_codes(_bf16_dev(K), T, _f32(U), codes, scale, ws)
-    torch.cuda.synchronize()
     rc, rs = O.qgs_codes(K, T, U)
-    assert np.array_equal(scale.cpu().numpy(), rs)
-    assert np.array_equal(codes.cpu().numpy(), rc)
+    # both forms: zc formed twice, and kept in a workspace between the passes
+    for zc in (None, torch.full((HKV_ * T * 32,), float("nan"), device=DEV)):
+        codes.zero_()
+        scale.zero_()
+        ops.qgs_codes(_bf16_dev(K), T, _f32(U), codes, scale, ws, zc)
+        torch.cuda.synchronize()
+        assert np.array_equal(scale.cpu().numpy(), rs)
+        assert np.array_equal(codes.cpu().numpy(), rc)
 
 
 @pytest.mark.parametrize("T", [4095, 1000])
