@@ -151,6 +151,7 @@ __global__ void __launch_bounds__(kCodeThreads) codes_write_kernel(const uint16_
 }
 
 // ---------------------------------------------------------------------------------- projection
+constexpr int kProjTiles = 8;    // 64-token tiles per wave (the row's W operands loaded once)
 // One wave per (64-token tile, query row).  Four 16-token blocks, each 16 tokens x 16 columns
 // from four v_mfma_f32_16x16x32_bf16 over d = 0..127 (A: token rows of K, B: the row's W).
 // Output layout of a 16x16 block: lane l holds tokens 4*(l/16) + i (i = 0..3) of column l % 16.
@@ -160,8 +161,9 @@ __global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long
                                                          int T, const uint16_t* W, float* zP,
                                                          long zps, uint16_t* zraw_out, double* tsum,
                                                          int ntiles) {
+  __shared__ uint4 s_z[64 * kRC / 8];             // the tile's bf16(k W), token rows of 32 bytes
+  uint16_t* s_zh = reinterpret_cast<uint16_t*>(s_z);
   const int lane = threadIdx.x;
-  const int tile = blockIdx.x;
   const int row = blockIdx.y;
   const uint16_t* krow = K + (long)(row / G) * ksh;
   const uint16_t* w = W + (long)row * kD * kRC;
@@ -172,6 +174,9 @@ __global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       bw[ch][e] = bits_bf16(w[(ch * 32 + 8 * (lane >> 4) + e) * kRC + (lane & 15)]);
+  const int tend = min(ntiles, (int)(blockIdx.x + 1) * kProjTiles);
+#pragma unroll 1
+  for (int tile = blockIdx.x * kProjTiles; tile < tend; ++tile) {
   double cs = 0.0;   // this lane's column (lane % 16) partial over its tokens, in block order
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
@@ -189,17 +194,32 @@ __global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long
       const int t = t0 + 4 * (lane >> 4) + i;
       const uint16_t hb = oa::f32_to_bf16_rn(acc[i]);
       const float v = oa::bf16_to_f32(hb);
+      s_zh[(blk * 16 + 4 * (lane >> 4) + i) * kRC + (lane & 15)] = hb;
       if (t < T) {
         if (zP) zP[(long)row * zps + (long)t * kRC + (lane & 15)] = v;
-        if (zraw_out) zraw_out[(long)row * zps + (long)t * kRC + (lane & 15)] = hb;
         cs += (double)v;
       }
+    }
+  }
+  // the tile's rows out through LDS: lane l writes token l's 32 bytes
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (zraw_out) {
+    const int t = tile * 64 + lane;
+    if (t < T) {
+      uint4* dst = reinterpret_cast<uint4*>(zraw_out + (long)row * zps + (long)t * kRC);
+      dst[0] = s_z[lane * 2];
+      dst[1] = s_z[lane * 2 + 1];
     }
   }
   // lanes j, 16 + j, 32 + j, 48 + j hold column j: ((g0 + g1) + (g2 + g3))
   cs += __shfl_xor(cs, 16, 64);
   cs += __shfl_xor(cs, 32, 64);
   if (lane < 16) tsum[((long)row * ntiles + tile) * kRC + lane] = cs;
+  // the next tile's stores to s_z wait for these reads
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  }
 }
 
 // colmean from the tile sums (tiles in order, fp64): one wave per row, lane j < 16 a column
@@ -507,8 +527,23 @@ __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, con
                                                           float* Sv, const int32_t* mem, long ms) {
   __shared__ int s_pos[kMemBuf];
   const int lane = threadIdx.x;
-  const int c = blockIdx.x;
-  const int row = blockIdx.y;
+  // every token's K and V rows are read once per query row of its KV row (each query row has its
+  // own clusters).  The G * C workgroups of a KV row run on one XCD, its query rows interleaved,
+  // so that they walk the KV row's positions together and the later reads of a row hit that
+  // XCD's L2 (workgroups are dealt to the 8 XCDs in turn)
+  int c, row;
+  {
+    const int b = blockIdx.x, rows = gridDim.x / C, kv_rows = rows / G;
+    if (kv_rows % 8 == 0) {
+      const int k = b >> 3, per = G * C;
+      const int j = k % per;
+      row = ((k / per) * 8 + (b & 7)) * G + j % G;
+      c = j / G;
+    } else {
+      row = b / C;
+      c = b % C;
+    }
+  }
   const uint16_t* kr = K + (long)(row / G) * ksh + 2 * lane;
   const uint16_t* vr = V + (long)(row / G) * ksh + 2 * lane;
   const int32_t* ml = mem + (long)row * ms + cstart[row * C + c];
@@ -574,11 +609,11 @@ extern "C" int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, i
   if (rows <= 0 || G <= 0 || rows % G || T <= 0 || !K || !W || (!zP && !zraw_out) || !colmean ||
       !tile_ws || k_stride_t < kD || k_stride_t % 8 || k_stride_h % 8 || zp_stride < (long)T * kRC ||
       zp_stride % 4 || (reinterpret_cast<uintptr_t>(K) & 15) || (reinterpret_cast<uintptr_t>(zP) & 15) ||
-      (reinterpret_cast<uintptr_t>(zraw_out) & 7))
+      (reinterpret_cast<uintptr_t>(zraw_out) & 15) || (zraw_out && zp_stride % 8))
     return OA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   const int ntiles = (T + 63) / 64;
-  hipLaunchKernelGGL(qgc_project_kernel, dim3(ntiles, rows), dim3(64), 0, s,
+  hipLaunchKernelGGL(qgc_project_kernel, dim3((ntiles + kProjTiles - 1) / kProjTiles, rows), dim3(64), 0, s,
                      reinterpret_cast<const uint16_t*>(K), k_stride_h, k_stride_t, G, T,
                      reinterpret_cast<const uint16_t*>(W), zP, zp_stride, zraw_out, tile_ws, ntiles);
   hipLaunchKernelGGL(qgc_colmean_kernel, dim3(rows), dim3(64), 0, s, T, tile_ws, ntiles, colmean);
@@ -631,7 +666,7 @@ extern "C" int oa_cluster_build(const void* K, const void* V, long kv_stride_h, 
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(csr_sort_kernel, dim3(rows), dim3(kSortThreads), 0, s, T, asg8, asg8_stride, C, nb,
                      cstart, clen, mem, mem_stride);
-  hipLaunchKernelGGL(cluster_sums_kernel, dim3(C, rows), dim3(64), 0, s,
+  hipLaunchKernelGGL(cluster_sums_kernel, dim3(C * rows), dim3(64), 0, s,
                      reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
                      kv_stride_h, kv_stride_t, G, C, cstart, clen, Sk, Sk2, Sv, mem, mem_stride);
   return OA_LAUNCH_STATUS();
