@@ -136,8 +136,13 @@ __device__ __forceinline__ float det_erff(float xf) {
   const double ax = x < 0.0 ? -x : x;
   if (ax >= 4.0) return x < 0.0 ? -1.0f : 1.0f;
   const double x2 = ax * ax;
-  double s = kErfC[71];
-  for (int n = 70; n >= 0; --n) s = fma(s, x2, kErfC[n]);
+  // the coefficients through vector loads (returned in order), so that the compiler keeps a
+  // few ahead of the fma chain instead of waiting on each batch of scalar loads
+  const double* tb = kErfC;
+  asm volatile("" : "+v"(tb));
+  double s = tb[71];
+#pragma unroll
+  for (int n = 70; n >= 0; --n) s = fma(s, x2, tb[n]);
   const double r = (ax * s) * 0x1.20dd750429b6dp+0;  // 2/sqrt(pi)
   const float rf = (float)r;
   return x < 0.0 ? -rf : rf;
