@@ -28,11 +28,11 @@
 extern "C" {
 #endif
 
-#define OA_ABI_VERSION 6
+#define OA_ABI_VERSION 7
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
-/* ABI version of this header (4). */
+/* ABI version of the loaded library (OA_ABI_VERSION of the header it was built from). */
 int oa_abi_version(void);
 
 /* Text for a status returned by any entry point. */
@@ -425,6 +425,18 @@ int oa_cluster_build(const void* K, const void* V, long kv_stride_h, long kv_str
                      int G, int T, const uint8_t* asg8, long asg8_stride, int C, float* nb,
                      float* Sk, float* Sk2, float* Sv, int32_t* mem, long mem_stride,
                      int32_t* cstart, int32_t* clen, void* stream);
+
+/*
+ * Top-k eigenpairs of symmetric positive semi-definite 128 x 128 fp32 matrices (one-sided Jacobi,
+ * one workgroup per matrix; the lower triangle is read).  M (batch, m_stride >= 128*128) row-major;
+ * evals (batch, k) and evecs (batch, 128, k) receive the k largest eigenvalues and their unit
+ * eigenvectors in ascending order (the last k of torch.linalg.eigh's order; signs are free);
+ * 1 <= k <= 64; n must be 128.  sweeps (batch) int32 or NULL: the Jacobi sweeps each matrix took
+ * (negative if it reached the sweep cap unconverged).  Replaces torch.linalg.eigh in the a10
+ * bases of inference/methods_eager.py:519-528.
+ */
+int oa_sym_eig_top(const float* M, long m_stride, int batch, int n, int k, float* evals,
+                   float* evecs, int* sweeps, void* stream);
 
 #ifdef __cplusplus
 }

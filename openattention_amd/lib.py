@@ -57,11 +57,12 @@ SIGNATURES = {
     "oa_kmeans_assign": [P, P, L, I, I, P, I, P, L, P, L, P],
     "oa_kmeans_update": [P, P, L, I, I, P, L, I, P, P, P, P, L, P, P, P],
     "oa_cluster_build": [P, P, L, L, I, I, I, P, L, I, P, P, P, P, P, L, P, P, P],
+    "oa_sym_eig_top": [P, L, I, I, I, P, P, P, P],
 }
 
 # must equal oa_abi_version() of the loaded library (OA_ABI_VERSION in the header): a library
 # built from sources with other argument lists would be handed wrong pointers
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _LIB = None
 

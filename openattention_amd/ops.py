@@ -554,6 +554,30 @@ def qgs_codes(K, T: int, U, codes, scale, amax_ws, zc_ws=None) -> None:
              codes.stride(0), _ptr(scale), _ptr(amax_ws), _ptr(zc_ws), _stream(dev))
 
 
+def sym_eig_top(M, k: int, sweeps=None):
+    """Top-k eigenpairs of symmetric positive semi-definite (batch, 128, 128) fp32 matrices (the
+    lower triangle is read): (evals (batch, k), evecs (batch, 128, k)), ascending, the last k of
+    torch.linalg.eigh's order; signs are free.  sweeps: (batch,) int32 or None, the Jacobi sweeps
+    each matrix took (negative: unconverged at the cap)."""
+    dev = _dev(M, sweeps)
+    _need(M.dtype == torch.float32 and M.dim() == 3 and M.shape[1:] == (HEAD_DIM, HEAD_DIM)
+          and M.stride(2) == 1 and M.stride(1) == HEAD_DIM
+          and (M.shape[0] <= 1 or M.stride(0) >= HEAD_DIM * HEAD_DIM),
+          "M: (batch, 128, 128) fp32 with contiguous matrices")
+    _need(1 <= k <= 64, "k: 1..64")
+    B = M.shape[0]
+    m_stride = M.stride(0) if B > 1 else HEAD_DIM * HEAD_DIM
+    if sweeps is not None:
+        _need(sweeps.dtype == torch.int32 and sweeps.is_contiguous() and sweeps.numel() >= B,
+              "sweeps: >= batch int32, contiguous")
+    ev = torch.empty(B, k, device=dev, dtype=torch.float32)
+    vec = torch.empty(B, HEAD_DIM, k, device=dev, dtype=torch.float32)
+    if B:
+        lib.call("oa_sym_eig_top", _ptr(M), m_stride, B, HEAD_DIM, k, _ptr(ev), _ptr(vec),
+                 _ptr(sweeps), _stream(dev))
+    return ev, vec
+
+
 def qgc_project(K, T: int, W, G: int, zraw, colmean, zP=None) -> None:
     """a12 projection: zraw (HQ, T, 16) int16/bf16 = bf16(k W) (what kmeans_assign and
     kmeans_update read); colmean (HQ, 16); zP (HQ, T, 16) fp32 = bf16(k W) - colmean, or None."""

@@ -7,8 +7,8 @@ multibin.py:1894):
        (StaticTopKMasker._rot_avg, static_top_k.py:103-131); M_q from P <= 64
        question rows, each rotated to T (static_top_k.py:185-194); M = 1/2 nt(M_st) + 1/2
        nt(M_q), nt = trace normalisation; U = top-32 eigenvectors of the group-mean M per KV
-       head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.  Host torch
-       (rocSOLVER eigh on the device).
+       head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.  The metric in
+       host torch on the device, the eigenpairs from oa_sym_eig_top (one-sided Jacobi).
   a11  codes: oa_qgs_codes (zc = k U, scale = max(max_t |zc| / 127, 1e-12), codes =
        clamp(rint(zc / scale), -127, 127); static_top_k.py:174-181).
   a12  oa_qgc_project (zP = bf16(k W) - colmean on the bf16 matrix cores), then 4 Lloyd
@@ -109,17 +109,32 @@ def kmeans_seed(layer: int) -> int:
     return 1234 + 31 * (layer + 1)
 
 
-def bases(M: torch.Tensor, HKV: int, G: int):
-    """a10 bases from the per-query-head metric M (HQ, D, D): U (HKV, D, 32) = top-32
-    eigenvectors of the group mean (methods_eager.py:519-520), W (HQ, D, 16) bf16 = top-16
-    eigenvectors * sqrt(eigenvalue) (methods_eager.py:527-528)."""
-    # one batched eigh over the HKV group means and the HQ metrics (each matrix is decomposed on
-    # its own; one solver call instead of two)
-    ev_all, U_all = torch.linalg.eigh(torch.cat([M.view(HKV, G, D, D).mean(1), M], 0))
-    U = U_all[:HKV, :, -RQ:].contiguous()
-    ev, Uq = ev_all[HKV:], U_all[HKV:]
-    W = (Uq[..., -RC:] * ev[..., -RC:].clamp(min=0).sqrt().unsqueeze(-2)).to(torch.bfloat16).contiguous()
+def basis_matrices(M: torch.Tensor, HKV: int, G: int) -> torch.Tensor:
+    """The matrices the bases come from: the HKV group means of the per-query-head metric M
+    (HQ, D, D) (methods_eager.py:519), then the HQ metrics themselves (methods_eager.py:527)."""
+    return torch.cat([M.view(HKV, G, D, D).mean(1), M], 0)
+
+
+def bases_from_eigenpairs(ev: torch.Tensor, vec: torch.Tensor, HKV: int):
+    """U, W from the top eigenpairs of basis_matrices' output, ascending (the last columns of an
+    eigh): U (HKV, D, 32) = the top-32 eigenvectors of each group mean (methods_eager.py:519-520),
+    W (HQ, D, 16) bf16 = the top-16 eigenvectors * sqrt(eigenvalue) of each metric
+    (methods_eager.py:527-528)."""
+    U = vec[:HKV, :, -RQ:].contiguous()
+    evq, Uq = ev[HKV:], vec[HKV:]
+    W = (Uq[..., -RC:] * evq[..., -RC:].clamp(min=0).sqrt().unsqueeze(-2)).to(torch.bfloat16).contiguous()
     return U, W
+
+
+def bases(M: torch.Tensor, HKV: int, G: int):
+    """a10 bases from the per-query-head metric M (HQ, D, D) on a HIP device: the top-32
+    eigenpairs of the HKV group means and the HQ metrics from one launch of the library's
+    Jacobi eigensolver (oa_sym_eig_top: one workgroup per matrix, each decomposed on its own),
+    then bases_from_eigenpairs.  The metric is a positive blend of second-moment matrices
+    (positive semi-definite), which the solver requires."""
+    from openattention_amd import ops
+    ev, vec = ops.sym_eig_top(basis_matrices(M, HKV, G).contiguous(), RQ)
+    return bases_from_eigenpairs(ev, vec, HKV)
 
 
 def kmeans_init(T: int, C: int, layer: int) -> torch.Tensor:
@@ -167,7 +182,7 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
                M_pre: torch.Tensor, inv_freq: torch.Tensor, scaling: float, layer: int,
                G: int = 4, marks: list | None = None) -> None:
     """build_row for every batch row of one layer at once: the bases of all rows from one
-    batched eigh (the per-row solver call dominates the build otherwise), then each HIP stage
+    eigensolver launch (one workgroup per matrix), then each HIP stage
     over all B * HQ rows in one launch (the stages are row-parallel: one launch per stage
     instead of one per stage and row).
 
@@ -206,8 +221,8 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
 def build_layers(states, Ks, Vs, qrows, T: int, M_pre: torch.Tensor, inv_freq: torch.Tensor,
                  scaling: float, layers, G: int = 4) -> None:
     """build_rows for several layers at once: every layer's metric first, then the bases of all
-    layers and rows from one batched eigh (at B = 1 a layer's 40 small matrices leave the solver
-    latency-bound; 32 layers in one call take about what one layer's call does), then each
+    layers and rows from one eigensolver launch (at B = 1 a layer's 40 matrices would hold 40 of
+    the 256 compute units; 32 layers' 1280 fill them), then each
     layer's HIP stages.  states[i], Ks[i], Vs[i], qrows[i] belong to layer layers[i]; M_pre is
     the (L, HQ, D, D) static metric of every layer."""
     if not (len(states) == len(Ks) == len(Vs) == len(qrows) == len(layers)) or not layers:

@@ -173,7 +173,11 @@ def test_bases_are_the_top_eigenvectors_of_the_right_matrices():
     rng = np.random.default_rng(11)
     M = _group_metrics(rng)
     Mg = M.reshape(HKV, G, D, D).mean(1)
-    U, W = prefill.bases(torch.from_numpy(M).float(), HKV, G)
+    # the host side of the bases (which matrices, which eigenpairs, the sqrt scaling) over an
+    # eigh's top-32 pairs; the device eigensolver that prefill.bases uses has its own GPU tests
+    Mall = prefill.basis_matrices(torch.from_numpy(M).float(), HKV, G)
+    ev, vec = torch.linalg.eigh(Mall.double())
+    U, W = prefill.bases_from_eigenpairs(ev[..., -32:].float(), vec[..., -32:].float(), HKV)
     U, W = U.double().numpy(), W.float().double().numpy()
     Uo, Wo = O.bases(M, HKV, G)
     assert _u_ok(U, Mg) and _u_ok(Uo, Mg)

@@ -34,7 +34,7 @@ def test_binding_matches_header():
 
 def test_library_loads_and_reports():
     L = lib.load()
-    assert L.oa_abi_version() == lib.ABI_VERSION == 6
+    assert L.oa_abi_version() == lib.ABI_VERSION == 7
     assert b"invalid argument" in L.oa_error_string(-22)
     for name in lib.SIGNATURES:
         assert getattr(L, name) is not None
@@ -54,6 +54,11 @@ def test_argument_checks_reject_before_launch():
     for tm, tmn in ((16, None), (None, 16)):
         assert L.oa_topq_heads(16, 64, 16, 64, 16, 4, 8, 64, 16, 8, 16, 16, 1, 16, 16, 16, 64, tm, tmn, 1, 0,
                                None) == -22
+    # eigensolver: n other than 128, k outside 1..64, a matrix stride below 128 * 128
+    assert L.oa_sym_eig_top(16, 64 * 64, 1, 64, 16, 16, 16, None, None) == -22
+    assert L.oa_sym_eig_top(16, 128 * 128, 1, 128, 65, 16, 16, None, None) == -22
+    assert L.oa_sym_eig_top(16, 128 * 128, 1, 128, 0, 16, 16, None, None) == -22
+    assert L.oa_sym_eig_top(16, 128 * 127, 1, 128, 32, 16, 16, None, None) == -22
 
 
 def test_noalloc_flash_rejects_oversized_request_before_launch():
