@@ -19,8 +19,12 @@
 // block meets H0 x H1 in h steps, its b columns moving one quad along (through LDS) after each
 // step.  Between levels the first h/2 quads of a block hand their b column to quad i + h/2 for
 // its a column, so each new block again holds one column of each of its halves per quad.
-// Sweeps repeat until one applies no rotation (at most kMaxSweeps).  Every matrix runs the same
-// fixed schedule on its own workgroup: results do not depend on the batch a matrix is in.
+// Each column's squared norm travels with it (recomputed at every sweep start), so a step forms
+// one dot product, a.b, per pair; a pair counts as orthogonal when |a.b| <= kTol |a| |b| or when
+// both columns are below 1e-6 |A|_F (numerically in the null space, where fp32 cannot resolve
+// their angle).  Sweeps repeat until one applies no rotation (at most kMaxSweeps).  Every matrix
+// runs the same fixed schedule on its own workgroup: results do not depend on the batch a
+// matrix is in.
 #include "oa_common.h"
 
 namespace {
@@ -31,7 +35,7 @@ constexpr int kRows = 32;                      // rows of each column held by on
 constexpr int kThreads = kQuads * 4;
 constexpr int kSubStride = kRows + 4;          // floats per lane chunk in LDS (padded)
 constexpr int kSlotStride = 4 * kSubStride;    // floats per column slot
-constexpr int kMaxSweeps = 30;
+constexpr int kMaxSweeps = 40;
 constexpr int kMaxK = 64;
 constexpr float kTol = 1e-5f;                  // |a.b| <= kTol |a| |b| counts as orthogonal
 
@@ -53,27 +57,47 @@ __device__ __forceinline__ int quad_sum(int v) {
   return v;
 }
 
-// one Jacobi rotation of the quad's column pair; true if the pair was not yet orthogonal
-__device__ __forceinline__ bool rotate_pair(float (&a)[kRows], float (&b)[kRows]) {
-  float al0 = 0.f, al1 = 0.f, be0 = 0.f, be1 = 0.f, ga0 = 0.f, ga1 = 0.f;
+// squared norm of the column part a lane holds, summed over the quad
+__device__ __forceinline__ float quad_norm2(const float (&a)[kRows]) {
+  float x0 = 0.f, x1 = 0.f;
 #pragma unroll
   for (int j = 0; j < kRows; j += 2) {
-    al0 = fmaf(a[j], a[j], al0);
-    be0 = fmaf(b[j], b[j], be0);
+    x0 = fmaf(a[j], a[j], x0);
+    x1 = fmaf(a[j + 1], a[j + 1], x1);
+  }
+  return quad_sum(x0 + x1);
+}
+
+// one Jacobi rotation of the quad's column pair, whose squared norms al, be are carried along
+// (recomputed at every sweep start) and updated as al - t ga, be + t ga (the rotated pair's Gram
+// diagonal); true if the pair was not yet orthogonal.  The rotation itself is skipped when no
+// pair of the wave needs one.
+__device__ __forceinline__ bool rotate_pair(float (&a)[kRows], float (&b)[kRows], float& al,
+                                            float& be, float floor2) {
+  float ga0 = 0.f, ga1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRows; j += 2) {
     ga0 = fmaf(a[j], b[j], ga0);
-    al1 = fmaf(a[j + 1], a[j + 1], al1);
-    be1 = fmaf(b[j + 1], b[j + 1], be1);
     ga1 = fmaf(a[j + 1], b[j + 1], ga1);
   }
-  // the quad's sums: every lane of the quad ends with the same bits
-  const float al = quad_sum(al0 + al1), be = quad_sum(be0 + be1), ga = quad_sum(ga0 + ga1);
-  const bool on = fabsf(ga) > kTol * (sqrtf(al) * sqrtf(be));
-  // (for ga = 0 the quotients below are inf or NaN; such a pair is not rotated)
-  const float zeta = (be - al) / (2.f * ga);
-  const float t = copysignf(1.f, zeta) / (fabsf(zeta) + sqrtf(fmaf(zeta, zeta, 1.f)));
-  const float cr = 1.f / sqrtf(fmaf(t, t, 1.f));
+  // the quad's sum: every lane of the quad ends with the same bits
+  const float ga = quad_sum(ga0 + ga1);
+  // orthogonal to the tolerance, or both columns negligible against the matrix (their norms
+  // below 1e-6 |A|_F: they cannot move the leading eigenvectors)
+  const bool on = ga * ga > (kTol * kTol) * (al * be) && al + be > floor2;
+  if (__ballot(on) == 0ull) return false;
+  // the angle from the hardware reciprocal and square roots (about 1 ulp): an error there only
+  // changes which orthogonal rotation is applied (c^2 + s^2 = 1 to about 2 ulp either way); for
+  // ga = 0 the quotients are inf or NaN and the pair is not rotated
+  const float zeta = (be - al) * __builtin_amdgcn_rcpf(2.f * ga);
+  const float t = copysignf(
+      __builtin_amdgcn_rcpf(fabsf(zeta) + __builtin_amdgcn_sqrtf(fmaf(zeta, zeta, 1.f))), zeta);
+  const float cr = __builtin_amdgcn_rsqf(fmaf(t, t, 1.f));
   const float c = on ? cr : 1.f;
   const float s = on ? cr * t : 0.f;
+  const float tg = on ? t * ga : 0.f;
+  al = fmaxf(al - tg, 0.f);
+  be = be + tg;
 #pragma unroll
   for (int j = 0; j < kRows; ++j) {
     const float x = a[j], y = b[j];
@@ -83,17 +107,20 @@ __device__ __forceinline__ bool rotate_pair(float (&a)[kRows], float (&b)[kRows]
   return on;
 }
 
-__device__ __forceinline__ void put32(float* p, const float (&v)[kRows]) {
+// a lane's part of a column and the column's squared norm (in the chunk's padding)
+__device__ __forceinline__ void put32(float* p, const float (&v)[kRows], float n2) {
 #pragma unroll
   for (int j = 0; j < kRows; j += 4)
     *reinterpret_cast<float4*>(p + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+  p[kRows] = n2;
 }
-__device__ __forceinline__ void get32(const float* p, float (&v)[kRows]) {
+__device__ __forceinline__ float get32(const float* p, float (&v)[kRows]) {
 #pragma unroll
   for (int j = 0; j < kRows; j += 4) {
     const float4 x = *reinterpret_cast<const float4*>(p + j);
     v[j] = x.x; v[j + 1] = x.y; v[j + 2] = x.z; v[j + 3] = x.w;
   }
+  return p[kRows];
 }
 
 // element (r, c) of the symmetric matrix from the lower triangle of row-major M
@@ -101,7 +128,7 @@ __device__ __forceinline__ float sym_at(const float* M, int r, int c) {
   return r >= c ? M[r * kN + c] : M[c * kN + r];
 }
 
-__global__ __launch_bounds__(kThreads) void sym_eig_top_kernel(const float* __restrict__ M,
+__global__ __launch_bounds__(kThreads, 4) void sym_eig_top_kernel(const float* __restrict__ M,
                                                                long m_stride, int k,
                                                                float* __restrict__ ev,
                                                                float* __restrict__ evec,
@@ -109,6 +136,7 @@ __global__ __launch_bounds__(kThreads) void sym_eig_top_kernel(const float* __re
   __shared__ __align__(16) float s_x[kQuads * kSlotStride];
   __shared__ double s_nrm[2 * kQuads];
   __shared__ int s_flag[kThreads / OA_WAVE];
+  __shared__ float s_fro[kThreads / OA_WAVE];
   const int m = blockIdx.x;
   const int tid = threadIdx.x, g = tid >> 2, sub = tid & 3;
   const float* A = M + (long)m * m_stride;
@@ -121,22 +149,33 @@ __global__ __launch_bounds__(kThreads) void sym_eig_top_kernel(const float* __re
     b[j] = sym_at(A, r0 + j, g + kQuads);
   }
   float* mine = s_x + g * kSlotStride + sub * kSubStride;
+  // |A|_F^2 (each quad's two columns, summed over the wave and then the four waves)
+  {
+    float f = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) f = fmaf(a[j], a[j], fmaf(b[j], b[j], f));
+    f = oa::wave_sum(f);
+    if ((tid & (OA_WAVE - 1)) == 0) s_fro[tid / OA_WAVE] = f;
+  }
+  __syncthreads();
+  const float floor2 = 1e-12f * ((s_fro[0] + s_fro[1]) + (s_fro[2] + s_fro[3]));
 
   int sweep = 0;
   bool more = true;
   while (more && sweep < kMaxSweeps) {
     unsigned long long any = 0;
+    float al = quad_norm2(a), be = quad_norm2(b);
     for (int lev = 0; lev < 7; ++lev) {
       const int h = kQuads >> lev;
       const int i = g & (h - 1), g0 = g - i;
       const float* next = s_x + (g0 + ((i + 1) & (h - 1))) * kSlotStride + sub * kSubStride;
       for (int t = 0; t < h; ++t) {
-        any |= __ballot(rotate_pair(a, b));
+        any |= __ballot(rotate_pair(a, b, al, be, floor2));
         if (t + 1 < h) {
           // quad i takes the b column of quad i + 1 (within the block)
-          put32(mine, b);
+          put32(mine, b, be);
           __syncthreads();
-          get32(next, b);
+          be = get32(next, b);
           __syncthreads();
         }
       }
@@ -144,14 +183,14 @@ __global__ __launch_bounds__(kThreads) void sym_eig_top_kernel(const float* __re
         const int hb = h >> 1;
         const float* partner = s_x + (i < hb ? g + hb : g - hb) * kSlotStride + sub * kSubStride;
         if (i < hb)
-          put32(mine, b);
+          put32(mine, b, be);
         else
-          put32(mine, a);
+          put32(mine, a, al);
         __syncthreads();
         if (i < hb)
-          get32(partner, b);
+          be = get32(partner, b);
         else
-          get32(partner, a);
+          al = get32(partner, a);
         __syncthreads();
       }
     }
@@ -193,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void sym_eig_top_kernel(const float* __re
     const float inv = na > 0.0 ? (float)(1.0 / na) : 0.f;
 #pragma unroll
     for (int j = 0; j < kRows; ++j) a[j] *= inv;
-    put32(s_x + p * kSlotStride + sub * kSubStride, a);
+    put32(s_x + p * kSlotStride + sub * kSubStride, a, 0.f);
     if (sub == 0) ev[(long)m * k + p] = (float)na;
   }
   if (rb < k) {
@@ -201,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void sym_eig_top_kernel(const float* __re
     const float inv = nb > 0.0 ? (float)(1.0 / nb) : 0.f;
 #pragma unroll
     for (int j = 0; j < kRows; ++j) b[j] *= inv;
-    put32(s_x + p * kSlotStride + sub * kSubStride, b);
+    put32(s_x + p * kSlotStride + sub * kSubStride, b, 0.f);
     if (sub == 0) ev[(long)m * k + p] = (float)nb;
   }
   __syncthreads();
