@@ -78,18 +78,53 @@ __global__ void __launch_bounds__(64) clear_u32_kernel(uint32_t* p, int n) {
 // pass 1: per (KV row, coordinate) the maximum |zc| over the tokens, as float bits (|zc| >= 0,
 // so the unsigned maximum of the bits is the float maximum); zc itself into zc_ws when given
 // (128 bytes per token), so that pass 2 quantizes without a second fma chain
-__global__ void __launch_bounds__(kCodeThreads) codes_amax_kernel(const uint16_t* K, long ksh, long kst,
-                                                                  int T, const float* U,
-                                                                  uint32_t* amax, float* zc_ws) {
-  __shared__ float sU[kD * kRQ];
+// The block's 256 key rows are staged through LDS, 64 dims at a time (coalesced 128-byte row
+// segments, rows padded to 144 bytes so that a 16-lane phase of row reads hits distinct banks):
+// a lane walking its own row straight from memory touched 64 lines per load and lost them to
+// the other rows before its next step (5.5x the keys' bytes fetched).  U's rows come through
+// scalar loads (the same for every lane; the fmas take them from SGPRs) rather than LDS
+// broadcasts, which bounded the pass by LDS bandwidth.  The fma chain over d is token_zc's, in
+// the same order.
+constexpr int kZcDims = 64;                    // dims staged per pass
+constexpr int kZcRowQ = kZcDims / 8 + 1;       // uint4 per staged row (8 + 1 pad)
+
+__global__ void __launch_bounds__(kCodeThreads) codes_amax_kernel(const uint16_t* __restrict__ K, long ksh,
+                                                                  long kst, int T,
+                                                                  const float* __restrict__ U,
+                                                                  uint32_t* __restrict__ amax,
+                                                                  float* __restrict__ zc_ws) {
   __shared__ uint32_t s_m[kRQ];
+  __shared__ uint4 s_k[kCodeThreads * kZcRowQ];
   const int h = blockIdx.y;
-  for (int i = threadIdx.x; i < kD * kRQ; i += kCodeThreads) sU[i] = U[(long)h * kD * kRQ + i];
+  const float* __restrict__ Uh = U + (long)h * kD * kRQ;
   if (threadIdx.x < kRQ) s_m[threadIdx.x] = 0u;
-  __syncthreads();
-  const int t = blockIdx.x * kCodeThreads + threadIdx.x;
+  const int t0 = blockIdx.x * kCodeThreads;
+  const int t = t0 + threadIdx.x;
+  const uint16_t* kh = K + (long)h * ksh;
   float z[kRQ];
-  token_zc(K + (long)h * ksh + (long)min(t, T - 1) * kst, sU, z);
+#pragma unroll
+  for (int r = 0; r < kRQ; ++r) z[r] = 0.f;
+  for (int d0 = 0; d0 < kD; d0 += kZcDims) {
+    if (d0) __syncthreads();   // every lane has read the previous dims
+#pragma unroll
+    for (int j = 0; j < kZcDims / 8; ++j) {
+      const int i = threadIdx.x + j * kCodeThreads;
+      const int r = i / (kZcDims / 8), c = i % (kZcDims / 8);
+      s_k[r * kZcRowQ + c] =
+          *reinterpret_cast<const uint4*>(kh + (long)min(t0 + r, T - 1) * kst + d0 + 8 * c);
+    }
+    __syncthreads();
+    for (int c = 0; c < kZcDims / 8; ++c) {
+      float kv[8];
+      oa::unpack8(s_k[threadIdx.x * kZcRowQ + c], kv);
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) {
+        const float* ud = Uh + (d0 + 8 * c + dd) * kRQ;
+#pragma unroll
+        for (int r = 0; r < kRQ; ++r) z[r] = fmaf(kv[dd], ud[r], z[r]);
+      }
+    }
+  }
   const bool in = t < T;
   if (zc_ws && in) {
     float4* zo = reinterpret_cast<float4*>(zc_ws + ((long)h * T + t) * kRQ);
