@@ -312,7 +312,9 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
                                                                     uint8_t* asg8, long a8s) {
   __shared__ uint16_t s_cb[kMaxC * kRC];
   __shared__ uint16_t s_half[kMaxC];
+  __shared__ int s_zh;                  // some real centroid has bf16(|c|^2 / 2) = +0
   const int lane = threadIdx.x & 63;
+  if (threadIdx.x == 0) s_zh = 0;
   const int wave = threadIdx.x >> 6;
   const int row = blockIdx.y;
   const int CB = (C + 15) / 16;
@@ -330,10 +332,14 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
         s = s + x * x;
       }
       hv = oa::f32_to_bf16(0.5f * s);
+      if (hv == 0) s_zh = 1;
     }
     s_half[c] = hv;
   }
   __syncthreads();
+  // bf16(x - half) is -0 only for half = +0 (x - x rounds to +0): without such a centroid the
+  // distances need no -0 -> +0 step, and their keys are formed two at a time from the packed pair
+  const bool fast = s_zh == 0;
   // zP = bf16(k W) - colmean, formed from the stored bf16 projection (the same fp32 values)
   float cm[4];
 #pragma unroll
@@ -367,10 +373,21 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
         const uint32_t p01 = cvt_pk_bf16(acc[0], acc[1]), p23 = cvt_pk_bf16(acc[2], acc[3]);
         const uint32_t q01 = cvt_pk_bf16(__uint_as_float(p01 << 16) - hf, __uint_as_float(p01 & 0xffff0000u) - hf);
         const uint32_t q23 = cvt_pk_bf16(__uint_as_float(p23 << 16) - hf, __uint_as_float(p23 & 0xffff0000u) - hf);
-        const float e[4] = {__uint_as_float(q01 << 16) + 0.f, __uint_as_float(q01 & 0xffff0000u) + 0.f,
-                            __uint_as_float(q23 << 16) + 0.f, __uint_as_float(q23 & 0xffff0000u) + 0.f};
+        if (fast) {
+          // the order-preserving key of each bf16 half (negative: every bit flipped; otherwise
+          // the sign bit set), two halves per instruction, then key << 16 | tag per distance
+          const uint32_t k01 = q01 ^ (((q01 >> 15) & 0x00010001u) * 0x7fffu | 0x80008000u);
+          const uint32_t k23 = q23 ^ (((q23 >> 15) & 0x00010001u) * 0x7fffu | 0x80008000u);
+          best[0] = max(best[0], (k01 << 16) | tag);
+          best[1] = max(best[1], (k01 & 0xffff0000u) | tag);
+          best[2] = max(best[2], (k23 << 16) | tag);
+          best[3] = max(best[3], (k23 & 0xffff0000u) | tag);
+        } else {
+          const float e[4] = {__uint_as_float(q01 << 16) + 0.f, __uint_as_float(q01 & 0xffff0000u) + 0.f,
+                              __uint_as_float(q23 << 16) + 0.f, __uint_as_float(q23 & 0xffff0000u) + 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) best[i] = max(best[i], (oa::float_key(e[i]) & 0xffff0000u) | tag);
+          for (int i = 0; i < 4; ++i) best[i] = max(best[i], (oa::float_key(e[i]) & 0xffff0000u) | tag);
+        }
       }
       // maximum over the 16 lanes of each DPP row (the 16 centroids of one block column set)
 #pragma unroll

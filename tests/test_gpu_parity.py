@@ -947,6 +947,35 @@ def test_build_projection_and_kmeans(T):
         assert np.array_equal(mem_ws.cpu().numpy()[:, :T], mem_ref)
 
 
+def test_kmeans_assign_with_a_zero_centroid():
+    """A centroid at the origin (bf16(|c|^2 / 2) = +0, where bf16(dot - half) can be -0): the
+    assignment takes its -0 -> +0 path for the whole row set and still agrees with the
+    restatement (-0 and +0 rank as one score, ties to the lower cluster)."""
+    print("[case] k-means assignment with a zero centroid", flush=True)
+    rng = np.random.default_rng(23)
+    HKV_, G_, Lmax, C, T = 2, 4, 4160, 64, 4095
+    R = HKV_ * G_
+    K = f32_to_bf16(rng.standard_normal((HKV_, Lmax, D)).astype(np.float32))
+    W = f32_to_bf16((rng.standard_normal((R, D, 16)) * 0.3).astype(np.float32))
+    zP = torch.empty(R, T, 16, device=DEV)
+    zraw = torch.empty(R, T, 16, device=DEV, dtype=torch.int16)
+    cm = torch.empty(R, 16, device=DEV)
+    ops.qgc_project(_bf16_dev(K), T, _bf16_dev(W), G_, zraw, cm, zP=zP)
+    init = rng.choice(T, C, replace=False)
+    cent = zP[:, torch.from_numpy(init).long().to(DEV)].contiguous()
+    cent[:, 5] = 0.0
+    asg = torch.full((R, Lmax), -1, device=DEV, dtype=torch.int32)
+    asg8 = torch.zeros(R, -(-Lmax // 64) * 64, device=DEV, dtype=torch.uint8)
+    ops.kmeans_assign(zraw, cm, T, cent, asg, asg8)
+    torch.cuda.synchronize()
+    a_gpu = asg.cpu().numpy()[:, :T]
+    a_ref = O.kmeans_assign(zP.cpu().numpy(), cent.cpu().numpy())
+    agree = (a_gpu == a_ref).mean()
+    print(f"  assignment agreement {agree:.6f}; cluster 5 holds {(a_gpu == 5).sum()} tokens")
+    assert agree > 0.999
+    assert np.array_equal(asg8.cpu().numpy()[:, :T], a_gpu.astype(np.uint8))
+
+
 @pytest.mark.parametrize("T,C", [(4095, 64), (600, 8)])
 def test_build_cluster_stats_bit_exact(T, C):
     print(f"[case] build cluster stats T={T} C={C}", flush=True)
