@@ -63,6 +63,8 @@ def parse():
     p.add_argument("--config5", action="store_true",
                    help="whole decode step of a Llama-3.1-8B-shaped random-init model (32 layers) under one "
                         "hipGraph, sparse vs dense attention, B in {1, 32}, N = 32768; one JSON line per B")
+    p.add_argument("--c5-batches", default="1,32",
+                   help="batch sizes of --config5, comma-separated (default 1,32)")
     p.add_argument("--config4", action="store_true",
                    help="long-context sweep instead: B=8, N in {65536, 131072}, 1%% and 3%%, 512-centre "
                         "mixture with 8 needles per KV head; one JSON line per point (us/layer-step, "
@@ -306,7 +308,7 @@ def config5_run(a):
     torch.cuda.set_device(0)
     N = a.ctx
     static = synth.static_metric(NLAYER)
-    for B in (1, 32):
+    for B in (int(x) for x in a.c5_batches.split(",")):
         n_total = 2 * (a.warmup + a.steps) + 4
         Lmax = N + n_total
         t0 = time.time()
