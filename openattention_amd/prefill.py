@@ -170,10 +170,11 @@ def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor,
     if marks is not None:
         mark("start")
     M = query_metric(M_pre.to(dev), qrows, T, inv_freq.to(dev), scaling)           # (HQ, D, D)
+    mark("metric")
     U, W = bases(M, HKV, G)
     st.U[b * HKV:(b + 1) * HKV] = U
     st.W[b * HQ:(b + 1) * HQ] = W
-    mark("metric_bases")
+    mark("bases")
     _build_device(st, b * HKV, K, V, T, layer, G, mark)
 
 
@@ -210,10 +211,11 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
     mst = 0.5 * trace_norm(rot_avg(M_pre.to(dev), inv_freq, scaling, T, WIN))
     Mq = question_moment(qrows.reshape(B * HQ, qrows.shape[2], D), inv_freq, scaling)
     M = mst + 0.5 * trace_norm(Mq).view(B, HQ, D, D)                                # (B, HQ, D, D)
+    mark("metric")
     U, W = bases(M.reshape(B * HQ, D, D), B * HKV, G)
     st.U[:B * HKV] = U
     st.W[:B * HQ] = W
-    mark("metric_bases")
+    mark("bases")
     _build_device(st, 0, K.reshape(B * HKV, K.shape[2], D), V.reshape(B * HKV, V.shape[2], D), T,
                   layer, G, mark)
 
