@@ -324,9 +324,7 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
                                                                     uint8_t* asg8, long a8s) {
   __shared__ uint16_t s_cb[kMaxC * kRC];
   __shared__ uint16_t s_half[kMaxC];
-  __shared__ int s_zh;                  // some real centroid has bf16(|c|^2 / 2) = +0
   const int lane = threadIdx.x & 63;
-  if (threadIdx.x == 0) s_zh = 0;
   const int wave = threadIdx.x >> 6;
   const int row = blockIdx.y;
   const int CB = (C + 15) / 16;
@@ -334,6 +332,7 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
   const float* cr = cent + (long)row * C * kRC;
   for (int i = threadIdx.x; i < CB * 16 * kRC; i += kAsgThreads)
     s_cb[i] = i < C * kRC ? oa::f32_to_bf16(cr[i]) : 0;
+  int zero_half = 0;          // this thread staged a real centroid with bf16(|c|^2 / 2) = +0
   for (int c = threadIdx.x; c < CB * 16; c += kAsgThreads) {
     uint16_t hv = 0x7f80u;   // padding centroids: +inf, a distance of -inf ranks below every real one
     if (c < C) {
@@ -344,14 +343,13 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
         s = s + x * x;
       }
       hv = oa::f32_to_bf16(0.5f * s);
-      if (hv == 0) s_zh = 1;
+      zero_half |= hv == 0;
     }
     s_half[c] = hv;
   }
-  __syncthreads();
   // bf16(x - half) is -0 only for half = +0 (x - x rounds to +0): without such a centroid the
   // distances need no -0 -> +0 step, and their keys are formed two at a time from the packed pair
-  const bool fast = s_zh == 0;
+  const bool fast = __syncthreads_or(zero_half) == 0;
   // zP = bf16(k W) - colmean, formed from the stored bf16 projection (the same fp32 values)
   float cm[4];
 #pragma unroll
