@@ -69,7 +69,7 @@ constexpr int kLdsLimit = 160 * 1024;
 constexpr int kSmallRows = 256;               // below: oa_topq_heads path 0 in one launch
 constexpr int32_t kRowMarked = -2;              // exp_idx[row][0] of a row left to the key-prefix kernel
 constexpr int kTileLd = 3;                      // tile extremes per thread (linear-bin kernel)
-constexpr int kRowGrid = 256;                   // key-prefix kernel over marked rows: one workgroup per unit
+constexpr int kRowGrid = 64;                    // key-prefix kernel over marked rows: workgroups
 
 enum : int { kModeNone = 0, kModeAll = 1, kModeStaged = 2, kModeBlock = 3, kModeSplit = 4 };
 
@@ -853,7 +853,7 @@ __global__ void __launch_bounds__(kThreads) topq_row_kernel(TopqArgs a) {
 }
 
 // After the linear-bin kernel: a grid of at most kRowGrid workgroups runs the rows it marked
-// (usually none), so an empty pass dispatches one workgroup per unit, not one per row.  Wave 0
+// (usually none), so an empty pass dispatches 64 workgroups, not one per row.  Wave 0
 // reads the marks of 64 of the workgroup's rows (blockIdx.x + j * gridDim.x) at once; their
 // ballot reaches every wave through LDS.
 template <int PPT, int LB>

@@ -87,8 +87,8 @@ def test_config3_batch32_matches_oracle(rho):
     res = _decode_both_dtypes(st, K, V, q, rho, N, Lmax, B, static, prefix_topq=rho in (0.01, 0.10))
     ns, nl, k = res[torch.bfloat16]["counts"]
     if "exp_idx_prefix" in res:
-        # all 1024 rows through the key-prefix kernel (one workgroup per unit walking four rows
-        # each) equal the step's linear-bin top-q on every row
+        # all 1024 rows through the key-prefix kernel (64 workgroups walking sixteen rows each)
+        # equal the step's linear-bin top-q on every row
         bad = np.nonzero((res["exp_idx_prefix"] != res[torch.bfloat16]["exp_idx"]).any(1))[0]
         assert bad.size == 0, f"key-prefix top-q over every row: rows {bad[:8]} differ"
     for b in seqs:
