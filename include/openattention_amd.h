@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define OA_ABI_VERSION 7
+#define OA_ABI_VERSION 8
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
@@ -425,6 +425,18 @@ int oa_cluster_build(const void* K, const void* V, long kv_stride_h, long kv_str
                      int G, int T, const uint8_t* asg8, long asg8_stride, int C, float* nb,
                      float* Sk, float* Sk2, float* Sv, int32_t* mem, long mem_stride,
                      int32_t* cstart, int32_t* clen, void* stream);
+
+/*
+ * Cluster statistics over member lists already built (the ones oa_kmeans_update leaves for the
+ * assignment it was given): nb = clen (as float), Sk = sum k, Sk2 = sum k*k, Sv = sum v (fp64
+ * sums in list order, one rounding); the same outputs as oa_cluster_build for that assignment,
+ * without sorting it again.  mem (rows, mem_stride), cstart / clen (rows, C) as oa_cluster_build
+ * writes them.  Replaces _k_cluster_sums (inference/ours_fastbuild.py:111-139) where the CSR
+ * lists of ours_fastbuild.py:293-301 are already at hand.
+ */
+int oa_cluster_sums(const void* K, const void* V, long kv_stride_h, long kv_stride_t, int rows, int G,
+                    int T, int C, float* nb, float* Sk, float* Sk2, float* Sv, const int32_t* mem,
+                    long mem_stride, const int32_t* cstart, const int32_t* clen, void* stream);
 
 /*
  * Top-k eigenpairs of symmetric positive semi-definite 128 x 128 fp32 matrices (one-sided Jacobi,

@@ -586,7 +586,8 @@ __global__ void __launch_bounds__(kSortThreads) csr_sort_kernel(int T, const uin
 __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, const uint16_t* V, long ksh,
                                                           long kst, int G, int C, const int32_t* cstart,
                                                           const int32_t* clen, float* Sk, float* Sk2,
-                                                          float* Sv, const int32_t* mem, long ms) {
+                                                          float* Sv, const int32_t* mem, long ms,
+                                                          float* nb) {
   __shared__ int s_pos[kMemBuf];
   const int lane = threadIdx.x;
   // every token's K and V rows are read once per query row of its KV row (each query row has its
@@ -610,6 +611,7 @@ __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, con
   const uint16_t* vr = V + (long)(row / G) * ksh + 2 * lane;
   const int32_t* ml = mem + (long)row * ms + cstart[row * C + c];
   const int cl = clen[row * C + c];
+  if (nb && lane == 0) nb[row * C + c] = (float)cl;   // (when the sort did not write it)
   double k0 = 0.0, k1 = 0.0, q0 = 0.0, q1 = 0.0, v0 = 0.0, v1 = 0.0;
   constexpr int U = 16;
   for (int i0 = 0; i0 < cl; i0 += kMemBuf) {
@@ -730,6 +732,22 @@ extern "C" int oa_cluster_build(const void* K, const void* V, long kv_stride_h, 
                      cstart, clen, mem, mem_stride);
   hipLaunchKernelGGL(cluster_sums_kernel, dim3(C * rows), dim3(64), 0, s,
                      reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
-                     kv_stride_h, kv_stride_t, G, C, cstart, clen, Sk, Sk2, Sv, mem, mem_stride);
+                     kv_stride_h, kv_stride_t, G, C, cstart, clen, Sk, Sk2, Sv, mem, mem_stride,
+                     static_cast<float*>(nullptr));
+  return OA_LAUNCH_STATUS();
+}
+
+extern "C" int oa_cluster_sums(const void* K, const void* V, long kv_stride_h, long kv_stride_t, int rows,
+                               int G, int T, int C, float* nb, float* Sk, float* Sk2, float* Sv,
+                               const int32_t* mem, long mem_stride, const int32_t* cstart,
+                               const int32_t* clen, void* stream) {
+  if (rows <= 0 || G <= 0 || rows % G || T <= 0 || C <= 0 || C > kMaxC || !K || !V || !nb || !Sk ||
+      !Sk2 || !Sv || !mem || !cstart || !clen || kv_stride_t < kD || kv_stride_t % 2 ||
+      kv_stride_h % 2 || mem_stride < T || (reinterpret_cast<uintptr_t>(K) & 3) ||
+      (reinterpret_cast<uintptr_t>(V) & 3))
+    return OA_EINVAL;
+  hipLaunchKernelGGL(cluster_sums_kernel, dim3(C * rows), dim3(64), 0, (hipStream_t)stream,
+                     reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
+                     kv_stride_h, kv_stride_t, G, C, cstart, clen, Sk, Sk2, Sv, mem, mem_stride, nb);
   return OA_LAUNCH_STATUS();
 }

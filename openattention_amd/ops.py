@@ -631,6 +631,22 @@ def kmeans_update(zraw, colmean, T: int, asg8, init, cent, mem, cstart, clen, cn
              _stream(dev))
 
 
+def cluster_sums(K, V, T: int, G: int, C: int, nb, Sk, Sk2, Sv, mem, cstart, clen) -> None:
+    """a13 over member lists already built (kmeans_update's for the assignment it was given):
+    nb = clen, Sk/Sk2/Sv as cluster_build, which would sort that assignment again."""
+    dev = _dev(K, V, nb, Sk, Sk2, Sv, mem, cstart, clen)
+    HQ = nb.shape[0]
+    _need(K.stride() == V.stride() and K.stride(-1) == 1, "K, V: same strides, contiguous rows")
+    _need(K.shape[0] * G == HQ and T <= K.shape[1], "K: HQ / G rows of at least T tokens")
+    for t, nm in ((nb, "nb"), (Sk, "Sk"), (Sk2, "Sk2"), (Sv, "Sv"), (cstart, "cstart"), (clen, "clen")):
+        _need(t.is_contiguous(), f"{nm} must be contiguous")
+    _need(mem.dtype == torch.int32 and mem.stride(-1) == 1 and cstart.dtype == torch.int32
+          and clen.dtype == torch.int32, "mem, cstart, clen: int32")
+    lib.call("oa_cluster_sums", _ptr(K), _ptr(V), K.stride(0), K.stride(1), HQ, G, T, C, _ptr(nb),
+             _ptr(Sk), _ptr(Sk2), _ptr(Sv), _ptr(mem), mem.stride(0), _ptr(cstart), _ptr(clen),
+             _stream(dev))
+
+
 def cluster_build(K, V, T: int, G: int, asg8, C: int, nb, Sk, Sk2, Sv, mem, cstart, clen) -> None:
     """a13: nb (HQ, C), Sk/Sk2/Sv (HQ, C, 128), mem (HQ, >=T), cstart/clen (HQ, C)."""
     dev = _dev(K, V, asg8, nb, Sk, Sk2, Sv, mem, cstart, clen)

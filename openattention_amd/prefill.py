@@ -288,9 +288,10 @@ def _build_device(st, r0: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: 
         ops.kmeans_update(zraw, colmean, T, asg8, init, cent, st.mem[q0:q0 + HQ], st.cstart[q0:q0 + HQ],
                           st.clen[q0:q0 + HQ])
         mark("kmeans_update")
-    # a13: cluster statistics and CSR member lists
-    ops.cluster_build(K, V, T, G, asg8, C, st.nb[q0:q0 + HQ], st.Sk[q0:q0 + HQ], st.Sk2[q0:q0 + HQ],
-                      st.Sv[q0:q0 + HQ], st.mem[q0:q0 + HQ], st.cstart[q0:q0 + HQ], st.clen[q0:q0 + HQ])
+    # a13: cluster statistics; the CSR member lists are the last update's (the assignment did not
+    # change after it), so they are not sorted again
+    ops.cluster_sums(K, V, T, G, C, st.nb[q0:q0 + HQ], st.Sk[q0:q0 + HQ], st.Sk2[q0:q0 + HQ],
+                     st.Sv[q0:q0 + HQ], st.mem[q0:q0 + HQ], st.cstart[q0:q0 + HQ], st.clen[q0:q0 + HQ])
     st.reccnt[q0:q0 + HQ] = 0
     mark("cluster_build")
 

@@ -1001,6 +1001,13 @@ def test_build_cluster_stats_bit_exact(T, C):
     for name, g, r in zip(("nb", "Sk", "Sk2", "Sv", "mem", "cstart", "clen"), got, ref):
         assert np.array_equal(g.cpu().numpy(), r), name
     assert np.all(mem.cpu().numpy()[:, T:] == -1)
+    # the statistics over lists already built (the k-means update's, in the build) are the same
+    nb2 = torch.full((R, C), float("nan"), device=DEV)
+    Sk_2, Sk2_2, Sv_2 = (torch.full((R, C, D), float("nan"), device=DEV) for _ in range(3))
+    ops.cluster_sums(_bf16_dev(K), _bf16_dev(V), T, G_, C, nb2, Sk_2, Sk2_2, Sv_2, mem, cstart, clen)
+    torch.cuda.synchronize()
+    for name, g, r in zip(("nb", "Sk", "Sk2", "Sv"), (nb2, Sk_2, Sk2_2, Sv_2), (nb, Sk, Sk2, Sv)):
+        assert torch.equal(g, r), name
 
 
 def test_build_rows_equals_build_row():
