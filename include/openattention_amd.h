@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define OA_ABI_VERSION 8
+#define OA_ABI_VERSION 9
 #define OA_EINVAL (-22)
 #define OA_ENOSPC (-28)
 
@@ -437,6 +437,21 @@ int oa_cluster_build(const void* K, const void* V, long kv_stride_h, long kv_str
 int oa_cluster_sums(const void* K, const void* V, long kv_stride_h, long kv_stride_t, int rows, int G,
                     int T, int C, float* nb, float* Sk, float* Sk2, float* Sv, const int32_t* mem,
                     long mem_stride, const int32_t* cstart, const int32_t* clen, void* stream);
+
+/*
+ * The a10 query metric of rows / G KV rows' G query-head rows each: for query row r, with its P
+ * picked question rows q_p (positions pick[p] of q's row r) advanced by their RoPE angles,
+ * r_p = scaling (cos_p * q_p + sin_p * rotate_half(q_p)) in fp64, Mq = fp32(sum_p r_p r_p^T / P),
+ * M_r = mst_half[r % heads] + 0.5 (Mq / max(tr Mq, 1e-12)), written to m_out[r]; the KV row's
+ * mean of its G metrics to gm_out[r / G].  q (rows, Qn, 128) bf16 (q_bf16 = 1) or fp32 with row
+ * and position strides in elements; pick (P) int32, 1 <= P <= 64; cosv, sinv (P, 128) fp64;
+ * mst_half (heads, 128, 128) fp32 (half the trace-normalised rotated static metric); gm_out
+ * (rows / G, 128, 128), m_out (rows, 128, 128) fp32, 16-byte aligned.  Replaces the metric of
+ * inference/methods_eager.py:510-519 (question moment static_top_k.py:185-194).
+ */
+int oa_query_metric(const void* q, int q_bf16, long q_stride_row, long q_stride_pos, int rows, int G,
+                    const int32_t* pick, int P, const double* cosv, const double* sinv, double scaling,
+                    const float* mst_half, int heads, float* gm_out, float* m_out, void* stream);
 
 /*
  * Top-k eigenpairs of symmetric positive semi-definite 128 x 128 fp32 matrices (one-sided Jacobi,

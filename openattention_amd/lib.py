@@ -58,12 +58,13 @@ SIGNATURES = {
     "oa_kmeans_update": [P, P, L, I, I, P, L, I, P, P, P, P, L, P, P, P],
     "oa_cluster_build": [P, P, L, L, I, I, I, P, L, I, P, P, P, P, P, L, P, P, P],
     "oa_cluster_sums": [P, P, L, L, I, I, I, I, P, P, P, P, P, L, P, P, P],
+    "oa_query_metric": [P, I, L, L, I, I, P, I, P, P, Dd, P, I, P, P, P],
     "oa_sym_eig_top": [P, L, I, I, I, P, P, P, P],
 }
 
 # must equal oa_abi_version() of the loaded library (OA_ABI_VERSION in the header): a library
 # built from sources with other argument lists would be handed wrong pointers
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _LIB = None
 

@@ -554,6 +554,36 @@ def qgs_codes(K, T: int, U, codes, scale, amax_ws, zc_ws=None) -> None:
              codes.stride(0), _ptr(scale), _ptr(amax_ws), _ptr(zc_ws), _stream(dev))
 
 
+def query_metric(q, pick, cosv, sinv, scaling: float, mst_half, G: int, gm_out=None, m_out=None):
+    """a10 metric of every query row of q (rows, Qn, 128) bf16 or fp32 (rows = KV rows * G):
+    returns (gm_out (rows / G, 128, 128) group means, m_out (rows, 128, 128) metrics), fp32.
+    pick (P,) int32 question positions; cosv, sinv (P, 128) fp64 RoPE cos / sin of each picked
+    row's advance; mst_half (heads, 128, 128) fp32, used for row r as mst_half[r % heads]."""
+    dev = _dev(q, pick, cosv, sinv, mst_half, gm_out, m_out)
+    _need(q.dim() == 3 and q.shape[-1] == HEAD_DIM and q.stride(-1) == 1
+          and q.dtype in (torch.bfloat16, torch.float32), "q: (rows, Qn, 128) bf16 or fp32, rows of dims contiguous")
+    rows = q.shape[0]
+    _need(rows % G == 0, "rows: a multiple of G")
+    _need(pick.dtype == torch.int32 and pick.dim() == 1 and pick.is_contiguous(), "pick: (P,) int32")
+    P = pick.numel()
+    _need(1 <= P <= 64, "P: 1..64 picked rows")
+    for t, nm in ((cosv, "cosv"), (sinv, "sinv")):
+        _need(t.dtype == torch.float64 and t.shape == (P, HEAD_DIM) and t.is_contiguous(), f"{nm}: (P, 128) fp64")
+    _need(mst_half.dtype == torch.float32 and mst_half.dim() == 3 and mst_half.shape[1:] == (HEAD_DIM, HEAD_DIM)
+          and mst_half.is_contiguous(), "mst_half: (heads, 128, 128) fp32 contiguous")
+    if gm_out is None:
+        gm_out = torch.empty(rows // G, HEAD_DIM, HEAD_DIM, device=dev, dtype=torch.float32)
+    if m_out is None:
+        m_out = torch.empty(rows, HEAD_DIM, HEAD_DIM, device=dev, dtype=torch.float32)
+    for t, n_, nm in ((gm_out, rows // G, "gm_out"), (m_out, rows, "m_out")):
+        _need(t.dtype == torch.float32 and t.is_contiguous() and t.shape == (n_, HEAD_DIM, HEAD_DIM),
+              f"{nm}: ({n_}, 128, 128) fp32 contiguous")
+    lib.call("oa_query_metric", _ptr(q), int(q.dtype == torch.bfloat16), q.stride(0), q.stride(1), rows, G,
+             _ptr(pick), P, _ptr(cosv), _ptr(sinv), float(scaling), _ptr(mst_half), mst_half.shape[0],
+             _ptr(gm_out), _ptr(m_out), _stream(dev))
+    return gm_out, m_out
+
+
 def sym_eig_top(M, k: int, sweeps=None):
     """Top-k eigenpairs of symmetric positive semi-definite (batch, 128, 128) fp32 matrices (the
     lower triangle is read): (evals (batch, k), evecs (batch, 128, k)), ascending, the last k of

@@ -7,8 +7,9 @@ multibin.py:1894):
        (StaticTopKMasker._rot_avg, static_top_k.py:103-131); M_q from P <= 64
        question rows, each rotated to T (static_top_k.py:185-194); M = 1/2 nt(M_st) + 1/2
        nt(M_q), nt = trace normalisation; U = top-32 eigenvectors of the group-mean M per KV
-       head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.  The metric in
-       host torch on the device, the eigenpairs from oa_sym_eig_top (one-sided Jacobi).
+       head; W = top-16 eigenvectors * sqrt(eigenvalue) per query head, in bf16.  The rotated
+       static metric in torch on the device, the question moments, blend and group means by
+       oa_query_metric, the eigenpairs by oa_sym_eig_top (one-sided Jacobi).
   a11  codes: oa_qgs_codes (zc = k U, scale = max(max_t |zc| / 127, 1e-12), codes =
        clamp(rint(zc / scale), -127, 127); static_top_k.py:174-181).
   a12  oa_qgc_project (zP = bf16(k W) - colmean on the bf16 matrix cores), then 4 Lloyd
@@ -137,6 +138,26 @@ def bases(M: torch.Tensor, HKV: int, G: int):
     return bases_from_eigenpairs(ev, vec, HKV)
 
 
+def metric_device(M_pre: torch.Tensor, qrows: torch.Tensor, T: int, inv_freq: torch.Tensor,
+                  scaling: float, G: int, gm_out=None, m_out=None):
+    """query_metric on the library's kernel for every query-head row of qrows (R, Qn, D) (R =
+    KV rows * G, row r using head r % HQ of M_pre (HQ, D, D)): the rotated static metric's half
+    is formed once here in torch (query_metric's arithmetic), the question moments, the blend and
+    each KV row's group mean by oa_query_metric.  Returns (group means (R / G, D, D), metrics
+    (R, D, D)), into gm_out / m_out when given: basis_matrices' two parts."""
+    from openattention_amd import ops
+    dev = qrows.device
+    inv_freq = inv_freq.to(dev)
+    mst = (0.5 * trace_norm(rot_avg(M_pre.to(dev), inv_freq, scaling, T, WIN))).contiguous()
+    Qn = qrows.shape[-2]
+    # the picks depend on Qn only: chosen on the host (on the device, unique() waits for the
+    # queue to drain to size its output)
+    pick = question_picks(Qn, "cpu")
+    pick_d = pick.to(device=dev, dtype=torch.int32)
+    c, sn = rope_trig(inv_freq, (Qn - pick).to(dev))
+    return ops.query_metric(qrows, pick_d, c.contiguous(), sn.contiguous(), scaling, mst, G, gm_out, m_out)
+
+
 def kmeans_init(T: int, C: int, layer: int) -> torch.Tensor:
     """Initial centroid positions: the first C of a seeded permutation of the T tokens
     (multibin.py:1894-1895; CPU generator, as the reference)."""
@@ -162,6 +183,7 @@ def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor,
             e.record()
             marks.append((name, e))
 
+    from openattention_amd import ops
     dev = K.device
     if dev.type != "cuda":
         raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
@@ -169,9 +191,10 @@ def build_row(st, b: int, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor,
     HQ = HKV * G
     if marks is not None:
         mark("start")
-    M = query_metric(M_pre.to(dev), qrows, T, inv_freq.to(dev), scaling)           # (HQ, D, D)
+    gm, M = metric_device(M_pre, qrows, T, inv_freq, scaling, G)                  # (HKV / HQ, D, D)
     mark("metric")
-    U, W = bases(M, HKV, G)
+    ev, vec = ops.sym_eig_top(torch.cat([gm, M], 0), RQ)
+    U, W = bases_from_eigenpairs(ev, vec, HKV)
     st.U[b * HKV:(b + 1) * HKV] = U
     st.W[b * HQ:(b + 1) * HQ] = W
     mark("bases")
@@ -195,6 +218,7 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
             e.record()
             marks.append((name, e))
 
+    from openattention_amd import ops
     dev = K.device
     if dev.type != "cuda":
         raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
@@ -205,14 +229,13 @@ def build_rows(st, K: torch.Tensor, V: torch.Tensor, qrows: torch.Tensor, T: int
     if B * HKV > st.U.shape[0] or qrows.shape[0] != B or qrows.shape[1] != HQ:
         raise ValueError("build_rows: K, qrows and the state disagree on B, HKV or HQ")
     mark("start")
-    # the rotated static metric depends on the layer and T only: formed once for all rows, with
-    # query_metric's arithmetic
-    inv_freq = inv_freq.to(dev)
-    mst = 0.5 * trace_norm(rot_avg(M_pre.to(dev), inv_freq, scaling, T, WIN))
-    Mq = question_moment(qrows.reshape(B * HQ, qrows.shape[2], D), inv_freq, scaling)
-    M = mst + 0.5 * trace_norm(Mq).view(B, HQ, D, D)                                # (B, HQ, D, D)
+    # the rotated static metric depends on the layer and T only: formed once for all rows
+    Mall = torch.empty(B * HKV + B * HQ, D, D, device=dev)
+    metric_device(M_pre, qrows.reshape(B * HQ, qrows.shape[2], D), T, inv_freq, scaling, G,
+                  Mall[:B * HKV], Mall[B * HKV:])
     mark("metric")
-    U, W = bases(M.reshape(B * HQ, D, D), B * HKV, G)
+    ev, vec = ops.sym_eig_top(Mall, RQ)
+    U, W = bases_from_eigenpairs(ev, vec, B * HKV)
     st.U[:B * HKV] = U
     st.W[:B * HQ] = W
     mark("bases")
@@ -229,24 +252,26 @@ def build_layers(states, Ks, Vs, qrows, T: int, M_pre: torch.Tensor, inv_freq: t
     the (L, HQ, D, D) static metric of every layer."""
     if not (len(states) == len(Ks) == len(Vs) == len(qrows) == len(layers)) or not layers:
         raise ValueError("build_layers: one state, K, V, question block and layer index per layer")
+    from openattention_amd import ops
     dev = Ks[0].device
     if dev.type != "cuda":
         raise RuntimeError("the index build runs on the HIP kernels: K, V must be on a HIP device")
     B, HKV = Ks[0].shape[0], Ks[0].shape[1]
     HQ = HKV * G
-    inv_freq = inv_freq.to(dev)
-    Ms = []
-    for st, K, V, q, layer in zip(states, Ks, Vs, qrows, layers):
+    nl = len(layers)
+    # every layer's group means first, then every layer's head metrics (basis_matrices' order)
+    Mall = torch.empty(nl * (B * HKV + B * HQ), D, D, device=dev)
+    for i, (st, K, V, q, layer) in enumerate(zip(states, Ks, Vs, qrows, layers)):
         if not (K.is_contiguous() and V.is_contiguous() and K.shape == V.shape and K.dim() == 4
                 and K.shape[:2] == (B, HKV)):
             raise ValueError("build_layers: K and V must be contiguous (B, HKV, Lmax, D) tensors of one shape")
         if B * HKV > st.U.shape[0] or q.shape[0] != B or q.shape[1] != HQ:
             raise ValueError("build_layers: K, qrows and the state disagree on B, HKV or HQ")
-        mst = 0.5 * trace_norm(rot_avg(M_pre[layer].to(dev), inv_freq, scaling, T, WIN))
-        Mq = question_moment(q.reshape(B * HQ, q.shape[2], D), inv_freq, scaling)
-        Ms.append((mst + 0.5 * trace_norm(Mq).view(B, HQ, D, D)).reshape(B * HQ, D, D))
-    nl = len(layers)
-    U, W = bases(torch.cat(Ms, 0), nl * B * HKV, G)
+        g0, m0 = i * B * HKV, nl * B * HKV + i * B * HQ
+        metric_device(M_pre[layer], q.reshape(B * HQ, q.shape[2], D), T, inv_freq, scaling, G,
+                      Mall[g0:g0 + B * HKV], Mall[m0:m0 + B * HQ])
+    ev, vec = ops.sym_eig_top(Mall, RQ)
+    U, W = bases_from_eigenpairs(ev, vec, nl * B * HKV)
     for i, (st, K, V, layer) in enumerate(zip(states, Ks, Vs, layers)):
         st.U[:B * HKV] = U[i * B * HKV:(i + 1) * B * HKV]
         st.W[:B * HQ] = W[i * B * HQ:(i + 1) * B * HQ]

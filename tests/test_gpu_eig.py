@@ -138,3 +138,31 @@ def test_bases_on_device_from_the_build_metric():
         P, Pr = vec[i] @ vec[i].T, V[:, -32:] @ V[:, -32:].T
         assert np.abs(P - Pr).max() < 1e-3
     print(f"  sweeps {sweeps.min()}..{sweeps.max()}")
+
+
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float32])
+def test_query_metric_kernel_against_host_metric_and_restatement(q_dtype):
+    """oa_query_metric (question moments in fp64, trace normalisation, the blend with the
+    rotated static metric's half, group means) against prefill.query_metric (host torch, pinned
+    to the oracle's explicit-rotation restatement by tests/test_a10_pins.py) and against the
+    oracle itself, for two sequences of one layer (row r uses head r % HQ)."""
+    print(f"[case] query metric kernel {q_dtype}", flush=True)
+    from tests.helpers import HKV as HKV_, G as G_
+    HQ_ = HKV_ * G_
+    static = synth.static_metric(1)
+    B, N = 2, 4096
+    _, _, _, qq, _ = synth.make_layer(1, B, N, N, 64, "cpu")
+    qrows = qq.to(q_dtype)                                         # (B, HQ, Qn, D)
+    T = N - 1
+    M_pre, inv, sc = static["M"][0], static["inv_freq"], float(static["attention_scaling"])
+    gm, M = prefill.metric_device(M_pre, qrows.reshape(B * HQ_, qrows.shape[2], D).to(DEV), T, inv, sc, G_)
+    torch.cuda.synchronize()
+    gm, M = gm.cpu().double().numpy(), M.cpu().double().numpy()
+    for b in range(B):
+        ref = prefill.query_metric(M_pre, qrows[b].float(), T, inv, sc).double().numpy()   # host torch
+        got = M[b * HQ_:(b + 1) * HQ_]
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+        refg = ref.reshape(HKV_, G_, D, D).mean(1)
+        assert np.abs(gm[b * HKV_:(b + 1) * HKV_] - refg).max() <= 1e-5 * np.abs(refg).max()
+        o = O.query_metric(M_pre.double().numpy(), qrows[b].float().numpy(), T, inv.double().numpy(), sc)
+        assert np.abs(got - o).max() <= 2e-5 * np.abs(o).max()

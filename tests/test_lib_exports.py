@@ -34,7 +34,7 @@ def test_binding_matches_header():
 
 def test_library_loads_and_reports():
     L = lib.load()
-    assert L.oa_abi_version() == lib.ABI_VERSION == 8
+    assert L.oa_abi_version() == lib.ABI_VERSION == 9
     assert b"invalid argument" in L.oa_error_string(-22)
     for name in lib.SIGNATURES:
         assert getattr(L, name) is not None
@@ -57,6 +57,9 @@ def test_argument_checks_reject_before_launch():
     # cluster sums over built lists: C above 256, rows not a multiple of G
     assert L.oa_cluster_sums(16, 16, 128 * 64, 128, 8, 4, 64, 300, 16, 16, 16, 16, 16, 64, 16, 16, None) == -22
     assert L.oa_cluster_sums(16, 16, 128 * 64, 128, 6, 4, 64, 8, 16, 16, 16, 16, 16, 64, 16, 16, None) == -22
+    # query metric: more than 64 picked rows, rows not a multiple of G
+    assert L.oa_query_metric(16, 1, 8192, 128, 8, 4, 16, 65, 16, 16, 1.0, 16, 32, 16, 16, None) == -22
+    assert L.oa_query_metric(16, 1, 8192, 128, 6, 4, 16, 8, 16, 16, 1.0, 16, 32, 16, 16, None) == -22
     # eigensolver: n other than 128, k outside 1..64, a matrix stride below 128 * 128
     assert L.oa_sym_eig_top(16, 64 * 64, 1, 64, 16, 16, 16, None, None) == -22
     assert L.oa_sym_eig_top(16, 128 * 128, 1, 128, 65, 16, 16, None, None) == -22
