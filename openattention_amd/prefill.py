@@ -138,6 +138,15 @@ def bases(M: torch.Tensor, HKV: int, G: int):
     return bases_from_eigenpairs(ev, vec, HKV)
 
 
+def _h2d(x: torch.Tensor, dev) -> torch.Tensor:
+    """x on dev; a host tensor goes through pinned memory without waiting for the stream (a
+    pageable copy makes the host wait for every queued launch, and the device then idles while the
+    next launches are issued)."""
+    if x.device.type != "cpu":
+        return x.to(dev)
+    return x.pin_memory().to(dev, non_blocking=True)
+
+
 def metric_device(M_pre: torch.Tensor, qrows: torch.Tensor, T: int, inv_freq: torch.Tensor,
                   scaling: float, G: int, gm_out=None, m_out=None):
     """query_metric on the library's kernel for every query-head row of qrows (R, Qn, D) (R =
@@ -147,14 +156,14 @@ def metric_device(M_pre: torch.Tensor, qrows: torch.Tensor, T: int, inv_freq: to
     (R, D, D)), into gm_out / m_out when given: basis_matrices' two parts."""
     from openattention_amd import ops
     dev = qrows.device
-    inv_freq = inv_freq.to(dev)
-    mst = (0.5 * trace_norm(rot_avg(M_pre.to(dev), inv_freq, scaling, T, WIN))).contiguous()
+    inv_freq = _h2d(inv_freq, dev)
+    mst = (0.5 * trace_norm(rot_avg(_h2d(M_pre, dev), inv_freq, scaling, T, WIN))).contiguous()
     Qn = qrows.shape[-2]
     # the picks depend on Qn only: chosen on the host (on the device, unique() waits for the
     # queue to drain to size its output)
     pick = question_picks(Qn, "cpu")
-    pick_d = pick.to(device=dev, dtype=torch.int32)
-    c, sn = rope_trig(inv_freq, (Qn - pick).to(dev))
+    pick_d = _h2d(pick.to(torch.int32), dev)
+    c, sn = rope_trig(inv_freq, Qn - pick_d)
     return ops.query_metric(qrows, pick_d, c.contiguous(), sn.contiguous(), scaling, mst, G, gm_out, m_out)
 
 
@@ -302,7 +311,7 @@ def _build_device(st, r0: int, K: torch.Tensor, V: torch.Tensor, T: int, layer: 
     colmean = st.colmean[q0:q0 + HQ]
     ops.qgc_project(K, T, st.W[q0:q0 + HQ], G, zraw, colmean)
     mark("project")
-    init = kmeans_init(T, C, layer).to(device=dev, dtype=torch.int32)
+    init = _h2d(kmeans_init(T, C, layer).to(torch.int32), dev)
     cent = st.cent[q0:q0 + HQ]
     cent.copy_(zraw.index_select(1, init.long()).float() - colmean[:, None, :])
     asg, asg8 = st.asg[q0:q0 + HQ], st.asg8[q0:q0 + HQ]
