@@ -426,6 +426,19 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
 
 constexpr int kMemBuf = 2048;   // member positions staged in LDS at a time
 
+// a wave copies n <= kMemBuf member positions into LDS, eight loads per lane in flight at a time
+// (one at a time, each copy waited on its load)
+__device__ __forceinline__ void stage_members(int* s_pos, const int32_t* ml, int n, int lane) {
+  for (int b = 0; b < n; b += 512) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = ml[min(b + lane + 64 * u, n - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (b + lane + 64 * u < n) s_pos[b + lane + 64 * u] = v[u];
+  }
+}
+
 // One wave per (cluster, query row): the members in position order (the row's member lists of
 // csr_sort_kernel), their zP rows staged kUB at a time through LDS (the next batch requested
 // while one is summed) and summed in fp64 by lanes 0..15 (one column each) in that order;
@@ -463,18 +476,18 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const uint16_t* zraw,
   for (int e = 0; e < 4; ++e) cq[e] = colmean[row * kRC + 4 * (lane & 3) + e];
   double acc = 0.0;
   int cnt = 0;
-  // lane l reads member quarter l % 4 of members l / 4 + 16 b of a batch
+  // lane l reads member quarter l % 4 of members l / 4 + 16 b of a batch; a slot past the last
+  // member reads the last member's row again (never summed), so the loads issue without branches
   auto load = [&](uint2* w, int k0, int n) {
 #pragma unroll
     for (int b = 0; b < kUB / 16; ++b) {
-      const int m = k0 + (lane >> 2) + 16 * b;
-      w[b] = m < n ? *reinterpret_cast<const uint2*>(zr + (long)s_pos[m] * kRC + 4 * (lane & 3))
-                   : make_uint2(0u, 0u);
+      const int m = min(k0 + (lane >> 2) + 16 * b, n - 1);
+      w[b] = *reinterpret_cast<const uint2*>(zr + (long)s_pos[m] * kRC + 4 * (lane & 3));
     }
   };
   for (int i0 = 0; i0 < cl; i0 += kMemBuf) {
     const int n = min(kMemBuf, cl - i0);
-    for (int i = lane; i < n; i += 64) s_pos[i] = ml[i0 + i];
+    stage_members(s_pos, ml + i0, n, lane);
     __syncthreads();
     uint2 w[kUB / 16];
     if (n > 0) load(w, 0, n);
@@ -488,9 +501,19 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const uint16_t* zraw,
       // the next batch's rows are requested while this one is summed
       if (k0 + kUB < n) load(w, k0 + kUB, n);
       if (lane < kRC) {
+        // 16 staged values read together, then added in member order (a slot past the last
+        // member adds +0, which leaves the sum as it is: it is never -0 starting from +0)
         const float* st = reinterpret_cast<const float*>(s_stage);
         const int mm = min(kUB, n - k0);
-        for (int m = 0; m < mm; ++m) acc += (double)st[m * kRC + lane];
+        for (int m0 = 0; m0 < mm; m0 += 16) {
+          float v[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) v[u] = st[(m0 + u) * kRC + lane];   // m0 + u < kUB
+#pragma unroll
+          for (int u = 0; u < 16; ++u) v[u] = m0 + u < mm ? v[u] : 0.f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u) acc += (double)v[u];
+        }
       }
       __syncthreads();
     }
@@ -616,7 +639,7 @@ __global__ void __launch_bounds__(64) cluster_sums_kernel(const uint16_t* K, con
   constexpr int U = 16;
   for (int i0 = 0; i0 < cl; i0 += kMemBuf) {
     const int n = min(kMemBuf, cl - i0);
-    for (int i = lane; i < n; i += 64) s_pos[i] = ml[i0 + i];
+    stage_members(s_pos, ml + i0, n, lane);
     __syncthreads();
     for (int k = 0; k < n; k += U) {
       uint32_t kw[U], vw[U];

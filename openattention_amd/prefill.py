@@ -142,9 +142,62 @@ def _h2d(x: torch.Tensor, dev) -> torch.Tensor:
     """x on dev; a host tensor goes through pinned memory without waiting for the stream (a
     pageable copy makes the host wait for every queued launch, and the device then idles while the
     next launches are issued)."""
-    if x.device.type != "cpu":
+    if x.device.type != "cpu" or torch.device(dev).type == "cpu":
         return x.to(dev)
     return x.pin_memory().to(dev, non_blocking=True)
+
+
+_CONSTS: dict = {}
+
+
+def _metric_consts(T: int, Qn: int, inv_freq: torch.Tensor, scaling: float, dev):
+    """What the device metric needs that depends on T, Qn, the RoPE frequencies and the scaling
+    only, formed once per such tuple and device (a host inv_freq is the key; a device one is not
+    cached): rot_avg's four window-mean coefficient matrices in fp32 with rotate_half's signs
+    folded in, rotate_half's index map (J x = sgn * x[perm]), the question picks and their RoPE
+    cos / sin."""
+    key = None
+    if inv_freq.device.type == "cpu":
+        key = (int(T), int(Qn), float(scaling), inv_freq.to(torch.float64).numpy().tobytes(),
+               str(torch.device(dev)))
+        hit = _CONSTS.get(key)
+        if hit is not None:
+            return hit
+    invd = _h2d(inv_freq, dev)
+    t = torch.arange(T, T + WIN, device=dev, dtype=torch.float64)
+    c, sn = rope_trig(invd, t)                                               # (WIN, D) each
+    s2 = float(scaling) * float(scaling) / WIN
+    a_cc = (c.T @ c) * s2
+    a_cs = (c.T @ sn) * s2
+    a_ss = (sn.T @ sn) * s2
+    half = D // 2
+    perm = torch.cat([torch.arange(half, D, device=dev), torch.arange(0, half, device=dev)])
+    sgn = torch.ones(D, device=dev, dtype=torch.float64)
+    sgn[:half] = -1.0
+    # a * (-m) == (-a) * m exactly, so these products are rot_avg's bit for bit
+    coef = (a_cc.float(), (a_cs * sgn[None, :]).float(), (a_cs.T * sgn[:, None]).float(),
+            (a_ss * sgn[:, None] * sgn[None, :]).float())
+    pick = question_picks(Qn, "cpu")
+    pick_d = _h2d(pick.to(torch.int32), dev)
+    cq, sq = rope_trig(invd, Qn - pick_d)
+    out = (coef, perm, pick_d, cq.contiguous(), sq.contiguous())
+    if key is not None:
+        if len(_CONSTS) >= 16:
+            _CONSTS.clear()
+        _CONSTS[key] = out
+    return out
+
+
+def static_half(M_pre: torch.Tensor, T: int, inv_freq: torch.Tensor, scaling: float, dev,
+                Qn: int = 1) -> torch.Tensor:
+    """1/2 trace_norm(rot_avg(M_pre, ..., T, WIN)) on dev, bit-identical to that expression:
+    with the cached coefficients the rotated metric is four products of M, M[:, perm],
+    M[perm, :] and M[perm][:, perm] (rotate_half as a gather), summed in rot_avg's order."""
+    (A1, A2, A3, A4), perm = _metric_consts(T, Qn, inv_freq, scaling, dev)[:2]
+    M = _h2d(M_pre, dev).float()
+    Mr = M.index_select(-2, perm)
+    raw = A1 * M + A2 * M.index_select(-1, perm) + A3 * Mr + A4 * Mr.index_select(-1, perm)
+    return 0.5 * trace_norm(raw)
 
 
 def metric_device(M_pre: torch.Tensor, qrows: torch.Tensor, T: int, inv_freq: torch.Tensor,
@@ -156,15 +209,12 @@ def metric_device(M_pre: torch.Tensor, qrows: torch.Tensor, T: int, inv_freq: to
     (R, D, D)), into gm_out / m_out when given: basis_matrices' two parts."""
     from openattention_amd import ops
     dev = qrows.device
-    inv_freq = _h2d(inv_freq, dev)
-    mst = (0.5 * trace_norm(rot_avg(_h2d(M_pre, dev), inv_freq, scaling, T, WIN))).contiguous()
     Qn = qrows.shape[-2]
     # the picks depend on Qn only: chosen on the host (on the device, unique() waits for the
-    # queue to drain to size its output)
-    pick = question_picks(Qn, "cpu")
-    pick_d = _h2d(pick.to(torch.int32), dev)
-    c, sn = rope_trig(inv_freq, Qn - pick_d)
-    return ops.query_metric(qrows, pick_d, c.contiguous(), sn.contiguous(), scaling, mst, G, gm_out, m_out)
+    # queue to drain to size its output), with the other T / Qn constants, once
+    _, _, pick_d, c, sn = _metric_consts(T, Qn, inv_freq, scaling, dev)
+    mst = static_half(M_pre, T, inv_freq, scaling, dev, Qn).contiguous()
+    return ops.query_metric(qrows, pick_d, c, sn, scaling, mst, G, gm_out, m_out)
 
 
 def kmeans_init(T: int, C: int, layer: int) -> torch.Tensor:

@@ -71,6 +71,24 @@ def test_static_metric_window_mean(p, s):
     assert np.allclose(ident, s * s * np.eye(D), atol=1e-6)
 
 
+@pytest.mark.parametrize("T", [100, 4095, 32767])
+def test_static_half_is_rot_avg_bit_for_bit(T):
+    """The device build's static half (cached coefficients with rotate_half's signs folded in,
+    rotate_half as a gather) equals 1/2 trace_norm(rot_avg(...)) exactly; the cached constants are
+    reused for a second call and the picks' trig matches rope_trig of Qn - pick."""
+    st = synth.static_metric(2)
+    sc = float(st["attention_scaling"])
+    for layer in range(2):
+        ref = 0.5 * prefill.trace_norm(prefill.rot_avg(st["M"][layer], st["inv_freq"], sc, T, prefill.WIN))
+        got = prefill.static_half(st["M"][layer], T, st["inv_freq"], sc, "cpu", 40)
+        assert torch.equal(ref, got)
+    a = prefill._metric_consts(T, 40, st["inv_freq"], sc, "cpu")
+    assert prefill._metric_consts(T, 40, st["inv_freq"], sc, "cpu") is a
+    pick = prefill.question_picks(40, "cpu")
+    c, sn = prefill.rope_trig(st["inv_freq"], 40 - pick)
+    assert torch.equal(a[2].long(), pick) and torch.equal(a[3], c) and torch.equal(a[4], sn)
+
+
 def test_static_metric_window_mean_is_not_a_single_rotation():
     """The window mean differs from rotating by p alone (a dropped average would pass the
     trace check but not this one)."""

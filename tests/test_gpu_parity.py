@@ -947,6 +947,37 @@ def test_build_projection_and_kmeans(T):
         assert np.array_equal(mem_ws.cpu().numpy()[:, :T], mem_ref)
 
 
+def test_kmeans_update_uneven_clusters():
+    """The update's member-ordered fp64 sums over clusters of 0, 1, 15, 16, 17, 129 and 2100 +
+    members (several staged batches, more than one LDS load of member positions, partial 16-value
+    chunks) and a planted assignment: bit-exact with the restatement."""
+    print("[case] k-means update, uneven clusters", flush=True)
+    rng = np.random.default_rng(23)
+    R, T, Lmax, C = 4, 4095, 4160, 8
+    zraw = torch.from_numpy(f32_to_bf16((rng.standard_normal((R, T, 16)) * 2.0).astype(np.float32))
+                            .view(np.int16)).to(DEV)
+    cm = torch.from_numpy(rng.standard_normal((R, 16)).astype(np.float32)).to(DEV)
+    zP_np = (bf16_to_f32(zraw.cpu().numpy().view(np.uint16)) - cm.cpu().numpy()[:, None, :]).astype(np.float32)
+    sizes = [0, 1, 15, 16, 17, 129]
+    a = np.empty((R, T), np.int32)
+    for r in range(R):
+        lab = np.concatenate([np.full(n, c, np.int32) for c, n in enumerate(sizes)]
+                             + [np.full(T - sum(sizes) - 300, 6, np.int32), np.full(300, 7, np.int32)])
+        a[r] = rng.permutation(lab)
+    asg8 = torch.zeros(R, -(-Lmax // 64) * 64, device=DEV, dtype=torch.uint8)
+    asg8[:, :T] = torch.from_numpy(a.astype(np.uint8)).to(DEV)
+    init = rng.choice(T, C, replace=False).astype(np.int32)
+    cent = torch.full((R, C, 16), float("nan"), device=DEV)
+    cnt = torch.empty(R, C, device=DEV)
+    mem_ws = torch.empty(R, Lmax, device=DEV, dtype=torch.int32)
+    cs_ws, cl_ws = (torch.empty(R, C, device=DEV, dtype=torch.int32) for _ in range(2))
+    ops.kmeans_update(zraw, cm, T, asg8, _i32(init), cent, mem_ws, cs_ws, cl_ws, cnt)
+    torch.cuda.synchronize()
+    c_ref, n_ref = O.kmeans_update(zP_np, a, C, init)
+    assert np.array_equal(cnt.cpu().numpy(), n_ref)
+    assert np.array_equal(cent.cpu().numpy(), c_ref)
+
+
 def test_kmeans_assign_with_a_zero_centroid():
     """A centroid at the origin (bf16(|c|^2 / 2) = +0, where bf16(dot - half) can be -0): the
     assignment takes its -0 -> +0 path for the whole row set and still agrees with the
