@@ -330,8 +330,18 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
   const int CB = (C + 15) / 16;
   const int ntiles = (T + 63) / 64;
   const float* cr = cent + (long)row * C * kRC;
-  for (int i = threadIdx.x; i < CB * 16 * kRC; i += kAsgThreads)
-    s_cb[i] = i < C * kRC ? oa::f32_to_bf16(cr[i]) : 0;
+  // four centroid values per thread and iteration (C * kRC is a multiple of 4)
+  for (int i = 4 * threadIdx.x; i < CB * 16 * kRC; i += 4 * kAsgThreads) {
+    if (i < C * kRC) {
+      const float4 x = *reinterpret_cast<const float4*>(cr + i);
+      s_cb[i] = oa::f32_to_bf16(x.x);
+      s_cb[i + 1] = oa::f32_to_bf16(x.y);
+      s_cb[i + 2] = oa::f32_to_bf16(x.z);
+      s_cb[i + 3] = oa::f32_to_bf16(x.w);
+    } else {
+      s_cb[i] = s_cb[i + 1] = s_cb[i + 2] = s_cb[i + 3] = 0;
+    }
+  }
   int zero_half = 0;          // this thread staged a real centroid with bf16(|c|^2 / 2) = +0
   for (int c = threadIdx.x; c < CB * 16; c += kAsgThreads) {
     uint16_t hv = 0x7f80u;   // padding centroids: +inf, a distance of -inf ranks below every real one
@@ -448,8 +458,10 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const uint16_t* zraw,
                                                            const int32_t* cstart, const int32_t* clen,
                                                            const int32_t* init_idx, float* cent,
                                                            float* cnt_out) {
-  constexpr int kUB = 128;                     // members per staged batch
-  __shared__ int s_pos[kMemBuf];
+  constexpr int kUB = 64;                      // members per staged batch
+  constexpr int kUpdBuf = 512;                 // member positions staged at a time (6 KB of LDS
+                                               // per wave: about 26 waves per compute unit)
+  __shared__ int s_pos[kUpdBuf];
   __shared__ float4 s_stage[kUB * (kRC / 4)];
   const int lane = threadIdx.x;
   // the C workgroups of a row run on one XCD (workgroups are dealt to the 8 XCDs in turn), so the
@@ -485,8 +497,8 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const uint16_t* zraw,
       w[b] = *reinterpret_cast<const uint2*>(zr + (long)s_pos[m] * kRC + 4 * (lane & 3));
     }
   };
-  for (int i0 = 0; i0 < cl; i0 += kMemBuf) {
-    const int n = min(kMemBuf, cl - i0);
+  for (int i0 = 0; i0 < cl; i0 += kUpdBuf) {
+    const int n = min(kUpdBuf, cl - i0);
     stage_members(s_pos, ml + i0, n, lane);
     __syncthreads();
     uint2 w[kUB / 16];
