@@ -548,19 +548,35 @@ __global__ void __launch_bounds__(64) kmeans_update_kernel(const uint16_t* zraw,
 // a 16-lane scan per cluster turns the counts into the waves' starts in wave order -- so equal
 // ids keep their position order inside a step, and the steps follow each other.
 constexpr int kSortThreads = 1024;
+constexpr int kSortStage = 32768;   // rows of at most this many ids are staged in LDS by the sort
 constexpr int kSortWaves = kSortThreads / 64;
 __global__ void __launch_bounds__(kSortThreads) csr_sort_kernel(int T, const uint8_t* asg8, long a8s, int C,
                                                                float* nb, int32_t* cstart, int32_t* clen,
-                                                               int32_t* mem, long ms) {
+                                                               int32_t* mem, long ms, int staged) {
   __shared__ int s_base[kMaxC];
   __shared__ int s_wcnt[kMaxC][kSortWaves];
+  __shared__ __align__(16) uint8_t s_ids[kSortStage];   // the row's ids when staged (T <= kSortStage)
   const int row = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint8_t* ar = asg8 + (long)row * a8s;
   int32_t* mr = mem + (long)row * ms;
   for (int c = tid; c < kMaxC; c += kSortThreads) s_base[c] = 0;
   __syncthreads();
-  for (int t = tid; t < T; t += kSortThreads) atomicAdd(&s_base[ar[t]], 1);
+  if (staged) {
+    // 16 ids per thread and load (rows 16-byte aligned, their stride a multiple of 16), kept in
+    // LDS for the scatter pass
+    const int T16 = (T + 15) / 16;
+    for (int i = tid; i < T16; i += kSortThreads) {
+      const uint4 w = reinterpret_cast<const uint4*>(ar)[i];
+      *reinterpret_cast<uint4*>(s_ids + 16 * i) = w;
+      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int b = 0; b < 16; ++b)
+        if (16 * i + b < T) atomicAdd(&s_base[(q[b >> 2] >> (8 * (b & 3))) & 0xffu], 1);
+    }
+  } else {
+    for (int t = tid; t < T; t += kSortThreads) atomicAdd(&s_base[ar[t]], 1);
+  }
   __syncthreads();
   if (wave == 0) {
     int v[4], loc = 0;
@@ -586,7 +602,7 @@ __global__ void __launch_bounds__(kSortThreads) csr_sort_kernel(int T, const uin
     __syncthreads();
     const int p = p0 + tid;
     const bool valid = p < T;
-    const int x = valid ? (int)ar[p] : 0;
+    const int x = valid ? (int)(staged ? s_ids[p] : ar[p]) : 0;
     unsigned long long m = __ballot(valid);
 #pragma unroll
     for (int bit = 0; bit < 8; ++bit) {
@@ -737,6 +753,13 @@ extern "C" int oa_kmeans_assign(const uint16_t* zraw, const float* colmean, long
   return OA_LAUNCH_STATUS();
 }
 
+// the sort stages a row's ids in LDS with 16-byte loads when the row fits and its rows are
+// 16-byte aligned with a stride that is a multiple of 16 (it then reads up to the next multiple of
+// 16 of T, inside the row's stride)
+static int sort_staged(int T, const uint8_t* asg8, long asg8_stride) {
+  return T <= kSortStage && asg8_stride % 16 == 0 && (reinterpret_cast<uintptr_t>(asg8) & 15) == 0;
+}
+
 extern "C" int oa_kmeans_update(const uint16_t* zraw, const float* colmean, long z_stride, int rows,
                                 int T, const uint8_t* asg8, long asg8_stride, int C,
                                 const int32_t* init_idx, float* cent, float* cnt_out, int32_t* mem_ws,
@@ -747,7 +770,7 @@ extern "C" int oa_kmeans_update(const uint16_t* zraw, const float* colmean, long
     return OA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(csr_sort_kernel, dim3(rows), dim3(kSortThreads), 0, s, T, asg8, asg8_stride, C,
-                     nullptr, cstart_ws, clen_ws, mem_ws, mem_stride);
+                     nullptr, cstart_ws, clen_ws, mem_ws, mem_stride, sort_staged(T, asg8, asg8_stride));
   hipLaunchKernelGGL(kmeans_update_kernel, dim3(C * rows), dim3(64), 0, s, zraw, colmean, z_stride, C,
                      mem_ws, mem_stride, cstart_ws, clen_ws, init_idx, cent, cnt_out);
   return OA_LAUNCH_STATUS();
@@ -764,7 +787,7 @@ extern "C" int oa_cluster_build(const void* K, const void* V, long kv_stride_h, 
     return OA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(csr_sort_kernel, dim3(rows), dim3(kSortThreads), 0, s, T, asg8, asg8_stride, C, nb,
-                     cstart, clen, mem, mem_stride);
+                     cstart, clen, mem, mem_stride, sort_staged(T, asg8, asg8_stride));
   hipLaunchKernelGGL(cluster_sums_kernel, dim3(C * rows), dim3(64), 0, s,
                      reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
                      kv_stride_h, kv_stride_t, G, C, cstart, clen, Sk, Sk2, Sv, mem, mem_stride,
