@@ -187,52 +187,62 @@ __global__ void __launch_bounds__(kCodeThreads) codes_write_kernel(const uint16_
 
 // ---------------------------------------------------------------------------------- projection
 constexpr int kProjTiles = 8;    // 64-token tiles per wave (the row's W operands loaded once)
-// One wave per (64-token tile, query row).  Four 16-token blocks, each 16 tokens x 16 columns
+// One wave per (8 64-token tiles, query row or KV row).  Four 16-token blocks, each 16 tokens x 16 columns
 // from four v_mfma_f32_16x16x32_bf16 over d = 0..127 (A: token rows of K, B: the row's W).
 // Output layout of a 16x16 block: lane l holds tokens 4*(l/16) + i (i = 0..3) of column l % 16.
 // zraw = bf16(acc) is written (as fp32) into zP, and the tile's column sums (fp64, lane order
 // below) into tsum[row][tile][16].
+// NG query rows per wave (NG == G: a KV row's query rows, whose K blocks are then loaded once for
+// all of them; NG == 1: blockIdx.y is the query row).
+template <int NG>
 __global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long ksh, long kst, int G,
                                                          int T, const uint16_t* W, float* zP,
                                                          long zps, uint16_t* zraw_out, double* tsum,
                                                          int ntiles) {
-  __shared__ uint4 s_z[64 * kRC / 8];             // the tile's bf16(k W), token rows of 32 bytes
-  uint16_t* s_zh = reinterpret_cast<uint16_t*>(s_z);
+  __shared__ uint4 s_z[NG][64 * kRC / 8];         // the tile's bf16(k W), token rows of 32 bytes
   const int lane = threadIdx.x;
-  const int row = blockIdx.y;
-  const uint16_t* krow = K + (long)(row / G) * ksh;
-  const uint16_t* w = W + (long)row * kD * kRC;
+  const int row0 = NG == 1 ? (int)blockIdx.y : (int)blockIdx.y * G;
+  const uint16_t* krow = K + (long)(row0 / G) * ksh;
   // B operand of chunk ch: column j = lane % 16, dims ch*32 + 8*(lane/16) + e, e = 0..7
-  bf16x8 bw[4];
+  bf16x8 bw[NG][4];
 #pragma unroll
-  for (int ch = 0; ch < 4; ++ch)
+  for (int g = 0; g < NG; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      bw[ch][e] = bits_bf16(w[(ch * 32 + 8 * (lane >> 4) + e) * kRC + (lane & 15)]);
+    for (int ch = 0; ch < 4; ++ch)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        bw[g][ch][e] = bits_bf16(W[(long)(row0 + g) * kD * kRC + (ch * 32 + 8 * (lane >> 4) + e) * kRC + (lane & 15)]);
   const int tend = min(ntiles, (int)(blockIdx.x + 1) * kProjTiles);
 #pragma unroll 1
   for (int tile = blockIdx.x * kProjTiles; tile < tend; ++tile) {
-  double cs = 0.0;   // this lane's column (lane % 16) partial over its tokens, in block order
+  double cs[NG];   // this lane's column (lane % 16) partial over its tokens, in block order
+#pragma unroll
+  for (int g = 0; g < NG; ++g) cs[g] = 0.0;
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
     const int t0 = tile * 64 + blk * 16;
     const int ta = min(t0 + (lane & 15), T - 1);          // A row: token t0 + lane % 16
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
+    uint4 av[4];
 #pragma unroll
-    for (int ch = 0; ch < 4; ++ch) {
-      const uint4 av = *reinterpret_cast<const uint4*>(krow + (long)ta * kst + ch * 32 + 8 * (lane >> 4));
-      bf16x8 a = __builtin_bit_cast(bf16x8, av);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bw[ch], acc, 0, 0, 0);
-    }
+    for (int ch = 0; ch < 4; ++ch)
+      av[ch] = *reinterpret_cast<const uint4*>(krow + (long)ta * kst + ch * 32 + 8 * (lane >> 4));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + 4 * (lane >> 4) + i;
-      const uint16_t hb = oa::f32_to_bf16_rn(acc[i]);
-      const float v = oa::bf16_to_f32(hb);
-      s_zh[(blk * 16 + 4 * (lane >> 4) + i) * kRC + (lane & 15)] = hb;
-      if (t < T) {
-        if (zP) zP[(long)row * zps + (long)t * kRC + (lane & 15)] = v;
-        cs += (double)v;
+    for (int g = 0; g < NG; ++g) {
+      float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[ch]), bw[g][ch], acc, 0, 0, 0);
+      uint16_t* s_zh = reinterpret_cast<uint16_t*>(s_z[g]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 4 * (lane >> 4) + i;
+        const uint16_t hb = oa::f32_to_bf16_rn(acc[i]);
+        const float v = oa::bf16_to_f32(hb);
+        s_zh[(blk * 16 + 4 * (lane >> 4) + i) * kRC + (lane & 15)] = hb;
+        if (t < T) {
+          if (zP) zP[(long)(row0 + g) * zps + (long)t * kRC + (lane & 15)] = v;
+          cs[g] += (double)v;
+        }
       }
     }
   }
@@ -242,15 +252,22 @@ __global__ void __launch_bounds__(64) qgc_project_kernel(const uint16_t* K, long
   if (zraw_out) {
     const int t = tile * 64 + lane;
     if (t < T) {
-      uint4* dst = reinterpret_cast<uint4*>(zraw_out + (long)row * zps + (long)t * kRC);
-      dst[0] = s_z[lane * 2];
-      dst[1] = s_z[lane * 2 + 1];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        uint4* dst = reinterpret_cast<uint4*>(zraw_out + (long)(row0 + g) * zps + (long)t * kRC);
+        dst[0] = s_z[g][lane * 2];
+        dst[1] = s_z[g][lane * 2 + 1];
+      }
     }
   }
   // lanes j, 16 + j, 32 + j, 48 + j hold column j: ((g0 + g1) + (g2 + g3))
-  cs += __shfl_xor(cs, 16, 64);
-  cs += __shfl_xor(cs, 32, 64);
-  if (lane < 16) tsum[((long)row * ntiles + tile) * kRC + lane] = cs;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    double c = cs[g];
+    c += __shfl_xor(c, 16, 64);
+    c += __shfl_xor(c, 32, 64);
+    if (lane < 16) tsum[((long)(row0 + g) * ntiles + tile) * kRC + lane] = c;
+  }
   // the next tile's stores to s_z wait for these reads
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -728,9 +745,15 @@ extern "C" int oa_qgc_project(const void* K, long k_stride_h, long k_stride_t, i
     return OA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   const int ntiles = (T + 63) / 64;
-  hipLaunchKernelGGL(qgc_project_kernel, dim3((ntiles + kProjTiles - 1) / kProjTiles, rows), dim3(64), 0, s,
-                     reinterpret_cast<const uint16_t*>(K), k_stride_h, k_stride_t, G, T,
-                     reinterpret_cast<const uint16_t*>(W), zP, zp_stride, zraw_out, tile_ws, ntiles);
+  const int nx = (ntiles + kProjTiles - 1) / kProjTiles;
+  if (G == 4)   // a KV row's four query rows per wave: each K block loaded once for all four
+    hipLaunchKernelGGL(qgc_project_kernel<4>, dim3(nx, rows / 4), dim3(64), 0, s,
+                       reinterpret_cast<const uint16_t*>(K), k_stride_h, k_stride_t, G, T,
+                       reinterpret_cast<const uint16_t*>(W), zP, zp_stride, zraw_out, tile_ws, ntiles);
+  else
+    hipLaunchKernelGGL(qgc_project_kernel<1>, dim3(nx, rows), dim3(64), 0, s,
+                       reinterpret_cast<const uint16_t*>(K), k_stride_h, k_stride_t, G, T,
+                       reinterpret_cast<const uint16_t*>(W), zP, zp_stride, zraw_out, tile_ws, ntiles);
   hipLaunchKernelGGL(qgc_colmean_kernel, dim3(rows), dim3(64), 0, s, T, tile_ws, ntiles, colmean);
   if (zP) {
     const int nb = std::min(16, (T * (kRC / 4) + 255) / 256);

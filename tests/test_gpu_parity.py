@@ -883,17 +883,17 @@ def test_build_codes_bit_exact(T):
         assert np.array_equal(codes.cpu().numpy(), rc)
 
 
-@pytest.mark.parametrize("T", [4095, 1000])
-def test_build_projection_and_kmeans(T):
+@pytest.mark.parametrize("T,G_", [(4095, 4), (1000, 4), (1000, 2)])
+def test_build_projection_and_kmeans(T, G_):
     """QGC projection on the bf16 matrix cores: bf16(k W) agrees with the exact-sum restatement
     up to rare bf16 ties; colmean and zP are bit-exact given the device's bf16(k W), and the
     projection without the fp32 zP writes the same bf16(k W) and colmean.  k-means (zP formed from
     the bf16 projection and colmean as the kernels read it): the assignment agrees with the
     restatement's on the same zP and centroids up to rare ties; the update is bit-exact given the
     device's assignment."""
-    print(f"[case] build projection + k-means T={T}", flush=True)
+    print(f"[case] build projection + k-means T={T} G={G_}", flush=True)
     rng = np.random.default_rng(7 + T)
-    HKV_, G_, Lmax, C = 2, 4, 4160, 64
+    HKV_, Lmax, C = 2, 4160, 64
     R = HKV_ * G_
     K = f32_to_bf16(rng.standard_normal((HKV_, Lmax, D)).astype(np.float32))
     W = f32_to_bf16((rng.standard_normal((R, D, 16)) * 0.3).astype(np.float32))
