@@ -453,8 +453,8 @@ __global__ void __launch_bounds__(kAsgThreads) kmeans_assign_kernel(const uint16
 
 constexpr int kMemBuf = 2048;   // member positions staged in LDS at a time
 
-// a wave copies n <= kMemBuf member positions into LDS, eight loads per lane in flight at a time
-// (one at a time, each copy waited on its load)
+// a wave copies 1 <= n <= (the LDS array's size) member positions into LDS, eight loads per lane
+// in flight at a time (one at a time, each copy waited on its load)
 __device__ __forceinline__ void stage_members(int* s_pos, const int32_t* ml, int n, int lane) {
   for (int b = 0; b < n; b += 512) {
     int v[8];
